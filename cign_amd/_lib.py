@@ -1,0 +1,99 @@
+"""ctypes binding of libcign_amd.so, the C-ABI declared in include/cign_amd.h.
+
+The library is loaded after ``import torch`` so that it binds to the HIP
+runtime torch already loaded (same soname, one runtime per process). Every
+entry point returns an int status; non-zero raises ``RuntimeError`` carrying
+``cign_last_error()``. There is no CPU fallback: a missing library or a
+missing GPU raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libcign_amd.so"
+
+_P = C.c_void_p
+_I32 = C.c_int32
+_I64 = C.c_int64
+_F32 = C.c_float
+_U64 = C.c_uint64
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "cign_last_error": (C.c_char_p, []),
+    "cign_version": (C.c_int, []),
+    "cign_row_schedule_size": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P]),
+    "cign_row_schedule_build": (C.c_int, [_P, _I32, _I32, _I32, _P, _I64]),
+    "cign_spmm_partial_bytes": (_I64, [_I32, _I32]),
+    "cign_spmm": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P]),
+    "cign_spmm_fwd3": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P]),
+    "cign_spmm_bwd3": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P]),
+}
+
+_LOCK = threading.Lock()
+_LIB = None
+_LIB_ERROR: BaseException | None = None
+
+
+class _Lib:
+    def __init__(self, handle: C.CDLL):
+        self._h = handle
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+            setattr(self, name, fn)
+
+    def call(self, name: str, *args) -> None:
+        rc = getattr(self, name)(*args)
+        if rc != 0:
+            msg = self.cign_last_error().decode(errors="replace")
+            raise RuntimeError(f"{name} failed (status {rc}): {msg}")
+
+
+def load_library(require_gpu: bool = True) -> _Lib:
+    """Loads libcign_amd.so once. Raises RuntimeError if it is not built or,
+    when ``require_gpu``, if no HIP device is visible."""
+    global _LIB, _LIB_ERROR
+    with _LOCK:
+        if _LIB is None:
+            if _LIB_ERROR is not None:
+                raise RuntimeError("libcign_amd previously failed to load") from _LIB_ERROR
+            try:
+                if not LIB_PATH.exists():
+                    raise RuntimeError(
+                        f"{LIB_PATH} is not built; run `python -m cign_amd._build` (hipcc, gfx950)"
+                    )
+                _LIB = _Lib(C.CDLL(str(LIB_PATH)))
+            except BaseException as exc:  # cached and re-raised, like the reference loaders
+                _LIB_ERROR = exc
+                raise
+    if require_gpu and not torch.cuda.is_available():
+        raise RuntimeError("libcign_amd kernels require a HIP GPU (torch.cuda.is_available() is False)")
+    return _LIB
+
+
+def exported_symbols() -> list[str]:
+    return sorted(_SIGNATURES)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_ptr(device: torch.device | None = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1}
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; expected float32 or bfloat16") from None

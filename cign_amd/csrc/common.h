@@ -1,0 +1,180 @@
+// Shared device helpers and C-ABI error plumbing for libcign_amd.
+//
+// Every kernel in this library is written for gfx950 (CDNA4): 64-lane
+// wavefronts, 256-thread workgroups (4 waves), fp32 accumulation. Feature
+// tensors are row-major; bf16 storage is supported through the load/store
+// helpers below (accumulation always stays fp32).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cign {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;
+constexpr int kWavesPerBlock = kBlock / kWave;
+
+// dtype codes used on the C-ABI.
+enum DType : int { kF32 = 0, kBF16 = 1 };
+
+// Return codes used on the C-ABI.
+enum Status : int { kOk = 0, kInvalid = 1, kHipError = 2 };
+
+// Thread-local "last error" text, readable through cign_last_error().
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32 (round to nearest even, NaN kept quiet).
+// ---------------------------------------------------------------------------
+struct bf16 {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16 v) {
+  return __uint_as_float(static_cast<uint32_t>(v.bits) << 16);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float f);
+template <>
+__device__ __forceinline__ float from_f32<float>(float f) { return f; }
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float f) {
+  uint32_t u = __float_as_uint(f);
+  bf16 r;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    r.bits = static_cast<uint16_t>((u >> 16) | 0x40u);
+  } else {
+    u += 0x7fffu + ((u >> 16) & 1u);
+    r.bits = static_cast<uint16_t>(u >> 16);
+  }
+  return r;
+}
+
+// A 16-byte (or 1-element) vector chunk of T, unpacked to fp32 registers.
+// W = elements per chunk: 4 (fp32 x4), 8 (bf16 x8) or 1 (scalar fallback).
+template <typename T, int W>
+struct Chunk;
+
+template <>
+struct Chunk<float, 4> {
+  static __device__ __forceinline__ void load(const float* p, float (&v)[4]) {
+    const float4 q = *reinterpret_cast<const float4*>(p);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&v)[4]) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+
+template <>
+struct Chunk<bf16, 8> {
+  static __device__ __forceinline__ void load(const bf16* p, float (&v)[8]) {
+    const uint4 q = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  static __device__ __forceinline__ void store(bf16* p, const float (&v)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = from_f32<bf16>(v[2 * i]).bits;
+      const uint32_t hi = from_f32<bf16>(v[2 * i + 1]).bits;
+      w[i] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+
+template <typename T>
+struct Chunk<T, 1> {
+  static __device__ __forceinline__ void load(const T* p, float (&v)[1]) { v[0] = to_f32(*p); }
+  static __device__ __forceinline__ void store(T* p, const float (&v)[1]) { *p = from_f32<T>(v[0]); }
+};
+
+// ---------------------------------------------------------------------------
+// Wavefront primitives (64 lanes).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
+
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ float shfl(float v, int src) { return __shfl(v, src, kWave); }
+__device__ __forceinline__ int shfl(int v, int src) { return __shfl(v, src, kWave); }
+
+// Sum over lanes whose ids differ only in bits >= `from` (all lanes sharing
+// lane % from); every such lane receives the total.
+__device__ __forceinline__ float sum_across(float v, int from) {
+  for (int o = from; o < kWave; o <<= 1) v += shfl_xor(v, o);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Math helpers shared by the GAT, pack and block kernels.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float leaky(float x, float slope) { return x > 0.0f ? x : x * slope; }
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float silu(float x) { return x * sigmoid(x); }
+__device__ __forceinline__ float silu_grad(float x) {
+  const float s = sigmoid(x);
+  return s * (1.0f + x * (1.0f - s));
+}
+
+// splitmix64 finaliser (Steele, Lea, Flood 2014; public-domain constants as
+// published by S. Vigna). Used by the dropout masks so they match the
+// reference bit for bit.
+__host__ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+constexpr uint64_t kIdxMul = 0xD2B74407B1CE6E93ull;
+
+// Edge-dropout keep bit of the collapsed GAT: 32-bit uniform, keep = u > p.
+__device__ __forceinline__ bool gat_keep(uint64_t seed, uint64_t idx, float p) {
+  const uint64_t r = splitmix64(seed ^ (idx * kIdxMul));
+  const uint32_t hi = static_cast<uint32_t>(r >> 32);
+  const float u = (static_cast<float>(hi) + 0.5f) * 2.3283064365386963e-10f;
+  return u > p;
+}
+
+// Block-op dropout keep bit: 53-bit uniform in double, keep = u >= p.
+__device__ __forceinline__ bool block_keep(uint64_t seed, uint64_t idx, float p) {
+  if (p <= 0.0f) return true;
+  const uint64_t r = splitmix64(seed ^ (idx * kIdxMul));
+  const double u = static_cast<double>(r >> 11) * (1.0 / 9007199254740992.0);
+  return u >= static_cast<double>(p);
+}
+
+// ---------------------------------------------------------------------------
+// Cross-workgroup "last arrival" for segmented rows. Each participating block
+// publishes its partial result, then calls this with thread 0's view of the
+// per-row counter. Exactly one block (the last to arrive) sees `true`; it
+// resets the counter so the next launch starts from zero again. No block ever
+// waits on another, so this cannot hang.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool arrive_last(int* counter, int expected, int* lds_flag) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = (prev == expected - 1);
+    if (last) {
+      __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __threadfence();
+    }
+    *lds_flag = last ? 1 : 0;
+  }
+  __syncthreads();
+  return *lds_flag != 0;
+}
+
+}  // namespace cign

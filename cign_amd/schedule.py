@@ -1,0 +1,79 @@
+"""Degree-bucketed row schedules (host side of csrc/schedule.h).
+
+A schedule is built once per fixed CSR/CSC row pointer, like the reference's
+one-time graph preparation (MultiHopCsrPlan::prepare,
+multihop_csr_ext/multihop_csr_pipeline_cuda.cu:246-262;
+GraphCliffordNet.prepare_fused_gat_graph, generic_engine/model_cign.py:1069-1158),
+and cached per row-pointer tensor for the stateless GAT entry points.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import weakref
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from ._lib import load_library
+
+# Rows with at most LIGHT_MAX edges get one wavefront; heavier rows are cut
+# into SEG_EDGES-edge segments, one 256-thread workgroup each.
+LIGHT_MAX = 64
+SEG_EDGES = 256
+
+
+@dataclass
+class RowSchedule:
+    buf: torch.Tensor        # int32 device buffer (csrc/schedule.h layout)
+    counters: torch.Tensor   # int32 [max(1, n_hrow)], zero; kernels leave it zero
+    n_rows: int
+    n_light: int
+    n_seg: int
+    n_hrow: int
+    max_degree: int
+
+    def args(self):
+        return (self.buf.data_ptr(), self.n_light, self.n_seg, self.n_hrow)
+
+
+def build_row_schedule(rowptr: torch.Tensor, device=None, light_max: int = LIGHT_MAX,
+                       seg_edges: int = SEG_EDGES) -> RowSchedule:
+    """Builds the schedule of a row pointer (any integer dtype, any device).
+    One host copy of the row pointer is taken (a synchronisation when it lives
+    on the GPU); this happens once per graph, outside timed regions."""
+    lib = load_library(require_gpu=False)
+    rp = np.ascontiguousarray(rowptr.detach().to("cpu", torch.int64).numpy())
+    n_rows = int(rp.shape[0]) - 1
+    if n_rows < 0:
+        raise ValueError("row pointer must have at least one entry")
+    nl, ns, nh = C.c_int32(), C.c_int32(), C.c_int32()
+    tot = C.c_int64()
+    lib.call("cign_row_schedule_size", rp.ctypes.data, n_rows, light_max, seg_edges,
+             C.byref(nl), C.byref(ns), C.byref(nh), C.byref(tot))
+    host = np.zeros(int(tot.value), dtype=np.int32)
+    lib.call("cign_row_schedule_build", rp.ctypes.data, n_rows, light_max, seg_edges,
+             host.ctypes.data, int(tot.value))
+    dev = device if device is not None else rowptr.device
+    buf = torch.from_numpy(host).to(dev)
+    counters = torch.zeros(max(1, nh.value), dtype=torch.int32, device=dev)
+    deg = np.diff(rp)
+    return RowSchedule(buf, counters, n_rows, int(nl.value), int(ns.value), int(nh.value),
+                       int(deg.max()) if deg.size else 0)
+
+
+_CACHE: dict[int, tuple[weakref.ref, int, RowSchedule]] = {}
+
+
+def cached_row_schedule(rowptr: torch.Tensor) -> RowSchedule:
+    """Schedule for a row-pointer tensor, built on first use and reused while
+    the tensor is alive and unmodified (checked through its version counter)."""
+    key = id(rowptr)
+    hit = _CACHE.get(key)
+    if hit is not None:
+        ref, version, sched = hit
+        if ref() is rowptr and version == rowptr._version and sched.n_rows == rowptr.numel() - 1:
+            return sched
+    sched = build_row_schedule(rowptr)
+    _CACHE[key] = (weakref.ref(rowptr, lambda _r, k=key: _CACHE.pop(k, None)), rowptr._version, sched)
+    return sched
