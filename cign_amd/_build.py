@@ -43,8 +43,13 @@ def sources() -> list[Path]:
     return sorted(list(SRC.glob("*.hip")) + list(SRC.glob("*.cpp")))
 
 
-def _compile(hipcc: str, src: Path) -> Path:
+def _compile(hipcc: str, src: Path, force: bool) -> Path:
     obj = OBJ / (src.stem + ".o")
+    if not force and obj.exists():
+        newest = max([src.stat().st_mtime, *(h.stat().st_mtime for h in SRC.glob("*.h")),
+                      Path(__file__).stat().st_mtime])
+        if obj.stat().st_mtime >= newest:
+            return obj
     cmd = [hipcc, *HIP_FLAGS, "-x", "hip", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
@@ -52,14 +57,18 @@ def _compile(hipcc: str, src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compiles every HIP source for gfx950 and links libcign_amd.so."""
+def build(verbose: bool = False, jobs: int | None = None, force: bool = True) -> Path:
+    """Compiles every HIP source for gfx950 and links libcign_amd.so.
+
+    ``force=False`` reuses object files that are newer than their source,
+    every header and this script (incremental developer builds)."""
     hipcc = _hipcc()
     OBJ.mkdir(parents=True, exist_ok=True)
-    srcs = sources()
+    # Slowest translation units first so the parallel build finishes early.
+    srcs = sorted(sources(), key=lambda p: ("hp32" not in p.name, p.name))
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)), 8)
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(lambda s: _compile(hipcc, s), srcs))
+        objs = list(pool.map(lambda s: _compile(hipcc, s, force), srcs))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -72,5 +81,5 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, force="--force" in sys.argv)
     sys.exit(0)

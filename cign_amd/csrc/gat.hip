@@ -1,0 +1,188 @@
+// C-ABI of the collapsed GAT (kernels in gat_kernels.h, instantiated in the
+// gat_inst_*.hip translation units so they compile in parallel).
+#include "gat_kernels.h"
+
+namespace cign {
+namespace gatk {
+CIGN_GAT_DECLARE(float, 4)
+CIGN_GAT_DECLARE(float, 8)
+CIGN_GAT_DECLARE(float, 32)
+CIGN_GAT_DECLARE(bf16, 4)
+CIGN_GAT_DECLARE(bf16, 8)
+CIGN_GAT_DECLARE(bf16, 32)
+}  // namespace gatk
+}  // namespace cign
+
+namespace cign {
+namespace gatk {
+
+// ---------------------------------------------------------------------------
+// Host dispatch over (HP, CP).
+// ---------------------------------------------------------------------------
+inline int pow2ceil(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+// Heads are padded to HP lanes (4, 8 or 32; unused head lanes idle) and
+// channels to CP-wide blocks (8, 16 or 32).
+template <template <typename, int, int> class Launcher, typename T, typename... Args>
+int dispatch_hc(int H, int C, Args&&... args) {
+  const int HP = H <= 4 ? 4 : (H <= 8 ? 8 : 32);
+  const int CP = C >= 32 ? 32 : (pow2ceil(C) < 8 ? 8 : pow2ceil(C));
+#define CIGN_CASE(hp, cp) \
+  if (HP == hp && CP == cp) return Launcher<T, hp, cp>::run(args...);
+#define CIGN_CASES(hp) CIGN_CASE(hp, 8) CIGN_CASE(hp, 16) CIGN_CASE(hp, 32)
+  CIGN_CASES(4) CIGN_CASES(8) CIGN_CASES(32)
+#undef CIGN_CASES
+#undef CIGN_CASE
+  return set_error(kInvalid, "collapsed GAT: unsupported heads=%d channels=%d", H, C);
+}
+
+struct BwdLayout {
+  int64_t grad_pre, gscore, bias_part, bias_l2, part_row, part_col, total;
+};
+
+inline int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
+
+inline BwdLayout bwd_layout(int n, int nnz, int H, int C, int row_blocks, int n_seg_rows, int n_seg_cols) {
+  BwdLayout L;
+  const int n_l2 = (row_blocks + 63) / 64;
+  int64_t off = 0;
+  L.grad_pre = off; off = align256(off + 4LL * n * C);
+  L.gscore = off; off = align256(off + 4LL * nnz * H);
+  L.bias_part = off; off = align256(off + 4LL * row_blocks * C);
+  L.bias_l2 = off; off = align256(off + 4LL * n_l2 * C);
+  L.part_row = off; off = align256(off + 4LL * n_seg_rows * H);
+  L.part_col = off; off = align256(off + 4LL * n_seg_cols * (static_cast<int64_t>(H) * C + H));
+  L.total = off;
+  return L;
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+int check_shape(const char* who, int n, int nnz, int H, int C) {
+  if (n < 0 || nnz < 0) return set_error(kInvalid, "%s: negative sizes", who);
+  if (H < 1 || H > kMaxH) return set_error(kInvalid, "%s: heads=%d outside [1, %d]", who, H, kMaxH);
+  if (C < 1 || C > kMaxC) return set_error(kInvalid, "%s: channels=%d outside [1, %d]", who, C, kMaxC);
+  return kOk;
+}
+
+}  // namespace gatk
+}  // namespace cign
+
+using namespace cign;
+using namespace cign::gatk;
+
+extern "C" {
+
+// fp32 workspace needed by cign_gat_fwd for a row schedule with n_seg segments.
+int64_t cign_gat_fwd_workspace_bytes(int32_t n_seg, int32_t heads, int32_t channels) {
+  return 4LL * n_seg * (static_cast<int64_t>(heads) * channels + 2LL * heads);
+}
+
+// Collapsed GAT forward. Replaces the ext `forward` of the reference
+// (collapsed_gat_ext/collapsed_gat.cpp:45-72 -> collapsed_gat_cuda.cu:434-478).
+// attn_row/attn_col [n,H] fp32, rowptr [n+1]/col [nnz] int32 (CSR by
+// destination), in_feat [n,H,C] (dtype), bias [C] fp32. Outputs: out [n,C]
+// (dtype), pre [n,C] fp32, edge_max/edge_sum [n,H] fp32, edge_mask [nnz,H] u8
+// (written only when attn_drop > 0). row_sched: schedule of rowptr.
+int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
+                 const float* attn_row, const float* attn_col, const int32_t* rowptr, const int32_t* col,
+                 const int32_t* row_sched, int32_t n_light, int32_t n_seg, int32_t n_hrow, int32_t* row_counters,
+                 float negative_slope, const void* in_feat, const float* bias, float attn_drop, uint64_t seed,
+                 void* out, float* pre, float* edge_max, float* edge_sum, uint8_t* edge_mask, void* workspace,
+                 int64_t workspace_bytes) {
+  int rc = check_shape("cign_gat_fwd", n, nnz, heads, channels);
+  if (rc) return rc;
+  if (!(attn_drop >= 0.0f && attn_drop < 1.0f)) return set_error(kInvalid, "cign_gat_fwd: attn_drop must be in [0,1)");
+  if (n_light + n_hrow != n) return set_error(kInvalid, "cign_gat_fwd: schedule does not cover %d rows", n);
+  if (workspace_bytes < cign_gat_fwd_workspace_bytes(n_seg, heads, channels))
+    return set_error(kInvalid, "cign_gat_fwd: workspace too small");
+  if (n == 0) return kOk;
+  const Sched s = make_sched(row_sched, n_light, n_seg, n_hrow);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto fill = [&](auto* xt, auto* ot) {
+    using T = std::remove_cv_t<std::remove_pointer_t<decltype(ot)>>;
+    GatFwdArgs<T> a;
+    a.n = n; a.H = heads; a.C = channels;
+    a.slope = negative_slope; a.p = attn_drop; a.inv_keep = attn_drop > 0.0f ? 1.0f / (1.0f - attn_drop) : 1.0f;
+    a.seed = seed;
+    a.vec = aligned16(xt) && (channels * static_cast<int>(sizeof(T))) % 16 == 0;
+    a.attn_row = attn_row; a.attn_col = attn_col; a.rowptr = rowptr; a.col = col;
+    a.x = xt; a.bias = bias; a.out = ot; a.pre = pre; a.emax = edge_max; a.esum = edge_sum;
+    a.mask = edge_mask; a.partial = static_cast<float*>(workspace); a.counters = row_counters;
+    return dispatch_hc<FwdLauncher, T>(heads, channels, st, a, s);
+  };
+  if (dtype == kF32) return fill(static_cast<const float*>(in_feat), static_cast<float*>(out));
+  if (dtype == kBF16) return fill(static_cast<const bf16*>(in_feat), static_cast<bf16*>(out));
+  return set_error(kInvalid, "cign_gat_fwd: unsupported dtype %d", dtype);
+}
+
+int64_t cign_gat_bwd_workspace_bytes(int32_t n, int32_t nnz, int32_t heads, int32_t channels, int32_t row_blocks,
+                                     int32_t n_seg_rows, int32_t n_seg_cols) {
+  return bwd_layout(n, nnz, heads, channels, row_blocks, n_seg_rows, n_seg_cols).total;
+}
+
+// Collapsed GAT backward. Replaces the ext `backward` of the reference
+// (collapsed_gat_ext/collapsed_gat.cpp:74-102 -> collapsed_gat_cuda.cu:480-545).
+// Needs the CSR schedule (rows) and the CSC schedule (colptr) plus their
+// counters; the CSC counter array must have n_hrow_cols + 1 entries.
+int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
+                 float negative_slope, float attn_drop, const int32_t* rowptr, const int32_t* col,
+                 const int32_t* colptr, const int32_t* rowind, const int32_t* perm, const float* edge_max,
+                 const float* edge_sum, const uint8_t* edge_mask, const void* in_feat, const float* attn_row,
+                 const float* attn_col, const float* pre, const void* grad_y, const int32_t* row_sched,
+                 int32_t r_light, int32_t r_seg, int32_t r_hrow, int32_t* row_counters, const int32_t* col_sched,
+                 int32_t c_light, int32_t c_seg, int32_t c_hrow, int32_t* col_counters, void* workspace,
+                 int64_t workspace_bytes, void* grad_feat, float* grad_attn_row, float* grad_attn_col,
+                 float* grad_bias) {
+  int rc = check_shape("cign_gat_bwd", n, nnz, heads, channels);
+  if (rc) return rc;
+  if (!(attn_drop >= 0.0f && attn_drop < 1.0f)) return set_error(kInvalid, "cign_gat_bwd: attn_drop must be in [0,1)");
+  if (r_light + r_hrow != n || c_light + c_hrow != n)
+    return set_error(kInvalid, "cign_gat_bwd: schedules do not cover %d rows/columns", n);
+  const Sched rs = make_sched(row_sched, r_light, r_seg, r_hrow);
+  const Sched cs = make_sched(col_sched, c_light, c_seg, c_hrow);
+  const int row_blocks = sched_blocks(rs);
+  const BwdLayout L = bwd_layout(n, nnz, heads, channels, row_blocks, r_seg, c_seg);
+  if (workspace_bytes < L.total) return set_error(kInvalid, "cign_gat_bwd: workspace too small (%lld < %lld)",
+                                                  static_cast<long long>(workspace_bytes), static_cast<long long>(L.total));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (n == 0) {
+    const hipError_t e = hipMemsetAsync(grad_bias, 0, sizeof(float) * channels, st);
+    return e == hipSuccess ? kOk : set_error(kHipError, "cign_gat_bwd: %s", hipGetErrorString(e));
+  }
+  char* ws = static_cast<char*>(workspace);
+  auto fill = [&](auto* xt, auto* gyt, auto* gxt) {
+    using T = std::remove_cv_t<std::remove_pointer_t<decltype(gxt)>>;
+    GatBwdArgs<T> a;
+    a.n = n; a.nnz = nnz; a.H = heads; a.C = channels;
+    a.slope = negative_slope; a.p = attn_drop; a.inv_h = 1.0f / static_cast<float>(heads);
+    a.vec_x = aligned16(xt) && (channels * static_cast<int>(sizeof(T))) % 16 == 0;
+    a.vec_gp = (channels % 4) == 0;
+    a.vec_gx = aligned16(gxt) && (channels * static_cast<int>(sizeof(T))) % 16 == 0;
+    a.rowptr = rowptr; a.col = col; a.colptr = colptr; a.rowind = rowind; a.perm = perm;
+    a.emax = edge_max; a.esum = edge_sum; a.mask = edge_mask; a.x = xt;
+    a.attn_row = attn_row; a.attn_col = attn_col; a.pre = pre; a.grad_y = gyt;
+    a.grad_pre = reinterpret_cast<float*>(ws + L.grad_pre);
+    a.gscore = reinterpret_cast<float*>(ws + L.gscore);
+    a.bias_part = reinterpret_cast<float*>(ws + L.bias_part);
+    a.bias_l2 = reinterpret_cast<float*>(ws + L.bias_l2);
+    a.part_row = reinterpret_cast<float*>(ws + L.part_row);
+    a.part_col = reinterpret_cast<float*>(ws + L.part_col);
+    a.row_counters = row_counters; a.col_counters = col_counters;
+    a.rows_blocks = row_blocks;
+    a.n_l2 = (row_blocks + 63) / 64;
+    a.grad_feat = gxt; a.grad_attn_row = grad_attn_row; a.grad_attn_col = grad_attn_col; a.grad_bias = grad_bias;
+    return dispatch_hc<BwdLauncher, T>(heads, channels, st, a, rs, cs);
+  };
+  if (dtype == kF32)
+    return fill(static_cast<const float*>(in_feat), static_cast<const float*>(grad_y), static_cast<float*>(grad_feat));
+  if (dtype == kBF16)
+    return fill(static_cast<const bf16*>(in_feat), static_cast<const bf16*>(grad_y), static_cast<bf16*>(grad_feat));
+  return set_error(kInvalid, "cign_gat_bwd: unsupported dtype %d", dtype);
+}
+
+}  // extern "C"

@@ -1,0 +1,4 @@
+// Explicit instantiation of the collapsed-GAT kernels for float, 32 head lanes.
+#include "gat_kernels.h"
+
+CIGN_GAT_INSTANTIATE(float, 32)

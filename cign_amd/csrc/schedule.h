@@ -16,6 +16,7 @@
 // them in segment order (deterministic) and writes the row.
 #pragma once
 
+#include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace cign {
@@ -51,6 +52,6 @@ inline int64_t sched_ints(int n_light, int n_seg, int n_hrow) {
 }
 
 // Grid size for a schedule: one workgroup per segment plus one per 4 light rows.
-inline int sched_blocks(const Sched& s) { return s.n_seg + (s.n_light + 3) / 4; }
+__host__ __device__ inline int sched_blocks(const Sched& s) { return s.n_seg + (s.n_light + 3) / 4; }
 
 }  // namespace cign

@@ -26,7 +26,7 @@ SEG_EDGES = 256
 @dataclass
 class RowSchedule:
     buf: torch.Tensor        # int32 device buffer (csrc/schedule.h layout)
-    counters: torch.Tensor   # int32 [max(1, n_hrow)], zero; kernels leave it zero
+    counters: torch.Tensor   # int32 [n_hrow + 1], zero; kernels leave it zero (last slot: spare global counter)
     n_rows: int
     n_light: int
     n_seg: int
@@ -56,7 +56,7 @@ def build_row_schedule(rowptr: torch.Tensor, device=None, light_max: int = LIGHT
              host.ctypes.data, int(tot.value))
     dev = device if device is not None else rowptr.device
     buf = torch.from_numpy(host).to(dev)
-    counters = torch.zeros(max(1, nh.value), dtype=torch.int32, device=dev)
+    counters = torch.zeros(nh.value + 1, dtype=torch.int32, device=dev)
     deg = np.diff(rp)
     return RowSchedule(buf, counters, n_rows, int(nl.value), int(ns.value), int(nh.value),
                        int(deg.max()) if deg.size else 0)
