@@ -1,0 +1,212 @@
+"""Benchmark of the CIGN sparse message-passing layer on one MI355X.
+
+One step = the headline layer of BASELINE.json, forward + backward, with all
+inputs resident in HBM:
+  * collapsed GAT core (c2: H=4 heads x C=16 channels, fp32) on the
+    24,492-node / 186,100-edge Chung-Lu graph + self-loops (E = 210,592):
+    cign_gat_fwd then cign_gat_bwd (2 kernels);
+  * 3-hop CSR SpMM pipeline (c3: D=64, fp32) on the normalized adjacency of
+    the same graph: cign_spmm_fwd3 then cign_spmm_bwd3 (3 + 3 kernels).
+value = E * K / t (edges/s over the timed K steps). The roofline object is
+computed for the dominant kernel from HIP events recorded on the launch
+stream inside the timed region; the CPU baseline times the numpy oracle on
+the host (a bounded sample of the same workload).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E vendor peak, GB/s
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 disables)")
+    ap.add_argument("--dtype", choices=["f32", "bf16"], default="f32")
+    return ap.parse_args()
+
+
+def cpu_baseline(w, seconds: float, H: int, C: int, D: int):
+    """Times the numpy oracle (single thread) on the same c2/c3 layer."""
+    import numpy as np
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except Exception:  # pragma: no cover
+        threadpool_limits = None
+    from oracle import cign_oracle as O
+
+    (rowptr, col), _, _ = w.gat_graph
+    rp, cl = rowptr.cpu().numpy().astype(np.int64), col.cpu().numpy().astype(np.int64)
+    n = w.n
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((n, H, C)).astype(np.float32)
+    ar, ac = rng.standard_normal((n, H)).astype(np.float32), rng.standard_normal((n, H)).astype(np.float32)
+    b, gy = rng.standard_normal(C).astype(np.float32), rng.standard_normal((n, C)).astype(np.float32)
+    csr, csr_t = w.operator.csr, w.operator.csr_t
+    p = (csr.crow_indices().cpu().numpy(), csr.col_indices().cpu().numpy(), csr.values().cpu().numpy())
+    pt = (csr_t.crow_indices().cpu().numpy(), csr_t.col_indices().cpu().numpy(), csr_t.values().cpu().numpy())
+    X = rng.standard_normal((n, D)).astype(np.float32)
+    G = [rng.standard_normal((n, D)).astype(np.float32) for _ in range(3)]
+
+    def one():
+        O.collapsed_gat_forward(ar, ac, rp, cl, 0.2, x, b)
+        O.collapsed_gat_backward(ar, ac, rp, cl, 0.2, x, b, gy)
+        O.multihop3_forward(p, X)
+        O.multihop3_backward(pt, *G)
+
+    ctx = threadpool_limits(limits=1) if threadpool_limits else None
+    try:
+        if ctx:
+            ctx.__enter__()
+        one()  # warmup
+        t0 = time.perf_counter()
+        k = 0
+        while True:
+            one()
+            k += 1
+            if time.perf_counter() - t0 >= seconds:
+                break
+        dt = time.perf_counter() - t0
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    return {"value": w.nnz_gat * k / dt, "unit": "edges/s", "cores": 1, "kind": "port",
+            "sample": f"{k} full c2+c3 layer fwd+bwd steps of the numpy/scipy oracle (float64) in {dt:.1f} s, "
+                      f"1 thread"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1 (multi-GPU sharding is "
+                                   "described in DESIGN.md and not run)"}), flush=True)
+        sys.exit(2)
+    import torch
+
+    from cign_amd import workloads
+    from cign_amd.collapsed_gat import ensure_collapsed_gat_loaded
+    from cign_amd.multihop_csr_pipeline import MultiHopCSR3GraphOperator
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    H, C, D = 4, 16, 64
+    dt = torch.float32 if args.dtype == "f32" else torch.bfloat16
+    w = workloads.build(workloads.C2, device=dev)
+    (rowptr, col), (row, colptr), perm = w.gat_graph
+    n, E = w.n, w.nnz_gat
+    g = torch.Generator(device="cpu").manual_seed(0)
+    rnd = lambda *s: torch.randn(*s, generator=g).to(dev)
+    x = rnd(n, H, C).to(dt)
+    ar, ac, bias = rnd(n, H), rnd(n, H), rnd(C)
+    gy = rnd(n, C).to(dt)
+    X = rnd(n, D).to(dt)
+    g1, g2, g3 = rnd(n, D).to(dt), rnd(n, D).to(dt), rnd(n, D).to(dt)
+    ext = ensure_collapsed_gat_loaded()
+    mh = MultiHopCSR3GraphOperator(w.operator, dense_cols=D, dense_dtype=dt)
+    plan = mh.plan
+
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    phases = ("gat_fwd", "spmm_fwd3", "gat_bwd", "spmm_bwd3")
+
+    def step(marks=None):
+        if marks is not None:
+            marks[0].record()
+        out, pre, emax, esum, mask = ext.forward(ar, ac, rowptr, col, 0.2, x, bias, 0.0, 0)
+        if marks is not None:
+            marks[1].record()
+        plan.forward3(X)
+        if marks is not None:
+            marks[2].record()
+        ext.backward(0.2, 0.0, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar, ac, pre, gy)
+        if marks is not None:
+            marks[3].record()
+        plan.backward3(g1, g2, g3)
+        if marks is not None:
+            marks[4].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region: K steps, synchronised on both sides. Phase events are
+    # recorded on the launch stream (torch's current stream, the stream every
+    # cign_* call is given).
+    marks = [[ev() for _ in range(5)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        step(marks[k])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    phase_ms = {p: 0.0 for p in phases}
+    for m in marks:
+        for i, p in enumerate(phases):
+            phase_ms[p] += m[i].elapsed_time(m[i + 1]) / args.steps
+
+    s = 2 if dt == torch.bfloat16 else 4
+    B = workloads.algorithmic_bytes(n, E, H, C, D, s_gat=s, s_mh=s)
+    ms = 1e3 * elapsed / args.steps
+    launches = {"gat_fwd": 1, "spmm_fwd3": 3, "gat_bwd": 2, "spmm_bwd3": 3}
+    bytes_per_launch = {"gat_fwd": B["gat_fwd"], "spmm_fwd3": B["spmm"], "gat_bwd": B["gat_bwd"] / 2,
+                        "spmm_bwd3": B["spmm"] + s * n * D * 2 / 3}
+    breakdown = {}
+    for p in phases:
+        per_launch_ms = phase_ms[p] / launches[p]
+        gbs = bytes_per_launch[p] / (per_launch_ms * 1e-3) / 1e9
+        breakdown[p] = {"ms": round(phase_ms[p], 4), "launches": launches[p], "GB_s": round(gbs, 1)}
+    dom = max(phases, key=lambda p: phase_ms[p])
+    dom_ms = phase_ms[dom] / launches[dom]
+    achieved = bytes_per_launch[dom] / (dom_ms * 1e-3) / 1e9
+    kernel_name = {"gat_fwd": "gat_fwd_kernel", "spmm_fwd3": "spmm_kernel (fwd hop)",
+                   "gat_bwd": "gat_bwd_rows_kernel + gat_bwd_cols_kernel (mean)",
+                   "spmm_bwd3": "spmm_kernel (bwd hop, fused add)"}[dom]
+    layer_gbs = B["layer"] / (ms * 1e-3) / 1e9
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = cpu_baseline(w, args.cpu_seconds, H, C, D)
+
+    line = {
+        "metric": "GAT+multihop layer fwd+bwd edges/sec; achieved HBM GB/s as % of roofline",
+        "value": E * args.steps / elapsed,
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic: seeded Chung-Lu power-law graph (gamma 2.5), N(0,1) features and gradient probes",
+        "config": {"workload": "c2+c3 layer: collapsed GAT H=4 x C=16 + 3-hop CSR SpMM D=64, forward+backward",
+                   "nodes": n, "edges_nnz": E, "heads": H, "channels": C, "dense_cols": D, "hops": 3,
+                   "max_in_degree": int(torch.diff(rowptr.long()).max())},
+        "layer_GB_s": round(layer_gbs, 1),
+        "layer_roofline_frac": round(layer_gbs / HBM_PEAK_GBS, 4),
+        "algorithmic_bytes_per_step": B["layer"],
+        "breakdown": breakdown,
+        "roofline": {"bound": "hbm", "kernel": kernel_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": bytes_per_launch[dom], "avg_launch_ms": round(dom_ms, 5)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

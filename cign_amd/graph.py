@@ -1,0 +1,325 @@
+"""Graph-format preparation (one-time, outside timed regions) and the fixed
+CSR operator of the reference.
+
+Mirrors:
+  * build_sparse_normalized_adjacency / prepare_gat_edge_index
+    (generic_engine/train_cign.py:1558-1590, 1759-1771) and the PyG utilities
+    they call (to_undirected, add_self_loops, remove_self_loops, degree),
+    restated here with torch ops in the same order;
+  * FixedCSRGraphOperator / prepare_fixed_csr_operator / fixed_sparse_mm /
+    selected_sparse_powers / FixedCSRSpMMFunction (model.py:57-252);
+  * GraphCliffordNet.prepare_fused_gat_graph (generic_engine/model_cign.py:
+    1069-1158) with the fused-GAT graph format (CSR by destination, CSC by
+    source, perm = CSR id of each CSC entry) built from its canonical
+    definition instead of PyG/torch_sparse.
+
+Every SpMM goes to the HIP kernel of libcign_amd (cign_spmm); there is no
+torch.sparse fallback.
+"""
+from __future__ import annotations
+
+from typing import Tuple
+
+import torch
+
+from . import _lib
+from .schedule import RowSchedule, build_row_schedule
+
+# ---------------------------------------------------------------------------
+# PyG-semantics edge utilities (restated).
+# ---------------------------------------------------------------------------
+
+
+def coalesce_edge_index(edge_index: torch.Tensor, num_nodes: int) -> torch.Tensor:
+    """Sort by (row, col) and drop duplicates (PyG ``coalesce`` without values)."""
+    row, col = edge_index[0].long(), edge_index[1].long()
+    key = row * num_nodes + col
+    key = torch.unique(key, sorted=True)
+    return torch.stack([key // num_nodes, key % num_nodes])
+
+
+def to_undirected(edge_index: torch.Tensor, num_nodes: int) -> torch.Tensor:
+    row, col = edge_index[0], edge_index[1]
+    both = torch.stack([torch.cat([row, col]), torch.cat([col, row])])
+    return coalesce_edge_index(both, num_nodes)
+
+
+def add_self_loops(edge_index: torch.Tensor, num_nodes: int) -> torch.Tensor:
+    loop = torch.arange(num_nodes, dtype=edge_index.dtype, device=edge_index.device)
+    return torch.cat([edge_index, torch.stack([loop, loop])], dim=1)
+
+
+def remove_self_loops(edge_index: torch.Tensor) -> torch.Tensor:
+    return edge_index[:, edge_index[0] != edge_index[1]]
+
+
+def degree(index: torch.Tensor, num_nodes: int, dtype=torch.float) -> torch.Tensor:
+    out = torch.zeros(num_nodes, dtype=dtype, device=index.device)
+    return out.scatter_add_(0, index.long(), torch.ones(index.numel(), dtype=dtype, device=index.device))
+
+
+def build_sparse_normalized_adjacency(edge_index: torch.Tensor, num_nodes: int, use_undirected: bool = True,
+                                      add_self_loop: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
+    """A_norm = D^-1/2 (A + I) D^-1/2 as a coalesced COO tensor
+    (generic_engine/train_cign.py:1558-1590)."""
+    if use_undirected:
+        edge_index = to_undirected(edge_index, num_nodes=num_nodes)
+    if add_self_loop:
+        edge_index = add_self_loops(edge_index, num_nodes=num_nodes)
+    row, col = edge_index
+    deg = degree(col, num_nodes=num_nodes, dtype=torch.float)
+    deg_inv_sqrt = deg.clamp(min=1.0).pow(-0.5)
+    edge_weight = deg_inv_sqrt[row] * deg_inv_sqrt[col]
+    adjacency = torch.sparse_coo_tensor(indices=edge_index, values=edge_weight, size=(num_nodes, num_nodes),
+                                        dtype=torch.float).coalesce()
+    return edge_index, adjacency
+
+
+def prepare_gat_edge_index(edge_index: torch.Tensor, num_nodes: int) -> torch.Tensor:
+    """remove + re-add one self-loop per node (generic_engine/train_cign.py:1759-1771)."""
+    return add_self_loops(remove_self_loops(edge_index), num_nodes=num_nodes)
+
+
+# ---------------------------------------------------------------------------
+# Fused-GAT graph format.
+# ---------------------------------------------------------------------------
+
+
+def _compressed(major: torch.Tensor, minor: torch.Tensor, n: int):
+    key = major.long() * n + minor.long()
+    order = torch.sort(key, stable=True).indices
+    ptr = torch.zeros(n + 1, dtype=torch.int64, device=major.device)
+    ptr[1:] = torch.cumsum(torch.bincount(major.long(), minlength=n), 0)
+    return ptr, minor[order].long(), order
+
+
+def to_graph_format(edge_index: torch.Tensor, size=None):
+    """Fused-GAT graph format of a (row -> col) edge list whose rows are the
+    output (destination) nodes: CSR entries sorted by (row, col), CSC entries
+    sorted by (col, row), perm[k] = CSR position of the k-th CSC entry.
+    Returns ((rowptr, col), (row, colptr), perm), all int32. Stable sorting
+    keeps duplicate edges in input order."""
+    n = int(size[0]) if size is not None else int(edge_index.max().item()) + 1
+    r, c = edge_index[0], edge_index[1]
+    rowptr, col, order_csr = _compressed(r, c, n)
+    colptr, row, order_csc = _compressed(c, r, n)
+    pos = torch.empty_like(order_csr)
+    pos[order_csr] = torch.arange(order_csr.numel(), device=order_csr.device)
+    perm = pos[order_csc]
+    i32 = torch.int32
+    return (rowptr.to(i32), col.to(i32)), (row.to(i32), colptr.to(i32)), perm.to(i32)
+
+
+@torch.no_grad()
+def prepare_fused_gat_graph(edge_index: torch.Tensor, num_nodes: int | None = None):
+    """GraphCliffordNet.prepare_fused_gat_graph (generic_engine/model_cign.py:
+    1069-1158): flip source->target to target->source, build the graph format,
+    clone to zero-offset 16-byte aligned storage. Returns
+    ((rowptr, col), (row, colptr), perm)."""
+    if edge_index.dim() != 2 or edge_index.size(0) != 2:
+        raise ValueError(f"edge_index must have shape [2, E], got {tuple(edge_index.shape)}")
+    if num_nodes is None:
+        num_nodes = int(edge_index.max().item()) + 1
+    flipped = edge_index.flip(0).contiguous()
+    (rowptr, col), (row, colptr), perm = to_graph_format(flipped, size=(num_nodes, num_nodes))
+    tensors = [t.clone().contiguous() for t in (rowptr, col, row, colptr, perm)]
+    for name, t in zip(("csr_rowptr", "csr_col", "csc_row", "csc_colptr", "perm"), tensors):
+        if t.storage_offset() != 0:
+            raise RuntimeError(f"{name} storage_offset={t.storage_offset()}, expected 0.")
+        if t.numel() and t.data_ptr() % 16 != 0:
+            raise RuntimeError(f"{name} is not 16-byte aligned (ptr_mod_16={t.data_ptr() % 16}).")
+    rowptr, col, row, colptr, perm = tensors
+    return (rowptr, col), (row, colptr), perm
+
+
+# ---------------------------------------------------------------------------
+# Fixed CSR operator (model.py:57-252).
+# ---------------------------------------------------------------------------
+
+
+class HipCsr:
+    """int32 CSR parts of one sparse operator on its device, plus the row
+    schedule the SpMM kernel runs on and its partial-sum scratch."""
+
+    __slots__ = ("crow", "col", "val", "n", "nnz", "sched", "device")
+
+    def __init__(self, csr: torch.Tensor):
+        if csr.layout != torch.sparse_csr:
+            raise TypeError(f"Expected sparse CSR tensor, got {csr.layout}.")
+        self.crow = csr.crow_indices().to(dtype=torch.int32).clone().contiguous()
+        self.col = csr.col_indices().to(dtype=torch.int32).clone().contiguous()
+        self.val = csr.values().to(dtype=torch.float32).clone().contiguous()
+        self.n = int(csr.shape[0])
+        self.nnz = int(self.val.numel())
+        self.device = csr.device
+        self.sched: RowSchedule = build_row_schedule(self.crow)
+
+    def spmm(self, x: torch.Tensor, add: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+        """out = P x (+ add) on the HIP kernel (current stream)."""
+        lib = _lib.load_library()
+        if x.dim() != 2 or x.size(0) != self.n:
+            raise RuntimeError(f"SpMM input must be [{self.n}, D], got {tuple(x.shape)}")
+        x = x.contiguous()
+        d = int(x.size(1))
+        if out is None:
+            out = torch.empty_like(x)
+        if add is not None:
+            add = add.to(dtype=x.dtype).contiguous()
+        part = scratch_partial(self.sched, d, x.device)
+        lib.call("cign_spmm", _lib.stream_ptr(x.device), _lib.dtype_code(x), self.n, d, self.crow.data_ptr(),
+                 self.col.data_ptr(), self.val.data_ptr(), *self.sched.args(), x.data_ptr(),
+                 _lib.ptr(add), out.data_ptr(), _lib.ptr(part), self.sched.counters.data_ptr())
+        return out
+
+
+def scratch_partial(sched: RowSchedule, d: int, device) -> torch.Tensor | None:
+    if sched.n_seg == 0:
+        return None
+    lib = _lib.load_library()
+    nbytes = int(lib.cign_spmm_partial_bytes(sched.n_seg, d))
+    return torch.empty(max(1, nbytes // 4), dtype=torch.float32, device=device)
+
+
+class FixedCSRSpMMFunction(torch.autograd.Function):
+    """Y = P X, grad_X = P^T grad_Y for a fixed operator (model.py:57-106).
+    The dense operand keeps the reference's dtype rule: it is cast to the
+    operator dtype (float32) and the gradient is returned in the input dtype."""
+
+    @staticmethod
+    def forward(ctx, X: torch.Tensor, operator_csr: torch.Tensor, operator_t_csr: torch.Tensor):
+        if operator_csr.layout != torch.sparse_csr:
+            raise TypeError(f"operator_csr must be sparse CSR, got {operator_csr.layout}")
+        if operator_t_csr.layout != torch.sparse_csr:
+            raise TypeError(f"operator_t_csr must be sparse CSR, got {operator_t_csr.layout}")
+        if operator_csr.dtype != operator_t_csr.dtype:
+            raise TypeError(
+                f"CSR(P) and CSR(P^T) must share dtype, got {operator_csr.dtype} and {operator_t_csr.dtype}")
+        ctx.operator_t_csr = operator_t_csr
+        ctx.input_dtype = X.dtype
+        return _hip_parts(operator_csr).spmm(X.to(dtype=operator_csr.dtype).contiguous())
+
+    @staticmethod
+    def backward(ctx, grad_output: torch.Tensor):
+        grad = _hip_parts(ctx.operator_t_csr).spmm(grad_output.to(dtype=ctx.operator_t_csr.dtype).contiguous())
+        if grad.dtype != ctx.input_dtype:
+            grad = grad.to(ctx.input_dtype)
+        return grad, None, None
+
+
+_HIP_PARTS: dict[int, tuple[object, HipCsr]] = {}
+
+
+def _hip_parts(csr: torch.Tensor) -> HipCsr:
+    """int32 parts + schedule of a sparse CSR tensor, cached per tensor."""
+    import weakref
+
+    key = id(csr)
+    hit = _HIP_PARTS.get(key)
+    if hit is not None and hit[0]() is csr:
+        return hit[1]
+    parts = HipCsr(csr)
+    _HIP_PARTS[key] = (weakref.ref(csr, lambda _r, k=key: _HIP_PARTS.pop(k, None)), parts)
+    return parts
+
+
+class FixedCSRGraphOperator:
+    """Immutable cache holding CSR(P) and CSR(P^T) (model.py:109-133)."""
+
+    __slots__ = ("csr", "csr_t", "shape", "nnz", "dtype", "device", "info")
+
+    def __init__(self, csr: torch.Tensor, csr_t: torch.Tensor):
+        self.csr = csr
+        self.csr_t = csr_t
+        self.shape = tuple(csr.shape)
+        self.nnz = int(csr.values().numel())
+        self.dtype = csr.dtype
+        self.device = csr.device
+        self.info = {
+            "layout": "csr",
+            "shape": self.shape,
+            "nnz": self.nnz,
+            "dtype": str(self.dtype),
+            "device": str(self.device),
+            "csr_crow_contiguous": bool(csr.crow_indices().is_contiguous()),
+            "csr_col_contiguous": bool(csr.col_indices().is_contiguous()),
+            "csr_values_contiguous": bool(csr.values().is_contiguous()),
+            "csr_t_crow_contiguous": bool(csr_t.crow_indices().is_contiguous()),
+            "csr_t_col_contiguous": bool(csr_t.col_indices().is_contiguous()),
+            "csr_t_values_contiguous": bool(csr_t.values().is_contiguous()),
+        }
+
+
+def _clone_csr_storage(csr: torch.Tensor) -> torch.Tensor:
+    return torch.sparse_csr_tensor(csr.crow_indices().clone().contiguous(), csr.col_indices().clone().contiguous(),
+                                   csr.values().clone().contiguous(), size=csr.shape, dtype=csr.dtype,
+                                   device=csr.device)
+
+
+@torch.no_grad()
+def prepare_fixed_csr_operator(operator: torch.Tensor) -> FixedCSRGraphOperator:
+    """COO/CSR operator -> cached CSR(P), CSR(P^T) (model.py:148-186)."""
+    if not isinstance(operator, torch.Tensor):
+        raise TypeError(f"operator must be a torch.Tensor, got {type(operator)!r}")
+    if operator.dim() != 2 or operator.size(0) != operator.size(1):
+        raise ValueError(f"Expected a square 2-D graph operator, got shape={tuple(operator.shape)}")
+    if operator.layout == torch.sparse_coo:
+        coo = operator.coalesce()
+    elif operator.layout == torch.sparse_csr:
+        coo = operator.to_sparse_coo().coalesce()
+    else:
+        raise TypeError("FixedCSRSpMM expects a sparse COO or sparse CSR graph operator; "
+                        f"got layout={operator.layout}.")
+    csr = _clone_csr_storage(coo.to_sparse_csr())
+    idx_t = coo.indices().flip(0).contiguous()
+    coo_t = torch.sparse_coo_tensor(idx_t, coo.values(), size=(coo.size(1), coo.size(0)), dtype=coo.dtype,
+                                    device=coo.device).coalesce()
+    csr_t = _clone_csr_storage(coo_t.to_sparse_csr())
+    return FixedCSRGraphOperator(csr=csr, csr_t=csr_t)
+
+
+def fixed_sparse_mm(operator, X: torch.Tensor) -> torch.Tensor:
+    """One P @ X (model.py:189-199)."""
+    if isinstance(operator, FixedCSRGraphOperator):
+        return FixedCSRSpMMFunction.apply(X, operator.csr, operator.csr_t)
+    if isinstance(operator, torch.Tensor):
+        if operator.layout != torch.sparse_csr:
+            operator = operator.coalesce().to_sparse_csr() if operator.layout == torch.sparse_coo else operator
+        return _hip_parts(operator).spmm(X.to(dtype=operator.dtype).contiguous())
+    raise TypeError(f"Unsupported graph operator type: {type(operator)!r}")
+
+
+def selected_sparse_powers(operator, X: torch.Tensor, powers):
+    """Requested powers of a fixed operator by recurrence, dispatching to the
+    native multihop operators (model.py:202-252)."""
+    from .multihop_csr_pipeline import (GenericMultiHopCSRGraphOperator, HybridNative3TailCSRGraphOperator,
+                                        MultiHopCSR3GraphOperator, generic_multihop_csr,
+                                        hybrid_native3_tail_csr, multihop_csr3)
+
+    requested = {int(power) for power in powers}
+    if not requested:
+        raise ValueError("powers cannot be empty.")
+    if min(requested) < 0:
+        raise ValueError(f"Graph-operator powers must be non-negative, got {sorted(requested)}.")
+    outputs = {}
+    if 0 in requested:
+        outputs[0] = X
+    if isinstance(operator, MultiHopCSR3GraphOperator) and requested == {1, 2, 3}:
+        y1, y2, y3 = multihop_csr3(operator, X)
+        outputs[1], outputs[2], outputs[3] = y1, y2, y3
+        return outputs
+    if isinstance(operator, HybridNative3TailCSRGraphOperator):
+        outputs.update(hybrid_native3_tail_csr(operator, X))
+        if 0 in requested:
+            outputs[0] = X
+        return outputs
+    if isinstance(operator, GenericMultiHopCSRGraphOperator):
+        outputs.update(generic_multihop_csr(operator, X))
+        if 0 in requested:
+            outputs[0] = X
+        return outputs
+    current = X
+    for power in range(1, max(requested) + 1):
+        current = fixed_sparse_mm(operator, current)
+        if power in requested:
+            outputs[power] = current
+    return outputs

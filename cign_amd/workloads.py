@@ -1,0 +1,75 @@
+"""Benchmark workloads (BASELINE configs c2/c3/c5) built through the
+product's host path: seeded Chung-Lu graph -> normalized adjacency
+(build_sparse_normalized_adjacency) -> fixed CSR operator for the SpMM
+pipeline, and the same undirected edge set -> prepare_gat_edge_index ->
+fused-GAT graph format, exactly as generic_engine/train_cign.py:2240-2253
+wires them. Graph preparation runs once on the host; tensors then move to
+the device.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import graph, graphgen
+
+# c2/c3: N = 24,492 nodes, 186,100 directed edges (93,050 undirected pairs),
+# Chung-Lu exponent 2.5, hubs up to ~1,000 in-degree.
+C2 = dict(n=24492, directed=186100, gamma=2.5, max_degree=1100.0, seed=0)
+# c5: N = 2.4M nodes, ~60M directed edges, exponent 2.2, hubs up to ~50K.
+C5 = dict(n=2_400_000, directed=60_000_000, gamma=2.2, max_degree=55_000.0, seed=0)
+
+
+@dataclass
+class Workload:
+    n: int
+    edge_index: torch.Tensor      # [2, E] int64 undirected (both directions), CPU
+    operator: graph.FixedCSRGraphOperator  # P on the device
+    gat_graph: tuple              # ((rowptr, col), (row, colptr), perm) int32 on the device
+    nnz_gat: int                  # CSR nnz of the GAT graph (includes one self-loop per node)
+    nnz_p: int                    # nnz of P (includes self-loops)
+
+
+def _to_device_csr(csr: torch.Tensor, device) -> torch.Tensor:
+    return torch.sparse_csr_tensor(csr.crow_indices().to(device), csr.col_indices().to(device),
+                                   csr.values().to(device), size=csr.shape, device=device)
+
+
+def build(cfg: dict = C2, device="cuda") -> Workload:
+    n = int(cfg["n"])
+    ei = graphgen.chung_lu_directed(n, int(cfg["directed"]), gamma=float(cfg["gamma"]),
+                                    max_degree=float(cfg["max_degree"]), seed=int(cfg["seed"]))
+    edge_index = torch.from_numpy(ei)
+    used, P = graph.build_sparse_normalized_adjacency(edge_index, n)
+    op_cpu = graph.prepare_fixed_csr_operator(P)
+    op = graph.FixedCSRGraphOperator(_to_device_csr(op_cpu.csr, device), _to_device_csr(op_cpu.csr_t, device))
+    gat_ei = graph.prepare_gat_edge_index(used, n)
+    (rowptr, col), (row, colptr), perm = graph.prepare_fused_gat_graph(gat_ei, n)
+    dev_graph = tuple(t.to(device).clone() for t in (rowptr, col, row, colptr, perm))
+    rowptr, col, row, colptr, perm = dev_graph
+    return Workload(n=n, edge_index=edge_index, operator=op, gat_graph=((rowptr, col), (row, colptr), perm),
+                    nnz_gat=int(col.numel()), nnz_p=int(op.nnz))
+
+
+def algorithmic_bytes(n: int, e: int, heads: int, channels: int, d: int, s_gat: int = 4, s_mh: int = 4,
+                      dropout: bool = False) -> dict:
+    """Algorithmic byte counts of one layer forward + backward (streamed
+    arrays once, gathered rows and per-edge scalars per edge; softmax
+    statistics recomputed): collapsed GAT (H heads x C channels, element size
+    s_gat) and the K=3 multihop pipeline over d columns (element size s_mh)."""
+    F = heads * channels
+    H, C, N, E = heads, channels, n, e
+    gat_fwd = 4 * (N + 1) + 4 * E + 4 * N * H + 4 * E * H + s_gat * E * F + 4 * C + 8 * N * C + 8 * N * H
+    gat_bwd = (8 * N * C
+               + (4 * (N + 1) + 8 * E + 12 * E * H + 4 * N * H + 4 * E * C + s_gat * N * F)
+               + (4 * (N + 1) + 4 * E + s_gat * E * F + 4 * N * C + 4 * E * H + 12 * N * H + 4 * N * H + 8 * E * H)
+               + 4 * C)
+    if dropout:
+        gat_fwd += E * H
+        gat_bwd += 2 * E * H
+    spmm = 4 * (N + 1) + 8 * E + s_mh * E * d + s_mh * N * d
+    mh = 6 * spmm + 2 * s_mh * N * d
+    return {"gat_fwd": gat_fwd, "gat_bwd": gat_bwd, "gat": gat_fwd + gat_bwd, "spmm": spmm, "multihop": mh,
+            "layer": gat_fwd + gat_bwd + mh}

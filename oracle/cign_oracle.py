@@ -119,7 +119,9 @@ def normalized_adjacency(edge_index: np.ndarray, n: int, use_undirected: bool = 
         row = np.concatenate([row, loop])
         col = np.concatenate([col, loop])
     deg = np.bincount(col, minlength=n).astype(np.float32)
-    dis = (1.0 / np.sqrt(np.maximum(deg, np.float32(1.0)).astype(np.float64))).astype(np.float32)
+    # torch's float32 pow(x, -0.5) is evaluated as 1 / sqrt(x) with two float32
+    # roundings (not a correctly rounded rsqrt); restated exactly.
+    dis = (np.float32(1.0) / np.sqrt(np.maximum(deg, np.float32(1.0)))).astype(np.float32)
     w = (dis[row] * dis[col]).astype(np.float32)
     pr, pc, pv = coalesce(row, col, n, w)
     return np.stack([row, col]), (pr, pc, pv.astype(np.float32))

@@ -1,0 +1,227 @@
+"""GPU parity of the collapsed GAT (forward + backward) against the oracle,
+through the drop-in API (collapsed_gat.ensure_collapsed_gat_loaded().forward/
+backward and collapsed_gat_mean_bias_silu with autograd), which calls the
+C-ABI. Tolerances: fp32 1e-4 rel / 1e-5 abs; bf16 2e-2 rel. Dropout masks and
+CSR/CSC/perm are bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cign_oracle as O
+from tests.conftest import assert_close, random_gat_graph
+
+pytestmark = pytest.mark.gpu
+TOL = {torch.float32: dict(rtol=1e-4, atol=1e-5), torch.bfloat16: dict(rtol=2e-2, atol=2e-2)}
+
+
+def _graph(rng, n, hubs):
+    ei = random_gat_graph(rng, n, avg_deg=5, hubs=hubs)
+    # also give two nodes a large out-degree (heavy CSC columns)
+    for j in list(hubs)[:2]:
+        extra = np.stack([np.full(min(600, n), j), rng.choice(n, size=min(600, n), replace=False)])
+        ei = np.concatenate([ei, extra], 1)
+    r, c, _ = O.coalesce(ei[0], ei[1], n)
+    return np.stack([r, c])
+
+
+def _dev_graph(ei, n):
+    from cign_amd.graph import prepare_fused_gat_graph
+
+    (rowptr, col), (row, colptr), perm = prepare_fused_gat_graph(torch.from_numpy(ei), n)
+    return tuple(t.cuda() for t in (rowptr, col, row, colptr, perm))
+
+
+def _inputs(rng, n, H, C, dtype):
+    x = torch.from_numpy(rng.standard_normal((n, H, C)).astype(np.float32)).to(dtype).cuda()
+    ar = torch.from_numpy(rng.standard_normal((n, H)).astype(np.float32)).cuda()
+    ac = torch.from_numpy(rng.standard_normal((n, H)).astype(np.float32)).cuda()
+    b = torch.from_numpy(rng.standard_normal(C).astype(np.float32)).cuda()
+    gy = torch.from_numpy(rng.standard_normal((n, C)).astype(np.float32)).to(dtype).cuda()
+    return x, ar, ac, b, gy
+
+
+CASES = [
+    (4, 16, 0.0, torch.float32, 600, {3: 1000, 7: 300}),
+    (4, 16, 0.3, torch.float32, 600, {3: 1000, 7: 300}),
+    (1, 3, 0.0, torch.float32, 500, {1: 900}),
+    (6, 40, 0.2, torch.float32, 400, {0: 700, 2: 260}),
+    (8, 32, 0.0, torch.float32, 256, {5: 513}),
+    (12, 8, 0.1, torch.float32, 200, {9: 257}),
+    (6, 256, 0.0, torch.float32, 300, {4: 800}),
+    (32, 16, 0.1, torch.float32, 64, {}),
+    (2, 5, 0.0, torch.float32, 100, {}),
+    (4, 16, 0.0, torch.bfloat16, 600, {3: 1000}),
+    (4, 32, 0.25, torch.bfloat16, 400, {0: 700}),
+    (6, 256, 0.0, torch.bfloat16, 200, {2: 300}),
+]
+
+
+@pytest.mark.parametrize("H,C,p,dtype,n,hubs", CASES)
+def test_ext_forward_backward_matches_oracle(H, C, p, dtype, n, hubs):
+    from cign_amd.collapsed_gat import ensure_collapsed_gat_loaded
+
+    print(f"gat ext H={H} C={C} p={p} dtype={dtype} n={n}", flush=True)
+    rng = np.random.default_rng(H * 1000 + C)
+    ei = _graph(rng, n, hubs)
+    rowptr, col, row, colptr, perm = _dev_graph(ei, n)
+    x, ar, ac, b, gy = _inputs(rng, n, H, C, dtype)
+    ext = ensure_collapsed_gat_loaded()
+    seed = 0x5EED_1234
+    out, pre, emax, esum, mask = ext.forward(ar, ac, rowptr, col, 0.2, x, b, p, seed)
+    grads = ext.backward(0.2, p, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar, ac, pre, gy)
+    rp, cl = rowptr.cpu().numpy().astype(np.int64), col.cpu().numpy().astype(np.int64)
+    E = cl.size
+    keep = O.gat_dropout_keep(seed, E * H, p).reshape(E, H) if p > 0 else None
+    if p > 0:
+        assert np.array_equal(mask.cpu().numpy() != 0, keep), "dropout mask must be bit-exact"
+    xn, gyn = x.double().cpu().numpy(), gy.double().cpu().numpy()
+    arn, acn, bn = ar.double().cpu().numpy(), ac.double().cpu().numpy(), b.double().cpu().numpy()
+    f = O.collapsed_gat_forward(arn, acn, rp, cl, 0.2, xn, bn, p, keep)
+    g = O.collapsed_gat_backward(arn, acn, rp, cl, 0.2, xn, bn, gyn, p, keep)
+    tol, t32 = TOL[dtype], TOL[torch.float32]
+    assert_close(out.double().cpu().numpy(), f["out"], name="out", **tol)
+    assert_close(pre.cpu().numpy(), f["pre"], name="pre", **t32)
+    assert_close(emax.cpu().numpy(), f["emax"], name="edge_max", **t32)
+    assert_close(esum.cpu().numpy(), f["esum"], name="edge_sum", **t32)
+    gx, gar, gac, gb = grads
+    assert gx.dtype == dtype and gar.dtype == torch.float32
+    assert_close(gx.double().cpu().numpy(), g["grad_feat"], name="grad_feat", **tol)
+    assert_close(gar.cpu().numpy(), g["grad_attn_row"], name="grad_attn_row", **t32)
+    assert_close(gac.cpu().numpy(), g["grad_attn_col"], name="grad_attn_col", **t32)
+    assert_close(gb.cpu().numpy(), g["grad_bias"], name="grad_bias", **t32)
+
+
+@pytest.fixture(scope="module")
+def c2():
+    from cign_amd import workloads
+
+    return workloads.build(workloads.C2, device="cuda")
+
+
+def test_autograd_full_c2(c2):
+    from cign_amd.collapsed_gat import collapsed_gat_mean_bias_silu
+
+    print("gat autograd c2 full size H=4 C=16", flush=True)
+    (rowptr, col), (row, colptr), perm = c2.gat_graph
+    rng = np.random.default_rng(0)
+    n, H, C = c2.n, 4, 16
+    x, ar, ac, b, gy = _inputs(rng, n, H, C, torch.float32)
+    for t in (x, ar, ac, b):
+        t.requires_grad_(True)
+    y = collapsed_gat_mean_bias_silu(ar, ac, (rowptr, col), (row, colptr), perm, 0.2, x, b, 0.0)
+    y.backward(gy)
+    rp, cl = rowptr.cpu().numpy().astype(np.int64), col.cpu().numpy().astype(np.int64)
+    args = (ar.detach().double().cpu().numpy(), ac.detach().double().cpu().numpy(), rp, cl, 0.2,
+            x.detach().double().cpu().numpy(), b.detach().double().cpu().numpy())
+    f = O.collapsed_gat_forward(*args)
+    g = O.collapsed_gat_backward(*args, gy.double().cpu().numpy())
+    t = TOL[torch.float32]
+    assert_close(y.detach().cpu().numpy(), f["out"], name="out", **t)
+    assert_close(x.grad.cpu().numpy(), g["grad_feat"], name="grad_feat", **t)
+    assert_close(ar.grad.cpu().numpy(), g["grad_attn_row"], name="grad_attn_row", **t)
+    assert_close(ac.grad.cpu().numpy(), g["grad_attn_col"], name="grad_attn_col", **t)
+    assert_close(b.grad.cpu().numpy(), g["grad_bias"], name="grad_bias", **t)
+    # Size-independent properties at full size: sum over edges of the softmax
+    # is 1 per (row, head) -> constant features give out = SiLU(mean_h v_h + b).
+    v = torch.from_numpy(rng.standard_normal((1, H, C)).astype(np.float32)).cuda()
+    yc = collapsed_gat_mean_bias_silu(ar.detach(), ac.detach(), (rowptr, col), (row, colptr), perm, 0.2,
+                                      v.expand(n, H, C).contiguous(), b.detach(), 0.0)
+    pre = (v.double().mean(1) + b.detach().double()).cpu().numpy()
+    assert_close(yc.cpu().numpy(), np.broadcast_to(pre / (1 + np.exp(-pre)), (n, C)), name="constant", **t)
+
+
+def test_dropout_seed_stream_matches_reference_formula(c2):
+    import cign_amd.collapsed_gat as cg
+
+    (rowptr, col), (row, colptr), perm = c2.gat_graph
+    rng = np.random.default_rng(1)
+    n, H, C = c2.n, 4, 16
+    x, ar, ac, b, _ = _inputs(rng, n, H, C, torch.float32)
+    torch.manual_seed(1234)
+    start = next(cg._CALL_COUNTER)  # consume one id so the next call uses start + 1
+    seen = []
+    orig = cg._CollapsedGATFn.apply
+
+    def spy(*a):
+        seen.append(a[-1])
+        return orig(*a)
+
+    cg._CollapsedGATFn.apply = spy
+    try:
+        cg.collapsed_gat_mean_bias_silu(ar, ac, (rowptr, col), (row, colptr), perm, 0.2, x, b, 0.5)
+        cg.collapsed_gat_mean_bias_silu(ar, ac, (rowptr, col), (row, colptr), perm, 0.2, x, b, 0.0)
+    finally:
+        cg._CollapsedGATFn.apply = orig
+    assert seen[0] == O.collapsed_gat_seed(1234, start + 1, 0.5)
+    assert seen[1] == 0
+    # The mask drawn with that seed is the reference's bit for bit.
+    ext = cg.ensure_collapsed_gat_loaded()
+    _, _, _, _, mask = ext.forward(ar, ac, rowptr, col, 0.2, x, b, 0.5, seen[0])
+    E = col.numel()
+    assert np.array_equal(mask.cpu().numpy() != 0, O.gat_dropout_keep(seen[0], E * H, 0.5).reshape(E, H))
+
+
+def test_rows_without_edges_and_single_node():
+    from cign_amd.collapsed_gat import ensure_collapsed_gat_loaded
+
+    ext = ensure_collapsed_gat_loaded()
+    n, H, C = 5, 2, 4
+    rowptr = torch.tensor([0, 0, 1, 1, 3, 3], dtype=torch.int32, device="cuda")  # rows 0, 2, 4 empty
+    col = torch.tensor([2, 0, 1], dtype=torch.int32, device="cuda")
+    rng = np.random.default_rng(2)
+    x, ar, ac, b, gy = _inputs(rng, n, H, C, torch.float32)
+    out, pre, emax, esum, _ = ext.forward(ar, ac, rowptr, col, 0.2, x, b, 0.0, 0)
+    assert torch.allclose(pre[0], b) and torch.allclose(pre[2], b) and torch.allclose(pre[4], b)
+    assert float(esum[0, 0]) == 0.0 and float(emax[0, 0]) == float(np.float32(-1.0e38))
+    from cign_amd.graph import to_graph_format
+
+    rows = torch.repeat_interleave(torch.arange(n), torch.diff(rowptr.cpu().long()))
+    (_, _), (row, colptr), perm = to_graph_format(torch.stack([rows, col.cpu().long()]), size=(n, n))
+    gx, gar, gac, gb = ext.backward(0.2, 0.0, rowptr, col, colptr.cuda(), row.cuda(), perm.cuda(), emax, esum,
+                                    torch.empty(3, H, dtype=torch.uint8, device="cuda"), x, ar, ac, pre, gy)
+    g = O.collapsed_gat_backward(ar.double().cpu().numpy(), ac.double().cpu().numpy(), rowptr.cpu().numpy(),
+                                 col.cpu().numpy(), 0.2, x.double().cpu().numpy(), b.double().cpu().numpy(),
+                                 gy.double().cpu().numpy())
+    assert_close(gx.cpu().numpy(), g["grad_feat"], name="gx", **TOL[torch.float32])
+    assert_close(gb.cpu().numpy(), g["grad_bias"], name="gb", **TOL[torch.float32])
+    # One node with its self-loop.
+    one = torch.tensor([0, 1], dtype=torch.int32, device="cuda")
+    z = torch.zeros(1, dtype=torch.int32, device="cuda")
+    x1, ar1, ac1, b1, _ = _inputs(rng, 1, 3, 7, torch.float32)
+    out1, pre1, _, _, _ = ext.forward(ar1, ac1, one, z, 0.2, x1, b1, 0.0, 0)
+    assert_close(pre1.cpu().numpy(), (x1.double().mean(1) + b1.double()).cpu().numpy(), name="one",
+                 **TOL[torch.float32])
+
+
+def test_deterministic_bitwise(c2):
+    from cign_amd.collapsed_gat import ensure_collapsed_gat_loaded
+
+    (rowptr, col), (row, colptr), perm = c2.gat_graph
+    rng = np.random.default_rng(3)
+    x, ar, ac, b, gy = _inputs(rng, c2.n, 4, 16, torch.float32)
+    ext = ensure_collapsed_gat_loaded()
+    r1 = ext.forward(ar, ac, rowptr, col, 0.2, x, b, 0.1, 77)
+    r2 = ext.forward(ar, ac, rowptr, col, 0.2, x, b, 0.1, 77)
+    for a, c in zip(r1, r2):
+        assert torch.equal(a, c)
+    g1 = ext.backward(0.2, 0.1, rowptr, col, colptr, row, perm, r1[2], r1[3], r1[4], x, ar, ac, r1[1], gy)
+    g2 = ext.backward(0.2, 0.1, rowptr, col, colptr, row, perm, r1[2], r1[3], r1[4], x, ar, ac, r1[1], gy)
+    for a, c in zip(g1, g2):
+        assert torch.equal(a, c)
+
+
+def test_argument_errors(c2):
+    from cign_amd.collapsed_gat import collapsed_gat_mean_bias_silu
+
+    (rowptr, col), (row, colptr), perm = c2.gat_graph
+    n = c2.n
+    ar = torch.zeros(n, 33, device="cuda")
+    with pytest.raises(ValueError, match="H<=32"):
+        collapsed_gat_mean_bias_silu(ar, ar, (rowptr, col), (row, colptr), perm, 0.2,
+                                     torch.zeros(n, 33, 4, device="cuda"), torch.zeros(4, device="cuda"), 0.0)
+    with pytest.raises(TypeError):
+        collapsed_gat_mean_bias_silu(ar, ar, (rowptr, col), (row, colptr), perm, 0.2, torch.zeros(n, 4, 4),
+                                     torch.zeros(4), 0.0)
+    with pytest.raises(ValueError, match="bias"):
+        collapsed_gat_mean_bias_silu(ar[:, :4], ar[:, :4], (rowptr, col), (row, colptr), perm, 0.2,
+                                     torch.zeros(n, 4, 4, device="cuda"), None, 0.0)

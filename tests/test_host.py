@@ -1,0 +1,141 @@
+"""CPU tests of the product's host logic: graph preparation (bit-exact
+against the oracle), synthetic generators, row schedules, and the C-ABI
+library (loads, exports every declared symbol; host-only entry points)."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from cign_amd import _lib, graph, graphgen
+from cign_amd.schedule import LIGHT_MAX, SEG_EDGES, build_row_schedule
+from oracle import cign_oracle as O
+from tests.conftest import random_gat_graph
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def test_normalized_adjacency_bit_exact(rng):
+    n = 300
+    ei = np.stack([rng.integers(0, n, 2000), rng.integers(0, n, 2000)])
+    used, P = graph.build_sparse_normalized_adjacency(torch.from_numpy(ei), n)
+    o_used, (pr, pc, pv) = O.normalized_adjacency(ei, n)
+    assert np.array_equal(used.numpy(), o_used)
+    assert np.array_equal(P.indices()[0].numpy(), pr)
+    assert np.array_equal(P.indices()[1].numpy(), pc)
+    assert np.array_equal(P.values().numpy(), pv)
+
+
+def test_fixed_csr_operator_and_transpose(rng):
+    n = 200
+    ei = np.stack([rng.integers(0, n, 900), rng.integers(0, n, 900)])
+    _, P = graph.build_sparse_normalized_adjacency(torch.from_numpy(ei), n)
+    op = graph.prepare_fixed_csr_operator(P)
+    _, (pr, pc, pv) = O.normalized_adjacency(ei, n)
+    rp, c, order = O.csr_from_coo(pr, pc, n)
+    assert np.array_equal(op.csr.crow_indices().numpy(), rp)
+    assert np.array_equal(op.csr.col_indices().numpy(), c)
+    assert np.array_equal(op.csr.values().numpy(), pv[order])
+    trp, tc, tv = O.transpose_csr(rp, c, pv[order], n)
+    assert np.array_equal(op.csr_t.crow_indices().numpy(), trp)
+    assert np.array_equal(op.csr_t.col_indices().numpy(), tc)
+    assert np.array_equal(op.csr_t.values().numpy(), tv.astype(np.float32))
+
+
+def test_gat_graph_format_bit_exact(rng):
+    n = 500
+    ei = random_gat_graph(rng, n, avg_deg=7, hubs={3: 300})
+    # prepare_fused_gat_graph takes PyG source->target edges.
+    (rowptr, col), (row, colptr), perm = graph.prepare_fused_gat_graph(torch.from_numpy(ei), n)
+    o = O.gat_graph_format(ei, n)
+    for got, want in zip((rowptr, col, row, colptr, perm), o):
+        assert got.dtype == torch.int32
+        assert np.array_equal(got.numpy(), want)
+
+
+def test_prepare_gat_edge_index():
+    ei = torch.tensor([[0, 1, 1, 2, 2], [1, 1, 0, 2, 0]])
+    out = graph.prepare_gat_edge_index(ei, 3)
+    assert np.array_equal(out.numpy(), O.gat_edge_index(ei.numpy(), 3))
+    assert out.tolist() == [[0, 1, 2, 0, 1, 2], [1, 0, 0, 0, 1, 2]]
+
+
+def test_chung_lu_c2_shape():
+    ei = graphgen.chung_lu_directed(24492, 186100, gamma=2.5, max_degree=1100, seed=0)
+    assert ei.shape == (2, 186100)
+    assert (ei[0] != ei[1]).all()
+    key = ei[0] * 24492 + ei[1]
+    assert np.unique(key).size == key.size
+    deg = np.bincount(ei[1], minlength=24492)
+    assert (np.diff(deg) <= 0).all()  # relabelled by descending degree
+    assert 900 <= deg.max() <= 1100
+    again = graphgen.chung_lu_directed(24492, 186100, gamma=2.5, max_degree=1100, seed=0)
+    assert np.array_equal(ei, again)
+
+
+def test_uniform_out_degree():
+    ei = graphgen.uniform_out_degree(200, 8, seed=0)
+    assert ei.shape == (2, 1600)
+    assert (ei[0] != ei[1]).all()
+    assert (np.bincount(ei[0], minlength=200) == 8).all()
+
+
+def _sched_host(rowptr):
+    s = build_row_schedule(torch.from_numpy(rowptr), device="cpu")
+    return s, s.buf.numpy()
+
+
+def test_row_schedule_layout(rng):
+    deg = rng.integers(0, 40, 300)
+    deg[5], deg[9], deg[11] = 1000, 257, 65
+    rowptr = np.concatenate([[0], np.cumsum(deg)])
+    s, b = _sched_host(rowptr)
+    assert (s.n_light, s.n_hrow) == ((deg <= LIGHT_MAX).sum(), (deg > LIGHT_MAX).sum())
+    assert s.n_seg == sum(-(-d // SEG_EDGES) for d in deg if d > LIGHT_MAX)
+    assert tuple(b[:4]) == (s.n_light, s.n_seg, s.n_hrow, SEG_EDGES)
+    light = b[4:4 + s.n_light]
+    assert sorted(light.tolist()) == sorted(np.nonzero(deg <= LIGHT_MAX)[0].tolist())
+    assert (np.diff(deg[light]) <= 0).all()
+    off = (4 + s.n_light + 3) & ~3
+    seg = b[off:off + 4 * s.n_seg].reshape(-1, 4)
+    hrow = b[off + 4 * s.n_seg:].reshape(-1, 2)
+    covered = {}
+    for r, beg, end, h in seg:
+        assert rowptr[r] <= beg < end <= rowptr[r + 1] and end - beg <= SEG_EDGES
+        covered.setdefault(r, []).append((beg, end))
+        first, cnt = hrow[h]
+        assert seg[first][0] == r
+    for r, spans in covered.items():
+        spans.sort()
+        assert spans[0][0] == rowptr[r] and spans[-1][1] == rowptr[r + 1]
+        assert all(a[1] == b_[0] for a, b_ in zip(spans, spans[1:]))
+
+
+def test_library_exports_declared_symbols():
+    lib = _lib.load_library(require_gpu=False)
+    header = (ROOT / "include" / "cign_amd.h").read_text()
+    declared = set(re.findall(r"\b(cign_[a-z0-9_]+)\s*\(", header))
+    assert declared, "no declarations parsed"
+    assert declared == set(_lib.exported_symbols()), declared ^ set(_lib.exported_symbols())
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in declared:
+        assert hasattr(raw, name), name
+    assert lib.cign_version() >= 1
+
+
+def test_host_entry_points_reject_bad_arguments():
+    lib = _lib.load_library(require_gpu=False)
+    rp = np.array([0, 2, 1], dtype=np.int64)  # not monotone
+    a, b, c = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    t = ctypes.c_int64()
+    rc = lib.cign_row_schedule_size(rp.ctypes.data, 2, 64, 256, ctypes.byref(a), ctypes.byref(b), ctypes.byref(c),
+                                    ctypes.byref(t))
+    assert rc == 1 and b"monotone" in lib.cign_last_error()
+
+
+def test_product_never_imports_oracle():
+    for p in (ROOT / "cign_amd").rglob("*.py"):
+        text = p.read_text()
+        assert not re.search(r"^\s*(from|import)\s+(\.\.)?oracle", text, re.M), p
+        assert "cign_oracle" not in text, p

@@ -1,0 +1,377 @@
+"""Pins the CPU oracle (oracle/cign_oracle.py) before it is trusted.
+
+Each check is independent of the oracle's own formula: published vectors,
+closed forms, brute-force loops, dense textbook definitions, an independent
+library routine, or finite differences of the oracle's forward (which pins
+the explicitly written backward formulas). CPU only.
+"""
+import numpy as np
+import pytest
+import scipy.special
+import torch
+
+from oracle import cign_oracle as O
+from tests.conftest import assert_close, random_gat_graph
+
+
+# ---------------------------------------------------------------- splitmix64
+def test_splitmix64_published_sequence():
+    # Vigna's splitmix64.c, state seeded with 1234567: first five outputs.
+    seed, golden = 1234567, 0x9E3779B97F4A7C15
+    states = np.array([(seed + k * golden) % 2**64 for k in range(5)], dtype=np.uint64)
+    got = [int(v) for v in O.splitmix64(states)]
+    assert got == [6457827717110365317, 3203168211198807973, 9817491932198370423, 4593380528125082431,
+                   16408922859458223821]
+
+
+def _mix_py(x):
+    m = (1 << 64) - 1
+    x = (x + 0x9E3779B97F4A7C15) & m
+    x = ((x ^ (x >> 30)) * 0xBF58476D1CE4E5B9) & m
+    x = ((x ^ (x >> 27)) * 0x94D049BB133111EB) & m
+    return x ^ (x >> 31)
+
+
+def test_gat_mask_bits_match_integer_restatement():
+    # keep = ((hi + 0.5f) * 2^-32 > p) in float32 (collapsed_gat_cuda.cu:42-45),
+    # restated with Python integers and numpy float32 scalars.
+    seed, p, n = 0x1234_5678_9ABC_DEF0, 0.3, 500
+    keep = O.gat_dropout_keep(seed, n, p)
+    for idx in range(n):
+        r = _mix_py(seed ^ ((idx * 0xD2B74407B1CE6E93) & ((1 << 64) - 1)))
+        u = (np.float32(r >> 32) + np.float32(0.5)) * np.float32(2.0 ** -32)
+        assert bool(u > np.float32(p)) == bool(keep[idx])
+    assert abs(keep.mean() - 0.7) < 0.08
+
+
+def test_block_mask_bits_match_integer_restatement():
+    seed, p, n = 987654321, 0.5, 400
+    keep = O.block_dropout_keep(seed, n, p)
+    for idx in range(n):
+        r = _mix_py(seed ^ ((idx * 0xD2B74407B1CE6E93) & ((1 << 64) - 1)))
+        assert ((r >> 11) * 2.0 ** -53 >= 0.5) == bool(keep[idx])
+    assert O.block_dropout_keep(seed, 10, 0.0).all()
+
+
+def test_seed_formulas():
+    assert O.collapsed_gat_seed(5, 0, 0.0) == 0
+    assert O.collapsed_gat_seed(5, 0, 0.1) == (5 + 0x9E3779B97F4A7C15) & ((1 << 63) - 1)
+    assert O.block_ops_seed(7, 2, 1, 0.2) == (7 + 2 * 0x9E3779B97F4A7C15 + 0xD2B74407B1CE6E93) & ((1 << 63) - 1)
+
+
+# ---------------------------------------------------------------- graph formats
+def test_gat_graph_format_brute_force(rng):
+    n = 40
+    ei = random_gat_graph(rng, n, avg_deg=4)
+    rowptr, col, row, colptr, perm = O.gat_graph_format(ei, n)
+    src, dst = ei
+    edges = sorted(zip(dst.tolist(), src.tolist()))  # CSR: by (dst, src)
+    assert col.tolist() == [s for _, s in edges]
+    assert rowptr.tolist() == [sum(1 for d, _ in edges if d < i) for i in range(n + 1)]
+    cedges = sorted(zip(src.tolist(), dst.tolist()))  # CSC: by (src, dst)
+    assert row.tolist() == [d for _, d in cedges]
+    assert colptr.tolist() == [sum(1 for s, _ in cedges if s < j) for j in range(n + 1)]
+    for k, (s, d) in enumerate(cedges):
+        assert edges[perm[k]] == (d, s)
+
+
+def test_normalized_adjacency_matches_torch_coalesce(rng):
+    n = 60
+    ei = np.stack([rng.integers(0, n, 300), rng.integers(0, n, 300)])
+    used, (pr, pc, pv) = O.normalized_adjacency(ei, n)
+    # Independent check with torch's own COO machinery (reference train_cign.py:1571-1587 ops).
+    e = torch.from_numpy(ei)
+    both = torch.cat([e, e.flip(0)], 1)
+    key = torch.unique(both[0] * n + both[1])
+    und = torch.stack([key // n, key % n])
+    loops = torch.arange(n)
+    full = torch.cat([und, torch.stack([loops, loops])], 1)
+    deg = torch.zeros(n).scatter_add_(0, full[1], torch.ones(full.size(1)))
+    dis = deg.clamp(min=1).pow(-0.5)
+    w = dis[full[0]] * dis[full[1]]
+    P = torch.sparse_coo_tensor(full, w, (n, n)).coalesce()
+    assert np.array_equal(P.indices()[0].numpy(), pr) and np.array_equal(P.indices()[1].numpy(), pc)
+    assert np.array_equal(pv, P.values().numpy()), "P values must be bit-identical"
+    # Symmetric operator and row sums of D^-1/2 (A+I) D^-1/2 against dense math.
+    A = np.zeros((n, n))
+    A[und[0].numpy(), und[1].numpy()] = 1
+    A += np.eye(n)
+    d = A.sum(1)
+    dense = A / np.sqrt(np.outer(d, d))
+    Pd = np.zeros((n, n))
+    Pd[pr, pc] = pv
+    assert_close(Pd, dense, 1e-6, 1e-7, "dense P")
+
+
+def test_transpose_csr(rng):
+    n = 30
+    r, c, v = O.coalesce(rng.integers(0, n, 120), rng.integers(0, n, 120), n, rng.standard_normal(120))
+    rp = np.zeros(n + 1, np.int64)
+    np.add.at(rp, r + 1, 1)
+    rp = np.cumsum(rp)
+    trp, tc, tv = O.transpose_csr(rp, c, v, n)
+    M = O.csr_matrix(rp, c, v, n).toarray()
+    assert_close(O.csr_matrix(trp, tc, tv, n).toarray(), M.T, 0, 0, "P^T")
+
+
+# ---------------------------------------------------------------- SpMM / multihop
+def _circulant(n):
+    # validate_a3v5.py:11-19: offsets {0, +-1, +-7, +-31, +-127}, w = 1/9.
+    offs = [0, 1, -1, 7, -7, 31, -31, 127, -127]
+    rows = np.repeat(np.arange(n), len(offs))
+    cols = (rows + np.tile(offs, n)) % n
+    r, c, v = O.coalesce(rows, cols, n, np.full(len(rows), 1.0 / 9.0))
+    rp = np.zeros(n + 1, np.int64)
+    np.add.at(rp, r + 1, 1)
+    return np.cumsum(rp), c, v, offs
+
+
+def test_spmm_circulant_known_answer(rng):
+    n, d = 512, 8
+    rp, c, v, offs = _circulant(n)
+    x = rng.standard_normal((n, d))
+    expect = sum(np.roll(x, -o, axis=0) for o in offs) / 9.0
+    assert_close(O.spmm(rp, c, v, x), expect, 1e-12, 1e-12, "circulant")
+
+
+def test_multihop_adjoint_and_dense(rng):
+    n, d = 80, 5
+    r, c, v = O.coalesce(rng.integers(0, n, 500), rng.integers(0, n, 500), n, rng.standard_normal(500))
+    rp = np.zeros(n + 1, np.int64)
+    np.add.at(rp, r + 1, 1)
+    rp = np.cumsum(rp)
+    p = (rp, c, v)
+    pt = O.transpose_csr(rp, c, v, n)
+    M = O.csr_matrix(rp, c, v, n).toarray()
+    x = rng.standard_normal((n, d))
+    y = O.multihop3_forward(p, x)
+    for k in range(3):
+        assert_close(y[k], np.linalg.matrix_power(M, k + 1) @ x, 1e-10, 1e-10, f"y{k+1}")
+    g = [rng.standard_normal((n, d)) for _ in range(3)]
+    gx = O.multihop3_backward(pt, *g)
+    lhs = sum((y[k] * g[k]).sum() for k in range(3))
+    assert abs(lhs - (x * gx).sum()) < 1e-9 * max(1, abs(lhs))
+    gen = O.multihop_generic_backward(pt, {1: g[0], 2: g[1], 3: g[2]}, 3, x.shape)
+    assert_close(gen, gx, 1e-12, 1e-12, "generic == native3")
+    fw = O.multihop_generic_forward(p, x, (1, 3, 5))
+    assert_close(fw[5], np.linalg.matrix_power(M, 5) @ x, 1e-9, 1e-9, "P^5")
+
+
+# ---------------------------------------------------------------- collapsed GAT
+def _gat_inputs(rng, n, H, C, deg=5, hubs=None):
+    ei = random_gat_graph(rng, n, avg_deg=deg, hubs=hubs)
+    rowptr, col, row, colptr, perm = O.gat_graph_format(ei, n)
+    return dict(rowptr=rowptr, col=col, x=rng.standard_normal((n, H, C)), ar=rng.standard_normal((n, H)),
+                ac=rng.standard_normal((n, H)), b=rng.standard_normal(C))
+
+
+def test_gat_dense_textbook_single_head(rng):
+    # H=1, p=0: out_i = SiLU(sum_j softmax_j(LeakyReLU(a_dst[i] + a_src[j])) x_j + b)
+    # with the softmax over the in-neighbours j of destination i (dense form).
+    n, C, slope = 25, 3, 0.2
+    d = _gat_inputs(rng, n, 1, C)
+    A = np.zeros((n, n), bool)
+    rows = np.repeat(np.arange(n), np.diff(d["rowptr"]))
+    A[rows, d["col"]] = True
+    S = d["ar"][:, 0][:, None] + d["ac"][:, 0][None, :]
+    S = np.where(S > 0, S, slope * S)
+    S = np.where(A, S, -np.inf)
+    W = scipy.special.softmax(S, axis=1)
+    pre = W @ d["x"][:, 0, :] + d["b"]
+    got = O.collapsed_gat_forward(d["ar"], d["ac"], d["rowptr"], d["col"], slope, d["x"], d["b"])
+    assert_close(got["pre"], pre, 1e-12, 1e-12, "pre")
+    assert_close(got["out"], pre / (1 + np.exp(-pre)), 1e-12, 1e-12, "out")
+
+
+def test_gat_closed_forms(rng):
+    n, H, C = 20, 3, 4
+    d = _gat_inputs(rng, n, H, C)
+    # attn_col = 0: every in-edge of a row has the same score -> uniform
+    # weights, whatever attn_row is. (A swapped row/col operand fails this.)
+    got = O.collapsed_gat_forward(d["ar"], np.zeros((n, H)), d["rowptr"], d["col"], 0.2, d["x"], d["b"])
+    deg = np.diff(d["rowptr"])
+    rows = np.repeat(np.arange(n), deg)
+    mean = np.zeros((n, C))
+    np.add.at(mean, rows, d["x"][d["col"]].mean(axis=1))
+    assert_close(got["pre"], mean / deg[:, None] + d["b"], 1e-12, 1e-12, "uniform")
+    # Only self-loops: softmax == 1.
+    self_only = np.arange(n + 1), np.arange(n)
+    got = O.collapsed_gat_forward(d["ar"], d["ac"], *self_only, 0.2, d["x"], d["b"])
+    assert_close(got["pre"], d["x"].mean(axis=1) + d["b"], 1e-12, 1e-12, "degree 1")
+    assert_close(got["esum"], np.ones((n, H)), 1e-12, 0, "esum")
+    # Empty row: pre = bias, max = -1e38, sum = 0 (collapsed_gat_cuda.cu:87-130).
+    rp = np.concatenate([[0], np.arange(n)])  # row 0 empty
+    got = O.collapsed_gat_forward(d["ar"], d["ac"], rp, np.arange(n - 1), 0.2, d["x"], d["b"])
+    assert_close(got["pre"][0], d["b"], 0, 0, "empty row")
+    assert got["emax"][0, 0] == O.NEG_BIG and got["esum"][0, 0] == 0
+
+
+def test_gat_brute_force_loops(rng):
+    n, H, C, slope, p = 12, 2, 3, 0.15, 0.4
+    d = _gat_inputs(rng, n, H, C, deg=3)
+    E = len(d["col"])
+    keep = rng.random((E, H)) > p
+    got = O.collapsed_gat_forward(d["ar"], d["ac"], d["rowptr"], d["col"], slope, d["x"], d["b"], p, keep)
+    for i in range(n):
+        acc = np.zeros(C)
+        for h in range(H):
+            es = range(d["rowptr"][i], d["rowptr"][i + 1])
+            sc = {e: d["ar"][i, h] + d["ac"][d["col"][e], h] for e in es}
+            sc = {e: (s if s > 0 else s * slope) for e, s in sc.items()}
+            m = max(sc.values())
+            z = sum(np.exp(s - m) for s in sc.values())
+            for e in es:
+                w = np.exp(sc[e] - m) / z
+                w = w / (1 - p) if keep[e, h] else 0.0
+                acc += w * d["x"][d["col"][e], h]
+        assert_close(got["pre"][i], acc / H + d["b"], 1e-12, 1e-12, f"row {i}")
+
+
+@pytest.mark.parametrize("p", [0.0, 0.35])
+def test_gat_backward_finite_differences(rng, p):
+    n, H, C, slope = 18, 3, 4, 0.2
+    d = _gat_inputs(rng, n, H, C, deg=4)
+    E = len(d["col"])
+    keep = rng.random((E, H)) > p if p > 0 else None
+    gy = rng.standard_normal((n, C))
+    g = O.collapsed_gat_backward(d["ar"], d["ac"], d["rowptr"], d["col"], slope, d["x"], d["b"], gy, p, keep)
+
+    def f(ar, ac, x, b):
+        out = O.collapsed_gat_forward(ar, ac, d["rowptr"], d["col"], slope, x, b, p, keep)["out"]
+        return (out * gy).sum()
+
+    base = dict(ar=d["ar"], ac=d["ac"], x=d["x"], b=d["b"])
+    grads = dict(ar=g["grad_attn_row"], ac=g["grad_attn_col"], x=g["grad_feat"], b=g["grad_bias"])
+    eps = 1e-6
+    for name in base:
+        v = rng.standard_normal(base[name].shape)
+        plus = dict(base)
+        minus = dict(base)
+        plus[name] = base[name] + eps * v
+        minus[name] = base[name] - eps * v
+        fd = (f(**plus) - f(**minus)) / (2 * eps)
+        an = (grads[name] * v).sum()
+        assert abs(fd - an) <= 1e-6 * max(1.0, abs(an)), (name, fd, an)
+
+
+# ---------------------------------------------------------------- side ops
+def test_attention_logits_and_head_silu(rng):
+    n, H, C = 7, 3, 5
+    x = rng.standard_normal((n, H, C))
+    a_s, a_d = rng.standard_normal((1, H, C)), rng.standard_normal((1, H, C))
+    s, dd = O.attention_logits_forward(x, a_s, a_d)
+    for i in range(n):
+        for h in range(H):
+            assert abs(s[i, h] - sum(x[i, h, c] * a_s[0, h, c] for c in range(C))) < 1e-12
+            assert abs(dd[i, h] - sum(x[i, h, c] * a_d[0, h, c] for c in range(C))) < 1e-12
+    gs, gd = rng.standard_normal((n, H)), rng.standard_normal((n, H))
+    gx, gas, gad = O.attention_logits_backward(gs, gd, x, a_s, a_d)
+    eps = 1e-6
+    f = lambda x_, s_, d_: (O.attention_logits_forward(x_, s_, d_)[0] * gs).sum() + \
+        (O.attention_logits_forward(x_, s_, d_)[1] * gd).sum()
+    for arg, an in ((0, gx), (1, gas), (2, gad)):
+        base = [x, a_s, a_d]
+        v = rng.standard_normal(base[arg].shape)
+        up = list(base); dn = list(base)
+        up[arg] = base[arg] + eps * v
+        dn[arg] = base[arg] - eps * v
+        assert abs((f(*up) - f(*dn)) / (2 * eps) - (an * v).sum()) < 1e-6
+    out = rng.standard_normal((n, H, C))
+    b = rng.standard_normal(C)
+    y, pre = O.head_silu_forward(out, b)
+    gy = rng.standard_normal((n, C))
+    go, gb = O.head_silu_backward(gy, pre, H)
+    v = rng.standard_normal(out.shape)
+    fd = ((O.head_silu_forward(out + eps * v, b)[0] - O.head_silu_forward(out - eps * v, b)[0]) * gy).sum() / (2 * eps)
+    assert abs(fd - (go * v).sum()) < 1e-6
+    vb = rng.standard_normal(C)
+    fdb = ((O.head_silu_forward(out, b + eps * vb)[0] - O.head_silu_forward(out, b - eps * vb)[0]) * gy).sum() / (2 * eps)
+    assert abs(fdb - (gb * vb).sum()) < 1e-6
+
+
+# ---------------------------------------------------------------- packs
+@pytest.mark.parametrize("interaction", [0, 1, 2])
+@pytest.mark.parametrize("weighting", [0, 1])
+@pytest.mark.parametrize("K", [1, 3, 4])
+def test_pack_backward_finite_differences(rng, interaction, weighting, K):
+    n, D = 6, 5
+    H, C = rng.standard_normal((n, D)), rng.standard_normal((n, D))
+    props = [rng.standard_normal((n, 2 * D)) for _ in range(K)]
+    A = rng.random((n, K))
+    out = O.clifford_pack_forward(H, C, props, A, interaction, weighting)
+    G = rng.standard_normal(out.shape)
+    gH, gC, gP, gA = O.clifford_pack_backward(G, H, C, props, A, interaction, weighting)
+
+    def f(H_, C_, P_, A_):
+        return (O.clifford_pack_forward(H_, C_, P_, A_, interaction, weighting) * G).sum()
+
+    eps = 1e-6
+    for which in range(4):
+        base = [H, C, props, A]
+        an_grad = [gH, gC, gP, gA][which]
+        if which == 2:
+            v = [rng.standard_normal(p.shape) for p in props]
+            up = [p + eps * w for p, w in zip(props, v)]
+            dn = [p - eps * w for p, w in zip(props, v)]
+            an = sum((g * w).sum() for g, w in zip(gP, v))
+        else:
+            v = rng.standard_normal(base[which].shape)
+            up, dn = base[which] + eps * v, base[which] - eps * v
+            an = (an_grad * v).sum()
+        bu, bd = list(base), list(base)
+        bu[which], bd[which] = up, dn
+        fd = (f(*bu) - f(*bd)) / (2 * eps)
+        assert abs(fd - an) <= 1e-6 * max(1.0, abs(an)), (which, fd, an)
+
+
+def test_pack_closed_forms(rng):
+    n, D = 4, 3
+    H, C = rng.standard_normal((n, D)), rng.standard_normal((n, D))
+    P = rng.standard_normal((n, 2 * D))
+    A = np.ones((n, 1))
+    th, tc = P[:, :D], P[:, D:]
+    old = O.clifford_pack_forward(H, C, [P], A, 0, 0)  # validate_a3.py:8-19 legacy_pack
+    z = H * tc
+    assert_close(old, np.concatenate([z - th * C, z / (1 + np.exp(-z))], 1), 1e-12, 1e-12, "old")
+    new = O.clifford_pack_forward(H, C, [P], A, 1, 1)  # validate_cign_acceleration.py:10-18
+    s, a = 0.5 * (H * tc + C * th), 0.5 * (H * tc - C * th)
+    assert_close(new, np.concatenate([s / (1 + np.exp(-s)), a], 1), 1e-12, 1e-12, "new/new")
+    tanh = O.clifford_pack_forward(H, C, [P], A, 2, 0)
+    assert_close(tanh, np.concatenate([np.tanh(a), s / (1 + np.exp(-s))], 1), 1e-12, 1e-12, "tanh/old")
+
+
+# ---------------------------------------------------------------- block ops
+def test_block_ops_against_torch_layer_norm(rng):
+    n, D, eps, p = 9, 7, 1e-5, 0.25
+    x = rng.standard_normal((n, D))
+    w, b = rng.standard_normal(D), rng.standard_normal(D)
+    keep = rng.random((n, D)) >= p
+    y, mu, rs = O.dropout_layernorm_forward(x, w, b, p, eps, keep)
+    xt = torch.tensor(np.where(keep, x / (1 - p), 0.0), requires_grad=True)
+    wt = torch.tensor(w, requires_grad=True)
+    bt = torch.tensor(b, requires_grad=True)
+    yt = torch.nn.functional.layer_norm(xt, (D,), wt, bt, eps)
+    assert_close(y, yt.detach().numpy(), 1e-12, 1e-12, "dropout-LN fwd")
+    gy = rng.standard_normal((n, D))
+    yt.backward(torch.tensor(gy))
+    dx, dw, db = O.dropout_layernorm_backward(gy, x, w, p, eps, keep)
+    assert_close(dx, np.where(keep, xt.grad.numpy() / (1 - p), 0), 1e-10, 1e-12, "dx")
+    assert_close(dw, wt.grad.numpy(), 1e-10, 1e-12, "dw")
+    assert_close(db, bt.grad.numpy(), 1e-10, 1e-12, "db")
+    a, b0 = rng.standard_normal((n, D)), rng.standard_normal((n, D))
+    y2, _, _ = O.add_layernorm_forward(a, b0, w, b, eps)
+    zt = torch.tensor(a + b0, requires_grad=True)
+    y2t = torch.nn.functional.layer_norm(zt, (D,), torch.tensor(w), torch.tensor(b), eps)
+    assert_close(y2, y2t.detach().numpy(), 1e-12, 1e-12, "add-LN fwd")
+    y2t.backward(torch.tensor(gy))
+    dz, _, _ = O.add_layernorm_backward(gy, a, b0, w, eps)
+    assert_close(dz, zt.grad.numpy(), 1e-10, 1e-12, "add-LN dz")
+    h, g, gamma = rng.standard_normal((n, D)), rng.standard_normal((n, D)), rng.standard_normal(D)
+    yr = O.gamma_residual_forward(h, g, gamma, p, keep)
+    assert_close(yr, h + gamma * np.where(keep, g / (1 - p), 0), 1e-12, 1e-12, "gamma residual")
+    gh, gg, ggam = O.gamma_residual_backward(gy, g, gamma, p, keep)
+    eps2 = 1e-6
+    v = rng.standard_normal(D)
+    fd = ((O.gamma_residual_forward(h, g, gamma + eps2 * v, p, keep) -
+           O.gamma_residual_forward(h, g, gamma - eps2 * v, p, keep)) * gy).sum() / (2 * eps2)
+    assert abs(fd - (ggam * v).sum()) < 1e-6
