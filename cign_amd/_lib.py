@@ -29,15 +29,16 @@ _SIGNATURES = {
     "cign_row_schedule_size": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P]),
     "cign_row_schedule_build": (C.c_int, [_P, _I32, _I32, _I32, _P, _I64]),
     "cign_spmm_partial_bytes": (_I64, [_I32, _I32]),
-    "cign_spmm": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P]),
-    "cign_spmm_fwd3": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P]),
-    "cign_spmm_bwd3": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cign_spmm": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cign_spmm_fwd3": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cign_spmm_bwd3": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cign_gat_schedule_params": (C.c_int, [_I32, _I32, _I32, _I32, _P, _P]),
     "cign_gat_fwd_workspace_bytes": (_I64, [_I32, _I32, _I32]),
-    "cign_gat_fwd": (C.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _I32, _I32, _I32, _P, _F32,
-                               _P, _P, _F32, _U64, _P, _P, _P, _P, _P, _P, _I64]),
+    "cign_gat_fwd": (C.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _F32, _P, _P, _F32, _U64,
+                               _P, _P, _P, _P, _P, _P, _I64]),
     "cign_gat_bwd_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32, _I32, _I32]),
-    "cign_gat_bwd": (C.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _F32, _F32] + [_P] * 13
-                     + [_P, _I32, _I32, _I32, _P, _P, _I32, _I32, _I32, _P, _P, _I64, _P, _P, _P, _P]),
+    "cign_gat_bwd": (C.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _F32, _F32] + [_P] * 11
+                     + [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P]),
 }
 
 _LOCK = threading.Lock()

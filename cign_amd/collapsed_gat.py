@@ -16,7 +16,7 @@ import itertools
 import torch
 
 from . import _lib
-from .schedule import cached_row_schedule
+from .schedule import gat_schedule
 
 _EXT = None
 _EXT_ERROR = None
@@ -65,7 +65,9 @@ class _CollapsedGATExt:
         n, H, C = (int(v) for v in in_feat.shape)
         nnz = int(col_ind.numel())
         dev = in_feat.device
-        sched = cached_row_schedule(row_ptr)
+        if in_feat.data_ptr() % 16:
+            in_feat = in_feat.clone()
+        sched = gat_schedule(row_ptr, 0, _lib.dtype_code(in_feat), H, C)
         out = torch.empty((n, C), dtype=in_feat.dtype, device=dev)
         pre = torch.empty((n, C), dtype=torch.float32, device=dev)
         edge_max = torch.empty((n, H), dtype=torch.float32, device=dev)
@@ -74,7 +76,7 @@ class _CollapsedGATExt:
         ws_bytes = int(lib.cign_gat_fwd_workspace_bytes(sched.n_seg, H, C))
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         lib.call("cign_gat_fwd", _lib.stream_ptr(dev), _lib.dtype_code(in_feat), n, nnz, H, C, attn_row.data_ptr(),
-                 attn_col.data_ptr(), row_ptr.data_ptr(), col_ind.data_ptr(), *sched.args(),
+                 attn_col.data_ptr(), col_ind.data_ptr(), *sched.args(),
                  sched.counters.data_ptr(), float(negative_slope), in_feat.data_ptr(), bias.data_ptr(),
                  float(attn_drop), int(seed) & ((1 << 64) - 1), out.data_ptr(), pre.data_ptr(), edge_max.data_ptr(),
                  edge_sum.data_ptr(), edge_mask.data_ptr(), ws.data_ptr(), ws_bytes)
@@ -99,8 +101,9 @@ class _CollapsedGATExt:
         n, H, C = (int(v) for v in in_feat.shape)
         nnz = int(col_ind.numel())
         dev = in_feat.device
-        rs = cached_row_schedule(row_ptr)
-        cs = cached_row_schedule(col_ptr)
+        code = _lib.dtype_code(in_feat)
+        rs = gat_schedule(row_ptr, 1, code, H, C)
+        cs = gat_schedule(col_ptr, 1, code, H, C)
         row_blocks = rs.n_seg + (rs.n_light + 3) // 4
         ws_bytes = int(lib.cign_gat_bwd_workspace_bytes(n, nnz, H, C, row_blocks, rs.n_seg, cs.n_seg))
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
@@ -109,7 +112,7 @@ class _CollapsedGATExt:
         grad_attn_col = torch.empty_like(attn_col)
         grad_bias = torch.empty((C,), dtype=torch.float32, device=dev)
         lib.call("cign_gat_bwd", _lib.stream_ptr(dev), _lib.dtype_code(in_feat), n, nnz, H, C, float(negative_slope),
-                 float(attn_drop), row_ptr.data_ptr(), col_ind.data_ptr(), col_ptr.data_ptr(), row_ind.data_ptr(),
+                 float(attn_drop), col_ind.data_ptr(), row_ind.data_ptr(),
                  permute.data_ptr(), edge_max.data_ptr(), edge_sum.data_ptr(), edge_mask.data_ptr(),
                  in_feat.data_ptr(), attn_row.data_ptr(), attn_col.data_ptr(), pre.data_ptr(), grad_y.data_ptr(),
                  *rs.args(), rs.counters.data_ptr(), *cs.args(), cs.counters.data_ptr(), ws.data_ptr(), ws_bytes,
@@ -155,8 +158,11 @@ class _CollapsedGATFn(torch.autograd.Function):
         in_feat = in_feat.contiguous()
         bias = bias.contiguous()
         # Schedules are keyed on the graph tensors the caller holds; build the
-        # column schedule now so the backward never synchronises.
-        cached_row_schedule(colptr)
+        # backward's schedules now so the backward never synchronises.
+        code = _lib.dtype_code(in_feat)
+        H, C = int(in_feat.size(1)), int(in_feat.size(2))
+        gat_schedule(rowptr, 1, code, H, C)
+        gat_schedule(colptr, 1, code, H, C)
         y, pre, edge_max, edge_sum, edge_mask = ext.forward(attn_row, attn_col, rowptr, col, float(negative_slope),
                                                             in_feat, bias, float(attn_drop), int(seed))
         ctx.save_for_backward(rowptr, col, colptr, row, perm, edge_max, edge_sum, edge_mask, in_feat, attn_row,

@@ -10,6 +10,8 @@ CIGN_GAT_DECLARE(float, 32)
 CIGN_GAT_DECLARE(bf16, 4)
 CIGN_GAT_DECLARE(bf16, 8)
 CIGN_GAT_DECLARE(bf16, 32)
+CIGN_GAT_FL_DECLARE(float)
+CIGN_GAT_FL_DECLARE(bf16)
 }  // namespace gatk
 }  // namespace cign
 
@@ -41,7 +43,7 @@ int dispatch_hc(int H, int C, Args&&... args) {
 }
 
 struct BwdLayout {
-  int64_t grad_pre, gscore, bias_part, bias_l2, part_row, part_col, total;
+  int64_t grad_pre, gscore, wsum, bias_part, bias_l2, part_row, part_col, total;
 };
 
 inline int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
@@ -52,9 +54,10 @@ inline BwdLayout bwd_layout(int n, int nnz, int H, int C, int row_blocks, int n_
   int64_t off = 0;
   L.grad_pre = off; off = align256(off + 4LL * n * C);
   L.gscore = off; off = align256(off + 4LL * nnz * H);
+  L.wsum = off; off = align256(off + 4LL * n * H);
   L.bias_part = off; off = align256(off + 4LL * row_blocks * C);
   L.bias_l2 = off; off = align256(off + 4LL * n_l2 * C);
-  L.part_row = off; off = align256(off + 4LL * n_seg_rows * H);
+  L.part_row = off; off = align256(off + 4LL * n_seg_rows * 3 * H);
   L.part_col = off; off = align256(off + 4LL * n_seg_cols * (static_cast<int64_t>(H) * C + H));
   L.total = off;
   return L;
@@ -69,6 +72,46 @@ int check_shape(const char* who, int n, int nnz, int H, int C) {
   return kOk;
 }
 
+__global__ void zero_floats(float* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+
+// Feature-layout forward eligibility (shape only): H <= 8 heads, C a
+// multiple of the 16-byte chunk width, H*C <= 64 chunks.
+inline bool fl_forward_ok(int dtype, int H, int C) {
+  const int W = dtype == kBF16 ? 8 : 4;
+  return H <= kFlHeads && C % W == 0 && (H * C) / W <= kWave;
+}
+
+// Schedule geometry (light_max, seg_edges) each GAT pass runs on.
+inline void gat_geometry(int pass, int dtype, int H, int C, int& light, int& seg) {
+  if (pass == 0 && fl_forward_ok(dtype, H, C)) {
+    light = 64;
+    seg = 256;
+  } else {
+    light = kGatLight;
+    seg = kGatSeg;
+  }
+}
+
+// Host view of a schedule header (schedule.h).
+struct Hdr {
+  int n_light, n_seg, n_hrow;
+};
+
+inline int read_hdr(const char* who, const int32_t* info, int n, int light, int seg, Hdr& h) {
+  if (!info) return set_error(kInvalid, "%s: null schedule header", who);
+  h.n_light = info[0];
+  h.n_seg = info[1];
+  h.n_hrow = info[2];
+  if (h.n_light + h.n_hrow != n) return set_error(kInvalid, "%s: schedule does not cover %d rows", who, n);
+  if (info[4] != light || info[3] != seg)
+    return set_error(kInvalid, "%s: schedule built with light_max=%d seg_edges=%d; this pass needs %d/%d "
+                     "(cign_gat_schedule_params)", who, info[4], info[3], light, seg);
+  return kOk;
+}
+
 }  // namespace gatk
 }  // namespace cign
 
@@ -77,6 +120,18 @@ using namespace cign::gatk;
 
 extern "C" {
 
+// Schedule geometry (light_max, seg_edges) the GAT pass (0 = forward on the
+// CSR, 1 = backward on the CSR and the CSC) needs for this dtype / shape.
+int cign_gat_schedule_params(int32_t pass, int32_t dtype, int32_t heads, int32_t channels, int32_t* light_max,
+                             int32_t* seg_edges) {
+  if (!light_max || !seg_edges) return set_error(kInvalid, "cign_gat_schedule_params: null output");
+  int l, s;
+  gat_geometry(pass, dtype, heads, channels, l, s);
+  *light_max = l;
+  *seg_edges = s;
+  return kOk;
+}
+
 // fp32 workspace needed by cign_gat_fwd for a row schedule with n_seg segments.
 int64_t cign_gat_fwd_workspace_bytes(int32_t n_seg, int32_t heads, int32_t channels) {
   return 4LL * n_seg * (static_cast<int64_t>(heads) * channels + 2LL * heads);
@@ -84,35 +139,48 @@ int64_t cign_gat_fwd_workspace_bytes(int32_t n_seg, int32_t heads, int32_t chann
 
 // Collapsed GAT forward. Replaces the ext `forward` of the reference
 // (collapsed_gat_ext/collapsed_gat.cpp:45-72 -> collapsed_gat_cuda.cu:434-478).
-// attn_row/attn_col [n,H] fp32, rowptr [n+1]/col [nnz] int32 (CSR by
-// destination), in_feat [n,H,C] (dtype), bias [C] fp32. Outputs: out [n,C]
-// (dtype), pre [n,C] fp32, edge_max/edge_sum [n,H] fp32, edge_mask [nnz,H] u8
-// (written only when attn_drop > 0). row_sched: schedule of rowptr.
 int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
-                 const float* attn_row, const float* attn_col, const int32_t* rowptr, const int32_t* col,
-                 const int32_t* row_sched, int32_t n_light, int32_t n_seg, int32_t n_hrow, int32_t* row_counters,
-                 float negative_slope, const void* in_feat, const float* bias, float attn_drop, uint64_t seed,
-                 void* out, float* pre, float* edge_max, float* edge_sum, uint8_t* edge_mask, void* workspace,
-                 int64_t workspace_bytes) {
+                 const float* attn_row, const float* attn_col, const int32_t* col, const int32_t* row_sched,
+                 const int32_t* row_sched_info, int32_t* row_counters, float negative_slope, const void* in_feat,
+                 const float* bias, float attn_drop, uint64_t seed, void* out, float* pre, float* edge_max,
+                 float* edge_sum, uint8_t* edge_mask, void* workspace, int64_t workspace_bytes) {
   int rc = check_shape("cign_gat_fwd", n, nnz, heads, channels);
   if (rc) return rc;
   if (!(attn_drop >= 0.0f && attn_drop < 1.0f)) return set_error(kInvalid, "cign_gat_fwd: attn_drop must be in [0,1)");
-  if (n_light + n_hrow != n) return set_error(kInvalid, "cign_gat_fwd: schedule does not cover %d rows", n);
-  if (workspace_bytes < cign_gat_fwd_workspace_bytes(n_seg, heads, channels))
+  Hdr hd;
+  int light, seg;
+  gat_geometry(0, dtype, heads, channels, light, seg);
+  if ((rc = read_hdr("cign_gat_fwd", row_sched_info, n, light, seg, hd))) return rc;
+  if (workspace_bytes < cign_gat_fwd_workspace_bytes(hd.n_seg, heads, channels))
     return set_error(kInvalid, "cign_gat_fwd: workspace too small");
   if (n == 0) return kOk;
-  const Sched s = make_sched(row_sched, n_light, n_seg, n_hrow);
+  const Sched s = make_sched(row_sched, hd.n_light, hd.n_seg, hd.n_hrow);
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto fill = [&](auto* xt, auto* ot) {
     using T = std::remove_cv_t<std::remove_pointer_t<decltype(ot)>>;
     GatFwdArgs<T> a;
     a.n = n; a.H = heads; a.C = channels;
-    a.slope = negative_slope; a.p = attn_drop; a.inv_keep = attn_drop > 0.0f ? 1.0f / (1.0f - attn_drop) : 1.0f;
-    a.seed = seed;
+    a.slope = negative_slope; a.p = attn_drop; a.seed = seed;
     a.vec = aligned16(xt) && (channels * static_cast<int>(sizeof(T))) % 16 == 0;
-    a.attn_row = attn_row; a.attn_col = attn_col; a.rowptr = rowptr; a.col = col;
+    a.attn_row = attn_row; a.attn_col = attn_col; a.col = col;
     a.x = xt; a.bias = bias; a.out = ot; a.pre = pre; a.emax = edge_max; a.esum = edge_sum;
     a.mask = edge_mask; a.partial = static_cast<float*>(workspace); a.counters = row_counters;
+    if (fl_forward_ok(dtype, heads, channels)) {
+      if (!aligned16(xt) || !aligned16(ot))
+        return set_error(kInvalid, "cign_gat_fwd: in_feat and out must be 16-byte aligned");
+      const int W = dtype == kBF16 ? 8 : 4;
+      int L = 1;
+      while (L < heads * channels / W) L <<= 1;
+      switch (L) {
+        case 1: return FwdFlLauncher<T, 1>::run(st, a, s, row_sched_info);
+        case 2: return FwdFlLauncher<T, 2>::run(st, a, s, row_sched_info);
+        case 4: return FwdFlLauncher<T, 4>::run(st, a, s, row_sched_info);
+        case 8: return FwdFlLauncher<T, 8>::run(st, a, s, row_sched_info);
+        case 16: return FwdFlLauncher<T, 16>::run(st, a, s, row_sched_info);
+        case 32: return FwdFlLauncher<T, 32>::run(st, a, s, row_sched_info);
+        default: return FwdFlLauncher<T, 64>::run(st, a, s, row_sched_info);
+      }
+    }
     return dispatch_hc<FwdLauncher, T>(heads, channels, st, a, s);
   };
   if (dtype == kF32) return fill(static_cast<const float*>(in_feat), static_cast<float*>(out));
@@ -127,32 +195,32 @@ int64_t cign_gat_bwd_workspace_bytes(int32_t n, int32_t nnz, int32_t heads, int3
 
 // Collapsed GAT backward. Replaces the ext `backward` of the reference
 // (collapsed_gat_ext/collapsed_gat.cpp:74-102 -> collapsed_gat_cuda.cu:480-545).
-// Needs the CSR schedule (rows) and the CSC schedule (colptr) plus their
-// counters; the CSC counter array must have n_hrow_cols + 1 entries.
 int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
-                 float negative_slope, float attn_drop, const int32_t* rowptr, const int32_t* col,
-                 const int32_t* colptr, const int32_t* rowind, const int32_t* perm, const float* edge_max,
-                 const float* edge_sum, const uint8_t* edge_mask, const void* in_feat, const float* attn_row,
-                 const float* attn_col, const float* pre, const void* grad_y, const int32_t* row_sched,
-                 int32_t r_light, int32_t r_seg, int32_t r_hrow, int32_t* row_counters, const int32_t* col_sched,
-                 int32_t c_light, int32_t c_seg, int32_t c_hrow, int32_t* col_counters, void* workspace,
-                 int64_t workspace_bytes, void* grad_feat, float* grad_attn_row, float* grad_attn_col,
-                 float* grad_bias) {
+                 float negative_slope, float attn_drop, const int32_t* col, const int32_t* rowind,
+                 const int32_t* perm, const float* edge_max, const float* edge_sum, const uint8_t* edge_mask,
+                 const void* in_feat, const float* attn_row, const float* attn_col, const float* pre,
+                 const void* grad_y, const int32_t* row_sched, const int32_t* row_sched_info,
+                 int32_t* row_counters, const int32_t* col_sched, const int32_t* col_sched_info,
+                 int32_t* col_counters, void* workspace, int64_t workspace_bytes, void* grad_feat,
+                 float* grad_attn_row, float* grad_attn_col, float* grad_bias) {
   int rc = check_shape("cign_gat_bwd", n, nnz, heads, channels);
   if (rc) return rc;
   if (!(attn_drop >= 0.0f && attn_drop < 1.0f)) return set_error(kInvalid, "cign_gat_bwd: attn_drop must be in [0,1)");
-  if (r_light + r_hrow != n || c_light + c_hrow != n)
-    return set_error(kInvalid, "cign_gat_bwd: schedules do not cover %d rows/columns", n);
-  const Sched rs = make_sched(row_sched, r_light, r_seg, r_hrow);
-  const Sched cs = make_sched(col_sched, c_light, c_seg, c_hrow);
+  Hdr rh, ch;
+  int light, seg;
+  gat_geometry(1, dtype, heads, channels, light, seg);
+  if ((rc = read_hdr("cign_gat_bwd (rows)", row_sched_info, n, light, seg, rh))) return rc;
+  if ((rc = read_hdr("cign_gat_bwd (cols)", col_sched_info, n, light, seg, ch))) return rc;
+  const Sched rs = make_sched(row_sched, rh.n_light, rh.n_seg, rh.n_hrow);
+  const Sched cs = make_sched(col_sched, ch.n_light, ch.n_seg, ch.n_hrow);
   const int row_blocks = sched_blocks(rs);
-  const BwdLayout L = bwd_layout(n, nnz, heads, channels, row_blocks, r_seg, c_seg);
+  const BwdLayout L = bwd_layout(n, nnz, heads, channels, row_blocks, rh.n_seg, ch.n_seg);
   if (workspace_bytes < L.total) return set_error(kInvalid, "cign_gat_bwd: workspace too small (%lld < %lld)",
                                                   static_cast<long long>(workspace_bytes), static_cast<long long>(L.total));
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (n == 0) {
-    const hipError_t e = hipMemsetAsync(grad_bias, 0, sizeof(float) * channels, st);
-    return e == hipSuccess ? kOk : set_error(kHipError, "cign_gat_bwd: %s", hipGetErrorString(e));
+    hipLaunchKernelGGL(zero_floats, dim3((channels + kBlock - 1) / kBlock), dim3(kBlock), 0, st, grad_bias, channels);
+    return check_launch("cign_gat_bwd");
   }
   char* ws = static_cast<char*>(workspace);
   auto fill = [&](auto* xt, auto* gyt, auto* gxt) {
@@ -162,12 +230,12 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
     a.slope = negative_slope; a.p = attn_drop; a.inv_h = 1.0f / static_cast<float>(heads);
     a.vec_x = aligned16(xt) && (channels * static_cast<int>(sizeof(T))) % 16 == 0;
     a.vec_gp = (channels % 4) == 0;
-    a.vec_gx = aligned16(gxt) && (channels * static_cast<int>(sizeof(T))) % 16 == 0;
-    a.rowptr = rowptr; a.col = col; a.colptr = colptr; a.rowind = rowind; a.perm = perm;
+    a.col = col; a.rowind = rowind; a.perm = perm;
     a.emax = edge_max; a.esum = edge_sum; a.mask = edge_mask; a.x = xt;
     a.attn_row = attn_row; a.attn_col = attn_col; a.pre = pre; a.grad_y = gyt;
     a.grad_pre = reinterpret_cast<float*>(ws + L.grad_pre);
     a.gscore = reinterpret_cast<float*>(ws + L.gscore);
+    a.wsum = reinterpret_cast<float*>(ws + L.wsum);
     a.bias_part = reinterpret_cast<float*>(ws + L.bias_part);
     a.bias_l2 = reinterpret_cast<float*>(ws + L.bias_l2);
     a.part_row = reinterpret_cast<float*>(ws + L.part_row);

@@ -1,4 +1,4 @@
-// Collapsed multi-head GAT (concat=False) for gfx950: edge score, per
+// Collapsed multi-head GAT (concat=False) kernels for gfx950: edge score, per
 // destination edge softmax, edge dropout, weighted aggregation and the fused
 // head-mean + bias + SiLU epilogue, forward and backward.
 //
@@ -9,19 +9,30 @@
 //   s_eh   = exp(sc - max_h) / sum_h (softmax over the in-edges of i),
 //   w_eh   = s_eh * keep_eh / (1 - p)   (keep_eh = splitmix64 bit, p > 0),
 //   pre_ic = (1/H) sum_h sum_e w_eh x[j,h,c] + bias_c,  out = SiLU(pre).
-// edge_max / edge_sum [N,H] are saved for the backward, and the mask [E,H]
-// is in CSR edge order (written only when p > 0, like the reference).
+// edge_max / edge_sum [N,H] are saved for the backward; the mask [E,H] is in
+// CSR edge order (written only when p > 0, like the reference).
 //
-// Design (own, MI355X-first): a lane owns one (edge, head) pair; the head
+// Design (own, MI355X-first). A lane owns one (edge, head) pair: the head
 // count is padded to HP = 2^k so lane = el * HP + h and every reduction over
-// edges is an xor-butterfly over lane bits >= log2(HP). Channels are handled
-// in blocks of CP <= 32 consecutive values per lane (16-byte loads when the
-// row layout allows). The backward is two kernels instead of five:
-//   gat_bwd_rows (CSR): g_pre = g_y * SiLU'(pre), per-edge g_w = <g_pre, x>/H,
-//     softmax + LeakyReLU backward, grad_attn_row; g_raw kept for kernel 2.
-//   gat_bwd_cols (CSC): grad_feat, grad_attn_col (no atomics), plus the
+// the edges of a row is an xor-butterfly over lane bits >= log2(HP). Channels
+// are handled in blocks of CP <= 32 consecutive values per lane (16-byte loads
+// when the row layout allows). A wavefront takes at most 16 edges of a row
+// (N = 16 / EPW tiles of EPW = 64 / HP edges per lane, N selected at run time
+// from the row's degree), issuing every load of the row before consuming any
+// (indices clamped to a valid edge and head, results masked): a row costs one
+// memory round per level of indirection, with a small register footprint.
+//
+// The backward is two kernels (the reference uses five):
+//   gat_bwd_rows (CSR, one pass): g_pre = g_y * SiLU'(pre); per edge
+//     ge' = keep/(1-p) * <g_pre, x[j,h,:]>/H (stored), s, l' = LeakyReLU';
+//     per row and head wsum = sum s ge', A = sum s ge' l', B = sum s l', so
+//     grad_attn_row = sum_e s (ge' - wsum) l' = A - wsum * B and wsum is saved;
+//   gat_bwd_cols (CSC): g_raw = s (ge' - wsum[i]) l' per edge, grad_attn_col =
+//     sum g_raw (no atomics), grad_feat = sum_e w g_pre[i] / H, plus the
 //     deterministic two-level grad_bias reduction in dedicated workgroups.
-// Heavy rows/columns use the segmented schedule of schedule.h.
+// Rows/columns with more than 16 edges use 64-edge segments of the schedule
+// (schedule.h, built with light_max = 16, seg_edges = 64), one workgroup
+// each, multi-segment rows merged by the last workgroup to finish.
 #pragma once
 
 #include <type_traits>
@@ -115,15 +126,30 @@ __device__ __forceinline__ void load_run(const T* p, int nvalid, bool vec, float
   }
 }
 
+// Lane geometry of the (edge, head) layout.
+template <int HP>
+struct Lanes {
+  static constexpr int LGH = ilog2c(HP);
+  static constexpr int EPW = kWave / HP;
+  int lane, h, el, hc;  // hc: head clamped to a valid head for loads
+  bool hv;
+  __device__ __forceinline__ explicit Lanes(int H) {
+    lane = lane_id();
+    h = lane & (HP - 1);
+    el = lane >> LGH;
+    hv = h < H;
+    hc = hv ? h : H - 1;
+  }
+};
+
 template <typename T>
 struct GatFwdArgs {
   int n, H, C;
-  float slope, p, inv_keep;
+  float slope, p;
   uint64_t seed;
   bool vec;  // 16-byte loads of x rows are legal
   const float* attn_row;
   const float* attn_col;
-  const int32_t* rowptr;
   const int32_t* col;
   const T* x;
   const float* bias;
@@ -136,35 +162,125 @@ struct GatFwdArgs {
   int32_t* counters;
 };
 
+// Calls f(std::integral_constant<int, n>) for a wave-uniform n in [1, NMAX],
+// so a row's tile count selects a fully unrolled, branch-free body.
+template <int K, int NMAX, typename F>
+__device__ __forceinline__ void dispatch_n(int n, F& f) {
+  if constexpr (K <= NMAX) {
+    if (n == K) {
+      f(std::integral_constant<int, K>{});
+      return;
+    }
+    dispatch_n<K + 1, NMAX>(n, f);
+  }
+}
+
+// Schedule geometry of the GAT kernels: a wavefront handles at most
+// kGatLight = 16 edges of a row (NTL = 16 / EPW tiles per lane, 1 for H <= 4),
+// rows with more edges go to 64-edge segments (one 16-edge tile per wave).
+constexpr int kGatLight = 16;
+constexpr int kGatSeg = kWavesPerBlock * kGatLight;
+template <int HP>
+constexpr int kNTL = Lanes<HP>::EPW >= kGatLight ? 1 : kGatLight / Lanes<HP>::EPW;
+
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
-// One 64-edge tile for one wave: scores into registers, local (m, s) per head.
-template <typename T, int HP>
-__device__ __forceinline__ void fwd_scores(const GatFwdArgs<T>& a, int row, int eb, int ee, float adst, int h,
-                                           int el, bool hv, int (&jR)[HP], float (&scR)[HP], float& m,
-                                           float& s) {
-  constexpr int EPW = kWave / HP;
-  m = kNegBig;
-  s = 0.0f;
+// The lane's N tiles of a wave's edges [eb, ee): indices, scores and (when it
+// fits in registers) the first channel block of x, all loads issued before
+// any result is consumed (indices clamped to a valid edge / head).
+template <typename T, int HP, int CP, int N>
+struct FwdWave {
+  static constexpr bool kPrefetch = N * CP <= 32;
+  int t[N], j[N];
+  float sc[N];
+  bool v[N];
+  float x0[kPrefetch ? N : 1][CP];
+
+  __device__ __forceinline__ void load(const GatFwdArgs<T>& a, const Lanes<HP>& L, int eb, int ee, float adst) {
+    if (ee <= eb) {
+      // No edges (wave-uniform): nothing is read; eb may equal nnz here.
 #pragma unroll
-  for (int k = 0; k < HP; ++k) {
-    const int t = eb + el + k * EPW;
-    jR[k] = 0;
-    scR[k] = kNegBig;
-    if (hv && t < ee) {
-      const int j = a.col[t];
-      jR[k] = j;
-      scR[k] = leaky(adst + a.attn_col[static_cast<int64_t>(j) * a.H + h], a.slope);
-      m = fmaxf(m, scR[k]);
+      for (int k = 0; k < N; ++k) {
+        t[k] = eb;
+        v[k] = false;
+        j[k] = 0;
+        sc[k] = kNegBig;
+        if constexpr (kPrefetch)
+#pragma unroll
+          for (int c = 0; c < CP; ++c) x0[k][c] = 0.0f;
+      }
+      return;
+    }
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      t[k] = eb + L.el + k * Lanes<HP>::EPW;
+      v[k] = L.hv && t[k] < ee;
+      j[k] = a.col[t[k] < ee ? t[k] : eb];
+    }
+    if constexpr (kPrefetch) {
+      const int nvalid = min(CP, a.C);
+#pragma unroll
+      for (int k = 0; k < N; ++k)
+        load_run<T, CP>(a.x + (static_cast<int64_t>(j[k]) * a.H + L.hc) * a.C, nvalid, a.vec, x0[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < N; ++k) sc[k] = leaky(adst + a.attn_col[static_cast<int64_t>(j[k]) * a.H + L.hc], a.slope);
+  }
+
+  // Lane-local softmax statistics.
+  __device__ __forceinline__ void stats(float& m, float& s) const {
+    m = kNegBig;
+#pragma unroll
+    for (int k = 0; k < N; ++k) m = v[k] ? fmaxf(m, sc[k]) : m;
+    s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < N; ++k) s += v[k] ? expf(sc[k] - m) : 0.0f;
+  }
+
+  // Weight of one (edge, head): normalised softmax, or exp(sc - M) for a
+  // segment partial, times keep / (1 - p); records the mask on block 0.
+  __device__ __forceinline__ float weight(const GatFwdArgs<T>& a, int k, int h, float M, float S, bool normalise,
+                                         bool write_mask) const {
+    if (!v[k]) return 0.0f;
+    bool keep = true;
+    if (a.p > 0.0f) {
+      const int64_t idx = static_cast<int64_t>(t[k]) * a.H + h;
+      keep = gat_keep(a.seed, static_cast<uint64_t>(idx), a.p);
+      if (write_mask) a.mask[idx] = keep ? 1 : 0;
+    }
+    if (!keep || (normalise && !(S > 0.0f))) return 0.0f;
+    float w = expf(sc[k] - M);
+    if (normalise) w = w / S;
+    if (a.p > 0.0f) w = w / (1.0f - a.p);
+    return w;
+  }
+
+  // acc[c] = sum over the lane's edges of w * x[j, h, cb*CP + c].
+  __device__ __forceinline__ void accumulate(const GatFwdArgs<T>& a, const Lanes<HP>& L, int cb, float M, float S,
+                                             bool normalise, float (&acc)[CP]) const {
+#pragma unroll
+    for (int c = 0; c < CP; ++c) acc[c] = 0.0f;
+    float xv[N][CP];
+    if (kPrefetch && cb == 0) {
+#pragma unroll
+      for (int k = 0; k < N; ++k)
+#pragma unroll
+        for (int c = 0; c < CP; ++c) xv[k][c] = x0[kPrefetch ? k : 0][c];
+    } else {
+      const int nvalid = min(CP, a.C - cb * CP);
+#pragma unroll
+      for (int k = 0; k < N; ++k)
+        load_run<T, CP>(a.x + (static_cast<int64_t>(j[k]) * a.H + L.hc) * a.C + cb * CP, nvalid, a.vec, xv[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      const float w = weight(a, k, L.h, M, S, normalise, cb == 0);
+#pragma unroll
+      for (int c = 0; c < CP; ++c) acc[c] = fmaf(w, xv[k][c], acc[c]);
     }
   }
-#pragma unroll
-  for (int k = 0; k < HP; ++k) {
-    const int t = eb + el + k * EPW;
-    if (hv && t < ee) s += expf(scR[k] - m);
-  }
-}
+};
 
 template <int HP>
 __device__ __forceinline__ void ms_reduce_heads(float& m, float& s) {
@@ -172,53 +288,6 @@ __device__ __forceinline__ void ms_reduce_heads(float& m, float& s) {
     const float m2 = shfl_xor(m, o);
     const float s2 = shfl_xor(s, o);
     ms_merge(m, s, m2, s2);
-  }
-}
-
-// Edge weights of one tile given the row's (M, S) per head; applies and (on
-// the first channel block) records the dropout mask.
-template <typename T, int HP>
-__device__ __forceinline__ void fwd_weights(const GatFwdArgs<T>& a, int eb, int ee, int h, int el, bool hv,
-                                            const float (&scR)[HP], float M, float S, bool normalise,
-                                            bool write_mask, float (&wR)[HP]) {
-  constexpr int EPW = kWave / HP;
-#pragma unroll
-  for (int k = 0; k < HP; ++k) {
-    const int t = eb + el + k * EPW;
-    float w = 0.0f;
-    if (hv && t < ee) {
-      bool keep = true;
-      if (a.p > 0.0f) {
-        const int64_t idx = static_cast<int64_t>(t) * a.H + h;
-        keep = gat_keep(a.seed, static_cast<uint64_t>(idx), a.p);
-        if (write_mask) a.mask[idx] = keep ? 1 : 0;
-      }
-      if (keep && (!normalise || S > 0.0f)) {
-        w = expf(scR[k] - M);
-        if (normalise) w = w / S;
-        if (a.p > 0.0f) w = w / (1.0f - a.p);
-      }
-    }
-    wR[k] = w;
-  }
-}
-
-template <typename T, int HP, int CP>
-__device__ __forceinline__ void fwd_gather(const GatFwdArgs<T>& a, int cb, int h, bool hv, const int (&jR)[HP],
-                                           const float (&wR)[HP], float (&acc)[CP]) {
-#pragma unroll
-  for (int c = 0; c < CP; ++c) acc[c] = 0.0f;
-  if (!hv) return;
-  const int nvalid = min(CP, a.C - cb * CP);
-#pragma unroll
-  for (int k = 0; k < HP; ++k) {
-    if (wR[k] != 0.0f) {
-      float xv[CP];
-      const T* p = a.x + (static_cast<int64_t>(jR[k]) * a.H + h) * a.C + cb * CP;
-      load_run<T, CP>(p, nvalid, a.vec, xv);
-#pragma unroll
-      for (int c = 0; c < CP; ++c) acc[c] = fmaf(wR[k], xv[c], acc[c]);
-    }
   }
 }
 
@@ -232,46 +301,49 @@ __device__ __forceinline__ void fwd_emit(const GatFwdArgs<T>& a, int row, int c,
 
 template <typename T, int HP, int CP>
 __global__ __launch_bounds__(kBlock) void gat_fwd_kernel(GatFwdArgs<T> a, Sched s) {
-  constexpr int LGH = ilog2c(HP);
-  const int lane = lane_id();
+  using GR1 = GroupReduce<CP, 1>;
+  using GRH = GroupReduce<CP, HP>;
+  constexpr int EPW = Lanes<HP>::EPW;
+  constexpr int NTL = kNTL<HP>;
+  const Lanes<HP> L(a.H);
   const int wave = wave_id();
-  const int h = lane & (HP - 1);
-  const int el = lane >> LGH;
-  const bool hv = h < a.H;
   const int ncb = (a.C + CP - 1) / CP;
   const int b = blockIdx.x;
-
-  int jR[HP];
-  float scR[HP], wR[HP], acc[CP];
 
   if (b >= s.n_seg) {
     const int li = (b - s.n_seg) * kWavesPerBlock + wave;
     if (li >= s.n_light) return;
-    const int row = s.light[li];
-    const int eb = a.rowptr[row], ee = a.rowptr[row + 1];
-    const float adst = hv ? a.attn_row[static_cast<int64_t>(row) * a.H + h] : 0.0f;
-    float m, sum;
-    fwd_scores<T, HP>(a, row, eb, ee, adst, h, el, hv, jR, scR, m, sum);
-    ms_reduce_heads<HP>(m, sum);
-    if (el == 0 && hv) {
-      a.emax[static_cast<int64_t>(row) * a.H + h] = m;
-      a.esum[static_cast<int64_t>(row) * a.H + h] = sum;
-    }
-    for (int cb = 0; cb < ncb; ++cb) {
-      fwd_weights<T, HP>(a, eb, ee, h, el, hv, scR, m, sum, true, cb == 0, wR);
-      fwd_gather<T, HP, CP>(a, cb, h, hv, jR, wR, acc);
-      GroupReduce<CP, 1>::run(acc, lane);
-      if (GroupReduce<CP, 1>::writer(lane)) {
-        const int c0 = cb * CP + GroupReduce<CP, 1>::chan_base(lane);
-#pragma unroll
-        for (int r = 0; r < GroupReduce<CP, 1>::R; ++r)
-          if (c0 + r < a.C) fwd_emit(a, row, c0 + r, acc[r]);
+    const int4 r = s.light[li];
+    const float adst = a.attn_row[static_cast<int64_t>(r.x) * a.H + L.hc];
+    const int nt = max(1, (r.z - r.y + EPW - 1) / EPW);
+    auto body = [&](auto NC) {
+      constexpr int N = decltype(NC)::value;
+      FwdWave<T, HP, CP, N> w;
+      w.load(a, L, r.y, r.z, adst);
+      float m, sum;
+      w.stats(m, sum);
+      ms_reduce_heads<HP>(m, sum);
+      if (L.el == 0 && L.hv) {
+        a.emax[static_cast<int64_t>(r.x) * a.H + L.h] = m;
+        a.esum[static_cast<int64_t>(r.x) * a.H + L.h] = sum;
       }
-    }
+      for (int cb = 0; cb < ncb; ++cb) {
+        float acc[CP];
+        w.accumulate(a, L, cb, m, sum, true, acc);
+        GR1::run(acc, L.lane);
+        if (GR1::writer(L.lane)) {
+          const int c0 = cb * CP + GR1::chan_base(L.lane);
+#pragma unroll
+          for (int q = 0; q < GR1::R; ++q)
+            if (c0 + q < a.C) fwd_emit(a, r.x, c0 + q, acc[q]);
+        }
+      }
+    };
+    dispatch_n<1, NTL>(nt, body);
     return;
   }
 
-  // Heavy-row segment: 4 waves, one 64-edge tile each.
+  // Heavy-row segment: 4 waves, one kGatLight-edge tile each.
   __shared__ float sm_m[kWavesPerBlock][HP], sm_s[kWavesPerBlock][HP];
   __shared__ float red[kWavesPerBlock][HP * CP];
   __shared__ float fin_m[HP], fin_s[HP];
@@ -280,32 +352,34 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_kernel(GatFwdArgs<T> a, Sched 
   const int row = sg.x;
   const int2 hr = s.hrow[sg.w];
   const bool single = hr.y == 1;
-  const int eb = sg.y + wave * kTile;
-  const int ee = min(sg.z, eb + kTile);
-  const float adst = hv ? a.attn_row[static_cast<int64_t>(row) * a.H + h] : 0.0f;
+  const int eb = min(sg.y + wave * kGatLight, sg.z);
+  const int ee = min(sg.z, eb + kGatLight);
+  const float adst = a.attn_row[static_cast<int64_t>(row) * a.H + L.hc];
+  FwdWave<T, HP, CP, NTL> w;
+  w.load(a, L, eb, ee, adst);
   float m, sum;
-  fwd_scores<T, HP>(a, row, eb, ee, adst, h, el, hv, jR, scR, m, sum);
+  w.stats(m, sum);
   ms_reduce_heads<HP>(m, sum);
-  if (el == 0) {
-    sm_m[wave][h] = m;
-    sm_s[wave][h] = sum;
+  if (L.el == 0) {
+    sm_m[wave][L.h] = m;
+    sm_s[wave][L.h] = sum;
   }
   __syncthreads();
-  float M = sm_m[0][h], S = sm_s[0][h];
+  float M = sm_m[0][L.h], S = sm_s[0][L.h];
 #pragma unroll
-  for (int w = 1; w < kWavesPerBlock; ++w) ms_merge(M, S, sm_m[w][h], sm_s[w][h]);
+  for (int q = 1; q < kWavesPerBlock; ++q) ms_merge(M, S, sm_m[q][L.h], sm_s[q][L.h]);
 
   const int HC = a.H * a.C;
   float* mine = a.partial + static_cast<int64_t>(b) * (HC + 2 * a.H);
   for (int cb = 0; cb < ncb; ++cb) {
-    fwd_weights<T, HP>(a, eb, ee, h, el, hv, scR, M, S, single, cb == 0, wR);
-    fwd_gather<T, HP, CP>(a, cb, h, hv, jR, wR, acc);
+    float acc[CP];
+    w.accumulate(a, L, cb, M, S, single, acc);
     if (single) {
-      GroupReduce<CP, 1>::run(acc, lane);
-      if (GroupReduce<CP, 1>::writer(lane)) {
-        const int c0 = GroupReduce<CP, 1>::chan_base(lane);
+      GR1::run(acc, L.lane);
+      if (GR1::writer(L.lane)) {
+        const int c0 = GR1::chan_base(L.lane);
 #pragma unroll
-        for (int r = 0; r < GroupReduce<CP, 1>::R; ++r) red[wave][c0 + r] = acc[r];
+        for (int q = 0; q < GR1::R; ++q) red[wave][c0 + q] = acc[q];
       }
       __syncthreads();
       for (int c = threadIdx.x; c < CP; c += kBlock) {
@@ -314,11 +388,11 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_kernel(GatFwdArgs<T> a, Sched 
       }
       __syncthreads();
     } else {
-      GroupReduce<CP, HP>::run(acc, lane);
-      if (GroupReduce<CP, HP>::writer(lane)) {
-        const int c0 = GroupReduce<CP, HP>::chan_base(lane);
+      GRH::run(acc, L.lane);
+      if (GRH::writer(L.lane)) {
+        const int c0 = GRH::chan_base(L.lane);
 #pragma unroll
-        for (int r = 0; r < GroupReduce<CP, HP>::R; ++r) red[wave][h * CP + c0 + r] = acc[r];
+        for (int q = 0; q < GRH::R; ++q) red[wave][L.h * CP + c0 + q] = acc[q];
       }
       __syncthreads();
       for (int q = threadIdx.x; q < HP * CP; q += kBlock) {
@@ -329,15 +403,15 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_kernel(GatFwdArgs<T> a, Sched 
     }
   }
   if (single) {
-    if (wave == 0 && el == 0 && hv) {
-      a.emax[static_cast<int64_t>(row) * a.H + h] = M;
-      a.esum[static_cast<int64_t>(row) * a.H + h] = S;
+    if (wave == 0 && L.el == 0 && L.hv) {
+      a.emax[static_cast<int64_t>(row) * a.H + L.h] = M;
+      a.esum[static_cast<int64_t>(row) * a.H + L.h] = S;
     }
     return;
   }
-  if (wave == 0 && el == 0 && hv) {
-    mine[HC + h] = M;
-    mine[HC + a.H + h] = S;
+  if (wave == 0 && L.el == 0 && L.hv) {
+    mine[HC + L.h] = M;
+    mine[HC + a.H + L.h] = S;
   }
   if (!arrive_last(a.counters + sg.w, hr.y, &flag)) return;
   // Last segment of this row: merge the per-segment (m, s, acc) in order.
@@ -370,7 +444,333 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_kernel(GatFwdArgs<T> a, Sched 
 }
 
 // ---------------------------------------------------------------------------
-// Backward, kernel 1: CSR rows.
+// Forward, feature layout (the fast path for H <= 8, C a multiple of the
+// 16-byte chunk width W, H*C <= 64*W).
+//
+// Like the SpMM: a group of L = pow2ceil(H*C/W) lanes owns one destination
+// row and lane q owns chunk q of an x row (head q / (C/W)). Softmax
+// statistics are computed lane-per-edge (each lane reads col and the H source
+// logits of one edge), the edge weights go through LDS, and the aggregation
+// gathers one 16-byte chunk per lane per edge with the whole batch of edges
+// in flight. Rows with degree <= L go one per group (64/L rows per wave),
+// rows with degree <= 64 one per wave (its groups split the edges), heavier
+// rows are 256-edge segments (4 waves), merged like the pair-layout kernel.
+// Uses the SpMM schedule geometry (light_max 64, seg_edges 256).
+// ---------------------------------------------------------------------------
+constexpr int kFlHeads = 8;
+
+template <typename T>
+struct FlGeom {
+  static constexpr int W = 16 / sizeof(T);
+};
+
+// Softmax statistics over R lanes (an aligned power-of-two block) that each
+// hold at most one edge: per head max, then sum of exp.
+template <int R>
+__device__ __forceinline__ void fl_stats(const float (&sc)[kFlHeads], bool valid, int H, float (&M)[kFlHeads],
+                                         float (&E)[kFlHeads], float (&S)[kFlHeads]) {
+#pragma unroll
+  for (int h = 0; h < kFlHeads; ++h) {
+    float m = (valid && h < H) ? sc[h] : kNegBig;
+    for (int o = 1; o < R; o <<= 1) m = fmaxf(m, shfl_xor(m, o));
+    M[h] = m;
+    const float e = (valid && h < H) ? expf(sc[h] - m) : 0.0f;
+    E[h] = e;
+    float t = e;
+    for (int o = 1; o < R; o <<= 1) t += shfl_xor(t, o);
+    S[h] = t;
+  }
+}
+
+// Lane-per-edge prologue of one row: edge id, source id, scores.
+template <typename T>
+__device__ __forceinline__ void fl_edge(const GatFwdArgs<T>& a, int row, int e, bool valid, int& j,
+                                        float (&sc)[kFlHeads]) {
+  j = valid ? a.col[e] : 0;
+  const float* ad = a.attn_row + static_cast<int64_t>(row) * a.H;
+  const float* as = a.attn_col + static_cast<int64_t>(j) * a.H;
+#pragma unroll
+  for (int h = 0; h < kFlHeads; ++h) sc[h] = h < a.H ? leaky(ad[h] + as[h], a.slope) : kNegBig;
+}
+
+// Writes the lane's edge weights (H of them) to LDS, recording the mask.
+template <typename T>
+__device__ __forceinline__ void fl_weights(const GatFwdArgs<T>& a, int e, bool valid, const float (&E)[kFlHeads],
+                                           const float (&S)[kFlHeads], bool normalise, float* wl) {
+#pragma unroll
+  for (int h = 0; h < kFlHeads; ++h) {
+    float w = 0.0f;
+    if (valid && h < a.H) {
+      bool keep = true;
+      if (a.p > 0.0f) {
+        const int64_t idx = static_cast<int64_t>(e) * a.H + h;
+        keep = gat_keep(a.seed, static_cast<uint64_t>(idx), a.p);
+        a.mask[idx] = keep ? 1 : 0;
+      }
+      if (keep && (!normalise || S[h] > 0.0f)) {
+        w = normalise ? E[h] / S[h] : E[h];
+        if (a.p > 0.0f) w = w / (1.0f - a.p);
+      }
+    }
+    wl[h] = w;
+  }
+}
+
+// acc += sum over edge slots u = first, first + step, ... < cnt of
+// w[u][head] * x[j_u, chunk q]; j_u from lane base + u, weights from LDS.
+template <typename T, int U>
+__device__ __forceinline__ void fl_gather(const GatFwdArgs<T>& a, int jj, int base, int first, int step, int cnt,
+                                          int q, int hq, bool qv, const float* wl, float (&acc)[FlGeom<T>::W]) {
+  constexpr int W = FlGeom<T>::W;
+  const int F = a.H * a.C;
+  for (int u0 = first; __any(u0 < cnt); u0 += U * step) {
+    float buf[U][W];
+    float wv[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int u = u0 + k * step;
+      const bool ok = u < cnt;
+      const int src = base + (ok ? u : 0);
+      const int j = shfl(jj, src & (kWave - 1));
+      wv[k] = ok ? wl[(src & (kWave - 1)) * kFlHeads + hq] : 0.0f;
+      if (qv) {
+        Chunk<T, W>::load(a.x + static_cast<int64_t>(j) * F + q * W, buf[k]);
+      } else {
+#pragma unroll
+        for (int w = 0; w < W; ++w) buf[k][w] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k)
+#pragma unroll
+      for (int w = 0; w < W; ++w) acc[w] = fmaf(wv[k], buf[k][w], acc[w]);
+  }
+}
+
+// Head mean + bias + SiLU of one row from per-chunk sums in LDS (xl holds the
+// row's nq chunks of W floats): lanes gl < C/W each emit W channels.
+template <typename T>
+__device__ __forceinline__ void fl_emit(const GatFwdArgs<T>& a, int row, int gl, const float* xl) {
+  constexpr int W = FlGeom<T>::W;
+  const int cq = a.C / W;
+  if (gl >= cq) return;
+  float o[W];
+  float pr[W];
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    float t = 0.0f;
+    for (int h = 0; h < a.H; ++h) t += xl[(h * cq + gl) * W + w];
+    pr[w] = t / static_cast<float>(a.H) + a.bias[gl * W + w];
+    o[w] = silu(pr[w]);
+  }
+  const int64_t base = static_cast<int64_t>(row) * a.C + gl * W;
+#pragma unroll
+  for (int w = 0; w < W; ++w) a.pre[base + w] = pr[w];
+  Chunk<T, W>::store(a.out + base, o);
+}
+
+template <typename T, int L>
+__global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sched s, int n_mid, int mid_blocks) {
+  constexpr int W = FlGeom<T>::W;
+  constexpr int G = kWave / L;
+  constexpr int LGL = ilog2c(L);
+  __shared__ float wl[kWavesPerBlock][kWave * kFlHeads];
+  __shared__ float xl[kWavesPerBlock][kWave * W];
+  __shared__ float bm[kWavesPerBlock][kFlHeads], bs[kWavesPerBlock][kFlHeads];
+  __shared__ int flag;
+  const int lane = lane_id();
+  const int wave = wave_id();
+  const int g = lane >> LGL;
+  const int gl = lane & (L - 1);
+  const int F = a.H * a.C;
+  const int nq = F / W;
+  const int cq = a.C / W;
+  const bool qv = gl < nq;
+  const int q = qv ? gl : 0;
+  const int hq = q / cq;
+  float* wlw = wl[wave];
+  float* xlw = xl[wave];
+  int b = blockIdx.x;
+  float acc[W];
+#pragma unroll
+  for (int w = 0; w < W; ++w) acc[w] = 0.0f;
+
+  if (b >= s.n_seg) {
+    b -= s.n_seg;
+    if (b >= mid_blocks) {
+      // Tiny rows: one per lane group (degree <= L).
+      const int li = n_mid + ((b - mid_blocks) * kWavesPerBlock + wave) * G + g;
+      const bool has = li < s.n_light;
+      const int4 r = has ? s.light[li] : make_int4(0, 0, 0, 0);
+      const int deg = r.z - r.y;
+      const bool valid = gl < deg;
+      int jj;
+      float sc[kFlHeads], M[kFlHeads], E[kFlHeads], S[kFlHeads];
+      fl_edge(a, r.x, r.y + gl, valid, jj, sc);
+      fl_stats<L>(sc, valid, a.H, M, E, S);
+      fl_weights(a, r.y + gl, valid, E, S, true, wlw + lane * kFlHeads);
+      if (has && gl < a.H) {
+#pragma unroll
+        for (int h = 0; h < kFlHeads; ++h)
+          if (h == gl) {
+            a.emax[static_cast<int64_t>(r.x) * a.H + h] = M[h];
+            a.esum[static_cast<int64_t>(r.x) * a.H + h] = S[h];
+          }
+      }
+      wave_sync();
+      fl_gather<T, (L < 16 ? L : 16)>(a, jj, g * L, 0, 1, deg, q, hq, qv, wlw, acc);
+#pragma unroll
+      for (int w = 0; w < W; ++w) xlw[lane * W + w] = acc[w];
+      wave_sync();
+      if (has) fl_emit(a, r.x, gl, xlw + g * L * W);
+      return;
+    }
+    // Medium rows: one per wave (L < degree <= 64); group g takes edges g, g+G, ...
+    const int li = b * kWavesPerBlock + wave;
+    if (li >= n_mid) return;
+    const int4 r = s.light[li];
+    const int deg = r.z - r.y;
+    const bool valid = lane < deg;
+    int jj;
+    float sc[kFlHeads], M[kFlHeads], E[kFlHeads], S[kFlHeads];
+    fl_edge(a, r.x, r.y + lane, valid, jj, sc);
+    fl_stats<kWave>(sc, valid, a.H, M, E, S);
+    fl_weights(a, r.y + lane, valid, E, S, true, wlw + lane * kFlHeads);
+    if (lane < a.H) {
+#pragma unroll
+      for (int h = 0; h < kFlHeads; ++h)
+        if (h == lane) {
+          a.emax[static_cast<int64_t>(r.x) * a.H + h] = M[h];
+          a.esum[static_cast<int64_t>(r.x) * a.H + h] = S[h];
+        }
+    }
+    wave_sync();
+    fl_gather<T, 16>(a, jj, 0, g, G, deg, q, hq, qv, wlw, acc);
+#pragma unroll
+    for (int w = 0; w < W; ++w) acc[w] = sum_across(acc[w], L);
+#pragma unroll
+    for (int w = 0; w < W; ++w) xlw[lane * W + w] = acc[w];
+    wave_sync();
+    fl_emit(a, r.x, lane, xlw);
+    return;
+  }
+
+  // Heavy-row segment: 4 waves x 64 edge slots.
+  const int4 sg = s.seg[b];
+  const int row = sg.x;
+  const int2 hr = s.hrow[sg.w];
+  const bool single = hr.y == 1;
+  const int e = sg.y + wave * kWave + lane;
+  const bool valid = e < sg.z;
+  int jj;
+  float sc[kFlHeads], M[kFlHeads], E[kFlHeads], S[kFlHeads];
+  fl_edge(a, row, e, valid, jj, sc);
+  fl_stats<kWave>(sc, valid, a.H, M, E, S);
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < kFlHeads; ++h) {
+      bm[wave][h] = M[h];
+      bs[wave][h] = S[h];
+    }
+  }
+  __syncthreads();
+  float Mb[kFlHeads], Sb[kFlHeads];
+#pragma unroll
+  for (int h = 0; h < kFlHeads; ++h) {
+    Mb[h] = bm[0][h];
+    Sb[h] = bs[0][h];
+#pragma unroll
+    for (int w = 1; w < kWavesPerBlock; ++w) ms_merge(Mb[h], Sb[h], bm[w][h], bs[w][h]);
+    E[h] = (valid && h < a.H) ? expf(sc[h] - Mb[h]) : 0.0f;
+  }
+  fl_weights(a, e, valid, E, Sb, single, wlw + lane * kFlHeads);
+  wave_sync();
+  const int cnt = max(0, min(kWave, sg.z - (sg.y + wave * kWave)));
+  fl_gather<T, 16>(a, jj, 0, g, G, cnt, q, hq, qv, wlw, acc);
+#pragma unroll
+  for (int w = 0; w < W; ++w) acc[w] = sum_across(acc[w], L);
+  if (g == 0) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) xlw[gl * W + w] = acc[w];
+  }
+  __syncthreads();
+  // Block sum of the four waves' chunk sums into xl[0].
+  for (int k = threadIdx.x; k < nq * W; k += kBlock) xl[0][k] = xl[0][k] + xl[1][k] + xl[2][k] + xl[3][k];
+  __syncthreads();
+  if (single) {
+    if (wave == 0) fl_emit(a, row, lane, xl[0]);
+    if (threadIdx.x < a.H) {
+      float mv = 0.0f, sv = 0.0f;
+#pragma unroll
+      for (int h = 0; h < kFlHeads; ++h)
+        if (h == static_cast<int>(threadIdx.x)) {
+          mv = Mb[h];
+          sv = Sb[h];
+        }
+      a.emax[static_cast<int64_t>(row) * a.H + threadIdx.x] = mv;
+      a.esum[static_cast<int64_t>(row) * a.H + threadIdx.x] = sv;
+    }
+    return;
+  }
+  const int stride = F + 2 * a.H;
+  float* mine = a.partial + static_cast<int64_t>(b) * stride;
+  for (int k = threadIdx.x; k < F; k += kBlock) mine[k] = xl[0][k];
+  if (threadIdx.x < a.H) {
+    float mv = 0.0f, sv = 0.0f;
+#pragma unroll
+    for (int h = 0; h < kFlHeads; ++h)
+      if (h == static_cast<int>(threadIdx.x)) {
+        mv = Mb[h];
+        sv = Sb[h];
+      }
+    mine[F + threadIdx.x] = mv;
+    mine[F + a.H + threadIdx.x] = sv;
+  }
+  if (!arrive_last(a.counters + sg.w, hr.y, &flag)) return;
+  // Merge segments: per head M = max m_q, S = sum s_q e^{m_q - M},
+  // acc = sum acc_q e^{m_q - M} / S; then head mean.
+  __shared__ float fm[kFlHeads], fs[kFlHeads];
+  if (threadIdx.x < a.H) {
+    float MM = kNegBig, SS = 0.0f;
+    for (int z = 0; z < hr.y; ++z) {
+      const float* pz = a.partial + static_cast<int64_t>(hr.x + z) * stride;
+      ms_merge(MM, SS, pz[F + threadIdx.x], pz[F + a.H + threadIdx.x]);
+    }
+    fm[threadIdx.x] = MM;
+    fs[threadIdx.x] = SS;
+    a.emax[static_cast<int64_t>(row) * a.H + threadIdx.x] = MM;
+    a.esum[static_cast<int64_t>(row) * a.H + threadIdx.x] = SS;
+  }
+  __syncthreads();
+  for (int k = threadIdx.x; k < F; k += kBlock) {
+    const int h = k / a.C;
+    float t = 0.0f;
+    for (int z = 0; z < hr.y; ++z) {
+      const float* pz = a.partial + static_cast<int64_t>(hr.x + z) * stride;
+      t += pz[k] * expf(pz[F + h] - fm[h]);
+    }
+    xl[0][k] = fs[h] > 0.0f ? t / fs[h] : 0.0f;
+  }
+  __syncthreads();
+  if (wave == 0) fl_emit(a, row, lane, xl[0]);
+}
+
+template <typename T, int L>
+struct FwdFlLauncher {
+  static int run(hipStream_t st, const GatFwdArgs<T>& a, const Sched& s, const int32_t* hdr) {
+    constexpr int G = kWave / L;
+    const int n_mid = G > 1 ? sched_count_gt(hdr, L) : s.n_light;
+    const int mid_blocks = (n_mid + kWavesPerBlock - 1) / kWavesPerBlock;
+    const int n_tiny = s.n_light - n_mid;
+    const int blocks = s.n_seg + mid_blocks + (n_tiny + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
+    if (blocks > 0)
+      hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid, mid_blocks);
+    return check_launch("cign_gat_fwd (feature layout)");
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Backward
 // ---------------------------------------------------------------------------
 template <typename T>
 struct GatBwdArgs {
@@ -378,10 +778,7 @@ struct GatBwdArgs {
   float slope, p, inv_h;
   bool vec_x;   // 16-byte loads of x rows are legal
   bool vec_gp;  // 16-byte loads of grad_pre rows are legal
-  bool vec_gx;  // 16-byte stores of grad_feat rows are legal
-  const int32_t* rowptr;
   const int32_t* col;
-  const int32_t* colptr;
   const int32_t* rowind;
   const int32_t* perm;
   const float* emax;
@@ -394,10 +791,11 @@ struct GatBwdArgs {
   const T* grad_y;
   // workspace
   float* grad_pre;   // [n, C]
-  float* gscore;     // [nnz, H]: g_w/(1-p)-masked, then g_raw
+  float* gscore;     // [nnz, H]: ge' = keep/(1-p) * <g_pre, x>/H
+  float* wsum;       // [n, H]: sum_e s ge'
   float* bias_part;  // [rows_blocks, C]
   float* bias_l2;    // [n_l2, C]
-  float* part_row;   // [n_seg_rows, H]
+  float* part_row;   // [n_seg_rows, 3H]
   float* part_col;   // [n_seg_cols, H*C + H]
   int32_t* row_counters;
   int32_t* col_counters;  // [n_hrow_cols + 1]; last slot = bias counter
@@ -409,70 +807,6 @@ struct GatBwdArgs {
   float* grad_attn_col;
   float* grad_bias;
 };
-
-// Per-edge first pass of one tile: ge = <g_pre, x[j,h,:]>/H with the dropout
-// mask and 1/(1-p) applied (the reference's grad_edge handling,
-// collapsed_gat_cuda.cu:394-396), soft = s_eh, raw; returns sum_e s*ge.
-template <typename T, int HP, int CP>
-__device__ __forceinline__ float bwd_edge_pass(const GatBwdArgs<T>& a, int row, int eb, int ee, int h, int el,
-                                               bool hv, float adst, float M, float S, const float* gp,
-                                               float (&geR)[HP], float (&sR)[HP], float (&rawR)[HP]) {
-  constexpr int EPW = kWave / HP;
-  const int ncb = (a.C + CP - 1) / CP;
-  float wpart = 0.0f;
-#pragma unroll
-  for (int k = 0; k < HP; ++k) {
-    const int t = eb + el + k * EPW;
-    geR[k] = 0.0f;
-    sR[k] = 0.0f;
-    rawR[k] = 0.0f;
-    if (hv && t < ee) {
-      const int j = a.col[t];
-      const T* xr = a.x + (static_cast<int64_t>(j) * a.H + h) * a.C;
-      float dot = 0.0f;
-      for (int cb = 0; cb < ncb; ++cb) {
-        const int nvalid = min(CP, a.C - cb * CP);
-        float xv[CP];
-        load_run<T, CP>(xr + cb * CP, nvalid, a.vec_x, xv);
-#pragma unroll
-        for (int c = 0; c < CP; ++c) dot = fmaf(gp[cb * CP + c], xv[c], dot);
-      }
-      float ge = dot * a.inv_h;
-      const float raw = adst + a.attn_col[static_cast<int64_t>(j) * a.H + h];
-      const float sc = leaky(raw, a.slope);
-      const float soft = S > 0.0f ? expf(sc - M) / S : 0.0f;
-      if (a.p > 0.0f) {
-        const bool keep = a.mask[static_cast<int64_t>(t) * a.H + h] != 0;
-        ge = keep ? ge : 0.0f;
-        ge = ge / (1.0f - a.p);
-      }
-      geR[k] = ge;
-      sR[k] = soft;
-      rawR[k] = raw;
-      wpart += soft * ge;
-    }
-  }
-  return wpart;
-}
-
-template <typename T, int HP>
-__device__ __forceinline__ float bwd_edge_finish(const GatBwdArgs<T>& a, int eb, int ee, int h, int el, bool hv,
-                                                 float wsum, const float (&geR)[HP], const float (&sR)[HP],
-                                                 const float (&rawR)[HP]) {
-  constexpr int EPW = kWave / HP;
-  float gdst = 0.0f;
-#pragma unroll
-  for (int k = 0; k < HP; ++k) {
-    const int t = eb + el + k * EPW;
-    if (hv && t < ee) {
-      float g = sR[k] * (geR[k] - wsum);
-      if (rawR[k] < 0.0f) g *= a.slope;
-      a.gscore[static_cast<int64_t>(t) * a.H + h] = g;
-      gdst += g;
-    }
-  }
-  return gdst;
-}
 
 // g_pre of one row into LDS (and, when `publish`, into the grad_pre
 // workspace); LDS entries [C, padded) are zeroed so whole channel blocks can
@@ -492,42 +826,97 @@ __device__ __forceinline__ void bwd_grad_pre(const GatBwdArgs<T>& a, int row, in
   }
 }
 
+// One pass over the lane's N tiles of [eb, ee): stores ge' and accumulates
+// (wsum, A, B) for the lane's head.
+template <typename T, int HP, int CP, int N>
+__device__ __forceinline__ void bwd_row_wave(const GatBwdArgs<T>& a, const Lanes<HP>& L, int eb, int ee, float adst,
+                                             float M, float S, const float* gp, float& wsum, float& A, float& B) {
+  wsum = A = B = 0.0f;
+  if (ee <= eb) return;  // no edges (wave-uniform); eb may equal nnz here
+  const int ncb = (a.C + CP - 1) / CP;
+  int t[N], j[N];
+  bool v[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    t[k] = eb + L.el + k * Lanes<HP>::EPW;
+    v[k] = L.hv && t[k] < ee;
+    j[k] = a.col[t[k] < ee ? t[k] : eb];
+  }
+  float raw[N], dot[N];
+  bool keep[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    raw[k] = adst + a.attn_col[static_cast<int64_t>(j[k]) * a.H + L.hc];
+    keep[k] = a.p > 0.0f ? a.mask[static_cast<int64_t>(v[k] ? t[k] : eb) * a.H + L.hc] != 0 : true;
+    dot[k] = 0.0f;
+  }
+  for (int cb = 0; cb < ncb; ++cb) {
+    const int nvalid = min(CP, a.C - cb * CP);
+    float xv[N][CP];
+#pragma unroll
+    for (int k = 0; k < N; ++k)
+      load_run<T, CP>(a.x + (static_cast<int64_t>(j[k]) * a.H + L.hc) * a.C + cb * CP, nvalid, a.vec_x, xv[k]);
+#pragma unroll
+    for (int c = 0; c < CP; ++c) {
+      const float g = gp[cb * CP + c];
+#pragma unroll
+      for (int k = 0; k < N; ++k) dot[k] = fmaf(g, xv[k][c], dot[k]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    float ge = dot[k] * a.inv_h;
+    if (a.p > 0.0f) ge = (keep[k] ? ge : 0.0f) / (1.0f - a.p);
+    const float soft = S > 0.0f ? expf(leaky(raw[k], a.slope) - M) / S : 0.0f;
+    const float lp = raw[k] < 0.0f ? a.slope : 1.0f;
+    if (v[k]) {
+      a.gscore[static_cast<int64_t>(t[k]) * a.H + L.h] = ge;
+      const float sg = soft * ge;
+      wsum += sg;
+      A += sg * lp;
+      B += soft * lp;
+    }
+  }
+}
+
 template <typename T, int HP, int CP>
 __global__ __launch_bounds__(kBlock) void gat_bwd_rows_kernel(GatBwdArgs<T> a, Sched s) {
-  constexpr int LGH = ilog2c(HP);
-  const int lane = lane_id();
+  constexpr int EPW = Lanes<HP>::EPW;
+  constexpr int NTL = kNTL<HP>;
+  const Lanes<HP> L(a.H);
   const int wave = wave_id();
-  const int h = lane & (HP - 1);
-  const int el = lane >> LGH;
-  const bool hv = h < a.H;
   const int b = blockIdx.x;
   const int padded = ((a.C + CP - 1) / CP) * CP;
   __shared__ float gp[kWavesPerBlock][kMaxC];
-  __shared__ float wred[kWavesPerBlock][HP];
-  __shared__ float fin[kMaxH];
+  __shared__ float red[kWavesPerBlock][3][HP];
   __shared__ int flag;
-
-  float geR[HP], sR[HP], rawR[HP];
 
   if (b >= s.n_seg) {
     const int li = (b - s.n_seg) * kWavesPerBlock + wave;
     const bool has = li < s.n_light;
-    const int row = has ? s.light[li] : 0;
+    const int4 r = has ? s.light[li] : make_int4(0, 0, 0, 0);
     if (has) {
-      bwd_grad_pre(a, row, lane, kWave, padded, gp[wave], true);
+      const int64_t rh = static_cast<int64_t>(r.x) * a.H + L.hc;
+      const float adst = a.attn_row[rh];
+      const float M = a.emax[rh];
+      const float S = a.esum[rh];
+      bwd_grad_pre(a, r.x, L.lane, kWave, padded, gp[wave], true);
       wave_sync();
-      const int eb = a.rowptr[row], ee = a.rowptr[row + 1];
-      const int64_t rh = static_cast<int64_t>(row) * a.H + h;
-      const float adst = hv ? a.attn_row[rh] : 0.0f;
-      const float M = hv ? a.emax[rh] : 0.0f;
-      const float S = hv ? a.esum[rh] : 0.0f;
-      float wsum = bwd_edge_pass<T, HP, CP>(a, row, eb, ee, h, el, hv, adst, M, S, gp[wave], geR, sR, rawR);
+      float wsum = 0.0f, A = 0.0f, B = 0.0f;
+      const int nt = max(1, (r.z - r.y + EPW - 1) / EPW);
+      auto body = [&](auto NC) {
+        bwd_row_wave<T, HP, CP, decltype(NC)::value>(a, L, r.y, r.z, adst, M, S, gp[wave], wsum, A, B);
+      };
+      dispatch_n<1, NTL>(nt, body);
       wsum = sum_across(wsum, HP);
-      float gdst = bwd_edge_finish<T, HP>(a, eb, ee, h, el, hv, wsum, geR, sR, rawR);
-      gdst = sum_across(gdst, HP);
-      if (el == 0 && hv) a.grad_attn_row[rh] = gdst;
+      A = sum_across(A, HP);
+      B = sum_across(B, HP);
+      if (L.el == 0 && L.hv) {
+        a.wsum[rh] = wsum;
+        a.grad_attn_row[rh] = A - wsum * B;
+      }
     } else {
-      for (int c = lane; c < padded; c += kWave) gp[wave][c] = 0.0f;
+      for (int c = L.lane; c < padded; c += kWave) gp[wave][c] = 0.0f;
     }
     __syncthreads();
     // Per-block bias partial: sum of this block's rows of g_pre.
@@ -545,124 +934,112 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_kernel(GatBwdArgs<T> a, S
   __syncthreads();
   for (int c = threadIdx.x; c < a.C; c += kBlock)
     a.bias_part[static_cast<int64_t>(b) * a.C + c] = first_seg ? gp[0][c] : 0.0f;
-  const int eb = sg.y + wave * kTile;
-  const int ee = min(sg.z, eb + kTile);
-  const int64_t rh = static_cast<int64_t>(row) * a.H + h;
-  const float adst = hv ? a.attn_row[rh] : 0.0f;
-  const float M = hv ? a.emax[rh] : 0.0f;
-  const float S = hv ? a.esum[rh] : 0.0f;
-  float wpart = bwd_edge_pass<T, HP, CP>(a, row, eb, ee, h, el, hv, adst, M, S, gp[0], geR, sR, rawR);
-  wpart = sum_across(wpart, HP);
-  if (el == 0) wred[wave][h] = wpart;
+  const int eb = min(sg.y + wave * kGatLight, sg.z);
+  const int ee = min(sg.z, eb + kGatLight);
+  const int64_t rh = static_cast<int64_t>(row) * a.H + L.hc;
+  float wsum, A, B;
+  bwd_row_wave<T, HP, CP, NTL>(a, L, eb, ee, a.attn_row[rh], a.emax[rh], a.esum[rh], gp[0], wsum, A, B);
+  wsum = sum_across(wsum, HP);
+  A = sum_across(A, HP);
+  B = sum_across(B, HP);
+  if (L.el == 0) {
+    red[wave][0][L.h] = wsum;
+    red[wave][1][L.h] = A;
+    red[wave][2][L.h] = B;
+  }
   __syncthreads();
-  const float wblk = wred[0][h] + wred[1][h] + wred[2][h] + wred[3][h];
+  if (threadIdx.x < 3 * HP) {
+    const int k = threadIdx.x / HP, hh = threadIdx.x % HP;
+    red[0][k][hh] = red[0][k][hh] + red[1][k][hh] + red[2][k][hh] + red[3][k][hh];
+  }
   __syncthreads();
   if (hr.y == 1) {
-    float gdst = bwd_edge_finish<T, HP>(a, eb, ee, h, el, hv, wblk, geR, sR, rawR);
-    gdst = sum_across(gdst, HP);
-    if (el == 0) wred[wave][h] = gdst;
-    __syncthreads();
-    if (wave == 0 && el == 0 && hv) a.grad_attn_row[rh] = wred[0][h] + wred[1][h] + wred[2][h] + wred[3][h];
+    if (threadIdx.x < a.H) {
+      const float w = red[0][0][threadIdx.x];
+      a.wsum[static_cast<int64_t>(row) * a.H + threadIdx.x] = w;
+      a.grad_attn_row[static_cast<int64_t>(row) * a.H + threadIdx.x] = red[0][1][threadIdx.x] - w * red[0][2][threadIdx.x];
+    }
     return;
   }
-  // Multi-segment row: publish g_w and the partial weighted sum, the last
-  // segment finishes every edge of the row.
-  {
-    constexpr int EPW = kWave / HP;
-#pragma unroll
-    for (int k = 0; k < HP; ++k) {
-      const int t = eb + el + k * EPW;
-      if (hv && t < ee) a.gscore[static_cast<int64_t>(t) * a.H + h] = geR[k];
-    }
-  }
-  if (wave == 0 && el == 0 && hv) a.part_row[static_cast<int64_t>(b) * a.H + h] = wblk;
+  float* mine = a.part_row + static_cast<int64_t>(b) * 3 * a.H;
+  if (threadIdx.x < 3 * a.H) mine[threadIdx.x] = red[0][threadIdx.x / a.H][threadIdx.x % a.H];
   if (!arrive_last(a.row_counters + sg.w, hr.y, &flag)) return;
   if (threadIdx.x < a.H) {
-    float t = 0.0f;
-    for (int q = 0; q < hr.y; ++q) t += a.part_row[static_cast<int64_t>(hr.x + q) * a.H + threadIdx.x];
-    fin[threadIdx.x] = t;
-  }
-  __syncthreads();
-  const int rb = a.rowptr[row], re = a.rowptr[row + 1];
-  // Thread -> (edge, head) with head = tid % HP fixed per thread.
-  const int th = threadIdx.x & (HP - 1);
-  const bool thv = th < a.H;
-  const float tadst = thv ? a.attn_row[static_cast<int64_t>(row) * a.H + th] : 0.0f;
-  const float tM = thv ? a.emax[static_cast<int64_t>(row) * a.H + th] : 0.0f;
-  const float tS = thv ? a.esum[static_cast<int64_t>(row) * a.H + th] : 0.0f;
-  const float tw = thv ? fin[th] : 0.0f;
-  float gdst = 0.0f;
-  if (thv) {
-    for (int t = rb + (threadIdx.x >> LGH); t < re; t += kBlock / HP) {
-      const int64_t eh = static_cast<int64_t>(t) * a.H + th;
-      const int j = a.col[t];
-      const float raw = tadst + a.attn_col[static_cast<int64_t>(j) * a.H + th];
-      const float sc = leaky(raw, a.slope);
-      const float soft = tS > 0.0f ? expf(sc - tM) / tS : 0.0f;
-      float g = soft * (a.gscore[eh] - tw);
-      if (raw < 0.0f) g *= a.slope;
-      a.gscore[eh] = g;
-      gdst += g;
+    float w = 0.0f, AA = 0.0f, BB = 0.0f;
+    for (int q = 0; q < hr.y; ++q) {
+      const float* pq = a.part_row + static_cast<int64_t>(hr.x + q) * 3 * a.H;
+      w += pq[threadIdx.x];
+      AA += pq[a.H + threadIdx.x];
+      BB += pq[2 * a.H + threadIdx.x];
     }
+    a.wsum[static_cast<int64_t>(row) * a.H + threadIdx.x] = w;
+    a.grad_attn_row[static_cast<int64_t>(row) * a.H + threadIdx.x] = AA - w * BB;
   }
-  gdst = sum_across(gdst, HP);
-  if (el == 0) wred[wave][h] = gdst;
-  __syncthreads();
-  if (threadIdx.x < a.H)
-    a.grad_attn_row[static_cast<int64_t>(row) * a.H + threadIdx.x] =
-        wred[0][threadIdx.x] + wred[1][threadIdx.x] + wred[2][threadIdx.x] + wred[3][threadIdx.x];
 }
 
-// ---------------------------------------------------------------------------
-// Backward, kernel 2: CSC columns (source nodes) + grad_bias.
-// ---------------------------------------------------------------------------
-template <typename T, int HP>
-__device__ __forceinline__ float bwd_col_weights(const GatBwdArgs<T>& a, int cb0, int ce, int h, int el, bool hv,
-                                                 float asrc, int (&iR)[HP], float (&wR)[HP]) {
-  constexpr int EPW = kWave / HP;
-  float gsrc = 0.0f;
+// The lane's N tiles of a CSC range [cb0, ce): per-edge weights w, source
+// rows i, and the lane's sum of g_raw = s (ge' - wsum[i]) LeakyReLU'.
+template <typename T, int HP, int N>
+__device__ __forceinline__ float bwd_col_wave(const GatBwdArgs<T>& a, const Lanes<HP>& L, int cb0, int ce,
+                                              float asrc, int (&i)[N], float (&w)[N]) {
+  if (ce <= cb0) {
+    // No edges (wave-uniform): nothing is read; cb0 may equal nnz here.
 #pragma unroll
-  for (int k = 0; k < HP; ++k) {
-    const int t = cb0 + el + k * EPW;
-    iR[k] = 0;
-    wR[k] = 0.0f;
-    if (hv && t < ce) {
-      const int i = a.rowind[t];
-      const int e = a.perm[t];
-      const int64_t ih = static_cast<int64_t>(i) * a.H + h;
-      const int64_t eh = static_cast<int64_t>(e) * a.H + h;
-      iR[k] = i;
-      const float raw = a.attn_row[ih] + asrc;
-      const float S = a.esum[ih];
-      float w = 0.0f;
-      bool keep = true;
-      if (a.p > 0.0f) keep = a.mask[eh] != 0;
-      if (keep && S > 0.0f) {
-        w = expf(leaky(raw, a.slope) - a.emax[ih]) / S;
-        if (a.p > 0.0f) w = w / (1.0f - a.p);
-      }
-      wR[k] = w;
-      gsrc += a.gscore[eh];
+    for (int k = 0; k < N; ++k) {
+      i[k] = 0;
+      w[k] = 0.0f;
     }
+    return 0.0f;
   }
-  return gsrc;
+  int e[N];
+  bool v[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const int t = cb0 + L.el + k * Lanes<HP>::EPW;
+    v[k] = L.hv && t < ce;
+    const int tc = t < ce ? t : cb0;
+    i[k] = a.rowind[tc];
+    e[k] = a.perm[tc];
+  }
+  float gsum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    const int64_t ih = static_cast<int64_t>(i[k]) * a.H + L.hc;
+    const int64_t eh = static_cast<int64_t>(e[k]) * a.H + L.hc;
+    const float raw = a.attn_row[ih] + asrc;
+    const float S = a.esum[ih];
+    const float M = a.emax[ih];
+    const float ws = a.wsum[ih];
+    const float ge = a.gscore[eh];
+    const bool keep = a.p > 0.0f ? a.mask[eh] != 0 : true;
+    const float soft = S > 0.0f ? expf(leaky(raw, a.slope) - M) / S : 0.0f;
+    float ww = 0.0f;
+    if (v[k] && keep) {
+      ww = soft;
+      if (a.p > 0.0f) ww = ww / (1.0f - a.p);
+    }
+    w[k] = ww;
+    float g = soft * (ge - ws);
+    if (raw < 0.0f) g *= a.slope;
+    gsum += v[k] ? g : 0.0f;
+  }
+  return gsum;
 }
 
-template <typename T, int HP, int CP>
-__device__ __forceinline__ void bwd_col_gather(const GatBwdArgs<T>& a, int cb, const int (&iR)[HP],
-                                               const float (&wR)[HP], float (&acc)[CP]) {
+template <typename T, int CP, int N>
+__device__ __forceinline__ void bwd_col_gather(const GatBwdArgs<T>& a, int cb, const int (&i)[N], const float (&w)[N],
+                                               float (&acc)[CP]) {
   const int nvalid = min(CP, a.C - cb * CP);
+  float gv[N][CP];
+#pragma unroll
+  for (int k = 0; k < N; ++k)
+    load_run<float, CP>(a.grad_pre + static_cast<int64_t>(i[k]) * a.C + cb * CP, nvalid, a.vec_gp, gv[k]);
 #pragma unroll
   for (int c = 0; c < CP; ++c) acc[c] = 0.0f;
 #pragma unroll
-  for (int k = 0; k < HP; ++k) {
-    if (wR[k] != 0.0f) {
-      float gv[CP];
-      load_run<float, CP>(a.grad_pre + static_cast<int64_t>(iR[k]) * a.C + cb * CP, nvalid, a.vec_gp, gv);
+  for (int k = 0; k < N; ++k)
 #pragma unroll
-      for (int c = 0; c < CP; ++c) acc[c] = fmaf(wR[k], gv[c], acc[c]);
-    }
-  }
+    for (int c = 0; c < CP; ++c) acc[c] = fmaf(w[k], gv[k][c], acc[c]);
 }
 
 template <typename T>
@@ -670,15 +1047,43 @@ __device__ __forceinline__ void store_gx(const GatBwdArgs<T>& a, int j, int h, i
   a.grad_feat[(static_cast<int64_t>(j) * a.H + h) * a.C + c] = from_f32<T>(v * a.inv_h);
 }
 
+// grad_bias = sum over kernel-1 blocks of their partials: level 1 in each
+// bias workgroup (64 partials), level 2 in the last one to finish. Partial
+// rows are summed by parallel thread groups, then combined through LDS.
+template <typename T>
+__device__ __forceinline__ void bias_reduce(const GatBwdArgs<T>& a, int q, int* counter, int* flag) {
+  __shared__ float red[kBlock];
+  const int C = a.C;
+  const int rows_per = kBlock / C;  // C <= kMaxC = kBlock
+  const int tid = threadIdx.x;
+  const int c = tid % C;
+  const int r0 = tid / C;
+  auto reduce = [&](const float* src, int lo, int hi, float* dst) {
+    float t = 0.0f;
+    if (r0 < rows_per)
+      for (int r = lo + r0; r < hi; r += rows_per) t += src[static_cast<int64_t>(r) * C + c];
+    red[tid] = r0 < rows_per ? t : 0.0f;
+    __syncthreads();
+    if (tid < C) {
+      float u = 0.0f;
+      for (int k = 0; k < rows_per; ++k) u += red[k * C + tid];
+      dst[tid] = u;
+    }
+    __syncthreads();
+  };
+  const int lo = q * 64, hi = min(a.rows_blocks, lo + 64);
+  reduce(a.bias_part, lo, hi, a.bias_l2 + static_cast<int64_t>(q) * C);
+  if (!arrive_last(counter, a.n_l2, flag)) return;
+  reduce(a.bias_l2, 0, a.n_l2, a.grad_bias);
+}
+
 template <typename T, int HP, int CP>
 __global__ __launch_bounds__(kBlock) void gat_bwd_cols_kernel(GatBwdArgs<T> a, Sched s) {
-  constexpr int LGH = ilog2c(HP);
   using GR = GroupReduce<CP, HP>;
-  const int lane = lane_id();
+  constexpr int EPW = Lanes<HP>::EPW;
+  constexpr int NTL = kNTL<HP>;
+  const Lanes<HP> L(a.H);
   const int wave = wave_id();
-  const int h = lane & (HP - 1);
-  const int el = lane >> LGH;
-  const bool hv = h < a.H;
   const int ncb = (a.C + CP - 1) / CP;
   const int b = blockIdx.x;
   const int nsched = sched_blocks(s);
@@ -687,47 +1092,39 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_kernel(GatBwdArgs<T> a, S
   __shared__ int flag;
 
   if (b >= nsched) {
-    // grad_bias: level 1 sums 64 per-block partials of kernel 1, level 2
-    // (last arriving workgroup) sums the level-1 results in order.
-    const int q = b - nsched;
-    const int lo = q * 64, hi = min(a.rows_blocks, lo + 64);
-    for (int c = threadIdx.x; c < a.C; c += kBlock) {
-      float t = 0.0f;
-      for (int r = lo; r < hi; ++r) t += a.bias_part[static_cast<int64_t>(r) * a.C + c];
-      a.bias_l2[static_cast<int64_t>(q) * a.C + c] = t;
-    }
-    if (!arrive_last(a.col_counters + s.n_hrow, a.n_l2, &flag)) return;
-    for (int c = threadIdx.x; c < a.C; c += kBlock) {
-      float t = 0.0f;
-      for (int r = 0; r < a.n_l2; ++r) t += a.bias_l2[static_cast<int64_t>(r) * a.C + c];
-      a.grad_bias[c] = t;
-    }
+    bias_reduce(a, b - nsched, a.col_counters + s.n_hrow, &flag);
     return;
   }
-
-  int iR[HP];
-  float wR[HP], acc[CP];
 
   if (b >= s.n_seg) {
     const int li = (b - s.n_seg) * kWavesPerBlock + wave;
     if (li >= s.n_light) return;
-    const int j = s.light[li];
-    const int cb0 = a.colptr[j], ce = a.colptr[j + 1];
-    const int64_t jh = static_cast<int64_t>(j) * a.H + h;
-    const float asrc = hv ? a.attn_col[jh] : 0.0f;
-    float gsrc = bwd_col_weights<T, HP>(a, cb0, ce, h, el, hv, asrc, iR, wR);
-    gsrc = sum_across(gsrc, HP);
-    if (el == 0 && hv) a.grad_attn_col[jh] = gsrc;
-    for (int cb = 0; cb < ncb; ++cb) {
-      bwd_col_gather<T, HP, CP>(a, cb, iR, wR, acc);
-      GR::run(acc, lane);
-      if (GR::writer(lane) && hv) {
-        const int c0 = cb * CP + GR::chan_base(lane);
+    const int4 r = s.light[li];
+    const int j = r.x;
+    const int64_t jh = static_cast<int64_t>(j) * a.H + L.hc;
+    const float asrc = a.attn_col[jh];
+    float gsrc = 0.0f;
+    const int nt = max(1, (r.z - r.y + EPW - 1) / EPW);
+    auto body = [&](auto NC) {
+      constexpr int N = decltype(NC)::value;
+      int i[N];
+      float w[N];
+      gsrc = bwd_col_wave<T, HP, N>(a, L, r.y, r.z, asrc, i, w);
+      for (int cb = 0; cb < ncb; ++cb) {
+        float acc[CP];
+        bwd_col_gather<T, CP, N>(a, cb, i, w, acc);
+        GR::run(acc, L.lane);
+        if (GR::writer(L.lane) && L.hv) {
+          const int c0 = cb * CP + GR::chan_base(L.lane);
 #pragma unroll
-        for (int r = 0; r < GR::R; ++r)
-          if (c0 + r < a.C) store_gx(a, j, h, c0 + r, acc[r]);
+          for (int q = 0; q < GR::R; ++q)
+            if (c0 + q < a.C) store_gx(a, j, L.h, c0 + q, acc[q]);
+        }
       }
-    }
+    };
+    dispatch_n<1, NTL>(nt, body);
+    gsrc = sum_across(gsrc, HP);
+    if (L.el == 0 && L.hv) a.grad_attn_col[jh] = gsrc;
     return;
   }
 
@@ -736,22 +1133,22 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_kernel(GatBwdArgs<T> a, S
   const int j = sg.x;
   const int2 hr = s.hrow[sg.w];
   const bool single = hr.y == 1;
-  const int t0 = sg.y + wave * kTile;
-  const int te = min(sg.z, t0 + kTile);
-  const int64_t jh = static_cast<int64_t>(j) * a.H + h;
-  const float asrc = hv ? a.attn_col[jh] : 0.0f;
-  float gsrc = bwd_col_weights<T, HP>(a, t0, te, h, el, hv, asrc, iR, wR);
-  gsrc = sum_across(gsrc, HP);
-  if (el == 0) gred[wave][h] = gsrc;
+  const int t0 = min(sg.y + wave * kGatLight, sg.z);
+  const int te = min(sg.z, t0 + kGatLight);
+  const float asrc = a.attn_col[static_cast<int64_t>(j) * a.H + L.hc];
   const int HC = a.H * a.C;
   float* mine = a.part_col + static_cast<int64_t>(b) * (HC + a.H);
+  int i[NTL];
+  float w[NTL];
+  float gsrc = bwd_col_wave<T, HP, NTL>(a, L, t0, te, asrc, i, w);
   for (int cb = 0; cb < ncb; ++cb) {
-    bwd_col_gather<T, HP, CP>(a, cb, iR, wR, acc);
-    GR::run(acc, lane);
-    if (GR::writer(lane)) {
-      const int c0 = GR::chan_base(lane);
+    float acc[CP];
+    bwd_col_gather<T, CP, NTL>(a, cb, i, w, acc);
+    GR::run(acc, L.lane);
+    if (GR::writer(L.lane)) {
+      const int c0 = GR::chan_base(L.lane);
 #pragma unroll
-      for (int r = 0; r < GR::R; ++r) red[wave][h * CP + c0 + r] = acc[r];
+      for (int q = 0; q < GR::R; ++q) red[wave][L.h * CP + c0 + q] = acc[q];
     }
     __syncthreads();
     for (int q = threadIdx.x; q < HP * CP; q += kBlock) {
@@ -764,6 +1161,9 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_kernel(GatBwdArgs<T> a, S
     }
     __syncthreads();
   }
+  gsrc = sum_across(gsrc, HP);
+  if (L.el == 0) gred[wave][L.h] = gsrc;
+  __syncthreads();
   if (threadIdx.x < a.H) {
     const int hh = threadIdx.x;
     const float v = gred[0][hh] + gred[1][hh] + gred[2][hh] + gred[3][hh];
@@ -781,7 +1181,9 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_kernel(GatBwdArgs<T> a, S
   }
 }
 
-
+// ---------------------------------------------------------------------------
+// Launchers (explicitly instantiated in gat_inst_*.hip).
+// ---------------------------------------------------------------------------
 template <typename T, int HP, int CP>
 struct FwdLauncher {
   static int run(hipStream_t st, const GatFwdArgs<T>& a, const Sched& s) {
@@ -807,7 +1209,6 @@ struct BwdLauncher {
   }
 };
 
-
 #define CIGN_GAT_INSTANTIATE(T, HP)                        \
   template struct ::cign::gatk::FwdLauncher<T, HP, 8>;     \
   template struct ::cign::gatk::FwdLauncher<T, HP, 16>;    \
@@ -815,6 +1216,24 @@ struct BwdLauncher {
   template struct ::cign::gatk::BwdLauncher<T, HP, 8>;     \
   template struct ::cign::gatk::BwdLauncher<T, HP, 16>;    \
   template struct ::cign::gatk::BwdLauncher<T, HP, 32>;
+
+#define CIGN_GAT_FL_INSTANTIATE(T)                       \
+  template struct ::cign::gatk::FwdFlLauncher<T, 1>;     \
+  template struct ::cign::gatk::FwdFlLauncher<T, 2>;     \
+  template struct ::cign::gatk::FwdFlLauncher<T, 4>;     \
+  template struct ::cign::gatk::FwdFlLauncher<T, 8>;     \
+  template struct ::cign::gatk::FwdFlLauncher<T, 16>;    \
+  template struct ::cign::gatk::FwdFlLauncher<T, 32>;    \
+  template struct ::cign::gatk::FwdFlLauncher<T, 64>;
+
+#define CIGN_GAT_FL_DECLARE(T)                                  \
+  extern template struct ::cign::gatk::FwdFlLauncher<T, 1>;     \
+  extern template struct ::cign::gatk::FwdFlLauncher<T, 2>;     \
+  extern template struct ::cign::gatk::FwdFlLauncher<T, 4>;     \
+  extern template struct ::cign::gatk::FwdFlLauncher<T, 8>;     \
+  extern template struct ::cign::gatk::FwdFlLauncher<T, 16>;    \
+  extern template struct ::cign::gatk::FwdFlLauncher<T, 32>;    \
+  extern template struct ::cign::gatk::FwdFlLauncher<T, 64>;
 
 #define CIGN_GAT_DECLARE(T, HP)                                   \
   extern template struct ::cign::gatk::FwdLauncher<T, HP, 8>;     \

@@ -166,7 +166,7 @@ class HipCsr:
         if add is not None:
             add = add.to(dtype=x.dtype).contiguous()
         part = scratch_partial(self.sched, d, x.device)
-        lib.call("cign_spmm", _lib.stream_ptr(x.device), _lib.dtype_code(x), self.n, d, self.crow.data_ptr(),
+        lib.call("cign_spmm", _lib.stream_ptr(x.device), _lib.dtype_code(x), self.n, d,
                  self.col.data_ptr(), self.val.data_ptr(), *self.sched.args(), x.data_ptr(),
                  _lib.ptr(add), out.data_ptr(), _lib.ptr(part), self.sched.counters.data_ptr())
         return out

@@ -144,7 +144,7 @@ class MultiHopCsrPlan:
         y1, y2, y3 = (torch.empty_like(x) for _ in range(3))
         crow, col, val = self._p
         lib.call("cign_spmm_fwd3", _lib.stream_ptr(self._device), _lib.dtype_code(x), self._rows, self._dense_cols,
-                 crow.data_ptr(), col.data_ptr(), val.data_ptr(), *self._p_sched.args(), x.data_ptr(),
+                 col.data_ptr(), val.data_ptr(), *self._p_sched.args(), x.data_ptr(),
                  y1.data_ptr(), y2.data_ptr(), y3.data_ptr(), _lib.ptr(self._part),
                  self._p_sched.counters.data_ptr())
         return [y1, y2, y3]
@@ -160,7 +160,7 @@ class MultiHopCsrPlan:
         t2, t1, gx = (torch.empty_like(grad_y1) for _ in range(3))
         crow, col, val = self._pt
         lib.call("cign_spmm_bwd3", _lib.stream_ptr(self._device), _lib.dtype_code(grad_y1), self._rows,
-                 self._dense_cols, crow.data_ptr(), col.data_ptr(), val.data_ptr(), *self._pt_sched.args(),
+                 self._dense_cols, col.data_ptr(), val.data_ptr(), *self._pt_sched.args(),
                  grad_y1.data_ptr(), grad_y2.data_ptr(), grad_y3.data_ptr(), t2.data_ptr(), t1.data_ptr(),
                  gx.data_ptr(), _lib.ptr(self._part), self._pt_sched.counters.data_ptr())
         return gx

@@ -17,15 +17,22 @@ import torch
 
 from ._lib import load_library
 
-# Rows with at most LIGHT_MAX edges get one wavefront; heavier rows are cut
-# into SEG_EDGES-edge segments, one 256-thread workgroup each.
+# SpMM schedules: rows with at most LIGHT_MAX edges get one wavefront (or a
+# lane group), heavier rows are cut into SEG_EDGES-edge segments, one
+# 256-thread workgroup each.
 LIGHT_MAX = 64
 SEG_EDGES = 256
+# Collapsed-GAT pair-layout schedules: one wavefront takes at most 16 edges
+# of a row, segments are 64 edges (16 per wave). The feature-layout forward
+# uses the SpMM geometry; cign_gat_schedule_params says which.
+GAT_LIGHT_MAX = 16
+GAT_SEG_EDGES = 64
 
 
 @dataclass
 class RowSchedule:
     buf: torch.Tensor        # int32 device buffer (csrc/schedule.h layout)
+    header: np.ndarray       # host copy of its 12-int header (passed to every launch)
     counters: torch.Tensor   # int32 [n_hrow + 1], zero; kernels leave it zero (last slot: spare global counter)
     n_rows: int
     n_light: int
@@ -34,7 +41,8 @@ class RowSchedule:
     max_degree: int
 
     def args(self):
-        return (self.buf.data_ptr(), self.n_light, self.n_seg, self.n_hrow)
+        """(device schedule, host header) pointers of the C-ABI."""
+        return (self.buf.data_ptr(), self.header.ctypes.data)
 
 
 def build_row_schedule(rowptr: torch.Tensor, device=None, light_max: int = LIGHT_MAX,
@@ -58,22 +66,33 @@ def build_row_schedule(rowptr: torch.Tensor, device=None, light_max: int = LIGHT
     buf = torch.from_numpy(host).to(dev)
     counters = torch.zeros(nh.value + 1, dtype=torch.int32, device=dev)
     deg = np.diff(rp)
-    return RowSchedule(buf, counters, n_rows, int(nl.value), int(ns.value), int(nh.value),
+    header = np.ascontiguousarray(host[:12].copy())
+    return RowSchedule(buf, header, counters, n_rows, int(nl.value), int(ns.value), int(nh.value),
                        int(deg.max()) if deg.size else 0)
 
 
-_CACHE: dict[int, tuple[weakref.ref, int, RowSchedule]] = {}
+_CACHE: dict[tuple, tuple[weakref.ref, int, RowSchedule]] = {}
 
 
-def cached_row_schedule(rowptr: torch.Tensor) -> RowSchedule:
+def cached_row_schedule(rowptr: torch.Tensor, light_max: int = LIGHT_MAX, seg_edges: int = SEG_EDGES) -> RowSchedule:
     """Schedule for a row-pointer tensor, built on first use and reused while
     the tensor is alive and unmodified (checked through its version counter)."""
-    key = id(rowptr)
+    key = (id(rowptr), int(light_max), int(seg_edges))
     hit = _CACHE.get(key)
     if hit is not None:
         ref, version, sched = hit
         if ref() is rowptr and version == rowptr._version and sched.n_rows == rowptr.numel() - 1:
             return sched
-    sched = build_row_schedule(rowptr)
+    sched = build_row_schedule(rowptr, light_max=light_max, seg_edges=seg_edges)
     _CACHE[key] = (weakref.ref(rowptr, lambda _r, k=key: _CACHE.pop(k, None)), rowptr._version, sched)
     return sched
+
+
+def gat_schedule(rowptr: torch.Tensor, pass_: int, dtype_code: int, heads: int, channels: int) -> RowSchedule:
+    """Schedule of a CSR/CSC pointer for a collapsed-GAT pass (0 = forward,
+    1 = backward), with the geometry the library asks for that shape."""
+    lib = load_library(require_gpu=False)
+    light, seg = C.c_int32(), C.c_int32()
+    lib.call("cign_gat_schedule_params", int(pass_), int(dtype_code), int(heads), int(channels), C.byref(light),
+             C.byref(seg))
+    return cached_row_schedule(rowptr, light.value, seg.value)

@@ -93,11 +93,16 @@ def test_row_schedule_layout(rng):
     s, b = _sched_host(rowptr)
     assert (s.n_light, s.n_hrow) == ((deg <= LIGHT_MAX).sum(), (deg > LIGHT_MAX).sum())
     assert s.n_seg == sum(-(-d // SEG_EDGES) for d in deg if d > LIGHT_MAX)
-    assert tuple(b[:4]) == (s.n_light, s.n_seg, s.n_hrow, SEG_EDGES)
-    light = b[4:4 + s.n_light]
+    lt = deg[deg <= LIGHT_MAX]
+    assert tuple(b[:12]) == (s.n_light, s.n_seg, s.n_hrow, SEG_EDGES, LIGHT_MAX, 0,
+                             *((lt > (1 << k)).sum() for k in range(6)))
+    assert np.array_equal(s.header, b[:12])
+    rec = b[12:12 + 4 * s.n_light].reshape(-1, 4)
+    light = rec[:, 0]
     assert sorted(light.tolist()) == sorted(np.nonzero(deg <= LIGHT_MAX)[0].tolist())
+    assert np.array_equal(rec[:, 1], rowptr[light]) and np.array_equal(rec[:, 2], rowptr[light + 1])
     assert (np.diff(deg[light]) <= 0).all()
-    off = (4 + s.n_light + 3) & ~3
+    off = 12 + 4 * s.n_light
     seg = b[off:off + 4 * s.n_seg].reshape(-1, 4)
     hrow = b[off + 4 * s.n_seg:].reshape(-1, 2)
     covered = {}
@@ -139,3 +144,46 @@ def test_product_never_imports_oracle():
         text = p.read_text()
         assert not re.search(r"^\s*(from|import)\s+(\.\.)?oracle", text, re.M), p
         assert "cign_oracle" not in text, p
+
+
+def _gat_wave_ranges(rowptr):
+    """Edge ranges walked by the GAT kernels' wavefronts (light rows and the
+    four 16-edge waves of each segment), from the real schedule."""
+    from cign_amd.schedule import GAT_LIGHT_MAX, GAT_SEG_EDGES
+
+    s = build_row_schedule(torch.from_numpy(rowptr.astype(np.int64)), device="cpu", light_max=GAT_LIGHT_MAX,
+                           seg_edges=GAT_SEG_EDGES)
+    b = s.buf.numpy()
+    rec = b[12:12 + 4 * s.n_light].reshape(-1, 4)
+    seg = b[12 + 4 * s.n_light:12 + 4 * s.n_light + 4 * s.n_seg].reshape(-1, 4)
+    out = [(r[1], r[2]) for r in rec]
+    for _, beg, end, _ in seg:
+        for w in range(4):
+            eb = min(beg + 16 * w, end)
+            out.append((eb, min(end, eb + 16)))
+    return out
+
+
+def test_gat_edge_index_reads_stay_in_bounds(rng):
+    # Emulates the clamped index arithmetic of gat_kernels.h: a wave reads
+    # col/rowind/perm at t < ee ? t : eb for every lane and tile, and reads
+    # nothing when its range is empty (an empty range may start at nnz).
+    rowptr = np.array([0, 0, 1, 1, 3, 3])  # rows 0, 2, 4 empty; row 4 starts at nnz
+    graphs = [rowptr]
+    ei = random_gat_graph(rng, 300, avg_deg=5, hubs={4: 800})
+    (rp, _), (_, cp), _ = graph.to_graph_format(torch.from_numpy(ei).flip(0), size=(300, 300))
+    graphs += [rp.numpy(), cp.numpy()]
+    for H in (1, 4, 6, 12):
+        HP = 4 if H <= 4 else (8 if H <= 8 else 32)
+        epw = 64 // HP
+        for rp in graphs:
+            nnz = int(rp[-1])
+            for eb, ee in _gat_wave_ranges(rp):
+                if ee <= eb:
+                    continue
+                nt = -(-(ee - eb) // epw)
+                assert nt <= max(1, 16 // epw)
+                for el in range(epw):
+                    for k in range(nt):
+                        t = eb + el + k * epw
+                        assert 0 <= (t if t < ee else eb) < nnz
