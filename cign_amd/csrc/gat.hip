@@ -48,8 +48,12 @@ struct BwdLayout {
 
 inline int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
+// row_blocks = n_seg + ceil(n_light / 4) of the row schedule; one more bias
+// partial is reserved because the feature-layout row grid (light rows split
+// into one-per-wave and several-per-wave blocks) can be one block longer.
 inline BwdLayout bwd_layout(int n, int nnz, int H, int C, int row_blocks, int n_seg_rows, int n_seg_cols) {
   BwdLayout L;
+  row_blocks += 1;
   const int n_l2 = (row_blocks + 63) / 64;
   int64_t off = 0;
   L.grad_pre = off; off = align256(off + 4LL * n * C);
@@ -84,9 +88,17 @@ inline bool fl_forward_ok(int dtype, int H, int C) {
   return H <= kFlHeads && C % W == 0 && (H * C) / W <= kWave;
 }
 
+// Feature-layout backward: as the forward, plus C/W a power of two (the
+// per-edge dot products are reduced over a head's C/W lanes by a butterfly).
+inline bool fl_backward_ok(int dtype, int H, int C) {
+  const int W = dtype == kBF16 ? 8 : 4;
+  const int cq = C / W;
+  return fl_forward_ok(dtype, H, C) && (cq & (cq - 1)) == 0;
+}
+
 // Schedule geometry (light_max, seg_edges) each GAT pass runs on.
 inline void gat_geometry(int pass, int dtype, int H, int C, int& light, int& seg) {
-  if (pass == 0 && fl_forward_ok(dtype, H, C)) {
+  if ((pass == 0 && fl_forward_ok(dtype, H, C)) || (pass == 1 && fl_backward_ok(dtype, H, C))) {
     light = 64;
     seg = 256;
   } else {
@@ -241,9 +253,31 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
     a.part_row = reinterpret_cast<float*>(ws + L.part_row);
     a.part_col = reinterpret_cast<float*>(ws + L.part_col);
     a.row_counters = row_counters; a.col_counters = col_counters;
+    a.grad_feat = gxt; a.grad_attn_row = grad_attn_row; a.grad_attn_col = grad_attn_col; a.grad_bias = grad_bias;
+    if (fl_backward_ok(dtype, heads, channels)) {
+      if (!aligned16(xt) || !aligned16(gyt) || !aligned16(gxt))
+        return set_error(kInvalid, "cign_gat_bwd: in_feat, grad_y and grad_feat must be 16-byte aligned");
+      const int W = dtype == kBF16 ? 8 : 4;
+      int Lq = 1;
+      while (Lq < heads * channels / W) Lq <<= 1;
+      auto go = [&](auto LC) {
+        constexpr int LL = decltype(LC)::value;
+        a.rows_blocks = BwdFlLauncher<T, LL>::row_blocks(rs, row_sched_info);
+        a.n_l2 = (a.rows_blocks + 63) / 64;
+        return BwdFlLauncher<T, LL>::run(st, a, rs, row_sched_info, cs, col_sched_info);
+      };
+      switch (Lq) {
+        case 1: return go(std::integral_constant<int, 1>());
+        case 2: return go(std::integral_constant<int, 2>());
+        case 4: return go(std::integral_constant<int, 4>());
+        case 8: return go(std::integral_constant<int, 8>());
+        case 16: return go(std::integral_constant<int, 16>());
+        case 32: return go(std::integral_constant<int, 32>());
+        default: return go(std::integral_constant<int, 64>());
+      }
+    }
     a.rows_blocks = row_blocks;
     a.n_l2 = (row_blocks + 63) / 64;
-    a.grad_feat = gxt; a.grad_attn_row = grad_attn_row; a.grad_attn_col = grad_attn_col; a.grad_bias = grad_bias;
     return dispatch_hc<BwdLauncher, T>(heads, channels, st, a, rs, cs);
   };
   if (dtype == kF32)

@@ -53,6 +53,9 @@ CASES = [
     (4, 16, 0.0, torch.bfloat16, 600, {3: 1000}),
     (4, 32, 0.25, torch.bfloat16, 400, {0: 700}),
     (6, 256, 0.0, torch.bfloat16, 200, {2: 300}),
+    (3, 8, 0.1, torch.float32, 300, {1: 2000}),
+    (1, 256, 0.0, torch.float32, 200, {0: 600}),
+    (5, 32, 0.0, torch.bfloat16, 300, {2: 520}),
 ]
 
 
