@@ -36,6 +36,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 disables)")
     ap.add_argument("--dtype", choices=["f32", "bf16"], default="f32")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="before warmup, run 3 plain 256 MiB elementwise copies (x * 1 -> y, fp32) whose "
+                         "FETCH_SIZE / WRITE_SIZE counters calibrate the per-kernel traffic figures")
     return ap.parse_args()
 
 
@@ -89,7 +92,99 @@ def cpu_baseline(w, seconds: float, H: int, C: int, D: int):
                       f"1 thread"}
 
 
+# ---------------------------------------------------------------------------
+# rocprofv3 summaries (profiles/): kernel statistics and copy-calibrated
+# FETCH_SIZE / WRITE_SIZE traffic per launch.
+# ---------------------------------------------------------------------------
+PHASE_KERNELS = {"gat_fwd": ("gat_fwd",), "spmm_fwd3": ("spmm_kernel",), "spmm_bwd3": ("spmm_kernel",),
+                 "gat_bwd": ("gat_bwd_rows", "gat_bwd_cols")}
+COPY_KIB = 256 * 1024  # the --calibrate-copy kernel reads and writes 256 MiB
+
+
+def _short(name: str) -> str:
+    name = name.removeprefix("void ").replace("(anonymous namespace)::", "")
+    return name.split("(")[0] if "(" in name else name
+
+
+def measured_traffic(dtype: str, phase: str):
+    """HBM bytes per launch of `phase` from the committed rocprofv3 --pmc summary, or (None, None)."""
+    path = ROOT / "profiles" / f"layer_c2c3_{dtype}_traffic.json"
+    if not path.exists():
+        return None, None
+    d = json.loads(path.read_text())
+    total = 0.0
+    for key in PHASE_KERNELS[phase]:
+        hits = [v for k, v in d["kernels"].items() if key in k]
+        if not hits:
+            return None, None
+        total += hits[0]["bytes"]
+    return total, f"profiles/{path.name}"
+
+
+def summarize(prof_dir: str, name: str, command: str) -> None:
+    """Writes profiles/<name>_kernel_stats.txt, _traffic.txt and _traffic.json
+    from rocprofv3 CSV output: <prof_dir>/kt (--kernel-trace --stats),
+    <prof_dir>/fetch (--pmc FETCH_SIZE) and <prof_dir>/write (--pmc WRITE_SIZE),
+    each made with --calibrate-copy for the counter runs."""
+    import csv
+    import glob
+    import statistics
+
+    prof = Path(prof_dir)
+    out = ROOT / "profiles"
+    out.mkdir(exist_ok=True)
+    stats = list(csv.DictReader(open(glob.glob(str(prof / "kt" / "*_kernel_stats.csv"))[0])))
+    lines = [f"# rocprofv3 kernel statistics: {name}", "", "Command (from the repository root, GPU box):", "",
+             "    " + command.replace("\n", "\n    "), "",
+             f"{'kernel':72s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'pct':>6s}"]
+    for r in stats[:16]:
+        lines.append(f"{_short(r['Name'])[:72]:72s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} "
+                     f"{float(r['MinNs']) / 1e3:9.2f} {float(r['MaxNs']) / 1e3:9.2f} {float(r['Percentage']):6.2f}")
+    (out / f"{name}_kernel_stats.txt").write_text("\n".join(lines) + "\n")
+
+    def counters(sub, counter):
+        per = {}
+        f = glob.glob(str(prof / sub / "*_counter_collection.csv"))[0]
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] == counter:
+                per.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return per
+
+    fetch, write = counters("fetch", "FETCH_SIZE"), counters("write", "WRITE_SIZE")
+    # the copy reads and writes 256 MiB (torch's fill that made its source only writes)
+    copy = sorted((k for k in write if "elementwise" in k and max(write[k]) > 0.9 * COPY_KIB and k in fetch),
+                  key=lambda k: -max(fetch[k]))
+    if not copy:
+        raise SystemExit("no calibration copy kernel in the counter runs (run bench.py with --calibrate-copy)")
+    fk = COPY_KIB / statistics.median(fetch[copy[0]])
+    wk = COPY_KIB / statistics.median(write[copy[0]])
+    kern = {}
+    for k in fetch:
+        if "cign" not in k:
+            continue
+        f_kib, w_kib = statistics.median(fetch[k]), statistics.median(write.get(k, [0.0]))
+        kern[_short(k)] = {"fetch_kib": f_kib, "write_kib": w_kib, "dispatches": len(fetch[k]),
+                           "bytes": round((f_kib * fk + w_kib * wk) * 1024)}
+    doc = {"command": command, "calibration": {"copy_kernel": _short(copy[0]), "copy_bytes_each_way": COPY_KIB * 1024,
+                                               "fetch_factor": round(fk, 4), "write_factor": round(wk, 4)},
+           "kernels": kern}
+    (out / f"{name}_traffic.json").write_text(json.dumps(doc, indent=1) + "\n")
+    lines = [f"# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch: {name}", "",
+             "Command (from the repository root, GPU box):", "", "    " + command.replace("\n", "\n    "), "",
+             f"Calibration: {_short(copy[0])} copying 256 MiB reads FETCH_SIZE x {fk:.4f} and WRITE_SIZE x {wk:.4f}",
+             "of the true bytes; traffic = FETCH_SIZE * fetch_factor + WRITE_SIZE * write_factor (KiB -> bytes).",
+             "", f"{'kernel':60s} {'FETCH KiB':>10s} {'WRITE KiB':>10s} {'traffic MB':>11s}"]
+    for k, v in kern.items():
+        lines.append(f"{k[:60]:60s} {v['fetch_kib']:10.0f} {v['write_kib']:10.0f} {v['bytes'] / 1e6:11.2f}")
+    (out / f"{name}_traffic.txt").write_text("\n".join(lines) + "\n")
+    print(f"wrote profiles/{name}_kernel_stats.txt, _traffic.txt, _traffic.json")
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize":
+        # python bench.py --summarize <rocprof dir> <name> <command text>
+        summarize(sys.argv[2], sys.argv[3], sys.argv[4])
+        return
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1 (multi-GPU sharding is "
@@ -138,6 +233,14 @@ def main():
         if marks is not None:
             marks[4].record()
 
+    if args.calibrate_copy:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -160,8 +263,10 @@ def main():
     s = 2 if dt == torch.bfloat16 else 4
     B = workloads.algorithmic_bytes(n, E, H, C, D, s_gat=s, s_mh=s)
     ms = 1e3 * elapsed / args.steps
-    launches = {"gat_fwd": 1, "spmm_fwd3": 3, "gat_bwd": 2, "spmm_bwd3": 3}
-    bytes_per_launch = {"gat_fwd": B["gat_fwd"], "spmm_fwd3": B["spmm"], "gat_bwd": B["gat_bwd"] / 2,
+    # One "launch" of the GAT backward is one cign_gat_bwd call (its rows and
+    # columns kernels back to back on the stream).
+    launches = {"gat_fwd": 1, "spmm_fwd3": 3, "gat_bwd": 1, "spmm_bwd3": 3}
+    bytes_per_launch = {"gat_fwd": B["gat_fwd"], "spmm_fwd3": B["spmm"], "gat_bwd": B["gat_bwd"],
                         "spmm_bwd3": B["spmm"] + s * n * D * 2 / 3}
     breakdown = {}
     for p in phases:
@@ -171,9 +276,10 @@ def main():
     dom = max(phases, key=lambda p: phase_ms[p])
     dom_ms = phase_ms[dom] / launches[dom]
     achieved = bytes_per_launch[dom] / (dom_ms * 1e-3) / 1e9
-    kernel_name = {"gat_fwd": "gat_fwd_kernel", "spmm_fwd3": "spmm_kernel (fwd hop)",
-                   "gat_bwd": "gat_bwd_rows_kernel + gat_bwd_cols_kernel (mean)",
+    kernel_name = {"gat_fwd": "cign_gat_fwd (gat_fwd_fl_kernel)", "spmm_fwd3": "spmm_kernel (fwd hop)",
+                   "gat_bwd": "cign_gat_bwd (gat_bwd_rows_fl_kernel + gat_bwd_cols_fl_kernel)",
                    "spmm_bwd3": "spmm_kernel (bwd hop, fused add)"}[dom]
+    traffic, traffic_src = measured_traffic(args.dtype, dom)
     layer_gbs = B["layer"] / (ms * 1e-3) / 1e9
 
     cpu = None
@@ -201,8 +307,9 @@ def main():
         "algorithmic_bytes_per_step": B["layer"],
         "breakdown": breakdown,
         "roofline": {"bound": "hbm", "kernel": kernel_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": bytes_per_launch[dom], "avg_launch_ms": round(dom_ms, 5)},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src, "bytes_per_launch": bytes_per_launch[dom],
+                     "avg_launch_ms": round(dom_ms, 5)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
