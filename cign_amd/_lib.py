@@ -39,6 +39,22 @@ _SIGNATURES = {
     "cign_gat_bwd_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32, _I32, _I32]),
     "cign_gat_bwd": (C.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _F32, _F32] + [_P] * 11
                      + [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P]),
+    # GAT side ops and block ops (nodeops.hip)
+    "cign_colsum_workspace_bytes": (_I64, [_I64, _I32, _I32]),
+    "cign_attn_logits_fwd": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P]),
+    "cign_attn_logits_bwd": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64]),
+    "cign_head_silu_fwd": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P]),
+    "cign_head_silu_bwd": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _I64]),
+    "cign_dropout_ln_fwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _F32, _F32, _U64, _P, _P, _P, _P]),
+    "cign_dropout_ln_bwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _F32, _P, _P, _P, _P, _I64]),
+    "cign_add_ln_fwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _F32, _P, _P, _P]),
+    "cign_add_ln_bwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64]),
+    "cign_gamma_residual_fwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _F32, _U64, _P, _P]),
+    "cign_gamma_residual_bwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _F32, _P, _P, _P, _I64]),
+    # Clifford packs (pack.hip)
+    "cign_pack_fwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _I64, _P, _P]),
+    "cign_pack_bwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I64,
+                                _P]),
 }
 
 _LOCK = threading.Lock()
@@ -90,6 +106,30 @@ def exported_symbols() -> list[str]:
 
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+def ptr_array(ptrs) -> C.Array:
+    """Host array of device pointers (the hop pointer arrays of the packs);
+    pass ``C.addressof(arr)`` and keep ``arr`` alive for the call."""
+    return (C.c_void_p * len(ptrs))(*ptrs)
+
+
+def check(cond: bool, msg: str) -> None:
+    """TORCH_CHECK equivalent of the reference bindings: RuntimeError."""
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def check_input(t: torch.Tensor, name: str, dtype: torch.dtype = torch.float32) -> None:
+    """CHECK_INPUT of the reference bindings: CUDA, contiguous, dtype."""
+    check(isinstance(t, torch.Tensor) and t.is_cuda, f"{name} must be CUDA")
+    check(t.is_contiguous(), f"{name} must be contiguous")
+    check(t.dtype == dtype, f"{name} must be {str(dtype).replace('torch.', '')}")
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Caller-owned scratch from torch's caching allocator (at least 1 byte)."""
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
 def stream_ptr(device: torch.device | None = None) -> int:

@@ -1,0 +1,736 @@
+// Per-node kernels of the GAT side ops and the block ops, and their C-ABI.
+//
+// GAT side ops (fused_gat_sideops_ext/fused_gat_sideops_cuda.cu:25-337):
+//   attention logits  alpha_src[n,h] = <x[n,h,:], att_src[h,:]>, alpha_dst
+//                     likewise; backward g_x = gs*att_src + gd*att_dst,
+//                     g_att[h,c] = sum_n g[n,h] x[n,h,c];
+//   head mean + bias + SiLU   pre = sum_h out[n,h,:] / H + bias, y = SiLU(pre);
+//                     backward g_out = g_y SiLU'(pre) / H per head, g_bias = sum_n.
+// Block ops (fused_block_ops.py:15 inline kernels, fused_block_ops_ext/
+// fused_block_ops_cuda.cu:45-322), rows of D <= 256:
+//   dropout + LayerNorm, add + LayerNorm, dropout-gamma-residual, with their
+//   backward passes (dx / dz, weight, bias and gamma gradients).
+// Row reductions are butterflies over a row's lanes; sums over nodes go
+// through deterministic per-row-block partials (rowops.h).
+#include "rowops.h"
+
+namespace cign {
+namespace rowops {
+
+__global__ void colsum_kernel(const float* part, int nb, int width, float* out0, float* out1) {
+  __shared__ float red[kBlock];
+  const float* src = part + static_cast<int64_t>(blockIdx.y) * nb * width;
+  float* out = blockIdx.y == 0 ? out0 : out1;
+  const int c0 = blockIdx.x * kBlock;
+  const int ct = min(kBlock, width - c0);
+  const int S = kBlock / ct;
+  const int t = threadIdx.x;
+  const int c = t % ct;
+  const int s = t / ct;
+  float acc = 0.0f;
+  if (s < S)
+    for (int b = s; b < nb; b += S) acc += src[static_cast<int64_t>(b) * width + c0 + c];
+  red[t] = acc;
+  __syncthreads();
+  if (t < ct) {
+    float tot = 0.0f;
+    for (int k = 0; k < S; ++k) tot += red[k * ct + t];
+    out[c0 + t] = tot;
+  }
+}
+
+__global__ void zero_kernel(float* a, int na, float* b, int nbv) {
+  const int i = blockIdx.x * kBlock + threadIdx.x;
+  if (i < na) a[i] = 0.0f;
+  if (b && i < nbv) b[i] = 0.0f;
+}
+
+int zero_outputs(hipStream_t st, float* a, int na, float* b, int nbv, const char* who) {
+  const int m = na > nbv ? na : nbv;
+  if (m <= 0) return kOk;
+  hipLaunchKernelGGL(zero_kernel, dim3((m + kBlock - 1) / kBlock), dim3(kBlock), 0, st, a, na, b, nbv);
+  return check_launch(who);
+}
+
+int launch_colsum(hipStream_t st, const float* part, int nb, int width, int quantities, float* out0, float* out1,
+                  const char* who) {
+  if (width <= 0) return kOk;
+  hipLaunchKernelGGL(colsum_kernel, dim3((width + kBlock - 1) / kBlock, quantities), dim3(kBlock), 0, st, part, nb,
+                     width, out0, out1);
+  return check_launch(who);
+}
+
+}  // namespace rowops
+
+namespace nodeops {
+using namespace rowops;
+
+// ---------------------------------------------------------------------------
+// Attention logits.
+// ---------------------------------------------------------------------------
+// Rows r of x viewed as [n*H, C]; head h = r % H.
+template <int LPR, int V, int W>
+__global__ __launch_bounds__(kBlock) void attn_fwd_kernel(int64_t rows, int H, int C, const float* x,
+                                                          const float* as, const float* ad, float* os, float* od) {
+  const Geo<LPR> g;
+  const int qc = C / W;
+  const int64_t step = static_cast<int64_t>(gridDim.x) * Geo<LPR>::RPB;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * Geo<LPR>::RPB + g.rl; r < rows; r += step) {
+    const int h = static_cast<int>(r % H);
+    float ss = 0.0f, sd = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int c = g.q + v * LPR;
+      if (c < qc) {
+        float xv[W], av[W], dv[W];
+        Chunk<float, W>::load(x + r * C + c * W, xv);
+        Chunk<float, W>::load(as + static_cast<int64_t>(h) * C + c * W, av);
+        Chunk<float, W>::load(ad + static_cast<int64_t>(h) * C + c * W, dv);
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          ss = fmaf(xv[w], av[w], ss);
+          sd = fmaf(xv[w], dv[w], sd);
+        }
+      }
+    }
+    ss = row_sum<LPR>(ss);
+    sd = row_sum<LPR>(sd);
+    if (g.q == 0) {
+      os[r] = ss;
+      od[r] = sd;
+    }
+  }
+}
+
+// Rows = nodes of width F = H*C; column tile blockIdx.y of LPR*V chunks.
+// Writes g_x and the tile's partial sums of gs*x and gd*x for row block
+// blockIdx.x (part layout [2][nb][F]).
+template <int LPR, int V, int W>
+__global__ __launch_bounds__(kBlock) void attn_bwd_kernel(int64_t n, int H, int C, const float* gs, const float* gd,
+                                                          const float* x, const float* as, const float* ad, float* gx,
+                                                          float* part, int nb) {
+  __shared__ float lds[kBlock * V * W];
+  const Geo<LPR> g;
+  const int F = H * C;
+  const int qf = F / W;
+  const int t0 = blockIdx.y * LPR * V;  // first chunk of the tile
+  int64_t r0, r1;
+  block_rows(n, nb, blockIdx.x, r0, r1);
+  float av[V][W], dv[V][W], accs[V][W], accd[V][W];
+  int hv[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int c = t0 + g.q + v * LPR;
+    hv[v] = c < qf ? (c * W) / C : 0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) accs[v][w] = accd[v][w] = av[v][w] = dv[v][w] = 0.0f;
+    if (c < qf) {
+      Chunk<float, W>::load(as + c * W, av[v]);
+      Chunk<float, W>::load(ad + c * W, dv[v]);
+    }
+  }
+  for (int64_t r = r0 + g.rl; r < r1; r += Geo<LPR>::RPB) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int c = t0 + g.q + v * LPR;
+      if (c < qf) {
+        const float s = gs[r * H + hv[v]];
+        const float d = gd[r * H + hv[v]];
+        float xv[W], o[W];
+        Chunk<float, W>::load(x + r * F + c * W, xv);
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          o[w] = s * av[v][w] + d * dv[v][w];
+          accs[v][w] = fmaf(s, xv[w], accs[v][w]);
+          accd[v][w] = fmaf(d, xv[w], accd[v][w]);
+        }
+        Chunk<float, W>::store(gx + r * F + c * W, o);
+      }
+    }
+  }
+  const int ncols = min(LPR * V * W, F - t0 * W);
+  block_colsum<LPR, V, W>(accs, lds, part + static_cast<int64_t>(blockIdx.x) * F + t0 * W, ncols);
+  block_colsum<LPR, V, W>(accd, lds, part + (static_cast<int64_t>(nb) + blockIdx.x) * F + t0 * W, ncols);
+}
+
+// ---------------------------------------------------------------------------
+// Head mean + bias + SiLU.
+// ---------------------------------------------------------------------------
+template <int W>
+__global__ __launch_bounds__(kBlock) void head_silu_fwd_kernel(int64_t n, int H, int C, const float* out,
+                                                               const float* bias, float* y, float* pre) {
+  const int qc = C / W;
+  const int64_t total = n * qc;
+  const float hf = static_cast<float>(H);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kBlock) {
+    const int64_t r = i / qc;
+    const int c = static_cast<int>(i - r * qc);
+    float s[W], b[W], p[W], o[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) s[w] = 0.0f;
+    for (int h = 0; h < H; ++h) {
+      float v[W];
+      Chunk<float, W>::load(out + (r * H + h) * C + c * W, v);
+#pragma unroll
+      for (int w = 0; w < W; ++w) s[w] += v[w];
+    }
+    Chunk<float, W>::load(bias + c * W, b);
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      p[w] = s[w] / hf + b[w];
+      o[w] = silu(p[w]);
+    }
+    Chunk<float, W>::store(pre + r * C + c * W, p);
+    Chunk<float, W>::store(y + r * C + c * W, o);
+  }
+}
+
+template <int LPR, int V, int W>
+__global__ __launch_bounds__(kBlock) void head_silu_bwd_kernel(int64_t n, int H, int C, const float* gy,
+                                                               const float* pre, float* gout, float* part, int nb) {
+  __shared__ float lds[kBlock * V * W];
+  const Geo<LPR> g;
+  const int qc = C / W;
+  const int t0 = blockIdx.y * LPR * V;
+  const float hf = static_cast<float>(H);
+  int64_t r0, r1;
+  block_rows(n, nb, blockIdx.x, r0, r1);
+  float acc[V][W];
+#pragma unroll
+  for (int v = 0; v < V; ++v)
+#pragma unroll
+    for (int w = 0; w < W; ++w) acc[v][w] = 0.0f;
+  for (int64_t r = r0 + g.rl; r < r1; r += Geo<LPR>::RPB) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int c = t0 + g.q + v * LPR;
+      if (c < qc) {
+        float gv[W], pv[W], o[W];
+        Chunk<float, W>::load(gy + r * C + c * W, gv);
+        Chunk<float, W>::load(pre + r * C + c * W, pv);
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          const float gp = gv[w] * silu_grad(pv[w]);
+          acc[v][w] += gp;
+          o[w] = gp / hf;
+        }
+        for (int h = 0; h < H; ++h) Chunk<float, W>::store(gout + (r * H + h) * C + c * W, o);
+      }
+    }
+  }
+  block_colsum<LPR, V, W>(acc, lds, part + static_cast<int64_t>(blockIdx.x) * C + t0 * W,
+                          min(LPR * V * W, C - t0 * W));
+}
+
+// ---------------------------------------------------------------------------
+// Block ops. MODE 0: dropout + LayerNorm of x; MODE 1: LayerNorm of a + b.
+// ---------------------------------------------------------------------------
+template <int W>
+__device__ __forceinline__ void store_mask(uint8_t* m, const bool (&k)[W]) {
+  if constexpr (W == 4) {
+    const uint32_t v = (k[0] ? 1u : 0u) | (k[1] ? 1u << 8 : 0u) | (k[2] ? 1u << 16 : 0u) | (k[3] ? 1u << 24 : 0u);
+    *reinterpret_cast<uint32_t*>(m) = v;
+  } else {
+    m[0] = k[0] ? 1 : 0;
+  }
+}
+
+template <int W>
+__device__ __forceinline__ void load_mask(const uint8_t* m, bool (&k)[W]) {
+  if constexpr (W == 4) {
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(m);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) k[w] = ((v >> (8 * w)) & 0xffu) != 0;
+  } else {
+    k[0] = m[0] != 0;
+  }
+}
+
+template <int MODE, int LPR, int V, int W>
+__global__ __launch_bounds__(kBlock) void ln_fwd_kernel(int64_t n, int D, const float* x, const float* x2,
+                                                        const float* wt, const float* bs, float p, float eps,
+                                                        uint64_t seed, float* y, float* mean, float* rstd,
+                                                        uint8_t* mask) {
+  const Geo<LPR> g;
+  const int qd = D / W;
+  const float scale = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
+  const float df = static_cast<float>(D);
+  const int64_t step = static_cast<int64_t>(gridDim.x) * Geo<LPR>::RPB;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * Geo<LPR>::RPB + g.rl; r < n; r += step) {
+    float qv[V][W];
+    float s = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int c = g.q + v * LPR;
+#pragma unroll
+      for (int w = 0; w < W; ++w) qv[v][w] = 0.0f;
+      if (c < qd) {
+        const int64_t base = r * D + c * W;
+        float xv[W];
+        Chunk<float, W>::load(x + base, xv);
+        if constexpr (MODE == 0) {
+          bool keep[W];
+#pragma unroll
+          for (int w = 0; w < W; ++w) {
+            keep[w] = block_keep(seed, static_cast<uint64_t>(base + w), p);
+            qv[v][w] = keep[w] ? xv[w] * scale : 0.0f;
+          }
+          store_mask<W>(mask + base, keep);
+        } else {
+          float bv[W];
+          Chunk<float, W>::load(x2 + base, bv);
+#pragma unroll
+          for (int w = 0; w < W; ++w) qv[v][w] = xv[w] + bv[w];
+        }
+#pragma unroll
+        for (int w = 0; w < W; ++w) s += qv[v][w];
+      }
+    }
+    const float mu = row_sum<LPR>(s) / df;
+    float cs = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      if (g.q + v * LPR < qd)
+#pragma unroll
+        for (int w = 0; w < W; ++w) cs += (qv[v][w] - mu) * (qv[v][w] - mu);
+    const float rs = 1.0f / sqrtf(row_sum<LPR>(cs) / df + eps);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int c = g.q + v * LPR;
+      if (c < qd) {
+        float wv[W], bv[W], o[W];
+        Chunk<float, W>::load(wt + c * W, wv);
+        Chunk<float, W>::load(bs + c * W, bv);
+#pragma unroll
+        for (int w = 0; w < W; ++w) o[w] = (qv[v][w] - mu) * rs * wv[w] + bv[w];
+        Chunk<float, W>::store(y + r * D + c * W, o);
+      }
+    }
+    if (g.q == 0) {
+      mean[r] = mu;
+      rstd[r] = rs;
+    }
+  }
+}
+
+// dx (MODE 0) or dz (MODE 1) per row, and the row block's partial sums of
+// gy*xhat (weight) and gy (bias): part layout [2][nb][D].
+template <int MODE, int LPR, int V, int W>
+__global__ __launch_bounds__(kBlock) void ln_bwd_kernel(int64_t n, int D, const float* gy, const float* x,
+                                                        const float* x2, const float* wt, const float* mean,
+                                                        const float* rstd, const uint8_t* mask, float p, float* dx,
+                                                        float* part, int nb) {
+  __shared__ float lds[kBlock * V * W];
+  const Geo<LPR> g;
+  const int qd = D / W;
+  const float scale = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
+  const float df = static_cast<float>(D);
+  int64_t r0, r1;
+  block_rows(n, nb, blockIdx.x, r0, r1);
+  float aw[V][W], ab[V][W], wv[V][W];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) aw[v][w] = ab[v][w] = wv[v][w] = 0.0f;
+    if (g.q + v * LPR < qd) Chunk<float, W>::load(wt + (g.q + v * LPR) * W, wv[v]);
+  }
+  // Every lane of a row runs the same trip count (the loop bound is per row).
+  for (int64_t r = r0 + g.rl; r < r1; r += Geo<LPR>::RPB) {
+    const float mu = mean[r];
+    const float rs = rstd[r];
+    float xh[V][W], dn[V][W], gv[V][W];
+    bool keep[V][W];
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int c = g.q + v * LPR;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        xh[v][w] = dn[v][w] = gv[v][w] = 0.0f;
+        keep[v][w] = true;
+      }
+      if (c < qd) {
+        const int64_t base = r * D + c * W;
+        float xv[W];
+        Chunk<float, W>::load(x + base, xv);
+        Chunk<float, W>::load(gy + base, gv[v]);
+        float qv[W];
+        if constexpr (MODE == 0) {
+          load_mask<W>(mask + base, keep[v]);
+#pragma unroll
+          for (int w = 0; w < W; ++w) qv[w] = keep[v][w] ? xv[w] * scale : 0.0f;
+        } else {
+          float bv[W];
+          Chunk<float, W>::load(x2 + base, bv);
+#pragma unroll
+          for (int w = 0; w < W; ++w) qv[w] = xv[w] + bv[w];
+        }
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          xh[v][w] = (qv[w] - mu) * rs;
+          dn[v][w] = gv[v][w] * wv[v][w];
+          s1 += dn[v][w];
+          s2 += dn[v][w] * xh[v][w];
+          aw[v][w] = fmaf(gv[v][w], xh[v][w], aw[v][w]);
+          ab[v][w] += gv[v][w];
+        }
+      }
+    }
+    s1 = row_sum<LPR>(s1);
+    s2 = row_sum<LPR>(s2);
+    const float k = rs / df;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int c = g.q + v * LPR;
+      if (c < qd) {
+        float o[W];
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          const float dq = k * (df * dn[v][w] - s1 - xh[v][w] * s2);
+          o[w] = MODE == 0 ? (keep[v][w] ? dq * scale : 0.0f) : dq;
+        }
+        Chunk<float, W>::store(dx + r * D + c * W, o);
+      }
+    }
+  }
+  block_colsum<LPR, V, W>(aw, lds, part + static_cast<int64_t>(blockIdx.x) * D, D);
+  block_colsum<LPR, V, W>(ab, lds, part + (static_cast<int64_t>(nb) + blockIdx.x) * D, D);
+}
+
+template <int W>
+__global__ __launch_bounds__(kBlock) void gamma_fwd_kernel(int64_t n, int D, const float* h, const float* gsrc,
+                                                           const float* gamma, float p, uint64_t seed, float* y,
+                                                           uint8_t* mask) {
+  const int qd = D / W;
+  const int64_t total = n * qd;
+  const float scale = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kBlock) {
+    const int64_t r = i / qd;
+    const int c = static_cast<int>(i - r * qd);
+    const int64_t base = r * D + c * W;
+    float hv[W], gv[W], gm[W], o[W];
+    bool keep[W];
+    Chunk<float, W>::load(h + base, hv);
+    Chunk<float, W>::load(gsrc + base, gv);
+    Chunk<float, W>::load(gamma + c * W, gm);
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      keep[w] = block_keep(seed, static_cast<uint64_t>(base + w), p);
+      const float gd = keep[w] ? gv[w] * scale : 0.0f;
+      o[w] = hv[w] + gm[w] * gd;
+    }
+    store_mask<W>(mask + base, keep);
+    Chunk<float, W>::store(y + base, o);
+  }
+}
+
+// grad_g = gy * gamma * m and the row block's partial sum of gy * g * m
+// (m = keep / (1 - p)).
+template <int LPR, int V, int W>
+__global__ __launch_bounds__(kBlock) void gamma_bwd_kernel(int64_t n, int D, const float* gy, const float* gsrc,
+                                                           const float* gamma, const uint8_t* mask, float p,
+                                                           float* grad_g, float* part, int nb) {
+  __shared__ float lds[kBlock * V * W];
+  const Geo<LPR> g;
+  const int qd = D / W;
+  const float scale = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
+  int64_t r0, r1;
+  block_rows(n, nb, blockIdx.x, r0, r1);
+  float acc[V][W], gm[V][W];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+#pragma unroll
+    for (int w = 0; w < W; ++w) acc[v][w] = gm[v][w] = 0.0f;
+    if (g.q + v * LPR < qd) Chunk<float, W>::load(gamma + (g.q + v * LPR) * W, gm[v]);
+  }
+  for (int64_t r = r0 + g.rl; r < r1; r += Geo<LPR>::RPB) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int c = g.q + v * LPR;
+      if (c < qd) {
+        const int64_t base = r * D + c * W;
+        float go[W], gv[W], o[W];
+        bool keep[W];
+        Chunk<float, W>::load(gy + base, go);
+        Chunk<float, W>::load(gsrc + base, gv);
+        load_mask<W>(mask + base, keep);
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          const float m = keep[w] ? scale : 0.0f;
+          o[w] = go[w] * gm[v][w] * m;
+          acc[v][w] += go[w] * gv[w] * m;
+        }
+        Chunk<float, W>::store(grad_g + base, o);
+      }
+    }
+  }
+  block_colsum<LPR, V, W>(acc, lds, part + static_cast<int64_t>(blockIdx.x) * D, D);
+}
+
+// ---------------------------------------------------------------------------
+// Host helpers.
+// ---------------------------------------------------------------------------
+inline int chunk_width(int width, std::initializer_list<const void*> ptrs) {
+  if (width % 4 != 0) return 1;
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return 1;
+  return 4;
+}
+
+int check_rows(const char* who, int64_t n, int D) {
+  if (n < 0) return set_error(kInvalid, "%s: negative row count", who);
+  if (D < 1 || D > 256) return set_error(kInvalid, "%s: requires 1<=D<=256, got %d", who, D);
+  return kOk;
+}
+
+int64_t colsum_bytes(int64_t n, int width, int quantities) {
+  return 4LL * quantities * colsum_blocks(n) * width;
+}
+
+}  // namespace nodeops
+}  // namespace cign
+
+using namespace cign;
+using namespace cign::rowops;
+using namespace cign::nodeops;
+
+extern "C" {
+
+// Workspace bytes of a backward whose parameter gradient sums `quantities`
+// vectors of `width` floats over n rows (see each entry point).
+int64_t cign_colsum_workspace_bytes(int64_t n, int32_t width, int32_t quantities) {
+  return colsum_bytes(n, width, quantities);
+}
+
+// ---- attention logits --------------------------------------------------------
+int cign_attn_logits_fwd(void* stream, int64_t n, int32_t H, int32_t C, const float* x, const float* att_src,
+                         const float* att_dst, float* alpha_src, float* alpha_dst) {
+  if (n < 0 || H < 1 || C < 1) return set_error(kInvalid, "cign_attn_logits_fwd: bad shape n=%lld H=%d C=%d",
+                                                static_cast<long long>(n), H, C);
+  if (n == 0) return kOk;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int W = chunk_width(C, {x, att_src, att_dst});
+  const int64_t rows = n * H;
+  const int rc = with_geo(C / W, [&](auto LC, auto VC) {
+    constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
+    const int grid = grid_for(rows, Geo<L>::RPB);
+    if (W == 4)
+      hipLaunchKernelGGL((attn_fwd_kernel<L, V, 4>), dim3(grid), dim3(kBlock), 0, st, rows, H, C, x, att_src, att_dst,
+                         alpha_src, alpha_dst);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<L, V, 1>), dim3(grid), dim3(kBlock), 0, st, rows, H, C, x, att_src, att_dst,
+                         alpha_src, alpha_dst);
+    return check_launch("cign_attn_logits_fwd");
+  });
+  if (rc < 0) return set_error(kInvalid, "cign_attn_logits_fwd: channels=%d too wide (max %d)", C, 256 * W);
+  return rc;
+}
+
+int cign_attn_logits_bwd(void* stream, int64_t n, int32_t H, int32_t C, const float* grad_src, const float* grad_dst,
+                         const float* x, const float* att_src, const float* att_dst, float* grad_x,
+                         float* grad_att_src, float* grad_att_dst, void* workspace, int64_t workspace_bytes) {
+  if (n < 0 || H < 1 || C < 1) return set_error(kInvalid, "cign_attn_logits_bwd: bad shape");
+  const int F = H * C;
+  if (workspace_bytes < colsum_bytes(n, F, 2)) return set_error(kInvalid, "cign_attn_logits_bwd: workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nb = colsum_blocks(n);
+  float* part = static_cast<float*>(workspace);
+  const int W = chunk_width(C, {x, att_src, att_dst, grad_x});
+  const int qf = F / W;
+  if (n > 0) {
+    auto launch = [&](auto LC, auto VC) {
+      constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
+      const dim3 grid(nb, (qf + L * V - 1) / (L * V));
+      if (W == 4)
+        hipLaunchKernelGGL((attn_bwd_kernel<L, V, 4>), grid, dim3(kBlock), 0, st, n, H, C, grad_src, grad_dst, x,
+                           att_src, att_dst, grad_x, part, nb);
+      else
+        hipLaunchKernelGGL((attn_bwd_kernel<L, V, 1>), grid, dim3(kBlock), 0, st, n, H, C, grad_src, grad_dst, x,
+                           att_src, att_dst, grad_x, part, nb);
+      return check_launch("cign_attn_logits_bwd");
+    };
+    const int rc = qf > 256 ? launch(IC<64>(), IC<4>()) : with_geo(qf, launch);
+    if (rc) return rc;
+  } else {
+    return zero_outputs(st, grad_att_src, F, grad_att_dst, F, "cign_attn_logits_bwd");
+  }
+  return launch_colsum(st, part, nb, F, 2, grad_att_src, grad_att_dst, "cign_attn_logits_bwd");
+}
+
+// ---- head mean + bias + SiLU ----------------------------------------------
+int cign_head_silu_fwd(void* stream, int64_t n, int32_t H, int32_t C, const float* out, const float* bias, float* y,
+                       float* pre) {
+  if (n < 0 || H < 1 || C < 1) return set_error(kInvalid, "cign_head_silu_fwd: bad shape");
+  if (n == 0) return kOk;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int W = chunk_width(C, {out, bias, y, pre});
+  const int grid = grid_for(n * (C / W), kBlock);
+  if (W == 4)
+    hipLaunchKernelGGL((head_silu_fwd_kernel<4>), dim3(grid), dim3(kBlock), 0, st, n, H, C, out, bias, y, pre);
+  else
+    hipLaunchKernelGGL((head_silu_fwd_kernel<1>), dim3(grid), dim3(kBlock), 0, st, n, H, C, out, bias, y, pre);
+  return check_launch("cign_head_silu_fwd");
+}
+
+int cign_head_silu_bwd(void* stream, int64_t n, int32_t H, int32_t C, const float* grad_y, const float* pre,
+                       float* grad_out, float* grad_bias, void* workspace, int64_t workspace_bytes) {
+  if (n < 0 || H < 1 || C < 1) return set_error(kInvalid, "cign_head_silu_bwd: bad shape");
+  if (workspace_bytes < colsum_bytes(n, C, 1)) return set_error(kInvalid, "cign_head_silu_bwd: workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nb = colsum_blocks(n);
+  float* part = static_cast<float*>(workspace);
+  const int W = chunk_width(C, {grad_y, pre, grad_out});
+  const int qc = C / W;
+  if (n > 0) {
+    auto launch = [&](auto LC, auto VC) {
+      constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
+      const dim3 grid(nb, (qc + L * V - 1) / (L * V));
+      if (W == 4)
+        hipLaunchKernelGGL((head_silu_bwd_kernel<L, V, 4>), grid, dim3(kBlock), 0, st, n, H, C, grad_y, pre, grad_out,
+                           part, nb);
+      else
+        hipLaunchKernelGGL((head_silu_bwd_kernel<L, V, 1>), grid, dim3(kBlock), 0, st, n, H, C, grad_y, pre, grad_out,
+                           part, nb);
+      return check_launch("cign_head_silu_bwd");
+    };
+    const int rc = qc > 256 ? launch(IC<64>(), IC<4>()) : with_geo(qc, launch);
+    if (rc) return rc;
+  } else {
+    return zero_outputs(st, grad_bias, C, nullptr, 0, "cign_head_silu_bwd");
+  }
+  return launch_colsum(st, part, nb, C, 1, grad_bias, nullptr, "cign_head_silu_bwd");
+}
+
+// ---- block ops ------------------------------------------------------------
+static int ln_fwd(int mode, void* stream, int64_t n, int32_t D, const float* x, const float* x2, const float* w,
+                  const float* b, float p, float eps, uint64_t seed, float* y, float* mean, float* rstd,
+                  uint8_t* mask, const char* who) {
+  int rc = check_rows(who, n, D);
+  if (rc) return rc;
+  if (!(p >= 0.0f && p < 1.0f)) return set_error(kInvalid, "%s: dropout_p must be in [0,1)", who);
+  if (n == 0) return kOk;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int W = chunk_width(D, {x, x2 ? x2 : x, w, b, y, mask ? static_cast<const void*>(mask) : x});
+  return with_geo(D / W, [&](auto LC, auto VC) {
+    constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
+    const int grid = grid_for(n, Geo<L>::RPB);
+#define CIGN_LN_FWD(M, WW)                                                                                          \
+  hipLaunchKernelGGL((ln_fwd_kernel<M, L, V, WW>), dim3(grid), dim3(kBlock), 0, st, n, D, x, x2, w, b, p, eps, seed, \
+                     y, mean, rstd, mask)
+    if (mode == 0) {
+      if (W == 4) CIGN_LN_FWD(0, 4); else CIGN_LN_FWD(0, 1);
+    } else {
+      if (W == 4) CIGN_LN_FWD(1, 4); else CIGN_LN_FWD(1, 1);
+    }
+#undef CIGN_LN_FWD
+    return check_launch(who);
+  });
+}
+
+static int ln_bwd(int mode, void* stream, int64_t n, int32_t D, const float* gy, const float* x, const float* x2,
+                  const float* w, const float* mean, const float* rstd, const uint8_t* mask, float p, float* dx,
+                  float* dw, float* db, void* workspace, int64_t workspace_bytes, const char* who) {
+  int rc = check_rows(who, n, D);
+  if (rc) return rc;
+  if (workspace_bytes < colsum_bytes(n, D, 2)) return set_error(kInvalid, "%s: workspace too small", who);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nb = colsum_blocks(n);
+  float* part = static_cast<float*>(workspace);
+  if (n > 0) {
+    const int W = chunk_width(D, {gy, x, x2 ? x2 : x, w, dx, mask ? static_cast<const void*>(mask) : x});
+    rc = with_geo(D / W, [&](auto LC, auto VC) {
+      constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
+#define CIGN_LN_BWD(M, WW)                                                                                           \
+  hipLaunchKernelGGL((ln_bwd_kernel<M, L, V, WW>), dim3(nb), dim3(kBlock), 0, st, n, D, gy, x, x2, w, mean, rstd, mask, \
+                     p, dx, part, nb)
+      if (mode == 0) {
+        if (W == 4) CIGN_LN_BWD(0, 4); else CIGN_LN_BWD(0, 1);
+      } else {
+        if (W == 4) CIGN_LN_BWD(1, 4); else CIGN_LN_BWD(1, 1);
+      }
+#undef CIGN_LN_BWD
+      return check_launch(who);
+    });
+    if (rc) return rc;
+  } else {
+    return zero_outputs(st, dw, D, db, D, who);
+  }
+  return launch_colsum(st, part, nb, D, 2, dw, db, who);
+}
+
+int cign_dropout_ln_fwd(void* stream, int64_t n, int32_t D, const float* x, const float* weight, const float* bias,
+                        float dropout_p, float eps, uint64_t seed, float* y, float* mean, float* rstd, uint8_t* mask) {
+  return ln_fwd(0, stream, n, D, x, nullptr, weight, bias, dropout_p, eps, seed, y, mean, rstd, mask,
+                "cign_dropout_ln_fwd");
+}
+
+int cign_dropout_ln_bwd(void* stream, int64_t n, int32_t D, const float* grad_y, const float* x, const float* weight,
+                        const float* mean, const float* rstd, const uint8_t* mask, float dropout_p, float* grad_x,
+                        float* grad_weight, float* grad_bias, void* workspace, int64_t workspace_bytes) {
+  return ln_bwd(0, stream, n, D, grad_y, x, nullptr, weight, mean, rstd, mask, dropout_p, grad_x, grad_weight,
+                grad_bias, workspace, workspace_bytes, "cign_dropout_ln_bwd");
+}
+
+int cign_add_ln_fwd(void* stream, int64_t n, int32_t D, const float* a, const float* b, const float* weight,
+                    const float* bias, float eps, float* y, float* mean, float* rstd) {
+  return ln_fwd(1, stream, n, D, a, b, weight, bias, 0.0f, eps, 0, y, mean, rstd, nullptr, "cign_add_ln_fwd");
+}
+
+int cign_add_ln_bwd(void* stream, int64_t n, int32_t D, const float* grad_y, const float* a, const float* b,
+                    const float* weight, const float* mean, const float* rstd, float* grad_z, float* grad_weight,
+                    float* grad_bias, void* workspace, int64_t workspace_bytes) {
+  return ln_bwd(1, stream, n, D, grad_y, a, b, weight, mean, rstd, nullptr, 0.0f, grad_z, grad_weight, grad_bias,
+                workspace, workspace_bytes, "cign_add_ln_bwd");
+}
+
+int cign_gamma_residual_fwd(void* stream, int64_t n, int32_t D, const float* h, const float* g, const float* gamma,
+                            float dropout_p, uint64_t seed, float* y, uint8_t* mask) {
+  int rc = check_rows("cign_gamma_residual_fwd", n, D);
+  if (rc) return rc;
+  if (!(dropout_p >= 0.0f && dropout_p < 1.0f))
+    return set_error(kInvalid, "cign_gamma_residual_fwd: dropout_p must be in [0,1)");
+  if (n == 0) return kOk;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int W = chunk_width(D, {h, g, gamma, y, mask});
+  const int grid = grid_for(n * (D / W), kBlock);
+  if (W == 4)
+    hipLaunchKernelGGL((gamma_fwd_kernel<4>), dim3(grid), dim3(kBlock), 0, st, n, D, h, g, gamma, dropout_p, seed, y,
+                       mask);
+  else
+    hipLaunchKernelGGL((gamma_fwd_kernel<1>), dim3(grid), dim3(kBlock), 0, st, n, D, h, g, gamma, dropout_p, seed, y,
+                       mask);
+  return check_launch("cign_gamma_residual_fwd");
+}
+
+int cign_gamma_residual_bwd(void* stream, int64_t n, int32_t D, const float* grad_y, const float* g,
+                            const float* gamma, const uint8_t* mask, float dropout_p, float* grad_g, float* grad_gamma,
+                            void* workspace, int64_t workspace_bytes) {
+  int rc = check_rows("cign_gamma_residual_bwd", n, D);
+  if (rc) return rc;
+  if (workspace_bytes < colsum_bytes(n, D, 1))
+    return set_error(kInvalid, "cign_gamma_residual_bwd: workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nb = colsum_blocks(n);
+  float* part = static_cast<float*>(workspace);
+  if (n > 0) {
+    const int W = chunk_width(D, {grad_y, g, gamma, mask, grad_g});
+    rc = with_geo(D / W, [&](auto LC, auto VC) {
+      constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
+      if (W == 4)
+        hipLaunchKernelGGL((gamma_bwd_kernel<L, V, 4>), dim3(nb), dim3(kBlock), 0, st, n, D, grad_y, g, gamma, mask,
+                           dropout_p, grad_g, part, nb);
+      else
+        hipLaunchKernelGGL((gamma_bwd_kernel<L, V, 1>), dim3(nb), dim3(kBlock), 0, st, n, D, grad_y, g, gamma, mask,
+                           dropout_p, grad_g, part, nb);
+      return check_launch("cign_gamma_residual_bwd");
+    });
+    if (rc) return rc;
+  } else {
+    return zero_outputs(st, grad_gamma, D, nullptr, 0, "cign_gamma_residual_bwd");
+  }
+  return launch_colsum(st, part, nb, D, 1, grad_gamma, nullptr, "cign_gamma_residual_bwd");
+}
+
+}  // extern "C"

@@ -123,6 +123,111 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
                  int32_t* col_counters, void* workspace, int64_t workspace_bytes, void* grad_feat,
                  float* grad_attn_row, float* grad_attn_col, float* grad_bias);
 
+/* ---- GAT side ops (float32) ---------------------------------------------- */
+
+/* Workspace bytes of a backward entry point below whose parameter gradient
+ * sums `quantities` vectors of `width` floats over n rows:
+ * cign_attn_logits_bwd (H*C, 2), cign_head_silu_bwd (C, 1),
+ * cign_dropout_ln_bwd / cign_add_ln_bwd (D, 2), cign_gamma_residual_bwd (D, 1).
+ * Replaces the temporaries of the reference's two-stage reductions
+ * (fused_block_ops_cuda.cu PARAM_CHUNK_N partials). */
+int64_t cign_colsum_workspace_bytes(int64_t n, int32_t width, int32_t quantities);
+
+/* alpha_src[n,h] = <x[n,h,:], att_src[h,:]>, alpha_dst likewise. x [n,H,C],
+ * att_* [1,H,C], alpha_* [n,H]. Replaces ext attention_forward
+ * (fused_gat_sideops_ext/fused_gat_sideops.cpp:45-51; kernels
+ * fused_gat_sideops_cuda.cu:25-60). C <= 1024. */
+int cign_attn_logits_fwd(void* stream, int64_t n, int32_t heads, int32_t channels, const float* x,
+                         const float* att_src, const float* att_dst, float* alpha_src, float* alpha_dst);
+
+/* grad_x = gs*att_src + gd*att_dst; grad_att_* [1,H,C] = sum_n g[n,h] x[n,h,:]
+ * (deterministic). Replaces ext attention_backward (fused_gat_sideops.cpp:54-66;
+ * kernels fused_gat_sideops_cuda.cu:65-167). */
+int cign_attn_logits_bwd(void* stream, int64_t n, int32_t heads, int32_t channels, const float* grad_src,
+                         const float* grad_dst, const float* x, const float* att_src, const float* att_dst,
+                         float* grad_x, float* grad_att_src, float* grad_att_dst, void* workspace,
+                         int64_t workspace_bytes);
+
+/* pre = sum_h out[n,h,:] / H + bias, y = SiLU(pre). Replaces ext
+ * head_silu_forward (fused_gat_sideops.cpp:68-76; kernel
+ * fused_gat_sideops_cuda.cu:171-195). */
+int cign_head_silu_fwd(void* stream, int64_t n, int32_t heads, int32_t channels, const float* out,
+                       const float* bias, float* y, float* pre);
+
+/* grad_out[n,h,:] = grad_y SiLU'(pre) / H, grad_bias = sum_n grad_y SiLU'(pre).
+ * Replaces ext head_silu_backward (fused_gat_sideops.cpp:78-90; kernels
+ * fused_gat_sideops_cuda.cu:197-239). */
+int cign_head_silu_bwd(void* stream, int64_t n, int32_t heads, int32_t channels, const float* grad_y,
+                       const float* pre, float* grad_out, float* grad_bias, void* workspace, int64_t workspace_bytes);
+
+/* ---- block ops (float32, 1 <= D <= 256) ----------------------------------- */
+
+/* q = keep * x / (1-p) (keep: splitmix64 53-bit bits of seed and n*D+c,
+ * u >= p; mask [n,D] u8 written), y = LayerNorm(q) * weight + bias; mean,
+ * rstd [n]. Replaces ext dropout_layernorm_forward (fused_block_ops.py:15,
+ * fused_block_ops_ext/fused_block_ops.cpp:39-45; kernels
+ * fused_block_ops_cuda.cu:45-70). */
+int cign_dropout_ln_fwd(void* stream, int64_t n, int32_t D, const float* x, const float* weight, const float* bias,
+                        float dropout_p, float eps, uint64_t seed, float* y, float* mean, float* rstd, uint8_t* mask);
+
+/* grad_x, grad_weight, grad_bias of the above. Replaces ext
+ * dropout_layernorm_backward (fused_block_ops.cpp:46-56; kernels
+ * fused_block_ops_cuda.cu:96-118 + param stages). */
+int cign_dropout_ln_bwd(void* stream, int64_t n, int32_t D, const float* grad_y, const float* x, const float* weight,
+                        const float* mean, const float* rstd, const uint8_t* mask, float dropout_p, float* grad_x,
+                        float* grad_weight, float* grad_bias, void* workspace, int64_t workspace_bytes);
+
+/* y = LayerNorm(a + b) * weight + bias. Replaces ext add_layernorm_forward
+ * (fused_block_ops.cpp:57-63; kernel fused_block_ops_cuda.cu:72-94). */
+int cign_add_ln_fwd(void* stream, int64_t n, int32_t D, const float* a, const float* b, const float* weight,
+                    const float* bias, float eps, float* y, float* mean, float* rstd);
+
+/* grad_z (the gradient of both a and b), grad_weight, grad_bias. Replaces ext
+ * add_layernorm_backward (fused_block_ops.cpp:64-73; kernels
+ * fused_block_ops_cuda.cu:120-139 + param stages). */
+int cign_add_ln_bwd(void* stream, int64_t n, int32_t D, const float* grad_y, const float* a, const float* b,
+                    const float* weight, const float* mean, const float* rstd, float* grad_z, float* grad_weight,
+                    float* grad_bias, void* workspace, int64_t workspace_bytes);
+
+/* y = h + gamma * keep * g / (1-p); mask [n,D] u8. Replaces ext
+ * dropout_gamma_residual_forward (fused_block_ops.cpp:74-81). */
+int cign_gamma_residual_fwd(void* stream, int64_t n, int32_t D, const float* h, const float* g, const float* gamma,
+                            float dropout_p, uint64_t seed, float* y, uint8_t* mask);
+
+/* grad_g = grad_y * gamma * m, grad_gamma = sum_n grad_y * g * m (m = keep/(1-p));
+ * grad_h = grad_y is the caller's. Replaces ext dropout_gamma_residual_backward
+ * (fused_block_ops.cpp:82-90). */
+int cign_gamma_residual_bwd(void* stream, int64_t n, int32_t D, const float* grad_y, const float* g,
+                            const float* gamma, const uint8_t* mask, float dropout_p, float* grad_g, float* grad_gamma,
+                            void* workspace, int64_t workspace_bytes);
+
+/* ---- Clifford packs (float32) ------------------------------------------- */
+
+/* Fused Clifford interaction + alpha weighting over K <= 16 hops.
+ * interaction: 0 old (D = SiLU(bhr), W = bhr - brh), 1 new (D = SiLU((bhr+brh)/2),
+ * W = (bhr-brh)/2), 2 new with tanh on W; weighting: 0 old (out [n, K*2D] =
+ * cat_k a_k [W_k, D_k]), 1 new (out [n, 2D] = [sum a_k D_k, sum a_k W_k]).
+ * props: HOST array of K device row pointers of the propagated hops, rows
+ * prop_stride floats apart (2D for separate [n,2D] tensors, 2KD for one
+ * stacked [n,K,2D] tensor); alpha [n,K]. Replaces the ext `forward` of
+ * fused_clifford_pack_ext/fused_clifford_pack.cpp:50-59 (old, K=3), the generic
+ * ext of fused_clifford_pack.py:46-63, generic_engine/fused_clifford_cign_pack_ext/
+ * fused_clifford_switch_pack.cpp:69-85 (and its tanh twin in
+ * generic_engine/fused_clifford_switch_pack_ext/), and
+ * generic_engine/fused_clifford_cign_generic.py:20-41. */
+int cign_pack_fwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t interaction, int32_t weighting,
+                  const float* H, const float* C, const float* const* props, int64_t prop_stride, const float* alpha,
+                  float* out);
+
+/* Backward of cign_pack_fwd: grad_H, grad_C [n,D], grad_props (HOST array of
+ * K device row pointers, rows grad_prop_stride apart), grad_alpha [n,K].
+ * Deterministic, no atomics. Replaces the ext `backward` of the same modules
+ * (fused_clifford_pack.cpp:61-80, fused_clifford_switch_pack.cpp:86-121). */
+int cign_pack_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t interaction, int32_t weighting,
+                  const float* grad_out, const float* H, const float* C, const float* const* props,
+                  int64_t prop_stride, const float* alpha, float* grad_H, float* grad_C, float* const* grad_props,
+                  int64_t grad_prop_stride, float* grad_alpha);
+
 #ifdef __cplusplus
 }
 #endif
