@@ -157,3 +157,28 @@ def ensure_loaded(state: dict, what: str):
     except Exception as exc:
         state["err"] = exc
         raise
+
+
+class CliffordPackFunction(torch.autograd.Function):
+    """Any interaction (0 old, 1 new, 2 new + tanh) x weighting (0 old, 1 new)
+    over K separate [N,2D] hops: the single HIP route the Clifford block uses
+    for every mode combination (the reference dispatches the same math over
+    its four pack modules and a torch fallback, model_cign.py:803-925)."""
+
+    @staticmethod
+    def forward(ctx, interaction, weighting, H, C, alpha, *props):
+        _validate(H, C, list(props), alpha)
+        ctx.modes = (int(interaction), int(weighting))
+        ctx.save_for_backward(H, C, alpha, *props)
+        return forward_list(H, C, list(props), alpha, int(interaction), int(weighting))
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        H, C, alpha, *props = ctx.saved_tensors
+        gH, gC, gP, gA = backward_list(grad_out.to(dtype=torch.float32).contiguous(), H, C, props, alpha, *ctx.modes)
+        return (None, None, gH, gC, gA, *gP)
+
+
+def clifford_pack_any(H_norm, C_norm, propagated, alpha, interaction: int, weighting: int) -> torch.Tensor:
+    H, C, props, A = prepare(H_norm, C_norm, propagated, alpha)
+    return CliffordPackFunction.apply(int(interaction), int(weighting), H, C, A, *props)

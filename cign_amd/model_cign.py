@@ -1,0 +1,226 @@
+"""The Clifford block of CIGN on the gfx950 route: a drop-in for the block-level
+classes of generic_engine/model_cign.py (GraphCliffordBlock,
+CompatibleCollapsedFusedGATConv and the helpers they use). The names,
+constructor arguments, parameter names and forward signatures are the
+reference's.
+
+The reference picks between PyG / dgNN / CUDA / torch paths with its
+``use_*`` flags. Here every flag combination runs the one HIP route:
+- fused dropout + LayerNorm (cign_dropout_ln_*);
+- the GAT ``lin`` projection (dense GEMM on MFMA via hipBLASLt);
+- fused attention logits and the collapsed GAT with head-mean + bias + SiLU;
+- fused add + LayerNorm;
+- the multihop SpMM (selected_sparse_powers);
+- the hop gate kernel;
+- the fused Clifford pack for any interaction x weighting x K;
+- the projection ``proj`` (hipBLASLt);
+- fused dropout-gamma-residual.
+
+The flags are accepted for signature compatibility and validated like the
+reference's. ``use_chunked_fused_gat`` (the dgNN chunking backend) is out of
+scope and raises.
+"""
+from __future__ import annotations
+
+import math
+import os
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _pack
+from .collapsed_gat import collapsed_gat_mean_bias_silu
+from .fused_block_ops import fused_add_layernorm, fused_dropout_gamma_residual, fused_dropout_layernorm
+from .fused_gat_sideops import fused_attention_logits
+from .graph import selected_sparse_powers
+from .hop_gate import global_hop_gate, node_hop_gate
+
+
+def cign_outer_difference(b_hr, b_rh, mode):
+    """model_cign.py:47-54: 0.5 (b_hr - b_rh), optionally through tanh."""
+    raw = 0.5 * (b_hr - b_rh)
+    if mode == "tanh":
+        return torch.tanh(raw)
+    if mode == "none":
+        return raw
+    raise ValueError(f"Invalid outer nonlinearity: {mode}")
+
+
+def _resolve_selective_amp_dtype(name: str):
+    name = str(name).strip().lower()
+    if name == "bf16":
+        return torch.bfloat16
+    if name == "fp16":
+        return torch.float16
+    raise ValueError(f"selective_amp_dtype must be bf16 or fp16, got {name!r}")
+
+
+def _resolve_old_new_mode(explicit_value, env_name: str, default: str = "old") -> str:
+    """model_cign.py:67-83: explicit argument, then environment, then default."""
+    if explicit_value is None:
+        explicit_value = os.environ.get(env_name, default)
+    value = str(explicit_value).strip().lower()
+    if value not in {"old", "new"}:
+        raise ValueError(f"{env_name} must be 'old' or 'new', got {explicit_value!r}")
+    return value
+
+
+def _local_amp_linear(linear: nn.Linear, x: torch.Tensor, enabled: bool, amp_dtype: torch.dtype) -> torch.Tensor:
+    """One dense Linear, optionally under local autocast, returned as fp32
+    (model_cign.py:86-103). On ROCm the GEMM runs on hipBLASLt (MFMA)."""
+    if bool(enabled) and x.is_cuda:
+        with torch.autocast(device_type="cuda", dtype=amp_dtype, enabled=True, cache_enabled=True):
+            y = linear(x)
+        return y.float()
+    return linear(x).float()
+
+
+def _glorot_(t: torch.Tensor) -> None:
+    """Glorot-uniform over the last two dims (PyG's GATConv initialisation)."""
+    fan = t.size(-2) + t.size(-1)
+    a = math.sqrt(6.0 / fan)
+    with torch.no_grad():
+        t.uniform_(-a, a)
+
+
+class CompatibleCollapsedFusedGATConv(nn.Module):
+    """GATConv (concat=False) whose message passing is the collapsed GAT
+    (model_cign.py:524-567). Parameters: lin.weight [H*C, in] (no bias),
+    att_src / att_dst [1,H,C], bias [C]; the names and shapes are PyG GATConv's,
+    so state dicts carry over."""
+
+    def __init__(self, in_channels: int, out_channels: int, heads: int = 1, concat: bool = False,
+                 negative_slope: float = 0.2, dropout: float = 0.0, add_self_loops: bool = False, bias: bool = True):
+        super().__init__()
+        if concat:
+            raise RuntimeError("collapsed GAT is specialized for concat=False")
+        self.in_channels, self.out_channels, self.heads = int(in_channels), int(out_channels), int(heads)
+        self.concat = False
+        self.negative_slope = float(negative_slope)
+        self.dropout = float(dropout)
+        self.add_self_loops = bool(add_self_loops)
+        self.lin = nn.Linear(in_channels, heads * out_channels, bias=False)
+        self.att_src = nn.Parameter(torch.empty(1, heads, out_channels))
+        self.att_dst = nn.Parameter(torch.empty(1, heads, out_channels))
+        self.bias = nn.Parameter(torch.empty(out_channels)) if bias else None
+        self.reset_parameters()
+
+    def reset_parameters(self):
+        _glorot_(self.lin.weight)
+        _glorot_(self.att_src)
+        _glorot_(self.att_dst)
+        if self.bias is not None:
+            nn.init.zeros_(self.bias)
+
+    def forward(self, x, csr, csc, perm):
+        H, C = self.heads, self.out_channels
+        if x.dim() != 2:
+            raise ValueError(f"FusedGAT expects a 2-D node feature tensor, got {tuple(x.shape)}")
+        if not (1 <= H <= 32) or not (1 <= C <= 256):
+            raise RuntimeError(f"Generalized collapsed GAT requires 1<=heads<=32 and 1<=channels<=256; got H={H},C={C}")
+        amp_enabled = bool(getattr(self, "_selective_amp_enabled", False))
+        amp_dtype = getattr(self, "_selective_amp_dtype", torch.bfloat16)
+        xp = _local_amp_linear(self.lin, x, amp_enabled, amp_dtype).view(-1, H, C)
+        alpha_src, alpha_dst = fused_attention_logits(xp, self.att_src, self.att_dst)
+        dropout = self.dropout if self.training else 0.0
+        return collapsed_gat_mean_bias_silu(attn_row=alpha_dst, attn_col=alpha_src, csr=csr, csc=csc, perm=perm,
+                                            negative_slope=self.negative_slope, in_feat=xp, bias=self.bias,
+                                            attn_drop=dropout)
+
+
+class GraphCliffordBlock(nn.Module):
+    """model_cign.py:573-937 on the HIP route."""
+
+    def __init__(self, hidden_dim: int, order_set=(1, 2, 3), dropout: float = 0.28, gat_heads: int = 6,
+                 gat_dropout: float = 0.32, use_fused_gat: bool = False, use_fused_gat_sideops: bool = False,
+                 use_chunked_fused_gat: bool = False, use_collapsed_fused_gat: bool = False,
+                 use_fused_clifford_pack: bool = False, use_fused_block_ops: bool = False,
+                 use_selective_amp: bool = False, selective_amp_dtype: str = "bf16", init_gamma: float = 0.49,
+                 gamma_mode: str = "vector", hop_gate_mode: str = "node", alpha_score_mode: str = None,
+                 interaction_mode: str = None, alpha_weighting_mode: str = None, use_bias: bool = True):
+        super().__init__()
+        if len(order_set) == 0:
+            raise ValueError("order_set / hop_scales cannot be empty.")
+        if any(int(s) < 0 for s in order_set):
+            raise ValueError("All propagation orders must be non-negative integers.")
+        if gamma_mode not in {"scalar", "vector"}:
+            raise ValueError("gamma_mode must be either 'scalar' or 'vector'.")
+        if hop_gate_mode not in {"none", "global", "node"}:
+            raise ValueError("hop_gate_mode must be one of {'none', 'global', 'node'}.")
+        if use_chunked_fused_gat:
+            raise ValueError("the chunked dgNN GAT backend is not part of the HIP route")
+        self.hidden_dim = hidden_dim
+        self.order_set = [int(s) for s in order_set]
+        self.num_hops = len(self.order_set)
+        self.dropout = dropout
+        self.gamma_mode = gamma_mode
+        self.hop_gate_mode = hop_gate_mode
+        self.alpha_score_mode = _resolve_old_new_mode(alpha_score_mode, "CIGN_ALPHA_SCORE_MODE", "new")
+        self.interaction_mode = _resolve_old_new_mode(interaction_mode, "CIGN_INTERACTION_MODE", "new")
+        self.alpha_weighting_mode = _resolve_old_new_mode(alpha_weighting_mode, "CIGN_ALPHA_WEIGHTING_MODE", "old")
+        self.use_fused_gat = bool(use_fused_gat)
+        self.use_fused_gat_sideops = bool(use_fused_gat_sideops)
+        self.use_chunked_fused_gat = False
+        self.use_collapsed_fused_gat = bool(use_collapsed_fused_gat)
+        self.outer_nonlinearity = os.environ.get("CIGN_OUTER_NONLINEARITY", "none").strip().lower()
+        if self.outer_nonlinearity not in {"tanh", "none"}:
+            raise ValueError("CIGN_OUTER_NONLINEARITY must be tanh or none")
+        self.use_fused_clifford_pack = bool(use_fused_clifford_pack)
+        self.use_fused_block_ops = bool(use_fused_block_ops)
+        self.use_selective_amp = bool(use_selective_amp)
+        self.selective_amp_dtype_name = str(selective_amp_dtype).strip().lower()
+        self.selective_amp_dtype = _resolve_selective_amp_dtype(self.selective_amp_dtype_name)
+
+        self.h_norm = nn.LayerNorm(hidden_dim)
+        self.c_norm = nn.LayerNorm(hidden_dim)
+        self.context_gat = CompatibleCollapsedFusedGATConv(in_channels=hidden_dim, out_channels=hidden_dim,
+                                                           heads=gat_heads, concat=False, dropout=gat_dropout,
+                                                           add_self_loops=False, bias=use_bias)
+        self.context_gat._selective_amp_enabled = self.use_selective_amp
+        self.context_gat._selective_amp_dtype = self.selective_amp_dtype
+        proj_in_dim = 2 * self.num_hops * hidden_dim if self.alpha_weighting_mode == "old" else 2 * hidden_dim
+        self.proj = nn.Linear(proj_in_dim, hidden_dim, bias=use_bias)
+        if hop_gate_mode == "global":
+            self.hop_gate_logits = nn.Parameter(torch.zeros(self.num_hops))
+            self.hop_gate_mlp = None
+        elif hop_gate_mode == "node":
+            self.hop_gate_logits = None
+            self.hop_gate_mlp = nn.Linear(2 * hidden_dim, self.num_hops, bias=True)
+        else:
+            self.hop_gate_logits = None
+            self.hop_gate_mlp = None
+        if gamma_mode == "vector":
+            self.gamma = nn.Parameter(torch.full((hidden_dim,), float(init_gamma)))
+        else:
+            self.gamma = nn.Parameter(torch.tensor(float(init_gamma)))
+
+    def compute_hop_gate(self, H_norm: torch.Tensor, C_norm: torch.Tensor):
+        if self.hop_gate_mode == "none":
+            return None
+        if self.hop_gate_mode == "global":
+            return global_hop_gate(self.hop_gate_logits, H_norm.size(0))
+        return node_hop_gate(H_norm, C_norm, self.hop_gate_mlp, self.alpha_score_mode)
+
+    def _interaction_code(self) -> int:
+        if self.interaction_mode == "old":
+            return 0
+        return 2 if self.outer_nonlinearity == "tanh" else 1
+
+    def forward(self, H: torch.Tensor, edge_index: torch.Tensor, graph_operator, fused_gat_graph=None) -> torch.Tensor:
+        p = self.dropout if self.training else 0.0
+        H_norm = fused_dropout_layernorm(H, self.h_norm.weight, self.h_norm.bias, p, self.h_norm.eps)
+        if fused_gat_graph is None:
+            raise RuntimeError("The GAT graph format cache was not prepared. Call prepare_fused_gat_graph(...) once "
+                               "before training.")
+        csr, csc, perm = fused_gat_graph
+        C_gat = self.context_gat(H_norm, csr, csc, perm)
+        C_norm = fused_add_layernorm(C_gat, H_norm, self.c_norm.weight, self.c_norm.bias, self.c_norm.eps)
+        HC_norm = torch.cat([H_norm, C_norm], dim=-1)
+        propagated = selected_sparse_powers(operator=graph_operator, X=HC_norm, powers=self.order_set)
+        hop_gate = self.compute_hop_gate(H_norm, C_norm)
+        G_raw = _pack.clifford_pack_any(H_norm, C_norm, [propagated[s] for s in self.order_set], hop_gate,
+                                        self._interaction_code(), 0 if self.alpha_weighting_mode == "old" else 1)
+        G_feat = _local_amp_linear(self.proj, G_raw, self.use_selective_amp, self.selective_amp_dtype)
+        gamma = self.gamma if self.gamma_mode == "vector" else self.gamma.expand(self.hidden_dim)
+        return fused_dropout_gamma_residual(H, G_feat, gamma.contiguous(), p)

@@ -201,6 +201,25 @@ int cign_gamma_residual_bwd(void* stream, int64_t n, int32_t D, const float* gra
                             const float* gamma, const uint8_t* mask, float dropout_p, float* grad_g, float* grad_gamma,
                             void* workspace, int64_t workspace_bytes);
 
+/* ---- hop gate (float32) ------------------------------------------------- */
+
+/* Node-mode hop gate: alpha [n,K] = softmax_k(score @ weight^T + bias), score
+ * [n,2D] = [H | C] (score_mode 0, old) or [H + C | |H - C|] (1, new); weight
+ * [K,2D], bias [K], K <= 16. Replaces GraphCliffordBlock.compute_hop_gate
+ * (generic_engine/model_cign.py:721-749: concatenation, Linear, softmax). */
+int cign_hop_gate_fwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t score_mode, const float* H,
+                      const float* C, const float* weight, const float* bias, float* alpha);
+
+/* Workspace bytes of cign_hop_gate_bwd. */
+int64_t cign_hop_gate_bwd_workspace_bytes(int64_t n, int32_t D, int32_t K);
+
+/* Backward of cign_hop_gate_fwd given alpha and grad_alpha: grad_H, grad_C
+ * [n,D], grad_weight [K,2D], grad_bias [K] (deterministic; sign(0) = 0 for the
+ * |H - C| term, as torch's abs). Replaces the autograd of the same lines. */
+int cign_hop_gate_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t score_mode, const float* H,
+                      const float* C, const float* weight, const float* alpha, const float* grad_alpha, float* grad_H,
+                      float* grad_C, float* grad_weight, float* grad_bias, void* workspace, int64_t workspace_bytes);
+
 /* ---- Clifford packs (float32) ------------------------------------------- */
 
 /* Fused Clifford interaction + alpha weighting over K <= 16 hops.

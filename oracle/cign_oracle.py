@@ -526,3 +526,45 @@ def gamma_residual_backward(gy, g, gamma, p, keep):
     m = np.where(keep, scale, 0.0)
     gy = np.asarray(gy, np.float64)
     return gy, gy * np.asarray(gamma, np.float64) * m, (gy * np.asarray(g, np.float64) * m).sum(axis=0)
+
+
+# ---------------------------------------------------------------------------
+# Hop gate (node mode)
+# ---------------------------------------------------------------------------
+def hop_gate_score(H, C, score_mode):
+    """generic_engine/model_cign.py:731-745: old [H | C], new [H + C | |H - C|]."""
+    H = np.asarray(H, np.float64)
+    C = np.asarray(C, np.float64)
+    if int(score_mode) == 0:
+        return np.concatenate([H, C], axis=1)
+    return np.concatenate([H + C, np.abs(H - C)], axis=1)
+
+
+def hop_gate_forward(H, C, weight, bias, score_mode):
+    """alpha = softmax_k(score @ weight.T + bias), model_cign.py:747-749."""
+    s = hop_gate_score(H, C, score_mode)
+    logits = s @ np.asarray(weight, np.float64).T + np.asarray(bias, np.float64)
+    logits = logits - logits.max(axis=1, keepdims=True)
+    e = np.exp(logits)
+    return e / e.sum(axis=1, keepdims=True)
+
+
+def hop_gate_backward(g_alpha, H, C, weight, bias, score_mode):
+    """Gradients (gH, gC, g_weight, g_bias) of hop_gate_forward: softmax
+    Jacobian, then the linear map, then the score (d|x|/dx = sign(x), 0 at 0)."""
+    H = np.asarray(H, np.float64)
+    C = np.asarray(C, np.float64)
+    Wt = np.asarray(weight, np.float64)
+    a = hop_gate_forward(H, C, weight, bias, score_mode)
+    g = np.asarray(g_alpha, np.float64)
+    gl = a * (g - (a * g).sum(axis=1, keepdims=True))
+    s = hop_gate_score(H, C, score_mode)
+    gs = gl @ Wt
+    D = H.shape[1]
+    g1, g2 = gs[:, :D], gs[:, D:]
+    if int(score_mode) == 0:
+        gH, gC = g1, g2
+    else:
+        sg = np.sign(H - C)
+        gH, gC = g1 + sg * g2, g1 - sg * g2
+    return gH, gC, gl.T @ s, gl.sum(axis=0)

@@ -1,0 +1,133 @@
+"""GPU parity of the Clifford block composition (cign_amd.model_cign.
+GraphCliffordBlock on the HIP route) against the float64 torch restatement of
+the reference block (oracle/block_oracle.py), forward output and the
+gradients of the input and of every parameter, in eval mode (no dropout; the
+dropout masks are pinned op by op in test_gpu_nodeops / test_gpu_gat).
+fp32 tolerance 1e-4 rel / 1e-5 abs, with atol scaled by the largest |value|
+for sums over nodes (parameter gradients); bf16 selective AMP 2e-2."""
+import numpy as np
+import pytest
+import torch
+
+from tests.conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(n=300, D=32, seed=0):
+    from cign_amd import graph, graphgen, workloads
+    from cign_amd.multihop_csr_pipeline import MultiHopCSR3GraphOperator
+
+    ei = graphgen.chung_lu_directed(n, 6 * n, gamma=2.5, max_degree=80.0, seed=seed)
+    edge_index = torch.from_numpy(ei)
+    used, P = graph.build_sparse_normalized_adjacency(edge_index, n)
+    op_cpu = graph.prepare_fixed_csr_operator(P)
+    op = graph.FixedCSRGraphOperator(workloads._to_device_csr(op_cpu.csr, "cuda"),
+                                     workloads._to_device_csr(op_cpu.csr_t, "cuda"))
+    gat_ei = graph.prepare_gat_edge_index(used, n)
+    (rowptr, col), (row, colptr), perm = graph.prepare_fused_gat_graph(gat_ei, n)
+    gat_graph = ((rowptr.cuda(), col.cuda()), (row.cuda(), colptr.cuda()), perm.cuda())
+    mh = MultiHopCSR3GraphOperator(op, dense_cols=2 * D)
+    csr = op_cpu.csr
+    p_np = (csr.crow_indices().numpy(), csr.col_indices().numpy(), csr.values().double().numpy())
+    return mh, gat_graph, (rowptr.numpy(), col.numpy()), p_np
+
+
+def _randomize(block, seed):
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name, p in block.named_parameters():
+            v = torch.randn(p.shape, generator=g) * 0.3
+            if name.endswith("norm.weight"):
+                v = 1.0 + v
+            p.copy_(v.to(p.device))
+
+
+def _close(actual, expected, name, rtol=1e-4, atol=1e-5):
+    a = actual.detach().double().cpu().numpy()
+    e = expected.detach().numpy()
+    scale = max(1.0, float(np.abs(e).max()) if e.size else 1.0)
+    assert_close(a, e, rtol=rtol, atol=atol * scale, name=name)
+
+
+MODES = [
+    # (score, interaction, weighting, gate, outer)
+    ("new", "new", "old", "node", "none"),
+    ("old", "old", "old", "node", "none"),
+    ("new", "new", "new", "node", "tanh"),
+    ("old", "old", "new", "global", "none"),
+    ("new", "new", "old", "none", "tanh"),
+]
+
+
+@pytest.mark.parametrize("score,interaction,weighting,gate,outer", MODES)
+def test_block_forward_backward_matches_oracle(score, interaction, weighting, gate, outer, monkeypatch):
+    from cign_amd.model_cign import GraphCliffordBlock
+    from oracle import block_oracle as B
+
+    print(f"block score={score} interaction={interaction} weighting={weighting} gate={gate} outer={outer}",
+          flush=True)
+    monkeypatch.setenv("CIGN_OUTER_NONLINEARITY", outer)
+    n, D, heads = 300, 32, 4
+    mh, gat_graph, (rp, cl), p_np = _setup(n, D)
+    block = GraphCliffordBlock(D, order_set=(1, 2, 3), gat_heads=heads, hop_gate_mode=gate, alpha_score_mode=score,
+                               interaction_mode=interaction, alpha_weighting_mode=weighting).cuda().eval()
+    _randomize(block, 1)
+    g = torch.Generator().manual_seed(2)
+    H0 = torch.randn(n, D, generator=g)
+    H = H0.cuda().requires_grad_()
+    out = block(H, None, mh, gat_graph)
+    params = {k: v.detach().double().cpu().requires_grad_() for k, v in block.named_parameters()}
+    H64 = H0.double().requires_grad_()
+    ref = B.block_forward(params, H64, rp, cl, p_np, (1, 2, 3), score_mode=0 if score == "old" else 1,
+                          interaction=0 if interaction == "old" else (2 if outer == "tanh" else 1),
+                          weighting=0 if weighting == "old" else 1, gate_mode=gate, heads=heads)
+    _close(out, ref, "out")
+    G = torch.randn(n, D, generator=g)
+    (out * G.cuda()).sum().backward()
+    (ref * G.double()).sum().backward()
+    _close(H.grad, H64.grad, "grad H")
+    for name, p in block.named_parameters():
+        assert p.grad is not None, name
+        _close(p.grad, params[name].grad, f"grad {name}")
+
+
+def test_block_selective_amp_bf16():
+    """use_selective_amp runs lin and proj under bf16 autocast (the GEMMs on
+    MFMA); everything else stays fp32. Compared to the fp64 oracle at 2e-2."""
+    from cign_amd.model_cign import GraphCliffordBlock
+    from oracle import block_oracle as B
+
+    n, D, heads = 300, 32, 4
+    mh, gat_graph, (rp, cl), p_np = _setup(n, D, seed=3)
+    block = GraphCliffordBlock(D, gat_heads=heads, use_selective_amp=True, alpha_score_mode="new",
+                               interaction_mode="new", alpha_weighting_mode="old").cuda().eval()
+    _randomize(block, 4)
+    H0 = torch.randn(n, D, generator=torch.Generator().manual_seed(5))
+    out = block(H0.cuda(), None, mh, gat_graph)
+    params = {k: v.detach().double().cpu() for k, v in block.named_parameters()}
+    ref = B.block_forward(params, H0.double(), rp, cl, p_np, (1, 2, 3), score_mode=1, interaction=1, weighting=0,
+                          gate_mode="node", heads=heads)
+    _close(out, ref, "out (bf16 GEMMs)", rtol=2e-2, atol=2e-2)
+
+
+def test_block_training_mode_runs_and_is_seeded():
+    """Training mode: dropout in the block ops and the GAT draws from the
+    reference's seed streams; two runs from the same torch seed agree
+    bit for bit."""
+    import cign_amd.collapsed_gat as CG
+    import cign_amd.fused_block_ops as FB
+    from cign_amd.model_cign import GraphCliffordBlock
+
+    n, D = 200, 32
+    mh, gat_graph, _, _ = _setup(n, D, seed=6)
+    block = GraphCliffordBlock(D, gat_heads=4).cuda().train()
+    H = torch.randn(n, D, device="cuda")
+    outs = []
+    for _ in range(2):
+        torch.manual_seed(77)
+        FB._CALL_COUNTER = __import__("itertools").count()
+        CG._CALL_COUNTER = __import__("itertools").count()
+        outs.append(block(H, None, mh, gat_graph))
+    assert torch.equal(outs[0], outs[1])
+    assert torch.isfinite(outs[0]).all()

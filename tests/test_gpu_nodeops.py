@@ -234,3 +234,28 @@ def test_block_ops_empty_rows_give_zero_parameter_grads():
     y, mean, rstd, mask = ext.dropout_layernorm_forward(x, w, w, 0.2, 1e-5, 1)
     dx, dw, db = ext.dropout_layernorm_backward(x, x, w, mean, rstd, mask, 0.2)
     assert dx.shape == (0, D) and torch.equal(dw, torch.zeros_like(dw)) and torch.equal(db, torch.zeros_like(db))
+
+
+# ---------------------------------------------------------------------------
+# hop gate
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("n,D,K,mode", [(1000, 256, 3, 1), (1000, 256, 3, 0), (300, 32, 5, 1), (77, 7, 16, 1),
+                                        (50, 300, 1, 0), (10, 4, 2, 1)])
+def test_hop_gate_matches_oracle(n, D, K, mode):
+    from cign_amd.hop_gate import HopGateFunction
+
+    print(f"hop gate n={n} D={D} K={K} mode={mode}", flush=True)
+    rng = np.random.default_rng(n + D + K)
+    H, C = rng.standard_normal((n, D)).astype(np.float32), rng.standard_normal((n, D)).astype(np.float32)
+    C[:, 0] = H[:, 0]  # ties of |H - C|: sign(0) = 0 in the gradient
+    W, b = (0.2 * rng.standard_normal((K, 2 * D))).astype(np.float32), rng.standard_normal(K).astype(np.float32)
+    g = rng.standard_normal((n, K)).astype(np.float32)
+    Ht, Ct, Wt, bt = (_t(a).requires_grad_() for a in (H, C, W, b))
+    a = HopGateFunction.apply(Ht, Ct, Wt, bt, mode)
+    assert_close(_n(a), O.hop_gate_forward(H, C, W, b, mode), name="alpha", **T32)
+    (a * _t(g)).sum().backward()
+    gH, gC, gW, gb = O.hop_gate_backward(g, H, C, W, b, mode)
+    assert_close(_n(Ht.grad), gH, name="grad H", **T32)
+    assert_close(_n(Ct.grad), gC, name="grad C", **T32)
+    assert_close(_n(Wt.grad), gW, name="grad weight", rtol=1e-4, atol=1e-4)
+    assert_close(_n(bt.grad), gb, name="grad bias", rtol=1e-4, atol=1e-4)

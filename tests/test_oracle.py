@@ -375,3 +375,73 @@ def test_block_ops_against_torch_layer_norm(rng):
     fd = ((O.gamma_residual_forward(h, g, gamma + eps2 * v, p, keep) -
            O.gamma_residual_forward(h, g, gamma - eps2 * v, p, keep)) * gy).sum() / (2 * eps2)
     assert abs(fd - (ggam * v).sum()) < 1e-6
+
+
+# ---------------------------------------------------------------------------
+# Hop gate
+# ---------------------------------------------------------------------------
+def test_hop_gate_oracle_against_torch_autograd_and_closed_forms():
+    """Pins hop_gate_forward/backward: torch fp64 autograd of the reference
+    expression (model_cign.py:731-749), rows summing to one, uniform alpha for
+    zero weights, and the old score reducing to the plain concatenation."""
+    import torch
+
+    rng = np.random.default_rng(7)
+    n, D, K = 40, 6, 3
+    H, C = rng.standard_normal((n, D)), rng.standard_normal((n, D))
+    C[0, 0] = H[0, 0]  # |H - C| at 0: gradient convention sign(0) = 0
+    W, b = rng.standard_normal((K, 2 * D)), rng.standard_normal(K)
+    g = rng.standard_normal((n, K))
+    for mode in (0, 1):
+        a = O.hop_gate_forward(H, C, W, b, mode)
+        assert np.allclose(a.sum(axis=1), 1.0)
+        Ht, Ct = torch.tensor(H, requires_grad=True), torch.tensor(C, requires_grad=True)
+        Wt, bt = torch.tensor(W, requires_grad=True), torch.tensor(b, requires_grad=True)
+        s = torch.cat([Ht, Ct], -1) if mode == 0 else torch.cat([Ht + Ct, torch.abs(Ht - Ct)], -1)
+        at = torch.softmax(torch.nn.functional.linear(s, Wt, bt), dim=-1)
+        (at * torch.tensor(g)).sum().backward()
+        assert np.allclose(a, at.detach().numpy(), rtol=1e-12, atol=1e-14)
+        gH, gC, gW, gb = O.hop_gate_backward(g, H, C, W, b, mode)
+        for mine, ref in ((gH, Ht.grad), (gC, Ct.grad), (gW, Wt.grad), (gb, bt.grad)):
+            assert np.allclose(mine, ref.numpy(), rtol=1e-10, atol=1e-12)
+    assert np.allclose(O.hop_gate_forward(H, C, np.zeros((K, 2 * D)), np.zeros(K), 1), 1.0 / K)
+    assert np.array_equal(O.hop_gate_score(H, C, 0), np.concatenate([H, C], 1))
+
+
+# ---------------------------------------------------------------------------
+# Block composition oracle (oracle/block_oracle.py)
+# ---------------------------------------------------------------------------
+def test_block_oracle_stages_match_numpy_oracle():
+    """The torch fp64 block restatement's GAT and pack stages equal the numpy
+    oracle's collapsed GAT and Clifford pack (every interaction x weighting,
+    with and without alpha), so the composition is pinned stage by stage."""
+    import torch
+    from oracle import block_oracle as B
+
+    rng = np.random.default_rng(11)
+    n, Hh, C = 60, 3, 5
+    ei = []
+    for i in range(n):
+        for j in rng.choice(n, size=int(rng.integers(0, 6)), replace=False):
+            ei.append((int(j), i))
+    ei = np.array(ei, dtype=np.int64).T
+    ge = O.gat_edge_index(ei, n)
+    r, c, _ = O.coalesce(ge[0], ge[1], n)
+    # rows = destinations: CSR of the flipped edge list
+    rowptr, col = O.csr_from_coo(c, r, n)[:2]
+    x = rng.standard_normal((n, Hh, C))
+    a_s, a_d, b = rng.standard_normal((n, Hh)), rng.standard_normal((n, Hh)), rng.standard_normal(C)
+    y = B._gat(torch.tensor(x), torch.tensor(a_s), torch.tensor(a_d), rowptr, col, 0.2, torch.tensor(b))
+    ref = O.collapsed_gat_forward(a_d, a_s, rowptr, col, 0.2, x, b)
+    assert np.allclose(y.numpy(), ref["out"], rtol=1e-12, atol=1e-12)
+    D, K = 4, 3
+    Hn, Cn = rng.standard_normal((n, D)), rng.standard_normal((n, D))
+    props = [rng.standard_normal((n, 2 * D)) for _ in range(K)]
+    alpha = rng.random((n, K))
+    for inter in (0, 1, 2):
+        for w in (0, 1):
+            for a in (alpha, None):
+                got = B._pack(torch.tensor(Hn), torch.tensor(Cn), [torch.tensor(p) for p in props],
+                              None if a is None else torch.tensor(a)[:, :, None], inter, w)
+                want = O.clifford_pack_forward(Hn, Cn, props, np.ones((n, K)) if a is None else a, inter, w)
+                assert np.allclose(got.numpy(), want, rtol=1e-12, atol=1e-12), (inter, w, a is None)
