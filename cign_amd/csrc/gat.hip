@@ -1,6 +1,6 @@
 // C-ABI of the collapsed GAT (kernels in gat_kernels.h, instantiated in the
 // gat_inst_*.hip translation units so they compile in parallel).
-#include "gat_kernels.h"
+#include "gat_fl.h"
 
 namespace cign {
 namespace gatk {
@@ -43,7 +43,7 @@ int dispatch_hc(int H, int C, Args&&... args) {
 }
 
 struct BwdLayout {
-  int64_t grad_pre, gscore, wsum, bias_part, bias_l2, part_row, part_col, total;
+  int64_t grad_pre, gscore, wsum, rowstat, bias_part, bias_l2, part_row, part_col, total;
 };
 
 inline int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
@@ -59,6 +59,7 @@ inline BwdLayout bwd_layout(int n, int nnz, int H, int C, int row_blocks, int n_
   L.grad_pre = off; off = align256(off + 4LL * n * C);
   L.gscore = off; off = align256(off + 4LL * nnz * H);
   L.wsum = off; off = align256(off + 4LL * n * H);
+  L.rowstat = off; off = align256(off + 16LL * n * H);
   L.bias_part = off; off = align256(off + 4LL * row_blocks * C);
   L.bias_l2 = off; off = align256(off + 4LL * n_l2 * C);
   L.part_row = off; off = align256(off + 4LL * n_seg_rows * 3 * H);
@@ -81,24 +82,25 @@ __global__ void zero_floats(float* p, int n) {
   if (i < n) p[i] = 0.0f;
 }
 
-// Feature-layout forward eligibility (shape only): H <= 8 heads, C a
-// multiple of the 16-byte chunk width, H*C <= 64 chunks.
-inline bool fl_forward_ok(int dtype, int H, int C) {
-  const int W = dtype == kBF16 ? 8 : 4;
-  return H <= kFlHeads && C % W == 0 && (H * C) / W <= kWave;
-}
-
-// Feature-layout backward: as the forward, plus C/W a power of two (the
-// per-edge dot products are reduced over a head's C/W lanes by a butterfly).
-inline bool fl_backward_ok(int dtype, int H, int C) {
+// Feature-layout eligibility (shape only): H <= 8 heads, C a multiple of the
+// 16-byte chunk width W with C/W a power of two (head sums and per-head dot
+// products are butterflies over lane bits), H*C <= 64 chunks.
+inline bool fl_ok(int dtype, int H, int C) {
   const int W = dtype == kBF16 ? 8 : 4;
   const int cq = C / W;
-  return fl_forward_ok(dtype, H, C) && (cq & (cq - 1)) == 0;
+  return H <= kFlHeads && C % W == 0 && (cq & (cq - 1)) == 0 && (H * C) / W <= kWave;
+}
+
+inline int fl_lgcq(int dtype, int C) {
+  const int W = dtype == kBF16 ? 8 : 4;
+  int lg = 0;
+  while ((1 << lg) < C / W) ++lg;
+  return lg;
 }
 
 // Schedule geometry (light_max, seg_edges) each GAT pass runs on.
 inline void gat_geometry(int pass, int dtype, int H, int C, int& light, int& seg) {
-  if ((pass == 0 && fl_forward_ok(dtype, H, C)) || (pass == 1 && fl_backward_ok(dtype, H, C))) {
+  if (fl_ok(dtype, H, C)) {
     light = 64;
     seg = 256;
   } else {
@@ -177,20 +179,21 @@ int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
     a.attn_row = attn_row; a.attn_col = attn_col; a.col = col;
     a.x = xt; a.bias = bias; a.out = ot; a.pre = pre; a.emax = edge_max; a.esum = edge_sum;
     a.mask = edge_mask; a.partial = static_cast<float*>(workspace); a.counters = row_counters;
-    if (fl_forward_ok(dtype, heads, channels)) {
-      if (!aligned16(xt) || !aligned16(ot))
-        return set_error(kInvalid, "cign_gat_fwd: in_feat and out must be 16-byte aligned");
+    if (fl_ok(dtype, heads, channels)) {
+      if (!aligned16(xt) || !aligned16(ot) || !aligned16(pre))
+        return set_error(kInvalid, "cign_gat_fwd: in_feat, out and pre must be 16-byte aligned");
+      const int lgcq = fl_lgcq(dtype, channels);
       const int W = dtype == kBF16 ? 8 : 4;
       int L = 1;
       while (L < heads * channels / W) L <<= 1;
       switch (L) {
-        case 1: return FwdFlLauncher<T, 1>::run(st, a, s, row_sched_info);
-        case 2: return FwdFlLauncher<T, 2>::run(st, a, s, row_sched_info);
-        case 4: return FwdFlLauncher<T, 4>::run(st, a, s, row_sched_info);
-        case 8: return FwdFlLauncher<T, 8>::run(st, a, s, row_sched_info);
-        case 16: return FwdFlLauncher<T, 16>::run(st, a, s, row_sched_info);
-        case 32: return FwdFlLauncher<T, 32>::run(st, a, s, row_sched_info);
-        default: return FwdFlLauncher<T, 64>::run(st, a, s, row_sched_info);
+        case 1: return FwdFlLauncher<T, 1>::run(st, a, s, row_sched_info, lgcq);
+        case 2: return FwdFlLauncher<T, 2>::run(st, a, s, row_sched_info, lgcq);
+        case 4: return FwdFlLauncher<T, 4>::run(st, a, s, row_sched_info, lgcq);
+        case 8: return FwdFlLauncher<T, 8>::run(st, a, s, row_sched_info, lgcq);
+        case 16: return FwdFlLauncher<T, 16>::run(st, a, s, row_sched_info, lgcq);
+        case 32: return FwdFlLauncher<T, 32>::run(st, a, s, row_sched_info, lgcq);
+        default: return FwdFlLauncher<T, 64>::run(st, a, s, row_sched_info, lgcq);
       }
     }
     return dispatch_hc<FwdLauncher, T>(heads, channels, st, a, s);
@@ -248,15 +251,17 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
     a.grad_pre = reinterpret_cast<float*>(ws + L.grad_pre);
     a.gscore = reinterpret_cast<float*>(ws + L.gscore);
     a.wsum = reinterpret_cast<float*>(ws + L.wsum);
+    a.rowstat = reinterpret_cast<float4*>(ws + L.rowstat);
     a.bias_part = reinterpret_cast<float*>(ws + L.bias_part);
     a.bias_l2 = reinterpret_cast<float*>(ws + L.bias_l2);
     a.part_row = reinterpret_cast<float*>(ws + L.part_row);
     a.part_col = reinterpret_cast<float*>(ws + L.part_col);
     a.row_counters = row_counters; a.col_counters = col_counters;
     a.grad_feat = gxt; a.grad_attn_row = grad_attn_row; a.grad_attn_col = grad_attn_col; a.grad_bias = grad_bias;
-    if (fl_backward_ok(dtype, heads, channels)) {
-      if (!aligned16(xt) || !aligned16(gyt) || !aligned16(gxt))
-        return set_error(kInvalid, "cign_gat_bwd: in_feat, grad_y and grad_feat must be 16-byte aligned");
+    if (fl_ok(dtype, heads, channels)) {
+      if (!aligned16(xt) || !aligned16(gyt) || !aligned16(gxt) || !aligned16(pre))
+        return set_error(kInvalid, "cign_gat_bwd: in_feat, pre, grad_y and grad_feat must be 16-byte aligned");
+      const int lgcq = fl_lgcq(dtype, channels);
       const int W = dtype == kBF16 ? 8 : 4;
       int Lq = 1;
       while (Lq < heads * channels / W) Lq <<= 1;
@@ -264,7 +269,7 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
         constexpr int LL = decltype(LC)::value;
         a.rows_blocks = BwdFlLauncher<T, LL>::row_blocks(rs, row_sched_info);
         a.n_l2 = (a.rows_blocks + 63) / 64;
-        return BwdFlLauncher<T, LL>::run(st, a, rs, row_sched_info, cs, col_sched_info);
+        return BwdFlLauncher<T, LL>::run(st, a, rs, row_sched_info, cs, col_sched_info, lgcq);
       };
       switch (Lq) {
         case 1: return go(std::integral_constant<int, 1>());

@@ -1,4 +1,4 @@
-// Explicit instantiation of the feature-layout collapsed-GAT forward for bf16.
-#include "gat_kernels.h"
+// Explicit instantiation of the feature-layout collapsed-GAT kernels for bf16.
+#include "gat_fl.h"
 
 CIGN_GAT_FL_INSTANTIATE(::cign::bf16)

@@ -1,4 +1,4 @@
-// Explicit instantiation of the feature-layout collapsed-GAT forward for float.
-#include "gat_kernels.h"
+// Explicit instantiation of the feature-layout collapsed-GAT kernels for float.
+#include "gat_fl.h"
 
 CIGN_GAT_FL_INSTANTIATE(float)

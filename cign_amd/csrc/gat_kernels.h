@@ -443,331 +443,6 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_kernel(GatFwdArgs<T> a, Sched 
   }
 }
 
-// ---------------------------------------------------------------------------
-// Forward, feature layout (the fast path for H <= 8, C a multiple of the
-// 16-byte chunk width W, H*C <= 64*W).
-//
-// Like the SpMM: a group of L = pow2ceil(H*C/W) lanes owns one destination
-// row and lane q owns chunk q of an x row (head q / (C/W)). Softmax
-// statistics are computed lane-per-edge (each lane reads col and the H source
-// logits of one edge), the edge weights go through LDS, and the aggregation
-// gathers one 16-byte chunk per lane per edge with the whole batch of edges
-// in flight. Rows with degree <= L go one per group (64/L rows per wave),
-// rows with degree <= 64 one per wave (its groups split the edges), heavier
-// rows are 256-edge segments (4 waves), merged like the pair-layout kernel.
-// Uses the SpMM schedule geometry (light_max 64, seg_edges 256).
-// ---------------------------------------------------------------------------
-constexpr int kFlHeads = 8;
-
-template <typename T>
-struct FlGeom {
-  static constexpr int W = 16 / sizeof(T);
-};
-
-// Softmax statistics over R lanes (an aligned power-of-two block) that each
-// hold at most one edge: per head max, then sum of exp.
-template <int R>
-__device__ __forceinline__ void fl_stats(const float (&sc)[kFlHeads], bool valid, int H, float (&M)[kFlHeads],
-                                         float (&E)[kFlHeads], float (&S)[kFlHeads]) {
-#pragma unroll
-  for (int h = 0; h < kFlHeads; ++h) {
-    float m = (valid && h < H) ? sc[h] : kNegBig;
-    for (int o = 1; o < R; o <<= 1) m = fmaxf(m, shfl_xor(m, o));
-    M[h] = m;
-    const float e = (valid && h < H) ? expf(sc[h] - m) : 0.0f;
-    E[h] = e;
-    float t = e;
-    for (int o = 1; o < R; o <<= 1) t += shfl_xor(t, o);
-    S[h] = t;
-  }
-}
-
-// Lane-per-edge prologue of one row: edge id, source id, scores.
-template <typename T>
-__device__ __forceinline__ void fl_edge(const GatFwdArgs<T>& a, int row, int e, bool valid, int& j,
-                                        float (&sc)[kFlHeads]) {
-  j = valid ? a.col[e] : 0;
-  const float* ad = a.attn_row + static_cast<int64_t>(row) * a.H;
-  const float* as = a.attn_col + static_cast<int64_t>(j) * a.H;
-#pragma unroll
-  for (int h = 0; h < kFlHeads; ++h) sc[h] = h < a.H ? leaky(ad[h] + as[h], a.slope) : kNegBig;
-}
-
-// Writes the lane's edge weights (H of them) to LDS, recording the mask.
-template <typename T>
-__device__ __forceinline__ void fl_weights(const GatFwdArgs<T>& a, int e, bool valid, const float (&E)[kFlHeads],
-                                           const float (&S)[kFlHeads], bool normalise, float* wl) {
-#pragma unroll
-  for (int h = 0; h < kFlHeads; ++h) {
-    float w = 0.0f;
-    if (valid && h < a.H) {
-      bool keep = true;
-      if (a.p > 0.0f) {
-        const int64_t idx = static_cast<int64_t>(e) * a.H + h;
-        keep = gat_keep(a.seed, static_cast<uint64_t>(idx), a.p);
-        a.mask[idx] = keep ? 1 : 0;
-      }
-      if (keep && (!normalise || S[h] > 0.0f)) {
-        w = normalise ? E[h] / S[h] : E[h];
-        if (a.p > 0.0f) w = w / (1.0f - a.p);
-      }
-    }
-    wl[h] = w;
-  }
-}
-
-// acc += sum over edge slots u = first, first + step, ... < cnt of
-// w[u][head] * x[j_u, chunk q]; j_u from lane base + u, weights from LDS.
-template <typename T, int U>
-__device__ __forceinline__ void fl_gather(const GatFwdArgs<T>& a, int jj, int base, int first, int step, int cnt,
-                                          int q, int hq, bool qv, const float* wl, float (&acc)[FlGeom<T>::W]) {
-  constexpr int W = FlGeom<T>::W;
-  const int F = a.H * a.C;
-  for (int u0 = first; __any(u0 < cnt); u0 += U * step) {
-    float buf[U][W];
-    float wv[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int u = u0 + k * step;
-      const bool ok = u < cnt;
-      const int src = base + (ok ? u : 0);
-      const int j = shfl(jj, src & (kWave - 1));
-      wv[k] = ok ? wl[(src & (kWave - 1)) * kFlHeads + hq] : 0.0f;
-      if (qv) {
-        Chunk<T, W>::load(a.x + static_cast<int64_t>(j) * F + q * W, buf[k]);
-      } else {
-#pragma unroll
-        for (int w = 0; w < W; ++w) buf[k][w] = 0.0f;
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < U; ++k)
-#pragma unroll
-      for (int w = 0; w < W; ++w) acc[w] = fmaf(wv[k], buf[k][w], acc[w]);
-  }
-}
-
-// Head mean + bias + SiLU of one row from per-chunk sums in LDS (xl holds the
-// row's nq chunks of W floats): lanes gl < C/W each emit W channels.
-template <typename T>
-__device__ __forceinline__ void fl_emit(const GatFwdArgs<T>& a, int row, int gl, const float* xl) {
-  constexpr int W = FlGeom<T>::W;
-  const int cq = a.C / W;
-  if (gl >= cq) return;
-  float o[W];
-  float pr[W];
-#pragma unroll
-  for (int w = 0; w < W; ++w) {
-    float t = 0.0f;
-    for (int h = 0; h < a.H; ++h) t += xl[(h * cq + gl) * W + w];
-    pr[w] = t / static_cast<float>(a.H) + a.bias[gl * W + w];
-    o[w] = silu(pr[w]);
-  }
-  const int64_t base = static_cast<int64_t>(row) * a.C + gl * W;
-#pragma unroll
-  for (int w = 0; w < W; ++w) a.pre[base + w] = pr[w];
-  Chunk<T, W>::store(a.out + base, o);
-}
-
-template <typename T, int L>
-__global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sched s, int n_mid, int mid_blocks) {
-  constexpr int W = FlGeom<T>::W;
-  constexpr int G = kWave / L;
-  constexpr int LGL = ilog2c(L);
-  __shared__ float wl[kWavesPerBlock][kWave * kFlHeads];
-  __shared__ float xl[kWavesPerBlock][kWave * W];
-  __shared__ float bm[kWavesPerBlock][kFlHeads], bs[kWavesPerBlock][kFlHeads];
-  __shared__ int flag;
-  const int lane = lane_id();
-  const int wave = wave_id();
-  const int g = lane >> LGL;
-  const int gl = lane & (L - 1);
-  const int F = a.H * a.C;
-  const int nq = F / W;
-  const int cq = a.C / W;
-  const bool qv = gl < nq;
-  const int q = qv ? gl : 0;
-  const int hq = q / cq;
-  float* wlw = wl[wave];
-  float* xlw = xl[wave];
-  int b = blockIdx.x;
-  float acc[W];
-#pragma unroll
-  for (int w = 0; w < W; ++w) acc[w] = 0.0f;
-
-  if (b >= s.n_seg) {
-    b -= s.n_seg;
-    if (b >= mid_blocks) {
-      // Tiny rows: one per lane group (degree <= L).
-      const int li = n_mid + ((b - mid_blocks) * kWavesPerBlock + wave) * G + g;
-      const bool has = li < s.n_light;
-      const int4 r = has ? s.light[li] : make_int4(0, 0, 0, 0);
-      const int deg = r.z - r.y;
-      const bool valid = gl < deg;
-      int jj;
-      float sc[kFlHeads], M[kFlHeads], E[kFlHeads], S[kFlHeads];
-      fl_edge(a, r.x, r.y + gl, valid, jj, sc);
-      fl_stats<L>(sc, valid, a.H, M, E, S);
-      fl_weights(a, r.y + gl, valid, E, S, true, wlw + lane * kFlHeads);
-      if (has && gl < a.H) {
-#pragma unroll
-        for (int h = 0; h < kFlHeads; ++h)
-          if (h == gl) {
-            a.emax[static_cast<int64_t>(r.x) * a.H + h] = M[h];
-            a.esum[static_cast<int64_t>(r.x) * a.H + h] = S[h];
-          }
-      }
-      wave_sync();
-      fl_gather<T, (L < 16 ? L : 16)>(a, jj, g * L, 0, 1, deg, q, hq, qv, wlw, acc);
-#pragma unroll
-      for (int w = 0; w < W; ++w) xlw[lane * W + w] = acc[w];
-      wave_sync();
-      if (has) fl_emit(a, r.x, gl, xlw + g * L * W);
-      return;
-    }
-    // Medium rows: one per wave (L < degree <= 64); group g takes edges g, g+G, ...
-    const int li = b * kWavesPerBlock + wave;
-    if (li >= n_mid) return;
-    const int4 r = s.light[li];
-    const int deg = r.z - r.y;
-    const bool valid = lane < deg;
-    int jj;
-    float sc[kFlHeads], M[kFlHeads], E[kFlHeads], S[kFlHeads];
-    fl_edge(a, r.x, r.y + lane, valid, jj, sc);
-    fl_stats<kWave>(sc, valid, a.H, M, E, S);
-    fl_weights(a, r.y + lane, valid, E, S, true, wlw + lane * kFlHeads);
-    if (lane < a.H) {
-#pragma unroll
-      for (int h = 0; h < kFlHeads; ++h)
-        if (h == lane) {
-          a.emax[static_cast<int64_t>(r.x) * a.H + h] = M[h];
-          a.esum[static_cast<int64_t>(r.x) * a.H + h] = S[h];
-        }
-    }
-    wave_sync();
-    fl_gather<T, 16>(a, jj, 0, g, G, deg, q, hq, qv, wlw, acc);
-#pragma unroll
-    for (int w = 0; w < W; ++w) acc[w] = sum_across(acc[w], L);
-#pragma unroll
-    for (int w = 0; w < W; ++w) xlw[lane * W + w] = acc[w];
-    wave_sync();
-    fl_emit(a, r.x, lane, xlw);
-    return;
-  }
-
-  // Heavy-row segment: 4 waves x 64 edge slots.
-  const int4 sg = s.seg[b];
-  const int row = sg.x;
-  const int2 hr = s.hrow[sg.w];
-  const bool single = hr.y == 1;
-  const int e = sg.y + wave * kWave + lane;
-  const bool valid = e < sg.z;
-  int jj;
-  float sc[kFlHeads], M[kFlHeads], E[kFlHeads], S[kFlHeads];
-  fl_edge(a, row, e, valid, jj, sc);
-  fl_stats<kWave>(sc, valid, a.H, M, E, S);
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < kFlHeads; ++h) {
-      bm[wave][h] = M[h];
-      bs[wave][h] = S[h];
-    }
-  }
-  __syncthreads();
-  float Mb[kFlHeads], Sb[kFlHeads];
-#pragma unroll
-  for (int h = 0; h < kFlHeads; ++h) {
-    Mb[h] = bm[0][h];
-    Sb[h] = bs[0][h];
-#pragma unroll
-    for (int w = 1; w < kWavesPerBlock; ++w) ms_merge(Mb[h], Sb[h], bm[w][h], bs[w][h]);
-    E[h] = (valid && h < a.H) ? expf(sc[h] - Mb[h]) : 0.0f;
-  }
-  fl_weights(a, e, valid, E, Sb, single, wlw + lane * kFlHeads);
-  wave_sync();
-  const int cnt = max(0, min(kWave, sg.z - (sg.y + wave * kWave)));
-  fl_gather<T, 16>(a, jj, 0, g, G, cnt, q, hq, qv, wlw, acc);
-#pragma unroll
-  for (int w = 0; w < W; ++w) acc[w] = sum_across(acc[w], L);
-  if (g == 0) {
-#pragma unroll
-    for (int w = 0; w < W; ++w) xlw[gl * W + w] = acc[w];
-  }
-  __syncthreads();
-  // Block sum of the four waves' chunk sums into xl[0].
-  for (int k = threadIdx.x; k < nq * W; k += kBlock) xl[0][k] = xl[0][k] + xl[1][k] + xl[2][k] + xl[3][k];
-  __syncthreads();
-  if (single) {
-    if (wave == 0) fl_emit(a, row, lane, xl[0]);
-    if (threadIdx.x < a.H) {
-      float mv = 0.0f, sv = 0.0f;
-#pragma unroll
-      for (int h = 0; h < kFlHeads; ++h)
-        if (h == static_cast<int>(threadIdx.x)) {
-          mv = Mb[h];
-          sv = Sb[h];
-        }
-      a.emax[static_cast<int64_t>(row) * a.H + threadIdx.x] = mv;
-      a.esum[static_cast<int64_t>(row) * a.H + threadIdx.x] = sv;
-    }
-    return;
-  }
-  const int stride = F + 2 * a.H;
-  float* mine = a.partial + static_cast<int64_t>(b) * stride;
-  for (int k = threadIdx.x; k < F; k += kBlock) mine[k] = xl[0][k];
-  if (threadIdx.x < a.H) {
-    float mv = 0.0f, sv = 0.0f;
-#pragma unroll
-    for (int h = 0; h < kFlHeads; ++h)
-      if (h == static_cast<int>(threadIdx.x)) {
-        mv = Mb[h];
-        sv = Sb[h];
-      }
-    mine[F + threadIdx.x] = mv;
-    mine[F + a.H + threadIdx.x] = sv;
-  }
-  if (!arrive_last(a.counters + sg.w, hr.y, &flag)) return;
-  // Merge segments: per head M = max m_q, S = sum s_q e^{m_q - M},
-  // acc = sum acc_q e^{m_q - M} / S; then head mean.
-  __shared__ float fm[kFlHeads], fs[kFlHeads];
-  if (threadIdx.x < a.H) {
-    float MM = kNegBig, SS = 0.0f;
-    for (int z = 0; z < hr.y; ++z) {
-      const float* pz = a.partial + static_cast<int64_t>(hr.x + z) * stride;
-      ms_merge(MM, SS, pz[F + threadIdx.x], pz[F + a.H + threadIdx.x]);
-    }
-    fm[threadIdx.x] = MM;
-    fs[threadIdx.x] = SS;
-    a.emax[static_cast<int64_t>(row) * a.H + threadIdx.x] = MM;
-    a.esum[static_cast<int64_t>(row) * a.H + threadIdx.x] = SS;
-  }
-  __syncthreads();
-  for (int k = threadIdx.x; k < F; k += kBlock) {
-    const int h = k / a.C;
-    float t = 0.0f;
-    for (int z = 0; z < hr.y; ++z) {
-      const float* pz = a.partial + static_cast<int64_t>(hr.x + z) * stride;
-      t += pz[k] * expf(pz[F + h] - fm[h]);
-    }
-    xl[0][k] = fs[h] > 0.0f ? t / fs[h] : 0.0f;
-  }
-  __syncthreads();
-  if (wave == 0) fl_emit(a, row, lane, xl[0]);
-}
-
-template <typename T, int L>
-struct FwdFlLauncher {
-  static int run(hipStream_t st, const GatFwdArgs<T>& a, const Sched& s, const int32_t* hdr) {
-    constexpr int G = kWave / L;
-    const int n_mid = G > 1 ? sched_count_gt(hdr, L) : s.n_light;
-    const int mid_blocks = (n_mid + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int n_tiny = s.n_light - n_mid;
-    const int blocks = s.n_seg + mid_blocks + (n_tiny + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
-    if (blocks > 0)
-      hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid, mid_blocks);
-    return check_launch("cign_gat_fwd (feature layout)");
-  }
-};
 
 // ---------------------------------------------------------------------------
 // Backward
@@ -793,6 +468,7 @@ struct GatBwdArgs {
   float* grad_pre;   // [n, C]
   float* gscore;     // [nnz, H]: ge' = keep/(1-p) * <g_pre, x>/H
   float* wsum;       // [n, H]: sum_e s ge'
+  float4* rowstat;   // [n, H]: {attn_row, edge_max, 1/edge_sum, wsum} (feature layout)
   float* bias_part;  // [rows_blocks, C]
   float* bias_l2;    // [n_l2, C]
   float* part_row;   // [n_seg_rows, 3H]
@@ -1181,488 +857,6 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_kernel(GatBwdArgs<T> a, S
   }
 }
 
-// ---------------------------------------------------------------------------
-// Backward, feature layout (fast path: H <= 8, C a multiple of W with C/W a
-// power of two, H*C <= 64*W; SpMM schedule geometry for both CSR and CSC).
-//
-// Rows (CSR): a lane-per-edge prologue computes s, LeakyReLU' and keep of
-// its edge for every head and publishes them through LDS; then, like the
-// forward, lane q owns x chunk q (head q / (C/W)) and for each edge of the
-// batch computes a partial <g_pre, x[j,h,:]>, reduced over the C/W lanes of
-// its head with a butterfly, giving ge' on every lane of that head; (wsum, A)
-// accumulate per head along the edges, B = sum s l' comes from the prologue.
-// Columns (CSC): the lane-per-entry prologue computes w and g_raw of its
-// entry for every head (weights to LDS, g_raw summed into grad_attn_col),
-// then lane q gathers grad_pre chunks of the destination rows: grad_feat[j]
-// chunk q = sum w[u][head] grad_pre[i_u, chunk] / H.
-// ---------------------------------------------------------------------------
-// Lane-per-edge prologue of a CSR row: per head s * keep / (1-p) stored in
-// LDS (wlane[h]), LeakyReLU' in lpl[h]; returns B_h contributions in B.
-template <typename T>
-__device__ __forceinline__ void flb_row_prologue(const GatBwdArgs<T>& a, int row, int e, bool valid, float* wlane,
-                                                 float* lplane, float (&B)[kFlHeads]) {
-  const int j = valid ? a.col[e] : 0;
-  const float* ad = a.attn_row + static_cast<int64_t>(row) * a.H;
-  const float* as = a.attn_col + static_cast<int64_t>(j) * a.H;
-  const float* em = a.emax + static_cast<int64_t>(row) * a.H;
-  const float* es = a.esum + static_cast<int64_t>(row) * a.H;
-#pragma unroll
-  for (int h = 0; h < kFlHeads; ++h) {
-    float soft = 0.0f, lp = 0.0f;
-    if (valid && h < a.H) {
-      const float raw = ad[h] + as[h];
-      const float S = es[h];
-      soft = S > 0.0f ? expf(leaky(raw, a.slope) - em[h]) / S : 0.0f;
-      lp = raw < 0.0f ? a.slope : 1.0f;
-    }
-    wlane[h] = soft;
-    lplane[h] = lp;
-    B[h] = soft * lp;
-  }
-}
-
-// Feature-layout pass over edge slots u = first, first+step, ... < cnt of one
-// row: returns the lane's (wsum, A) for its head hq and stores ge'.
-template <typename T, int U>
-__device__ __forceinline__ void flb_row_edges(const GatBwdArgs<T>& a, int eb, int jj_lane_base, int jj, int first,
-                                              int step, int cnt, int q, int hq, int cw, bool qv, int cq,
-                                              const float (&gpv)[FlGeom<T>::W], const float* softl, const float* lpl,
-                                              float& wsum, float& A) {
-  constexpr int W = FlGeom<T>::W;
-  const int F = a.H * a.C;
-  wsum = A = 0.0f;
-  for (int u0 = first; __any(u0 < cnt); u0 += U * step) {
-    float buf[U][W];
-    int uu[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int u = u0 + k * step;
-      uu[k] = u;
-      const int src = jj_lane_base + (u < cnt ? u : 0);
-      const int j = shfl(jj, src & (kWave - 1));
-      if (qv) {
-        Chunk<T, W>::load(a.x + static_cast<int64_t>(j) * F + q * W, buf[k]);
-      } else {
-#pragma unroll
-        for (int w = 0; w < W; ++w) buf[k][w] = 0.0f;
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      float d = 0.0f;
-#pragma unroll
-      for (int w = 0; w < W; ++w) d = fmaf(gpv[w], buf[k][w], d);
-      for (int o = 1; o < cq; o <<= 1) d += shfl_xor(d, o);
-      const int u = uu[k];
-      const bool ok = u < cnt && qv;
-      const int slot = (jj_lane_base + (u < cnt ? u : 0)) & (kWave - 1);
-      float ge = d * a.inv_h;
-      if (a.p > 0.0f) {
-        const bool keep = ok ? a.mask[static_cast<int64_t>(eb + u) * a.H + hq] != 0 : false;
-        ge = (keep ? ge : 0.0f) / (1.0f - a.p);
-      }
-      if (ok) {
-        const float soft = softl[slot * kFlHeads + hq];
-        const float sg = soft * ge;
-        wsum += sg;
-        A += sg * lpl[slot * kFlHeads + hq];
-        if (cw == 0) a.gscore[static_cast<int64_t>(eb + u) * a.H + hq] = ge;
-      }
-    }
-  }
-}
-
-// g_pre chunk cw of a row (W channels), optionally published to grad_pre.
-template <typename T>
-__device__ __forceinline__ void flb_grad_pre(const GatBwdArgs<T>& a, int row, int cw, bool publish,
-                                             float (&gpv)[FlGeom<T>::W]) {
-  constexpr int W = FlGeom<T>::W;
-  const int64_t base = static_cast<int64_t>(row) * a.C + cw * W;
-  float gy[W];
-  Chunk<T, W>::load(a.grad_y + base, gy);
-#pragma unroll
-  for (int w = 0; w < W; ++w) gpv[w] = gy[w] * silu_grad(a.pre[base + w]);
-  if (publish)
-#pragma unroll
-    for (int w = 0; w < W; ++w) a.grad_pre[base + w] = gpv[w];
-}
-
-template <typename T, int L>
-__global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a, Sched s, int n_mid, int mid_blocks) {
-  constexpr int W = FlGeom<T>::W;
-  constexpr int G = kWave / L;
-  constexpr int LGL = ilog2c(L);
-  __shared__ float softl[kWavesPerBlock][kWave * kFlHeads];
-  __shared__ float lpl[kWavesPerBlock][kWave * kFlHeads];
-  __shared__ float red[kWavesPerBlock][3][kFlHeads];
-  __shared__ int flag;
-  const int lane = lane_id();
-  const int wave = wave_id();
-  const int g = lane >> LGL;
-  const int gl = lane & (L - 1);
-  const int cq = a.C / W;
-  const int nq = a.H * cq;
-  const bool qv = gl < nq;
-  const int q = qv ? gl : 0;
-  const int hq = q / cq;
-  const int cw = q % cq;
-  float* sw = softl[wave];
-  float* lw = lpl[wave];
-  int b = blockIdx.x;
-  float wsum = 0.0f, A = 0.0f, B[kFlHeads];
-  float gpv[W];
-
-  if (b >= s.n_seg) {
-    b -= s.n_seg;
-    const bool tiny = b >= mid_blocks;
-    int4 r = make_int4(0, 0, 0, 0);
-    bool has;
-    int slot_base, first, step, R;
-    if (tiny) {
-      const int li = n_mid + ((b - mid_blocks) * kWavesPerBlock + wave) * G + g;
-      has = li < s.n_light;
-      if (has) r = s.light[li];
-      slot_base = g * L;
-      first = 0;
-      step = 1;
-      R = L;
-    } else {
-      const int li = b * kWavesPerBlock + wave;
-      has = li < n_mid;
-      if (has) r = s.light[li];
-      slot_base = 0;
-      first = g;
-      step = G;
-      R = kWave;
-    }
-    const int deg = r.z - r.y;
-    const int slot = tiny ? gl : lane;
-    const bool valid = slot < deg;
-    flb_row_prologue(a, r.x, r.y + slot, valid, sw + lane * kFlHeads, lw + lane * kFlHeads, B);
-    const int jj = valid ? a.col[r.y + slot] : 0;
-    // B over the row's lanes.
-#pragma unroll
-    for (int h = 0; h < kFlHeads; ++h)
-      for (int o = 1; o < R; o <<= 1) B[h] += shfl_xor(B[h], o);
-    const bool emit_lane = tiny || g == 0;  // lanes holding the row's chunk sums
-    const bool own_chunk = has && emit_lane && hq == 0 && qv;  // one lane per g_pre chunk of the row
-    flb_grad_pre(a, r.x, cw, own_chunk, gpv);
-    wave_sync();
-    flb_row_edges<T, 16>(a, r.y, slot_base, jj, first, step, deg, q, hq, cw, qv, cq, gpv, sw, lw, wsum, A);
-    if (!tiny) {
-      wsum = sum_across(wsum, L);
-      A = sum_across(A, L);
-    }
-    if (has && emit_lane && qv && cw == 0) {
-      float Bh = 0.0f;
-#pragma unroll
-      for (int h = 0; h < kFlHeads; ++h)
-        if (h == hq) Bh = B[h];
-      const int64_t rh = static_cast<int64_t>(r.x) * a.H + hq;
-      a.wsum[rh] = wsum;
-      a.grad_attn_row[rh] = A - wsum * Bh;
-    }
-    // Bias partial: the wave's g_pre rows summed over its groups (lane q of
-    // group 0 ends up with chunk q), then over the 4 waves through LDS
-    // (reusing the softmax staging area once every wave is done with it).
-    float gb[W];
-#pragma unroll
-    for (int w = 0; w < W; ++w) gb[w] = sum_across(own_chunk ? gpv[w] : 0.0f, L);
-    __syncthreads();
-    if (lane < cq)
-#pragma unroll
-      for (int w = 0; w < W; ++w) sw[lane * W + w] = gb[w];
-    __syncthreads();
-    for (int c = threadIdx.x; c < a.C; c += kBlock)
-      a.bias_part[static_cast<int64_t>(blockIdx.x) * a.C + c] = softl[0][c] + softl[1][c] + softl[2][c] + softl[3][c];
-    return;
-  }
-
-  // Heavy-row segment: 4 waves x 64 edge slots.
-  const int4 sg = s.seg[b];
-  const int row = sg.x;
-  const int2 hr = s.hrow[sg.w];
-  const bool first_seg = (b == hr.x);
-  const int e = sg.y + wave * kWave + lane;
-  const bool valid = e < sg.z;
-  flb_row_prologue(a, row, e, valid, sw + lane * kFlHeads, lw + lane * kFlHeads, B);
-  const int jj = valid ? a.col[e] : 0;
-#pragma unroll
-  for (int h = 0; h < kFlHeads; ++h) B[h] = sum_across(B[h], 1);
-  flb_grad_pre(a, row, cw, first_seg && wave == 0 && g == 0 && hq == 0 && qv, gpv);
-  wave_sync();
-  const int cnt = max(0, min(kWave, sg.z - (sg.y + wave * kWave)));
-  flb_row_edges<T, 16>(a, sg.y + wave * kWave, 0, jj, g, G, cnt, q, hq, cw, qv, cq, gpv, sw, lw, wsum, A);
-  wsum = sum_across(wsum, L);
-  A = sum_across(A, L);
-  if (lane < nq && cw == 0) {
-    red[wave][0][hq] = wsum;
-    red[wave][1][hq] = A;
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < kFlHeads; ++h) red[wave][2][h] = B[h];
-  }
-  __syncthreads();
-  for (int c = threadIdx.x; c < a.C; c += kBlock) {
-    float t = 0.0f;
-    if (first_seg) {
-      // g_pre of the row (bias partial of the first segment only).
-      const int64_t idx = static_cast<int64_t>(row) * a.C + c;
-      t = to_f32(a.grad_y[idx]) * silu_grad(a.pre[idx]);
-    }
-    a.bias_part[static_cast<int64_t>(blockIdx.x) * a.C + c] = t;
-  }
-  if (threadIdx.x < 3 * kFlHeads) {
-    const int k = threadIdx.x / kFlHeads, hh = threadIdx.x % kFlHeads;
-    red[0][k][hh] = red[0][k][hh] + red[1][k][hh] + red[2][k][hh] + red[3][k][hh];
-  }
-  __syncthreads();
-  if (hr.y == 1) {
-    if (threadIdx.x < a.H) {
-      const float w = red[0][0][threadIdx.x];
-      a.wsum[static_cast<int64_t>(row) * a.H + threadIdx.x] = w;
-      a.grad_attn_row[static_cast<int64_t>(row) * a.H + threadIdx.x] = red[0][1][threadIdx.x] - w * red[0][2][threadIdx.x];
-    }
-    return;
-  }
-  float* mine = a.part_row + static_cast<int64_t>(b) * 3 * a.H;
-  if (threadIdx.x < 3 * a.H) mine[threadIdx.x] = red[0][threadIdx.x / a.H][threadIdx.x % a.H];
-  if (!arrive_last(a.row_counters + sg.w, hr.y, &flag)) return;
-  if (threadIdx.x < a.H) {
-    float w = 0.0f, AA = 0.0f, BB = 0.0f;
-    for (int z = 0; z < hr.y; ++z) {
-      const float* pz = a.part_row + static_cast<int64_t>(hr.x + z) * 3 * a.H;
-      w += pz[threadIdx.x];
-      AA += pz[a.H + threadIdx.x];
-      BB += pz[2 * a.H + threadIdx.x];
-    }
-    a.wsum[static_cast<int64_t>(row) * a.H + threadIdx.x] = w;
-    a.grad_attn_row[static_cast<int64_t>(row) * a.H + threadIdx.x] = AA - w * BB;
-  }
-}
-
-// Lane-per-entry prologue of a CSC column j: weights w[h] to LDS, returns
-// the per-head g_raw of the entry in graw, and the destination row.
-template <typename T>
-__device__ __forceinline__ int flb_col_prologue(const GatBwdArgs<T>& a, int j, int t, bool valid, float* wlane,
-                                                float (&graw)[kFlHeads]) {
-  const int i = valid ? a.rowind[t] : 0;
-  const int e = valid ? a.perm[t] : 0;
-  const float* ad = a.attn_row + static_cast<int64_t>(i) * a.H;
-  const float* as = a.attn_col + static_cast<int64_t>(j) * a.H;
-  const float* em = a.emax + static_cast<int64_t>(i) * a.H;
-  const float* es = a.esum + static_cast<int64_t>(i) * a.H;
-  const float* ws = a.wsum + static_cast<int64_t>(i) * a.H;
-  const float* gs = a.gscore + static_cast<int64_t>(e) * a.H;
-#pragma unroll
-  for (int h = 0; h < kFlHeads; ++h) {
-    float w = 0.0f, g = 0.0f;
-    if (valid && h < a.H) {
-      const float raw = ad[h] + as[h];
-      const float S = es[h];
-      const float soft = S > 0.0f ? expf(leaky(raw, a.slope) - em[h]) / S : 0.0f;
-      bool keep = true;
-      if (a.p > 0.0f) keep = a.mask[static_cast<int64_t>(e) * a.H + h] != 0;
-      if (keep) {
-        w = soft;
-        if (a.p > 0.0f) w = w / (1.0f - a.p);
-      }
-      g = soft * (gs[h] - ws[h]);
-      if (raw < 0.0f) g *= a.slope;
-    }
-    wlane[h] = w;
-    graw[h] = g;
-  }
-  return i;
-}
-
-// acc += sum over entry slots u of w[u][head] * grad_pre[i_u, chunk cw].
-template <typename T, int U>
-__device__ __forceinline__ void flb_col_gather(const GatBwdArgs<T>& a, int ii, int base, int first, int step, int cnt,
-                                               int hq, int cw, bool qv, const float* wl, float (&acc)[FlGeom<T>::W]) {
-  constexpr int W = FlGeom<T>::W;
-  for (int u0 = first; __any(u0 < cnt); u0 += U * step) {
-    float buf[U][W];
-    float wv[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int u = u0 + k * step;
-      const bool ok = u < cnt;
-      const int src = (base + (ok ? u : 0)) & (kWave - 1);
-      const int i = shfl(ii, src);
-      wv[k] = ok ? wl[src * kFlHeads + hq] : 0.0f;
-      if (qv) {
-        Chunk<float, 4>::load(a.grad_pre + static_cast<int64_t>(i) * a.C + cw * W, *reinterpret_cast<float(*)[4]>(buf[k]));
-        if constexpr (W == 8)
-          Chunk<float, 4>::load(a.grad_pre + static_cast<int64_t>(i) * a.C + cw * W + 4,
-                                *reinterpret_cast<float(*)[4]>(buf[k] + 4));
-      } else {
-#pragma unroll
-        for (int w = 0; w < W; ++w) buf[k][w] = 0.0f;
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < U; ++k)
-#pragma unroll
-      for (int w = 0; w < W; ++w) acc[w] = fmaf(wv[k], buf[k][w], acc[w]);
-  }
-}
-
-template <typename T, int L>
-__global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a, Sched s, int n_mid, int mid_blocks) {
-  constexpr int W = FlGeom<T>::W;
-  constexpr int G = kWave / L;
-  constexpr int LGL = ilog2c(L);
-  __shared__ float wl[kWavesPerBlock][kWave * kFlHeads];
-  __shared__ float red[kWavesPerBlock][kWave * W];
-  __shared__ float gred[kWavesPerBlock][kFlHeads];
-  __shared__ int flag;
-  const int lane = lane_id();
-  const int wave = wave_id();
-  const int g = lane >> LGL;
-  const int gl = lane & (L - 1);
-  const int cq = a.C / W;
-  const int nq = a.H * cq;
-  const bool qv = gl < nq;
-  const int q = qv ? gl : 0;
-  const int hq = q / cq;
-  const int cw = q % cq;
-  const int F = a.H * a.C;
-  float* wlw = wl[wave];
-  int b = blockIdx.x;
-  const int nsched = s.n_seg + mid_blocks + (s.n_light - n_mid + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
-  if (b >= nsched) {
-    bias_reduce(a, b - nsched, a.col_counters + s.n_hrow, &flag);
-    return;
-  }
-  float acc[W];
-#pragma unroll
-  for (int w = 0; w < W; ++w) acc[w] = 0.0f;
-  float graw[kFlHeads];
-
-  if (b >= s.n_seg) {
-    b -= s.n_seg;
-    const bool tiny = b >= mid_blocks;
-    int4 r = make_int4(0, 0, 0, 0);
-    bool has;
-    if (tiny) {
-      const int li = n_mid + ((b - mid_blocks) * kWavesPerBlock + wave) * G + g;
-      has = li < s.n_light;
-      if (has) r = s.light[li];
-    } else {
-      const int li = b * kWavesPerBlock + wave;
-      has = li < n_mid;
-      if (has) r = s.light[li];
-    }
-    if (!tiny && !has) return;
-    const int deg = r.z - r.y;
-    const int slot = tiny ? gl : lane;
-    const bool valid = slot < deg;
-    const int ii = flb_col_prologue(a, r.x, r.y + slot, valid, wlw + lane * kFlHeads, graw);
-    const int R = tiny ? L : kWave;
-#pragma unroll
-    for (int h = 0; h < kFlHeads; ++h)
-      for (int o = 1; o < R; o <<= 1) graw[h] += shfl_xor(graw[h], o);
-    wave_sync();
-    if (tiny) flb_col_gather<T, 16>(a, ii, g * L, 0, 1, deg, hq, cw, qv, wlw, acc);
-    else flb_col_gather<T, 16>(a, ii, 0, g, G, deg, hq, cw, qv, wlw, acc);
-    if (!tiny)
-#pragma unroll
-      for (int w = 0; w < W; ++w) acc[w] = sum_across(acc[w], L);
-    const bool emit = has && (tiny || g == 0);
-    if (emit && qv) {
-      float o[W];
-#pragma unroll
-      for (int w = 0; w < W; ++w) o[w] = acc[w] * a.inv_h;
-      Chunk<T, W>::store(a.grad_feat + static_cast<int64_t>(r.x) * F + q * W, o);
-    }
-    if (emit && gl < a.H) {
-      float v = 0.0f;
-#pragma unroll
-      for (int h = 0; h < kFlHeads; ++h)
-        if (h == gl) v = graw[h];
-      a.grad_attn_col[static_cast<int64_t>(r.x) * a.H + gl] = v;
-    }
-    return;
-  }
-
-  // Heavy column segment: 4 waves x 64 entry slots.
-  const int4 sg = s.seg[b];
-  const int j = sg.x;
-  const int2 hr = s.hrow[sg.w];
-  const bool single = hr.y == 1;
-  const int t = sg.y + wave * kWave + lane;
-  const bool valid = t < sg.z;
-  const int ii = flb_col_prologue(a, j, t, valid, wlw + lane * kFlHeads, graw);
-#pragma unroll
-  for (int h = 0; h < kFlHeads; ++h) graw[h] = sum_across(graw[h], 1);
-  wave_sync();
-  const int cnt = max(0, min(kWave, sg.z - (sg.y + wave * kWave)));
-  flb_col_gather<T, 16>(a, ii, 0, g, G, cnt, hq, cw, qv, wlw, acc);
-#pragma unroll
-  for (int w = 0; w < W; ++w) acc[w] = sum_across(acc[w], L);
-  if (g == 0)
-#pragma unroll
-    for (int w = 0; w < W; ++w) red[wave][gl * W + w] = acc[w];
-  if (lane == 0)
-#pragma unroll
-    for (int h = 0; h < kFlHeads; ++h) gred[wave][h] = graw[h];
-  __syncthreads();
-  const int HC = F;
-  float* mine = a.part_col + static_cast<int64_t>(b) * (HC + a.H);
-  for (int k = threadIdx.x; k < nq * W; k += kBlock) {
-    const float v = red[0][k] + red[1][k] + red[2][k] + red[3][k];
-    if (single) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<T>(v * a.inv_h);
-    else mine[k] = v;
-  }
-  if (threadIdx.x < a.H) {
-    const int hh = threadIdx.x;
-    const float v = gred[0][hh] + gred[1][hh] + gred[2][hh] + gred[3][hh];
-    if (single) a.grad_attn_col[static_cast<int64_t>(j) * a.H + hh] = v;
-    else mine[HC + hh] = v;
-  }
-  if (single) return;
-  if (!arrive_last(a.col_counters + sg.w, hr.y, &flag)) return;
-  const int stride = HC + a.H;
-  for (int k = threadIdx.x; k < HC + a.H; k += kBlock) {
-    float v = 0.0f;
-    for (int z = 0; z < hr.y; ++z) v += a.part_col[static_cast<int64_t>(hr.x + z) * stride + k];
-    if (k < HC) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<T>(v * a.inv_h);
-    else a.grad_attn_col[static_cast<int64_t>(j) * a.H + (k - HC)] = v;
-  }
-}
-
-template <typename T, int L>
-struct BwdFlLauncher {
-  static int run(hipStream_t st, const GatBwdArgs<T>& a, const Sched& rs, const int32_t* rhdr, const Sched& cs,
-                 const int32_t* chdr) {
-    constexpr int G = kWave / L;
-    const int r_mid = G > 1 ? sched_count_gt(rhdr, L) : rs.n_light;
-    const int r_mid_blocks = (r_mid + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int rb = rs.n_seg + r_mid_blocks + (rs.n_light - r_mid + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
-    if (rb > 0) {
-      hipLaunchKernelGGL((gat_bwd_rows_fl_kernel<T, L>), dim3(rb), dim3(kBlock), 0, st, a, rs, r_mid, r_mid_blocks);
-      const int rc = check_launch("cign_gat_bwd (rows, feature layout)");
-      if (rc) return rc;
-    }
-    const int c_mid = G > 1 ? sched_count_gt(chdr, L) : cs.n_light;
-    const int c_mid_blocks = (c_mid + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int cb = cs.n_seg + c_mid_blocks + (cs.n_light - c_mid + kWavesPerBlock * G - 1) / (kWavesPerBlock * G) +
-                   a.n_l2;
-    if (cb > 0)
-      hipLaunchKernelGGL((gat_bwd_cols_fl_kernel<T, L>), dim3(cb), dim3(kBlock), 0, st, a, cs, c_mid, c_mid_blocks);
-    return check_launch("cign_gat_bwd (cols, feature layout)");
-  }
-
-  // Workgroups of the row kernel (the number of grad_bias partials).
-  static int row_blocks(const Sched& rs, const int32_t* rhdr) {
-    constexpr int G = kWave / L;
-    const int r_mid = G > 1 ? sched_count_gt(rhdr, L) : rs.n_light;
-    return rs.n_seg + (r_mid + kWavesPerBlock - 1) / kWavesPerBlock +
-           (rs.n_light - r_mid + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
-  }
-};
 
 // ---------------------------------------------------------------------------
 // Launchers (explicitly instantiated in gat_inst_*.hip).
@@ -1699,38 +893,6 @@ struct BwdLauncher {
   template struct ::cign::gatk::BwdLauncher<T, HP, 8>;     \
   template struct ::cign::gatk::BwdLauncher<T, HP, 16>;    \
   template struct ::cign::gatk::BwdLauncher<T, HP, 32>;
-
-#define CIGN_GAT_FL_INSTANTIATE(T)                       \
-  template struct ::cign::gatk::BwdFlLauncher<T, 1>;     \
-  template struct ::cign::gatk::BwdFlLauncher<T, 2>;     \
-  template struct ::cign::gatk::BwdFlLauncher<T, 4>;     \
-  template struct ::cign::gatk::BwdFlLauncher<T, 8>;     \
-  template struct ::cign::gatk::BwdFlLauncher<T, 16>;    \
-  template struct ::cign::gatk::BwdFlLauncher<T, 32>;    \
-  template struct ::cign::gatk::BwdFlLauncher<T, 64>;    \
-  template struct ::cign::gatk::FwdFlLauncher<T, 1>;     \
-  template struct ::cign::gatk::FwdFlLauncher<T, 2>;     \
-  template struct ::cign::gatk::FwdFlLauncher<T, 4>;     \
-  template struct ::cign::gatk::FwdFlLauncher<T, 8>;     \
-  template struct ::cign::gatk::FwdFlLauncher<T, 16>;    \
-  template struct ::cign::gatk::FwdFlLauncher<T, 32>;    \
-  template struct ::cign::gatk::FwdFlLauncher<T, 64>;
-
-#define CIGN_GAT_FL_DECLARE(T)                                  \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 1>;     \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 2>;     \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 4>;     \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 8>;     \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 16>;    \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 32>;    \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 64>;    \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 1>;     \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 2>;     \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 4>;     \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 8>;     \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 16>;    \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 32>;    \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 64>;
 
 #define CIGN_GAT_DECLARE(T, HP)                                   \
   extern template struct ::cign::gatk::FwdLauncher<T, HP, 8>;     \

@@ -56,6 +56,9 @@ CASES = [
     (3, 8, 0.1, torch.float32, 300, {1: 2000}),
     (1, 256, 0.0, torch.float32, 200, {0: 600}),
     (5, 32, 0.0, torch.bfloat16, 300, {2: 520}),
+    (1, 4, 0.1, torch.float32, 300, {2: 400}),
+    (4, 4, 0.0, torch.float32, 300, {1: 700}),
+    (2, 8, 0.2, torch.bfloat16, 300, {1: 500}),
 ]
 
 
