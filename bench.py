@@ -7,12 +7,16 @@ inputs resident in HBM:
     cign_gat_fwd then cign_gat_bwd (2 kernels);
   * 3-hop CSR SpMM pipeline (c3: D=64, fp32) on the normalized adjacency of
     the same graph: cign_spmm_fwd3 then cign_spmm_bwd3 (3 + 3 kernels).
-value = E * K / t (edges/s over the timed K steps). The roofline object is
-computed for the dominant kernel from HIP events recorded on the launch
-stream inside the timed region; the CPU baseline times the numpy oracle on
-the host (a bounded sample of the same workload).
+value = E * K / t (edges/s over the timed K steps; each step is one replay
+of the step captured as a HIP graph, or with --eager the four drop-in API
+calls). The roofline object is computed for the dominant kernel from HIP
+events recorded on the launch stream in a second timed region, where each
+phase is launched back to back (captured as one graph of 20 launches and
+replayed), which is the per-kernel average rocprofv3 reports. The CPU
+baseline times the numpy oracle on the host (a bounded sample of the same
+workload).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--eager] [--dtype f32|bf16]
 """
 from __future__ import annotations
 
@@ -36,6 +40,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 disables)")
     ap.add_argument("--dtype", choices=["f32", "bf16"], default="f32")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every step through the Python drop-in API instead of replaying it as a HIP graph")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="before warmup, run 3 plain 256 MiB elementwise copies (x * 1 -> y, fp32) whose "
                          "FETCH_SIZE / WRITE_SIZE counters calibrate the per-kernel traffic figures")
@@ -216,22 +222,19 @@ def main():
 
     ev = lambda: torch.cuda.Event(enable_timing=True)
     phases = ("gat_fwd", "spmm_fwd3", "gat_bwd", "spmm_bwd3")
+    fwd_out = {}
 
-    def step(marks=None):
-        if marks is not None:
-            marks[0].record()
-        out, pre, emax, esum, mask = ext.forward(ar, ac, rowptr, col, 0.2, x, bias, 0.0, 0)
-        if marks is not None:
-            marks[1].record()
-        plan.forward3(X)
-        if marks is not None:
-            marks[2].record()
-        ext.backward(0.2, 0.0, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar, ac, pre, gy)
-        if marks is not None:
-            marks[3].record()
-        plan.backward3(g1, g2, g3)
-        if marks is not None:
-            marks[4].record()
+    def run_phase(p):
+        if p == "gat_fwd":
+            fwd_out["gat"] = ext.forward(ar, ac, rowptr, col, 0.2, x, bias, 0.0, 0)
+        elif p == "spmm_fwd3":
+            fwd_out["mh"] = plan.forward3(X)
+        elif p == "gat_bwd":
+            out, pre, emax, esum, mask = fwd_out["gat"]
+            fwd_out["gat_bwd"] = ext.backward(0.2, 0.0, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar,
+                                              ac, pre, gy)
+        else:
+            fwd_out["mh_bwd"] = plan.backward3(g1, g2, g3)
 
     if args.calibrate_copy:
         src = torch.ones(64 << 20, dtype=torch.float32, device=dev)  # 256 MiB
@@ -241,24 +244,75 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    for _ in range(args.warmup):
-        step()
+    # Eager warmup: builds the row schedules (one host copy of each row
+    # pointer) and the workspaces, and gives the reference outputs.
+    for _ in range(max(1, args.warmup)):
+        for p in phases:
+            run_phase(p)
     torch.cuda.synchronize()
+    eager = {k: [t.clone() for t in v] for k, v in fwd_out.items()}
 
-    # Timed region: K steps, synchronised on both sides. Phase events are
-    # recorded on the launch stream (torch's current stream, the stream every
-    # cign_* call is given).
-    marks = [[ev() for _ in range(5)] for _ in range(args.steps)]
+    def capture(fn):
+        """HIP graph of fn() (allocations settle in a side-stream run first)."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        return g
+
+    def whole_step():
+        for p in phases:
+            run_phase(p)
+
+    if args.eager:
+        launch_step = whole_step
+    else:
+        # The step as one HIP graph: its host work is one launch, and every
+        # replay recomputes every kernel of the four phases.
+        launch_step = capture(whole_step).replay
+        for _ in range(max(1, args.warmup)):
+            launch_step()
+        torch.cuda.synchronize()
+        # Replays reproduce the eager results bit for bit (the GAT forward's
+        # edge_mask, output 4, is only written when attn_drop > 0).
+        for k, v in fwd_out.items():
+            for i, (a_, b_) in enumerate(zip(v, eager[k])):
+                if not (k == "gat" and i == 4) and not torch.equal(a_, b_):
+                    raise SystemExit(f"graph replay of {k}[{i}] differs from the eager result")
+
+    # Timed region: K steps, synchronised on both sides.
+    start, stop = ev(), ev()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for k in range(args.steps):
-        step(marks[k])
+    start.record()
+    for _ in range(args.steps):
+        launch_step()
+    stop.record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    phase_ms = {p: 0.0 for p in phases}
-    for m in marks:
-        for i, p in enumerate(phases):
-            phase_ms[p] += m[i].elapsed_time(m[i + 1]) / args.steps
+    gpu_step_ms = start.elapsed_time(stop) / args.steps
+
+    # Per-phase kernel durations: each phase launched R times back to back
+    # (one HIP graph) and timed with HIP events on the launch stream.
+    R, M = 20, max(2, args.steps // 10)
+    phase_ms = {}
+    for p in phases:
+        gp = capture(lambda p=p: [run_phase(p) for _ in range(R)])
+        gp.replay()
+        a0, a1 = ev(), ev()
+        torch.cuda.synchronize()
+        a0.record()
+        for _ in range(M):
+            gp.replay()
+        a1.record()
+        torch.cuda.synchronize()
+        phase_ms[p] = a0.elapsed_time(a1) / (M * R)
+        del gp
 
     s = 2 if dt == torch.bfloat16 else 4
     B = workloads.algorithmic_bytes(n, E, H, C, D, s_gat=s, s_mh=s)
@@ -294,12 +348,14 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
+        "gpu_ms_per_step": round(gpu_step_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": args.dtype,
         "data": "synthetic: seeded Chung-Lu power-law graph (gamma 2.5), N(0,1) features and gradient probes",
         "config": {"workload": "c2+c3 layer: collapsed GAT H=4 x C=16 + 3-hop CSR SpMM D=64, forward+backward",
+                   "launch": "eager" if args.eager else "hip_graph_per_step",
                    "nodes": n, "edges_nnz": E, "heads": H, "channels": C, "dense_cols": D, "hops": 3,
                    "max_in_degree": int(torch.diff(rowptr.long()).max())},
         "layer_GB_s": round(layer_gbs, 1),

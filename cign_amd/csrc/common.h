@@ -61,6 +61,13 @@ struct Chunk;
 
 template <>
 struct Chunk<float, 4> {
+  // The 16 raw bytes (kept in flight by gather batches, unpacked on use).
+  using Raw = float4;
+  static __device__ __forceinline__ Raw load_raw(const float* p) { return *reinterpret_cast<const float4*>(p); }
+  static __device__ __forceinline__ Raw zero_raw() { return make_float4(0.0f, 0.0f, 0.0f, 0.0f); }
+  static __device__ __forceinline__ void unpack(const Raw& q, float (&v)[4]) {
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  }
   static __device__ __forceinline__ void load(const float* p, float (&v)[4]) {
     const float4 q = *reinterpret_cast<const float4*>(p);
     v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
@@ -72,6 +79,17 @@ struct Chunk<float, 4> {
 
 template <>
 struct Chunk<bf16, 8> {
+  using Raw = uint4;
+  static __device__ __forceinline__ Raw load_raw(const bf16* p) { return *reinterpret_cast<const uint4*>(p); }
+  static __device__ __forceinline__ Raw zero_raw() { return make_uint4(0u, 0u, 0u, 0u); }
+  static __device__ __forceinline__ void unpack(const Raw& q, float (&v)[8]) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
   static __device__ __forceinline__ void load(const bf16* p, float (&v)[8]) {
     const uint4 q = *reinterpret_cast<const uint4*>(p);
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
@@ -95,6 +113,10 @@ struct Chunk<bf16, 8> {
 
 template <typename T>
 struct Chunk<T, 1> {
+  using Raw = T;
+  static __device__ __forceinline__ Raw load_raw(const T* p) { return *p; }
+  static __device__ __forceinline__ Raw zero_raw() { return from_f32<T>(0.0f); }
+  static __device__ __forceinline__ void unpack(const Raw& q, float (&v)[1]) { v[0] = to_f32(q); }
   static __device__ __forceinline__ void load(const T* p, float (&v)[1]) { v[0] = to_f32(*p); }
   static __device__ __forceinline__ void store(T* p, const float (&v)[1]) { *p = from_f32<T>(v[0]); }
 };
@@ -108,6 +130,28 @@ __device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
 __device__ __forceinline__ float shfl(float v, int src) { return __shfl(v, src, kWave); }
 __device__ __forceinline__ int shfl(int v, int src) { return __shfl(v, src, kWave); }
+
+__device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, kWave); }
+
+// Edge-batch driver of the gather kernels: runs fn.template run<U>(k0) for
+// k0 = 0, U, 2U, ... < need, with U the smallest power of two >= need, capped
+// at UMAX. `need` must be wave-uniform: a batch issues all of its U gathers
+// before consuming any, so U is the number of loads a lane keeps in flight.
+template <int UMAX, typename Fn>
+__device__ __forceinline__ void for_batches(int need, Fn& fn) {
+  if (need <= 0) return;
+  if (need <= 1) {
+    fn.template run<1>(0);
+  } else if (need <= 2 || UMAX == 2) {
+    for (int k0 = 0; k0 < need; k0 += 2) fn.template run<2>(k0);
+  } else if (need <= 4 || UMAX == 4) {
+    for (int k0 = 0; k0 < need; k0 += 4) fn.template run<4>(k0);
+  } else if (need <= 8 || UMAX == 8) {
+    for (int k0 = 0; k0 < need; k0 += 8) fn.template run<8>(k0);
+  } else {
+    for (int k0 = 0; k0 < need; k0 += 16) fn.template run<16>(k0);
+  }
+}
 
 // Sum over lanes whose ids differ only in bits >= `from` (all lanes sharing
 // lane % from); every such lane receives the total.

@@ -63,26 +63,6 @@ struct FlGeom {
   static constexpr int W = 16 / sizeof(T);
 };
 
-__device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, kWave); }
-
-// Runs fn.template run<U>(k0) for k0 = 0, U, 2U, ... < need, with U the
-// smallest power of two >= need, capped at UMAX (need is wave-uniform).
-template <int UMAX, typename Fn>
-__device__ __forceinline__ void for_batches(int need, Fn& fn) {
-  if (need <= 0) return;
-  if (need <= 1) {
-    fn.template run<1>(0);
-  } else if (need <= 2 || UMAX == 2) {
-    for (int k0 = 0; k0 < need; k0 += 2) fn.template run<2>(k0);
-  } else if (need <= 4 || UMAX == 4) {
-    for (int k0 = 0; k0 < need; k0 += 4) fn.template run<4>(k0);
-  } else if (need <= 8 || UMAX == 8) {
-    for (int k0 = 0; k0 < need; k0 += 8) fn.template run<8>(k0);
-  } else {
-    for (int k0 = 0; k0 < need; k0 += 16) fn.template run<16>(k0);
-  }
-}
-
 // Lane geometry of a group of L lanes (one row).
 template <int L>
 struct FlLane {
@@ -186,14 +166,14 @@ struct FwdBatches {
   template <int U>
   __device__ __forceinline__ void run(int k0) {
     const int F = a.H * a.C;
-    float xb[U][W];
+    typename Chunk<T, W>::Raw xb[U];
     float sc[U];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
       const int j = shfl(jj, (base + (u < cnt ? u : 0)) & (kWave - 1));
       sc[k] = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq];
-      Chunk<T, W>::load(a.x + static_cast<int64_t>(j) * F + ln.q * W, xb[k]);
+      xb[k] = Chunk<T, W>::load_raw(a.x + static_cast<int64_t>(j) * F + ln.q * W);
     }
     float mx = st.m;
 #pragma unroll
@@ -222,8 +202,10 @@ struct FwdBatches {
         }
         wk = keep ? pk / (1.0f - a.p) : 0.0f;
       }
+      float xv[W];
+      Chunk<T, W>::unpack(xb[k], xv);
 #pragma unroll
-      for (int w = 0; w < W; ++w) st.acc[w] = fmaf(wk, xb[k][w], st.acc[w]);
+      for (int w = 0; w < W; ++w) st.acc[w] = fmaf(wk, xv[w], st.acc[w]);
     }
   }
 };
@@ -445,7 +427,7 @@ struct RowBatches {
   template <int U>
   __device__ __forceinline__ void run(int k0) {
     const int F = a.H * a.C;
-    float xb[U][W];
+    typename Chunk<T, W>::Raw xb[U];
     float ab[U];
     float kw[U];
 #pragma unroll
@@ -453,7 +435,7 @@ struct RowBatches {
       const int u = first + (k0 + k) * step;
       const int j = shfl(jj, (base + (u < cnt ? u : 0)) & (kWave - 1));
       ab[k] = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq];
-      Chunk<T, W>::load(a.x + static_cast<int64_t>(j) * F + ln.q * W, xb[k]);
+      xb[k] = Chunk<T, W>::load_raw(a.x + static_cast<int64_t>(j) * F + ln.q * W);
       if constexpr (DROP) kw[k] = (u < cnt && a.mask[static_cast<int64_t>(ebase + u) * a.H + ln.hq]) ? 1.0f : 0.0f;
     }
 #pragma unroll
@@ -466,10 +448,12 @@ struct RowBatches {
       if constexpr (DROP) sk = kw[k] != 0.0f ? sm / (1.0f - a.p) : 0.0f;
       const float skl = sk * lp;
       st.B = fmaf(sm, lp, st.B);
+      float xv[W];
+      Chunk<T, W>::unpack(xb[k], xv);
 #pragma unroll
       for (int w = 0; w < W; ++w) {
-        st.vs[w] = fmaf(sk, xb[k][w], st.vs[w]);
-        st.vsl[w] = fmaf(skl, xb[k][w], st.vsl[w]);
+        st.vs[w] = fmaf(sk, xv[w], st.vs[w]);
+        st.vsl[w] = fmaf(skl, xv[w], st.vsl[w]);
       }
     }
   }

@@ -58,50 +58,67 @@ __device__ __forceinline__ void zero(float (&acc)[VPL][W]) {
     for (int w = 0; w < W; ++w) acc[v][w] = 0.0f;
 }
 
-// acc += v * x[j, lane's chunks]
+// Raw chunks of x[j] owned by lane gl (zero past the tile).
 template <typename T, int W, int VPL>
-__device__ __forceinline__ void load_row(const SpmmArgs<T, W, VPL>& a, int j, int gl, float (&buf)[VPL][W]) {
+__device__ __forceinline__ void load_row(const SpmmArgs<T, W, VPL>& a, int j, int gl,
+                                         typename Chunk<T, W>::Raw (&buf)[VPL]) {
   const T* base = a.x + static_cast<int64_t>(j) * a.ld + a.c0;
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int c = gl + (v << a.lgL);
-    if (c < a.nch) {
-      Chunk<T, W>::load(base + c * W, buf[v]);
-    } else {
-#pragma unroll
-      for (int w = 0; w < W; ++w) buf[v][w] = 0.0f;
-    }
+    buf[v] = c < a.nch ? Chunk<T, W>::load_raw(base + c * W) : Chunk<T, W>::zero_raw();
   }
 }
 
-// Wave-cooperative tile: edges [eb, ee) (at most 64), group g takes edges
-// g, g + G, ...; U batched gathers per step.
-template <typename T, int W, int VPL, int U>
-__device__ __forceinline__ void gather_tile(const SpmmArgs<T, W, VPL>& a, int eb, int ee, float (&acc)[VPL][W]) {
-  const int lane = lane_id();
-  const int G = kWave >> a.lgL;
-  const int g = lane >> a.lgL;
-  const int gl = lane & (a.L - 1);
-  const int cnt = ee - eb;
-  const bool mine = lane < cnt;
-  const int jj = a.col[mine ? eb + lane : eb];
-  const float vv = mine ? a.val[eb + lane] : 0.0f;
-  for (int k = 0; k < cnt; k += G * U) {
-    float buf[U][VPL][W];
+// Batches of U edge slots of a lane group: slot u = first + (k0 + k) * step,
+// valid while u < cnt, whose column index and weight lane (base + u) holds in
+// jj / vv. Every gather of a batch is issued before any is consumed; slots
+// past the end reload an edge of the group with weight 0.
+template <typename T, int W, int VPL>
+struct SpmmBatches {
+  const SpmmArgs<T, W, VPL>& a;
+  int jj;
+  float vv;
+  int base, first, step, cnt, gl;
+  float (&acc)[VPL][W];
+
+  template <int U>
+  __device__ __forceinline__ void run(int k0) {
+    typename Chunk<T, W>::Raw buf[U][VPL];
     float wv[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int src = (k + u * G + g) & (kWave - 1);
-      wv[u] = shfl(vv, src);
-      load_row(a, shfl(jj, src), gl, buf[u]);
+    for (int k = 0; k < U; ++k) {
+      const int u = first + (k0 + k) * step;
+      const int src = (base + (u < cnt ? u : 0)) & (kWave - 1);
+      const float v = shfl(vv, src);
+      wv[k] = u < cnt ? v : 0.0f;
+      load_row(a, shfl(jj, src), gl, buf[k]);
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int k = 0; k < U; ++k)
 #pragma unroll
-      for (int v = 0; v < VPL; ++v)
+      for (int v = 0; v < VPL; ++v) {
+        float f[W];
+        Chunk<T, W>::unpack(buf[k][v], f);
 #pragma unroll
-        for (int w = 0; w < W; ++w) acc[v][w] = fmaf(wv[u], buf[u][v][w], acc[v][w]);
+        for (int w = 0; w < W; ++w) acc[v][w] = fmaf(wv[k], f[w], acc[v][w]);
+      }
   }
+};
+
+// Largest of v over the lane groups of a wavefront (runtime group size L).
+__device__ __forceinline__ int wave_max_over_groups(int v, int L) {
+  for (int o = L; o < kWave; o <<= 1) v = max(v, shfl_xor_i(v, o));
+  return v;
+}
+
+// Gathers `need` (wave-uniform) slots per lane group, at most 16 chunks in
+// flight per lane.
+template <typename T, int W, int VPL>
+__device__ __forceinline__ void gather(const SpmmArgs<T, W, VPL>& a, int jj, float vv, int base, int first, int step,
+                                       int cnt, int need, int gl, float (&acc)[VPL][W]) {
+  SpmmBatches<T, W, VPL> sb{a, jj, vv, base, first, step, cnt, gl, acc};
+  for_batches<16 / VPL>(need, sb);
 }
 
 template <typename T, int W, int VPL>
@@ -125,11 +142,13 @@ __device__ __forceinline__ void write_row(const SpmmArgs<T, W, VPL>& a, int row,
   }
 }
 
-template <typename T, int W, int VPL, int U>
+template <typename T, int W, int VPL>
 __global__ __launch_bounds__(kBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a, Sched s) {
   const int lane = lane_id();
   const int wave = wave_id();
   const int gl = lane & (a.L - 1);
+  const int G = kWave >> a.lgL;
+  const int g = lane >> a.lgL;
   int b = blockIdx.x;
   float acc[VPL][W];
   zero<T, W, VPL>(acc);
@@ -137,11 +156,16 @@ __global__ __launch_bounds__(kBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a, Sch
   if (b >= s.n_seg) {
     b -= s.n_seg;
     if (b < a.mid_blocks) {
-      // Medium row: one per wavefront.
+      // Medium row (L < degree <= 64): one per wavefront, group g takes edges
+      // g, g + G, ...
       const int li = b * kWavesPerBlock + wave;
       if (li >= a.n_mid) return;
       const int4 r = s.light[li];
-      for (int t = r.y; t < r.z; t += kTile) gather_tile<T, W, VPL, U>(a, t, min(r.z, t + kTile), acc);
+      const int deg = r.z - r.y;
+      const bool mine = lane < deg;
+      const int jj = mine ? a.col[r.y + lane] : 0;
+      const float vv = mine ? a.val[r.y + lane] : 0.0f;
+      gather(a, jj, vv, 0, g, G, deg, (deg + G - 1) / G, gl, acc);
 #pragma unroll
       for (int v = 0; v < VPL; ++v)
 #pragma unroll
@@ -149,9 +173,7 @@ __global__ __launch_bounds__(kBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a, Sch
       if (lane < a.L) write_row(a, r.x, gl, acc);
       return;
     }
-    // Tiny rows: one per lane group (degree <= L).
-    const int G = kWave >> a.lgL;
-    const int g = lane >> a.lgL;
+    // Tiny rows (degree <= L): one per lane group.
     const int li = a.n_mid + ((b - a.mid_blocks) * kWavesPerBlock + wave) * G + g;
     const bool has = li < s.n_light;
     const int4 r = has ? s.light[li] : make_int4(0, 0, 0, 0);
@@ -159,35 +181,23 @@ __global__ __launch_bounds__(kBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a, Sch
     const bool mine = gl < deg;
     const int jj = mine ? a.col[r.y + gl] : 0;
     const float vv = mine ? a.val[r.y + gl] : 0.0f;
-    for (int k = 0; k < a.L; k += U) {
-      // Wave-uniform: stop once no group of this wave has edges left.
-      if (!__any(k < deg)) break;
-      float buf[U][VPL][W];
-      float wv[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int src = (g << a.lgL) + ((k + u) & (a.L - 1));
-        wv[u] = shfl(vv, src);
-        load_row(a, shfl(jj, src), gl, buf[u]);
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int v = 0; v < VPL; ++v)
-#pragma unroll
-          for (int w = 0; w < W; ++w) acc[v][w] = fmaf(wv[u], buf[u][v][w], acc[v][w]);
-    }
+    gather(a, jj, vv, g << a.lgL, 0, 1, deg, wave_max_over_groups(deg, a.L), gl, acc);
     if (has) write_row(a, r.x, gl, acc);
     return;
   }
 
-  // Heavy-row segment: one 64-edge tile per wave, reduced through LDS.
+  // Heavy-row segment: wave w takes the segment's edges [64w, 64w + 64),
+  // reduced through LDS.
   __shared__ float red[kWavesPerBlock][VPL * W * kWave];
   __shared__ int flag;
   const int4 sg = s.seg[b];
   const int row = sg.x;
-  for (int t = sg.y + wave * kTile; t < sg.z; t += kSegEdges)
-    gather_tile<T, W, VPL, U>(a, t, min(sg.z, t + kTile), acc);
+  const int tb = sg.y + wave * kTile;
+  const int cnt = max(0, min(kTile, sg.z - tb));
+  const bool mine = lane < cnt;
+  const int jj = mine ? a.col[tb + lane] : 0;
+  const float vv = mine ? a.val[tb + lane] : 0.0f;
+  gather(a, jj, vv, 0, g, G, cnt, (cnt + G - 1) / G, gl, acc);
 #pragma unroll
   for (int v = 0; v < VPL; ++v)
 #pragma unroll
@@ -213,8 +223,8 @@ __global__ __launch_bounds__(kBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a, Sch
     }
     return;
   }
-  float* mine = a.partial + static_cast<int64_t>(b) * width;
-  for (int c = threadIdx.x; c < width; c += kBlock) mine[c] = red[0][c] + red[1][c] + red[2][c] + red[3][c];
+  float* part = a.partial + static_cast<int64_t>(b) * width;
+  for (int c = threadIdx.x; c < width; c += kBlock) part[c] = red[0][c] + red[1][c] + red[2][c] + red[3][c];
   if (!arrive_last(a.counters + sg.w, hr.y, &flag)) return;
   for (int c = threadIdx.x; c < width; c += kBlock) {
     float t = 0.0f;
@@ -266,17 +276,7 @@ int launch_tile(hipStream_t stream, const Sched& s, const SchedInfo& info, int l
   const int tiny_blocks = (n_tiny + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
   const int blocks = s.n_seg + a.mid_blocks + tiny_blocks;
   if (blocks == 0) return kOk;
-  // Unroll U steps so a 64-edge tile (or a tiny row) needs one dependent
-  // gather round (G * U <= 64), keeping at most 16 chunks in flight per lane.
-  const int cap = 16 / VPL;
-  const int U = min(cap, kWave / G);
-  switch (U) {
-    case 16: hipLaunchKernelGGL((spmm_kernel<T, W, VPL, 16>), dim3(blocks), dim3(kBlock), 0, stream, a, s); break;
-    case 8: hipLaunchKernelGGL((spmm_kernel<T, W, VPL, 8>), dim3(blocks), dim3(kBlock), 0, stream, a, s); break;
-    case 4: hipLaunchKernelGGL((spmm_kernel<T, W, VPL, 4>), dim3(blocks), dim3(kBlock), 0, stream, a, s); break;
-    case 2: hipLaunchKernelGGL((spmm_kernel<T, W, VPL, 2>), dim3(blocks), dim3(kBlock), 0, stream, a, s); break;
-    default: hipLaunchKernelGGL((spmm_kernel<T, W, VPL, 1>), dim3(blocks), dim3(kBlock), 0, stream, a, s); break;
-  }
+  hipLaunchKernelGGL((spmm_kernel<T, W, VPL>), dim3(blocks), dim3(kBlock), 0, stream, a, s);
   return check_launch("cign_spmm");
 }
 
