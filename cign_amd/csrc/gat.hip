@@ -101,8 +101,8 @@ inline int fl_lgcq(int dtype, int C) {
 // Schedule geometry (light_max, seg_edges) each GAT pass runs on.
 inline void gat_geometry(int pass, int dtype, int H, int C, int& light, int& seg) {
   if (fl_ok(dtype, H, C)) {
-    light = 64;
-    seg = 256;
+    light = kFlLightMax;
+    seg = kFlSegEdges;
   } else {
     light = kGatLight;
     seg = kGatSeg;

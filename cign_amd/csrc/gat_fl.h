@@ -4,12 +4,13 @@
 // of gat_kernels.h (reference collapsed_gat_cuda.cu:34-430).
 //
 // Geometry (shared with the SpMM, schedule.h built with light_max = 64,
-// seg_edges = 256). A group of L = pow2ceil(H*C/W) lanes owns one row; lane q
+// seg_edges = 512). A group of L = pow2ceil(H*C/W) lanes owns one row; lane q
 // owns chunk q of a feature row, i.e. head hq = q / (C/W) and channel chunk
 // cw = q % (C/W). Rows with degree <= L go one per group (64/L rows per
 // wavefront), rows with degree <= 64 one per wavefront (its groups split the
-// edges), heavier rows are 256-edge segments (one 4-wave workgroup each) whose
-// partial results the last workgroup to finish merges in segment order.
+// edges), heavier rows are 512-edge segments (one 4-wave workgroup each, two
+// rounds of 256 edges) whose partial results the last workgroup to finish
+// merges in segment order.
 //
 // Every lane gathers, for each edge of its batch, the 16-byte chunk of the
 // source feature row AND the source logit of its own head in the same memory
@@ -57,6 +58,15 @@ constexpr int kFlHeads = 8;
 constexpr int kFwdU = CIGN_FL_FWD_U;
 constexpr int kRowsU = CIGN_FL_ROWS_U;
 constexpr int kColsU = CIGN_FL_COLS_U;
+
+// Heavy rows are segments of at most kFlSegEdges edges (one workgroup each),
+// processed in rounds of kSegRound = 4 waves x 64 edges. Longer segments mean
+// fewer rows whose partial results need a cross-workgroup merge (an
+// agent-scope release / acquire, which writes back and invalidates the L2 of
+// the XCDs involved) at the cost of more rounds per workgroup.
+constexpr int kFlLightMax = 64;
+constexpr int kFlSegEdges = 512;
+constexpr int kSegRound = kWavesPerBlock * kWave;
 
 template <typename T>
 struct FlGeom {
@@ -307,18 +317,20 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
     return;
   }
 
-  // Heavy-row segment: wave w takes the segment's edges [64w, 64w + 64).
+  // Heavy-row segment: wave w takes edges [64w, 64w + 64) of every 256-edge
+  // round of the segment.
   __shared__ float hm[kWavesPerBlock][kWave], hs[kWavesPerBlock][kWave];
   __shared__ float hacc[kWavesPerBlock][kWave * W];
   __shared__ int flag;
   const int4 sg = s.seg[b];
   const int row = sg.x;
   const int2 hr = s.hrow[sg.w];
-  const int tb = sg.y + wave * kWave;
-  const int cnt = max(0, min(kWave, sg.z - tb));
-  const int jj = ln.lane < cnt ? a.col[tb + ln.lane] : 0;
   const float ar = a.attn_row[static_cast<int64_t>(row) * a.H + ln.hq];
-  fwd_edges<T, L, DROP>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, ar, st);
+  for (int tb = sg.y + wave * kWave; tb < sg.z; tb += kSegRound) {
+    const int cnt = min(kWave, sg.z - tb);
+    const int jj = ln.lane < cnt ? a.col[tb + ln.lane] : 0;
+    fwd_edges<T, L, DROP>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, ar, st);
+  }
   fwd_merge_groups<L, W>(st);
   if (ln.g == 0) {
     hm[wave][ln.gl] = st.m;
@@ -567,12 +579,13 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a
     const int4 sg = s.seg[b];
     row = sg.x;
     const int2 hr = s.hrow[sg.w];
-    const int tb = sg.y + wave * kWave;
-    const int cnt = max(0, min(kWave, sg.z - tb));
-    const int jj = ln.lane < cnt ? a.col[tb + ln.lane] : 0;
     rh = row_head(a, row, ln.hq);
     grad_pre_chunk(a, row, ln.cw, gp);
-    rows_edges<T, L, DROP>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, rh, st);
+    for (int tb = sg.y + wave * kWave; tb < sg.z; tb += kSegRound) {
+      const int cnt = min(kWave, sg.z - tb);
+      const int jj = ln.lane < cnt ? a.col[tb + ln.lane] : 0;
+      rows_edges<T, L, DROP>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, rh, st);
+    }
     group_sum<L, W>(st.vs);
     group_sum<L, W>(st.vsl);
     st.B = group_sum1<L>(st.B);
@@ -778,19 +791,21 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
     return;
   }
 
-  // Heavy column segment: wave w takes entries [64w, 64w + 64).
+  // Heavy column segment: wave w takes entries [64w, 64w + 64) of every
+  // 256-entry round of the segment.
   const int4 sg = s.seg[b];
   const int j = sg.x;
   const int2 hr = s.hrow[sg.w];
-  const int tb = sg.y + wave * kWave;
-  const int cnt = max(0, min(kWave, sg.z - tb));
-  const bool own = ln.lane < cnt;
-  const int ii = own ? a.rowind[tb + ln.lane] : 0;
-  const int ee = (DROP && own) ? a.perm[tb + ln.lane] : 0;
   const float ac = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq];
   float xj[W];
   Chunk<T, W>::load(a.x + static_cast<int64_t>(j) * F + ln.q * W, xj);
-  cols_edges<T, L, DROP>(a, ln, ii, ee, 0, ln.g, G, cnt, (cnt + G - 1) / G, ac, st);
+  for (int tb = sg.y + wave * kWave; tb < sg.z; tb += kSegRound) {
+    const int cnt = min(kWave, sg.z - tb);
+    const bool own = ln.lane < cnt;
+    const int ii = own ? a.rowind[tb + ln.lane] : 0;
+    const int ee = (DROP && own) ? a.perm[tb + ln.lane] : 0;
+    cols_edges<T, L, DROP>(a, ln, ii, ee, 0, ln.g, G, cnt, (cnt + G - 1) / G, ac, st);
+  }
   group_sum<L, W>(st.ug);
   group_sum<L, W>(st.ua);
   st.t = group_sum1<L>(st.t);

@@ -14,15 +14,17 @@
 // the tile's chunks, 16-byte loads, lane l owns chunks l, l + L, ...). Three
 // work shapes, from the degree-sorted schedule (schedule.h):
 //   tiny rows   (degree <= L):  one row per lane group, G = 64 / L rows per
-//                               wavefront; all of a row's gathers issue at
-//                               once (one col/val load, U = L unrolled loads);
+//                               wavefront; one col/val load, then the row's
+//                               gathers in one batch;
 //   medium rows (<= 64 edges):  one row per wavefront, its G groups split the
 //                               edges, reduced with a butterfly;
-//   heavy rows:                 256-edge segments, one workgroup each (one
-//                               64-edge tile per wave); multi-segment rows
-//                               merge through `partial` in segment order.
-// Every load inside a batch is unconditional (indices clamped to a valid
-// edge, weight zero) so the compiler issues the whole batch before waiting.
+//   heavy rows:                 segments (512 edges by the host default), one
+//                               workgroup each, in rounds of 64 edges per
+//                               wave; multi-segment rows merge through
+//                               `partial` in segment order.
+// A batch's gathers are unconditional (indices clamped to a valid edge,
+// weight zero) so they all issue before the first is consumed; its size is
+// the wavefront's largest per-group edge count rounded up to a power of two.
 #include "common.h"
 #include "schedule.h"
 
@@ -186,18 +188,20 @@ __global__ __launch_bounds__(kBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a, Sch
     return;
   }
 
-  // Heavy-row segment: wave w takes the segment's edges [64w, 64w + 64),
-  // reduced through LDS.
+  // Heavy-row segment: wave w takes the segment's edges [64w, 64w + 64) of
+  // every 256-edge round, reduced through LDS.
   __shared__ float red[kWavesPerBlock][VPL * W * kWave];
   __shared__ int flag;
   const int4 sg = s.seg[b];
   const int row = sg.x;
-  const int tb = sg.y + wave * kTile;
-  const int cnt = max(0, min(kTile, sg.z - tb));
-  const bool mine = lane < cnt;
-  const int jj = mine ? a.col[tb + lane] : 0;
-  const float vv = mine ? a.val[tb + lane] : 0.0f;
-  gather(a, jj, vv, 0, g, G, cnt, (cnt + G - 1) / G, gl, acc);
+  // Rounds of 4 x 64 edges when the schedule's segments are longer than 256.
+  for (int tb = sg.y + wave * kTile; tb < sg.z; tb += kSegEdges) {
+    const int cnt = min(kTile, sg.z - tb);
+    const bool mine = lane < cnt;
+    const int jj = mine ? a.col[tb + lane] : 0;
+    const float vv = mine ? a.val[tb + lane] : 0.0f;
+    gather(a, jj, vv, 0, g, G, cnt, (cnt + G - 1) / G, gl, acc);
+  }
 #pragma unroll
   for (int v = 0; v < VPL; ++v)
 #pragma unroll

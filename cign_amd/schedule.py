@@ -19,9 +19,11 @@ from ._lib import load_library
 
 # SpMM schedules: rows with at most LIGHT_MAX edges get one wavefront (or a
 # lane group), heavier rows are cut into SEG_EDGES-edge segments, one
-# 256-thread workgroup each.
+# 256-thread workgroup each (two rounds of 256 edges). Rows longer than one
+# segment merge their partial sums across workgroups, which costs an
+# agent-scope release/acquire; 512 keeps those rare on power-law graphs.
 LIGHT_MAX = 64
-SEG_EDGES = 256
+SEG_EDGES = 512
 # Collapsed-GAT pair-layout schedules: one wavefront takes at most 16 edges
 # of a row, segments are 64 edges (16 per wave). The feature-layout forward
 # uses the SpMM geometry; cign_gat_schedule_params says which.

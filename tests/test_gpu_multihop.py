@@ -195,3 +195,39 @@ def test_plan_errors(c3):
         op.plan.forward3(torch.zeros(8, c3.n, device="cuda").t())
     with pytest.raises(ValueError):
         MultiHopCSR3GraphOperator(c3.operator, dense_cols=8, algorithm=4)
+
+
+@pytest.mark.parametrize("seg_edges", [256, 512, 2048])
+@pytest.mark.parametrize("dtype,d", [(torch.float32, 64), (torch.float32, 1100), (torch.bfloat16, 256),
+                                     (torch.bfloat16, 24)])
+def test_spmm_big_hubs_segment_sizes(seg_edges, dtype, d):
+    """Rows of 3,000-6,000 edges: many segments merged across workgroups, and
+    segments longer than one 256-edge round of a workgroup."""
+    from cign_amd.graph import HipCsr
+    from cign_amd.schedule import build_row_schedule
+
+    print(f"spmm big hubs seg={seg_edges} dtype={dtype} d={d}", flush=True)
+    rng = np.random.default_rng(seg_edges + d)
+    n = 7000
+    deg = rng.integers(0, 12, n)
+    deg[[5, 100, 6999]] = [3000, 6000, 1500]
+    deg[[7, 8]] = [65, 257]
+    rp = np.zeros(n + 1, np.int64)
+    rp[1:] = np.cumsum(deg)
+    col = np.concatenate([np.sort(rng.choice(n, size=int(k), replace=False)) for k in deg]).astype(np.int64)
+    # positive weights normalised per row, like the propagation operator
+    # (random-sign weights over 6,000 terms cancel below fp32's reach)
+    val = rng.random(col.size) / np.repeat(np.maximum(deg, 1), deg)
+    crow = torch.from_numpy(rp).cuda()
+    A = torch.sparse_csr_tensor(crow, torch.from_numpy(col).cuda(), torch.from_numpy(val).float().cuda(),
+                                size=(n, n))
+    parts = HipCsr(A)
+    parts.sched = build_row_schedule(crow, seg_edges=seg_edges)
+    x = _rand((n, d), dtype, 3)
+    y = parts.spmm(x)
+    ref = O.spmm(rp, col, val.astype(np.float32).astype(np.float64), x.double().cpu().numpy())
+    if dtype == torch.float32:
+        assert_close(y.cpu().numpy(), ref, name="spmm", **F32_TOL)
+    else:
+        assert_close(y.double().cpu().numpy(), ref, 2e-2, 2e-2, "spmm bf16")
+    assert int(parts.sched.counters.abs().sum()) == 0
