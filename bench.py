@@ -234,7 +234,7 @@ def main():
             fwd_out["gat_bwd"] = ext.backward(0.2, 0.0, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar,
                                               ac, pre, gy)
         else:
-            fwd_out["mh_bwd"] = plan.backward3(g1, g2, g3)
+            fwd_out["mh_bwd"] = [plan.backward3(g1, g2, g3)]
 
     if args.calibrate_copy:
         src = torch.ones(64 << 20, dtype=torch.float32, device=dev)  # 256 MiB
@@ -250,7 +250,6 @@ def main():
         for p in phases:
             run_phase(p)
     torch.cuda.synchronize()
-    eager = {k: [t.clone() for t in v] for k, v in fwd_out.items()}
 
     def capture(fn):
         """HIP graph of fn() (allocations settle in a side-stream run first)."""
@@ -272,6 +271,7 @@ def main():
     if args.eager:
         launch_step = whole_step
     else:
+        eager = {k: [t.clone() for t in v] for k, v in fwd_out.items()}
         # The step as one HIP graph: its host work is one launch, and every
         # replay recomputes every kernel of the four phases.
         launch_step = capture(whole_step).replay
@@ -298,21 +298,25 @@ def main():
     gpu_step_ms = start.elapsed_time(stop) / args.steps
 
     # Per-phase kernel durations: each phase launched R times back to back
-    # (one HIP graph) and timed with HIP events on the launch stream.
+    # (one HIP graph, or R drop-in calls with --eager) and timed with HIP
+    # events on the launch stream.
     R, M = 20, max(2, args.steps // 10)
     phase_ms = {}
     for p in phases:
-        gp = capture(lambda p=p: [run_phase(p) for _ in range(R)])
-        gp.replay()
+        if args.eager:
+            rep = lambda p=p: [run_phase(p) for _ in range(R)]
+        else:
+            gp = capture(lambda p=p: [run_phase(p) for _ in range(R)])
+            rep = gp.replay
+        rep()
         a0, a1 = ev(), ev()
         torch.cuda.synchronize()
         a0.record()
         for _ in range(M):
-            gp.replay()
+            rep()
         a1.record()
         torch.cuda.synchronize()
         phase_ms[p] = a0.elapsed_time(a1) / (M * R)
-        del gp
 
     s = 2 if dt == torch.bfloat16 else 4
     B = workloads.algorithmic_bytes(n, E, H, C, D, s_gat=s, s_mh=s)
