@@ -54,7 +54,10 @@ inline int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 inline BwdLayout bwd_layout(int n, int nnz, int H, int C, int row_blocks, int n_seg_rows, int n_seg_cols) {
   BwdLayout L;
   row_blocks += 1;
-  const int n_l2 = (row_blocks + 63) / 64;
+  // Second-level grad_bias partials: (row_blocks + 63) / 64 for the pair
+  // layout (partials of row blocks), kFlBiasBlocks for the feature layout
+  // (partials of grad_pre rows).
+  const int n_l2 = max((row_blocks + 63) / 64, kFlBiasBlocks);
   int64_t off = 0;
   L.grad_pre = off; off = align256(off + 4LL * n * C);
   L.gscore = off; off = align256(off + 4LL * nnz * H);
@@ -259,8 +262,9 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
     a.row_counters = row_counters; a.col_counters = col_counters;
     a.grad_feat = gxt; a.grad_attn_row = grad_attn_row; a.grad_attn_col = grad_attn_col; a.grad_bias = grad_bias;
     if (fl_ok(dtype, heads, channels)) {
-      if (!aligned16(xt) || !aligned16(gyt) || !aligned16(gxt) || !aligned16(pre))
-        return set_error(kInvalid, "cign_gat_bwd: in_feat, pre, grad_y and grad_feat must be 16-byte aligned");
+      if (!aligned16(xt) || !aligned16(gyt) || !aligned16(gxt) || !aligned16(pre) || !aligned16(grad_bias))
+        return set_error(kInvalid, "cign_gat_bwd: in_feat, pre, grad_y, grad_feat and grad_bias must be 16-byte "
+                                   "aligned");
       const int lgcq = fl_lgcq(dtype, channels);
       const int W = dtype == kBF16 ? 8 : 4;
       int Lq = 1;
@@ -268,7 +272,7 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
       auto go = [&](auto LC) {
         constexpr int LL = decltype(LC)::value;
         a.rows_blocks = BwdFlLauncher<T, LL>::row_blocks(rs, row_sched_info);
-        a.n_l2 = (a.rows_blocks + 63) / 64;
+        a.n_l2 = fl_bias_blocks(n);
         return BwdFlLauncher<T, LL>::run(st, a, rs, row_sched_info, cs, col_sched_info, lgcq);
       };
       switch (Lq) {

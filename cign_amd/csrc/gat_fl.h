@@ -33,8 +33,9 @@
 //   grad_feat[j,h]     = sum_i s kw g_pre[i] / H
 //   grad_attn_col[j,h] = <sum_i s l' kw g_pre[i], x[j,h]> / H - sum_i s l' wsum_i
 // gathering per entry one 16-byte row record {attn_row, edge_max, 1/edge_sum,
-// wsum} (written by the rows kernel) and the g_pre chunk. grad_bias is the
-// deterministic two-level reduction of per-workgroup g_pre sums.
+// wsum} (written by the rows kernel) and the g_pre chunk. grad_bias is a
+// deterministic two-level column sum of g_pre done by the columns kernel's
+// trailing workgroups, so the rows kernel has no block barrier on light rows.
 #pragma once
 
 #include "gat_kernels.h"
@@ -67,6 +68,11 @@ constexpr int kColsU = CIGN_FL_COLS_U;
 constexpr int kFlLightMax = 64;
 constexpr int kFlSegEdges = 512;
 constexpr int kSegRound = kWavesPerBlock * kWave;
+
+// grad_bias of the feature layout: the columns kernel's last
+// ceil(n / 256) (at most kFlBiasBlocks) workgroups sum grad_pre rows.
+constexpr int kFlBiasBlocks = 256;
+inline int fl_bias_blocks(int n) { return max(1, min(kFlBiasBlocks, (n + 255) / 256)); }
 
 template <typename T>
 struct FlGeom {
@@ -524,21 +530,14 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a
   const int nq = a.H * cq;
   const FlLane<L> ln(lgcq, nq);
   const int wave = wave_id();
-  __shared__ float bsh[kWavesPerBlock][kMaxC];
   __shared__ float red[kWavesPerBlock][3][kFlHeads];
   __shared__ int flag;
   RowAcc<W> st;
   st.clear();
   float gp[W];
-  float bv[W];  // this lane's g_pre contribution to the block's bias partial
-#pragma unroll
-  for (int w = 0; w < W; ++w) bv[w] = 0.0f;
   int b = blockIdx.x;
-  const bool heavy = b < s.n_seg;
-  int row = 0;
-  RowHead rh;
 
-  if (!heavy) {
+  if (b >= s.n_seg) {
     b -= s.n_seg;
     const bool tiny = b >= mid_blocks;
     int4 r = make_int4(0, 0, 0, 0);
@@ -552,11 +551,11 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a
       has = li < n_mid;
       if (has) r = s.light[li];
     }
-    row = r.x;
+    const int row = r.x;
     const int deg = r.z - r.y;
     const int slot = tiny ? ln.gl : ln.lane;
     const int jj = slot < deg ? a.col[r.y + slot] : 0;
-    rh = row_head(a, row, ln.hq);
+    const RowHead rh = row_head(a, row, ln.hq);
     grad_pre_chunk(a, row, ln.cw, gp);
     if (tiny) {
       rows_edges<T, L, DROP>(a, ln, jj, ln.g * L, 0, 1, deg, wave_group_max<L>(deg), r.y, rh, st);
@@ -570,54 +569,36 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a
     rows_dots<W>(st, gp, cq, a.inv_h, wsum, A);
     const bool write = has && (tiny || ln.g == 0) && ln.qv;
     if (write && ln.cw == 0) rows_store(a, row, ln.hq, rh, wsum, A, st.B);
-    if (write && ln.hq == 0) {
-      store_f32<W>(a.grad_pre + static_cast<int64_t>(row) * a.C + ln.cw * W, gp);
-#pragma unroll
-      for (int w = 0; w < W; ++w) bv[w] = gp[w];
-    }
-  } else {
-    const int4 sg = s.seg[b];
-    row = sg.x;
-    const int2 hr = s.hrow[sg.w];
-    rh = row_head(a, row, ln.hq);
-    grad_pre_chunk(a, row, ln.cw, gp);
-    for (int tb = sg.y + wave * kWave; tb < sg.z; tb += kSegRound) {
-      const int cnt = min(kWave, sg.z - tb);
-      const int jj = ln.lane < cnt ? a.col[tb + ln.lane] : 0;
-      rows_edges<T, L, DROP>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, rh, st);
-    }
-    group_sum<L, W>(st.vs);
-    group_sum<L, W>(st.vsl);
-    st.B = group_sum1<L>(st.B);
-    float wsum, A;
-    rows_dots<W>(st, gp, cq, a.inv_h, wsum, A);
-    if (ln.g == 0 && ln.qv && ln.cw == 0) {
-      red[wave][0][ln.hq] = wsum;
-      red[wave][1][ln.hq] = A;
-      red[wave][2][ln.hq] = st.B;
-    }
-    // The row's g_pre enters the bias once, from its first segment.
-    if (b == hr.x && wave == 0 && ln.g == 0 && ln.qv && ln.hq == 0) {
-      store_f32<W>(a.grad_pre + static_cast<int64_t>(row) * a.C + ln.cw * W, gp);
-#pragma unroll
-      for (int w = 0; w < W; ++w) bv[w] = gp[w];
-    }
+    if (write && ln.hq == 0) store_f32<W>(a.grad_pre + static_cast<int64_t>(row) * a.C + ln.cw * W, gp);
+    return;
   }
 
-  // Block partial of grad_bias: lanes hq = 0 hold chunk cw of their row.
-  group_sum<L, W>(bv);
-  if (ln.g == 0 && ln.qv && ln.hq == 0)
-#pragma unroll
-    for (int w = 0; w < W; ++w) bsh[wave][ln.cw * W + w] = bv[w];
-  __syncthreads();
-  for (int c = threadIdx.x; c < a.C; c += kBlock)
-    a.bias_part[static_cast<int64_t>(blockIdx.x) * a.C + c] = bsh[0][c] + bsh[1][c] + bsh[2][c] + bsh[3][c];
-  if (!heavy) return;
-
-  // Heavy segment: the four waves' (wsum, A, B) per head, then across the
+  // Heavy-row segment: the four waves' (wsum, A, B) per head, then across the
   // row's segments (last to finish, in segment order).
   const int4 sg = s.seg[b];
+  const int row = sg.x;
   const int2 hr = s.hrow[sg.w];
+  const RowHead rh = row_head(a, row, ln.hq);
+  grad_pre_chunk(a, row, ln.cw, gp);
+  for (int tb = sg.y + wave * kWave; tb < sg.z; tb += kSegRound) {
+    const int cnt = min(kWave, sg.z - tb);
+    const int jj = ln.lane < cnt ? a.col[tb + ln.lane] : 0;
+    rows_edges<T, L, DROP>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, rh, st);
+  }
+  group_sum<L, W>(st.vs);
+  group_sum<L, W>(st.vsl);
+  st.B = group_sum1<L>(st.B);
+  float wsum, A;
+  rows_dots<W>(st, gp, cq, a.inv_h, wsum, A);
+  if (ln.g == 0 && ln.qv && ln.cw == 0) {
+    red[wave][0][ln.hq] = wsum;
+    red[wave][1][ln.hq] = A;
+    red[wave][2][ln.hq] = st.B;
+  }
+  // The row's g_pre is published once, by its first segment.
+  if (b == hr.x && wave == 0 && ln.g == 0 && ln.qv && ln.hq == 0)
+    store_f32<W>(a.grad_pre + static_cast<int64_t>(row) * a.C + ln.cw * W, gp);
+  __syncthreads();
   if (threadIdx.x < 3 * kFlHeads) {
     const int k = threadIdx.x / kFlHeads, h = threadIdx.x % kFlHeads;
     red[0][k][h] = red[0][k][h] + red[1][k][h] + red[2][k][h] + red[3][k][h];
@@ -743,7 +724,7 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
   int b = blockIdx.x;
   const int nsched = s.n_seg + mid_blocks + (s.n_light - n_mid + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
   if (b >= nsched) {
-    bias_reduce(a, b - nsched, a.col_counters + s.n_hrow, &flag);
+    bias_from_grad_pre(a, b - nsched, a.col_counters + s.n_hrow, &flag);
     return;
   }
   ColAcc<W> st;

@@ -753,6 +753,52 @@ __device__ __forceinline__ void bias_reduce(const GatBwdArgs<T>& a, int q, int* 
   reduce(a.bias_l2, 0, a.n_l2, a.grad_bias);
 }
 
+// grad_bias = sum_n grad_pre[n, :] in two deterministic levels: workgroup q
+// of a.n_l2 sums rows [q*R, q*R + R) (R = ceil(n / n_l2)) into bias_l2[q];
+// the last one to finish sums the n_l2 partials in order. Threads own a
+// (row, 4-channel chunk) pair and read float4 (C % 4 == 0, rows 16-byte
+// aligned), 256 / (C/4) rows per step.
+template <typename T>
+__device__ __forceinline__ void bias_from_grad_pre(const GatBwdArgs<T>& a, int q, int* counter, int* flag) {
+  __shared__ float4 red[kBlock];
+  const int C = a.C;
+  const int c4n = C / 4;
+  const int rpi = kBlock / c4n;
+  const int tid = threadIdx.x;
+  const int c4 = tid % c4n;
+  const int r0 = tid / c4n;
+  auto reduce = [&](const float* src, int lo, int hi, float* dst) {
+    float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 4
+    for (int r = lo + r0; r < hi; r += rpi) {
+      const float4 v = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(r) * C + c4 * 4);
+      t.x += v.x;
+      t.y += v.y;
+      t.z += v.z;
+      t.w += v.w;
+    }
+    red[tid] = t;
+    __syncthreads();
+    if (tid < c4n) {
+      float4 u = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      for (int k = 0; k < rpi; ++k) {
+        const float4 v = red[k * c4n + tid];
+        u.x += v.x;
+        u.y += v.y;
+        u.z += v.z;
+        u.w += v.w;
+      }
+      *reinterpret_cast<float4*>(dst + tid * 4) = u;
+    }
+    __syncthreads();
+  };
+  const int R = (a.n + a.n_l2 - 1) / a.n_l2;
+  const int lo = min(a.n, q * R), hi = min(a.n, lo + R);
+  reduce(a.grad_pre, lo, hi, a.bias_l2 + static_cast<int64_t>(q) * C);
+  if (!arrive_last(counter, a.n_l2, flag)) return;
+  reduce(a.bias_l2, 0, a.n_l2, a.grad_bias);
+}
+
 template <typename T, int HP, int CP>
 __global__ __launch_bounds__(kBlock) void gat_bwd_cols_kernel(GatBwdArgs<T> a, Sched s) {
   using GR = GroupReduce<CP, HP>;

@@ -31,8 +31,15 @@
 namespace cign {
 namespace {
 
+// Workgroup shape of the SpMM: kSpmmWaves wavefronts; a heavy-row segment is
+// processed in rounds of kSpmmWaves x 64 edges.
+#ifndef CIGN_SPMM_WAVES
+#define CIGN_SPMM_WAVES 4
+#endif
+constexpr int kSpmmWaves = CIGN_SPMM_WAVES;
+constexpr int kSpmmBlock = kSpmmWaves * kWave;
 constexpr int kTile = 64;
-constexpr int kSegEdges = kWavesPerBlock * kTile;
+constexpr int kSegEdges = kSpmmWaves * kTile;
 
 template <typename T, int W, int VPL>
 struct SpmmArgs {
@@ -145,7 +152,7 @@ __device__ __forceinline__ void write_row(const SpmmArgs<T, W, VPL>& a, int row,
 }
 
 template <typename T, int W, int VPL>
-__global__ __launch_bounds__(kBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a, Sched s) {
+__global__ __launch_bounds__(kSpmmBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a, Sched s) {
   const int lane = lane_id();
   const int wave = wave_id();
   const int gl = lane & (a.L - 1);
@@ -160,7 +167,7 @@ __global__ __launch_bounds__(kBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a, Sch
     if (b < a.mid_blocks) {
       // Medium row (L < degree <= 64): one per wavefront, group g takes edges
       // g, g + G, ...
-      const int li = b * kWavesPerBlock + wave;
+      const int li = b * kSpmmWaves + wave;
       if (li >= a.n_mid) return;
       const int4 r = s.light[li];
       const int deg = r.z - r.y;
@@ -176,7 +183,7 @@ __global__ __launch_bounds__(kBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a, Sch
       return;
     }
     // Tiny rows (degree <= L): one per lane group.
-    const int li = a.n_mid + ((b - a.mid_blocks) * kWavesPerBlock + wave) * G + g;
+    const int li = a.n_mid + ((b - a.mid_blocks) * kSpmmWaves + wave) * G + g;
     const bool has = li < s.n_light;
     const int4 r = has ? s.light[li] : make_int4(0, 0, 0, 0);
     const int deg = r.z - r.y;
@@ -190,7 +197,7 @@ __global__ __launch_bounds__(kBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a, Sch
 
   // Heavy-row segment: wave w takes the segment's edges [64w, 64w + 64) of
   // every 256-edge round, reduced through LDS.
-  __shared__ float red[kWavesPerBlock][VPL * W * kWave];
+  __shared__ float red[kSpmmWaves][VPL * W * kWave];
   __shared__ int flag;
   const int4 sg = s.seg[b];
   const int row = sg.x;
@@ -219,8 +226,10 @@ __global__ __launch_bounds__(kBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a, Sch
   __syncthreads();
   const int2 hr = s.hrow[sg.w];
   if (hr.y == 1) {
-    for (int c = threadIdx.x; c < width; c += kBlock) {
-      float t = red[0][c] + red[1][c] + red[2][c] + red[3][c];
+    for (int c = threadIdx.x; c < width; c += kSpmmBlock) {
+      float t = 0.0f;
+#pragma unroll
+      for (int v = 0; v < kSpmmWaves; ++v) t += red[v][c];
       const int64_t off = static_cast<int64_t>(row) * a.ld + a.c0 + c;
       if (a.add) t += to_f32(a.add[off]);
       a.y[off] = from_f32<T>(t);
@@ -228,9 +237,14 @@ __global__ __launch_bounds__(kBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a, Sch
     return;
   }
   float* part = a.partial + static_cast<int64_t>(b) * width;
-  for (int c = threadIdx.x; c < width; c += kBlock) part[c] = red[0][c] + red[1][c] + red[2][c] + red[3][c];
+  for (int c = threadIdx.x; c < width; c += kSpmmBlock) {
+    float t = 0.0f;
+#pragma unroll
+    for (int v = 0; v < kSpmmWaves; ++v) t += red[v][c];
+    part[c] = t;
+  }
   if (!arrive_last(a.counters + sg.w, hr.y, &flag)) return;
-  for (int c = threadIdx.x; c < width; c += kBlock) {
+  for (int c = threadIdx.x; c < width; c += kSpmmBlock) {
     float t = 0.0f;
     for (int q = 0; q < hr.y; ++q) t += a.partial[static_cast<int64_t>(hr.x + q) * width + c];
     const int64_t off = static_cast<int64_t>(row) * a.ld + a.c0 + c;
@@ -275,12 +289,12 @@ int launch_tile(hipStream_t stream, const Sched& s, const SchedInfo& info, int l
   // light list (sorted by degree, descending) one per wavefront.
   const int n_mid = (G > 1 && a.L >= 8) ? sched_count_gt(info.hdr, a.L) : info.n_light;
   a.n_mid = n_mid;
-  a.mid_blocks = (n_mid + kWavesPerBlock - 1) / kWavesPerBlock;
+  a.mid_blocks = (n_mid + kSpmmWaves - 1) / kSpmmWaves;
   const int n_tiny = info.n_light - n_mid;
-  const int tiny_blocks = (n_tiny + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
+  const int tiny_blocks = (n_tiny + kSpmmWaves * G - 1) / (kSpmmWaves * G);
   const int blocks = s.n_seg + a.mid_blocks + tiny_blocks;
   if (blocks == 0) return kOk;
-  hipLaunchKernelGGL((spmm_kernel<T, W, VPL>), dim3(blocks), dim3(kBlock), 0, stream, a, s);
+  hipLaunchKernelGGL((spmm_kernel<T, W, VPL>), dim3(blocks), dim3(kSpmmBlock), 0, stream, a, s);
   return check_launch("cign_spmm");
 }
 
