@@ -55,6 +55,13 @@ _SIGNATURES = {
     "cign_hop_gate_bwd_workspace_bytes": (_I64, [_I64, _I32, _I32]),
     "cign_hop_gate_fwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P]),
     "cign_hop_gate_bwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64]),
+    # MFMA projections (gemm.hip)
+    "cign_linear_fwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P]),
+    "cign_linear_logits_fwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P]),
+    "cign_linear_gamma_fwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _F32, _U64, _P, _P,
+                                        _P]),
+    "cign_linear_bwd_workspace_bytes": (_I64, [_I64, _I32, _I32, _I32]),
+    "cign_linear_bwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _I64]),
     # Clifford packs (pack.hip)
     "cign_pack_fwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _I64, _P, _P]),
     "cign_pack_bwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I64,

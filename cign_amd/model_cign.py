@@ -7,14 +7,15 @@ reference's.
 The reference picks between PyG / dgNN / CUDA / torch paths with its
 ``use_*`` flags. Here every flag combination runs the one HIP route:
 - fused dropout + LayerNorm (cign_dropout_ln_*);
-- the GAT ``lin`` projection (dense GEMM on MFMA via hipBLASLt);
-- fused attention logits and the collapsed GAT with head-mean + bias + SiLU;
+- the GAT ``lin`` projection with the attention logits in its epilogue (one
+  MFMA kernel, cign_linear_logits_fwd);
+- the collapsed GAT with head-mean + bias + SiLU;
 - fused add + LayerNorm;
 - the multihop SpMM (selected_sparse_powers);
 - the hop gate kernel;
 - the fused Clifford pack for any interaction x weighting x K;
-- the projection ``proj`` (hipBLASLt);
-- fused dropout-gamma-residual.
+- the projection ``proj`` with bias, dropout and the gamma residual in its
+  epilogue (one MFMA kernel, cign_linear_gamma_fwd).
 
 The flags are accepted for signature compatibility and validated like the
 reference's. ``use_chunked_fused_gat`` (the dgNN chunking backend) is out of
@@ -31,10 +32,10 @@ import torch.nn.functional as F
 
 from . import _pack
 from .collapsed_gat import collapsed_gat_mean_bias_silu
-from .fused_block_ops import fused_add_layernorm, fused_dropout_gamma_residual, fused_dropout_layernorm
-from .fused_gat_sideops import fused_attention_logits
+from .fused_block_ops import fused_add_layernorm, fused_dropout_layernorm
 from .graph import selected_sparse_powers
 from .hop_gate import global_hop_gate, node_hop_gate
+from .linear import linear_attention_logits, linear_gamma_residual, mfma_linear
 
 
 def cign_outer_difference(b_hr, b_rh, mode):
@@ -67,13 +68,9 @@ def _resolve_old_new_mode(explicit_value, env_name: str, default: str = "old") -
 
 
 def _local_amp_linear(linear: nn.Linear, x: torch.Tensor, enabled: bool, amp_dtype: torch.dtype) -> torch.Tensor:
-    """One dense Linear, optionally under local autocast, returned as fp32
-    (model_cign.py:86-103). On ROCm the GEMM runs on hipBLASLt (MFMA)."""
-    if bool(enabled) and x.is_cuda:
-        with torch.autocast(device_type="cuda", dtype=amp_dtype, enabled=True, cache_enabled=True):
-            y = linear(x)
-        return y.float()
-    return linear(x).float()
+    """One dense Linear, optionally under local bf16 autocast, returned as
+    fp32 (model_cign.py:86-103), on the MFMA kernel (cign_linear_fwd)."""
+    return mfma_linear(linear, x, enabled, amp_dtype)
 
 
 def _glorot_(t: torch.Tensor) -> None:
@@ -121,8 +118,8 @@ class CompatibleCollapsedFusedGATConv(nn.Module):
             raise RuntimeError(f"Generalized collapsed GAT requires 1<=heads<=32 and 1<=channels<=256; got H={H},C={C}")
         amp_enabled = bool(getattr(self, "_selective_amp_enabled", False))
         amp_dtype = getattr(self, "_selective_amp_dtype", torch.bfloat16)
-        xp = _local_amp_linear(self.lin, x, amp_enabled, amp_dtype).view(-1, H, C)
-        alpha_src, alpha_dst = fused_attention_logits(xp, self.att_src, self.att_dst)
+        xp, alpha_src, alpha_dst = linear_attention_logits(x, self.lin.weight, self.att_src, self.att_dst, H,
+                                                           amp_enabled, amp_dtype)
         dropout = self.dropout if self.training else 0.0
         return collapsed_gat_mean_bias_silu(attn_row=alpha_dst, attn_col=alpha_src, csr=csr, csc=csc, perm=perm,
                                             negative_slope=self.negative_slope, in_feat=xp, bias=self.bias,
@@ -221,6 +218,6 @@ class GraphCliffordBlock(nn.Module):
         hop_gate = self.compute_hop_gate(H_norm, C_norm)
         G_raw = _pack.clifford_pack_any(H_norm, C_norm, [propagated[s] for s in self.order_set], hop_gate,
                                         self._interaction_code(), 0 if self.alpha_weighting_mode == "old" else 1)
-        G_feat = _local_amp_linear(self.proj, G_raw, self.use_selective_amp, self.selective_amp_dtype)
         gamma = self.gamma if self.gamma_mode == "vector" else self.gamma.expand(self.hidden_dim)
-        return fused_dropout_gamma_residual(H, G_feat, gamma.contiguous(), p)
+        return linear_gamma_residual(H, G_raw, self.proj, gamma.contiguous(), p, self.use_selective_amp,
+                                     self.selective_amp_dtype)

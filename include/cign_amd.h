@@ -247,6 +247,49 @@ int cign_pack_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t interac
                   int64_t prop_stride, const float* alpha, float* grad_H, float* grad_C, float* const* grad_props,
                   int64_t grad_prop_stride, float* grad_alpha);
 
+/* ---- dense projections on MFMA ------------------------------------------ */
+
+/* math: 0 = float32 (fp32 MFMA, exact fp32 products), 1 = bf16 autocast
+ * (inputs rounded to bf16, bf16 MFMA with fp32 accumulation, output rounded to
+ * bf16 and stored as float32). x [M,K] float32 or bfloat16 (x_dtype; bf16
+ * needs math 1), weight [N,K] float32 (nn.Linear layout), bias [N] or NULL.
+ * Any M, N, K; rows that start 16-byte aligned are read with vector loads. */
+
+/* y [M,N] = x W^T + b. Replaces _local_amp_linear / nn.Linear
+ * (generic_engine/model_cign.py:86-103: GAT lin :546-553, proj :927-929,
+ * input projections :1165-1171). */
+int cign_linear_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t x_dtype, int32_t math, const void* x,
+                    const float* w, const float* bias, float* y);
+
+/* GAT lin + attention logits in one kernel: y [M,H*C] = x W^T (no bias),
+ * alpha_src[m,h] = <y[m,h,:], att_src[h,:]>, alpha_dst likewise; C in
+ * {16, 32, 64, 128}. Replaces the lin call of CompatibleCollapsedFusedGATConv
+ * (model_cign.py:546-553) followed by ext attention_forward
+ * (fused_gat_sideops.cpp:45-52). */
+int cign_linear_logits_fwd(void* stream, int64_t M, int32_t heads, int32_t channels, int32_t K, int32_t x_dtype,
+                           int32_t math, const void* x, const float* w, const float* att_src, const float* att_dst,
+                           float* y, float* alpha_src, float* alpha_dst);
+
+/* Projection + dropout-gamma-residual: g_out [M,N] = x W^T + b,
+ * y = h + gamma * keep * g_out / (1-p), mask [M,N] u8 (keep = 53-bit
+ * splitmix64 of seed and m*N+n, keep when u >= p). Replaces proj
+ * (model_cign.py:927-929) followed by ext dropout_gamma_residual_forward
+ * (fused_block_ops.cpp:72-80). */
+int cign_linear_gamma_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t x_dtype, int32_t math,
+                          const void* x, const float* w, const float* bias, const float* h, const float* gamma,
+                          float dropout_p, uint64_t seed, float* g_out, float* y, uint8_t* mask);
+
+/* Workspace bytes of cign_linear_bwd. */
+int64_t cign_linear_bwd_workspace_bytes(int64_t M, int32_t N, int32_t K, int32_t with_bias);
+
+/* grad_x [M,K] = grad_y W (NULL to skip; bf16 MFMA when math = 1),
+ * grad_w [N,K] = grad_y^T x and grad_b [N] = sum_m grad_y (NULL to skip) in
+ * fp32 MFMA, deterministic. grad_y, x float32. Replaces the autograd backward
+ * of the Linear layers above. */
+int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math, const float* grad_y, const float* x,
+                    const float* w, float* grad_x, float* grad_w, float* grad_b, void* workspace,
+                    int64_t workspace_bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -568,3 +568,41 @@ def hop_gate_backward(g_alpha, H, C, weight, bias, score_mode):
         sg = np.sign(H - C)
         gH, gC = g1 + sg * g2, g1 - sg * g2
     return gH, gC, gl.T @ s, gl.sum(axis=0)
+
+
+# ---------------------------------------------------------------------------
+# Dense projections (nn.Linear under _local_amp_linear)
+# ---------------------------------------------------------------------------
+def bf16_round(x):
+    """Round-to-nearest-even to bfloat16, returned as float64 (the cast that
+    torch.autocast applies to Linear inputs and outputs). Pinned against
+    torch's own float32 -> bfloat16 conversion in tests/test_oracle.py."""
+    a = np.ascontiguousarray(np.asarray(x, np.float32))
+    u = a.view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    r = np.where(nan, u | 0x400000, r).astype(np.uint32)
+    return r.view(np.float32).astype(np.float64)
+
+
+def linear_forward(x, w, b=None, amp=False):
+    """_local_amp_linear (generic_engine/model_cign.py:86-103): y = x W^T + b
+    in float64; with amp (local bf16 autocast) inputs, weight and bias are
+    rounded to bf16 first and the output is rounded to bf16 (autocast output
+    dtype) before the cast back to float32. Pinned by the closed form (float64
+    matmul) and by the autocast rounding points."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    if amp:
+        x, w = bf16_round(x), bf16_round(w)
+        b = None if b is None else bf16_round(b)
+    y = x @ w.T
+    if b is not None:
+        y = y + np.asarray(b, np.float64)
+    return bf16_round(y) if amp else y
+
+
+def linear_backward(gy, x, w):
+    """grad_x = gy W, grad_W = gy^T x, grad_b = sum_n gy (float64)."""
+    gy, x, w = (np.asarray(v, np.float64) for v in (gy, x, w))
+    return gy @ w, gy.T @ x, gy.sum(axis=0)

@@ -445,3 +445,39 @@ def test_block_oracle_stages_match_numpy_oracle():
                               None if a is None else torch.tensor(a)[:, :, None], inter, w)
                 want = O.clifford_pack_forward(Hn, Cn, props, np.ones((n, K)) if a is None else a, inter, w)
                 assert np.allclose(got.numpy(), want, rtol=1e-12, atol=1e-12), (inter, w, a is None)
+
+
+def test_bf16_round_matches_torch_cast():
+    """The oracle's bf16 rounding is torch's float32 -> bfloat16 cast (RNE),
+    including ties, subnormals, infinities and NaN."""
+    import torch
+
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.integers(-40, 38, 20000),
+                           np.array([0.0, -0.0, 1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, 1e-45, -3e-39, np.inf, -np.inf,
+                                     3.3895314e38], dtype=np.float32)]).astype(np.float32)
+    got = O.bf16_round(vals)
+    want = torch.from_numpy(vals).to(torch.bfloat16).double().numpy()
+    assert np.array_equal(got, want)
+    assert np.isnan(O.bf16_round(np.array([np.nan], np.float32)))[0]
+
+
+def test_linear_oracle_amp_rounding_points():
+    """amp: operands and output rounded to bf16 (torch CPU autocast of
+    F.linear gives the same within one bf16 ulp of the output)."""
+    import torch
+
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((64, 48)).astype(np.float32)
+    w = rng.standard_normal((24, 48)).astype(np.float32) / 7
+    b = rng.standard_normal(24).astype(np.float32)
+    y = O.linear_forward(x, w, b, amp=True)
+    assert np.array_equal(O.bf16_round(y), y)
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        t = torch.nn.functional.linear(torch.from_numpy(x), torch.from_numpy(w), torch.from_numpy(b))
+    assert t.dtype == torch.bfloat16
+    np.testing.assert_allclose(t.double().numpy(), y, rtol=2 ** -7, atol=2 ** -7)
+    gx, gw, gb = O.linear_backward(np.ones((64, 24)), x, w)
+    np.testing.assert_allclose(gw, np.tile(x.astype(np.float64).sum(0), (24, 1)), rtol=1e-12)
+    np.testing.assert_allclose(gb, np.full(24, 64.0))
+    np.testing.assert_allclose(gx, np.tile(w.astype(np.float64).sum(0), (64, 1)), rtol=1e-12)
