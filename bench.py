@@ -39,7 +39,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 disables)")
-    ap.add_argument("--dtype", choices=["f32", "bf16"], default="f32")
+    ap.add_argument("--workload", choices=["layer", "scale"], default="layer",
+                    help="layer: the headline c2+c3 layer (24,492 nodes); scale: the same layer at c5 size "
+                         "(2.4M nodes, ~62M edges, GAT 4x32 + SpMM D=256, bf16 by default)")
+    ap.add_argument("--dtype", choices=["f32", "bf16"], default=None)
     ap.add_argument("--eager", action="store_true",
                     help="launch every step through the Python drop-in API instead of replaying it as a HIP graph")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -98,6 +101,40 @@ def cpu_baseline(w, seconds: float, H: int, C: int, D: int):
                       f"1 thread"}
 
 
+def invariants(torch, w, ext, plan, H, C, D, dt):
+    """Size-independent checks of the full-size run (no oracle at this size):
+    * P = D^-1/2 (A+I) D^-1/2 has x_i = sqrt(deg_i) as a fixed point, so
+      forward3 returns (x, x, x) and backward3(0, 0, x) returns x;
+    * constant features make every per-head aggregate exactly 1 (the softmax
+      weights of a row sum to 1), so pre = 1 + bias, and the attention
+      gradients vanish (ge' is constant along a row, so ge' - wsum = 0).
+    Returns the worst relative errors."""
+    n = w.n
+    (rowptr, col), (row, colptr), perm = w.gat_graph
+    deg = torch.diff(w.operator.csr.crow_indices()).float()
+    xs = deg.sqrt()[:, None].expand(n, D).contiguous().to(dt)
+    ref = xs.float()
+    ys = plan.forward3(xs)
+    zero = torch.zeros_like(xs)
+    gx = plan.backward3(zero, zero, xs)
+    scale = float(ref.abs().max())
+    mh_err = max(float((y.float() - ref).abs().max()) for y in (*ys, gx)) / scale
+    ones = torch.ones(n, H, C, device=xs.device, dtype=dt)
+    g = torch.Generator(device="cpu").manual_seed(1)
+    ar = torch.randn(n, H, generator=g).to(xs.device)
+    ac = torch.randn(n, H, generator=g).to(xs.device)
+    bias = torch.randn(C, generator=g).to(xs.device)
+    gy = torch.randn(n, C, generator=g).to(xs.device).to(dt)
+    out, pre, emax, esum, mask = ext.forward(ar, ac, rowptr, col, 0.2, ones, bias, 0.0, 0)
+    gat_err = float((pre - (1.0 + bias)[None]).abs().max()) / float((1.0 + bias).abs().max())
+    gf, gar, gac, gb = ext.backward(0.2, 0.0, rowptr, col, colptr, row, perm, emax, esum, mask, ones, ar, ac, pre, gy)
+    gscale = float(gf.float().abs().max())
+    att_err = max(float(gar.abs().max()), float(gac.abs().max())) / gscale
+    torch.cuda.synchronize()
+    return {"multihop_fixed_point_rel_err": mh_err, "gat_constant_feature_pre_rel_err": gat_err,
+            "gat_constant_feature_attention_grad_rel": att_err}
+
+
 # ---------------------------------------------------------------------------
 # rocprofv3 summaries (profiles/): kernel statistics and copy-calibrated
 # FETCH_SIZE / WRITE_SIZE traffic per launch.
@@ -112,9 +149,10 @@ def _short(name: str) -> str:
     return name.split("(")[0] if "(" in name else name
 
 
-def measured_traffic(dtype: str, phase: str):
-    """HBM bytes per launch of `phase` from the committed rocprofv3 --pmc summary, or (None, None)."""
-    path = ROOT / "profiles" / f"layer_c2c3_{dtype}_traffic.json"
+def measured_traffic(name: str, phase: str):
+    """HBM bytes per launch of `phase` from the committed rocprofv3 --pmc summary
+    profiles/<name>_traffic.json, or (None, None)."""
+    path = ROOT / "profiles" / f"{name}_traffic.json"
     if not path.exists():
         return None, None
     d = json.loads(path.read_text())
@@ -157,9 +195,12 @@ def summarize(prof_dir: str, name: str, command: str) -> None:
         return per
 
     fetch, write = counters("fetch", "FETCH_SIZE"), counters("write", "WRITE_SIZE")
-    # the copy reads and writes 256 MiB (torch's fill that made its source only writes)
-    copy = sorted((k for k in write if "elementwise" in k and max(write[k]) > 0.9 * COPY_KIB and k in fetch),
-                  key=lambda k: -max(fetch[k]))
+    # The calibration copy is torch.mul(src, 1.0, out=dst) over 256 MiB: the
+    # MulFunctor elementwise kernel whose writes are 256 MiB (other elementwise
+    # kernels of the run, e.g. dtype conversions, may move more).
+    copy = sorted((k for k in write if "MulFunctor" in k and k in fetch
+                   and abs(statistics.median(write[k]) - COPY_KIB) < 0.1 * COPY_KIB),
+                  key=lambda k: abs(statistics.median(write[k]) - COPY_KIB))
     if not copy:
         raise SystemExit("no calibration copy kernel in the counter runs (run bench.py with --calibrate-copy)")
     fk = COPY_KIB / statistics.median(fetch[copy[0]])
@@ -204,9 +245,20 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    H, C, D = 4, 16, 64
+    scale = args.workload == "scale"
+    if args.dtype is None:
+        args.dtype = "bf16" if scale else "f32"
+    H, C, D = (4, 32, 256) if scale else (4, 16, 64)
     dt = torch.float32 if args.dtype == "f32" else torch.bfloat16
-    w = workloads.build(workloads.C2, device=dev)
+    t_build = time.perf_counter()
+    if scale:
+        print("building the c5 graph on the host (about 1.5 minutes)...", file=sys.stderr, flush=True)
+        # Captured graphs would keep one output set per captured launch; at
+        # this size the GPU is the bottleneck, so launches stay eager.
+        args.eager = True
+    w = workloads.build(workloads.C5 if scale else workloads.C2, device=dev)
+    if scale:
+        print(f"graph built in {time.perf_counter() - t_build:.0f} s", file=sys.stderr, flush=True)
     (rowptr, col), (row, colptr), perm = w.gat_graph
     n, E = w.n, w.nnz_gat
     g = torch.Generator(device="cpu").manual_seed(0)
@@ -300,7 +352,7 @@ def main():
     # Per-phase kernel durations: each phase launched R times back to back
     # (one HIP graph, or R drop-in calls with --eager) and timed with HIP
     # events on the launch stream.
-    R, M = 20, max(2, args.steps // 10)
+    R, M = (1, max(2, args.steps)) if scale else (20, max(2, args.steps // 10))
     phase_ms = {}
     for p in phases:
         if args.eager:
@@ -337,11 +389,13 @@ def main():
     kernel_name = {"gat_fwd": "cign_gat_fwd (gat_fwd_fl_kernel)", "spmm_fwd3": "spmm_kernel (fwd hop)",
                    "gat_bwd": "cign_gat_bwd (gat_bwd_rows_fl_kernel + gat_bwd_cols_fl_kernel)",
                    "spmm_bwd3": "spmm_kernel (bwd hop, fused add)"}[dom]
-    traffic, traffic_src = measured_traffic(args.dtype, dom)
+    traffic, traffic_src = measured_traffic(f"layer_{'c5' if scale else 'c2c3'}_{args.dtype}", dom)
     layer_gbs = B["layer"] / (ms * 1e-3) / 1e9
 
+    checks = invariants(torch, w, ext, plan, H, C, D, dt) if scale else None
+
     cpu = None
-    if args.cpu_seconds > 0:
+    if args.cpu_seconds > 0 and not scale:
         cpu = cpu_baseline(w, args.cpu_seconds, H, C, D)
 
     line = {
@@ -357,8 +411,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": args.dtype,
-        "data": "synthetic: seeded Chung-Lu power-law graph (gamma 2.5), N(0,1) features and gradient probes",
-        "config": {"workload": "c2+c3 layer: collapsed GAT H=4 x C=16 + 3-hop CSR SpMM D=64, forward+backward",
+        "data": (f"synthetic: seeded Chung-Lu power-law graph (gamma {2.2 if scale else 2.5}), N(0,1) features "
+                 "and gradient probes"),
+        "config": {"workload": (f"{'c5 scale' if scale else 'c2+c3'} layer: collapsed GAT H={H} x C={C} + 3-hop "
+                                f"CSR SpMM D={D}, forward+backward"),
                    "launch": "eager" if args.eager else "hip_graph_per_step",
                    "nodes": n, "edges_nnz": E, "heads": H, "channels": C, "dense_cols": D, "hops": 3,
                    "max_in_degree": int(torch.diff(rowptr.long()).max())},
@@ -372,6 +428,8 @@ def main():
                      "avg_launch_ms": round(dom_ms, 5)},
         "cpu_baseline": cpu,
     }
+    if checks is not None:
+        line["invariants"] = checks
     print(json.dumps(line), flush=True)
 
 

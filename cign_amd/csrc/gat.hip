@@ -101,11 +101,14 @@ inline int fl_lgcq(int dtype, int C) {
   return lg;
 }
 
-// Schedule geometry (light_max, seg_edges) each GAT pass runs on.
+// Schedule geometry (light_max, seg_edges) each GAT pass runs on. The
+// feature-layout kernels take any segment length that is a multiple of their
+// 256-edge round (reported as seg_edges = 0, "any"); the pair-layout kernels
+// need exactly kGatSeg.
 inline void gat_geometry(int pass, int dtype, int H, int C, int& light, int& seg) {
   if (fl_ok(dtype, H, C)) {
     light = kFlLightMax;
-    seg = kFlSegEdges;
+    seg = 0;
   } else {
     light = kGatLight;
     seg = kGatSeg;
@@ -123,9 +126,11 @@ inline int read_hdr(const char* who, const int32_t* info, int n, int light, int 
   h.n_seg = info[1];
   h.n_hrow = info[2];
   if (h.n_light + h.n_hrow != n) return set_error(kInvalid, "%s: schedule does not cover %d rows", who, n);
-  if (info[4] != light || info[3] != seg)
-    return set_error(kInvalid, "%s: schedule built with light_max=%d seg_edges=%d; this pass needs %d/%d "
-                     "(cign_gat_schedule_params)", who, info[4], info[3], light, seg);
+  const bool seg_ok = seg == 0 ? (info[3] > 0 && info[3] % kSegRound == 0) : info[3] == seg;
+  if (info[4] != light || !seg_ok)
+    return set_error(kInvalid, "%s: schedule built with light_max=%d seg_edges=%d; this pass needs light_max=%d and "
+                     "seg_edges %s%d (cign_gat_schedule_params)", who, info[4], info[3], light,
+                     seg == 0 ? "a multiple of " : "", seg == 0 ? kSegRound : seg);
   return kOk;
 }
 

@@ -3,14 +3,14 @@
 // a power of two and H*C/W <= 64 chunks. Semantics are those stated at the top
 // of gat_kernels.h (reference collapsed_gat_cuda.cu:34-430).
 //
-// Geometry (shared with the SpMM, schedule.h built with light_max = 64,
-// seg_edges = 512). A group of L = pow2ceil(H*C/W) lanes owns one row; lane q
+// Geometry (shared with the SpMM, schedule.h built with light_max = 64 and a
+// segment length that is a multiple of 256). A group of L = pow2ceil(H*C/W) lanes owns one row; lane q
 // owns chunk q of a feature row, i.e. head hq = q / (C/W) and channel chunk
 // cw = q % (C/W). Rows with degree <= L go one per group (64/L rows per
 // wavefront), rows with degree <= 64 one per wavefront (its groups split the
-// edges), heavier rows are 512-edge segments (one 4-wave workgroup each, two
-// rounds of 256 edges) whose partial results the last workgroup to finish
-// merges in segment order.
+// edges), heavier rows are segments (one 4-wave workgroup each, rounds of 256
+// edges) whose partial results the last workgroup to finish merges in segment
+// order.
 //
 // Every lane gathers, for each edge of its batch, the 16-byte chunk of the
 // source feature row AND the source logit of its own head in the same memory
@@ -60,13 +60,13 @@ constexpr int kFwdU = CIGN_FL_FWD_U;
 constexpr int kRowsU = CIGN_FL_ROWS_U;
 constexpr int kColsU = CIGN_FL_COLS_U;
 
-// Heavy rows are segments of at most kFlSegEdges edges (one workgroup each),
-// processed in rounds of kSegRound = 4 waves x 64 edges. Longer segments mean
-// fewer rows whose partial results need a cross-workgroup merge (an
-// agent-scope release / acquire, which writes back and invalidates the L2 of
-// the XCDs involved) at the cost of more rounds per workgroup.
+// Heavy rows are segments (one workgroup each; any multiple of 256 edges,
+// chosen by the host from the graph size) processed in rounds of kSegRound =
+// 4 waves x 64 edges. Longer segments mean fewer rows whose partial results
+// need a cross-workgroup merge (an agent-scope release / acquire, which
+// writes back and invalidates the L2 of the XCDs involved) at the cost of
+// more rounds per workgroup.
 constexpr int kFlLightMax = 64;
-constexpr int kFlSegEdges = 512;
 constexpr int kSegRound = kWavesPerBlock * kWave;
 
 // grad_bias of the feature layout: the columns kernel's last

@@ -18,12 +18,29 @@ import torch
 from ._lib import load_library
 
 # SpMM schedules: rows with at most LIGHT_MAX edges get one wavefront (or a
-# lane group), heavier rows are cut into SEG_EDGES-edge segments, one
-# 256-thread workgroup each (two rounds of 256 edges). Rows longer than one
-# segment merge their partial sums across workgroups, which costs an
-# agent-scope release/acquire; 512 keeps those rare on power-law graphs.
+# lane group), heavier rows are cut into segments of seg_edges edges, one
+# 256-thread workgroup each, processed in rounds of 256 edges. Rows longer
+# than one segment merge their partial sums across workgroups, which costs an
+# agent-scope release/acquire (an L2 write-back and invalidate on the XCDs
+# involved); long segments instead serialise rounds inside one workgroup.
+# segment_edges_for() balances the two by graph size.
 LIGHT_MAX = 64
-SEG_EDGES = 512
+SEG_EDGES = 512       # smallest segment (small graphs)
+SEG_EDGES_MAX = 16384
+
+
+def segment_edges_for(nnz: int) -> int:
+    """Segment length for a graph of nnz edges: the power of two nearest
+    above nnz / 4096, clamped to [512, 16384]. One segment is then at most
+    ~1/16 of the edges a CU handles, so the longest workgroup stays short
+    against the whole launch, while rows that need a cross-workgroup merge
+    become rare (at 62M edges a 512-edge segment leaves 9,250 merging rows
+    and takes 2.2x longer per hop than 16,384)."""
+    want = max(1, int(nnz) // 4096)
+    seg = SEG_EDGES
+    while seg < want and seg < SEG_EDGES_MAX:
+        seg *= 2
+    return seg
 # Collapsed-GAT pair-layout schedules: one wavefront takes at most 16 edges
 # of a row, segments are 64 edges (16 per wave). The feature-layout forward
 # uses the SpMM geometry; cign_gat_schedule_params says which.
@@ -48,15 +65,18 @@ class RowSchedule:
 
 
 def build_row_schedule(rowptr: torch.Tensor, device=None, light_max: int = LIGHT_MAX,
-                       seg_edges: int = SEG_EDGES) -> RowSchedule:
+                       seg_edges: int | None = None) -> RowSchedule:
     """Builds the schedule of a row pointer (any integer dtype, any device).
-    One host copy of the row pointer is taken (a synchronisation when it lives
-    on the GPU); this happens once per graph, outside timed regions."""
+    seg_edges None picks segment_edges_for(nnz). One host copy of the row
+    pointer is taken (a synchronisation when it lives on the GPU); this
+    happens once per graph, outside timed regions."""
     lib = load_library(require_gpu=False)
     rp = np.ascontiguousarray(rowptr.detach().to("cpu", torch.int64).numpy())
     n_rows = int(rp.shape[0]) - 1
     if n_rows < 0:
         raise ValueError("row pointer must have at least one entry")
+    if seg_edges is None:
+        seg_edges = segment_edges_for(int(rp[-1]) if rp.size else 0)
     nl, ns, nh = C.c_int32(), C.c_int32(), C.c_int32()
     tot = C.c_int64()
     lib.call("cign_row_schedule_size", rp.ctypes.data, n_rows, light_max, seg_edges,
@@ -76,10 +96,10 @@ def build_row_schedule(rowptr: torch.Tensor, device=None, light_max: int = LIGHT
 _CACHE: dict[tuple, tuple[weakref.ref, int, RowSchedule]] = {}
 
 
-def cached_row_schedule(rowptr: torch.Tensor, light_max: int = LIGHT_MAX, seg_edges: int = SEG_EDGES) -> RowSchedule:
+def cached_row_schedule(rowptr: torch.Tensor, light_max: int = LIGHT_MAX, seg_edges: int | None = None) -> RowSchedule:
     """Schedule for a row-pointer tensor, built on first use and reused while
     the tensor is alive and unmodified (checked through its version counter)."""
-    key = (id(rowptr), int(light_max), int(seg_edges))
+    key = (id(rowptr), int(light_max), None if seg_edges is None else int(seg_edges))
     hit = _CACHE.get(key)
     if hit is not None:
         ref, version, sched = hit
@@ -92,9 +112,12 @@ def cached_row_schedule(rowptr: torch.Tensor, light_max: int = LIGHT_MAX, seg_ed
 
 def gat_schedule(rowptr: torch.Tensor, pass_: int, dtype_code: int, heads: int, channels: int) -> RowSchedule:
     """Schedule of a CSR/CSC pointer for a collapsed-GAT pass (0 = forward,
-    1 = backward), with the geometry the library asks for that shape."""
+    1 = backward), with the geometry the library asks for that shape. When
+    the library accepts any multiple of 256 as the segment length (its
+    feature-layout kernels, seg_edges reported as 0 = "any"), the length
+    follows the graph size like the SpMM's."""
     lib = load_library(require_gpu=False)
     light, seg = C.c_int32(), C.c_int32()
     lib.call("cign_gat_schedule_params", int(pass_), int(dtype_code), int(heads), int(channels), C.byref(light),
              C.byref(seg))
-    return cached_row_schedule(rowptr, light.value, seg.value)
+    return cached_row_schedule(rowptr, light.value, seg.value if seg.value > 0 else None)

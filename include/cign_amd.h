@@ -81,7 +81,9 @@ int cign_spmm_bwd3(void* stream, int32_t dtype, int32_t n_rows, int32_t d, const
 /* ---- collapsed GAT ------------------------------------------------------- */
 
 /* Schedule geometry (light_max, seg_edges) to build the schedules of a GAT
- * pass with: pass 0 = forward (CSR), 1 = backward (CSR and CSC). */
+ * pass with: pass 0 = forward (CSR), 1 = backward (CSR and CSC). seg_edges 0
+ * means any multiple of 256 (the feature-layout kernels); the host picks it
+ * from the graph size like the SpMM's. */
 int cign_gat_schedule_params(int32_t pass, int32_t dtype, int32_t heads, int32_t channels, int32_t* light_max,
                              int32_t* seg_edges);
 

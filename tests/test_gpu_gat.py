@@ -231,3 +231,40 @@ def test_argument_errors(c2):
     with pytest.raises(ValueError, match="bias"):
         collapsed_gat_mean_bias_silu(ar[:, :4], ar[:, :4], (rowptr, col), (row, colptr), perm, 0.2,
                                      torch.zeros(n, 4, 4, device="cuda"), None, 0.0)
+
+
+@pytest.mark.parametrize("seg", [256, 1024, 4096])
+@pytest.mark.parametrize("dtype,p", [(torch.float32, 0.0), (torch.float32, 0.2), (torch.bfloat16, 0.0)])
+def test_long_segments_multi_round(seg, dtype, p, monkeypatch):
+    """Hub rows/columns of 2,500-6,000 edges cut into segments of `seg` edges
+    (several 256-edge rounds per workgroup, several workgroups per row)."""
+    import cign_amd.schedule as S
+
+    print(f"gat long segments seg={seg} dtype={dtype} p={p}", flush=True)
+    monkeypatch.setattr(S, "segment_edges_for", lambda nnz: seg)
+    S._CACHE.clear()
+    rng = np.random.default_rng(seg)
+    n, H, C = 7000, 4, 16
+    ei = random_gat_graph(rng, n, avg_deg=4, hubs={3: 6000, 40: 2500})
+    ei = np.concatenate([ei, np.stack([np.full(5000, 11), rng.choice(n, 5000, replace=False)])], 1)
+    r, c, _ = O.coalesce(ei[0], ei[1], n)
+    rowptr, col, row, colptr, perm = _dev_graph(np.stack([r, c]), n)
+    x, ar, ac, b, gy = _inputs(rng, n, H, C, dtype)
+    ext = __import__("cign_amd.collapsed_gat", fromlist=["x"]).ensure_collapsed_gat_loaded()
+    out, pre, emax, esum, mask = ext.forward(ar, ac, rowptr, col, 0.2, x, b, p, 99)
+    gf, gar, gac, gb = ext.backward(0.2, p, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar, ac, pre, gy)
+    rp, cl = rowptr.cpu().numpy().astype(np.int64), col.cpu().numpy().astype(np.int64)
+    keep = mask.cpu().numpy().astype(bool) if p > 0 else None
+    if p > 0:
+        assert np.array_equal(keep.reshape(-1), O.gat_dropout_keep(99, cl.size * H, p))
+    args = (ar.double().cpu().numpy(), ac.double().cpu().numpy(), rp, cl, 0.2, x.double().cpu().numpy(),
+            b.double().cpu().numpy())
+    f = O.collapsed_gat_forward(*args, p=p, keep=keep)
+    gr = O.collapsed_gat_backward(*args, gy.double().cpu().numpy(), p=p, keep=keep)
+    tol = TOL[dtype]
+    assert_close(pre.cpu().numpy(), f["pre"], name="pre", **tol)
+    assert_close(gf.double().cpu().numpy(), gr["grad_feat"], name="grad_feat", **tol)
+    assert_close(gar.cpu().numpy(), gr["grad_attn_row"], name="grad_attn_row", **tol)
+    assert_close(gac.cpu().numpy(), gr["grad_attn_col"], name="grad_attn_col", **tol)
+    assert_close(gb.cpu().numpy(), gr["grad_bias"], name="grad_bias", **tol)
+    S._CACHE.clear()

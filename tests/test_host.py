@@ -187,3 +187,18 @@ def test_gat_edge_index_reads_stay_in_bounds(rng):
                     for k in range(nt):
                         t = eb + el + k * epw
                         assert 0 <= (t if t < ee else eb) < nnz
+
+
+def test_segment_edges_for_graph_size():
+    """Segment length: 512 on small graphs (c2/c3), 16384 at c5 (62.4M edges),
+    a power of two in between that grows with nnz."""
+    from cign_amd.schedule import SEG_EDGES_MAX, segment_edges_for
+
+    assert segment_edges_for(0) == SEG_EDGES == 512
+    assert segment_edges_for(210_592) == 512
+    assert segment_edges_for(62_400_000) == SEG_EDGES_MAX == 16384
+    prev = 0
+    for nnz in np.logspace(3, 9, 40).astype(np.int64):
+        s = segment_edges_for(int(nnz))
+        assert s >= prev and s & (s - 1) == 0 and s % 256 == 0
+        prev = s
