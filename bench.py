@@ -39,9 +39,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 disables)")
-    ap.add_argument("--workload", choices=["layer", "scale"], default="layer",
+    ap.add_argument("--workload", choices=["layer", "scale", "block"], default="layer",
                     help="layer: the headline c2+c3 layer (24,492 nodes); scale: the same layer at c5 size "
-                         "(2.4M nodes, ~62M edges, GAT 4x32 + SpMM D=256, bf16 by default)")
+                         "(2.4M nodes, ~62M edges, GAT 4x32 + SpMM D=256, bf16 by default); block: the full "
+                         "Clifford block forward+backward at the production shape (D=256, 6 GAT heads, hops 1-3) "
+                         "with every component kernel timed against its own roofline (bf16 = selective AMP GEMMs)")
     ap.add_argument("--dtype", choices=["f32", "bf16"], default=None)
     ap.add_argument("--eager", action="store_true",
                     help="launch every step through the Python drop-in API instead of replaying it as a HIP graph")
@@ -227,6 +229,192 @@ def summarize(prof_dir: str, name: str, command: str) -> None:
     print(f"wrote profiles/{name}_kernel_stats.txt, _traffic.txt, _traffic.json")
 
 
+MFMA_PEAK = {"f32": 157.3, "bf16": 2500.0}  # MI355X dense matrix TFLOP/s
+
+
+def run_block(args, torch):
+    """The Clifford block of the reference at its production shape on the c2
+    graph: GraphCliffordBlock(D=256, gat_heads=6, hops (1,2,3), interaction
+    new, weighting old, node hop gate), training mode (dropout 0.28 / GAT
+    0.32), forward + backward. One step = one block forward+backward; value =
+    edges/s. Then each component's kernels are launched back to back (HIP
+    graph of 20 launches) and timed with HIP events against their own
+    roofline: algorithmic bytes / HBM peak, or flops / MFMA peak for the
+    projections (the lower of the two bounds)."""
+    from cign_amd import _lib, _pack, workloads
+    from cign_amd.model_cign import GraphCliffordBlock
+    from cign_amd.multihop_csr_pipeline import MultiHopCSR3GraphOperator
+
+    dev = torch.device("cuda:0")
+    amp = args.dtype == "bf16"
+    lib = _lib.load_library()
+    D, heads, K = 256, 6, 3
+    w = workloads.build(workloads.C2, device=dev)
+    n, E = w.n, w.nnz_gat
+    mh = MultiHopCSR3GraphOperator(w.operator, dense_cols=2 * D)
+    torch.manual_seed(0)
+    block = GraphCliffordBlock(D, order_set=(1, 2, 3), gat_heads=heads, use_selective_amp=amp,
+                               alpha_score_mode="new", interaction_mode="new", alpha_weighting_mode="old",
+                               hop_gate_mode="node").to(dev).train()
+    g = torch.Generator(device="cpu").manual_seed(0)
+    H0 = torch.randn(n, D, generator=g).to(dev).requires_grad_(True)
+    G0 = torch.randn(n, D, generator=g).to(dev)
+
+    def step():
+        out = block(H0, None, mh, w.gat_graph)
+        out.backward(G0)
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    a0, a1 = ev(), ev()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    a0.record()
+    for _ in range(args.steps):
+        step()
+    a1.record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    gpu_ms = a0.elapsed_time(a1) / args.steps
+
+    # ---- components -------------------------------------------------------
+    st = lambda: _lib.stream_ptr(dev)
+    rnd = lambda *s: torch.randn(*s, generator=g).to(dev)
+    x, hh, cc = rnd(n, D), rnd(n, D), rnd(n, D)
+    lnw, lnb = rnd(D), rnd(D)
+    y, y2 = torch.empty(n, D, device=dev), torch.empty(n, D, device=dev)
+    mean, rstd = torch.empty(n, device=dev), torch.empty(n, device=dev)
+    mask = torch.empty(n, D, dtype=torch.uint8, device=dev)
+    gw_, gb_ = torch.empty(D, device=dev), torch.empty(D, device=dev)
+    ws = torch.empty(int(lib.cign_colsum_workspace_bytes(n, D, 2)) + 256, dtype=torch.uint8, device=dev)
+    props = [rnd(n, 2 * D) for _ in range(K)]
+    alpha = torch.softmax(rnd(n, K), 1).contiguous()
+    gate_w, gate_b = rnd(K, 2 * D) * 0.05, rnd(K)
+    gate_ws = torch.empty(int(lib.cign_hop_gate_bwd_workspace_bytes(n, D, K)) + 256, dtype=torch.uint8, device=dev)
+    ga, gH_, gC_ = torch.empty(n, K, device=dev), torch.empty(n, D, device=dev), torch.empty(n, D, device=dev)
+    gwt, gbt = torch.empty(K, 2 * D, device=dev), torch.empty(K, device=dev)
+    gout = rnd(n, 2 * K * D)
+    Wp, bp = rnd(D, 2 * K * D) * 0.02, rnd(D)
+    Wl = rnd(heads * D, D) * 0.05
+    gp_out, yp = torch.empty(n, D, device=dev), torch.empty(n, D, device=dev)
+    xl = torch.empty(n, heads * D, device=dev)
+    lin_ws = torch.empty(int(lib.cign_linear_bwd_workspace_bytes(n, D, 2 * K * D, 1)), dtype=torch.uint8, device=dev)
+    gxp, gWp, gbp = torch.empty(n, 2 * K * D, device=dev), torch.empty(D, 2 * K * D, device=dev), torch.empty(D, device=dev)
+    math = 1 if amp else 0
+    s4 = 4
+    NDb = n * D
+    comps = {
+        # name: (callable, bytes, flops)
+        "dropout_ln_fwd": (lambda: lib.call("cign_dropout_ln_fwd", st(), n, D, x.data_ptr(), lnw.data_ptr(),
+                                            lnb.data_ptr(), 0.28, 1e-5, 7, y.data_ptr(), mean.data_ptr(),
+                                            rstd.data_ptr(), mask.data_ptr()), 9 * NDb + 8 * n, 0),
+        "dropout_ln_bwd": (lambda: lib.call("cign_dropout_ln_bwd", st(), n, D, hh.data_ptr(), x.data_ptr(),
+                                            lnw.data_ptr(), mean.data_ptr(), rstd.data_ptr(), mask.data_ptr(),
+                                            0.28, y2.data_ptr(), gw_.data_ptr(), gb_.data_ptr(), ws.data_ptr(),
+                                            ws.numel()), 13 * NDb + 8 * n, 0),
+        "add_ln_fwd": (lambda: lib.call("cign_add_ln_fwd", st(), n, D, x.data_ptr(), hh.data_ptr(), lnw.data_ptr(),
+                                        lnb.data_ptr(), 1e-5, y.data_ptr(), mean.data_ptr(), rstd.data_ptr()),
+                       12 * NDb + 8 * n, 0),
+        "add_ln_bwd": (lambda: lib.call("cign_add_ln_bwd", st(), n, D, cc.data_ptr(), x.data_ptr(), hh.data_ptr(),
+                                        lnw.data_ptr(), mean.data_ptr(), rstd.data_ptr(), y2.data_ptr(),
+                                        gw_.data_ptr(), gb_.data_ptr(), ws.data_ptr(), ws.numel()),
+                       16 * NDb + 8 * n, 0),
+        "hop_gate_fwd": (lambda: lib.call("cign_hop_gate_fwd", st(), n, D, K, 1, hh.data_ptr(), cc.data_ptr(),
+                                          gate_w.data_ptr(), gate_b.data_ptr(), alpha.data_ptr()),
+                         8 * NDb + 4 * n * K, 0),
+        "hop_gate_bwd": (lambda: lib.call("cign_hop_gate_bwd", st(), n, D, K, 1, hh.data_ptr(), cc.data_ptr(),
+                                          gate_w.data_ptr(), alpha.data_ptr(), ga.data_ptr(), gH_.data_ptr(),
+                                          gC_.data_ptr(), gwt.data_ptr(), gbt.data_ptr(), gate_ws.data_ptr(),
+                                          gate_ws.numel()), 16 * NDb + 8 * n * K, 0),
+        "pack_fwd": (lambda: _pack.forward_list(hh, cc, props, alpha, 1, 0), 8 * NDb + 16 * K * NDb + 4 * n * K, 0),
+        "pack_bwd": (lambda: _pack.backward_list(gout, hh, cc, props, alpha, 1, 0),
+                     24 * K * NDb + 16 * NDb + 8 * n * K, 0),
+        "proj_gamma_fwd": (lambda: lib.call("cign_linear_gamma_fwd", st(), n, D, 2 * K * D, 0, math, gout.data_ptr(),
+                                            Wp.data_ptr(), bp.data_ptr(), hh.data_ptr(), lnw.data_ptr(), 0.28, 9,
+                                            gp_out.data_ptr(), yp.data_ptr(), mask.data_ptr()),
+                           s4 * n * 2 * K * D + 13 * NDb, 2 * n * 2 * K * D * D),
+        "proj_bwd": (lambda: lib.call("cign_linear_bwd", st(), n, D, 2 * K * D, math, hh.data_ptr(), gout.data_ptr(),
+                                      Wp.data_ptr(), gxp.data_ptr(), gWp.data_ptr(), gbp.data_ptr(),
+                                      lin_ws.data_ptr(), lin_ws.numel()),
+                     2 * s4 * n * 2 * K * D + 2 * 4 * NDb, 4 * n * 2 * K * D * D),
+        "gat_lin_fwd": (lambda: lib.call("cign_linear_fwd", st(), n, heads * D, D, 0, math, x.data_ptr(),
+                                         Wl.data_ptr(), None, xl.data_ptr()),
+                        4 * NDb + 4 * n * heads * D, 2 * n * D * heads * D),
+    }
+    R = 20
+    kernels = []
+    for name, (fn, nbytes, flops) in comps.items():
+        fn()
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(R):
+                fn()
+        gr.replay()
+        b0, b1 = ev(), ev()
+        torch.cuda.synchronize()
+        b0.record()
+        M = 5
+        for _ in range(M):
+            gr.replay()
+        b1.record()
+        torch.cuda.synchronize()
+        ms = b0.elapsed_time(b1) / (M * R)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rec = {"kernel": name, "avg_launch_ms": round(ms, 5), "bytes_per_launch": int(nbytes),
+               "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        if flops:
+            tfs = flops / (ms * 1e-3) / 1e12
+            peak = MFMA_PEAK[args.dtype]
+            rec.update({"flops_per_launch": int(flops), "TFLOP_s": round(tfs, 2), "mfma_frac": round(tfs / peak, 4)})
+            # the bound is whichever roofline the ideal time hits first
+            rec["bound"] = "mfma" if flops / (peak * 1e12) > nbytes / (HBM_PEAK_GBS * 1e9) else "hbm"
+        else:
+            rec["bound"] = "hbm"
+        kernels.append(rec)
+        del gr
+
+    dom = max(kernels, key=lambda r: r["avg_launch_ms"])
+    if dom["bound"] == "mfma":
+        roof = {"bound": "mfma", "kernel": dom["kernel"], "achieved": dom["TFLOP_s"], "peak": MFMA_PEAK[args.dtype],
+                "unit": "TFLOP/s", "frac": dom["mfma_frac"], "traffic": None,
+                "avg_launch_ms": dom["avg_launch_ms"], "flops_per_launch": dom["flops_per_launch"]}
+    else:
+        roof = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["GB_s"], "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": dom["hbm_frac"], "traffic": None, "avg_launch_ms": dom["avg_launch_ms"],
+                "bytes_per_launch": dom["bytes_per_launch"]}
+    line = {
+        "metric": "Clifford block fwd+bwd edges/sec (production shape); per-kernel roofline fractions",
+        "value": E * args.steps / elapsed,
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": 1e3 * elapsed / args.steps,
+        "gpu_ms_per_step": round(gpu_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16-gemm" if amp else "f32",
+        "data": "synthetic: seeded Chung-Lu power-law graph (gamma 2.5), N(0,1) features, random-init block",
+        "config": {"workload": "Clifford block (c4/prod): D=256, 6 GAT heads x 256, hops 1-3, interaction new, "
+                               "weighting old, node hop gate, training mode, forward+backward",
+                   "nodes": n, "edges_nnz": E},
+        "kernels": kernels,
+        "roofline": roof,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     if len(sys.argv) > 1 and sys.argv[1] == "--summarize":
         # python bench.py --summarize <rocprof dir> <name> <command text>
@@ -245,6 +433,11 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload == "block":
+        if args.dtype is None:
+            args.dtype = "f32"
+        run_block(args, torch)
+        return
     scale = args.workload == "scale"
     if args.dtype is None:
         args.dtype = "bf16" if scale else "f32"

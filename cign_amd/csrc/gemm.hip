@@ -10,31 +10,32 @@
 //   proj + dropout-gamma-residual          g = x W^T + b, out = h + gamma * drop(g)
 //                                          (model_cign.py:927-933, fused_block_ops
 //                                          gamma residual, keep = 53-bit splitmix64)
-//   backward                               grad_x = grad_y W, grad_W = grad_y^T x,
-//                                          grad_b = sum_n grad_y
+//   backward                               grad_x = grad_y W, grad_W = grad_y^T x
+//                                          (plain GEMMs, rocBLAS), grad_b = sum_n
+//                                          grad_y (chunked column sums)
 //
 // Math: fp32 (v_mfma_f32_16x16x4_f32, exact fp32 products) or bf16
-// (v_mfma_f32_16x16x32_bf16, the autocast path of _local_amp_linear: inputs
-// rounded to bf16 in registers, fp32 accumulation, output rounded to bf16 and
-// returned as fp32). The skinny shapes of the block (N <= 1536 outputs, K <=
-// 1536, M = nodes) are HBM-bound in bf16 and MFMA-bound in fp32.
+// (v_mfma_f32_16x16x32_bf16, the autocast path of _local_amp_linear: operands
+// rounded to bf16, fp32 accumulation, output rounded to bf16 and returned as
+// fp32). The skinny shapes of the block (outputs <= 1536, K <= 1536, M =
+// nodes) are HBM-bound in bf16 and MFMA-bound in fp32.
 //
-// Forward tiling: a workgroup is 4 wavefronts x 32 rows = 128 rows and BN =
-// 16*NF (64 or 128) columns; a wavefront holds 2 x NF 16x16 accumulator tiles and, per K
-// chunk (16 in fp32, 32 in bf16), loads its A fragments (16 bytes per lane per
-// row tile) and its B fragments straight from global memory (W is small and
-// stays in L2), prefetching the next chunk before the current chunk's MFMAs.
-// Fragment layouts (16x16xK MFMA, lane l): A supplies row l%16 and k-slice
-// l/16, B supplies column l%16 and the same k-slice, D holds rows 4*(l/16)+i,
-// i < 4, of column l%16.
-//
-// Backward: grad_x is the same kernel on the transposed weight (one small
-// transpose into the workspace); grad_W and grad_b are split over row chunks
-// of M (fp32 MFMA, deterministic partials summed in chunk order).
+// Forward tiling: a workgroup computes a 128 x BN tile (BN = 64 or 128) with 4
+// wavefronts of 32 rows x BN columns each (2 x BN/16 accumulator tiles of
+// 16x16). Per K step of 32 the A (128 x 32) and B (BN x 32) tiles are staged
+// in LDS in the MFMA operand type (bf16 conversion happens once, at the LDS
+// store), double buffered: the next step's global loads are in flight while
+// the current step's MFMAs run. LDS rows are padded so the 16-byte fragment
+// reads of 16 consecutive rows fall on distinct banks. MFMA fragment layouts
+// (16x16xK, lane l): A supplies row l%16 and k-slice l/16, B supplies column
+// l%16 and the same k-slice, D holds rows 4*(l/16)+i, i < 4, of column l%16.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
-#include "common.h"
+#include <rocblas/rocblas.h>
+
+#include "rowops.h"
 
 namespace cign {
 namespace gemm {
@@ -45,16 +46,16 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 enum Epi : int { kEpiStore = 0, kEpiLogits = 1, kEpiGamma = 2 };
 enum Math : int { kMathF32 = 0, kMathBF16 = 1 };
 
-constexpr int kWaves = 4;
+constexpr int kThreads = 256;
+constexpr int kBM = 128;
+constexpr int kBK = 32;
 constexpr int kRowsPerWave = 32;
-constexpr int kBM = kWaves * kRowsPerWave;
 
 struct GemmArgs {
   int64_t M;
   int N, K;
-  const void* x;      // [M, K] fp32 or bf16 (x_bf16)
-  bool x_bf16;
-  bool vec;           // rows of x and w are 16-byte aligned (vector loads)
+  const void* x;      // [M, K] fp32 or bf16
+  bool vec;           // rows of x and w start 16-byte aligned (vector loads)
   const float* w;     // [N, K] fp32
   const float* bias;  // [N] or null
   float* y;           // [M, N]
@@ -74,106 +75,152 @@ struct GemmArgs {
   uint8_t* mask;
 };
 
-__device__ __forceinline__ float round_bf16(float v) { return to_f32(from_f32<bf16>(v)); }
+// Round to nearest even (gfx950 converts with v_cvt_pk_bf16_f32).
+__device__ __forceinline__ float round_bf16(float v) { return static_cast<float>(static_cast<__bf16>(v)); }
 
-// One lane's share of a K chunk for one 16-wide fragment: VK consecutive k
-// values of one row (zeros past K or past the last row).
+// Operand type in LDS and the row padding of the LDS tiles.
 template <int MATH>
-struct Frag;
+struct Op;
 
 template <>
-struct Frag<kMathF32> {
-  static constexpr int KC = 16;  // k per chunk (4 lanes groups x 4)
-  static constexpr int VK = 4;
-  float4 v;
+struct Op<kMathF32> {
+  using T = float;
+  static constexpr int PAD = 4;  // row stride 36 floats (144 B)
 };
 
 template <>
-struct Frag<kMathBF16> {
-  static constexpr int KC = 32;  // 4 lane groups x 8
-  static constexpr int VK = 8;
-  bf16x8 v;
+struct Op<kMathBF16> {
+  using T = __bf16;
+  static constexpr int PAD = 8;  // row stride 40 bf16 (80 B)
 };
 
-__device__ __forceinline__ __bf16 to_bf16(float f) {
-  const bf16 b = from_f32<bf16>(f);
-  return __builtin_bit_cast(__bf16, b.bits);
-}
-
-// Loads VK values of a row starting at k (row pointer p, row valid, K bound).
 template <int MATH>
-__device__ __forceinline__ void load_frag(const float* p, bool valid, int k, int K, bool vec, Frag<MATH>& f) {
-  constexpr int VK = Frag<MATH>::VK;
-  float t[VK];
-  if (vec && valid && k + VK <= K) {
+constexpr int lds_stride() { return kBK + Op<MATH>::PAD; }
+
+// Loads CNT consecutive values (4 fp32 or 8 bf16) at element k of row p, as
+// fp32; zero past the row or K.
+template <typename TS, int CNT>
+__device__ __forceinline__ void gload(const TS* p, bool valid, int k, int K, bool vec, float (&v)[CNT]) {
+  if constexpr (std::is_same_v<TS, float>) {
+    static_assert(CNT == 4, "fp32 chunks are 4 values");
+    if (vec && valid && k + 4 <= K) {
+      const float4 u = *reinterpret_cast<const float4*>(p + k);
+      v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+    } else {
 #pragma unroll
-    for (int q = 0; q < VK; q += 4) {
-      const float4 u = *reinterpret_cast<const float4*>(p + k + q);
-      t[q] = u.x;
-      t[q + 1] = u.y;
-      t[q + 2] = u.z;
-      t[q + 3] = u.w;
+      for (int q = 0; q < 4; ++q) v[q] = (valid && k + q < K) ? p[k + q] : 0.0f;
     }
   } else {
+    static_assert(CNT == 8, "bf16 chunks are 8 values");
+    if (vec && valid && k + 8 <= K) {
+      const uint4 u = *reinterpret_cast<const uint4*>(p + k);
+      const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-    for (int q = 0; q < VK; ++q) t[q] = (valid && k + q < K) ? p[k + q] : 0.0f;
-  }
-  if constexpr (MATH == kMathF32) {
-    f.v = make_float4(t[0], t[1], t[2], t[3]);
-  } else {
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(w4[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w4[i] & 0xffff0000u);
+      }
+    } else {
 #pragma unroll
-    for (int q = 0; q < VK; ++q) f.v[q] = to_bf16(t[q]);
-  }
-}
-
-template <int MATH>
-__device__ __forceinline__ void load_frag(const bf16* p, bool valid, int k, int K, bool vec, Frag<MATH>& f) {
-  static_assert(MATH == kMathBF16, "bf16 inputs feed the bf16 MFMA");
-  if (vec && valid && k + 8 <= K) {
-    const uint4 u = *reinterpret_cast<const uint4*>(p + k);
-    f.v = __builtin_bit_cast(bf16x8, u);
-  } else {
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint16_t b = (valid && k + q < K) ? p[k + q].bits : 0;
-      f.v[q] = __builtin_bit_cast(__bf16, b);
+      for (int q = 0; q < 8; ++q) v[q] = (valid && k + q < K) ? to_f32(p[k + q]) : 0.0f;
     }
   }
 }
 
-template <int MATH>
-__device__ __forceinline__ void mma(f32x4& acc, const Frag<MATH>& a, const Frag<MATH>& b) {
-  if constexpr (MATH == kMathF32) {
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v.x, b.v.x, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v.y, b.v.y, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v.z, b.v.z, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v.w, b.v.w, acc, 0, 0, 0);
-  } else {
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
-  }
-}
+// The tile loads of one K step held in registers between the global load
+// and the LDS store. A: 128 x 32 of x; B: BN x 32 of w (fp32).
+template <typename TX, int MATH, int BN>
+struct StageRegs {
+  static constexpr int XC = std::is_same_v<TX, float> ? 4 : 8;  // values per x chunk (16 bytes)
+  static constexpr int A_CHUNKS = kBM * kBK / XC / kThreads;   // per thread
+  static constexpr int B_CHUNKS = BN * kBK / 4 / kThreads;
+  float a[A_CHUNKS][XC];
+  float b[B_CHUNKS][4];
 
-// The fragments of one K chunk for a wavefront: 2 row tiles x NF column tiles.
-template <typename TX, int MATH, int NF>
-struct ChunkFrags {
-  Frag<MATH> a[2];
-  Frag<MATH> b[NF];
-
-  __device__ __forceinline__ void load(const GemmArgs& g, const TX* x, int64_t row0, int n0, int k0, int lane) {
-    constexpr int VK = Frag<MATH>::VK;
-    const int kk = k0 + (lane >> 4) * VK;
+  __device__ __forceinline__ void load(const GemmArgs& g, const TX* x, int64_t m0, int n0, int k0) {
+    constexpr int ACPR = kBK / XC;  // chunks per A row
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int64_t row = row0 + 16 * r + (lane & 15);
-      load_frag<MATH>(x + row * g.K, row < g.M, kk, g.K, g.vec, a[r]);
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      const int r = id / ACPR, c = id % ACPR;
+      const int64_t m = m0 + r;
+      gload<TX, XC>(x + m * g.K, m < g.M, k0 + c * XC, g.K, g.vec, a[i]);
     }
+    constexpr int BCPR = kBK / 4;
 #pragma unroll
-    for (int f = 0; f < NF; ++f) {
-      const int n = n0 + 16 * f + (lane & 15);
-      load_frag<MATH>(g.w + static_cast<int64_t>(n) * g.K, n < g.N, kk, g.K, g.vec, b[f]);
+    for (int i = 0; i < B_CHUNKS; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      const int r = id / BCPR, c = id % BCPR;
+      const int n = n0 + r;
+      gload<float, 4>(g.w + static_cast<int64_t>(n) * g.K, n < g.N, k0 + c * 4, g.K, g.vec, b[i]);
+    }
+  }
+
+  __device__ __forceinline__ void store(typename Op<MATH>::T* As, typename Op<MATH>::T* Bs) const {
+    using T = typename Op<MATH>::T;
+    constexpr int S = lds_stride<MATH>();
+    constexpr int ACPR = kBK / XC;
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      const int r = id / ACPR, c = id % ACPR;
+      T* d = As + r * S + c * XC;
+#pragma unroll
+      for (int q = 0; q < XC; ++q) d[q] = static_cast<T>(a[i][q]);
+    }
+    constexpr int BCPR = kBK / 4;
+#pragma unroll
+    for (int i = 0; i < B_CHUNKS; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      const int r = id / BCPR, c = id % BCPR;
+      T* d = Bs + r * S + c * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) d[q] = static_cast<T>(b[i][q]);
     }
   }
 };
+
+// MFMAs of one K step on the LDS tiles: the wave's 2 row tiles x TN column
+// tiles.
+template <int MATH, int TN>
+__device__ __forceinline__ void mma_step(const typename Op<MATH>::T* As, const typename Op<MATH>::T* Bs, int wave,
+                                         int lane, f32x4 (&acc)[2][TN]) {
+  constexpr int S = lds_stride<MATH>();
+  const int rl = lane & 15, ks = lane >> 4;
+  if constexpr (MATH == kMathBF16) {
+    bf16x8 a[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      a[r] = *reinterpret_cast<const bf16x8*>(As + (wave * kRowsPerWave + 16 * r + rl) * S + ks * 8);
+#pragma unroll
+    for (int f = 0; f < TN; ++f) {
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(Bs + (16 * f + rl) * S + ks * 8);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[r], b, acc[r][f], 0, 0, 0);
+    }
+  } else {
+    // Two 16-k halves; within a half, lane group ks supplies k = 4*ks .. +3
+    // to four 16x16x4 MFMAs (the k order inside a sum is immaterial).
+#pragma unroll
+    for (int hk = 0; hk < kBK; hk += 16) {
+      float4 a[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+        a[r] = *reinterpret_cast<const float4*>(As + (wave * kRowsPerWave + 16 * r + rl) * S + hk + ks * 4);
+#pragma unroll
+      for (int f = 0; f < TN; ++f) {
+        const float4 b = *reinterpret_cast<const float4*>(Bs + (16 * f + rl) * S + hk + ks * 4);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r].x, b.x, acc[r][f], 0, 0, 0);
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r].y, b.y, acc[r][f], 0, 0, 0);
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r].z, b.z, acc[r][f], 0, 0, 0);
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r].w, b.w, acc[r][f], 0, 0, 0);
+        }
+      }
+    }
+  }
+}
 
 // Block index -> (row tile, column tile). Workgroups are dealt to the 8 XCDs
 // round robin; consecutive blocks of one XCD take the column tiles of one row
@@ -189,41 +236,48 @@ __device__ __forceinline__ void tile_of(int nrt, int nct, int& rt, int& ct) {
   ct = v % nct;
 }
 
-template <typename TX, int MATH, int NF, int EPI>
-__global__ __launch_bounds__(kWaves * kWave) void gemm_nt_kernel(GemmArgs g, int nrt, int nct) {
+template <typename TX, int MATH, int BN, int EPI>
+__global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs g, int nrt, int nct) {
+  using T = typename Op<MATH>::T;
+  constexpr int S = lds_stride<MATH>();
+  constexpr int TN = BN / 16;
+  __shared__ __align__(16) T As[2][kBM * S];
+  __shared__ __align__(16) T Bs[2][BN * S];
   const int lane = lane_id();
   const int wave = wave_id();
   int rt, ct;
   tile_of(nrt, nct, rt, ct);
-  const int64_t row0 = static_cast<int64_t>(rt) * kBM + wave * kRowsPerWave;
-  const int n0 = ct * (16 * NF);
+  const int64_t m0 = static_cast<int64_t>(rt) * kBM;
+  const int n0 = ct * BN;
   const TX* x = static_cast<const TX*>(g.x);
-  constexpr int KC = Frag<MATH>::KC;
 
-  f32x4 acc[2][NF];
+  f32x4 acc[2][TN];
 #pragma unroll
   for (int r = 0; r < 2; ++r)
 #pragma unroll
-    for (int f = 0; f < NF; ++f) acc[r][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int f = 0; f < TN; ++f) acc[r][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  ChunkFrags<TX, MATH, NF> cur;
-  cur.load(g, x, row0, n0, 0, lane);
-  for (int k0 = 0; k0 < g.K; k0 += KC) {
-    ChunkFrags<TX, MATH, NF> nxt;
-    if (k0 + KC < g.K) nxt.load(g, x, row0, n0, k0 + KC, lane);
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int f = 0; f < NF; ++f) mma<MATH>(acc[r][f], cur.a[r], cur.b[f]);
-    cur = nxt;
+  StageRegs<TX, MATH, BN> regs;
+  regs.load(g, x, m0, n0, 0);
+  regs.store(As[0], Bs[0]);
+  __syncthreads();
+  int buf = 0;
+  for (int k0 = 0; k0 < g.K; k0 += kBK) {
+    const bool more = k0 + kBK < g.K;
+    if (more) regs.load(g, x, m0, n0, k0 + kBK);
+    mma_step<MATH, TN>(As[buf], Bs[buf], wave, lane, acc);
+    if (more) regs.store(As[buf ^ 1], Bs[buf ^ 1]);
+    __syncthreads();
+    buf ^= 1;
   }
 
-  // Epilogue: lane holds rows row0 + 16r + 4*(lane/16) + i of column
+  // Epilogue: lane holds rows m0 + 32*wave + 16r + 4*(lane/16) + i of column
   // n0 + 16f + lane%16.
   const int cl = lane & 15;
   const int rq = (lane >> 4) * 4;
+  const int64_t row0 = m0 + wave * kRowsPerWave;
 #pragma unroll
-  for (int f = 0; f < NF; ++f) {
+  for (int f = 0; f < TN; ++f) {
     const int n = n0 + 16 * f + cl;
     const bool nv = n < g.N;
     const float bv = (g.bias && nv) ? g.bias[n] : 0.0f;
@@ -252,7 +306,7 @@ __global__ __launch_bounds__(kWaves * kWave) void gemm_nt_kernel(GemmArgs g, int
     // column lanes.
     const int H = g.N / g.C;
     const int fph = g.C / 16;
-    for (int h0 = 0; h0 < NF; h0 += fph) {
+    for (int h0 = 0; h0 < TN; h0 += fph) {
       const int head = (n0 + 16 * h0) / g.C;
       float ss[2][4], sd[2][4];
 #pragma unroll
@@ -260,7 +314,7 @@ __global__ __launch_bounds__(kWaves * kWave) void gemm_nt_kernel(GemmArgs g, int
 #pragma unroll
         for (int i = 0; i < 4; ++i) ss[r][i] = sd[r][i] = 0.0f;
 #pragma unroll
-      for (int f = 0; f < NF; ++f) {
+      for (int f = 0; f < TN; ++f) {
         if (f < h0 || f >= h0 + fph) continue;
         const int n = n0 + 16 * f + cl;
         const int c = n - head * g.C;
@@ -300,100 +354,40 @@ __global__ __launch_bounds__(kWaves * kWave) void gemm_nt_kernel(GemmArgs g, int
 }
 
 // ---------------------------------------------------------------------------
-// grad_W / grad_b: partial[c] = grad_y[rows of chunk c]^T x[rows of chunk c].
-// A workgroup computes a 64 (outputs) x 64 (inputs) tile over one row chunk:
-// wave w owns outputs [16w, 16w + 16) and the tile's 4 input fragments. Per
-// group of 16 rows, lane l reads grad_y[m][o] and x[m][k] for rows
-// m = m0 + 4j + l/16 (j < 4): column slices of 16 consecutive values, fed to
-// 16x16x4 fp32 MFMAs whose k dimension is the row index.
+// Backward helpers
 // ---------------------------------------------------------------------------
-struct WgradArgs {
-  int64_t M;
-  int N, K;
-  int64_t chunk;        // rows per chunk
-  const float* gy;      // [M, N]
-  const float* x;       // [M, K]
-  float* part_w;        // [chunks, N, K]
-  float* part_b;        // [chunks, N] or null
-};
-
-__global__ __launch_bounds__(kWaves * kWave) void wgrad_kernel(WgradArgs g, int nkt) {
-  const int lane = lane_id();
-  const int wave = wave_id();
-  const int ot = blockIdx.x / nkt, kt = blockIdx.x % nkt;
-  const int c = blockIdx.y;
-  const int o = ot * 64 + wave * 16 + (lane & 15);
-  const int kbase = kt * 64;
-  const int64_t mb = c * g.chunk, me = min(g.M, mb + g.chunk);
-  f32x4 acc[4];
-#pragma unroll
-  for (int f = 0; f < 4; ++f) acc[f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  float bsum = 0.0f;
-  const bool ov = o < g.N;
-  for (int64_t m0 = mb; m0 < me; m0 += 16) {
-    float av[4], bvv[4][4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t m = m0 + 4 * j + (lane >> 4);
-      const bool mv = m < me;
-      av[j] = (mv && ov) ? g.gy[m * g.N + o] : 0.0f;
-#pragma unroll
-      for (int f = 0; f < 4; ++f) {
-        const int k = kbase + 16 * f + (lane & 15);
-        bvv[f][j] = (mv && k < g.K) ? g.x[m * g.K + k] : 0.0f;
-      }
+// part[c][n] = sum of grad_y rows of chunk c (a workgroup: 64 columns x 4 row
+// slices, four accumulators per thread, slices combined in order).
+__global__ __launch_bounds__(kThreads) void bias_grad_kernel(const float* gy, int64_t M, int N, int64_t chunk,
+                                                             float* part) {
+  __shared__ float red[kThreads];
+  const int t = threadIdx.x;
+  const int n = blockIdx.x * 64 + (t & 63);
+  const int s = t >> 6;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * chunk;
+  const int64_t r1 = r0 + chunk < M ? r0 + chunk : M;
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  if (n < N) {
+    int64_t r = r0 + s;
+    for (; r + 12 < r1; r += 16) {
+      a0 += gy[r * N + n];
+      a1 += gy[(r + 4) * N + n];
+      a2 += gy[(r + 8) * N + n];
+      a3 += gy[(r + 12) * N + n];
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      bsum += av[j];
-#pragma unroll
-      for (int f = 0; f < 4; ++f) acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], bvv[f][j], acc[f], 0, 0, 0);
-    }
+    for (; r < r1; r += 4) a0 += gy[r * N + n];
   }
-  // acc[f] lane l: rows (outputs) 4*(l/16)+i of this wave's 16, column
-  // (input) kbase + 16f + l%16.
-  const int rq = (lane >> 4) * 4;
-  float* pw = g.part_w + static_cast<int64_t>(c) * g.N * g.K;
-#pragma unroll
-  for (int f = 0; f < 4; ++f) {
-    const int k = kbase + 16 * f + (lane & 15);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int oo = ot * 64 + wave * 16 + rq + i;
-      if (oo < g.N && k < g.K) pw[static_cast<int64_t>(oo) * g.K + k] = acc[f][i];
-    }
-  }
-  if (g.part_b && kt == 0) {
-    bsum += shfl_xor(bsum, 16);
-    bsum += shfl_xor(bsum, 32);
-    if (lane < 16 && ov) g.part_b[static_cast<int64_t>(c) * g.N + o] = bsum;
-  }
-}
-
-// out[i] = sum_c part[c * len + i], c = 0 .. chunks-1 (in order).
-__global__ void sum_chunks_kernel(const float* part, int chunks, int64_t len, float* out) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < len;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    float t = 0.0f;
-    for (int c = 0; c < chunks; ++c) t += part[c * len + i];
-    out[i] = t;
-  }
-}
-
-// wt[k, n] = w[n, k]
-__global__ void transpose_kernel(const float* w, int N, int K, float* wt) {
-  __shared__ float tile[32][33];
-  const int k0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
-  const int tx = threadIdx.x % 32, ty = threadIdx.x / 32;
-  for (int j = ty; j < 32; j += 8) {
-    const int n = n0 + j, k = k0 + tx;
-    tile[j][tx] = (n < N && k < K) ? w[static_cast<int64_t>(n) * K + k] : 0.0f;
-  }
+  red[t] = (a0 + a1) + (a2 + a3);
   __syncthreads();
-  for (int j = ty; j < 32; j += 8) {
-    const int k = k0 + j, n = n0 + tx;
-    if (k < K && n < N) wt[static_cast<int64_t>(k) * N + n] = tile[tx][j];
-  }
+  if (s == 0 && n < N)
+    part[static_cast<int64_t>(blockIdx.y) * N + n] = red[t] + red[t + 64] + red[t + 128] + red[t + 192];
+}
+
+// dst[i] = bf16(src[i])
+__global__ void to_bf16_kernel(const float* src, int64_t n, __bf16* dst) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    dst[i] = static_cast<__bf16>(src[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -401,42 +395,43 @@ __global__ void transpose_kernel(const float* w, int N, int K, float* wt) {
 // ---------------------------------------------------------------------------
 inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
-// Column tile of NF 16-wide fragments: 4 (64 columns) or 8 (128 columns;
-// wider tiles leave one wavefront per SIMD). For the logits epilogue the tile
-// must hold whole heads.
-inline int pick_nf(int N, int C) {
-  int nf = N <= 64 ? 4 : 8;
+// Column tile: 64 for N <= 64, else 128. For the logits epilogue the tile
+// must hold whole heads of 16..128 columns.
+inline int pick_bn(int N, int C) {
+  int bn = N <= 64 ? 64 : 128;
   if (C > 0) {
-    while (nf < 8 && (16 * nf) % C != 0) nf *= 2;
-    if ((16 * nf) % C != 0) return 0;
+    if (C % 16 != 0 || C > 128) return 0;
+    if (bn % C != 0) bn = 128;
+    if (bn % C != 0) return 0;
   }
-  return nf;
+  return bn;
 }
 
 template <typename TX, int MATH, int EPI>
-int launch_nt(hipStream_t st, const GemmArgs& g, int nf) {
+int launch_nt(hipStream_t st, const GemmArgs& g, int bn) {
   const int nrt = static_cast<int>((g.M + kBM - 1) / kBM);
-  const int nct = (g.N + 16 * nf - 1) / (16 * nf);
+  const int nct = (g.N + bn - 1) / bn;
   const int64_t blocks = static_cast<int64_t>(nrt) * nct;
   if (blocks == 0) return kOk;
   if (blocks > 0x7fffffff) return set_error(kInvalid, "cign linear: too many tiles");
-#define CIGN_NT(NF) \
-  hipLaunchKernelGGL((gemm_nt_kernel<TX, MATH, NF, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kWaves * kWave), 0, st, g, nrt, nct)
-  if (nf == 4) CIGN_NT(4);
-  else CIGN_NT(8);
-#undef CIGN_NT
+  if (bn == 64)
+    hipLaunchKernelGGL((gemm_nt_kernel<TX, MATH, 64, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                       st, g, nrt, nct);
+  else
+    hipLaunchKernelGGL((gemm_nt_kernel<TX, MATH, 128, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                       st, g, nrt, nct);
   return check_launch("cign linear");
 }
 
 template <int EPI>
-int dispatch_nt(hipStream_t st, const GemmArgs& g, int x_dtype, int math, int nf) {
+int dispatch_nt(hipStream_t st, const GemmArgs& g, int x_dtype, int math, int bn) {
   if (x_dtype == kBF16) {
     if (math != kMathBF16) return set_error(kInvalid, "cign linear: bfloat16 inputs need math=1 (bf16 MFMA)");
-    return launch_nt<bf16, kMathBF16, EPI>(st, g, nf);
+    return launch_nt<bf16, kMathBF16, EPI>(st, g, bn);
   }
   if (x_dtype != kF32) return set_error(kInvalid, "cign linear: unsupported x dtype %d", x_dtype);
-  if (math == kMathF32) return launch_nt<float, kMathF32, EPI>(st, g, nf);
-  if (math == kMathBF16) return launch_nt<float, kMathBF16, EPI>(st, g, nf);
+  if (math == kMathF32) return launch_nt<float, kMathF32, EPI>(st, g, bn);
+  if (math == kMathBF16) return launch_nt<float, kMathBF16, EPI>(st, g, bn);
   return set_error(kInvalid, "cign linear: math must be 0 (fp32) or 1 (bf16)");
 }
 
@@ -453,28 +448,51 @@ inline bool rows_aligned(const void* x, int x_dtype, const float* w, int K) {
   return aligned16(x) && aligned16(w) && xrow % 16 == 0 && (K * 4) % 16 == 0;
 }
 
+// One rocBLAS handle per device, created on first use.
+rocblas_handle blas_handle(int& rc) {
+  static std::mutex mu;
+  static rocblas_handle handles[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    rc = set_error(kHipError, "cign_linear_bwd: no current HIP device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!handles[dev] && rocblas_create_handle(&handles[dev]) != rocblas_status_success) {
+    handles[dev] = nullptr;
+    rc = set_error(kHipError, "cign_linear_bwd: rocblas_create_handle failed");
+    return nullptr;
+  }
+  rc = kOk;
+  return handles[dev];
+}
+
 // Workspace layout of cign_linear_bwd.
 struct BwdWs {
   int chunks;
-  int64_t chunk, wt, part_w, part_b, total;
+  int64_t chunk, part_b, gy16, x16, w16, total;
 };
 
-inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias) {
+inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias, int math) {
   BwdWs L;
-  const int tiles = ((N + 63) / 64) * ((K + 63) / 64);
-  // about 4 x 256 workgroups, chunks of at least 256 rows
-  int chunks = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>((1024 + tiles - 1) / tiles, (M + 255) / 256)));
-  chunks = std::min(chunks, 256);
-  L.chunks = chunks;
-  L.chunk = (M + chunks - 1) / chunks;
-  L.chunk = ((L.chunk + 15) / 16) * 16;
+  int64_t chunks = std::max<int64_t>(1, std::min<int64_t>(1024, (M + 63) / 64));
+  L.chunk = std::max<int64_t>(1, (M + chunks - 1) / chunks);
+  chunks = M > 0 ? (M + L.chunk - 1) / L.chunk : 1;
+  L.chunks = static_cast<int>(chunks);
   auto al = [](int64_t v) { return (v + 255) & ~int64_t(255); };
   int64_t off = 0;
-  L.wt = off; off = al(off + 4LL * N * K);
-  L.part_w = off; off = al(off + 4LL * chunks * N * K);
   L.part_b = off; off = al(off + (bias ? 4LL * chunks * N : 0));
+  const bool b16 = math == kMathBF16;
+  L.gy16 = off; off = al(off + (b16 ? 2LL * M * N : 0));
+  L.x16 = off; off = al(off + (b16 ? 2LL * M * K : 0));
+  L.w16 = off; off = al(off + (b16 ? 2LL * N * K : 0));
   L.total = off;
   return L;
+}
+
+inline int blas_check(rocblas_status s, const char* what) {
+  return s == rocblas_status_success ? kOk
+                                     : set_error(kHipError, "cign_linear_bwd: %s failed (rocblas %d)", what, static_cast<int>(s));
 }
 
 }  // namespace gemm
@@ -491,10 +509,10 @@ int cign_linear_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t x_dty
   if (rc) return rc;
   if (M == 0) return kOk;
   GemmArgs g{};
-  g.M = M; g.N = N; g.K = K; g.x = x; g.x_bf16 = x_dtype == kBF16; g.w = w; g.bias = bias; g.y = y;
+  g.M = M; g.N = N; g.K = K; g.x = x; g.w = w; g.bias = bias; g.y = y;
   g.vec = rows_aligned(x, x_dtype, w, K);
   g.round_bf16 = math == kMathBF16;
-  return dispatch_nt<kEpiStore>(static_cast<hipStream_t>(stream), g, x_dtype, math, pick_nf(N, 0));
+  return dispatch_nt<kEpiStore>(static_cast<hipStream_t>(stream), g, x_dtype, math, pick_bn(N, 0));
 }
 
 int cign_linear_logits_fwd(void* stream, int64_t M, int32_t heads, int32_t channels, int32_t K, int32_t x_dtype,
@@ -505,17 +523,17 @@ int cign_linear_logits_fwd(void* stream, int64_t M, int32_t heads, int32_t chann
   if (rc) return rc;
   if (!att_src || !att_dst || (M > 0 && (!alpha_src || !alpha_dst)))
     return set_error(kInvalid, "cign_linear_logits_fwd: null pointer");
-  const int nf = channels % 16 == 0 ? pick_nf(N, channels) : 0;
-  if (nf == 0)
+  const int bn = pick_bn(N, channels);
+  if (bn == 0)
     return set_error(kInvalid, "cign_linear_logits_fwd: channels=%d must be 16, 32, 64 or 128 (use cign_linear_fwd + "
                      "cign_attn_logits_fwd)", channels);
   if (M == 0) return kOk;
   GemmArgs g{};
-  g.M = M; g.N = N; g.K = K; g.x = x; g.x_bf16 = x_dtype == kBF16; g.w = w; g.y = y;
+  g.M = M; g.N = N; g.K = K; g.x = x; g.w = w; g.y = y;
   g.vec = rows_aligned(x, x_dtype, w, K);
   g.round_bf16 = math == kMathBF16;
   g.C = channels; g.att_src = att_src; g.att_dst = att_dst; g.alpha_src = alpha_src; g.alpha_dst = alpha_dst;
-  return dispatch_nt<kEpiLogits>(static_cast<hipStream_t>(stream), g, x_dtype, math, nf);
+  return dispatch_nt<kEpiLogits>(static_cast<hipStream_t>(stream), g, x_dtype, math, bn);
 }
 
 int cign_linear_gamma_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t x_dtype, int32_t math,
@@ -528,15 +546,16 @@ int cign_linear_gamma_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t
     return set_error(kInvalid, "cign_linear_gamma_fwd: dropout_p must be in [0,1)");
   if (M == 0) return kOk;
   GemmArgs g{};
-  g.M = M; g.N = N; g.K = K; g.x = x; g.x_bf16 = x_dtype == kBF16; g.w = w; g.bias = bias; g.y = g_out;
+  g.M = M; g.N = N; g.K = K; g.x = x; g.w = w; g.bias = bias; g.y = g_out;
   g.vec = rows_aligned(x, x_dtype, w, K);
   g.round_bf16 = math == kMathBF16;
   g.h = h; g.gamma = gamma; g.p = dropout_p; g.seed = seed; g.out = y; g.mask = mask;
-  return dispatch_nt<kEpiGamma>(static_cast<hipStream_t>(stream), g, x_dtype, math, pick_nf(N, 0));
+  return dispatch_nt<kEpiGamma>(static_cast<hipStream_t>(stream), g, x_dtype, math, pick_bn(N, 0));
 }
 
 int64_t cign_linear_bwd_workspace_bytes(int64_t M, int32_t N, int32_t K, int32_t with_bias) {
-  return bwd_ws(M, N, K, with_bias != 0).total;
+  // sized for either math (the bf16 operand copies are used with math = 1)
+  return bwd_ws(M, N, K, with_bias != 0, kMathBF16).total;
 }
 
 int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math, const float* grad_y, const float* x,
@@ -545,48 +564,64 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
   if (M < 0 || N <= 0 || K <= 0) return set_error(kInvalid, "cign_linear_bwd: bad sizes");
   if (!w || !grad_w || (M > 0 && (!grad_y || !x))) return set_error(kInvalid, "cign_linear_bwd: null pointer");
   if (math != kMathF32 && math != kMathBF16) return set_error(kInvalid, "cign_linear_bwd: math must be 0 or 1");
-  const BwdWs L = bwd_ws(M, N, K, grad_b != nullptr);
-  if (!workspace || workspace_bytes < L.total)
+  if (M > 0x7fffffff) return set_error(kInvalid, "cign_linear_bwd: M too large");
+  const BwdWs L = bwd_ws(M, N, K, grad_b != nullptr, math);
+  if (workspace_bytes < L.total || (L.total > 0 && !workspace))
     return set_error(kInvalid, "cign_linear_bwd: workspace too small (%lld < %lld)",
                      static_cast<long long>(workspace_bytes), static_cast<long long>(L.total));
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  float* wt = reinterpret_cast<float*>(ws + L.wt);
-  float* part_w = reinterpret_cast<float*>(ws + L.part_w);
-  float* part_b = grad_b ? reinterpret_cast<float*>(ws + L.part_b) : nullptr;
-  // grad_x = grad_y W : the forward kernel on W^T ([K, N]).
-  if (grad_x && M > 0) {
-    hipLaunchKernelGGL(transpose_kernel, dim3((K + 31) / 32, (N + 31) / 32), dim3(256), 0, st, w, N, K, wt);
-    int rc = check_launch("cign_linear_bwd (transpose)");
-    if (rc) return rc;
-    GemmArgs g{};
-    g.M = M; g.N = K; g.K = N; g.x = grad_y; g.w = wt; g.y = grad_x;
-    g.vec = rows_aligned(grad_y, kF32, wt, N);
-    g.round_bf16 = false;
-    rc = dispatch_nt<kEpiStore>(st, g, kF32, math, pick_nf(K, 0));
+  int rc;
+  if (M == 0) return rowops::zero_outputs(st, grad_w, N * K, grad_b, grad_b ? N : 0, "cign_linear_bwd");
+  rocblas_handle hdl = blas_handle(rc);
+  if (!hdl) return rc;
+  if ((rc = blas_check(rocblas_set_stream(hdl, st), "rocblas_set_stream"))) return rc;
+  const float one = 1.0f, zero = 0.0f;
+  const void *gy_op = grad_y, *x_op = x, *w_op = w;
+  rocblas_datatype in_t = rocblas_datatype_f32_r;
+  if (math == kMathBF16) {
+    // autocast semantics: the backward GEMMs read bf16 operands
+    __bf16* gy16 = reinterpret_cast<__bf16*>(ws + L.gy16);
+    __bf16* x16 = reinterpret_cast<__bf16*>(ws + L.x16);
+    __bf16* w16 = reinterpret_cast<__bf16*>(ws + L.w16);
+    auto conv = [&](const float* s, int64_t n, __bf16* d) {
+      const int64_t gb = std::min<int64_t>((n + 255) / 256, 8192);
+      hipLaunchKernelGGL(to_bf16_kernel, dim3(static_cast<unsigned>(gb)), dim3(256), 0, st, s, n, d);
+      return check_launch("cign_linear_bwd (bf16 operands)");
+    };
+    if ((rc = conv(grad_y, M * N, gy16)) || (rc = conv(x, M * K, x16)) ||
+        (rc = conv(w, static_cast<int64_t>(N) * K, w16)))
+      return rc;
+    gy_op = gy16;
+    x_op = x16;
+    w_op = w16;
+    in_t = rocblas_datatype_bf16_r;
+  }
+  const int m32 = static_cast<int>(M);
+  // Row-major C = A B is column-major C^T = B^T A^T.
+  // grad_x [M,K] = grad_y [M,N] W [N,K]:  (K x M) = W_cm (K x N) * gy_cm (N x M)
+  if (grad_x) {
+    rc = blas_check(rocblas_gemm_ex(hdl, rocblas_operation_none, rocblas_operation_none, K, m32, N, &one, w_op, in_t, K,
+                                    gy_op, in_t, N, &zero, grad_x, rocblas_datatype_f32_r, K, grad_x,
+                                    rocblas_datatype_f32_r, K, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0,
+                                    0),
+                    "grad_x gemm");
     if (rc) return rc;
   }
-  // grad_W, grad_b: split over row chunks, partials summed in chunk order.
-  WgradArgs a{};
-  a.M = M; a.N = N; a.K = K; a.chunk = L.chunk; a.gy = grad_y; a.x = x; a.part_w = part_w; a.part_b = part_b;
-  const int nkt = (K + 63) / 64;
-  const int chunks = M > 0 ? static_cast<int>((M + L.chunk - 1) / L.chunk) : 0;
-  if (chunks > 0) {
-    hipLaunchKernelGGL(wgrad_kernel, dim3(((N + 63) / 64) * nkt, chunks), dim3(kWaves * kWave), 0, st, a, nkt);
-    int rc = check_launch("cign_linear_bwd (grad_w)");
-    if (rc) return rc;
-  }
-  const int64_t len = static_cast<int64_t>(N) * K;
-  hipLaunchKernelGGL(sum_chunks_kernel, dim3(static_cast<unsigned>(std::min<int64_t>((len + 255) / 256, 4096))),
-                     dim3(256), 0, st, part_w, chunks, len, grad_w);
-  int rc = check_launch("cign_linear_bwd (sum)");
+  // grad_W [N,K] = grad_y^T [N,M] x [M,K]:  (K x N) = x_cm (K x M) * gy_cm^T (M x N)
+  rc = blas_check(rocblas_gemm_ex(hdl, rocblas_operation_none, rocblas_operation_transpose, K, N, m32, &one, x_op, in_t,
+                                  K, gy_op, in_t, N, &zero, grad_w, rocblas_datatype_f32_r, K, grad_w,
+                                  rocblas_datatype_f32_r, K, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0),
+                  "grad_w gemm");
   if (rc) return rc;
   if (grad_b) {
-    hipLaunchKernelGGL(sum_chunks_kernel, dim3((N + 255) / 256), dim3(256), 0, st, part_b, chunks,
-                       static_cast<int64_t>(N), grad_b);
-    rc = check_launch("cign_linear_bwd (bias)");
+    float* part = reinterpret_cast<float*>(ws + L.part_b);
+    hipLaunchKernelGGL(bias_grad_kernel, dim3((N + 63) / 64, L.chunks), dim3(kThreads), 0, st, grad_y, M, N, L.chunk,
+                       part);
+    if ((rc = check_launch("cign_linear_bwd (bias partials)"))) return rc;
+    return rowops::launch_colsum(st, part, L.chunks, N, 1, grad_b, nullptr, "cign_linear_bwd (bias)");
   }
-  return rc;
+  return kOk;
 }
 
 }  // extern "C"

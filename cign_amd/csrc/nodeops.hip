@@ -17,25 +17,37 @@
 namespace cign {
 namespace rowops {
 
-__global__ void colsum_kernel(const float* part, int nb, int width, float* out0, float* out1) {
-  __shared__ float red[kBlock];
+// out[c] = sum_b part[b][c] over the nb row-block partials, in a fixed order:
+// a workgroup of kColsumThreads covers 64 columns; thread (c, s) sums the
+// partials b = s, s + 16, ... with four independent accumulators (combined in
+// a fixed order), then the 16 slices are added in order through LDS.
+__global__ __launch_bounds__(kColsumThreads) void colsum_kernel(const float* part, int nb, int width, float* out0,
+                                                                float* out1) {
+  constexpr int kCols = 64;
+  constexpr int kSlices = kColsumThreads / kCols;
+  __shared__ float red[kColsumThreads];
   const float* src = part + static_cast<int64_t>(blockIdx.y) * nb * width;
   float* out = blockIdx.y == 0 ? out0 : out1;
-  const int c0 = blockIdx.x * kBlock;
-  const int ct = min(kBlock, width - c0);
-  const int S = kBlock / ct;
   const int t = threadIdx.x;
-  const int c = t % ct;
-  const int s = t / ct;
-  float acc = 0.0f;
-  if (s < S)
-    for (int b = s; b < nb; b += S) acc += src[static_cast<int64_t>(b) * width + c0 + c];
-  red[t] = acc;
+  const int c = blockIdx.x * kCols + t % kCols;
+  const int s = t / kCols;
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  if (c < width) {
+    int b = s;
+    for (; b + 3 * kSlices < nb; b += 4 * kSlices) {
+      a0 += src[static_cast<int64_t>(b) * width + c];
+      a1 += src[static_cast<int64_t>(b + kSlices) * width + c];
+      a2 += src[static_cast<int64_t>(b + 2 * kSlices) * width + c];
+      a3 += src[static_cast<int64_t>(b + 3 * kSlices) * width + c];
+    }
+    for (; b < nb; b += kSlices) a0 += src[static_cast<int64_t>(b) * width + c];
+  }
+  red[t] = (a0 + a1) + (a2 + a3);
   __syncthreads();
-  if (t < ct) {
+  if (s == 0 && c < width) {
     float tot = 0.0f;
-    for (int k = 0; k < S; ++k) tot += red[k * ct + t];
-    out[c0 + t] = tot;
+    for (int k = 0; k < kSlices; ++k) tot += red[k * kCols + t];
+    out[c] = tot;
   }
 }
 
@@ -55,7 +67,7 @@ int zero_outputs(hipStream_t st, float* a, int na, float* b, int nbv, const char
 int launch_colsum(hipStream_t st, const float* part, int nb, int width, int quantities, float* out0, float* out1,
                   const char* who) {
   if (width <= 0) return kOk;
-  hipLaunchKernelGGL(colsum_kernel, dim3((width + kBlock - 1) / kBlock, quantities), dim3(kBlock), 0, st, part, nb,
+  hipLaunchKernelGGL(colsum_kernel, dim3((width + 63) / 64, quantities), dim3(kColsumThreads), 0, st, part, nb,
                      width, out0, out1);
   return check_launch(who);
 }

@@ -23,9 +23,16 @@ namespace rowops {
 template <int N>
 using IC = std::integral_constant<int, N>;
 
-// Number of row blocks (partial rows) of a reduction over n rows; the
-// workspace of such a reduction is quantities * colsum_blocks(n) * width floats.
-inline int colsum_blocks(int64_t n) { return static_cast<int>(n < 1 ? 1 : (n < 2048 ? n : 2048)); }
+// Number of row blocks (partial rows) of a reduction over n rows: about 8
+// rows per block, at most 1024 blocks (4 per CU); the workspace of such a
+// reduction is quantities * colsum_blocks(n) * width floats.
+inline int colsum_blocks(int64_t n) {
+  const int64_t b = (n + 7) / 8;
+  return static_cast<int>(b < 1 ? 1 : (b < 1024 ? b : 1024));
+}
+
+// Threads of the colsum_kernel workgroup (64 columns x 16 partial slices).
+constexpr int kColsumThreads = 1024;
 
 template <int LPR>
 struct Geo {
