@@ -4,7 +4,9 @@ One step = the headline layer of BASELINE.json, forward + backward, with all
 inputs resident in HBM:
   * collapsed GAT core (c2: H=4 heads x C=16 channels, fp32) on the
     24,492-node / 186,100-edge Chung-Lu graph + self-loops (E = 210,592):
-    cign_gat_fwd then cign_gat_bwd (2 kernels);
+    cign_gat_fwd (which also writes the per-row aggregates the backward
+    streams, as the drop-in autograd function runs it) then cign_gat_bwd
+    (rows and columns kernels);
   * 3-hop CSR SpMM pipeline (c3: D=64, fp32) on the normalized adjacency of
     the same graph: cign_spmm_fwd3 then cign_spmm_bwd3 (3 + 3 kernels).
 value = E * K / t (edges/s over the timed K steps; each step is one replay
@@ -127,9 +129,10 @@ def invariants(torch, w, ext, plan, H, C, D, dt):
     ac = torch.randn(n, H, generator=g).to(xs.device)
     bias = torch.randn(C, generator=g).to(xs.device)
     gy = torch.randn(n, C, generator=g).to(xs.device).to(dt)
-    out, pre, emax, esum, mask = ext.forward(ar, ac, rowptr, col, 0.2, ones, bias, 0.0, 0)
+    (out, pre, emax, esum, mask), agg = ext.forward_agg(ar, ac, rowptr, col, 0.2, ones, bias, 0.0, 0, True)
     gat_err = float((pre - (1.0 + bias)[None]).abs().max()) / float((1.0 + bias).abs().max())
-    gf, gar, gac, gb = ext.backward(0.2, 0.0, rowptr, col, colptr, row, perm, emax, esum, mask, ones, ar, ac, pre, gy)
+    gf, gar, gac, gb = ext.backward(0.2, 0.0, rowptr, col, colptr, row, perm, emax, esum, mask, ones, ar, ac, pre, gy,
+                                    agg)
     gscale = float(gf.float().abs().max())
     att_err = max(float(gar.abs().max()), float(gac.abs().max())) / gscale
     torch.cuda.synchronize()
@@ -470,14 +473,18 @@ def main():
     fwd_out = {}
 
     def run_phase(p):
+        # The GAT runs as the drop-in autograd function does: the forward
+        # also writes the per-row aggregates its backward streams.
         if p == "gat_fwd":
-            fwd_out["gat"] = ext.forward(ar, ac, rowptr, col, 0.2, x, bias, 0.0, 0)
+            outs, agg = ext.forward_agg(ar, ac, rowptr, col, 0.2, x, bias, 0.0, 0, True)
+            fwd_out["gat"] = outs + ([agg] if agg is not None else [])
         elif p == "spmm_fwd3":
             fwd_out["mh"] = plan.forward3(X)
         elif p == "gat_bwd":
-            out, pre, emax, esum, mask = fwd_out["gat"]
+            out, pre, emax, esum, mask = fwd_out["gat"][:5]
+            agg = fwd_out["gat"][5] if len(fwd_out["gat"]) > 5 else None
             fwd_out["gat_bwd"] = ext.backward(0.2, 0.0, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar,
-                                              ac, pre, gy)
+                                              ac, pre, gy, agg)
         else:
             fwd_out["mh_bwd"] = [plan.backward3(g1, g2, g3)]
 
@@ -569,7 +576,9 @@ def main():
     # One "launch" of the GAT backward is one cign_gat_bwd call (its rows and
     # columns kernels back to back on the stream).
     launches = {"gat_fwd": 1, "spmm_fwd3": 3, "gat_bwd": 1, "spmm_bwd3": 3}
-    bytes_per_launch = {"gat_fwd": B["gat_fwd"], "spmm_fwd3": B["spmm"], "gat_bwd": B["gat_bwd"],
+    agg_path = len(fwd_out["gat"]) > 5
+    gkey = "_agg" if agg_path else ""
+    bytes_per_launch = {"gat_fwd": B["gat_fwd" + gkey], "spmm_fwd3": B["spmm"], "gat_bwd": B["gat_bwd" + gkey],
                         "spmm_bwd3": B["spmm"] + s * n * D * 2 / 3}
     breakdown = {}
     for p in phases:
@@ -580,10 +589,12 @@ def main():
     dom_ms = phase_ms[dom] / launches[dom]
     achieved = bytes_per_launch[dom] / (dom_ms * 1e-3) / 1e9
     kernel_name = {"gat_fwd": "cign_gat_fwd (gat_fwd_fl_kernel)", "spmm_fwd3": "spmm_kernel (fwd hop)",
-                   "gat_bwd": "cign_gat_bwd (gat_bwd_rows_fl_kernel + gat_bwd_cols_fl_kernel)",
+                   "gat_bwd": ("cign_gat_bwd (gat_bwd_rows_agg_kernel + gat_bwd_cols_fl_kernel)" if agg_path else
+                               "cign_gat_bwd (gat_bwd_rows_fl_kernel + gat_bwd_cols_fl_kernel)"),
                    "spmm_bwd3": "spmm_kernel (bwd hop, fused add)"}[dom]
     traffic, traffic_src = measured_traffic(f"layer_{'c5' if scale else 'c2c3'}_{args.dtype}", dom)
     layer_gbs = B["layer"] / (ms * 1e-3) / 1e9
+    layer_own_gbs = B["layer" + gkey] / (ms * 1e-3) / 1e9
 
     checks = invariants(torch, w, ext, plan, H, C, D, dt) if scale else None
 
@@ -614,6 +625,10 @@ def main():
         "layer_GB_s": round(layer_gbs, 1),
         "layer_roofline_frac": round(layer_gbs / HBM_PEAK_GBS, 4),
         "algorithmic_bytes_per_step": B["layer"],
+        # The same step priced with the bytes of the algorithm that runs
+        # (per-row aggregates instead of the backward's second gather).
+        "layer_own_bytes_per_step": B["layer" + gkey],
+        "layer_own_roofline_frac": round(layer_own_gbs / HBM_PEAK_GBS, 4),
         "breakdown": breakdown,
         "roofline": {"bound": "hbm", "kernel": kernel_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

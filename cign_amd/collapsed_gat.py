@@ -48,6 +48,15 @@ class _CollapsedGATExt:
 
     @staticmethod
     def forward(attn_row, attn_col, row_ptr, col_ind, negative_slope, in_feat, bias, attn_drop, seed):
+        return _CollapsedGATExt.forward_agg(attn_row, attn_col, row_ptr, col_ind, negative_slope, in_feat, bias,
+                                            attn_drop, seed, False)[0]
+
+    @staticmethod
+    def forward_agg(attn_row, attn_col, row_ptr, col_ind, negative_slope, in_feat, bias, attn_drop, seed,
+                    want_agg):
+        """forward() plus, with ``want_agg`` on shapes that support it, the
+        per-row aggregate buffer that lets backward() skip its second gather
+        of in_feat (None otherwise)."""
         for t, n in ((attn_row, "attn_row"), (attn_col, "attn_col"), (bias, "bias")):
             _check_dev(t, n, _F32)
         _check_dev(row_ptr, "row_ptr", _I32)
@@ -75,16 +84,23 @@ class _CollapsedGATExt:
         edge_mask = torch.empty((nnz, H), dtype=torch.uint8, device=dev)
         ws_bytes = int(lib.cign_gat_fwd_workspace_bytes(sched.n_seg, H, C))
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        agg = None
+        if want_agg:
+            agg_floats = int(lib.cign_gat_row_agg_floats(_lib.dtype_code(in_feat), n, H, C))
+            if agg_floats > 0:
+                agg = torch.empty(agg_floats, dtype=torch.float32, device=dev)
         lib.call("cign_gat_fwd", _lib.stream_ptr(dev), _lib.dtype_code(in_feat), n, nnz, H, C, attn_row.data_ptr(),
                  attn_col.data_ptr(), col_ind.data_ptr(), *sched.args(),
                  sched.counters.data_ptr(), float(negative_slope), in_feat.data_ptr(), bias.data_ptr(),
                  float(attn_drop), int(seed) & ((1 << 64) - 1), out.data_ptr(), pre.data_ptr(), edge_max.data_ptr(),
-                 edge_sum.data_ptr(), edge_mask.data_ptr(), ws.data_ptr(), ws_bytes)
-        return [out, pre, edge_max, edge_sum, edge_mask]
+                 edge_sum.data_ptr(), edge_mask.data_ptr(), ws.data_ptr(), ws_bytes, _lib.ptr(agg))
+        return [out, pre, edge_max, edge_sum, edge_mask], agg
 
     @staticmethod
     def backward(negative_slope, attn_drop, row_ptr, col_ind, col_ptr, row_ind, permute, edge_max, edge_sum,
-                 edge_mask, in_feat, attn_row, attn_col, pre, grad_y):
+                 edge_mask, in_feat, attn_row, attn_col, pre, grad_y, row_agg=None):
+        """``row_agg``: the buffer forward_agg() returned for the same inputs,
+        or None (the rows pass then gathers in_feat per edge)."""
         for t, n in ((row_ptr, "row_ptr"), (col_ind, "col_ind"), (col_ptr, "col_ptr"), (row_ind, "row_ind"),
                      (permute, "permute")):
             _check_dev(t, n, _I32)
@@ -116,7 +132,8 @@ class _CollapsedGATExt:
                  permute.data_ptr(), edge_max.data_ptr(), edge_sum.data_ptr(), edge_mask.data_ptr(),
                  in_feat.data_ptr(), attn_row.data_ptr(), attn_col.data_ptr(), pre.data_ptr(), grad_y.data_ptr(),
                  *rs.args(), rs.counters.data_ptr(), *cs.args(), cs.counters.data_ptr(), ws.data_ptr(), ws_bytes,
-                 grad_feat.data_ptr(), grad_attn_row.data_ptr(), grad_attn_col.data_ptr(), grad_bias.data_ptr())
+                 grad_feat.data_ptr(), grad_attn_row.data_ptr(), grad_attn_col.data_ptr(), grad_bias.data_ptr(),
+                 _lib.ptr(row_agg))
         return [grad_feat, grad_attn_row, grad_attn_col, grad_bias]
 
 
@@ -163,10 +180,12 @@ class _CollapsedGATFn(torch.autograd.Function):
         H, C = int(in_feat.size(1)), int(in_feat.size(2))
         gat_schedule(rowptr, 1, code, H, C)
         gat_schedule(colptr, 1, code, H, C)
-        y, pre, edge_max, edge_sum, edge_mask = ext.forward(attn_row, attn_col, rowptr, col, float(negative_slope),
-                                                            in_feat, bias, float(attn_drop), int(seed))
+        (y, pre, edge_max, edge_sum, edge_mask), agg = ext.forward_agg(
+            attn_row, attn_col, rowptr, col, float(negative_slope), in_feat, bias, float(attn_drop), int(seed), True)
+        # agg (per-row aggregates, or None) spares the backward a second
+        # gather of in_feat; it is saved beside the reference's tensors.
         ctx.save_for_backward(rowptr, col, colptr, row, perm, edge_max, edge_sum, edge_mask, in_feat, attn_row,
-                              attn_col, pre)
+                              attn_col, pre, agg)
         ctx.graph = (rowptr, colptr)  # keeps the schedule cache keys alive and identical
         ctx.negative_slope = float(negative_slope)
         ctx.attn_drop = float(attn_drop)
@@ -176,11 +195,11 @@ class _CollapsedGATFn(torch.autograd.Function):
     def backward(ctx, grad_y):
         ext = ensure_collapsed_gat_loaded(False)
         (_rowptr, col, _colptr, row, perm, edge_max, edge_sum, edge_mask, in_feat, attn_row, attn_col,
-         pre) = ctx.saved_tensors
+         pre, agg) = ctx.saved_tensors
         rowptr, colptr = ctx.graph
         grad_feat, grad_attn_row, grad_attn_col, grad_bias = ext.backward(
             float(ctx.negative_slope), float(ctx.attn_drop), rowptr, col, colptr, row, perm, edge_max, edge_sum,
-            edge_mask, in_feat, attn_row, attn_col, pre, grad_y.to(dtype=in_feat.dtype).contiguous())
+            edge_mask, in_feat, attn_row, attn_col, pre, grad_y.to(dtype=in_feat.dtype).contiguous(), agg)
         return (grad_attn_row, grad_attn_col, None, None, None, None, None, None, grad_feat, grad_bias, None, None)
 
 

@@ -154,9 +154,17 @@ int cign_gat_schedule_params(int32_t pass, int32_t dtype, int32_t heads, int32_t
   return kOk;
 }
 
-// fp32 workspace needed by cign_gat_fwd for a row schedule with n_seg segments.
+// fp32 workspace needed by cign_gat_fwd for a row schedule with n_seg
+// segments: one partial {acc, accl, m, s, bl} per segment.
 int64_t cign_gat_fwd_workspace_bytes(int32_t n_seg, int32_t heads, int32_t channels) {
-  return 4LL * n_seg * (static_cast<int64_t>(heads) * channels + 2LL * heads);
+  return 4LL * n_seg * (2LL * heads * channels + 3LL * heads);
+}
+
+// Floats of the per-row aggregate buffer of cign_gat_fwd / cign_gat_bwd for
+// this shape, 0 when the shape's kernels do not use one.
+int64_t cign_gat_row_agg_floats(int32_t dtype, int32_t n, int32_t heads, int32_t channels) {
+  if (n < 0 || heads < 1 || channels < 1 || !fl_ok(dtype, heads, channels)) return 0;
+  return static_cast<int64_t>(n) * heads * (2LL * channels + 1);
 }
 
 // Collapsed GAT forward. Replaces the ext `forward` of the reference
@@ -165,7 +173,7 @@ int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
                  const float* attn_row, const float* attn_col, const int32_t* col, const int32_t* row_sched,
                  const int32_t* row_sched_info, int32_t* row_counters, float negative_slope, const void* in_feat,
                  const float* bias, float attn_drop, uint64_t seed, void* out, float* pre, float* edge_max,
-                 float* edge_sum, uint8_t* edge_mask, void* workspace, int64_t workspace_bytes) {
+                 float* edge_sum, uint8_t* edge_mask, void* workspace, int64_t workspace_bytes, float* row_agg) {
   int rc = check_shape("cign_gat_fwd", n, nnz, heads, channels);
   if (rc) return rc;
   if (!(attn_drop >= 0.0f && attn_drop < 1.0f)) return set_error(kInvalid, "cign_gat_fwd: attn_drop must be in [0,1)");
@@ -175,6 +183,9 @@ int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
   if ((rc = read_hdr("cign_gat_fwd", row_sched_info, n, light, seg, hd))) return rc;
   if (workspace_bytes < cign_gat_fwd_workspace_bytes(hd.n_seg, heads, channels))
     return set_error(kInvalid, "cign_gat_fwd: workspace too small");
+  if (row_agg && (cign_gat_row_agg_floats(dtype, n, heads, channels) == 0 || !aligned16(row_agg)))
+    return set_error(kInvalid, "cign_gat_fwd: row_agg must be null for this shape (cign_gat_row_agg_floats) or "
+                     "16-byte aligned");
   if (n == 0) return kOk;
   const Sched s = make_sched(row_sched, hd.n_light, hd.n_seg, hd.n_hrow);
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -187,6 +198,7 @@ int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
     a.attn_row = attn_row; a.attn_col = attn_col; a.col = col;
     a.x = xt; a.bias = bias; a.out = ot; a.pre = pre; a.emax = edge_max; a.esum = edge_sum;
     a.mask = edge_mask; a.partial = static_cast<float*>(workspace); a.counters = row_counters;
+    a.agg = row_agg;
     if (fl_ok(dtype, heads, channels)) {
       if (!aligned16(xt) || !aligned16(ot) || !aligned16(pre))
         return set_error(kInvalid, "cign_gat_fwd: in_feat, out and pre must be 16-byte aligned");
@@ -225,8 +237,11 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
                  const void* grad_y, const int32_t* row_sched, const int32_t* row_sched_info,
                  int32_t* row_counters, const int32_t* col_sched, const int32_t* col_sched_info,
                  int32_t* col_counters, void* workspace, int64_t workspace_bytes, void* grad_feat,
-                 float* grad_attn_row, float* grad_attn_col, float* grad_bias) {
+                 float* grad_attn_row, float* grad_attn_col, float* grad_bias, const float* row_agg) {
   int rc = check_shape("cign_gat_bwd", n, nnz, heads, channels);
+  if (row_agg && (cign_gat_row_agg_floats(dtype, n, heads, channels) == 0 || !aligned16(row_agg)))
+    return set_error(kInvalid, "cign_gat_bwd: row_agg must be null for this shape (cign_gat_row_agg_floats) or "
+                     "16-byte aligned");
   if (rc) return rc;
   if (!(attn_drop >= 0.0f && attn_drop < 1.0f)) return set_error(kInvalid, "cign_gat_bwd: attn_drop must be in [0,1)");
   Hdr rh, ch;
@@ -255,7 +270,7 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
     a.vec_gp = (channels % 4) == 0;
     a.col = col; a.rowind = rowind; a.perm = perm;
     a.emax = edge_max; a.esum = edge_sum; a.mask = edge_mask; a.x = xt;
-    a.attn_row = attn_row; a.attn_col = attn_col; a.pre = pre; a.grad_y = gyt;
+    a.attn_row = attn_row; a.attn_col = attn_col; a.pre = pre; a.grad_y = gyt; a.agg = row_agg;
     a.grad_pre = reinterpret_cast<float*>(ws + L.grad_pre);
     a.gscore = reinterpret_cast<float*>(ws + L.gscore);
     a.wsum = reinterpret_cast<float*>(ws + L.wsum);

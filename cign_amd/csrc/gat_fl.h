@@ -146,23 +146,42 @@ __device__ __forceinline__ float head_sum(float v, int cq) {
 // ===========================================================================
 // Forward
 // ===========================================================================
+// Online-softmax state of a lane: running max m, sum s and the unnormalised
+// accumulators acc = sum p kw x, accl = sum p kw l' x, bl = sum p l' (p =
+// exp(score - m)); accl and bl are the per-row aggregates the backward reads
+// instead of gathering the source rows again.
 template <int W>
 struct FwdState {
-  float m, s;
-  float acc[W];
+  float m, s, bl;
+  float acc[W], accl[W];
   __device__ __forceinline__ void clear() {
     m = kNegBig;
     s = 0.0f;
+    bl = 0.0f;
 #pragma unroll
-    for (int w = 0; w < W; ++w) acc[w] = 0.0f;
+    for (int w = 0; w < W; ++w) acc[w] = accl[w] = 0.0f;
   }
-  // (m, s, acc) <- (m, s, acc) (+) (m2, s2, acc2)
-  __device__ __forceinline__ void merge(float m2, float s2, const float (&acc2)[W]) {
+  __device__ __forceinline__ void scale(float f) {
+    s *= f;
+    bl *= f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      acc[w] *= f;
+      accl[w] *= f;
+    }
+  }
+  // state <- state (+) (m2, s2, bl2, acc2, accl2)
+  __device__ __forceinline__ void merge(float m2, float s2, float bl2, const float (&acc2)[W],
+                                        const float (&accl2)[W]) {
     const float mx = fmaxf(m, m2);
     const float f1 = expf(m - mx), f2 = expf(m2 - mx);
     s = s * f1 + s2 * f2;
+    bl = bl * f1 + bl2 * f2;
 #pragma unroll
-    for (int w = 0; w < W; ++w) acc[w] = acc[w] * f1 + acc2[w] * f2;
+    for (int w = 0; w < W; ++w) {
+      acc[w] = acc[w] * f1 + acc2[w] * f2;
+      accl[w] = accl[w] * f1 + accl2[w] * f2;
+    }
     m = mx;
   }
 };
@@ -191,23 +210,23 @@ struct FwdBatches {
       sc[k] = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq];
       xb[k] = Chunk<T, W>::load_raw(a.x + static_cast<int64_t>(j) * F + ln.q * W);
     }
+    // sc[k] becomes the raw score (before LeakyReLU): its sign gives l'.
     float mx = st.m;
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
-      sc[k] = u < cnt ? leaky(ar + sc[k], a.slope) : kNegBig;
-      mx = fmaxf(mx, sc[k]);
+      sc[k] += ar;
+      if (u < cnt) mx = fmaxf(mx, leaky(sc[k], a.slope));
     }
-    const float f = expf(st.m - mx);
-    st.s *= f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) st.acc[w] *= f;
+    st.scale(expf(st.m - mx));
     st.m = mx;
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
-      const float pk = u < cnt ? expf(sc[k] - mx) : 0.0f;
+      const float pk = u < cnt ? expf(leaky(sc[k], a.slope) - mx) : 0.0f;
+      const float lp = sc[k] < 0.0f ? a.slope : 1.0f;
       st.s += pk;
+      st.bl = fmaf(pk, lp, st.bl);
       float wk = pk;
       if constexpr (DROP) {
         bool keep = false;
@@ -218,10 +237,14 @@ struct FwdBatches {
         }
         wk = keep ? pk / (1.0f - a.p) : 0.0f;
       }
+      const float wl = wk * lp;
       float xv[W];
       Chunk<T, W>::unpack(xb[k], xv);
 #pragma unroll
-      for (int w = 0; w < W; ++w) st.acc[w] = fmaf(wk, xv[w], st.acc[w]);
+      for (int w = 0; w < W; ++w) {
+        st.acc[w] = fmaf(wk, xv[w], st.acc[w]);
+        st.accl[w] = fmaf(wl, xv[w], st.accl[w]);
+      }
     }
   }
 };
@@ -239,18 +262,23 @@ template <int L, int W>
 __device__ __forceinline__ void fwd_merge_groups(FwdState<W>& st) {
 #pragma unroll
   for (int o = L; o < kWave; o <<= 1) {
-    float a2[W];
+    float a2[W], l2[W];
 #pragma unroll
-    for (int w = 0; w < W; ++w) a2[w] = shfl_xor(st.acc[w], o);
-    const float m2 = shfl_xor(st.m, o), s2 = shfl_xor(st.s, o);
-    st.merge(m2, s2, a2);
+    for (int w = 0; w < W; ++w) {
+      a2[w] = shfl_xor(st.acc[w], o);
+      l2[w] = shfl_xor(st.accl[w], o);
+    }
+    const float m2 = shfl_xor(st.m, o), s2 = shfl_xor(st.s, o), b2 = shfl_xor(st.bl, o);
+    st.merge(m2, s2, b2, a2, l2);
   }
 }
 
 // Head mean + bias + SiLU of a row; every lane of the wavefront calls this
 // (the head sum is a butterfly inside the group), `write` selects the group
 // that stores. Lane q of head 0 writes channels [cw*W, cw*W + W) of pre/out;
-// lane cw = 0 of each head writes edge_max / edge_sum.
+// lane cw = 0 of each head writes edge_max / edge_sum. With a.agg, lane q
+// also writes its normalised chunks of the two aggregates and lane cw = 0 the
+// head's sum_e s l'.
 template <typename T, int L>
 __device__ __forceinline__ void fwd_emit(const GatFwdArgs<T>& a, const FlLane<L>& ln, int cq, int row, bool write,
                                          const FwdState<FlGeom<T>::W>& st) {
@@ -259,6 +287,16 @@ __device__ __forceinline__ void fwd_emit(const GatFwdArgs<T>& a, const FlLane<L>
   float y[W];
 #pragma unroll
   for (int w = 0; w < W; ++w) y[w] = ln.qv ? st.acc[w] * inv : 0.0f;
+  if (a.agg && write && ln.qv) {
+    const int F = a.H * a.C;
+    const int64_t nF = static_cast<int64_t>(a.n) * F;
+    float yl[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) yl[w] = st.accl[w] * inv;
+    store_f32<W>(a.agg + static_cast<int64_t>(row) * F + ln.q * W, y);
+    store_f32<W>(a.agg + nF + static_cast<int64_t>(row) * F + ln.q * W, yl);
+    if (ln.cw == 0) a.agg[2 * nF + static_cast<int64_t>(row) * a.H + ln.hq] = st.bl * inv;
+  }
   for (int o = cq; o < L; o <<= 1)
 #pragma unroll
     for (int w = 0; w < W; ++w) y[w] += shfl_xor(y[w], o);
@@ -325,8 +363,8 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
 
   // Heavy-row segment: wave w takes edges [64w, 64w + 64) of every 256-edge
   // round of the segment.
-  __shared__ float hm[kWavesPerBlock][kWave], hs[kWavesPerBlock][kWave];
-  __shared__ float hacc[kWavesPerBlock][kWave * W];
+  __shared__ float hm[kWavesPerBlock][kWave], hs[kWavesPerBlock][kWave], hb[kWavesPerBlock][kWave];
+  __shared__ float hacc[kWavesPerBlock][kWave * W], haccl[kWavesPerBlock][kWave * W];
   __shared__ int flag;
   const int4 sg = s.seg[b];
   const int row = sg.x;
@@ -341,33 +379,47 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
   if (ln.g == 0) {
     hm[wave][ln.gl] = st.m;
     hs[wave][ln.gl] = st.s;
+    hb[wave][ln.gl] = st.bl;
 #pragma unroll
-    for (int w = 0; w < W; ++w) hacc[wave][ln.gl * W + w] = st.acc[w];
+    for (int w = 0; w < W; ++w) {
+      hacc[wave][ln.gl * W + w] = st.acc[w];
+      haccl[wave][ln.gl * W + w] = st.accl[w];
+    }
   }
   __syncthreads();
   // Every wave forms the merged state of its lane slot gl (identical copies).
   st.m = hm[0][ln.gl];
   st.s = hs[0][ln.gl];
+  st.bl = hb[0][ln.gl];
 #pragma unroll
-  for (int w = 0; w < W; ++w) st.acc[w] = hacc[0][ln.gl * W + w];
+  for (int w = 0; w < W; ++w) {
+    st.acc[w] = hacc[0][ln.gl * W + w];
+    st.accl[w] = haccl[0][ln.gl * W + w];
+  }
 #pragma unroll
   for (int v = 1; v < kWavesPerBlock; ++v) {
-    float a2[W];
+    float a2[W], l2[W];
 #pragma unroll
-    for (int w = 0; w < W; ++w) a2[w] = hacc[v][ln.gl * W + w];
-    st.merge(hm[v][ln.gl], hs[v][ln.gl], a2);
+    for (int w = 0; w < W; ++w) {
+      a2[w] = hacc[v][ln.gl * W + w];
+      l2[w] = haccl[v][ln.gl * W + w];
+    }
+    st.merge(hm[v][ln.gl], hs[v][ln.gl], hb[v][ln.gl], a2, l2);
   }
   if (hr.y == 1) {
     if (wave == 0) fwd_emit<T, L>(a, ln, cq, row, ln.g == 0, st);
     return;
   }
-  const int stride = F + 2 * a.H;
+  // Segment partial: acc [F], accl [F], then m, s, bl per head.
+  const int stride = 2 * F + 3 * a.H;
   float* mine = a.partial + static_cast<int64_t>(b) * stride;
   if (wave == 0 && ln.g == 0 && ln.qv) {
     store_f32<W>(mine + ln.q * W, st.acc);
+    store_f32<W>(mine + F + ln.q * W, st.accl);
     if (ln.cw == 0) {
-      mine[F + ln.hq] = st.m;
-      mine[F + a.H + ln.hq] = st.s;
+      mine[2 * F + ln.hq] = st.m;
+      mine[2 * F + a.H + ln.hq] = st.s;
+      mine[2 * F + 2 * a.H + ln.hq] = st.bl;
     }
   }
   if (!arrive_last(a.counters + sg.w, hr.y, &flag)) return;
@@ -376,9 +428,10 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
   st.clear();
   for (int z = 0; z < hr.y; ++z) {
     const float* pz = a.partial + static_cast<int64_t>(hr.x + z) * stride;
-    float a2[W];
+    float a2[W], l2[W];
     load_f32<W>(pz + ln.q * W, a2);
-    st.merge(pz[F + ln.hq], pz[F + a.H + ln.hq], a2);
+    load_f32<W>(pz + F + ln.q * W, l2);
+    st.merge(pz[2 * F + ln.hq], pz[2 * F + a.H + ln.hq], pz[2 * F + 2 * a.H + ln.hq], a2, l2);
   }
   fwd_emit<T, L>(a, ln, cq, row, ln.g == 0, st);
 }
@@ -627,6 +680,32 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a
   }
 }
 
+// Rows pass from the forward's per-row aggregates (a.agg): the same
+// (wsum, A, B) as gat_bwd_rows_fl_kernel without gathering any source row, a
+// stream over the rows. A group of L lanes per row, G rows per wavefront.
+template <typename T, int L>
+__global__ __launch_bounds__(kBlock) void gat_bwd_rows_agg_kernel(GatBwdArgs<T> a, int lgcq) {
+  constexpr int W = FlGeom<T>::W;
+  constexpr int G = kWave / L;
+  const int cq = 1 << lgcq;
+  const FlLane<L> ln(lgcq, a.H * cq);
+  const int row = (blockIdx.x * kWavesPerBlock + wave_id()) * G + ln.g;
+  if (row >= a.n) return;  // no barrier follows
+  const int F = a.H * a.C;
+  const int64_t nF = static_cast<int64_t>(a.n) * F;
+  RowAcc<W> st;
+  load_f32<W>(a.agg + static_cast<int64_t>(row) * F + ln.q * W, st.vs);
+  load_f32<W>(a.agg + nF + static_cast<int64_t>(row) * F + ln.q * W, st.vsl);
+  st.B = a.agg[2 * nF + static_cast<int64_t>(row) * a.H + ln.hq];
+  float gp[W];
+  grad_pre_chunk(a, row, ln.cw, gp);
+  float wsum, A;
+  rows_dots<W>(st, gp, cq, a.inv_h, wsum, A);
+  if (!ln.qv) return;
+  if (ln.cw == 0) rows_store(a, row, ln.hq, row_head(a, row, ln.hq), wsum, A, st.B);
+  if (ln.hq == 0) store_f32<W>(a.grad_pre + static_cast<int64_t>(row) * a.C + ln.cw * W, gp);
+}
+
 // ===========================================================================
 // Backward, columns (CSC)
 // ===========================================================================
@@ -836,7 +915,14 @@ struct BwdFlLauncher {
     const int r_mid = G > 1 ? sched_count_gt(rhdr, L) : rs.n_light;
     const int r_mid_blocks = (r_mid + kWavesPerBlock - 1) / kWavesPerBlock;
     const int rb = row_blocks(rs, rhdr);
-    if (rb > 0) {
+    if (a.agg) {
+      const int ab = (a.n + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
+      if (ab > 0) {
+        hipLaunchKernelGGL((gat_bwd_rows_agg_kernel<T, L>), dim3(ab), dim3(kBlock), 0, st, a, lgcq);
+        const int rc = check_launch("cign_gat_bwd (rows from aggregates, feature layout)");
+        if (rc) return rc;
+      }
+    } else if (rb > 0) {
       if (a.p > 0.0f)
         hipLaunchKernelGGL((gat_bwd_rows_fl_kernel<T, L, true>), dim3(rb), dim3(kBlock), 0, st, a, rs, r_mid,
                            r_mid_blocks, lgcq);

@@ -158,8 +158,12 @@ struct GatFwdArgs {
   float* emax;
   float* esum;
   uint8_t* mask;
-  float* partial;  // [n_seg, H*C + 2H]
+  float* partial;  // [n_seg, 2*H*C + 3H]
   int32_t* counters;
+  // Optional (feature layout): per-row aggregates for the backward, null to
+  // skip. agg [n, H*C] = sum_e s kw x[j_e], then [n, H*C] = sum_e s kw l'
+  // x[j_e], then [n, H] = sum_e s l'.
+  float* agg;
 };
 
 // Calls f(std::integral_constant<int, n>) for a wave-uniform n in [1, NMAX],
@@ -464,6 +468,7 @@ struct GatBwdArgs {
   const float* attn_col;
   const float* pre;
   const T* grad_y;
+  const float* agg;  // per-row aggregates written by the forward, or null
   // workspace
   float* grad_pre;   // [n, C]
   float* gscore;     // [nnz, H]: ge' = keep/(1-p) * <g_pre, x>/H

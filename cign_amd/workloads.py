@@ -58,7 +58,9 @@ def algorithmic_bytes(n: int, e: int, heads: int, channels: int, d: int, s_gat: 
     """Algorithmic byte counts of one layer forward + backward (streamed
     arrays once, gathered rows and per-edge scalars per edge; softmax
     statistics recomputed): collapsed GAT (H heads x C channels, element size
-    s_gat) and the K=3 multihop pipeline over d columns (element size s_mh)."""
+    s_gat) and the K=3 multihop pipeline over d columns (element size s_mh).
+    The *_agg entries count the path whose forward saves per-row aggregates
+    for the backward (cign_gat_row_agg_floats) instead of a second gather."""
     F = heads * channels
     H, C, N, E = heads, channels, n, e
     gat_fwd = 4 * (N + 1) + 4 * E + 4 * N * H + 4 * E * H + s_gat * E * F + 4 * C + 8 * N * C + 8 * N * H
@@ -66,10 +68,20 @@ def algorithmic_bytes(n: int, e: int, heads: int, channels: int, d: int, s_gat: 
                + (4 * (N + 1) + 8 * E + 12 * E * H + 4 * N * H + 4 * E * C + s_gat * N * F)
                + (4 * (N + 1) + 4 * E + s_gat * E * F + 4 * N * C + 4 * E * H + 12 * N * H + 4 * N * H + 8 * E * H)
                + 4 * C)
+    # The rows pass of that model gathers x per edge a second time; the
+    # feature-layout path instead writes per-row aggregates in the forward
+    # ([N,F] twice and [N,H], fp32) and streams them in the backward.
+    rows_gather = 4 * (N + 1) + 4 * E + s_gat * E * F + 4 * N * C + 4 * E * H + 12 * N * H + 4 * N * H + 8 * E * H
+    rows_stream = 8 * N * F + 36 * N * H + 4 * N * C
+    gat_fwd_agg = gat_fwd + 4 * N * (2 * F + H)
+    gat_bwd_agg = gat_bwd - rows_gather + rows_stream
     if dropout:
         gat_fwd += E * H
         gat_bwd += 2 * E * H
+        gat_fwd_agg += E * H
+        gat_bwd_agg += E * H
     spmm = 4 * (N + 1) + 8 * E + s_mh * E * d + s_mh * N * d
     mh = 6 * spmm + 2 * s_mh * N * d
     return {"gat_fwd": gat_fwd, "gat_bwd": gat_bwd, "gat": gat_fwd + gat_bwd, "spmm": spmm, "multihop": mh,
-            "layer": gat_fwd + gat_bwd + mh}
+            "layer": gat_fwd + gat_bwd + mh,
+            "gat_fwd_agg": gat_fwd_agg, "gat_bwd_agg": gat_bwd_agg, "layer_agg": gat_fwd_agg + gat_bwd_agg + mh}

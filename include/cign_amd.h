@@ -90,6 +90,17 @@ int cign_gat_schedule_params(int32_t pass, int32_t dtype, int32_t heads, int32_t
 /* Workspace bytes of cign_gat_fwd for a row schedule with n_seg segments. */
 int64_t cign_gat_fwd_workspace_bytes(int32_t n_seg, int32_t heads, int32_t channels);
 
+/* Floats of the optional per-row aggregate buffer (row_agg) that
+ * cign_gat_fwd fills and cign_gat_bwd reads, n*H*(2C+1) for the shapes of
+ * the feature-layout kernels (H <= 8, C a multiple of 16 bytes' worth of
+ * elements with C/that a power of two, H*C <= 64 such chunks), 0 otherwise.
+ * The buffer holds sum_e s kw x[j], sum_e s kw l' x[j] ([n,H,C] each) and
+ * sum_e s l' ([n,H]) per destination row, so the backward need not gather
+ * the source rows a second time. No counterpart in the reference: its
+ * _CollapsedGATFn saves the same tensors (collapsed_gat.py:106-110) and its
+ * backward re-gathers in_feat per edge (collapsed_gat_cuda.cu:176-300). */
+int64_t cign_gat_row_agg_floats(int32_t dtype, int32_t n, int32_t heads, int32_t channels);
+
 /* Collapsed GAT forward: edge score, per-destination softmax, edge dropout,
  * weighted aggregation, head mean + bias + SiLU. Replaces the extension
  * `forward` (collapsed_gat_ext/collapsed_gat.cpp:45-72; kernels
@@ -98,12 +109,14 @@ int64_t cign_gat_fwd_workspace_bytes(int32_t n_seg, int32_t heads, int32_t chann
  * (CSR by destination; row_sched built from its row pointer), in_feat
  * [n,H,C] (dtype), bias [C] f32, seed as derived by collapsed_gat.py:204-211.
  * Outputs: out [n,C] (dtype), pre [n,C] f32, edge_max/edge_sum [n,H] f32,
- * edge_mask [nnz,H] u8 (written only when attn_drop > 0). */
+ * edge_mask [nnz,H] u8 (written only when attn_drop > 0). row_agg: null, or
+ * cign_gat_row_agg_floats() floats (16-byte aligned) to receive the per-row
+ * aggregates of the backward. */
 int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
                  const float* attn_row, const float* attn_col, const int32_t* col, const int32_t* row_sched,
                  const int32_t* row_sched_info, int32_t* row_counters, float negative_slope, const void* in_feat,
                  const float* bias, float attn_drop, uint64_t seed, void* out, float* pre, float* edge_max,
-                 float* edge_sum, uint8_t* edge_mask, void* workspace, int64_t workspace_bytes);
+                 float* edge_sum, uint8_t* edge_mask, void* workspace, int64_t workspace_bytes, float* row_agg);
 
 /* Workspace bytes of cign_gat_bwd; row_blocks = n_seg + ceil(n_light / 4) of
  * the row schedule. */
@@ -115,7 +128,9 @@ int64_t cign_gat_bwd_workspace_bytes(int32_t n, int32_t nnz, int32_t heads, int3
  * Replaces the extension `backward` (collapsed_gat_ext/collapsed_gat.cpp:
  * 74-102; kernels collapsed_gat_cuda.cu:176-430, host :480-545). rowind /
  * perm are the CSC of the same graph (col_sched built from its column
- * pointer) with perm[k] = CSR id of CSC entry k. grad_y has in_feat's dtype. */
+ * pointer) with perm[k] = CSR id of CSC entry k. grad_y has in_feat's dtype.
+ * row_agg: null (the rows pass gathers in_feat per edge) or the buffer the
+ * forward filled for the same inputs (the rows pass streams it instead). */
 int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
                  float negative_slope, float attn_drop, const int32_t* col, const int32_t* rowind,
                  const int32_t* perm, const float* edge_max, const float* edge_sum, const uint8_t* edge_mask,
@@ -123,7 +138,7 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
                  const void* grad_y, const int32_t* row_sched, const int32_t* row_sched_info,
                  int32_t* row_counters, const int32_t* col_sched, const int32_t* col_sched_info,
                  int32_t* col_counters, void* workspace, int64_t workspace_bytes, void* grad_feat,
-                 float* grad_attn_row, float* grad_attn_col, float* grad_bias);
+                 float* grad_attn_row, float* grad_attn_col, float* grad_bias, const float* row_agg);
 
 /* ---- GAT side ops (float32) ---------------------------------------------- */
 

@@ -336,6 +336,30 @@ def collapsed_gat_backward(attn_row, attn_col, rowptr, col, slope, x, bias, grad
             "grad_pre": g_pre, "grad_raw": g_raw}
 
 
+def collapsed_gat_row_aggregates(attn_row, attn_col, rowptr, col, slope, x, p=0.0, keep=None):
+    """Per-destination-row aggregates the feature-layout forward saves for its
+    backward (no reference counterpart; they regroup the sums of
+    collapsed_gat_cuda.cu:295-430): with w = s * keep/(1-p) and l' the
+    LeakyReLU slope of the raw score,
+      agg[i,h]   = sum_e w x[j_e,h],   agg_l[i,h] = sum_e w l' x[j_e,h],
+      b_l[i,h]   = sum_e s l'.
+    Then <g_pre[i], agg_l[i,h]>/H - <g_pre[i], agg[i,h]>/H * b_l[i,h] is
+    grad_attn_row[i,h] of collapsed_gat_backward (pinned in tests)."""
+    x = np.asarray(x, dtype=np.float64)
+    n, H, C = x.shape
+    raw, soft, _, _ = gat_softmax(np.asarray(attn_row, np.float64), np.asarray(attn_col, np.float64),
+                                  rowptr, col, slope)
+    w = _edge_weights(soft, keep, p)
+    lp = np.where(raw < 0, slope, 1.0)
+    agg = np.zeros((n, H, C))
+    agg_l = np.zeros((n, H, C))
+    for h in range(H):
+        agg[:, h, :] = sp.csr_matrix((w[:, h], col, rowptr), shape=(n, n)) @ x[:, h, :]
+        agg_l[:, h, :] = sp.csr_matrix((w[:, h] * lp[:, h], col, rowptr), shape=(n, n)) @ x[:, h, :]
+    b_l = _segment_reduce(np.add, soft * lp, rowptr, 0.0)
+    return {"agg": agg, "agg_l": agg_l, "b_l": b_l}
+
+
 # ---------------------------------------------------------------------------
 # GAT side ops
 # ---------------------------------------------------------------------------

@@ -62,19 +62,31 @@ CASES = [
 ]
 
 
+def _forward(ext, agg_mode, *args):
+    """ext.forward, or with agg_mode ext.forward_agg (the autograd path): the
+    outputs and the per-row aggregate buffer (None for shapes without one)."""
+    if agg_mode:
+        return ext.forward_agg(*args, True)
+    return ext.forward(*args), None
+
+
+@pytest.mark.parametrize("agg_mode", [False, True])
 @pytest.mark.parametrize("H,C,p,dtype,n,hubs", CASES)
-def test_ext_forward_backward_matches_oracle(H, C, p, dtype, n, hubs):
+def test_ext_forward_backward_matches_oracle(H, C, p, dtype, n, hubs, agg_mode):
+    from cign_amd import _lib
     from cign_amd.collapsed_gat import ensure_collapsed_gat_loaded
 
-    print(f"gat ext H={H} C={C} p={p} dtype={dtype} n={n}", flush=True)
+    print(f"gat ext H={H} C={C} p={p} dtype={dtype} n={n} agg={agg_mode}", flush=True)
     rng = np.random.default_rng(H * 1000 + C)
     ei = _graph(rng, n, hubs)
     rowptr, col, row, colptr, perm = _dev_graph(ei, n)
     x, ar, ac, b, gy = _inputs(rng, n, H, C, dtype)
     ext = ensure_collapsed_gat_loaded()
     seed = 0x5EED_1234
-    out, pre, emax, esum, mask = ext.forward(ar, ac, rowptr, col, 0.2, x, b, p, seed)
-    grads = ext.backward(0.2, p, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar, ac, pre, gy)
+    (out, pre, emax, esum, mask), agg = _forward(ext, agg_mode, ar, ac, rowptr, col, 0.2, x, b, p, seed)
+    floats = int(_lib.load_library().cign_gat_row_agg_floats(_lib.dtype_code(x), n, H, C))
+    assert (agg is None) == (not agg_mode or floats == 0)
+    grads = ext.backward(0.2, p, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar, ac, pre, gy, agg)
     rp, cl = rowptr.cpu().numpy().astype(np.int64), col.cpu().numpy().astype(np.int64)
     E = cl.size
     keep = O.gat_dropout_keep(seed, E * H, p).reshape(E, H) if p > 0 else None
@@ -95,6 +107,15 @@ def test_ext_forward_backward_matches_oracle(H, C, p, dtype, n, hubs):
     assert_close(gar.cpu().numpy(), g["grad_attn_row"], name="grad_attn_row", **t32)
     assert_close(gac.cpu().numpy(), g["grad_attn_col"], name="grad_attn_col", **t32)
     assert_close(gb.cpu().numpy(), g["grad_bias"], name="grad_bias", **t32)
+    if agg is not None:
+        # The aggregates themselves: per (row, head) softmax-weighted sums of
+        # the source rows, with and without the LeakyReLU slope, and sum s l'.
+        F = H * C
+        a = agg.double().cpu().numpy()
+        ref = O.collapsed_gat_row_aggregates(arn, acn, rp, cl, 0.2, xn, p, keep)
+        assert_close(a[:n * F].reshape(n, H, C), ref["agg"], name="agg", **tol)
+        assert_close(a[n * F:2 * n * F].reshape(n, H, C), ref["agg_l"], name="agg_l", **tol)
+        assert_close(a[2 * n * F:].reshape(n, H), ref["b_l"], name="b_l", **t32)
 
 
 @pytest.fixture(scope="module")
@@ -233,14 +254,15 @@ def test_argument_errors(c2):
                                      torch.zeros(n, 4, 4, device="cuda"), None, 0.0)
 
 
+@pytest.mark.parametrize("agg_mode", [False, True])
 @pytest.mark.parametrize("seg", [256, 1024, 4096])
 @pytest.mark.parametrize("dtype,p", [(torch.float32, 0.0), (torch.float32, 0.2), (torch.bfloat16, 0.0)])
-def test_long_segments_multi_round(seg, dtype, p, monkeypatch):
+def test_long_segments_multi_round(seg, dtype, p, agg_mode, monkeypatch):
     """Hub rows/columns of 2,500-6,000 edges cut into segments of `seg` edges
     (several 256-edge rounds per workgroup, several workgroups per row)."""
     import cign_amd.schedule as S
 
-    print(f"gat long segments seg={seg} dtype={dtype} p={p}", flush=True)
+    print(f"gat long segments seg={seg} dtype={dtype} p={p} agg={agg_mode}", flush=True)
     monkeypatch.setattr(S, "segment_edges_for", lambda nnz: seg)
     S._CACHE.clear()
     rng = np.random.default_rng(seg)
@@ -251,8 +273,10 @@ def test_long_segments_multi_round(seg, dtype, p, monkeypatch):
     rowptr, col, row, colptr, perm = _dev_graph(np.stack([r, c]), n)
     x, ar, ac, b, gy = _inputs(rng, n, H, C, dtype)
     ext = __import__("cign_amd.collapsed_gat", fromlist=["x"]).ensure_collapsed_gat_loaded()
-    out, pre, emax, esum, mask = ext.forward(ar, ac, rowptr, col, 0.2, x, b, p, 99)
-    gf, gar, gac, gb = ext.backward(0.2, p, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar, ac, pre, gy)
+    (out, pre, emax, esum, mask), agg = _forward(ext, agg_mode, ar, ac, rowptr, col, 0.2, x, b, p, 99)
+    assert (agg is not None) == agg_mode
+    gf, gar, gac, gb = ext.backward(0.2, p, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar, ac, pre, gy,
+                                    agg)
     rp, cl = rowptr.cpu().numpy().astype(np.int64), col.cpu().numpy().astype(np.int64)
     keep = mask.cpu().numpy().astype(bool) if p > 0 else None
     if p > 0:

@@ -254,6 +254,27 @@ def test_gat_backward_finite_differences(rng, p):
         assert abs(fd - an) <= 1e-6 * max(1.0, abs(an)), (name, fd, an)
 
 
+@pytest.mark.parametrize("p", [0.0, 0.35])
+def test_gat_row_aggregates_give_backward(rng, p):
+    """The saved per-row aggregates reproduce the (finite-difference pinned)
+    backward: grad_attn_row = <g, agg_l>/H - <g, agg>/H * b_l, and the head
+    mean of agg is pre - bias. A dropped slope, keep factor or head index in
+    the aggregates fails one of the two."""
+    n, H, C, slope = 30, 3, 4, 0.2
+    d = _gat_inputs(rng, n, H, C, deg=5, hubs={2: 20})
+    E = len(d["col"])
+    keep = rng.random((E, H)) > p if p > 0 else None
+    gy = rng.standard_normal((n, C))
+    g = O.collapsed_gat_backward(d["ar"], d["ac"], d["rowptr"], d["col"], slope, d["x"], d["b"], gy, p, keep)
+    f = O.collapsed_gat_forward(d["ar"], d["ac"], d["rowptr"], d["col"], slope, d["x"], d["b"], p, keep)
+    a = O.collapsed_gat_row_aggregates(d["ar"], d["ac"], d["rowptr"], d["col"], slope, d["x"], p, keep)
+    gp = g["grad_pre"]
+    wsum = np.einsum("nc,nhc->nh", gp, a["agg"]) / H
+    A = np.einsum("nc,nhc->nh", gp, a["agg_l"]) / H
+    assert_close(A - wsum * a["b_l"], g["grad_attn_row"], 1e-10, 1e-12, "grad_attn_row from aggregates")
+    assert_close(a["agg"].mean(axis=1), f["pre"] - d["b"], 1e-12, 1e-12, "head mean of agg")
+
+
 # ---------------------------------------------------------------- side ops
 def test_attention_logits_and_head_silu(rng):
     n, H, C = 7, 3, 5
