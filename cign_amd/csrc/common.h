@@ -139,9 +139,10 @@ __device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m
 // before consuming any, so U is the number of loads a lane keeps in flight.
 template <int UMAX, typename Fn>
 __device__ __forceinline__ void for_batches(int need, Fn& fn) {
+  static_assert(UMAX == 1 || UMAX == 2 || UMAX == 4 || UMAX == 8 || UMAX == 16, "UMAX is a power of two <= 16");
   if (need <= 0) return;
-  if (need <= 1) {
-    fn.template run<1>(0);
+  if (need <= 1 || UMAX == 1) {
+    for (int k0 = 0; k0 < need; ++k0) fn.template run<1>(k0);
   } else if (need <= 2 || UMAX == 2) {
     for (int k0 = 0; k0 < need; k0 += 2) fn.template run<2>(k0);
   } else if (need <= 4 || UMAX == 4) {

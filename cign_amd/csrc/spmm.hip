@@ -34,9 +34,19 @@ namespace {
 // Workgroup shape of the SpMM: kSpmmWaves wavefronts; a heavy-row segment is
 // processed in rounds of kSpmmWaves x 64 edges.
 #ifndef CIGN_SPMM_WAVES
-#define CIGN_SPMM_WAVES 4
+#define CIGN_SPMM_WAVES 8
 #endif
 constexpr int kSpmmWaves = CIGN_SPMM_WAVES;
+// Chunks in flight per lane (a batch of U edges x VPL chunks), and the
+// smallest number of chunks a lane owns per row (more rows per wavefront).
+#ifndef CIGN_SPMM_INFLIGHT
+#define CIGN_SPMM_INFLIGHT 8
+#endif
+#ifndef CIGN_SPMM_MIN_VPL
+#define CIGN_SPMM_MIN_VPL 1
+#endif
+constexpr int kSpmmInflight = CIGN_SPMM_INFLIGHT;
+constexpr int kSpmmMinVpl = CIGN_SPMM_MIN_VPL;
 constexpr int kSpmmBlock = kSpmmWaves * kWave;
 constexpr int kTile = 64;
 constexpr int kSegEdges = kSpmmWaves * kTile;
@@ -121,13 +131,13 @@ __device__ __forceinline__ int wave_max_over_groups(int v, int L) {
   return v;
 }
 
-// Gathers `need` (wave-uniform) slots per lane group, at most 16 chunks in
-// flight per lane.
+// Gathers `need` (wave-uniform) slots per lane group, at most kSpmmInflight
+// chunks in flight per lane.
 template <typename T, int W, int VPL>
 __device__ __forceinline__ void gather(const SpmmArgs<T, W, VPL>& a, int jj, float vv, int base, int first, int step,
                                        int cnt, int need, int gl, float (&acc)[VPL][W]) {
   SpmmBatches<T, W, VPL> sb{a, jj, vv, base, first, step, cnt, gl, acc};
-  for_batches<16 / VPL>(need, sb);
+  for_batches<(kSpmmInflight / VPL > 0 ? kSpmmInflight / VPL : 1)>(need, sb);
 }
 
 template <typename T, int W, int VPL>
@@ -306,9 +316,9 @@ int launch_all(hipStream_t stream, const Sched& s, const SchedInfo& info, int ld
   for (int ch0 = 0; ch0 < total_ch; ch0 += kMaxCh) {
     const int nch = min(kMaxCh, total_ch - ch0);
     int rc;
-    if (nch <= kWave) {
+    if (nch <= kWave && kSpmmMinVpl <= 1) {
       rc = launch_tile<T, W, 1>(stream, s, info, ld, ch0 * W, nch, col, val, x, add, y, partial, counters);
-    } else if (nch <= 2 * kWave) {
+    } else if (nch <= 2 * kWave && kSpmmMinVpl <= 2) {
       rc = launch_tile<T, W, 2>(stream, s, info, ld, ch0 * W, nch, col, val, x, add, y, partial, counters);
     } else {
       rc = launch_tile<T, W, 4>(stream, s, info, ld, ch0 * W, nch, col, val, x, add, y, partial, counters);
