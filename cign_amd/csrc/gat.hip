@@ -85,13 +85,57 @@ __global__ void zero_floats(float* p, int n) {
   if (i < n) p[i] = 0.0f;
 }
 
-// Feature-layout eligibility (shape only): H <= 8 heads, C a multiple of the
-// 16-byte chunk width W with C/W a power of two (head sums and per-head dot
-// products are butterflies over lane bits), H*C <= 64 chunks.
-inline bool fl_ok(int dtype, int H, int C) {
+// Feature-layout geometry of a shape: lanes per row L and chunks per lane V,
+// or false. H <= 8 heads, C a multiple of the 16-byte chunk width W with cq =
+// C/W a power of two (head sums and per-head dot products are butterflies
+// over lane bits); narrow rows (H*cq <= 64 chunks) take L = pow2ceil(H*cq),
+// V = 1; wide rows take L = 64 and V = H*cq/64 in {2, 3, 4, 6, 8} (cq <= 64
+// divides 64, so a lane's chunks share one channel chunk).
+inline bool fl_geom(int dtype, int H, int C, int& L, int& V) {
   const int W = dtype == kBF16 ? 8 : 4;
   const int cq = C / W;
-  return H <= kFlHeads && C % W == 0 && (cq & (cq - 1)) == 0 && (H * C) / W <= kWave;
+  if (H < 1 || H > kFlHeads || C % W != 0 || cq < 1 || (cq & (cq - 1)) != 0) return false;
+  const int nq = H * cq;
+  if (nq <= kWave) {
+    L = 1;
+    while (L < nq) L <<= 1;
+    V = 1;
+    return true;
+  }
+  if (cq > kWave || nq % kWave != 0) return false;
+  L = kWave;
+  V = nq / kWave;
+  return V == 2 || V == 3 || V == 4 || V == 6 || V == 8;
+}
+
+inline bool fl_ok(int dtype, int H, int C) {
+  int L, V;
+  return fl_geom(dtype, H, C, L, V);
+}
+
+// Calls go(integral_constant<L>, integral_constant<V>) for an instantiated
+// (L, V) of the feature-layout kernels.
+template <typename Go>
+int fl_dispatch(int L, int V, Go&& go) {
+  using std::integral_constant;
+  if (V == 1) {
+    switch (L) {
+      case 1: return go(integral_constant<int, 1>(), integral_constant<int, 1>());
+      case 2: return go(integral_constant<int, 2>(), integral_constant<int, 1>());
+      case 4: return go(integral_constant<int, 4>(), integral_constant<int, 1>());
+      case 8: return go(integral_constant<int, 8>(), integral_constant<int, 1>());
+      case 16: return go(integral_constant<int, 16>(), integral_constant<int, 1>());
+      case 32: return go(integral_constant<int, 32>(), integral_constant<int, 1>());
+      default: return go(integral_constant<int, 64>(), integral_constant<int, 1>());
+    }
+  }
+  switch (V) {
+    case 2: return go(integral_constant<int, 64>(), integral_constant<int, 2>());
+    case 3: return go(integral_constant<int, 64>(), integral_constant<int, 3>());
+    case 4: return go(integral_constant<int, 64>(), integral_constant<int, 4>());
+    case 6: return go(integral_constant<int, 64>(), integral_constant<int, 6>());
+    default: return go(integral_constant<int, 64>(), integral_constant<int, 8>());
+  }
 }
 
 inline int fl_lgcq(int dtype, int C) {
@@ -203,18 +247,12 @@ int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
       if (!aligned16(xt) || !aligned16(ot) || !aligned16(pre))
         return set_error(kInvalid, "cign_gat_fwd: in_feat, out and pre must be 16-byte aligned");
       const int lgcq = fl_lgcq(dtype, channels);
-      const int W = dtype == kBF16 ? 8 : 4;
-      int L = 1;
-      while (L < heads * channels / W) L <<= 1;
-      switch (L) {
-        case 1: return FwdFlLauncher<T, 1>::run(st, a, s, row_sched_info, lgcq);
-        case 2: return FwdFlLauncher<T, 2>::run(st, a, s, row_sched_info, lgcq);
-        case 4: return FwdFlLauncher<T, 4>::run(st, a, s, row_sched_info, lgcq);
-        case 8: return FwdFlLauncher<T, 8>::run(st, a, s, row_sched_info, lgcq);
-        case 16: return FwdFlLauncher<T, 16>::run(st, a, s, row_sched_info, lgcq);
-        case 32: return FwdFlLauncher<T, 32>::run(st, a, s, row_sched_info, lgcq);
-        default: return FwdFlLauncher<T, 64>::run(st, a, s, row_sched_info, lgcq);
-      }
+      int L, V;
+      fl_geom(dtype, heads, channels, L, V);
+      auto go = [&](auto LC, auto VC) {
+        return FwdFlLauncher<T, decltype(LC)::value, decltype(VC)::value>::run(st, a, s, row_sched_info, lgcq);
+      };
+      return fl_dispatch(L, V, go);
     }
     return dispatch_hc<FwdLauncher, T>(heads, channels, st, a, s);
   };
@@ -286,24 +324,15 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
         return set_error(kInvalid, "cign_gat_bwd: in_feat, pre, grad_y, grad_feat and grad_bias must be 16-byte "
                                    "aligned");
       const int lgcq = fl_lgcq(dtype, channels);
-      const int W = dtype == kBF16 ? 8 : 4;
-      int Lq = 1;
-      while (Lq < heads * channels / W) Lq <<= 1;
-      auto go = [&](auto LC) {
-        constexpr int LL = decltype(LC)::value;
-        a.rows_blocks = BwdFlLauncher<T, LL>::row_blocks(rs, row_sched_info);
+      int L, V;
+      fl_geom(dtype, heads, channels, L, V);
+      auto go = [&](auto LC, auto VC) {
+        constexpr int LL = decltype(LC)::value, VV = decltype(VC)::value;
+        a.rows_blocks = BwdFlLauncher<T, LL, VV>::row_blocks(rs, row_sched_info);
         a.n_l2 = fl_bias_blocks(n);
-        return BwdFlLauncher<T, LL>::run(st, a, rs, row_sched_info, cs, col_sched_info, lgcq);
+        return BwdFlLauncher<T, LL, VV>::run(st, a, rs, row_sched_info, cs, col_sched_info, lgcq);
       };
-      switch (Lq) {
-        case 1: return go(std::integral_constant<int, 1>());
-        case 2: return go(std::integral_constant<int, 2>());
-        case 4: return go(std::integral_constant<int, 4>());
-        case 8: return go(std::integral_constant<int, 8>());
-        case 16: return go(std::integral_constant<int, 16>());
-        case 32: return go(std::integral_constant<int, 32>());
-        default: return go(std::integral_constant<int, 64>());
-      }
+      return fl_dispatch(L, V, go);
     }
     a.rows_blocks = row_blocks;
     a.n_l2 = (row_blocks + 63) / 64;

@@ -1,26 +1,32 @@
 // Collapsed GAT, feature layout: the gfx950 fast path for H <= 8 heads and C
-// a multiple of the 16-byte chunk width W (4 fp32 or 8 bf16 values) with C/W
-// a power of two and H*C/W <= 64 chunks. Semantics are those stated at the top
-// of gat_kernels.h (reference collapsed_gat_cuda.cu:34-430).
+// a multiple of the 16-byte chunk width W (4 fp32 or 8 bf16 values) with
+// cq = C/W a power of two, and either H*cq <= 64 chunks (narrow rows) or cq <=
+// 64 with V = H*cq/64 in {2, 3, 4, 6, 8} chunks per lane (wide rows, e.g. the
+// production H=6 x C=256). Semantics are those stated at the top of
+// gat_kernels.h (reference collapsed_gat_cuda.cu:34-430).
 //
 // Geometry (shared with the SpMM, schedule.h built with light_max = 64 and a
-// segment length that is a multiple of 256). A group of L = pow2ceil(H*C/W) lanes owns one row; lane q
-// owns chunk q of a feature row, i.e. head hq = q / (C/W) and channel chunk
-// cw = q % (C/W). Rows with degree <= L go one per group (64/L rows per
-// wavefront), rows with degree <= 64 one per wavefront (its groups split the
-// edges), heavier rows are segments (one 4-wave workgroup each, rounds of 256
-// edges) whose partial results the last workgroup to finish merges in segment
-// order.
+// segment length that is a multiple of 256). A group of L lanes owns one row;
+// lane gl owns the V chunks q = v*L + gl (v < V) of a feature row, chunk q
+// being head hq = q / cq, channel chunk cw = q % cq. Narrow rows have V = 1
+// and L = pow2ceil(H*cq); wide rows have L = 64 and, as cq divides 64, every
+// chunk of a lane has the same channel chunk cw = gl % cq and its own head.
+// Rows with degree <= L go one per group (64/L rows per wavefront), rows
+// with degree <= 64 one per wavefront (its groups split the edges), heavier
+// rows are segments (one 4-wave workgroup each, rounds of 256 edges) whose
+// partial results the last workgroup to finish merges in segment order.
 //
-// Every lane gathers, for each edge of its batch, the 16-byte chunk of the
-// source feature row AND the source logit of its own head in the same memory
-// round, right after the column index: the softmax is online (running max m,
-// sum s and unnormalised accumulator rescaled per batch, flash style), so no
-// lane-per-edge prologue, LDS staging or per-edge cross-lane reduction sits
-// between the index load and the feature gather. A row costs one dependent
-// round per level of indirection (schedule record -> column index -> source
-// data). The batch size U (1..16) is the wavefront's largest per-group edge
-// count rounded up to a power of two, so short rows issue few wasted loads.
+// Every lane gathers, for each edge of its batch, the 16-byte chunks of the
+// source feature row AND the source logits of its own heads in the same
+// memory round, right after the column index: the softmax is online (running
+// max m, sum s and unnormalised accumulators rescaled per batch, flash
+// style), so no lane-per-edge prologue, LDS staging or per-edge cross-lane
+// reduction sits between the index load and the feature gather. A row costs
+// one dependent round per level of indirection (schedule record -> column
+// index -> source data). The batch size U is the wavefront's largest
+// per-group edge count rounded up to a power of two, capped so that a lane
+// keeps at most 16 (forward, rows) or 8 (columns) edge slots x V chunks in
+// flight.
 //
 // Backward without per-edge reductions. With g = g_pre[i] (= g_y SiLU'(pre)),
 // s the softmax weight, kw = keep/(1-p) (1 without dropout), l' the
@@ -28,14 +34,17 @@
 //   wsum_ih = sum_e s ge'          = <g, sum_e s kw x[j_e,h]> / H
 //   A_ih    = sum_e s ge' l'       = <g, sum_e s kw l' x[j_e,h]> / H
 //   grad_attn_row[i,h] = A - wsum * B,   B = sum_e s l'
-// so the rows kernel accumulates two feature chunks per lane and reduces the
-// dot products once per row. The columns kernel (CSC, column j) uses
+// so the rows pass needs two feature sums per (row, head) and one dot product
+// per row. The forward can save those sums (the per-row aggregates, a.agg);
+// the rows pass then streams them (gat_bwd_rows_agg_kernel), otherwise it
+// gathers the source rows again (gat_bwd_rows_fl_kernel). The columns kernel
+// (CSC, column j) uses
 //   grad_feat[j,h]     = sum_i s kw g_pre[i] / H
 //   grad_attn_col[j,h] = <sum_i s l' kw g_pre[i], x[j,h]> / H - sum_i s l' wsum_i
 // gathering per entry one 16-byte row record {attn_row, edge_max, 1/edge_sum,
-// wsum} (written by the rows kernel) and the g_pre chunk. grad_bias is a
-// deterministic two-level column sum of g_pre done by the columns kernel's
-// trailing workgroups, so the rows kernel has no block barrier on light rows.
+// wsum} per head (written by the rows pass) and the g_pre chunk. grad_bias is
+// a deterministic two-level column sum of g_pre done by the columns kernel's
+// trailing workgroups, so the rows pass has no block barrier on light rows.
 #pragma once
 
 #include "gat_kernels.h"
@@ -45,8 +54,9 @@ namespace gatk {
 
 constexpr int kFlHeads = 8;
 
-// Largest batch (edge slots gathered per lane before any is consumed) of
-// each kernel; the cap trades loads in flight per wave for waves per SIMD.
+// Largest batch (edge slots gathered per lane before any is consumed, times
+// the chunks per lane) of each kernel; the cap trades loads in flight per
+// wave for waves per SIMD.
 #ifndef CIGN_FL_FWD_U
 #define CIGN_FL_FWD_U 16
 #endif
@@ -59,6 +69,11 @@ constexpr int kFlHeads = 8;
 constexpr int kFwdU = CIGN_FL_FWD_U;
 constexpr int kRowsU = CIGN_FL_ROWS_U;
 constexpr int kColsU = CIGN_FL_COLS_U;
+
+// Batch cap for V chunks per lane: the largest power of two <= umax / V.
+constexpr int batch_cap(int umax, int v) {
+  return umax / v >= 16 ? 16 : umax / v >= 8 ? 8 : umax / v >= 4 ? 4 : umax / v >= 2 ? 2 : 1;
+}
 
 // Heavy rows are segments (one workgroup each; any multiple of 256 edges,
 // chosen by the host from the graph size) processed in rounds of kSegRound =
@@ -79,19 +94,25 @@ struct FlGeom {
   static constexpr int W = 16 / sizeof(T);
 };
 
-// Lane geometry of a group of L lanes (one row).
-template <int L>
+// Lane geometry of a group of L lanes (one row) owning V chunks per lane.
+template <int L, int V>
 struct FlLane {
-  int lane, g, gl, q, hq, cw;
-  bool qv;
+  static_assert(V == 1 || L == kWave, "several chunks per lane need a full wavefront per row");
+  int lane, g, gl, cw;
+  int q[V], hq[V];
+  bool qv[V];
   __device__ __forceinline__ FlLane(int lgcq, int nq) {
     lane = lane_id();
     g = lane / L;
     gl = lane & (L - 1);
-    qv = gl < nq;
-    q = qv ? gl : 0;
-    hq = q >> lgcq;
-    cw = q & ((1 << lgcq) - 1);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int qq = v * L + gl;
+      qv[v] = qq < nq;
+      q[v] = qv[v] ? qq : 0;
+      hq[v] = q[v] >> lgcq;
+    }
+    cw = V == 1 ? (q[0] & ((1 << lgcq) - 1)) : (gl & ((1 << lgcq) - 1));
   }
 };
 
@@ -137,7 +158,7 @@ __device__ __forceinline__ float group_sum1(float v) {
   return v;
 }
 
-// Sum over the C/W lanes of a head (lane bits below log2(C/W)).
+// Sum over the cq lanes of a head (lane bits below log2(cq)).
 __device__ __forceinline__ float head_sum(float v, int cq) {
   for (int o = 1; o < cq; o <<= 1) v += shfl_xor(v, o);
   return v;
@@ -146,162 +167,192 @@ __device__ __forceinline__ float head_sum(float v, int cq) {
 // ===========================================================================
 // Forward
 // ===========================================================================
-// Online-softmax state of a lane: running max m, sum s and the unnormalised
-// accumulators acc = sum p kw x, accl = sum p kw l' x, bl = sum p l' (p =
-// exp(score - m)); accl and bl are the per-row aggregates the backward reads
-// instead of gathering the source rows again.
-template <int W>
+// Online-softmax state of a lane, per owned chunk v: running max m, sum s and
+// the unnormalised accumulators acc = sum p kw x, accl = sum p kw l' x, bl =
+// sum p l' (p = exp(score - m)); accl and bl are the per-row aggregates the
+// backward reads instead of gathering the source rows again.
+template <int W, int V>
 struct FwdState {
-  float m, s, bl;
-  float acc[W], accl[W];
+  float m[V], s[V], bl[V];
+  float acc[V][W], accl[V][W];
   __device__ __forceinline__ void clear() {
-    m = kNegBig;
-    s = 0.0f;
-    bl = 0.0f;
 #pragma unroll
-    for (int w = 0; w < W; ++w) acc[w] = accl[w] = 0.0f;
-  }
-  __device__ __forceinline__ void scale(float f) {
-    s *= f;
-    bl *= f;
+    for (int v = 0; v < V; ++v) {
+      m[v] = kNegBig;
+      s[v] = 0.0f;
+      bl[v] = 0.0f;
 #pragma unroll
-    for (int w = 0; w < W; ++w) {
-      acc[w] *= f;
-      accl[w] *= f;
+      for (int w = 0; w < W; ++w) acc[v][w] = accl[v][w] = 0.0f;
     }
   }
-  // state <- state (+) (m2, s2, bl2, acc2, accl2)
-  __device__ __forceinline__ void merge(float m2, float s2, float bl2, const float (&acc2)[W],
+  __device__ __forceinline__ void scale(int v, float f) {
+    s[v] *= f;
+    bl[v] *= f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      acc[v][w] *= f;
+      accl[v][w] *= f;
+    }
+  }
+  // chunk v's state <- state (+) (m2, s2, bl2, acc2, accl2)
+  __device__ __forceinline__ void merge(int v, float m2, float s2, float bl2, const float (&acc2)[W],
                                         const float (&accl2)[W]) {
-    const float mx = fmaxf(m, m2);
-    const float f1 = expf(m - mx), f2 = expf(m2 - mx);
-    s = s * f1 + s2 * f2;
-    bl = bl * f1 + bl2 * f2;
+    const float mx = fmaxf(m[v], m2);
+    const float f1 = expf(m[v] - mx), f2 = expf(m2 - mx);
+    s[v] = s[v] * f1 + s2 * f2;
+    bl[v] = bl[v] * f1 + bl2 * f2;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      acc[w] = acc[w] * f1 + acc2[w] * f2;
-      accl[w] = accl[w] * f1 + accl2[w] * f2;
+      acc[v][w] = acc[v][w] * f1 + acc2[w] * f2;
+      accl[v][w] = accl[v][w] * f1 + accl2[w] * f2;
     }
-    m = mx;
+    m[v] = mx;
   }
 };
 
 // Batches of U edge slots of a lane group: slot u = first + (k0 + k) * step,
 // valid while u < cnt; its column index is held by lane (base + u) of the
 // wavefront, its CSR edge id is ebase + u. DROP: edge dropout (p > 0).
-template <typename T, int L, bool DROP>
+template <typename T, int L, int V, bool DROP>
 struct FwdBatches {
   static constexpr int W = FlGeom<T>::W;
   const GatFwdArgs<T>& a;
-  const FlLane<L>& ln;
+  const FlLane<L, V>& ln;
   int jj, base, first, step, cnt, ebase;
-  float ar;
-  FwdState<W>& st;
+  const float (&ar)[V];
+  FwdState<W, V>& st;
 
   template <int U>
   __device__ __forceinline__ void run(int k0) {
     const int F = a.H * a.C;
-    typename Chunk<T, W>::Raw xb[U];
-    float sc[U];
+    typename Chunk<T, W>::Raw xb[U][V];
+    float sc[U][V];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
       const int j = shfl(jj, (base + (u < cnt ? u : 0)) & (kWave - 1));
-      sc[k] = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq];
-      xb[k] = Chunk<T, W>::load_raw(a.x + static_cast<int64_t>(j) * F + ln.q * W);
-    }
-    // sc[k] becomes the raw score (before LeakyReLU): its sign gives l'.
-    float mx = st.m;
 #pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int u = first + (k0 + k) * step;
-      sc[k] += ar;
-      if (u < cnt) mx = fmaxf(mx, leaky(sc[k], a.slope));
-    }
-    st.scale(expf(st.m - mx));
-    st.m = mx;
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int u = first + (k0 + k) * step;
-      const float pk = u < cnt ? expf(leaky(sc[k], a.slope) - mx) : 0.0f;
-      const float lp = sc[k] < 0.0f ? a.slope : 1.0f;
-      st.s += pk;
-      st.bl = fmaf(pk, lp, st.bl);
-      float wk = pk;
-      if constexpr (DROP) {
-        bool keep = false;
-        if (u < cnt) {
-          const int64_t idx = static_cast<int64_t>(ebase + u) * a.H + ln.hq;
-          keep = gat_keep(a.seed, static_cast<uint64_t>(idx), a.p);
-          if (ln.qv && ln.cw == 0) a.mask[idx] = keep ? 1 : 0;
-        }
-        wk = keep ? pk / (1.0f - a.p) : 0.0f;
+      for (int v = 0; v < V; ++v) {
+        sc[k][v] = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq[v]];
+        xb[k][v] = Chunk<T, W>::load_raw(a.x + static_cast<int64_t>(j) * F + ln.q[v] * W);
       }
-      const float wl = wk * lp;
-      float xv[W];
-      Chunk<T, W>::unpack(xb[k], xv);
+    }
+    // sc becomes the raw score (before LeakyReLU): its sign gives l'.
 #pragma unroll
-      for (int w = 0; w < W; ++w) {
-        st.acc[w] = fmaf(wk, xv[w], st.acc[w]);
-        st.accl[w] = fmaf(wl, xv[w], st.accl[w]);
+    for (int v = 0; v < V; ++v) {
+      float mx = st.m[v];
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        const int u = first + (k0 + k) * step;
+        sc[k][v] += ar[v];
+        if (u < cnt) mx = fmaxf(mx, leaky(sc[k][v], a.slope));
+      }
+      st.scale(v, expf(st.m[v] - mx));
+      st.m[v] = mx;
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int u = first + (k0 + k) * step;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float pk = u < cnt ? expf(leaky(sc[k][v], a.slope) - st.m[v]) : 0.0f;
+        const float lp = sc[k][v] < 0.0f ? a.slope : 1.0f;
+        st.s[v] += pk;
+        st.bl[v] = fmaf(pk, lp, st.bl[v]);
+        float wk = pk;
+        if constexpr (DROP) {
+          bool keep = false;
+          if (u < cnt) {
+            const int64_t idx = static_cast<int64_t>(ebase + u) * a.H + ln.hq[v];
+            keep = gat_keep(a.seed, static_cast<uint64_t>(idx), a.p);
+            if (ln.qv[v] && ln.cw == 0) a.mask[idx] = keep ? 1 : 0;
+          }
+          wk = keep ? pk / (1.0f - a.p) : 0.0f;
+        }
+        const float wl = wk * lp;
+        float xv[W];
+        Chunk<T, W>::unpack(xb[k][v], xv);
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          st.acc[v][w] = fmaf(wk, xv[w], st.acc[v][w]);
+          st.accl[v][w] = fmaf(wl, xv[w], st.accl[v][w]);
+        }
       }
     }
   }
 };
 
 // All edge slots of a lane group: `need` (wave-uniform) slots per group.
-template <typename T, int L, bool DROP>
-__device__ __forceinline__ void fwd_edges(const GatFwdArgs<T>& a, const FlLane<L>& ln, int jj, int base, int first,
-                                          int step, int cnt, int need, int ebase, float ar,
-                                          FwdState<FlGeom<T>::W>& st) {
-  FwdBatches<T, L, DROP> fb{a, ln, jj, base, first, step, cnt, ebase, ar, st};
-  for_batches<kFwdU>(need, fb);
+template <typename T, int L, int V, bool DROP>
+__device__ __forceinline__ void fwd_edges(const GatFwdArgs<T>& a, const FlLane<L, V>& ln, int jj, int base, int first,
+                                          int step, int cnt, int need, int ebase, const float (&ar)[V],
+                                          FwdState<FlGeom<T>::W, V>& st) {
+  FwdBatches<T, L, V, DROP> fb{a, ln, jj, base, first, step, cnt, ebase, ar, st};
+  for_batches<batch_cap(kFwdU, V)>(need, fb);
 }
 
-template <int L, int W>
-__device__ __forceinline__ void fwd_merge_groups(FwdState<W>& st) {
+template <int L, int W, int V>
+__device__ __forceinline__ void fwd_merge_groups(FwdState<W, V>& st) {
 #pragma unroll
-  for (int o = L; o < kWave; o <<= 1) {
-    float a2[W], l2[W];
+  for (int o = L; o < kWave; o <<= 1)
 #pragma unroll
-    for (int w = 0; w < W; ++w) {
-      a2[w] = shfl_xor(st.acc[w], o);
-      l2[w] = shfl_xor(st.accl[w], o);
+    for (int v = 0; v < V; ++v) {
+      float a2[W], l2[W];
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        a2[w] = shfl_xor(st.acc[v][w], o);
+        l2[w] = shfl_xor(st.accl[v][w], o);
+      }
+      const float m2 = shfl_xor(st.m[v], o), s2 = shfl_xor(st.s[v], o), b2 = shfl_xor(st.bl[v], o);
+      st.merge(v, m2, s2, b2, a2, l2);
     }
-    const float m2 = shfl_xor(st.m, o), s2 = shfl_xor(st.s, o), b2 = shfl_xor(st.bl, o);
-    st.merge(m2, s2, b2, a2, l2);
-  }
+}
+
+template <typename T, int L, int V>
+__device__ __forceinline__ void load_attn_row(const GatFwdArgs<T>& a, const FlLane<L, V>& ln, int row,
+                                              float (&ar)[V]) {
+#pragma unroll
+  for (int v = 0; v < V; ++v) ar[v] = a.attn_row[static_cast<int64_t>(row) * a.H + ln.hq[v]];
 }
 
 // Head mean + bias + SiLU of a row; every lane of the wavefront calls this
-// (the head sum is a butterfly inside the group), `write` selects the group
-// that stores. Lane q of head 0 writes channels [cw*W, cw*W + W) of pre/out;
-// lane cw = 0 of each head writes edge_max / edge_sum. With a.agg, lane q
-// also writes its normalised chunks of the two aggregates and lane cw = 0 the
-// head's sum_e s l'.
-template <typename T, int L>
-__device__ __forceinline__ void fwd_emit(const GatFwdArgs<T>& a, const FlLane<L>& ln, int cq, int row, bool write,
-                                         const FwdState<FlGeom<T>::W>& st) {
+// (the head sum is an in-lane sum over the chunks plus a butterfly inside the
+// group), `write` selects the group that stores. Lanes of head 0 write
+// channels [cw*W, cw*W + W) of pre/out; lane cw = 0 of each head writes
+// edge_max / edge_sum. With a.agg, a lane also writes its normalised chunks
+// of the two aggregates and lane cw = 0 the head's sum_e s l'.
+template <typename T, int L, int V>
+__device__ __forceinline__ void fwd_emit(const GatFwdArgs<T>& a, const FlLane<L, V>& ln, int cq, int row, bool write,
+                                         const FwdState<FlGeom<T>::W, V>& st) {
   constexpr int W = FlGeom<T>::W;
-  const float inv = st.s > 0.0f ? 1.0f / st.s : 0.0f;
+  const int F = a.H * a.C;
+  const int64_t nF = static_cast<int64_t>(a.n) * F;
   float y[W];
 #pragma unroll
-  for (int w = 0; w < W; ++w) y[w] = ln.qv ? st.acc[w] * inv : 0.0f;
-  if (a.agg && write && ln.qv) {
-    const int F = a.H * a.C;
-    const int64_t nF = static_cast<int64_t>(a.n) * F;
-    float yl[W];
+  for (int w = 0; w < W; ++w) y[w] = 0.0f;
 #pragma unroll
-    for (int w = 0; w < W; ++w) yl[w] = st.accl[w] * inv;
-    store_f32<W>(a.agg + static_cast<int64_t>(row) * F + ln.q * W, y);
-    store_f32<W>(a.agg + nF + static_cast<int64_t>(row) * F + ln.q * W, yl);
-    if (ln.cw == 0) a.agg[2 * nF + static_cast<int64_t>(row) * a.H + ln.hq] = st.bl * inv;
+  for (int v = 0; v < V; ++v) {
+    const float inv = st.s[v] > 0.0f ? 1.0f / st.s[v] : 0.0f;
+    float yv[W];
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      yv[w] = ln.qv[v] ? st.acc[v][w] * inv : 0.0f;
+      y[w] += yv[w];
+    }
+    if (a.agg && write && ln.qv[v]) {
+      float yl[W];
+#pragma unroll
+      for (int w = 0; w < W; ++w) yl[w] = st.accl[v][w] * inv;
+      store_f32<W>(a.agg + static_cast<int64_t>(row) * F + ln.q[v] * W, yv);
+      store_f32<W>(a.agg + nF + static_cast<int64_t>(row) * F + ln.q[v] * W, yl);
+      if (ln.cw == 0) a.agg[2 * nF + static_cast<int64_t>(row) * a.H + ln.hq[v]] = st.bl[v] * inv;
+    }
   }
   for (int o = cq; o < L; o <<= 1)
 #pragma unroll
     for (int w = 0; w < W; ++w) y[w] += shfl_xor(y[w], o);
-  if (!write || !ln.qv) return;
-  if (ln.hq == 0) {
+  if (!write) return;
+  if (ln.qv[0] && ln.hq[0] == 0) {
     const int64_t base = static_cast<int64_t>(row) * a.C + ln.cw * W;
     float pr[W], o[W];
 #pragma unroll
@@ -312,13 +363,52 @@ __device__ __forceinline__ void fwd_emit(const GatFwdArgs<T>& a, const FlLane<L>
     store_f32<W>(a.pre + base, pr);
     Chunk<T, W>::store(a.out + base, o);
   }
-  if (ln.cw == 0) {
-    a.emax[static_cast<int64_t>(row) * a.H + ln.hq] = st.m;
-    a.esum[static_cast<int64_t>(row) * a.H + ln.hq] = st.s;
+  if (ln.cw == 0)
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      if (ln.qv[v]) {
+        a.emax[static_cast<int64_t>(row) * a.H + ln.hq[v]] = st.m[v];
+        a.esum[static_cast<int64_t>(row) * a.H + ln.hq[v]] = st.s[v];
+      }
+}
+
+// Heavy-segment merge of the four waves' states into wave 0, one wave at a
+// time through one LDS slot of V * 64 * (2W + 3) floats.
+template <int W, int V>
+__device__ __forceinline__ void fwd_merge_waves(FwdState<W, V>& st, float* slot, int wave, int gl, bool publish) {
+  constexpr int S = 2 * W + 3;
+  for (int src = 1; src < kWavesPerBlock; ++src) {
+    if (wave == src && publish)
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        float* d = slot + (v * kWave + gl) * S;
+        d[0] = st.m[v];
+        d[1] = st.s[v];
+        d[2] = st.bl[v];
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          d[3 + w] = st.acc[v][w];
+          d[3 + W + w] = st.accl[v][w];
+        }
+      }
+    __syncthreads();
+    if (wave == 0)
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float* d = slot + (v * kWave + gl) * S;
+        float a2[W], l2[W];
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          a2[w] = d[3 + w];
+          l2[w] = d[3 + W + w];
+        }
+        st.merge(v, d[0], d[1], d[2], a2, l2);
+      }
+    __syncthreads();
   }
 }
 
-template <typename T, int L, bool DROP>
+template <typename T, int L, int V, bool DROP>
 __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sched s, int n_mid, int mid_blocks,
                                                             int lgcq) {
   constexpr int W = FlGeom<T>::W;
@@ -326,10 +416,11 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
   const int cq = 1 << lgcq;
   const int nq = a.H * cq;
   const int F = a.H * a.C;
-  const FlLane<L> ln(lgcq, nq);
+  const FlLane<L, V> ln(lgcq, nq);
   const int wave = wave_id();
-  FwdState<W> st;
+  FwdState<W, V> st;
   st.clear();
+  float ar[V];
   int b = blockIdx.x;
 
   if (b >= s.n_seg) {
@@ -341,10 +432,10 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
       const int4 r = has ? s.light[li] : make_int4(0, 0, 0, 0);
       const int deg = r.z - r.y;
       const int jj = ln.gl < deg ? a.col[r.y + ln.gl] : 0;
-      const float ar = a.attn_row[static_cast<int64_t>(r.x) * a.H + ln.hq];
+      load_attn_row(a, ln, r.x, ar);
       const int need = wave_group_max<L>(deg);
-      fwd_edges<T, L, DROP>(a, ln, jj, ln.g * L, 0, 1, deg, need, r.y, ar, st);
-      fwd_emit<T, L>(a, ln, cq, r.x, has, st);
+      fwd_edges<T, L, V, DROP>(a, ln, jj, ln.g * L, 0, 1, deg, need, r.y, ar, st);
+      fwd_emit<T, L, V>(a, ln, cq, r.x, has, st);
       return;
     }
     // Medium rows (L < degree <= 64): one per wavefront, group g takes edges
@@ -354,89 +445,65 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
     const int4 r = s.light[li];
     const int deg = r.z - r.y;
     const int jj = ln.lane < deg ? a.col[r.y + ln.lane] : 0;
-    const float ar = a.attn_row[static_cast<int64_t>(r.x) * a.H + ln.hq];
-    fwd_edges<T, L, DROP>(a, ln, jj, 0, ln.g, G, deg, (deg + G - 1) / G, r.y, ar, st);
-    fwd_merge_groups<L, W>(st);
-    fwd_emit<T, L>(a, ln, cq, r.x, ln.g == 0, st);
+    load_attn_row(a, ln, r.x, ar);
+    fwd_edges<T, L, V, DROP>(a, ln, jj, 0, ln.g, G, deg, (deg + G - 1) / G, r.y, ar, st);
+    fwd_merge_groups<L, W, V>(st);
+    fwd_emit<T, L, V>(a, ln, cq, r.x, ln.g == 0, st);
     return;
   }
 
   // Heavy-row segment: wave w takes edges [64w, 64w + 64) of every 256-edge
   // round of the segment.
-  __shared__ float hm[kWavesPerBlock][kWave], hs[kWavesPerBlock][kWave], hb[kWavesPerBlock][kWave];
-  __shared__ float hacc[kWavesPerBlock][kWave * W], haccl[kWavesPerBlock][kWave * W];
+  __shared__ float slot[V * kWave * (2 * W + 3)];
   __shared__ int flag;
   const int4 sg = s.seg[b];
   const int row = sg.x;
   const int2 hr = s.hrow[sg.w];
-  const float ar = a.attn_row[static_cast<int64_t>(row) * a.H + ln.hq];
+  load_attn_row(a, ln, row, ar);
   for (int tb = sg.y + wave * kWave; tb < sg.z; tb += kSegRound) {
     const int cnt = min(kWave, sg.z - tb);
     const int jj = ln.lane < cnt ? a.col[tb + ln.lane] : 0;
-    fwd_edges<T, L, DROP>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, ar, st);
+    fwd_edges<T, L, V, DROP>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, ar, st);
   }
-  fwd_merge_groups<L, W>(st);
-  if (ln.g == 0) {
-    hm[wave][ln.gl] = st.m;
-    hs[wave][ln.gl] = st.s;
-    hb[wave][ln.gl] = st.bl;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      hacc[wave][ln.gl * W + w] = st.acc[w];
-      haccl[wave][ln.gl * W + w] = st.accl[w];
-    }
-  }
-  __syncthreads();
-  // Every wave forms the merged state of its lane slot gl (identical copies).
-  st.m = hm[0][ln.gl];
-  st.s = hs[0][ln.gl];
-  st.bl = hb[0][ln.gl];
-#pragma unroll
-  for (int w = 0; w < W; ++w) {
-    st.acc[w] = hacc[0][ln.gl * W + w];
-    st.accl[w] = haccl[0][ln.gl * W + w];
-  }
-#pragma unroll
-  for (int v = 1; v < kWavesPerBlock; ++v) {
-    float a2[W], l2[W];
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      a2[w] = hacc[v][ln.gl * W + w];
-      l2[w] = haccl[v][ln.gl * W + w];
-    }
-    st.merge(hm[v][ln.gl], hs[v][ln.gl], hb[v][ln.gl], a2, l2);
-  }
+  fwd_merge_groups<L, W, V>(st);
+  fwd_merge_waves<W, V>(st, slot, wave, ln.gl, ln.g == 0);
   if (hr.y == 1) {
-    if (wave == 0) fwd_emit<T, L>(a, ln, cq, row, ln.g == 0, st);
+    if (wave == 0) fwd_emit<T, L, V>(a, ln, cq, row, ln.g == 0, st);
     return;
   }
   // Segment partial: acc [F], accl [F], then m, s, bl per head.
   const int stride = 2 * F + 3 * a.H;
   float* mine = a.partial + static_cast<int64_t>(b) * stride;
-  if (wave == 0 && ln.g == 0 && ln.qv) {
-    store_f32<W>(mine + ln.q * W, st.acc);
-    store_f32<W>(mine + F + ln.q * W, st.accl);
-    if (ln.cw == 0) {
-      mine[2 * F + ln.hq] = st.m;
-      mine[2 * F + a.H + ln.hq] = st.s;
-      mine[2 * F + 2 * a.H + ln.hq] = st.bl;
-    }
-  }
+  if (wave == 0 && ln.g == 0)
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      if (ln.qv[v]) {
+        store_f32<W>(mine + ln.q[v] * W, st.acc[v]);
+        store_f32<W>(mine + F + ln.q[v] * W, st.accl[v]);
+        if (ln.cw == 0) {
+          mine[2 * F + ln.hq[v]] = st.m[v];
+          mine[2 * F + a.H + ln.hq[v]] = st.s[v];
+          mine[2 * F + 2 * a.H + ln.hq[v]] = st.bl[v];
+        }
+      }
   if (!arrive_last(a.counters + sg.w, hr.y, &flag)) return;
   if (wave != 0) return;
   // Last segment to finish: merge every segment's partial in segment order.
   st.clear();
   for (int z = 0; z < hr.y; ++z) {
     const float* pz = a.partial + static_cast<int64_t>(hr.x + z) * stride;
-    float a2[W], l2[W];
-    load_f32<W>(pz + ln.q * W, a2);
-    load_f32<W>(pz + F + ln.q * W, l2);
-    st.merge(pz[2 * F + ln.hq], pz[2 * F + a.H + ln.hq], pz[2 * F + 2 * a.H + ln.hq], a2, l2);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float a2[W], l2[W];
+      load_f32<W>(pz + ln.q[v] * W, a2);
+      load_f32<W>(pz + F + ln.q[v] * W, l2);
+      st.merge(v, pz[2 * F + ln.hq[v]], pz[2 * F + a.H + ln.hq[v]], pz[2 * F + 2 * a.H + ln.hq[v]], a2, l2);
+    }
   }
-  fwd_emit<T, L>(a, ln, cq, row, ln.g == 0, st);
+  fwd_emit<T, L, V>(a, ln, cq, row, ln.g == 0, st);
 }
 
-template <typename T, int L>
+template <typename T, int L, int V>
 struct FwdFlLauncher {
   static int run(hipStream_t st, const GatFwdArgs<T>& a, const Sched& s, const int32_t* hdr, int lgcq) {
     constexpr int G = kWave / L;
@@ -446,10 +513,10 @@ struct FwdFlLauncher {
     const int blocks = s.n_seg + mid_blocks + (n_tiny + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
     if (blocks > 0) {
       if (a.p > 0.0f)
-        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, true>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
+        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, true>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
                            mid_blocks, lgcq);
       else
-        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, false>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
+        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, false>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
                            mid_blocks, lgcq);
     }
     return check_launch("cign_gat_fwd (feature layout)");
@@ -459,83 +526,112 @@ struct FwdFlLauncher {
 // ===========================================================================
 // Backward, rows (CSR)
 // ===========================================================================
-template <int W>
+template <int W, int V>
 struct RowAcc {
-  float vs[W], vsl[W];
-  float B;
+  float vs[V][W], vsl[V][W];
+  float B[V];
   __device__ __forceinline__ void clear() {
 #pragma unroll
-    for (int w = 0; w < W; ++w) vs[w] = vsl[w] = 0.0f;
-    B = 0.0f;
+    for (int v = 0; v < V; ++v) {
+#pragma unroll
+      for (int w = 0; w < W; ++w) vs[v][w] = vsl[v][w] = 0.0f;
+      B[v] = 0.0f;
+    }
   }
 };
 
-// Per-row constants of a lane's head.
+// Per-row constants of a lane's heads: attn_row, edge_max, 1 / edge_sum (0
+// for an empty row).
+template <int V>
 struct RowHead {
-  float ar, em, ies;  // attn_row, edge_max, 1 / edge_sum (0 for an empty row)
+  float ar[V], em[V], ies[V];
 };
 
 template <typename T>
-__device__ __forceinline__ RowHead row_head(const GatBwdArgs<T>& a, int row, int hq) {
+__device__ __forceinline__ void row_head1(const GatBwdArgs<T>& a, int row, int hq, float& ar, float& em,
+                                          float& ies) {
   const int64_t rh = static_cast<int64_t>(row) * a.H + hq;
-  RowHead h;
-  h.ar = a.attn_row[rh];
-  h.em = a.emax[rh];
+  ar = a.attn_row[rh];
+  em = a.emax[rh];
   const float es = a.esum[rh];
-  h.ies = es > 0.0f ? 1.0f / es : 0.0f;
+  ies = es > 0.0f ? 1.0f / es : 0.0f;
+}
+
+template <typename T, int L, int V>
+__device__ __forceinline__ RowHead<V> row_head(const GatBwdArgs<T>& a, int row, const FlLane<L, V>& ln) {
+  RowHead<V> h;
+#pragma unroll
+  for (int v = 0; v < V; ++v) row_head1(a, row, ln.hq[v], h.ar[v], h.em[v], h.ies[v]);
   return h;
 }
 
-template <typename T, int L, bool DROP>
+template <typename T, int L, int V, bool DROP>
 struct RowBatches {
   static constexpr int W = FlGeom<T>::W;
   const GatBwdArgs<T>& a;
-  const FlLane<L>& ln;
+  const FlLane<L, V>& ln;
   int jj, base, first, step, cnt, ebase;
-  const RowHead& rh;
-  RowAcc<W>& st;
+  const RowHead<V>& rh;
+  RowAcc<W, V>& st;
 
   template <int U>
   __device__ __forceinline__ void run(int k0) {
     const int F = a.H * a.C;
-    typename Chunk<T, W>::Raw xb[U];
-    float ab[U];
-    float kw[U];
+    typename Chunk<T, W>::Raw xb[U][V];
+    float ab[U][V];
+    float kw[U][V];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
       const int j = shfl(jj, (base + (u < cnt ? u : 0)) & (kWave - 1));
-      ab[k] = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq];
-      xb[k] = Chunk<T, W>::load_raw(a.x + static_cast<int64_t>(j) * F + ln.q * W);
-      if constexpr (DROP) kw[k] = (u < cnt && a.mask[static_cast<int64_t>(ebase + u) * a.H + ln.hq]) ? 1.0f : 0.0f;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        ab[k][v] = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq[v]];
+        xb[k][v] = Chunk<T, W>::load_raw(a.x + static_cast<int64_t>(j) * F + ln.q[v] * W);
+        if constexpr (DROP)
+          kw[k][v] = (u < cnt && a.mask[static_cast<int64_t>(ebase + u) * a.H + ln.hq[v]]) ? 1.0f : 0.0f;
+      }
     }
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
-      const float raw = rh.ar + ab[k];
-      const float lp = raw < 0.0f ? a.slope : 1.0f;
-      const float sm = u < cnt ? expf(leaky(raw, a.slope) - rh.em) * rh.ies : 0.0f;
-      float sk = sm;
-      if constexpr (DROP) sk = kw[k] != 0.0f ? sm / (1.0f - a.p) : 0.0f;
-      const float skl = sk * lp;
-      st.B = fmaf(sm, lp, st.B);
-      float xv[W];
-      Chunk<T, W>::unpack(xb[k], xv);
 #pragma unroll
-      for (int w = 0; w < W; ++w) {
-        st.vs[w] = fmaf(sk, xv[w], st.vs[w]);
-        st.vsl[w] = fmaf(skl, xv[w], st.vsl[w]);
+      for (int v = 0; v < V; ++v) {
+        const float raw = rh.ar[v] + ab[k][v];
+        const float lp = raw < 0.0f ? a.slope : 1.0f;
+        const float sm = u < cnt ? expf(leaky(raw, a.slope) - rh.em[v]) * rh.ies[v] : 0.0f;
+        float sk = sm;
+        if constexpr (DROP) sk = kw[k][v] != 0.0f ? sm / (1.0f - a.p) : 0.0f;
+        const float skl = sk * lp;
+        st.B[v] = fmaf(sm, lp, st.B[v]);
+        float xv[W];
+        Chunk<T, W>::unpack(xb[k][v], xv);
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          st.vs[v][w] = fmaf(sk, xv[w], st.vs[v][w]);
+          st.vsl[v][w] = fmaf(skl, xv[w], st.vsl[v][w]);
+        }
       }
     }
   }
 };
 
-template <typename T, int L, bool DROP>
-__device__ __forceinline__ void rows_edges(const GatBwdArgs<T>& a, const FlLane<L>& ln, int jj, int base, int first,
-                                           int step, int cnt, int need, int ebase, const RowHead& rh,
-                                           RowAcc<FlGeom<T>::W>& st) {
-  RowBatches<T, L, DROP> rb{a, ln, jj, base, first, step, cnt, ebase, rh, st};
-  for_batches<kRowsU>(need, rb);
+template <typename T, int L, int V, bool DROP>
+__device__ __forceinline__ void rows_edges(const GatBwdArgs<T>& a, const FlLane<L, V>& ln, int jj, int base,
+                                           int first, int step, int cnt, int need, int ebase, const RowHead<V>& rh,
+                                           RowAcc<FlGeom<T>::W, V>& st) {
+  RowBatches<T, L, V, DROP> rb{a, ln, jj, base, first, step, cnt, ebase, rh, st};
+  for_batches<batch_cap(kRowsU, V)>(need, rb);
+}
+
+template <int L, int W, int V>
+__device__ __forceinline__ void rows_group_sum(RowAcc<W, V>& st) {
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    group_sum<L, W>(st.vs[v]);
+    group_sum<L, W>(st.vsl[v]);
+    st.B[v] = group_sum1<L>(st.B[v]);
+  }
 }
 
 // g_pre chunk cw of a row: g_y * SiLU'(pre).
@@ -551,43 +647,61 @@ __device__ __forceinline__ void grad_pre_chunk(const GatBwdArgs<T>& a, int row, 
   for (int w = 0; w < W; ++w) gp[w] = gy[w] * silu_grad(pr[w]);
 }
 
-// (wsum, A) of the lane's head from the accumulated chunks: dot with g_pre,
-// summed over the head's C/W lanes, divided by H.
-template <int W>
-__device__ __forceinline__ void rows_dots(const RowAcc<W>& st, const float (&gp)[W], int cq, float inv_h, float& wsum,
-                                          float& A) {
-  float d1 = 0.0f, d2 = 0.0f;
+// (wsum, A) of each of the lane's heads from the accumulated chunks: dot with
+// g_pre, summed over the head's cq lanes, divided by H.
+template <int W, int V>
+__device__ __forceinline__ void rows_dots(const RowAcc<W, V>& st, const float (&gp)[W], int cq, float inv_h,
+                                          float (&wsum)[V], float (&A)[V]) {
 #pragma unroll
-  for (int w = 0; w < W; ++w) {
-    d1 = fmaf(gp[w], st.vs[w], d1);
-    d2 = fmaf(gp[w], st.vsl[w], d2);
+  for (int v = 0; v < V; ++v) {
+    float d1 = 0.0f, d2 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      d1 = fmaf(gp[w], st.vs[v][w], d1);
+      d2 = fmaf(gp[w], st.vsl[v][w], d2);
+    }
+    wsum[v] = head_sum(d1, cq) * inv_h;
+    A[v] = head_sum(d2, cq) * inv_h;
   }
-  wsum = head_sum(d1, cq) * inv_h;
-  A = head_sum(d2, cq) * inv_h;
 }
 
 template <typename T>
-__device__ __forceinline__ void rows_store(const GatBwdArgs<T>& a, int row, int hq, const RowHead& rh, float wsum,
-                                           float A, float B) {
+__device__ __forceinline__ void rows_store(const GatBwdArgs<T>& a, int row, int hq, float ar, float em, float ies,
+                                           float wsum, float A, float B) {
   const int64_t idx = static_cast<int64_t>(row) * a.H + hq;
   a.grad_attn_row[idx] = A - wsum * B;
-  a.rowstat[idx] = make_float4(rh.ar, rh.em, rh.ies, wsum);
+  a.rowstat[idx] = make_float4(ar, em, ies, wsum);
 }
 
-template <typename T, int L, bool DROP>
+// Lane stores of a finished light row: grad_attn_row / rowstat of its heads
+// (lanes cw = 0) and the g_pre chunk (head-0 lanes).
+template <typename T, int L, int V>
+__device__ __forceinline__ void rows_emit(const GatBwdArgs<T>& a, const FlLane<L, V>& ln, int row,
+                                          const RowHead<V>& rh, const float (&wsum)[V], const float (&A)[V],
+                                          const float (&B)[V], const float (&gp)[FlGeom<T>::W]) {
+  constexpr int W = FlGeom<T>::W;
+  if (ln.cw == 0)
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      if (ln.qv[v]) rows_store(a, row, ln.hq[v], rh.ar[v], rh.em[v], rh.ies[v], wsum[v], A[v], B[v]);
+  if (ln.qv[0] && ln.hq[0] == 0) store_f32<W>(a.grad_pre + static_cast<int64_t>(row) * a.C + ln.cw * W, gp);
+}
+
+template <typename T, int L, int V, bool DROP>
 __global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a, Sched s, int n_mid, int mid_blocks,
                                                                  int lgcq) {
   constexpr int W = FlGeom<T>::W;
   constexpr int G = kWave / L;
   const int cq = 1 << lgcq;
   const int nq = a.H * cq;
-  const FlLane<L> ln(lgcq, nq);
+  const FlLane<L, V> ln(lgcq, nq);
   const int wave = wave_id();
   __shared__ float red[kWavesPerBlock][3][kFlHeads];
   __shared__ int flag;
-  RowAcc<W> st;
+  RowAcc<W, V> st;
   st.clear();
   float gp[W];
+  float wsum[V], A[V];
   int b = blockIdx.x;
 
   if (b >= s.n_seg) {
@@ -608,21 +722,16 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a
     const int deg = r.z - r.y;
     const int slot = tiny ? ln.gl : ln.lane;
     const int jj = slot < deg ? a.col[r.y + slot] : 0;
-    const RowHead rh = row_head(a, row, ln.hq);
+    const RowHead<V> rh = row_head(a, row, ln);
     grad_pre_chunk(a, row, ln.cw, gp);
     if (tiny) {
-      rows_edges<T, L, DROP>(a, ln, jj, ln.g * L, 0, 1, deg, wave_group_max<L>(deg), r.y, rh, st);
+      rows_edges<T, L, V, DROP>(a, ln, jj, ln.g * L, 0, 1, deg, wave_group_max<L>(deg), r.y, rh, st);
     } else {
-      rows_edges<T, L, DROP>(a, ln, jj, 0, ln.g, G, deg, (deg + G - 1) / G, r.y, rh, st);
-      group_sum<L, W>(st.vs);
-      group_sum<L, W>(st.vsl);
-      st.B = group_sum1<L>(st.B);
+      rows_edges<T, L, V, DROP>(a, ln, jj, 0, ln.g, G, deg, (deg + G - 1) / G, r.y, rh, st);
+      rows_group_sum<L, W, V>(st);
     }
-    float wsum, A;
-    rows_dots<W>(st, gp, cq, a.inv_h, wsum, A);
-    const bool write = has && (tiny || ln.g == 0) && ln.qv;
-    if (write && ln.cw == 0) rows_store(a, row, ln.hq, rh, wsum, A, st.B);
-    if (write && ln.hq == 0) store_f32<W>(a.grad_pre + static_cast<int64_t>(row) * a.C + ln.cw * W, gp);
+    rows_dots<W, V>(st, gp, cq, a.inv_h, wsum, A);
+    if (has && (tiny || ln.g == 0)) rows_emit(a, ln, row, rh, wsum, A, st.B, gp);
     return;
   }
 
@@ -631,25 +740,25 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a
   const int4 sg = s.seg[b];
   const int row = sg.x;
   const int2 hr = s.hrow[sg.w];
-  const RowHead rh = row_head(a, row, ln.hq);
+  const RowHead<V> rh = row_head(a, row, ln);
   grad_pre_chunk(a, row, ln.cw, gp);
   for (int tb = sg.y + wave * kWave; tb < sg.z; tb += kSegRound) {
     const int cnt = min(kWave, sg.z - tb);
     const int jj = ln.lane < cnt ? a.col[tb + ln.lane] : 0;
-    rows_edges<T, L, DROP>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, rh, st);
+    rows_edges<T, L, V, DROP>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, rh, st);
   }
-  group_sum<L, W>(st.vs);
-  group_sum<L, W>(st.vsl);
-  st.B = group_sum1<L>(st.B);
-  float wsum, A;
-  rows_dots<W>(st, gp, cq, a.inv_h, wsum, A);
-  if (ln.g == 0 && ln.qv && ln.cw == 0) {
-    red[wave][0][ln.hq] = wsum;
-    red[wave][1][ln.hq] = A;
-    red[wave][2][ln.hq] = st.B;
-  }
+  rows_group_sum<L, W, V>(st);
+  rows_dots<W, V>(st, gp, cq, a.inv_h, wsum, A);
+  if (ln.g == 0 && ln.cw == 0)
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      if (ln.qv[v]) {
+        red[wave][0][ln.hq[v]] = wsum[v];
+        red[wave][1][ln.hq[v]] = A[v];
+        red[wave][2][ln.hq[v]] = st.B[v];
+      }
   // The row's g_pre is published once, by its first segment.
-  if (b == hr.x && wave == 0 && ln.g == 0 && ln.qv && ln.hq == 0)
+  if (b == hr.x && wave == 0 && ln.g == 0 && ln.qv[0] && ln.hq[0] == 0)
     store_f32<W>(a.grad_pre + static_cast<int64_t>(row) * a.C + ln.cw * W, gp);
   __syncthreads();
   if (threadIdx.x < 3 * kFlHeads) {
@@ -660,7 +769,9 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a
   if (hr.y == 1) {
     if (threadIdx.x < a.H) {
       const int h = threadIdx.x;
-      rows_store(a, row, h, row_head(a, row, h), red[0][0][h], red[0][1][h], red[0][2][h]);
+      float ar, em, ies;
+      row_head1(a, row, h, ar, em, ies);
+      rows_store(a, row, h, ar, em, ies, red[0][0][h], red[0][1][h], red[0][2][h]);
     }
     return;
   }
@@ -676,118 +787,153 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a
       AA += pz[a.H + h];
       BB += pz[2 * a.H + h];
     }
-    rows_store(a, row, h, row_head(a, row, h), w, AA, BB);
+    float ar, em, ies;
+    row_head1(a, row, h, ar, em, ies);
+    rows_store(a, row, h, ar, em, ies, w, AA, BB);
   }
 }
 
 // Rows pass from the forward's per-row aggregates (a.agg): the same
 // (wsum, A, B) as gat_bwd_rows_fl_kernel without gathering any source row, a
 // stream over the rows. A group of L lanes per row, G rows per wavefront.
-template <typename T, int L>
+template <typename T, int L, int V>
 __global__ __launch_bounds__(kBlock) void gat_bwd_rows_agg_kernel(GatBwdArgs<T> a, int lgcq) {
   constexpr int W = FlGeom<T>::W;
   constexpr int G = kWave / L;
   const int cq = 1 << lgcq;
-  const FlLane<L> ln(lgcq, a.H * cq);
+  const FlLane<L, V> ln(lgcq, a.H * cq);
   const int row = (blockIdx.x * kWavesPerBlock + wave_id()) * G + ln.g;
   if (row >= a.n) return;  // no barrier follows
   const int F = a.H * a.C;
   const int64_t nF = static_cast<int64_t>(a.n) * F;
-  RowAcc<W> st;
-  load_f32<W>(a.agg + static_cast<int64_t>(row) * F + ln.q * W, st.vs);
-  load_f32<W>(a.agg + nF + static_cast<int64_t>(row) * F + ln.q * W, st.vsl);
-  st.B = a.agg[2 * nF + static_cast<int64_t>(row) * a.H + ln.hq];
+  RowAcc<W, V> st;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    load_f32<W>(a.agg + static_cast<int64_t>(row) * F + ln.q[v] * W, st.vs[v]);
+    load_f32<W>(a.agg + nF + static_cast<int64_t>(row) * F + ln.q[v] * W, st.vsl[v]);
+    st.B[v] = a.agg[2 * nF + static_cast<int64_t>(row) * a.H + ln.hq[v]];
+  }
   float gp[W];
   grad_pre_chunk(a, row, ln.cw, gp);
-  float wsum, A;
-  rows_dots<W>(st, gp, cq, a.inv_h, wsum, A);
-  if (!ln.qv) return;
-  if (ln.cw == 0) rows_store(a, row, ln.hq, row_head(a, row, ln.hq), wsum, A, st.B);
-  if (ln.hq == 0) store_f32<W>(a.grad_pre + static_cast<int64_t>(row) * a.C + ln.cw * W, gp);
+  float wsum[V], A[V];
+  rows_dots<W, V>(st, gp, cq, a.inv_h, wsum, A);
+  rows_emit(a, ln, row, row_head(a, row, ln), wsum, A, st.B, gp);
 }
 
 // ===========================================================================
 // Backward, columns (CSC)
 // ===========================================================================
-template <int W>
+template <int W, int V>
 struct ColAcc {
-  float ug[W], ua[W];
-  float t;
+  float ug[V][W], ua[V][W];
+  float t[V];
   __device__ __forceinline__ void clear() {
 #pragma unroll
-    for (int w = 0; w < W; ++w) ug[w] = ua[w] = 0.0f;
-    t = 0.0f;
+    for (int v = 0; v < V; ++v) {
+#pragma unroll
+      for (int w = 0; w < W; ++w) ug[v][w] = ua[v][w] = 0.0f;
+      t[v] = 0.0f;
+    }
   }
 };
 
 // Batches of CSC entries of column j: slot u's destination row is held by
-// lane (base + u) in ii, its CSR edge id (used only with dropout) in ee.
-template <typename T, int L, bool DROP>
+// lane (base + u) in ii, its CSR edge id (used only with dropout) in ee. The
+// g_pre chunk of a destination row is shared by the lane's V heads.
+template <typename T, int L, int V, bool DROP>
 struct ColBatches {
   static constexpr int W = FlGeom<T>::W;
   const GatBwdArgs<T>& a;
-  const FlLane<L>& ln;
+  const FlLane<L, V>& ln;
   int ii, ee, base, first, step, cnt;
-  float ac;
-  ColAcc<W>& st;
+  const float (&ac)[V];
+  ColAcc<W, V>& st;
 
   template <int U>
   __device__ __forceinline__ void run(int k0) {
     float gb[U][W];
-    float4 rs[U];
-    float kw[U];
+    float4 rs[U][V];
+    float kw[U][V];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
       const int src = (base + (u < cnt ? u : 0)) & (kWave - 1);
       const int i = shfl(ii, src);
-      rs[k] = a.rowstat[static_cast<int64_t>(i) * a.H + ln.hq];
       load_f32<W>(a.grad_pre + static_cast<int64_t>(i) * a.C + ln.cw * W, gb[k]);
-      if constexpr (DROP) {
-        const int e = shfl(ee, src);
-        kw[k] = (u < cnt && a.mask[static_cast<int64_t>(e) * a.H + ln.hq]) ? 1.0f : 0.0f;
+      int e = 0;
+      if constexpr (DROP) e = shfl(ee, src);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        rs[k][v] = a.rowstat[static_cast<int64_t>(i) * a.H + ln.hq[v]];
+        if constexpr (DROP)
+          kw[k][v] = (u < cnt && a.mask[static_cast<int64_t>(e) * a.H + ln.hq[v]]) ? 1.0f : 0.0f;
       }
     }
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
-      const float raw = rs[k].x + ac;
-      const float lp = raw < 0.0f ? a.slope : 1.0f;
-      const float sm = u < cnt ? expf(leaky(raw, a.slope) - rs[k].y) * rs[k].z : 0.0f;
-      float w = sm;
-      if constexpr (DROP) w = kw[k] != 0.0f ? sm / (1.0f - a.p) : 0.0f;
-      const float wl = w * lp;
-      st.t = fmaf(sm * lp, rs[k].w, st.t);
 #pragma unroll
-      for (int q = 0; q < W; ++q) {
-        st.ug[q] = fmaf(w, gb[k][q], st.ug[q]);
-        st.ua[q] = fmaf(wl, gb[k][q], st.ua[q]);
+      for (int v = 0; v < V; ++v) {
+        const float raw = rs[k][v].x + ac[v];
+        const float lp = raw < 0.0f ? a.slope : 1.0f;
+        const float sm = u < cnt ? expf(leaky(raw, a.slope) - rs[k][v].y) * rs[k][v].z : 0.0f;
+        float w = sm;
+        if constexpr (DROP) w = kw[k][v] != 0.0f ? sm / (1.0f - a.p) : 0.0f;
+        const float wl = w * lp;
+        st.t[v] = fmaf(sm * lp, rs[k][v].w, st.t[v]);
+#pragma unroll
+        for (int q = 0; q < W; ++q) {
+          st.ug[v][q] = fmaf(w, gb[k][q], st.ug[v][q]);
+          st.ua[v][q] = fmaf(wl, gb[k][q], st.ua[v][q]);
+        }
       }
     }
   }
 };
 
-template <typename T, int L, bool DROP>
-__device__ __forceinline__ void cols_edges(const GatBwdArgs<T>& a, const FlLane<L>& ln, int ii, int ee, int base,
-                                           int first, int step, int cnt, int need, float ac,
-                                           ColAcc<FlGeom<T>::W>& st) {
-  ColBatches<T, L, DROP> cb{a, ln, ii, ee, base, first, step, cnt, ac, st};
-  for_batches<kColsU>(need, cb);
+template <typename T, int L, int V, bool DROP>
+__device__ __forceinline__ void cols_edges(const GatBwdArgs<T>& a, const FlLane<L, V>& ln, int ii, int ee, int base,
+                                           int first, int step, int cnt, int need, const float (&ac)[V],
+                                           ColAcc<FlGeom<T>::W, V>& st) {
+  ColBatches<T, L, V, DROP> cb{a, ln, ii, ee, base, first, step, cnt, ac, st};
+  for_batches<batch_cap(kColsU, V)>(need, cb);
 }
 
-// The lane's part of grad_attn_col[j, hq]: <ua, x[j] chunk> summed over the
-// head's lanes / H, minus t.
-template <typename T>
-__device__ __forceinline__ float cols_gac(const GatBwdArgs<T>& a, const ColAcc<FlGeom<T>::W>& st,
-                                          const float (&xj)[FlGeom<T>::W], int cq) {
-  constexpr int W = FlGeom<T>::W;
-  float d = 0.0f;
+template <int L, int W, int V>
+__device__ __forceinline__ void cols_group_sum(ColAcc<W, V>& st) {
 #pragma unroll
-  for (int w = 0; w < W; ++w) d = fmaf(st.ua[w], xj[w], d);
-  return head_sum(d, cq) * a.inv_h - st.t;
+  for (int v = 0; v < V; ++v) {
+    group_sum<L, W>(st.ug[v]);
+    group_sum<L, W>(st.ua[v]);
+    st.t[v] = group_sum1<L>(st.t[v]);
+  }
 }
 
-template <typename T, int L, bool DROP>
+// The lane's part of grad_attn_col[j, hq[v]] for each chunk v: <ua, x[j]
+// chunk> summed over the head's lanes / H, minus t.
+template <typename T, int L, int V>
+__device__ __forceinline__ void cols_gac(const GatBwdArgs<T>& a, const FlLane<L, V>& ln, const ColAcc<FlGeom<T>::W, V>& st,
+                                         int j, int cq, float (&gac)[V]) {
+  constexpr int W = FlGeom<T>::W;
+  const int F = a.H * a.C;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    float xj[W];
+    Chunk<T, W>::load(a.x + static_cast<int64_t>(j) * F + ln.q[v] * W, xj);
+    float d = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) d = fmaf(st.ua[v][w], xj[w], d);
+    gac[v] = head_sum(d, cq) * a.inv_h - st.t[v];
+  }
+}
+
+template <typename T, int L, int V>
+__device__ __forceinline__ void load_attn_col(const GatBwdArgs<T>& a, const FlLane<L, V>& ln, int j, float (&ac)[V]) {
+#pragma unroll
+  for (int v = 0; v < V; ++v) ac[v] = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq[v]];
+}
+
+template <typename T, int L, int V, bool DROP>
 __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a, Sched s, int n_mid, int mid_blocks,
                                                                  int lgcq) {
   constexpr int W = FlGeom<T>::W;
@@ -795,9 +941,9 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
   const int cq = 1 << lgcq;
   const int nq = a.H * cq;
   const int F = a.H * a.C;
-  const FlLane<L> ln(lgcq, nq);
+  const FlLane<L, V> ln(lgcq, nq);
   const int wave = wave_id();
-  __shared__ float red[kWavesPerBlock][kWave * W];
+  __shared__ float red[V * kWave * W];
   __shared__ float gred[kWavesPerBlock][kFlHeads];
   __shared__ int flag;
   int b = blockIdx.x;
@@ -806,8 +952,9 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
     bias_from_grad_pre(a, b - nsched, a.col_counters + s.n_hrow, &flag);
     return;
   }
-  ColAcc<W> st;
+  ColAcc<W, V> st;
   st.clear();
+  float ac[V], gac[V];
 
   if (b >= s.n_seg) {
     b -= s.n_seg;
@@ -830,57 +977,65 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
     const bool own = slot < deg;
     const int ii = own ? a.rowind[r.y + slot] : 0;
     const int ee = (DROP && own) ? a.perm[r.y + slot] : 0;
-    const float ac = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq];
-    float xj[W];
-    Chunk<T, W>::load(a.x + static_cast<int64_t>(j) * F + ln.q * W, xj);
+    load_attn_col(a, ln, j, ac);
     if (tiny) {
-      cols_edges<T, L, DROP>(a, ln, ii, ee, ln.g * L, 0, 1, deg, wave_group_max<L>(deg), ac, st);
+      cols_edges<T, L, V, DROP>(a, ln, ii, ee, ln.g * L, 0, 1, deg, wave_group_max<L>(deg), ac, st);
     } else {
-      cols_edges<T, L, DROP>(a, ln, ii, ee, 0, ln.g, G, deg, (deg + G - 1) / G, ac, st);
-      group_sum<L, W>(st.ug);
-      group_sum<L, W>(st.ua);
-      st.t = group_sum1<L>(st.t);
+      cols_edges<T, L, V, DROP>(a, ln, ii, ee, 0, ln.g, G, deg, (deg + G - 1) / G, ac, st);
+      cols_group_sum<L, W, V>(st);
     }
-    const float gac = cols_gac(a, st, xj, cq);
-    if (!(has && (tiny || ln.g == 0) && ln.qv)) return;
-    float o[W];
+    cols_gac(a, ln, st, j, cq, gac);
+    if (!(has && (tiny || ln.g == 0))) return;
 #pragma unroll
-    for (int w = 0; w < W; ++w) o[w] = st.ug[w] * a.inv_h;
-    Chunk<T, W>::store(a.grad_feat + static_cast<int64_t>(j) * F + ln.q * W, o);
-    if (ln.cw == 0) a.grad_attn_col[static_cast<int64_t>(j) * a.H + ln.hq] = gac;
+    for (int v = 0; v < V; ++v) {
+      if (!ln.qv[v]) continue;
+      float o[W];
+#pragma unroll
+      for (int w = 0; w < W; ++w) o[w] = st.ug[v][w] * a.inv_h;
+      Chunk<T, W>::store(a.grad_feat + static_cast<int64_t>(j) * F + ln.q[v] * W, o);
+      if (ln.cw == 0) a.grad_attn_col[static_cast<int64_t>(j) * a.H + ln.hq[v]] = gac[v];
+    }
     return;
   }
 
   // Heavy column segment: wave w takes entries [64w, 64w + 64) of every
-  // 256-entry round of the segment.
+  // 256-entry round of the segment; the waves' sums meet in one LDS slot.
   const int4 sg = s.seg[b];
   const int j = sg.x;
   const int2 hr = s.hrow[sg.w];
-  const float ac = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq];
-  float xj[W];
-  Chunk<T, W>::load(a.x + static_cast<int64_t>(j) * F + ln.q * W, xj);
+  load_attn_col(a, ln, j, ac);
   for (int tb = sg.y + wave * kWave; tb < sg.z; tb += kSegRound) {
     const int cnt = min(kWave, sg.z - tb);
     const bool own = ln.lane < cnt;
     const int ii = own ? a.rowind[tb + ln.lane] : 0;
     const int ee = (DROP && own) ? a.perm[tb + ln.lane] : 0;
-    cols_edges<T, L, DROP>(a, ln, ii, ee, 0, ln.g, G, cnt, (cnt + G - 1) / G, ac, st);
+    cols_edges<T, L, V, DROP>(a, ln, ii, ee, 0, ln.g, G, cnt, (cnt + G - 1) / G, ac, st);
   }
-  group_sum<L, W>(st.ug);
-  group_sum<L, W>(st.ua);
-  st.t = group_sum1<L>(st.t);
-  const float gac = cols_gac(a, st, xj, cq);
-  if (ln.g == 0 && ln.qv) {
+  cols_group_sum<L, W, V>(st);
+  cols_gac(a, ln, st, j, cq, gac);
+  if (ln.g == 0 && ln.cw == 0)
 #pragma unroll
-    for (int w = 0; w < W; ++w) red[wave][ln.q * W + w] = st.ug[w];
-    if (ln.cw == 0) gred[wave][ln.hq] = gac;
+    for (int v = 0; v < V; ++v)
+      if (ln.qv[v]) gred[wave][ln.hq[v]] = gac[v];
+  // red[q * W + w] (feature order) = sum of the waves' ug, added one wave at
+  // a time.
+  for (int src = 0; src < kWavesPerBlock; ++src) {
+    if (wave == src && ln.g == 0)
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        if (ln.qv[v])
+#pragma unroll
+          for (int w = 0; w < W; ++w) {
+            float& d = red[ln.q[v] * W + w];
+            d = src == 0 ? st.ug[v][w] : d + st.ug[v][w];
+          }
+    __syncthreads();
   }
-  __syncthreads();
   const bool single = hr.y == 1;
   const int stride = F + a.H;
   float* mine = a.part_col + static_cast<int64_t>(b) * stride;
   for (int k = threadIdx.x; k < F; k += kBlock) {
-    const float v = red[0][k] + red[1][k] + red[2][k] + red[3][k];
+    const float v = red[k];
     if (single) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<T>(v * a.inv_h);
     else mine[k] = v;
   }
@@ -900,7 +1055,7 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
   }
 }
 
-template <typename T, int L>
+template <typename T, int L, int V>
 struct BwdFlLauncher {
   static int row_blocks(const Sched& rs, const int32_t* rhdr) {
     constexpr int G = kWave / L;
@@ -918,16 +1073,16 @@ struct BwdFlLauncher {
     if (a.agg) {
       const int ab = (a.n + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
       if (ab > 0) {
-        hipLaunchKernelGGL((gat_bwd_rows_agg_kernel<T, L>), dim3(ab), dim3(kBlock), 0, st, a, lgcq);
+        hipLaunchKernelGGL((gat_bwd_rows_agg_kernel<T, L, V>), dim3(ab), dim3(kBlock), 0, st, a, lgcq);
         const int rc = check_launch("cign_gat_bwd (rows from aggregates, feature layout)");
         if (rc) return rc;
       }
     } else if (rb > 0) {
       if (a.p > 0.0f)
-        hipLaunchKernelGGL((gat_bwd_rows_fl_kernel<T, L, true>), dim3(rb), dim3(kBlock), 0, st, a, rs, r_mid,
+        hipLaunchKernelGGL((gat_bwd_rows_fl_kernel<T, L, V, true>), dim3(rb), dim3(kBlock), 0, st, a, rs, r_mid,
                            r_mid_blocks, lgcq);
       else
-        hipLaunchKernelGGL((gat_bwd_rows_fl_kernel<T, L, false>), dim3(rb), dim3(kBlock), 0, st, a, rs, r_mid,
+        hipLaunchKernelGGL((gat_bwd_rows_fl_kernel<T, L, V, false>), dim3(rb), dim3(kBlock), 0, st, a, rs, r_mid,
                            r_mid_blocks, lgcq);
       const int rc = check_launch("cign_gat_bwd (rows, feature layout)");
       if (rc) return rc;
@@ -938,47 +1093,33 @@ struct BwdFlLauncher {
                    a.n_l2;
     if (cb > 0) {
       if (a.p > 0.0f)
-        hipLaunchKernelGGL((gat_bwd_cols_fl_kernel<T, L, true>), dim3(cb), dim3(kBlock), 0, st, a, cs, c_mid,
+        hipLaunchKernelGGL((gat_bwd_cols_fl_kernel<T, L, V, true>), dim3(cb), dim3(kBlock), 0, st, a, cs, c_mid,
                            c_mid_blocks, lgcq);
       else
-        hipLaunchKernelGGL((gat_bwd_cols_fl_kernel<T, L, false>), dim3(cb), dim3(kBlock), 0, st, a, cs, c_mid,
+        hipLaunchKernelGGL((gat_bwd_cols_fl_kernel<T, L, V, false>), dim3(cb), dim3(kBlock), 0, st, a, cs, c_mid,
                            c_mid_blocks, lgcq);
     }
     return check_launch("cign_gat_bwd (cols, feature layout)");
   }
 };
 
-#define CIGN_GAT_FL_INSTANTIATE(T)                       \
-  template struct ::cign::gatk::BwdFlLauncher<T, 1>;     \
-  template struct ::cign::gatk::BwdFlLauncher<T, 2>;     \
-  template struct ::cign::gatk::BwdFlLauncher<T, 4>;     \
-  template struct ::cign::gatk::BwdFlLauncher<T, 8>;     \
-  template struct ::cign::gatk::BwdFlLauncher<T, 16>;    \
-  template struct ::cign::gatk::BwdFlLauncher<T, 32>;    \
-  template struct ::cign::gatk::BwdFlLauncher<T, 64>;    \
-  template struct ::cign::gatk::FwdFlLauncher<T, 1>;     \
-  template struct ::cign::gatk::FwdFlLauncher<T, 2>;     \
-  template struct ::cign::gatk::FwdFlLauncher<T, 4>;     \
-  template struct ::cign::gatk::FwdFlLauncher<T, 8>;     \
-  template struct ::cign::gatk::FwdFlLauncher<T, 16>;    \
-  template struct ::cign::gatk::FwdFlLauncher<T, 32>;    \
-  template struct ::cign::gatk::FwdFlLauncher<T, 64>;
+// Narrow rows: one chunk per lane, groups of 1..64 lanes.
+#define CIGN_GAT_FL_LIST_NARROW(X, T) \
+  X(T, 1, 1) X(T, 2, 1) X(T, 4, 1) X(T, 8, 1) X(T, 16, 1) X(T, 32, 1) X(T, 64, 1)
+// Wide rows: a wavefront per row, V chunks per lane.
+#define CIGN_GAT_FL_LIST_WIDE(X, T) X(T, 64, 2) X(T, 64, 3) X(T, 64, 4) X(T, 64, 6) X(T, 64, 8)
 
-#define CIGN_GAT_FL_DECLARE(T)                                  \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 1>;     \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 2>;     \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 4>;     \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 8>;     \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 16>;    \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 32>;    \
-  extern template struct ::cign::gatk::BwdFlLauncher<T, 64>;    \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 1>;     \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 2>;     \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 4>;     \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 8>;     \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 16>;    \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 32>;    \
-  extern template struct ::cign::gatk::FwdFlLauncher<T, 64>;
+#define CIGN_GAT_FL_INST_ONE(T, L, V)                      \
+  template struct ::cign::gatk::BwdFlLauncher<T, L, V>;    \
+  template struct ::cign::gatk::FwdFlLauncher<T, L, V>;
+#define CIGN_GAT_FL_DECL_ONE(T, L, V)                             \
+  extern template struct ::cign::gatk::BwdFlLauncher<T, L, V>;    \
+  extern template struct ::cign::gatk::FwdFlLauncher<T, L, V>;
+
+#define CIGN_GAT_FL_INSTANTIATE(T) CIGN_GAT_FL_LIST_NARROW(CIGN_GAT_FL_INST_ONE, T)
+#define CIGN_GAT_FLW_INSTANTIATE(T) CIGN_GAT_FL_LIST_WIDE(CIGN_GAT_FL_INST_ONE, T)
+#define CIGN_GAT_FL_DECLARE(T) \
+  CIGN_GAT_FL_LIST_NARROW(CIGN_GAT_FL_DECL_ONE, T) CIGN_GAT_FL_LIST_WIDE(CIGN_GAT_FL_DECL_ONE, T)
 
 }  // namespace gatk
 }  // namespace cign

@@ -1,0 +1,5 @@
+// Explicit instantiation of the wide-row feature-layout collapsed-GAT kernels
+// (several chunks per lane) for float.
+#include "gat_fl.h"
+
+CIGN_GAT_FLW_INSTANTIATE(float)

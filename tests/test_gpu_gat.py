@@ -59,6 +59,14 @@ CASES = [
     (1, 4, 0.1, torch.float32, 300, {2: 400}),
     (4, 4, 0.0, torch.float32, 300, {1: 700}),
     (2, 8, 0.2, torch.bfloat16, 300, {1: 500}),
+    # wide rows (several chunks per lane): V = H*C/(W*64) = 4, 4, 8, 2, 2 and
+    # a narrow bf16 row of 64 chunks
+    (4, 256, 0.1, torch.float32, 300, {2: 700}),
+    (8, 128, 0.0, torch.float32, 300, {1: 400}),
+    (8, 256, 0.2, torch.float32, 150, {0: 300}),
+    (8, 64, 0.3, torch.float32, 300, {3: 600}),
+    (4, 256, 0.2, torch.bfloat16, 300, {2: 500}),
+    (2, 256, 0.0, torch.bfloat16, 300, {1: 400}),
 ]
 
 
@@ -287,6 +295,48 @@ def test_long_segments_multi_round(seg, dtype, p, agg_mode, monkeypatch):
     gr = O.collapsed_gat_backward(*args, gy.double().cpu().numpy(), p=p, keep=keep)
     tol = TOL[dtype]
     assert_close(pre.cpu().numpy(), f["pre"], name="pre", **tol)
+    assert_close(gf.double().cpu().numpy(), gr["grad_feat"], name="grad_feat", **tol)
+    assert_close(gar.cpu().numpy(), gr["grad_attn_row"], name="grad_attn_row", **tol)
+    assert_close(gac.cpu().numpy(), gr["grad_attn_col"], name="grad_attn_col", **tol)
+    assert_close(gb.cpu().numpy(), gr["grad_bias"], name="grad_bias", **tol)
+    S._CACHE.clear()
+
+
+@pytest.mark.parametrize("agg_mode", [False, True])
+@pytest.mark.parametrize("H,C,dtype,p", [(6, 256, torch.float32, 0.0), (6, 256, torch.float32, 0.3),
+                                         (6, 256, torch.bfloat16, 0.0)])
+def test_wide_rows_long_segments(H, C, dtype, p, agg_mode, monkeypatch):
+    """Production-shape rows (H=6 x C=256: 6 chunks per lane in fp32, 3 in
+    bf16) with hub rows and columns split into several 512-edge segments."""
+    import cign_amd.schedule as S
+
+    print(f"gat wide long segments H={H} C={C} dtype={dtype} p={p} agg={agg_mode}", flush=True)
+    monkeypatch.setattr(S, "segment_edges_for", lambda nnz: 512)
+    S._CACHE.clear()
+    rng = np.random.default_rng(H * C)
+    n = 2500
+    ei = random_gat_graph(rng, n, avg_deg=4, hubs={5: 2400, 17: 1100})
+    ei = np.concatenate([ei, np.stack([np.full(1800, 9), rng.choice(n, 1800, replace=False)])], 1)
+    r, c, _ = O.coalesce(ei[0], ei[1], n)
+    rowptr, col, row, colptr, perm = _dev_graph(np.stack([r, c]), n)
+    x, ar, ac, b, gy = _inputs(rng, n, H, C, dtype)
+    ext = __import__("cign_amd.collapsed_gat", fromlist=["x"]).ensure_collapsed_gat_loaded()
+    (out, pre, emax, esum, mask), agg = _forward(ext, agg_mode, ar, ac, rowptr, col, 0.2, x, b, p, 7)
+    assert (agg is not None) == agg_mode
+    gf, gar, gac, gb = ext.backward(0.2, p, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar, ac, pre, gy,
+                                    agg)
+    rp, cl = rowptr.cpu().numpy().astype(np.int64), col.cpu().numpy().astype(np.int64)
+    keep = mask.cpu().numpy().astype(bool) if p > 0 else None
+    if p > 0:
+        assert np.array_equal(keep.reshape(-1), O.gat_dropout_keep(7, cl.size * H, p))
+    args = (ar.double().cpu().numpy(), ac.double().cpu().numpy(), rp, cl, 0.2, x.double().cpu().numpy(),
+            b.double().cpu().numpy())
+    f = O.collapsed_gat_forward(*args, p=p, keep=keep)
+    gr = O.collapsed_gat_backward(*args, gy.double().cpu().numpy(), p=p, keep=keep)
+    tol, t32 = TOL[dtype], TOL[torch.float32]
+    assert_close(pre.cpu().numpy(), f["pre"], name="pre", **tol)
+    assert_close(emax.cpu().numpy(), f["emax"], name="edge_max", **t32)
+    assert_close(esum.cpu().numpy(), f["esum"], name="edge_sum", **t32)
     assert_close(gf.double().cpu().numpy(), gr["grad_feat"], name="grad_feat", **tol)
     assert_close(gar.cpu().numpy(), gr["grad_attn_row"], name="grad_attn_row", **tol)
     assert_close(gac.cpu().numpy(), gr["grad_attn_col"], name="grad_attn_col", **tol)
