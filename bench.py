@@ -41,7 +41,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 disables)")
-    ap.add_argument("--workload", choices=["layer", "scale", "block"], default="layer",
+    ap.add_argument("--workload", choices=["layer", "scale", "block", "train"], default="layer",
                     help="layer: the headline c2+c3 layer (24,492 nodes); scale: the same layer at c5 size "
                          "(2.4M nodes, ~62M edges, GAT 4x32 + SpMM D=256, bf16 by default); block: the full "
                          "Clifford block forward+backward at the production shape (D=256, 6 GAT heads, hops 1-3) "
@@ -235,6 +235,214 @@ def summarize(prof_dir: str, name: str, command: str) -> None:
 MFMA_PEAK = {"f32": 157.3, "bf16": 2500.0}  # MI355X dense matrix TFLOP/s
 
 
+def time_components(comps: dict, dtype: str, torch):
+    """Launches each component R=20 times back to back (one HIP graph,
+    replayed M=5 times), timed with HIP events on the launch stream, against
+    its roofline: algorithmic bytes / HBM peak, or flops / MFMA peak (the
+    bound is whichever ideal time is longer). comps: name -> (callable,
+    bytes, flops). Returns (per-kernel records, roofline of the dominant)."""
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    R = 20
+    kernels = []
+    for name, (fn, nbytes, flops) in comps.items():
+        fn()
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for _ in range(R):
+                fn()
+        gr.replay()
+        b0, b1 = ev(), ev()
+        torch.cuda.synchronize()
+        b0.record()
+        M = 5
+        for _ in range(M):
+            gr.replay()
+        b1.record()
+        torch.cuda.synchronize()
+        ms = b0.elapsed_time(b1) / (M * R)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rec = {"kernel": name, "avg_launch_ms": round(ms, 5), "bytes_per_launch": int(nbytes),
+               "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        if flops:
+            tfs = flops / (ms * 1e-3) / 1e12
+            peak = MFMA_PEAK[dtype]
+            rec.update({"flops_per_launch": int(flops), "TFLOP_s": round(tfs, 2), "mfma_frac": round(tfs / peak, 4)})
+            # the bound is whichever roofline the ideal time hits first
+            rec["bound"] = "mfma" if flops / (peak * 1e12) > nbytes / (HBM_PEAK_GBS * 1e9) else "hbm"
+        else:
+            rec["bound"] = "hbm"
+        kernels.append(rec)
+        del gr
+
+    dom = max(kernels, key=lambda r: r["avg_launch_ms"])
+    if dom["bound"] == "mfma":
+        roof = {"bound": "mfma", "kernel": dom["kernel"], "achieved": dom["TFLOP_s"], "peak": MFMA_PEAK[dtype],
+                "unit": "TFLOP/s", "frac": dom["mfma_frac"], "traffic": None,
+                "avg_launch_ms": dom["avg_launch_ms"], "flops_per_launch": dom["flops_per_launch"]}
+    else:
+        roof = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["GB_s"], "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": dom["hbm_frac"], "traffic": None, "avg_launch_ms": dom["avg_launch_ms"],
+                "bytes_per_launch": dom["bytes_per_launch"]}
+    return kernels, roof
+
+
+def cpu_train_baseline(seconds: float, torch):
+    """The reference's CPU case (BASELINE config c1): the full CIGN model
+    forward + cross-entropy + backward + Adam step, restated in float64 torch
+    on the host (oracle/block_oracle.net_forward; the torch/PyG fallback
+    path of the reference, eval-mode numerics), on N=2000 nodes with
+    out-degree 8 uniform-random edges (symmetrised, as the reference's
+    default use_undirected) plus self-loops, 64-dim features, 2 layers, 4
+    heads x 64, hops (1, 2), 5 classes, seed 0. Times whole steps for about
+    `seconds` with every host thread torch uses."""
+    import numpy as np
+
+    from cign_amd import workloads
+    from oracle import block_oracle as B
+
+    d, hidden, heads, classes = 64, 64, 4, 5
+    w = workloads.build(workloads.C1, device="cpu")
+    n = w.n
+    (rowptr, col), _, _ = w.gat_graph
+    rp, cl = rowptr.numpy().astype(np.int64), col.numpy().astype(np.int64)
+    Pc = w.operator.csr
+    p_np = (Pc.crow_indices().numpy(), Pc.col_indices().numpy(), Pc.values().double().numpy())
+    g = torch.Generator().manual_seed(0)
+    t = lambda *s: (torch.randn(*s, generator=g, dtype=torch.float64) * 0.1).requires_grad_()
+    params = {"input_proj_0.weight": t(hidden, d), "input_proj_0.bias": t(hidden), "input_proj_1.weight": t(hidden, d),
+              "input_proj_1.bias": t(hidden), "input_eta": torch.tensor(0.1, dtype=torch.float64, requires_grad=True),
+              "output_norm.weight": t(3 * hidden), "output_norm.bias": t(3 * hidden),
+              "classifier.weight": t(classes, 3 * hidden), "classifier.bias": t(classes)}
+    for i in range(2):
+        for k, shape in {"h_norm.weight": (hidden,), "h_norm.bias": (hidden,), "c_norm.weight": (hidden,),
+                         "c_norm.bias": (hidden,), "context_gat.lin.weight": (heads * hidden, hidden),
+                         "context_gat.att_src": (1, heads, hidden), "context_gat.att_dst": (1, heads, hidden),
+                         "context_gat.bias": (hidden,), "proj.weight": (hidden, 4 * hidden), "proj.bias": (hidden,),
+                         "hop_gate_mlp.weight": (2, 2 * hidden), "hop_gate_mlp.bias": (2,), "gamma": (hidden,)}.items():
+            params[f"blocks.{i}.{k}"] = t(*shape)
+    x = torch.randn(n, d, generator=g, dtype=torch.float64)
+    y = torch.randint(0, classes, (n,), generator=g)
+    mask = torch.rand(n, generator=g) < 0.5
+    opt = torch.optim.Adam(list(params.values()), lr=3e-3, weight_decay=1e-5)
+
+    def step():
+        opt.zero_grad()
+        logits = B.net_forward(params, x, rp, cl, p_np, (1, 2), num_layers=2, dual=True, layer_combine="concat",
+                               score_mode=1, interaction=1, weighting=0, gate_mode="node", heads=heads)
+        torch.nn.functional.cross_entropy(logits[mask], y[mask]).backward()
+        opt.step()
+
+    step()
+    t0 = time.perf_counter()
+    k = 0
+    while True:
+        step()
+        k += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": int(col.numel()) * k / dt, "unit": "edges/s", "cores": torch.get_num_threads(), "kind": "port",
+            "ms_per_step": 1e3 * dt / k,
+            "sample": f"{k} c1 training steps (N=2000, E_nnz={int(col.numel())}, in 64, hidden 64, 2 layers, 4 heads, "
+                      f"hops 1-2, float64 torch restatement + Adam) in {dt:.1f} s"}
+
+
+def run_train(args, torch):
+    """A full 2-layer CIGN training step (BASELINE config c4, second half):
+    GraphCliffordNet(in 256, hidden 256, 5 classes, 2 layers, 6 GAT heads x
+    256, hops 1-3, default dropouts, selective bf16 AMP unless --dtype f32)
+    on the c2 graph; one step = zero_grad -> forward -> cross-entropy over a
+    50% train mask -> backward -> Adam (lr 3e-3, weight decay 1e-5), as
+    generic_engine/train_cign.py:2103-2148 times it. value = GAT edges (with
+    self-loops) per second of training. The CPU baseline is the reference's
+    own CPU case c1 (cpu_train_baseline); the same model at c1 is also timed
+    on the GPU for a like-for-like ratio."""
+    import torch.nn.functional as F
+
+    from cign_amd import workloads
+    from cign_amd.model_cign import GraphCliffordNet
+    from cign_amd.multihop_csr_pipeline import prepare_multihop_csr_operator
+
+    dev = torch.device("cuda:0")
+    amp = args.dtype != "f32"
+
+    def make(w, in_dim, hidden, heads, layers, order_set):
+        torch.manual_seed(0)
+        model = GraphCliffordNet(in_dim, hidden, 5, num_layers=layers, order_set=order_set, gat_heads=heads,
+                                 use_selective_amp=amp).to(dev).train()
+        model._fused_gat_graph = w.gat_graph
+        # the operator the reference's driver prepares for these hops
+        mh = prepare_multihop_csr_operator(w.operator, dense_cols=2 * hidden, powers=order_set)
+        g = torch.Generator(device="cpu").manual_seed(0)
+        x = torch.randn(w.n, in_dim, generator=g).to(dev)
+        y = torch.randint(0, 5, (w.n,), generator=g).to(dev)
+        mask = (torch.rand(w.n, generator=g) < 0.5).to(dev)
+        opt = torch.optim.Adam(model.parameters(), lr=3e-3, weight_decay=1e-5)
+
+        def step():
+            opt.zero_grad()
+            logits = model(x, None, mh)
+            loss = F.cross_entropy(logits[mask], y[mask])
+            loss.backward()
+            opt.step()
+            return loss
+
+        return step
+
+    def timed(step, steps, warmup):
+        for _ in range(max(1, warmup)):
+            loss = step()
+        torch.cuda.synchronize()
+        if not torch.isfinite(loss):
+            raise SystemExit("non-finite training loss")
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        a0.record()
+        for _ in range(steps):
+            step()
+        a1.record()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, a0.elapsed_time(a1) / steps
+
+    w = workloads.build(workloads.C2, device=dev)
+    elapsed, gpu_ms = timed(make(w, 256, 256, 6, 2, (1, 2, 3)), args.steps, args.warmup)
+    # The reference's CPU case on the GPU (c1: N=2000, 64-dim, 4 heads, hops 1-2).
+    w1 = workloads.build(workloads.C1, device=dev)
+    e1, _ = timed(make(w1, 64, 64, 4, 2, (1, 2)), 20, 3)
+    cpu = cpu_train_baseline(args.cpu_seconds, torch) if args.cpu_seconds > 0 else None
+    line = {
+        "metric": "CIGN 2-layer training step edges/sec (zero_grad, forward, cross-entropy, backward, Adam)",
+        "value": w.nnz_gat * args.steps / elapsed,
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": 1e3 * elapsed / args.steps,
+        "gpu_ms_per_step": round(gpu_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16-gemm" if amp else "f32",
+        "data": "synthetic: seeded Chung-Lu power-law graph (gamma 2.5), N(0,1) features, uniform 5-class labels, "
+                "random-init model",
+        "config": {"workload": "c4 training step: GraphCliffordNet in 256, hidden 256, 2 layers, 6 GAT heads x 256, "
+                               "hops 1-3, dropout 0.28 / GAT 0.32, concat, Adam",
+                   "nodes": w.n, "edges_nnz": w.nnz_gat},
+        "c1_gpu": {"ms_per_step": 1e3 * e1 / 20, "edges_nnz": w1.nnz_gat,
+                   "edges_per_s": w1.nnz_gat * 20 / e1},
+        "roofline": None,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def run_block(args, torch):
     """The Clifford block of the reference at its production shape on the c2
     graph: GraphCliffordBlock(D=256, gat_heads=6, hops (1,2,3), interaction
@@ -346,54 +554,33 @@ def run_block(args, torch):
                                          Wl.data_ptr(), None, xl.data_ptr()),
                         4 * NDb + 4 * n * heads * D, 2 * n * D * heads * D),
     }
-    R = 20
-    kernels = []
-    for name, (fn, nbytes, flops) in comps.items():
-        fn()
-        torch.cuda.synchronize()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            fn()
-        torch.cuda.current_stream().wait_stream(side)
-        torch.cuda.synchronize()
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr):
-            for _ in range(R):
-                fn()
-        gr.replay()
-        b0, b1 = ev(), ev()
-        torch.cuda.synchronize()
-        b0.record()
-        M = 5
-        for _ in range(M):
-            gr.replay()
-        b1.record()
-        torch.cuda.synchronize()
-        ms = b0.elapsed_time(b1) / (M * R)
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        rec = {"kernel": name, "avg_launch_ms": round(ms, 5), "bytes_per_launch": int(nbytes),
-               "GB_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
-        if flops:
-            tfs = flops / (ms * 1e-3) / 1e12
-            peak = MFMA_PEAK[args.dtype]
-            rec.update({"flops_per_launch": int(flops), "TFLOP_s": round(tfs, 2), "mfma_frac": round(tfs / peak, 4)})
-            # the bound is whichever roofline the ideal time hits first
-            rec["bound"] = "mfma" if flops / (peak * 1e12) > nbytes / (HBM_PEAK_GBS * 1e9) else "hbm"
-        else:
-            rec["bound"] = "hbm"
-        kernels.append(rec)
-        del gr
+    # The block's collapsed GAT (H=6 x C=256, fp32 projections) and one hop
+    # of its multihop SpMM (D = 2 x 256), as the block runs them.
+    from cign_amd.collapsed_gat import ensure_collapsed_gat_loaded
 
-    dom = max(kernels, key=lambda r: r["avg_launch_ms"])
-    if dom["bound"] == "mfma":
-        roof = {"bound": "mfma", "kernel": dom["kernel"], "achieved": dom["TFLOP_s"], "peak": MFMA_PEAK[args.dtype],
-                "unit": "TFLOP/s", "frac": dom["mfma_frac"], "traffic": None,
-                "avg_launch_ms": dom["avg_launch_ms"], "flops_per_launch": dom["flops_per_launch"]}
-    else:
-        roof = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["GB_s"], "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": dom["hbm_frac"], "traffic": None, "avg_launch_ms": dom["avg_launch_ms"],
-                "bytes_per_launch": dom["bytes_per_launch"]}
+    ext = ensure_collapsed_gat_loaded()
+    (rowptr, col), (row_, colptr), perm = w.gat_graph
+    xg = rnd(n, heads, D)
+    ar_, ac_, bg_ = rnd(n, heads) * 0.1, rnd(n, heads) * 0.1, rnd(D)
+    gyg = rnd(n, D)
+    gat_state = {}
+
+    def gat_fwd():
+        gat_state["f"] = ext.forward_agg(ar_, ac_, rowptr, col, 0.2, xg, bg_, 0.32, 5, True)
+
+    def gat_bwd():
+        (_, pre_, em_, es_, mk_), agg_ = gat_state["f"]
+        ext.backward(0.2, 0.32, rowptr, col, colptr, row_, perm, em_, es_, mk_, xg, ar_, ac_, pre_, gyg, agg_)
+
+    gat_fwd()
+    Bg = workloads.algorithmic_bytes(n, E, heads, D, 2 * D, dropout=True)
+    Xs = rnd(n, 2 * D)
+    comps["gat_fwd"] = (gat_fwd, Bg["gat_fwd_agg"], 0)
+    comps["gat_bwd"] = (gat_bwd, Bg["gat_bwd_agg"], 0)
+    from cign_amd.multihop_csr_pipeline import _csr_mm
+
+    comps["spmm_hop"] = (lambda: _csr_mm(w.operator.csr, Xs), Bg["spmm"], 0)
+    kernels, roof = time_components(comps, args.dtype, torch)
     line = {
         "metric": "Clifford block fwd+bwd edges/sec (production shape); per-kernel roofline fractions",
         "value": E * args.steps / elapsed,
@@ -440,6 +627,11 @@ def main():
         if args.dtype is None:
             args.dtype = "f32"
         run_block(args, torch)
+        return
+    if args.workload == "train":
+        if args.dtype is None:
+            args.dtype = "bf16"
+        run_train(args, torch)
         return
     scale = args.workload == "scale"
     if args.dtype is None:

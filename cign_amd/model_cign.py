@@ -221,3 +221,140 @@ class GraphCliffordBlock(nn.Module):
         gamma = self.gamma if self.gamma_mode == "vector" else self.gamma.expand(self.hidden_dim)
         return linear_gamma_residual(H, G_raw, self.proj, gamma.contiguous(), p, self.use_selective_amp,
                                      self.selective_amp_dtype)
+
+
+class GraphCliffordNet(nn.Module):
+    """The full CIGN model (generic_engine/model_cign.py:943-1210) on the HIP
+    route: dual input projection (MFMA, selective bf16 autocast), the Clifford
+    blocks, concatenated layer states, output LayerNorm and an fp32
+    classifier (MFMA). Constructor arguments, parameter names and forward
+    signature are the reference's. The input / output dropouts and the output
+    LayerNorm (width hidden*(layers+1), beyond the fused row kernels' 256) are
+    torch ops, as in the reference."""
+
+    def __init__(self, in_dim: int, hidden_dim: int, out_dim: int, num_layers: int = 4, order_set=(1, 2, 3),
+                 dropout: float = 0.28, gat_heads: int = 6, gat_dropout: float = 0.32, use_fused_gat: bool = False,
+                 use_fused_gat_sideops: bool = False, use_chunked_fused_gat: bool = False,
+                 dgnn_chunk_max_nodes: int = 45000, dgnn_chunk_target_nodes: int = 8192,
+                 use_collapsed_fused_gat: bool = False, use_fused_clifford_pack: bool = False,
+                 use_fused_block_ops: bool = False, use_selective_amp: bool = False, selective_amp_dtype: str = "bf16",
+                 init_gamma: float = 0.49, gamma_mode: str = "vector", hop_gate_mode: str = "node",
+                 alpha_score_mode: str = None, interaction_mode: str = None, alpha_weighting_mode: str = None,
+                 layer_combine: str = "concat", use_dual_input_projection: bool = True, init_input_eta: float = 0.1,
+                 use_bias: bool = True):
+        super().__init__()
+        # Validation of model_cign.py:978-1020 (the backend flags are accepted;
+        # every combination runs the one HIP route).
+        if num_layers <= 0:
+            raise ValueError("num_layers must be positive.")
+        if layer_combine not in {"last", "concat"}:
+            raise ValueError("layer_combine must be either 'last' or 'concat'.")
+        if hop_gate_mode not in {"none", "global", "node"}:
+            raise ValueError("hop_gate_mode must be one of {'none', 'global', 'node'}.")
+        if use_chunked_fused_gat and not use_fused_gat:
+            raise ValueError("use_chunked_fused_gat=True requires use_fused_gat=True")
+        if use_chunked_fused_gat and use_collapsed_fused_gat:
+            raise ValueError("chunked dgNN and collapsed GAT are mutually exclusive")
+        if use_fused_gat_sideops and not use_fused_gat:
+            raise ValueError("use_fused_gat_sideops=True requires use_fused_gat=True")
+        if use_collapsed_fused_gat and not use_fused_gat:
+            raise ValueError("use_collapsed_fused_gat=True requires use_fused_gat=True")
+        if use_collapsed_fused_gat and not use_fused_gat_sideops:
+            raise ValueError("A3-v6 requires use_fused_gat_sideops=True")
+        self.dropout = dropout
+        self.layer_combine = layer_combine
+        self.num_layers = num_layers
+        self.hidden_dim = hidden_dim
+        self.hop_gate_mode = hop_gate_mode
+        self.alpha_score_mode = _resolve_old_new_mode(alpha_score_mode, "CIGN_ALPHA_SCORE_MODE", "new")
+        self.interaction_mode = _resolve_old_new_mode(interaction_mode, "CIGN_INTERACTION_MODE", "new")
+        self.alpha_weighting_mode = _resolve_old_new_mode(alpha_weighting_mode, "CIGN_ALPHA_WEIGHTING_MODE", "old")
+        self.use_dual_input_projection = bool(use_dual_input_projection)
+        self.use_fused_gat = bool(use_fused_gat)
+        self.use_fused_gat_sideops = bool(use_fused_gat_sideops)
+        self.use_chunked_fused_gat = bool(use_chunked_fused_gat)
+        self.dgnn_chunk_max_nodes = int(dgnn_chunk_max_nodes)
+        self.dgnn_chunk_target_nodes = int(dgnn_chunk_target_nodes)
+        self.use_collapsed_fused_gat = bool(use_collapsed_fused_gat)
+        self.use_fused_clifford_pack = bool(use_fused_clifford_pack)
+        self.use_fused_block_ops = bool(use_fused_block_ops)
+        self.use_selective_amp = bool(use_selective_amp)
+        self.selective_amp_dtype_name = str(selective_amp_dtype).strip().lower()
+        self.selective_amp_dtype = _resolve_selective_amp_dtype(self.selective_amp_dtype_name)
+        self._fused_gat_graph = None
+        self._fused_gat_graph_info = None
+
+        self.input_act = nn.SiLU()
+        if self.use_dual_input_projection:
+            self.input_proj_0 = nn.Linear(in_dim, hidden_dim, bias=use_bias)
+            self.input_proj_1 = nn.Linear(in_dim, hidden_dim, bias=use_bias)
+            self.input_eta = nn.Parameter(torch.tensor(float(init_input_eta)))
+        else:
+            self.input_proj = nn.Linear(in_dim, hidden_dim, bias=use_bias)
+        self.blocks = nn.ModuleList([
+            GraphCliffordBlock(hidden_dim=hidden_dim, order_set=order_set, dropout=dropout, gat_heads=gat_heads,
+                               gat_dropout=gat_dropout, use_fused_gat=self.use_fused_gat,
+                               use_fused_gat_sideops=self.use_fused_gat_sideops,
+                               use_collapsed_fused_gat=self.use_collapsed_fused_gat,
+                               use_fused_clifford_pack=self.use_fused_clifford_pack,
+                               use_fused_block_ops=self.use_fused_block_ops,
+                               use_selective_amp=self.use_selective_amp,
+                               selective_amp_dtype=self.selective_amp_dtype_name, init_gamma=init_gamma,
+                               gamma_mode=gamma_mode, hop_gate_mode=hop_gate_mode,
+                               alpha_score_mode=self.alpha_score_mode, interaction_mode=self.interaction_mode,
+                               alpha_weighting_mode=self.alpha_weighting_mode, use_bias=use_bias)
+            for _ in range(num_layers)
+        ])
+        final_dim = hidden_dim * (num_layers + 1) if layer_combine == "concat" else hidden_dim
+        self.output_norm = nn.LayerNorm(final_dim)
+        self.classifier = nn.Linear(final_dim, out_dim, bias=use_bias)
+
+    @torch.no_grad()
+    def prepare_fused_gat_graph(self, edge_index: torch.Tensor, num_nodes: int = None):
+        """model_cign.py:1069-1158: the GAT graph format (destination CSR, CSC,
+        perm; int32, zero storage offset, 16-byte aligned), built once. The HIP
+        route always runs the collapsed GAT, so the graph is prepared whatever
+        use_fused_gat says. Returns the reference's info dict."""
+        from .graph import prepare_fused_gat_graph
+
+        if edge_index.dim() != 2 or edge_index.size(0) != 2:
+            raise ValueError(f"edge_index must have shape [2, E], got {tuple(edge_index.shape)}")
+        if num_nodes is None:
+            num_nodes = int(edge_index.max().item()) + 1
+        (rowptr, col), (row, colptr), perm = prepare_fused_gat_graph(edge_index, int(num_nodes))
+        dev = self.classifier.weight.device
+        rowptr, col, row, colptr, perm = (t.to(dev) for t in (rowptr, col, row, colptr, perm))
+        self._fused_gat_graph = ((rowptr, col), (row, colptr), perm)
+        self._fused_gat_graph_info = {
+            "num_nodes": int(num_nodes), "num_edges": int(col.numel()),
+            "csr_rowptr_ptr_mod_16": int(rowptr.data_ptr() % 16), "csr_col_ptr_mod_16": int(col.data_ptr() % 16),
+            "csc_row_ptr_mod_16": int(row.data_ptr() % 16), "csc_colptr_ptr_mod_16": int(colptr.data_ptr() % 16),
+            "perm_ptr_mod_16": int(perm.data_ptr() % 16),
+        }
+        return dict(self._fused_gat_graph_info)
+
+    def _forward_impl(self, x: torch.Tensor, edge_index: torch.Tensor, graph_operator):
+        """model_cign.py:1160-1204."""
+        H_in = F.dropout(x, p=self.dropout, training=self.training)
+        amp, amp_dtype = self.use_selective_amp, self.selective_amp_dtype
+        if self.use_dual_input_projection:
+            H_base = self.input_act(_local_amp_linear(self.input_proj_0, H_in, amp, amp_dtype))
+            H_vel = self.input_act(_local_amp_linear(self.input_proj_1, H_in, amp, amp_dtype))
+            H = H_base + self.input_eta * H_vel
+        else:
+            H = self.input_act(_local_amp_linear(self.input_proj, H_in, amp, amp_dtype))
+        states = [H]
+        for block in self.blocks:
+            H = block(H, edge_index, graph_operator, fused_gat_graph=self._fused_gat_graph)
+            states.append(H)
+        H_out = torch.cat(states, dim=-1) if self.layer_combine == "concat" else states[-1]
+        # Final LayerNorm and classifier stay in fp32 (the classifier on the
+        # fp32 MFMA kernel).
+        H_out = self.output_norm(H_out.float())
+        H_out = F.dropout(H_out, p=self.dropout, training=self.training)
+        return mfma_linear(self.classifier, H_out, False).float()
+
+    def forward(self, x: torch.Tensor, edge_index: torch.Tensor, graph_operator=None) -> torch.Tensor:
+        if graph_operator is None:
+            raise ValueError("GraphCliffordNet requires a sparse graph operator as the third input.")
+        return self._forward_impl(x, edge_index, graph_operator)

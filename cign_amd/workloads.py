@@ -18,6 +18,10 @@ from . import graph, graphgen
 # c2/c3: N = 24,492 nodes, 186,100 directed edges (93,050 undirected pairs),
 # Chung-Lu exponent 2.5, hubs up to ~1,000 in-degree.
 C2 = dict(n=24492, directed=186100, gamma=2.5, max_degree=1100.0, seed=0)
+# c1: the reference's CPU case, N = 2,000 nodes with 8 uniform-random
+# out-edges each (symmetrised by build_sparse_normalized_adjacency, as the
+# reference's default use_undirected=True does).
+C1 = dict(n=2000, out_degree=8, seed=0)
 # c5: N = 2.4M nodes, ~60M directed edges, exponent 2.2, hubs up to ~50K.
 C5 = dict(n=2_400_000, directed=60_000_000, gamma=2.2, max_degree=55_000.0, seed=0)
 
@@ -39,8 +43,11 @@ def _to_device_csr(csr: torch.Tensor, device) -> torch.Tensor:
 
 def build(cfg: dict = C2, device="cuda") -> Workload:
     n = int(cfg["n"])
-    ei = graphgen.chung_lu_directed(n, int(cfg["directed"]), gamma=float(cfg["gamma"]),
-                                    max_degree=float(cfg["max_degree"]), seed=int(cfg["seed"]))
+    if "out_degree" in cfg:
+        ei = graphgen.uniform_out_degree(n, int(cfg["out_degree"]), seed=int(cfg["seed"]))
+    else:
+        ei = graphgen.chung_lu_directed(n, int(cfg["directed"]), gamma=float(cfg["gamma"]),
+                                        max_degree=float(cfg["max_degree"]), seed=int(cfg["seed"]))
     edge_index = torch.from_numpy(ei)
     used, P = graph.build_sparse_normalized_adjacency(edge_index, n)
     op_cpu = graph.prepare_fixed_csr_operator(P)

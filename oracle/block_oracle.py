@@ -93,3 +93,29 @@ def block_forward(params: dict, H, rowptr, col, p_csr, order_set, *, score_mode,
     Gf = F.linear(G, g["proj.weight"], g["proj.bias"])
     gamma = g["gamma"]
     return H + (gamma.unsqueeze(0) if gamma.dim() == 1 else gamma) * Gf
+
+
+def net_forward(params: dict, x, rowptr, col, p_csr, order_set, *, num_layers, dual, layer_combine, score_mode,
+                interaction, weighting, gate_mode, heads, slope=0.2, eps=1e-5):
+    """Eval-mode GraphCliffordNet._forward_impl (generic_engine/model_cign.py:
+    1160-1204) in float64: dual input projection H = SiLU(lin0 x) + eta
+    SiLU(lin1 x) (or one projection), the blocks (block_forward on each
+    block's parameters), concatenated (or last) layer states, output
+    LayerNorm, classifier. Returns the logits."""
+    g = params
+    if dual:
+        hb = F.silu(F.linear(x, g["input_proj_0.weight"], g.get("input_proj_0.bias")))
+        hv = F.silu(F.linear(x, g["input_proj_1.weight"], g.get("input_proj_1.bias")))
+        H = hb + g["input_eta"] * hv
+    else:
+        H = F.silu(F.linear(x, g["input_proj.weight"], g.get("input_proj.bias")))
+    states = [H]
+    for i in range(num_layers):
+        pre = f"blocks.{i}."
+        bp = {k[len(pre):]: v for k, v in g.items() if k.startswith(pre)}
+        H = block_forward(bp, H, rowptr, col, p_csr, order_set, score_mode=score_mode, interaction=interaction,
+                          weighting=weighting, gate_mode=gate_mode, heads=heads, slope=slope, eps=eps)
+        states.append(H)
+    out = torch.cat(states, dim=-1) if layer_combine == "concat" else states[-1]
+    out = F.layer_norm(out, (out.size(1),), g["output_norm.weight"], g["output_norm.bias"], eps)
+    return F.linear(out, g["classifier.weight"], g.get("classifier.bias"))

@@ -502,3 +502,54 @@ def test_linear_oracle_amp_rounding_points():
     np.testing.assert_allclose(gw, np.tile(x.astype(np.float64).sum(0), (24, 1)), rtol=1e-12)
     np.testing.assert_allclose(gb, np.full(24, 64.0))
     np.testing.assert_allclose(gx, np.tile(w.astype(np.float64).sum(0), (64, 1)), rtol=1e-12)
+
+
+def test_net_oracle_closed_forms():
+    """net_forward's outer composition: with gamma = 0 every block is the
+    identity (H + 0 * G), so the logits are classifier(LN([H0]*(L+1))) with H0
+    = SiLU(lin0 x) + eta SiLU(lin1 x); with eta = 0 the second projection
+    drops out and 'last' combine keeps one state. A swapped projection, a
+    missing SiLU or a wrong concat count fails one of these."""
+    import torch
+    import torch.nn.functional as F
+    from oracle import block_oracle as B
+
+    rng = np.random.default_rng(5)
+    n, D, heads, in_dim, L = 40, 8, 2, 6, 2
+    ei = np.array([[j, i] for i in range(n) for j in rng.choice(n, 3, replace=False)], dtype=np.int64).T
+    ge = O.gat_edge_index(ei, n)
+    r, c, _ = O.coalesce(ge[0], ge[1], n)
+    rowptr, col = O.csr_from_coo(c, r, n)[:2]
+    prow, pcol, _ = O.csr_from_coo(r, c, n)
+    pval = np.full(pcol.size, 0.1)
+    t = lambda *s: torch.tensor(rng.standard_normal(s))
+    g = {"input_proj_0.weight": t(D, in_dim), "input_proj_0.bias": t(D), "input_proj_1.weight": t(D, in_dim),
+         "input_proj_1.bias": t(D), "input_eta": torch.tensor(0.3, dtype=torch.float64),
+         "output_norm.weight": t((L + 1) * D), "output_norm.bias": t((L + 1) * D),
+         "classifier.weight": t(5, (L + 1) * D), "classifier.bias": t(5)}
+    for i in range(L):
+        for k, shape in {"h_norm.weight": (D,), "h_norm.bias": (D,), "c_norm.weight": (D,), "c_norm.bias": (D,),
+                         "context_gat.lin.weight": (heads * D, D), "context_gat.att_src": (1, heads, D),
+                         "context_gat.att_dst": (1, heads, D), "context_gat.bias": (D,),
+                         "proj.weight": (D, 6 * D), "proj.bias": (D,), "hop_gate_mlp.weight": (3, 2 * D),
+                         "hop_gate_mlp.bias": (3,)}.items():
+            g[f"blocks.{i}.{k}"] = t(*shape)
+        g[f"blocks.{i}.gamma"] = torch.zeros(D, dtype=torch.float64)
+    x = t(n, in_dim)
+    kw = dict(num_layers=L, dual=True, layer_combine="concat", score_mode=1, interaction=1, weighting=0,
+              gate_mode="node", heads=heads)
+    got = B.net_forward(g, x, rowptr, col, (prow, pcol, pval), (1, 2, 3), **kw)
+    h0 = F.silu(x @ g["input_proj_0.weight"].T + g["input_proj_0.bias"]) + \
+        0.3 * F.silu(x @ g["input_proj_1.weight"].T + g["input_proj_1.bias"])
+    z = torch.cat([h0] * (L + 1), dim=1)
+    z = (z - z.mean(1, keepdim=True)) / torch.sqrt(z.var(1, unbiased=False, keepdim=True) + 1e-5)
+    z = z * g["output_norm.weight"] + g["output_norm.bias"]
+    want = z @ g["classifier.weight"].T + g["classifier.bias"]
+    assert torch.allclose(got, want, rtol=1e-10, atol=1e-10)
+    g2 = dict(g, input_eta=torch.tensor(0.0, dtype=torch.float64))
+    g2["output_norm.weight"], g2["output_norm.bias"] = t(D), t(D)
+    g2["classifier.weight"] = t(5, D)
+    got2 = B.net_forward(g2, x, rowptr, col, (prow, pcol, pval), (1, 2, 3), **dict(kw, layer_combine="last"))
+    h = F.silu(x @ g["input_proj_0.weight"].T + g["input_proj_0.bias"])
+    z = F.layer_norm(h, (D,), g2["output_norm.weight"], g2["output_norm.bias"], 1e-5)
+    assert torch.allclose(got2, z @ g2["classifier.weight"].T + g["classifier.bias"], rtol=1e-10, atol=1e-10)
