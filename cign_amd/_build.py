@@ -43,11 +43,25 @@ def sources() -> list[Path]:
     return sorted(list(SRC.glob("*.hip")) + list(SRC.glob("*.cpp")))
 
 
+def _deps(src: Path) -> set[Path]:
+    """src and the local headers it includes, transitively."""
+    seen, todo = set(), [src]
+    while todo:
+        f = todo.pop()
+        if f in seen or not f.exists():
+            continue
+        seen.add(f)
+        for line in f.read_text().splitlines():
+            line = line.strip()
+            if line.startswith("#include \""):
+                todo.append(SRC / line.split('"')[1])
+    return seen
+
+
 def _compile(hipcc: str, src: Path, force: bool) -> Path:
     obj = OBJ / (src.stem + ".o")
     if not force and obj.exists():
-        newest = max([src.stat().st_mtime, *(h.stat().st_mtime for h in SRC.glob("*.h")),
-                      Path(__file__).stat().st_mtime])
+        newest = max([*(d.stat().st_mtime for d in _deps(src)), Path(__file__).stat().st_mtime])
         if obj.stat().st_mtime >= newest:
             return obj
     cmd = [hipcc, *HIP_FLAGS, "-x", "hip", "-c", str(src), "-o", str(obj)]

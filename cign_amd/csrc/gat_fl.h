@@ -164,6 +164,38 @@ __device__ __forceinline__ float head_sum(float v, int cq) {
   return v;
 }
 
+// Dropout keep bits of a batch's U x H (edge slot k, head h) pairs, each
+// computed once. Slots are laid out S = min(L, 8) >= H bits apart, SPR = L / S
+// slots per round: pair (k, h) belongs to lane (k % SPR) * S + h of its group
+// in round k / SPR, and the round's ballot holds it at bit g*L + (k % SPR)*S
+// + h for group g, so a lookup indexes the ballot array with a compile-time
+// round. keep_of(k, h, own) is called by every lane of every round (with a
+// valid (k, h) even when the lane owns no pair, own = false) and returns the
+// pair's bit (false when !own), so shuffles inside it see the whole
+// wavefront.
+template <int U, int L>
+struct PairBits {
+  static constexpr int S = L < 8 ? L : 8;
+  static constexpr int SPR = L / S;
+  static constexpr int R = (U + SPR - 1) / SPR;
+  uint64_t w[R];
+
+  template <typename Fn>
+  __device__ __forceinline__ void compute(int H, int gl, Fn&& keep_of) {
+    const int h = gl % S;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int k = r * SPR + gl / S;
+      const bool own = h < H && k < U;
+      const bool keep = keep_of(k < U ? k : U - 1, h < H ? h : H - 1, own);
+      w[r] = __ballot(keep);
+    }
+  }
+  __device__ __forceinline__ bool get(int k, int h, int g) const {
+    return (w[k / SPR] >> (g * L + (k % SPR) * S + h)) & 1ull;
+  }
+};
+
 // ===========================================================================
 // Forward
 // ===========================================================================
@@ -237,6 +269,18 @@ struct FwdBatches {
         xb[k][v] = Chunk<T, W>::load_raw(a.x + static_cast<int64_t>(j) * F + ln.q[v] * W);
       }
     }
+    // Dropout: each (edge, head) pair hashed once, its mask byte written by
+    // the lane that hashed it.
+    PairBits<(DROP ? U : 1), L> kb;
+    if constexpr (DROP)
+      kb.compute(a.H, ln.gl, [&](int k, int h, bool own) {
+        const int u = first + (k0 + k) * step;
+        if (!own || u >= cnt) return false;
+        const int64_t idx = static_cast<int64_t>(ebase + u) * a.H + h;
+        const bool keep = gat_keep(a.seed, static_cast<uint64_t>(idx), a.p);
+        a.mask[idx] = keep ? 1 : 0;
+        return keep;
+      });
     // sc becomes the raw score (before LeakyReLU): its sign gives l'.
 #pragma unroll
     for (int v = 0; v < V; ++v) {
@@ -260,15 +304,7 @@ struct FwdBatches {
         st.s[v] += pk;
         st.bl[v] = fmaf(pk, lp, st.bl[v]);
         float wk = pk;
-        if constexpr (DROP) {
-          bool keep = false;
-          if (u < cnt) {
-            const int64_t idx = static_cast<int64_t>(ebase + u) * a.H + ln.hq[v];
-            keep = gat_keep(a.seed, static_cast<uint64_t>(idx), a.p);
-            if (ln.qv[v] && ln.cw == 0) a.mask[idx] = keep ? 1 : 0;
-          }
-          wk = keep ? pk / (1.0f - a.p) : 0.0f;
-        }
+        if constexpr (DROP) wk = kb.get(k, ln.hq[v], ln.g) ? pk / (1.0f - a.p) : 0.0f;
         const float wl = wk * lp;
         float xv[W];
         Chunk<T, W>::unpack(xb[k][v], xv);
@@ -579,7 +615,6 @@ struct RowBatches {
     const int F = a.H * a.C;
     typename Chunk<T, W>::Raw xb[U][V];
     float ab[U][V];
-    float kw[U][V];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
@@ -588,10 +623,15 @@ struct RowBatches {
       for (int v = 0; v < V; ++v) {
         ab[k][v] = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq[v]];
         xb[k][v] = Chunk<T, W>::load_raw(a.x + static_cast<int64_t>(j) * F + ln.q[v] * W);
-        if constexpr (DROP)
-          kw[k][v] = (u < cnt && a.mask[static_cast<int64_t>(ebase + u) * a.H + ln.hq[v]]) ? 1.0f : 0.0f;
       }
     }
+    // Dropout mask bytes: each (edge, head) pair loaded once.
+    PairBits<(DROP ? U : 1), L> kb;
+    if constexpr (DROP)
+      kb.compute(a.H, ln.gl, [&](int k, int h, bool own) {
+        const int u = first + (k0 + k) * step;
+        return own && u < cnt && a.mask[static_cast<int64_t>(ebase + u) * a.H + h] != 0;
+      });
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
@@ -601,7 +641,7 @@ struct RowBatches {
         const float lp = raw < 0.0f ? a.slope : 1.0f;
         const float sm = u < cnt ? expf(leaky(raw, a.slope) - rh.em[v]) * rh.ies[v] : 0.0f;
         float sk = sm;
-        if constexpr (DROP) sk = kw[k][v] != 0.0f ? sm / (1.0f - a.p) : 0.0f;
+        if constexpr (DROP) sk = kb.get(k, ln.hq[v], ln.g) ? sm / (1.0f - a.p) : 0.0f;
         const float skl = sk * lp;
         st.B[v] = fmaf(sm, lp, st.B[v]);
         float xv[W];
@@ -853,22 +893,24 @@ struct ColBatches {
   __device__ __forceinline__ void run(int k0) {
     float gb[U][W];
     float4 rs[U][V];
-    float kw[U][V];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
       const int src = (base + (u < cnt ? u : 0)) & (kWave - 1);
       const int i = shfl(ii, src);
       load_f32<W>(a.grad_pre + static_cast<int64_t>(i) * a.C + ln.cw * W, gb[k]);
-      int e = 0;
-      if constexpr (DROP) e = shfl(ee, src);
 #pragma unroll
-      for (int v = 0; v < V; ++v) {
-        rs[k][v] = a.rowstat[static_cast<int64_t>(i) * a.H + ln.hq[v]];
-        if constexpr (DROP)
-          kw[k][v] = (u < cnt && a.mask[static_cast<int64_t>(e) * a.H + ln.hq[v]]) ? 1.0f : 0.0f;
-      }
+      for (int v = 0; v < V; ++v) rs[k][v] = a.rowstat[static_cast<int64_t>(i) * a.H + ln.hq[v]];
     }
+    // Dropout mask bytes (CSR edge id from perm): each (entry, head) pair
+    // loaded once.
+    PairBits<(DROP ? U : 1), L> kb;
+    if constexpr (DROP)
+      kb.compute(a.H, ln.gl, [&](int k, int h, bool own) {
+        const int u = first + (k0 + k) * step;
+        const int e = shfl(ee, (base + (u < cnt ? u : 0)) & (kWave - 1));
+        return own && u < cnt && a.mask[static_cast<int64_t>(e) * a.H + h] != 0;
+      });
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
@@ -878,7 +920,7 @@ struct ColBatches {
         const float lp = raw < 0.0f ? a.slope : 1.0f;
         const float sm = u < cnt ? expf(leaky(raw, a.slope) - rs[k][v].y) * rs[k][v].z : 0.0f;
         float w = sm;
-        if constexpr (DROP) w = kw[k][v] != 0.0f ? sm / (1.0f - a.p) : 0.0f;
+        if constexpr (DROP) w = kb.get(k, ln.hq[v], ln.g) ? sm / (1.0f - a.p) : 0.0f;
         const float wl = w * lp;
         st.t[v] = fmaf(sm * lp, rs[k][v].w, st.t[v]);
 #pragma unroll
