@@ -20,15 +20,19 @@
 // fp32). The skinny shapes of the block (outputs <= 1536, K <= 1536, M =
 // nodes) are HBM-bound in bf16 and MFMA-bound in fp32.
 //
-// Forward tiling: a workgroup computes a 128 x BN tile (BN = 64 or 128) with 4
-// wavefronts of 32 rows x BN columns each (2 x BN/16 accumulator tiles of
-// 16x16). Per K step of 32 the A (128 x 32) and B (BN x 32) tiles are staged
-// in LDS in the MFMA operand type (bf16 conversion happens once, at the LDS
-// store), double buffered: the next step's global loads are in flight while
-// the current step's MFMAs run. LDS rows are padded so the 16-byte fragment
-// reads of 16 consecutive rows fall on distinct banks. MFMA fragment layouts
-// (16x16xK, lane l): A supplies row l%16 and k-slice l/16, B supplies column
-// l%16 and the same k-slice, D holds rows 4*(l/16)+i, i < 4, of column l%16.
+// Forward tiling: a 256-thread workgroup computes a 128 x BN tile (BN = 64 or
+// 128), each wavefront 32 rows x BN columns (2 x BN/16 accumulator tiles of
+// 16x16). x rows belong to one wavefront, so its MFMA fragments go straight
+// from global memory to registers, two K steps (of 32) ahead; the W tile
+// (BN x 32 per step) is shared by the four wavefronts through a
+// double-buffered LDS tile in the MFMA operand type (converted once, at the
+// LDS store), rows padded so 16 consecutive rows' 16-byte reads fall on
+// distinct banks. W is the MFMA's first operand and x the second, so the
+// accumulator layout gives each lane four consecutive output columns of one
+// row: the epilogue stores 16 bytes per lane. MFMA fragment layouts (16x16xK,
+// lane l): the first operand supplies row l%16 and k-slice l/16, the second
+// column l%16 and the same k-slice, D holds rows 4*(l/16)+i, i < 4, of
+// column l%16.
 #include <algorithm>
 #include <mutex>
 #include <type_traits>
@@ -41,6 +45,7 @@ namespace cign {
 namespace gemm {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 enum Epi : int { kEpiStore = 0, kEpiLogits = 1, kEpiGamma = 2 };
@@ -48,7 +53,10 @@ enum Math : int { kMathF32 = 0, kMathBF16 = 1 };
 
 constexpr int kThreads = 256;
 constexpr int kBM = 128;
-constexpr int kBK = 32;
+#ifndef CIGN_GEMM_BK
+#define CIGN_GEMM_BK 32
+#endif
+constexpr int kBK = CIGN_GEMM_BK;  // K per LDS stage (a multiple of 32)
 constexpr int kRowsPerWave = 32;
 
 struct GemmArgs {
@@ -56,6 +64,7 @@ struct GemmArgs {
   int N, K;
   const void* x;      // [M, K] fp32 or bf16
   bool vec;           // rows of x and w start 16-byte aligned (vector loads)
+  bool vec4;          // y (and h, out, mask) rows take 16-byte (4-column) stores
   const float* w;     // [N, K] fp32
   const float* bias;  // [N] or null
   float* y;           // [M, N]
@@ -99,6 +108,9 @@ constexpr int lds_stride() { return kBK + Op<MATH>::PAD; }
 
 // Loads CNT consecutive values (4 fp32 or 8 bf16) at element k of row p, as
 // fp32; zero past the row or K.
+template <typename TS>
+constexpr int CNT_OF = std::is_same_v<TS, float> ? 4 : 8;
+
 template <typename TS, int CNT>
 __device__ __forceinline__ void gload(const TS* p, bool valid, int k, int K, bool vec, float (&v)[CNT]) {
   if constexpr (std::is_same_v<TS, float>) {
@@ -127,10 +139,310 @@ __device__ __forceinline__ void gload(const TS* p, bool valid, int k, int K, boo
   }
 }
 
-// The tile loads of one K step held in registers between the global load
-// and the LDS store. A: 128 x 32 of x; B: BN x 32 of w (fp32).
+// One vector LDS store of N values converted to the operand type (16 bytes
+// for fp32 x 4 and bf16 x 8, 8 bytes for bf16 x 4).
+template <typename T, int N>
+__device__ __forceinline__ void st_lds(T* d, const float (&v)[N]) {
+  if constexpr (std::is_same_v<T, float>) {
+    static_assert(N == 4, "fp32 LDS chunks are 4 values");
+    *reinterpret_cast<float4*>(d) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if constexpr (N == 4) {
+    *reinterpret_cast<bf16x4*>(d) = bf16x4{static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1]),
+                                           static_cast<__bf16>(v[2]), static_cast<__bf16>(v[3])};
+  } else {
+    static_assert(N == 8, "bf16 LDS chunks are 4 or 8 values");
+    bf16x8 t;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) t[q] = static_cast<__bf16>(v[q]);
+    *reinterpret_cast<bf16x8*>(d) = t;
+  }
+}
+
+// x fragments of one K step (32) for one 16-row tile, loaded straight from
+// global memory into registers (a wavefront owns its rows, so x needs no LDS
+// staging): lane l holds row l%16 and, for bf16 math, k = 8*(l/16) .. +7;
+// for fp32 math, k = 4*(l/16) .. +3 and 16 + 4*(l/16) .. +3.
+template <typename TX, int MATH>
+__device__ __forceinline__ void load_x(const GemmArgs& g, const TX* x, int64_t m, int k0, int ks, float (&v)[8]) {
+  const bool valid = m < g.M;
+  const TX* p = x + (valid ? m : 0) * g.K;
+  float lo[CNT_OF<TX>], hi[CNT_OF<TX>];
+  if constexpr (!std::is_same_v<TX, float>) {
+    gload<TX, 8>(p, valid, k0 + 8 * ks, g.K, g.vec, lo);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = lo[q];
+  } else {
+    const int ka = MATH == kMathBF16 ? k0 + 8 * ks : k0 + 4 * ks;
+    const int kb = MATH == kMathBF16 ? ka + 4 : ka + 16;
+    gload<float, 4>(p, valid, ka, g.K, g.vec, lo);
+    gload<float, 4>(p, valid, kb, g.K, g.vec, hi);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      v[q] = lo[q];
+      v[4 + q] = hi[q];
+    }
+  }
+}
+
+// One K step's x fragments of a wavefront: its two 16-row tiles.
+struct XStep {
+  float v[2][8];
+};
+
+template <typename TX, int MATH>
+__device__ __forceinline__ void load_xstep(const GemmArgs& g, const TX* x, int64_t row0, int k0, int lane, XStep& a) {
+#pragma unroll
+  for (int r = 0; r < 2; ++r) load_x<TX, MATH>(g, x, row0 + 16 * r + (lane & 15), k0, lane >> 4, a.v[r]);
+}
+
+// W tile of one K step (BN rows x 32) held in registers between the global
+// load and the LDS store; all 256 threads share it.
+template <int MATH, int BN>
+struct WStage {
+  static constexpr int CHUNKS = BN * kBK / 4 / kThreads;  // 16-byte fp32 chunks per thread
+  float b[CHUNKS][4];
+
+  __device__ __forceinline__ void load(const GemmArgs& g, int n0, int k0) {
+    constexpr int CPR = kBK / 4;
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      const int r = id / CPR, c = id % CPR;
+      const int n = n0 + r;
+      gload<float, 4>(g.w + static_cast<int64_t>(n < g.N ? n : 0) * g.K, n < g.N, k0 + c * 4, g.K, g.vec, b[i]);
+    }
+  }
+  __device__ __forceinline__ void store(typename Op<MATH>::T* Bs) const {
+    constexpr int S = lds_stride<MATH>();
+    constexpr int CPR = kBK / 4;
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      const int r = id / CPR, c = id % CPR;
+      st_lds<typename Op<MATH>::T, 4>(Bs + r * S + c * 4, b[i]);
+    }
+  }
+};
+
+// MFMAs of one K step. The W tile is the MFMA's first operand and x the
+// second, so D = W x^T: lane l holds output rows (of y) 16r + l%16 and, per
+// 16-column tile f, the four consecutive columns 16f + 4*(l/16) + q.
+template <int MATH, int TN>
+__device__ __forceinline__ void mma_step(const XStep& a, const typename Op<MATH>::T* Bs, int lane,
+                                         f32x4 (&acc)[2][TN]) {
+  constexpr int S = lds_stride<MATH>();
+  const int rl = lane & 15, ks = lane >> 4;
+  if constexpr (MATH == kMathBF16) {
+    bf16x8 xa[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) xa[r][q] = static_cast<__bf16>(a.v[r][q]);
+#pragma unroll
+    for (int f = 0; f < TN; ++f) {
+      const bf16x8 wb = *reinterpret_cast<const bf16x8*>(Bs + (16 * f + rl) * S + ks * 8);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb, xa[r], acc[r][f], 0, 0, 0);
+    }
+  } else {
+    // Two 16-k halves; within a half, lane group ks supplies k = 4*ks .. +3
+    // to four 16x16x4 MFMAs (the k order inside a sum is immaterial).
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int f = 0; f < TN; ++f) {
+        const float4 wb = *reinterpret_cast<const float4*>(Bs + (16 * f + rl) * S + 16 * h + ks * 4);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const float* xv = a.v[r] + 4 * h;
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.x, xv[0], acc[r][f], 0, 0, 0);
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.y, xv[1], acc[r][f], 0, 0, 0);
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.z, xv[2], acc[r][f], 0, 0, 0);
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.w, xv[3], acc[r][f], 0, 0, 0);
+        }
+      }
+  }
+}
+
+// Block index -> (row tile, column tile). Workgroups are dealt to the 8 XCDs
+// round robin; consecutive blocks of one XCD take the column tiles of one row
+// tile, so that row tile's x rows are fetched into one L2.
+__device__ __forceinline__ void tile_of(int nrt, int nct, int& rt, int& ct) {
+  const int b = blockIdx.x;
+  const int total = nrt * nct;
+  constexpr int kXcd = 8;
+  const int full = total - total % kXcd;
+  int v = b;
+  if (b < full) v = (b % kXcd) * (full / kXcd) + b / kXcd;
+  rt = v / nct;
+  ct = v % nct;
+}
+
+// y = x W^T (+ bias) with the epilogue EPI, one 128 x BN tile per workgroup.
+// The K loop keeps the x fragments of the next two K steps in flight (a
+// two-slot register ring per wavefront) and double-buffers the shared W tile
+// in LDS.
+template <typename TX, int MATH, int BN, int EPI>
+__global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs g, int nrt, int nct) {
+  using T = typename Op<MATH>::T;
+  constexpr int S = lds_stride<MATH>();
+  constexpr int TN = BN / 16;
+  __shared__ __align__(16) T Bs[2][BN * S];
+  const int lane = lane_id();
+  const int wave = wave_id();
+  int rt, ct;
+  tile_of(nrt, nct, rt, ct);
+  const int64_t row0 = static_cast<int64_t>(rt) * kBM + wave * kRowsPerWave;
+  const int n0 = ct * BN;
+  const TX* x = static_cast<const TX*>(g.x);
+
+  f32x4 acc[2][TN];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int f = 0; f < TN; ++f) acc[r][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int nk = (g.K + kBK - 1) / kBK;
+  XStep a0, a1;
+  WStage<MATH, BN> wst;
+  load_xstep<TX, MATH>(g, x, row0, 0, lane, a0);
+  if (nk > 1) load_xstep<TX, MATH>(g, x, row0, kBK, lane, a1);
+  wst.load(g, n0, 0);
+  wst.store(Bs[0]);
+  __syncthreads();
+  int buf = 0;
+  for (int s = 0; s < nk; s += 2) {
+    if (s + 1 < nk) wst.load(g, n0, (s + 1) * kBK);
+    mma_step<MATH, TN>(a0, Bs[buf], lane, acc);
+    if (s + 2 < nk) load_xstep<TX, MATH>(g, x, row0, (s + 2) * kBK, lane, a0);
+    if (s + 1 < nk) wst.store(Bs[buf ^ 1]);
+    __syncthreads();
+    buf ^= 1;
+    if (s + 1 >= nk) break;  // uniform
+    if (s + 2 < nk) wst.load(g, n0, (s + 2) * kBK);
+    mma_step<MATH, TN>(a1, Bs[buf], lane, acc);
+    if (s + 3 < nk) load_xstep<TX, MATH>(g, x, row0, (s + 3) * kBK, lane, a1);
+    if (s + 2 < nk) wst.store(Bs[buf ^ 1]);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  // Epilogue: lane holds row m = row0 + 16r + lane%16 and columns
+  // n = n0 + 16f + 4*(lane/16) + q, q < 4.
+  const int cg = (lane >> 4) * 4;
+#pragma unroll
+  for (int f = 0; f < TN; ++f) {
+    const int nb = n0 + 16 * f + cg;
+    const bool full4 = g.vec4 && nb + 4 <= g.N;
+    float bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bv[q] = (g.bias && nb + q < g.N) ? g.bias[nb + q] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int64_t m = row0 + 16 * r + (lane & 15);
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v[q] = acc[r][f][q] + bv[q];
+        if (g.round_bf16) v[q] = round_bf16(v[q]);
+        acc[r][f][q] = v[q];
+      }
+      if (m >= g.M) continue;
+      const int64_t o = m * g.N + nb;
+      if (full4) {
+        *reinterpret_cast<float4*>(g.y + o) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (nb + q < g.N) g.y[o + q] = v[q];
+      }
+      if constexpr (EPI == kEpiGamma) {
+        float hv[4], ov[4];
+        uint8_t mk[4];
+        if (full4) {
+          const float4 t = *reinterpret_cast<const float4*>(g.h + o);
+          hv[0] = t.x; hv[1] = t.y; hv[2] = t.z; hv[3] = t.w;
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) hv[q] = nb + q < g.N ? g.h[o + q] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const bool keep = block_keep(g.seed, static_cast<uint64_t>(o + q), g.p);
+          const float dv = keep ? (g.p > 0.0f ? v[q] / (1.0f - g.p) : v[q]) : 0.0f;
+          ov[q] = hv[q] + (nb + q < g.N ? g.gamma[nb + q] : 0.0f) * dv;
+          mk[q] = keep ? 1 : 0;
+        }
+        if (full4) {
+          *reinterpret_cast<float4*>(g.out + o) = make_float4(ov[0], ov[1], ov[2], ov[3]);
+          *reinterpret_cast<uchar4*>(g.mask + o) = make_uchar4(mk[0], mk[1], mk[2], mk[3]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (nb + q < g.N) {
+              g.out[o + q] = ov[q];
+              g.mask[o + q] = mk[q];
+            }
+        }
+      }
+    }
+  }
+  if constexpr (EPI == kEpiLogits) {
+    // Heads of C columns lie whole inside the tile (host: BN % C == 0,
+    // C % 16 == 0): sum y * att over a head's tiles and the lane's four
+    // columns, then over the four lane groups.
+    const int H = g.N / g.C;
+    const int fph = g.C / 16;
+    for (int h0 = 0; h0 < TN; h0 += fph) {
+      const int head = (n0 + 16 * h0) / g.C;
+      float ss[2] = {0.0f, 0.0f}, sd[2] = {0.0f, 0.0f};
+#pragma unroll
+      for (int f = 0; f < TN; ++f) {
+        if (f < h0 || f >= h0 + fph) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = n0 + 16 * f + cg + q;
+          const int c = n - head * g.C;
+          const float as = n < g.N ? g.att_src[static_cast<int64_t>(head) * g.C + c] : 0.0f;
+          const float ad = n < g.N ? g.att_dst[static_cast<int64_t>(head) * g.C + c] : 0.0f;
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            ss[r] = fmaf(acc[r][f][q], as, ss[r]);
+            sd[r] = fmaf(acc[r][f][q], ad, sd[r]);
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int o = 16; o < kWave; o <<= 1) {
+          ss[r] += shfl_xor(ss[r], o);
+          sd[r] += shfl_xor(sd[r], o);
+        }
+      if (lane < 16 && head < H) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int64_t m = row0 + 16 * r + lane;
+          if (m < g.M) {
+            g.alpha_src[m * H + head] = ss[r];
+            g.alpha_dst[m * H + head] = sd[r];
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 math: both operands staged through LDS
+// ---------------------------------------------------------------------------
+// With bf16 MFMAs (four times the fp32 rate) the K loop is bound by operand
+// delivery; staging x and W tiles in LDS as bf16 (converted once) and keeping
+// three workgroups per CU measured faster than register-resident x
+// fragments, which need the raw fp32 rows in flight. The tile loads of one K
+// step are held in registers between the global load and the LDS store. A: 128 x 32 of x; B: BN x 32 of w (fp32).
 template <typename TX, int MATH, int BN>
-struct StageRegs {
+struct LdsStage {
   static constexpr int XC = std::is_same_v<TX, float> ? 4 : 8;  // values per x chunk (16 bytes)
   static constexpr int A_CHUNKS = kBM * kBK / XC / kThreads;   // per thread
   static constexpr int B_CHUNKS = BN * kBK / 4 / kThreads;
@@ -164,18 +476,14 @@ struct StageRegs {
     for (int i = 0; i < A_CHUNKS; ++i) {
       const int id = threadIdx.x + i * kThreads;
       const int r = id / ACPR, c = id % ACPR;
-      T* d = As + r * S + c * XC;
-#pragma unroll
-      for (int q = 0; q < XC; ++q) d[q] = static_cast<T>(a[i][q]);
+      st_lds<T, XC>(As + r * S + c * XC, a[i]);
     }
     constexpr int BCPR = kBK / 4;
 #pragma unroll
     for (int i = 0; i < B_CHUNKS; ++i) {
       const int id = threadIdx.x + i * kThreads;
       const int r = id / BCPR, c = id % BCPR;
-      T* d = Bs + r * S + c * 4;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) d[q] = static_cast<T>(b[i][q]);
+      st_lds<T, 4>(Bs + r * S + c * 4, b[i]);
     }
   }
 };
@@ -183,7 +491,7 @@ struct StageRegs {
 // MFMAs of one K step on the LDS tiles: the wave's 2 row tiles x TN column
 // tiles.
 template <int MATH, int TN>
-__device__ __forceinline__ void mma_step(const typename Op<MATH>::T* As, const typename Op<MATH>::T* Bs, int wave,
+__device__ __forceinline__ void mma_step_lds(const typename Op<MATH>::T* As, const typename Op<MATH>::T* Bs, int wave,
                                          int lane, f32x4 (&acc)[2][TN]) {
   constexpr int S = lds_stride<MATH>();
   const int rl = lane & 15, ks = lane >> 4;
@@ -222,22 +530,9 @@ __device__ __forceinline__ void mma_step(const typename Op<MATH>::T* As, const t
   }
 }
 
-// Block index -> (row tile, column tile). Workgroups are dealt to the 8 XCDs
-// round robin; consecutive blocks of one XCD take the column tiles of one row
-// tile, so that row tile's x rows are fetched into one L2.
-__device__ __forceinline__ void tile_of(int nrt, int nct, int& rt, int& ct) {
-  const int b = blockIdx.x;
-  const int total = nrt * nct;
-  constexpr int kXcd = 8;
-  const int full = total - total % kXcd;
-  int v = b;
-  if (b < full) v = (b % kXcd) * (full / kXcd) + b / kXcd;
-  rt = v / nct;
-  ct = v % nct;
-}
 
 template <typename TX, int MATH, int BN, int EPI>
-__global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs g, int nrt, int nct) {
+__global__ __launch_bounds__(kThreads) void gemm_nt_lds_kernel(GemmArgs g, int nrt, int nct) {
   using T = typename Op<MATH>::T;
   constexpr int S = lds_stride<MATH>();
   constexpr int TN = BN / 16;
@@ -257,7 +552,7 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs g, int nrt, 
 #pragma unroll
     for (int f = 0; f < TN; ++f) acc[r][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  StageRegs<TX, MATH, BN> regs;
+  LdsStage<TX, MATH, BN> regs;
   regs.load(g, x, m0, n0, 0);
   regs.store(As[0], Bs[0]);
   __syncthreads();
@@ -265,7 +560,7 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs g, int nrt, 
   for (int k0 = 0; k0 < g.K; k0 += kBK) {
     const bool more = k0 + kBK < g.K;
     if (more) regs.load(g, x, m0, n0, k0 + kBK);
-    mma_step<MATH, TN>(As[buf], Bs[buf], wave, lane, acc);
+    mma_step_lds<MATH, TN>(As[buf], Bs[buf], wave, lane, acc);
     if (more) regs.store(As[buf ^ 1], Bs[buf ^ 1]);
     __syncthreads();
     buf ^= 1;
@@ -354,6 +649,8 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs g, int nrt, 
 }
 
 // ---------------------------------------------------------------------------
+
+// ---------------------------------------------------------------------------
 // Backward helpers
 // ---------------------------------------------------------------------------
 // part[c][n] = sum of grad_y rows of chunk c (a workgroup: 64 columns x 4 row
@@ -397,8 +694,11 @@ inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 1
 
 // Column tile: 64 for N <= 64, else 128. For the logits epilogue the tile
 // must hold whole heads of 16..128 columns.
-inline int pick_bn(int N, int C) {
-  int bn = N <= 64 ? 64 : 128;
+// Column tile: fp32 math 64 (two waves per SIMD with the register-resident x
+// fragments), bf16 math 64 for N <= 64 else 128. For the logits epilogue the
+// tile must hold whole heads of 16..128 columns.
+inline int pick_bn(int N, int C, int math) {
+  int bn = (math == kMathF32 || N <= 64) ? 64 : 128;
   if (C > 0) {
     if (C % 16 != 0 || C > 128) return 0;
     if (bn % C != 0) bn = 128;
@@ -414,12 +714,21 @@ int launch_nt(hipStream_t st, const GemmArgs& g, int bn) {
   const int64_t blocks = static_cast<int64_t>(nrt) * nct;
   if (blocks == 0) return kOk;
   if (blocks > 0x7fffffff) return set_error(kInvalid, "cign linear: too many tiles");
-  if (bn == 64)
-    hipLaunchKernelGGL((gemm_nt_kernel<TX, MATH, 64, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
-                       st, g, nrt, nct);
-  else
-    hipLaunchKernelGGL((gemm_nt_kernel<TX, MATH, 128, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
-                       st, g, nrt, nct);
+  if constexpr (MATH == kMathBF16) {
+    if (bn == 64)
+      hipLaunchKernelGGL((gemm_nt_lds_kernel<TX, MATH, 64, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
+                         0, st, g, nrt, nct);
+    else
+      hipLaunchKernelGGL((gemm_nt_lds_kernel<TX, MATH, 128, EPI>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(kThreads), 0, st, g, nrt, nct);
+  } else {
+    if (bn == 64)
+      hipLaunchKernelGGL((gemm_nt_kernel<TX, MATH, 64, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+                         st, g, nrt, nct);
+    else
+      hipLaunchKernelGGL((gemm_nt_kernel<TX, MATH, 128, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
+                         0, st, g, nrt, nct);
+  }
   return check_launch("cign linear");
 }
 
@@ -511,8 +820,9 @@ int cign_linear_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t x_dty
   GemmArgs g{};
   g.M = M; g.N = N; g.K = K; g.x = x; g.w = w; g.bias = bias; g.y = y;
   g.vec = rows_aligned(x, x_dtype, w, K);
+  g.vec4 = N % 4 == 0 && aligned16(y);
   g.round_bf16 = math == kMathBF16;
-  return dispatch_nt<kEpiStore>(static_cast<hipStream_t>(stream), g, x_dtype, math, pick_bn(N, 0));
+  return dispatch_nt<kEpiStore>(static_cast<hipStream_t>(stream), g, x_dtype, math, pick_bn(N, 0, math));
 }
 
 int cign_linear_logits_fwd(void* stream, int64_t M, int32_t heads, int32_t channels, int32_t K, int32_t x_dtype,
@@ -523,7 +833,7 @@ int cign_linear_logits_fwd(void* stream, int64_t M, int32_t heads, int32_t chann
   if (rc) return rc;
   if (!att_src || !att_dst || (M > 0 && (!alpha_src || !alpha_dst)))
     return set_error(kInvalid, "cign_linear_logits_fwd: null pointer");
-  const int bn = pick_bn(N, channels);
+  const int bn = pick_bn(N, channels, math);
   if (bn == 0)
     return set_error(kInvalid, "cign_linear_logits_fwd: channels=%d must be 16, 32, 64 or 128 (use cign_linear_fwd + "
                      "cign_attn_logits_fwd)", channels);
@@ -531,6 +841,7 @@ int cign_linear_logits_fwd(void* stream, int64_t M, int32_t heads, int32_t chann
   GemmArgs g{};
   g.M = M; g.N = N; g.K = K; g.x = x; g.w = w; g.y = y;
   g.vec = rows_aligned(x, x_dtype, w, K);
+  g.vec4 = N % 4 == 0 && aligned16(y);
   g.round_bf16 = math == kMathBF16;
   g.C = channels; g.att_src = att_src; g.att_dst = att_dst; g.alpha_src = alpha_src; g.alpha_dst = alpha_dst;
   return dispatch_nt<kEpiLogits>(static_cast<hipStream_t>(stream), g, x_dtype, math, bn);
@@ -548,9 +859,11 @@ int cign_linear_gamma_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t
   GemmArgs g{};
   g.M = M; g.N = N; g.K = K; g.x = x; g.w = w; g.bias = bias; g.y = g_out;
   g.vec = rows_aligned(x, x_dtype, w, K);
+  g.vec4 = N % 4 == 0 && aligned16(g_out) && aligned16(h) && aligned16(y) &&
+           reinterpret_cast<uintptr_t>(mask) % 4 == 0;
   g.round_bf16 = math == kMathBF16;
   g.h = h; g.gamma = gamma; g.p = dropout_p; g.seed = seed; g.out = y; g.mask = mask;
-  return dispatch_nt<kEpiGamma>(static_cast<hipStream_t>(stream), g, x_dtype, math, pick_bn(N, 0));
+  return dispatch_nt<kEpiGamma>(static_cast<hipStream_t>(stream), g, x_dtype, math, pick_bn(N, 0, math));
 }
 
 int64_t cign_linear_bwd_workspace_bytes(int64_t M, int32_t N, int32_t K, int32_t with_bias) {
