@@ -695,10 +695,11 @@ inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 1
 // Column tile: 64 for N <= 64, else 128. For the logits epilogue the tile
 // must hold whole heads of 16..128 columns.
 // Column tile: fp32 math 64 (two waves per SIMD with the register-resident x
-// fragments), bf16 math 64 for N <= 64 else 128. For the logits epilogue the
-// tile must hold whole heads of 16..128 columns.
+// fragments); bf16 math 64 up to N = 256 (more workgroups for the skinny
+// shapes), else 128. For the logits epilogue the tile must hold whole heads
+// of 16..128 columns.
 inline int pick_bn(int N, int C, int math) {
-  int bn = (math == kMathF32 || N <= 64) ? 64 : 128;
+  int bn = (math == kMathF32 || N <= 256) ? 64 : 128;
   if (C > 0) {
     if (C % 16 != 0 || C > 128) return 0;
     if (bn % C != 0) bn = 128;
