@@ -855,9 +855,10 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_agg_kernel(GatBwdArgs<T> 
   }
   float gp[W];
   grad_pre_chunk(a, row, ln.cw, gp);
+  const RowHead<V> rh = row_head(a, row, ln);  // issued with the loads above, before any use
   float wsum[V], A[V];
   rows_dots<W, V>(st, gp, cq, a.inv_h, wsum, A);
-  rows_emit(a, ln, row, row_head(a, row, ln), wsum, A, st.B, gp);
+  rows_emit(a, ln, row, rh, wsum, A, st.B, gp);
 }
 
 // ===========================================================================
@@ -951,17 +952,39 @@ __device__ __forceinline__ void cols_group_sum(ColAcc<W, V>& st) {
   }
 }
 
+// The column's own x chunks, needed after its entries: loaded before the
+// entry loop (off the critical path) when a lane owns at most two chunks,
+// after it otherwise (to keep registers for the entry batches).
+template <typename T, int V>
+struct XCol {
+  static constexpr int W = FlGeom<T>::W;
+  static constexpr bool kEarly = V <= 2;
+  typename Chunk<T, W>::Raw raw[kEarly ? V : 1];
+
+  template <int L>
+  __device__ __forceinline__ void prefetch(const GatBwdArgs<T>& a, const FlLane<L, V>& ln, int j) {
+    if constexpr (kEarly)
+#pragma unroll
+      for (int v = 0; v < V; ++v) raw[v] = Chunk<T, W>::load_raw(a.x + static_cast<int64_t>(j) * a.H * a.C + ln.q[v] * W);
+  }
+  template <int L>
+  __device__ __forceinline__ void get(const GatBwdArgs<T>& a, const FlLane<L, V>& ln, int j, int v,
+                                      float (&xj)[W]) const {
+    if constexpr (kEarly) Chunk<T, W>::unpack(raw[v], xj);
+    else Chunk<T, W>::load(a.x + static_cast<int64_t>(j) * a.H * a.C + ln.q[v] * W, xj);
+  }
+};
+
 // The lane's part of grad_attn_col[j, hq[v]] for each chunk v: <ua, x[j]
 // chunk> summed over the head's lanes / H, minus t.
 template <typename T, int L, int V>
 __device__ __forceinline__ void cols_gac(const GatBwdArgs<T>& a, const FlLane<L, V>& ln, const ColAcc<FlGeom<T>::W, V>& st,
-                                         int j, int cq, float (&gac)[V]) {
+                                         const XCol<T, V>& xc, int j, int cq, float (&gac)[V]) {
   constexpr int W = FlGeom<T>::W;
-  const int F = a.H * a.C;
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     float xj[W];
-    Chunk<T, W>::load(a.x + static_cast<int64_t>(j) * F + ln.q[v] * W, xj);
+    xc.get(a, ln, j, v, xj);
     float d = 0.0f;
 #pragma unroll
     for (int w = 0; w < W; ++w) d = fmaf(st.ua[v][w], xj[w], d);
@@ -1020,13 +1043,15 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
     const int ii = own ? a.rowind[r.y + slot] : 0;
     const int ee = (DROP && own) ? a.perm[r.y + slot] : 0;
     load_attn_col(a, ln, j, ac);
+    XCol<T, V> xc;
+    xc.prefetch(a, ln, j);
     if (tiny) {
       cols_edges<T, L, V, DROP>(a, ln, ii, ee, ln.g * L, 0, 1, deg, wave_group_max<L>(deg), ac, st);
     } else {
       cols_edges<T, L, V, DROP>(a, ln, ii, ee, 0, ln.g, G, deg, (deg + G - 1) / G, ac, st);
       cols_group_sum<L, W, V>(st);
     }
-    cols_gac(a, ln, st, j, cq, gac);
+    cols_gac(a, ln, st, xc, j, cq, gac);
     if (!(has && (tiny || ln.g == 0))) return;
 #pragma unroll
     for (int v = 0; v < V; ++v) {
@@ -1046,6 +1071,8 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
   const int j = sg.x;
   const int2 hr = s.hrow[sg.w];
   load_attn_col(a, ln, j, ac);
+  XCol<T, V> xc;
+  xc.prefetch(a, ln, j);
   for (int tb = sg.y + wave * kWave; tb < sg.z; tb += kSegRound) {
     const int cnt = min(kWave, sg.z - tb);
     const bool own = ln.lane < cnt;
@@ -1054,7 +1081,7 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
     cols_edges<T, L, V, DROP>(a, ln, ii, ee, 0, ln.g, G, cnt, (cnt + G - 1) / G, ac, st);
   }
   cols_group_sum<L, W, V>(st);
-  cols_gac(a, ln, st, j, cq, gac);
+  cols_gac(a, ln, st, xc, j, cq, gac);
   if (ln.g == 0 && ln.cw == 0)
 #pragma unroll
     for (int v = 0; v < V; ++v)
