@@ -687,6 +687,85 @@ __global__ void to_bf16_kernel(const float* src, int64_t n, __bf16* dst) {
     dst[i] = static_cast<__bf16>(src[i]);
 }
 
+// ---- Backward of a projection with few outputs (N <= kSmallN, e.g. the
+// classifier): two streaming passes on the VALU, where the library GEMMs
+// pick poor kernels for the degenerate shapes. Under autocast (RB) every
+// operand is rounded to bf16 before its product, as the bf16 GEMM would.
+constexpr int kSmallN = 16;
+
+__device__ __forceinline__ float rb_if(bool rb, float v) { return rb ? round_bf16(v) : v; }
+
+// grad_x[m, 4c .. 4c+3] = sum_n grad_y[m, n] W[n, 4c .. 4c+3]; a workgroup
+// covers 4 rows x 64 column quads (16-byte stores when K % 4 == 0).
+template <bool RB>
+__global__ __launch_bounds__(kThreads) void small_n_grad_x_kernel(const float* gy, int64_t M, int N, int K,
+                                                                  const float* w, float* gx) {
+  const int k = (blockIdx.x * 64 + (threadIdx.x & 63)) * 4;
+  const int64_t m = static_cast<int64_t>(blockIdx.y) * 4 + (threadIdx.x >> 6);
+  if (m >= M || k >= K) return;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const bool full = (K & 3) == 0;
+  for (int n = 0; n < N; ++n) {
+    const float g = rb_if(RB, gy[m * N + n]);
+    const float* wr = w + static_cast<int64_t>(n) * K + k;
+    if (full) {
+      const float4 t = *reinterpret_cast<const float4*>(wr);
+      acc[0] = fmaf(g, rb_if(RB, t.x), acc[0]);
+      acc[1] = fmaf(g, rb_if(RB, t.y), acc[1]);
+      acc[2] = fmaf(g, rb_if(RB, t.z), acc[2]);
+      acc[3] = fmaf(g, rb_if(RB, t.w), acc[3]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (k + q < K) acc[q] = fmaf(g, rb_if(RB, wr[q]), acc[q]);
+    }
+  }
+  float* o = gx + m * K + k;
+  if (full) {
+    *reinterpret_cast<float4*>(o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (k + q < K) o[q] = acc[q];
+  }
+}
+
+// part[c][n][k] = sum over the rows of chunk c of grad_y[m, n] x[m, k]; a
+// thread owns four consecutive k for all n.
+template <bool RB>
+__global__ __launch_bounds__(kThreads) void small_n_grad_w_kernel(const float* gy, const float* x, int64_t M, int N,
+                                                                  int K, int64_t chunk, float* part) {
+  const int K4 = (K + 3) / 4;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * chunk;
+  const int64_t r1 = r0 + chunk < M ? r0 + chunk : M;
+  for (int c4 = blockIdx.x * kThreads + threadIdx.x; c4 < K4; c4 += gridDim.x * kThreads) {
+    const int k = c4 * 4;
+    float acc[kSmallN][4];
+#pragma unroll
+    for (int n = 0; n < kSmallN; ++n)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[n][q] = 0.0f;
+#pragma unroll 4
+    for (int64_t m = r0; m < r1; ++m) {
+      float xv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) xv[q] = k + q < K ? rb_if(RB, x[m * K + k + q]) : 0.0f;
+#pragma unroll
+      for (int n = 0; n < kSmallN; ++n) {
+        const float g = n < N ? rb_if(RB, gy[m * N + n]) : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[n][q] = fmaf(g, xv[q], acc[n][q]);
+      }
+    }
+    float* out = part + static_cast<int64_t>(blockIdx.y) * N * K;
+#pragma unroll
+    for (int n = 0; n < kSmallN; ++n)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (n < N && k + q < K) out[static_cast<int64_t>(n) * K + k + q] = acc[n][q];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -780,19 +859,26 @@ rocblas_handle blas_handle(int& rc) {
 // Workspace layout of cign_linear_bwd.
 struct BwdWs {
   int chunks;
-  int64_t chunk, part_b, gy16, x16, w16, total;
+  int64_t chunk, part_b, part_w, gy16, x16, w16, total;
 };
 
 inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias, int math) {
   BwdWs L;
-  int64_t chunks = std::max<int64_t>(1, std::min<int64_t>(1024, (M + 63) / 64));
+  // row chunks of the bias (and, for few outputs, grad_W) partials: 64 rows,
+  // or 16 for few outputs (more workgroups for the per-chunk VALU sums)
+  const int64_t rows_per = N <= kSmallN ? 16 : 64;
+  int64_t chunks = std::max<int64_t>(1, std::min<int64_t>(N <= kSmallN ? 4096 : 1024, (M + rows_per - 1) / rows_per));
   L.chunk = std::max<int64_t>(1, (M + chunks - 1) / chunks);
   chunks = M > 0 ? (M + L.chunk - 1) / L.chunk : 1;
   L.chunks = static_cast<int>(chunks);
   auto al = [](int64_t v) { return (v + 255) & ~int64_t(255); };
   int64_t off = 0;
   L.part_b = off; off = al(off + (bias ? 4LL * chunks * N : 0));
-  const bool b16 = math == kMathBF16;
+  // few outputs: grad_W partials per row chunk; otherwise the library GEMMs
+  // (bf16 copies of their operands under autocast)
+  const bool small = N <= kSmallN;
+  L.part_w = off; off = al(off + (small ? 4LL * chunks * N * K : 0));
+  const bool b16 = math == kMathBF16 && !small;
   L.gy16 = off; off = al(off + (b16 ? 2LL * M * N : 0));
   L.x16 = off; off = al(off + (b16 ? 2LL * M * K : 0));
   L.w16 = off; off = al(off + (b16 ? 2LL * N * K : 0));
@@ -887,6 +973,36 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
   char* ws = static_cast<char*>(workspace);
   int rc;
   if (M == 0) return rowops::zero_outputs(st, grad_w, N * K, grad_b, grad_b ? N : 0, "cign_linear_bwd");
+  auto bias_grad = [&]() -> int {
+    if (!grad_b) return kOk;
+    float* part = reinterpret_cast<float*>(ws + L.part_b);
+    hipLaunchKernelGGL(bias_grad_kernel, dim3((N + 63) / 64, L.chunks), dim3(kThreads), 0, st, grad_y, M, N, L.chunk,
+                       part);
+    const int r = check_launch("cign_linear_bwd (bias partials)");
+    return r ? r : rowops::launch_colsum(st, part, L.chunks, N, 1, grad_b, nullptr, "cign_linear_bwd (bias)");
+  };
+  if (N <= kSmallN) {
+    const bool rb = math == kMathBF16;
+    const int K4 = (K + 3) / 4;
+    if (grad_x) {
+      const dim3 gxg((K4 + 63) / 64, static_cast<unsigned>((M + 3) / 4));
+      if (rb)
+        hipLaunchKernelGGL(small_n_grad_x_kernel<true>, gxg, dim3(kThreads), 0, st, grad_y, M, N, K, w, grad_x);
+      else
+        hipLaunchKernelGGL(small_n_grad_x_kernel<false>, gxg, dim3(kThreads), 0, st, grad_y, M, N, K, w, grad_x);
+      if ((rc = check_launch("cign_linear_bwd (grad_x, few outputs)"))) return rc;
+    }
+    float* part = reinterpret_cast<float*>(ws + L.part_w);
+    const dim3 grid((K4 + kThreads - 1) / kThreads, L.chunks);
+    if (rb)
+      hipLaunchKernelGGL(small_n_grad_w_kernel<true>, grid, dim3(kThreads), 0, st, grad_y, x, M, N, K, L.chunk, part);
+    else
+      hipLaunchKernelGGL(small_n_grad_w_kernel<false>, grid, dim3(kThreads), 0, st, grad_y, x, M, N, K, L.chunk, part);
+    if ((rc = check_launch("cign_linear_bwd (grad_W partials, few outputs)"))) return rc;
+    if ((rc = rowops::launch_colsum(st, part, L.chunks, N * K, 1, grad_w, nullptr, "cign_linear_bwd (grad_W)")))
+      return rc;
+    return bias_grad();
+  }
   rocblas_handle hdl = blas_handle(rc);
   if (!hdl) return rc;
   if ((rc = blas_check(rocblas_set_stream(hdl, st), "rocblas_set_stream"))) return rc;
@@ -928,14 +1044,7 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
                                   rocblas_datatype_f32_r, K, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0),
                   "grad_w gemm");
   if (rc) return rc;
-  if (grad_b) {
-    float* part = reinterpret_cast<float*>(ws + L.part_b);
-    hipLaunchKernelGGL(bias_grad_kernel, dim3((N + 63) / 64, L.chunks), dim3(kThreads), 0, st, grad_y, M, N, L.chunk,
-                       part);
-    if ((rc = check_launch("cign_linear_bwd (bias partials)"))) return rc;
-    return rowops::launch_colsum(st, part, L.chunks, N, 1, grad_b, nullptr, "cign_linear_bwd (bias)");
-  }
-  return kOk;
+  return bias_grad();
 }
 
 }  // extern "C"

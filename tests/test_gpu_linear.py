@@ -28,7 +28,7 @@ def _np(t):
 
 
 @pytest.mark.parametrize("M,N,K", [(1000, 64, 300), (777, 256, 1536), (130, 1536, 256), (5, 48, 20), (300, 50, 8),
-                                   (129, 3, 37), (64, 17, 5), (0, 16, 16)])
+                                   (129, 3, 37), (64, 17, 5), (0, 16, 16), (2000, 5, 768), (333, 16, 70)])
 @pytest.mark.parametrize("amp", [False, True])
 def test_linear_forward_backward(M, N, K, amp):
     from cign_amd.linear import mfma_linear
