@@ -37,7 +37,10 @@
 #include <mutex>
 #include <type_traits>
 
+#include <hipblaslt/hipblaslt.h>
 #include <rocblas/rocblas.h>
+
+#include <vector>
 
 #include "rowops.h"
 
@@ -859,8 +862,10 @@ rocblas_handle blas_handle(int& rc) {
 // Workspace layout of cign_linear_bwd.
 struct BwdWs {
   int chunks;
-  int64_t chunk, part_b, part_w, gy16, x16, w16, total;
+  int64_t chunk, part_b, part_w, gy16, x16, w16, lt, total;
 };
+
+constexpr int64_t kLtWs = 16 << 20;  // hipBLASLt workspace carved from the caller's
 
 inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias, int math) {
   BwdWs L;
@@ -882,8 +887,90 @@ inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias, int math) {
   L.gy16 = off; off = al(off + (b16 ? 2LL * M * N : 0));
   L.x16 = off; off = al(off + (b16 ? 2LL * M * K : 0));
   L.w16 = off; off = al(off + (b16 ? 2LL * N * K : 0));
+  L.lt = off; off = al(off + (small ? 0 : kLtWs));
   L.total = off;
   return L;
+}
+
+// ---- hipBLASLt for the backward's plain GEMMs (D = op(A) op(B), column
+// major, fp32 accumulation and output), one handle per device and one
+// heuristic choice per problem, cached; problems it has no kernel for fall
+// back to rocBLAS.
+
+struct LtPlan {
+  int dev, ta, tb, in_t;
+  int64_t m, n, k, lda, ldb, ldd;
+  bool ok;
+  hipblasLtMatmulDesc_t desc;
+  hipblasLtMatrixLayout_t a, b, d;
+  hipblasLtMatmulAlgo_t algo;
+  size_t ws;
+};
+
+hipblasLtHandle_t lt_handle(int dev) {
+  static std::mutex mu;
+  static hipblasLtHandle_t handles[64] = {};
+  if (dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!handles[dev] && hipblasLtCreate(&handles[dev]) != HIPBLAS_STATUS_SUCCESS) handles[dev] = nullptr;
+  return handles[dev];
+}
+
+// The cached plan of a problem (ok = false: no hipBLASLt kernel for it).
+const LtPlan* lt_plan(int dev, hipblasLtHandle_t h, int ta, int tb, int64_t m, int64_t n, int64_t k, int in_t,
+                      int64_t lda, int64_t ldb, int64_t ldd) {
+  static std::mutex mu;
+  static std::vector<LtPlan*> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const LtPlan* p : cache)
+    if (p->dev == dev && p->ta == ta && p->tb == tb && p->m == m && p->n == n && p->k == k && p->in_t == in_t &&
+        p->lda == lda && p->ldb == ldb && p->ldd == ldd)
+      return p;
+  LtPlan* p = new LtPlan{dev, ta, tb, in_t, m, n, k, lda, ldb, ldd, false, nullptr, nullptr, nullptr, nullptr, {}, 0};
+  cache.push_back(p);
+  const hipDataType it = static_cast<hipDataType>(in_t);
+  const hipblasOperation_t oa = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, ob = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+  if (hipblasLtMatmulDescCreate(&p->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return p;
+  if (hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &oa, sizeof(oa)) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &ob, sizeof(ob)) != HIPBLAS_STATUS_SUCCESS)
+    return p;
+  if (hipblasLtMatrixLayoutCreate(&p->a, it, ta ? k : m, ta ? m : k, lda) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&p->b, it, tb ? n : k, tb ? k : n, ldb) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&p->d, HIP_R_32F, m, n, ldd) != HIPBLAS_STATUS_SUCCESS)
+    return p;
+  hipblasLtMatmulPreference_t pref;
+  if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return p;
+  const uint64_t max_ws = kLtWs;
+  hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &max_ws, sizeof(max_ws));
+  hipblasLtMatmulHeuristicResult_t res[1];
+  int count = 0;
+  if (hipblasLtMatmulAlgoGetHeuristic(h, p->desc, p->a, p->b, p->d, p->d, pref, 1, res, &count) ==
+          HIPBLAS_STATUS_SUCCESS &&
+      count > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS && static_cast<int64_t>(res[0].workspaceSize) <= kLtWs) {
+    p->algo = res[0].algo;
+    p->ws = res[0].workspaceSize;
+    p->ok = true;
+  }
+  hipblasLtMatmulPreferenceDestroy(pref);
+  return p;
+}
+
+// D (fp32) = op(A) op(B) through hipBLASLt; false when it has no kernel (the
+// caller then uses rocBLAS), an error code in rc when the call fails.
+bool lt_gemm(hipStream_t st, int ta, int tb, int64_t m, int64_t n, int64_t k, const void* A, int64_t lda,
+             const void* B, int64_t ldb, float* D, int64_t ldd, int in_t, void* ws, int& rc) {
+  rc = kOk;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  hipblasLtHandle_t h = lt_handle(dev);
+  if (!h) return false;
+  const LtPlan* p = lt_plan(dev, h, ta, tb, m, n, k, in_t, lda, ldb, ldd);
+  if (!p->ok) return false;
+  const float one = 1.0f, zero = 0.0f;
+  if (hipblasLtMatmul(h, p->desc, &one, A, p->a, B, p->b, &zero, D, p->d, D, p->d, &p->algo, ws, p->ws, st) !=
+      HIPBLAS_STATUS_SUCCESS)
+    rc = set_error(kHipError, "cign_linear_bwd: hipblasLtMatmul failed");
+  return true;
 }
 
 inline int blas_check(rocblas_status s, const char* what) {
@@ -1030,19 +1117,23 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
   const int m32 = static_cast<int>(M);
   // Row-major C = A B is column-major C^T = B^T A^T.
   // grad_x [M,K] = grad_y [M,N] W [N,K]:  (K x M) = W_cm (K x N) * gy_cm (N x M)
-  if (grad_x) {
+  const int lt_t = math == kMathBF16 ? HIP_R_16BF : HIP_R_32F;
+  void* lt_ws = ws + L.lt;
+  if (grad_x && !lt_gemm(st, 0, 0, K, M, N, w_op, K, gy_op, N, grad_x, K, lt_t, lt_ws, rc)) {
     rc = blas_check(rocblas_gemm_ex(hdl, rocblas_operation_none, rocblas_operation_none, K, m32, N, &one, w_op, in_t, K,
                                     gy_op, in_t, N, &zero, grad_x, rocblas_datatype_f32_r, K, grad_x,
                                     rocblas_datatype_f32_r, K, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0,
                                     0),
                     "grad_x gemm");
-    if (rc) return rc;
   }
+  if (rc) return rc;
   // grad_W [N,K] = grad_y^T [N,M] x [M,K]:  (K x N) = x_cm (K x M) * gy_cm^T (M x N)
-  rc = blas_check(rocblas_gemm_ex(hdl, rocblas_operation_none, rocblas_operation_transpose, K, N, m32, &one, x_op, in_t,
-                                  K, gy_op, in_t, N, &zero, grad_w, rocblas_datatype_f32_r, K, grad_w,
-                                  rocblas_datatype_f32_r, K, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0),
-                  "grad_w gemm");
+  if (!lt_gemm(st, 0, 1, K, N, M, x_op, K, gy_op, N, grad_w, K, lt_t, lt_ws, rc))
+    rc = blas_check(rocblas_gemm_ex(hdl, rocblas_operation_none, rocblas_operation_transpose, K, N, m32, &one, x_op,
+                                    in_t, K, gy_op, in_t, N, &zero, grad_w, rocblas_datatype_f32_r, K, grad_w,
+                                    rocblas_datatype_f32_r, K, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0,
+                                    0),
+                    "grad_w gemm");
   if (rc) return rc;
   return bias_grad();
 }
