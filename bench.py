@@ -174,7 +174,8 @@ def summarize(prof_dir: str, name: str, command: str) -> None:
     """Writes profiles/<name>_kernel_stats.txt, _traffic.txt and _traffic.json
     from rocprofv3 CSV output: <prof_dir>/kt (--kernel-trace --stats),
     <prof_dir>/fetch (--pmc FETCH_SIZE) and <prof_dir>/write (--pmc WRITE_SIZE),
-    each made with --calibrate-copy for the counter runs."""
+    each made with --calibrate-copy for the counter runs (kernel statistics
+    only when there are no counter runs)."""
     import csv
     import glob
     import statistics
@@ -190,6 +191,9 @@ def summarize(prof_dir: str, name: str, command: str) -> None:
         lines.append(f"{_short(r['Name'])[:72]:72s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} "
                      f"{float(r['MinNs']) / 1e3:9.2f} {float(r['MaxNs']) / 1e3:9.2f} {float(r['Percentage']):6.2f}")
     (out / f"{name}_kernel_stats.txt").write_text("\n".join(lines) + "\n")
+    if not (prof / "fetch").exists():
+        print(f"wrote profiles/{name}_kernel_stats.txt (no counter runs)")
+        return
 
     def counters(sub, counter):
         per = {}

@@ -690,6 +690,159 @@ __global__ void to_bf16_kernel(const float* src, int64_t n, __bf16* dst) {
     dst[i] = static_cast<__bf16>(src[i]);
 }
 
+// ---- grad_W = grad_y^T x of the larger projections: a reduction over the
+// M node rows with a small output, which the library GEMMs run at a fraction
+// of their speed. A workgroup owns a 128 x 128 tile of grad_W and a chunk of
+// rows; per 32-row step it loads the grad_y and x row slices (fp32, 16-byte
+// loads), converts them to the MFMA operand type and stores them transposed
+// in LDS ([n][m] and [k][m], double buffered), so each MFMA operand fragment
+// (8 consecutive m of one n or k) is one 16-byte LDS read. The four
+// wavefronts each compute 64 x 64 outputs. Each chunk writes its partial
+// tile; colsum_kernel adds the chunks in order (deterministic, no atomics).
+constexpr int kWgT = 128;  // grad_W tile (n and k)
+constexpr int kWgM = 32;   // rows per step
+
+// LDS layout of a transposed operand tile: 128 rows (n or k) of 32 m values
+// in the MFMA operand type, no padding; the 16-byte chunk c of row j is
+// stored at chunk position c ^ ((j / 4) % chunks), which spreads the
+// transposed stores of one wavefront over the banks while every operand
+// fragment stays one aligned 16-byte read.
+template <int MATH>
+struct WgLayout {
+  using T = typename Op<MATH>::T;
+  static constexpr int CE = 16 / sizeof(T);  // elements per 16-byte chunk
+  static constexpr int NC = kWgM / CE;       // chunks per row
+  __device__ __forceinline__ static int pos(int j, int m) {
+    return j * kWgM + (((m / CE) ^ ((j / 4) % NC)) * CE) + m % CE;
+  }
+  __device__ __forceinline__ static int frag(int j, int chunk) { return j * kWgM + ((chunk ^ ((j / 4) % NC)) * CE); }
+};
+
+template <int MATH>
+struct WgStage {
+  // 128 columns x 32 rows of one operand: 1024 float4, four per thread.
+  // Thread id takes row id / 8 and column quads id % 8 + 8i, so a
+  // wavefront's load covers 8 rows x 128 contiguous bytes.
+  float v[4][4];
+  __device__ __forceinline__ void load(const float* src, int64_t ld, int64_t m0, int64_t m1, int c0, int cmax,
+                                       bool vec) {
+    const int r = threadIdx.x / 8;
+    const int64_t m = m0 + r;
+    const bool ok = m < m1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = ((threadIdx.x % 8) + 8 * i) * 4;
+      const float* p = src + (ok ? m : 0) * ld + c0 + c;
+      if (vec && ok && c0 + c + 4 <= cmax) {
+        const float4 t = *reinterpret_cast<const float4*>(p);
+        v[i][0] = t.x; v[i][1] = t.y; v[i][2] = t.z; v[i][3] = t.w;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[i][q] = (ok && c0 + c + q < cmax) ? p[q] : 0.0f;
+      }
+    }
+  }
+  __device__ __forceinline__ void store(typename Op<MATH>::T* Ts) const {
+    using T = typename Op<MATH>::T;
+    const int r = threadIdx.x / 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = ((threadIdx.x % 8) + 8 * i) * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) Ts[WgLayout<MATH>::pos(c + q, r)] = static_cast<T>(v[i][q]);
+    }
+  }
+};
+
+template <int MATH>
+__global__ __launch_bounds__(kThreads) void wgrad_kernel(const float* gy, const float* x, int64_t M, int N, int K,
+                                                         int64_t chunk, int ntk, bool vec, float* part) {
+  using T = typename Op<MATH>::T;
+  using Lay = WgLayout<MATH>;
+  __shared__ __align__(16) T Gs[2][kWgT * kWgM];
+  __shared__ __align__(16) T Xs[2][kWgT * kWgM];
+  const int lane = lane_id();
+  const int wave = wave_id();
+  const int n0 = (blockIdx.x / ntk) * kWgT, k0 = (blockIdx.x % ntk) * kWgT;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * chunk;
+  const int64_t m1 = m0 + chunk < M ? m0 + chunk : M;
+  const int wn = (wave >> 1) * 64, wk = (wave & 1) * 64;  // the wave's 64 x 64 quadrant
+  const int rl = lane & 15, ks = lane >> 4;
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  WgStage<MATH> sg, sx;
+  sg.load(gy, N, m0, m1, n0, N, vec);
+  sx.load(x, K, m0, m1, k0, K, vec);
+  sg.store(Gs[0]);
+  sx.store(Xs[0]);
+  __syncthreads();
+  int buf = 0;
+  for (int64_t mb = m0; mb < m1; mb += kWgM) {
+    const bool more = mb + kWgM < m1;
+    if (more) {
+      sg.load(gy, N, mb + kWgM, m1, n0, N, vec);
+      sx.load(x, K, mb + kWgM, m1, k0, K, vec);
+    }
+    const T* G = Gs[buf];
+    const T* X = Xs[buf];
+    if constexpr (MATH == kMathBF16) {
+      bf16x8 xb[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xb[j] = *reinterpret_cast<const bf16x8*>(X + Lay::frag(wk + 16 * j + rl, ks));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bf16x8 gb = *reinterpret_cast<const bf16x8*>(G + Lay::frag(wn + 16 * i + rl, ks));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gb, xb[j], acc[i][j], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float4 xb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          xb[j] = *reinterpret_cast<const float4*>(X + Lay::frag(wk + 16 * j + rl, 4 * h + ks));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 gb = *reinterpret_cast<const float4*>(G + Lay::frag(wn + 16 * i + rl, 4 * h + ks));
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.x, xb[j].x, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.y, xb[j].y, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.z, xb[j].z, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.w, xb[j].w, acc[i][j], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (more) {
+      sg.store(Gs[buf ^ 1]);
+      sx.store(Xs[buf ^ 1]);
+    }
+    __syncthreads();
+    buf ^= 1;
+  }
+  // lane holds grad_W rows n = n0 + wn + 16i + 4*(lane/16) + q of column
+  // k = k0 + wk + 16j + lane%16
+  float* out = part + static_cast<int64_t>(blockIdx.y) * N * K;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = k0 + wk + 16 * j + rl;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn + 16 * i + 4 * ks + q;
+        if (n < N && k < K) out[static_cast<int64_t>(n) * K + k] = acc[i][j][q];
+      }
+    }
+}
+
 // ---- Backward of a projection with few outputs (N <= kSmallN, e.g. the
 // classifier): two streaming passes on the VALU, where the library GEMMs
 // pick poor kernels for the degenerate shapes. Under autocast (RB) every
@@ -861,8 +1014,8 @@ rocblas_handle blas_handle(int& rc) {
 
 // Workspace layout of cign_linear_bwd.
 struct BwdWs {
-  int chunks;
-  int64_t chunk, part_b, part_w, gy16, x16, w16, lt, total;
+  int chunks, wg_chunks;
+  int64_t chunk, wg_chunk, part_b, part_w, gy16, w16, lt, total;
 };
 
 constexpr int64_t kLtWs = 16 << 20;  // hipBLASLt workspace carved from the caller's
@@ -879,13 +1032,19 @@ inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias, int math) {
   auto al = [](int64_t v) { return (v + 255) & ~int64_t(255); };
   int64_t off = 0;
   L.part_b = off; off = al(off + (bias ? 4LL * chunks * N : 0));
-  // few outputs: grad_W partials per row chunk; otherwise the library GEMMs
-  // (bf16 copies of their operands under autocast)
+  // grad_W partials per row chunk: the few-output VALU sums use the bias
+  // chunks; the MFMA kernel takes chunks of >= 256 rows, about 512
+  // workgroups over its 128 x 128 tiles
   const bool small = N <= kSmallN;
-  L.part_w = off; off = al(off + (small ? 4LL * chunks * N * K : 0));
+  const int64_t tiles = static_cast<int64_t>((N + kWgT - 1) / kWgT) * ((K + kWgT - 1) / kWgT);
+  int64_t wgc = std::max<int64_t>(1, std::min<int64_t>((M + 255) / 256, 512 / tiles));
+  L.wg_chunk = std::max<int64_t>(kWgM, ((M + wgc - 1) / wgc + kWgM - 1) / kWgM * kWgM);
+  wgc = M > 0 ? (M + L.wg_chunk - 1) / L.wg_chunk : 1;
+  L.wg_chunks = static_cast<int>(wgc);
+  L.part_w = off; off = al(off + 4LL * (small ? chunks : wgc) * N * K);
+  // grad_x on the library GEMM: bf16 copies of grad_y and W under autocast
   const bool b16 = math == kMathBF16 && !small;
   L.gy16 = off; off = al(off + (b16 ? 2LL * M * N : 0));
-  L.x16 = off; off = al(off + (b16 ? 2LL * M * K : 0));
   L.w16 = off; off = al(off + (b16 ? 2LL * N * K : 0));
   L.lt = off; off = al(off + (small ? 0 : kLtWs));
   L.total = off;
@@ -1090,50 +1249,53 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
       return rc;
     return bias_grad();
   }
-  rocblas_handle hdl = blas_handle(rc);
-  if (!hdl) return rc;
-  if ((rc = blas_check(rocblas_set_stream(hdl, st), "rocblas_set_stream"))) return rc;
-  const float one = 1.0f, zero = 0.0f;
-  const void *gy_op = grad_y, *x_op = x, *w_op = w;
+  // grad_W [N,K] = grad_y^T x: split-M MFMA partials, then chunk sums.
+  {
+    const int ntk = (K + kWgT - 1) / kWgT;
+    const dim3 grid(static_cast<unsigned>(((N + kWgT - 1) / kWgT) * ntk), static_cast<unsigned>(L.wg_chunks));
+    const bool vec = N % 4 == 0 && K % 4 == 0 && aligned16(grad_y) && aligned16(x);
+    float* part = reinterpret_cast<float*>(ws + L.part_w);
+    if (math == kMathBF16)
+      hipLaunchKernelGGL(wgrad_kernel<kMathBF16>, grid, dim3(kThreads), 0, st, grad_y, x, M, N, K, L.wg_chunk, ntk,
+                         vec, part);
+    else
+      hipLaunchKernelGGL(wgrad_kernel<kMathF32>, grid, dim3(kThreads), 0, st, grad_y, x, M, N, K, L.wg_chunk, ntk,
+                         vec, part);
+    if ((rc = check_launch("cign_linear_bwd (grad_W partials)"))) return rc;
+    if ((rc = rowops::launch_colsum(st, part, L.wg_chunks, N * K, 1, grad_w, nullptr, "cign_linear_bwd (grad_W)")))
+      return rc;
+  }
+  if (!grad_x) return bias_grad();
+  // grad_x [M,K] = grad_y [M,N] W [N,K] on the library GEMM. Row-major C = A B
+  // is column-major C^T = B^T A^T: (K x M) = W_cm (K x N) * gy_cm (N x M).
+  const void *gy_op = grad_y, *w_op = w;
   rocblas_datatype in_t = rocblas_datatype_f32_r;
   if (math == kMathBF16) {
-    // autocast semantics: the backward GEMMs read bf16 operands
+    // autocast semantics: the backward GEMM reads bf16 operands
     __bf16* gy16 = reinterpret_cast<__bf16*>(ws + L.gy16);
-    __bf16* x16 = reinterpret_cast<__bf16*>(ws + L.x16);
     __bf16* w16 = reinterpret_cast<__bf16*>(ws + L.w16);
-    auto conv = [&](const float* s, int64_t n, __bf16* d) {
+    auto conv = [&](const float* src, int64_t n, __bf16* d) {
       const int64_t gb = std::min<int64_t>((n + 255) / 256, 8192);
-      hipLaunchKernelGGL(to_bf16_kernel, dim3(static_cast<unsigned>(gb)), dim3(256), 0, st, s, n, d);
+      hipLaunchKernelGGL(to_bf16_kernel, dim3(static_cast<unsigned>(gb)), dim3(256), 0, st, src, n, d);
       return check_launch("cign_linear_bwd (bf16 operands)");
     };
-    if ((rc = conv(grad_y, M * N, gy16)) || (rc = conv(x, M * K, x16)) ||
-        (rc = conv(w, static_cast<int64_t>(N) * K, w16)))
-      return rc;
+    if ((rc = conv(grad_y, M * N, gy16)) || (rc = conv(w, static_cast<int64_t>(N) * K, w16))) return rc;
     gy_op = gy16;
-    x_op = x16;
     w_op = w16;
     in_t = rocblas_datatype_bf16_r;
   }
-  const int m32 = static_cast<int>(M);
-  // Row-major C = A B is column-major C^T = B^T A^T.
-  // grad_x [M,K] = grad_y [M,N] W [N,K]:  (K x M) = W_cm (K x N) * gy_cm (N x M)
   const int lt_t = math == kMathBF16 ? HIP_R_16BF : HIP_R_32F;
-  void* lt_ws = ws + L.lt;
-  if (grad_x && !lt_gemm(st, 0, 0, K, M, N, w_op, K, gy_op, N, grad_x, K, lt_t, lt_ws, rc)) {
-    rc = blas_check(rocblas_gemm_ex(hdl, rocblas_operation_none, rocblas_operation_none, K, m32, N, &one, w_op, in_t, K,
-                                    gy_op, in_t, N, &zero, grad_x, rocblas_datatype_f32_r, K, grad_x,
-                                    rocblas_datatype_f32_r, K, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0,
-                                    0),
+  if (!lt_gemm(st, 0, 0, K, M, N, w_op, K, gy_op, N, grad_x, K, lt_t, ws + L.lt, rc)) {
+    rocblas_handle hdl = blas_handle(rc);
+    if (!hdl) return rc;
+    if ((rc = blas_check(rocblas_set_stream(hdl, st), "rocblas_set_stream"))) return rc;
+    const float one = 1.0f, zero = 0.0f;
+    rc = blas_check(rocblas_gemm_ex(hdl, rocblas_operation_none, rocblas_operation_none, K, static_cast<int>(M), N,
+                                    &one, w_op, in_t, K, gy_op, in_t, N, &zero, grad_x, rocblas_datatype_f32_r, K,
+                                    grad_x, rocblas_datatype_f32_r, K, rocblas_datatype_f32_r,
+                                    rocblas_gemm_algo_standard, 0, 0),
                     "grad_x gemm");
   }
-  if (rc) return rc;
-  // grad_W [N,K] = grad_y^T [N,M] x [M,K]:  (K x N) = x_cm (K x M) * gy_cm^T (M x N)
-  if (!lt_gemm(st, 0, 1, K, N, M, x_op, K, gy_op, N, grad_w, K, lt_t, lt_ws, rc))
-    rc = blas_check(rocblas_gemm_ex(hdl, rocblas_operation_none, rocblas_operation_transpose, K, N, m32, &one, x_op,
-                                    in_t, K, gy_op, in_t, N, &zero, grad_w, rocblas_datatype_f32_r, K, grad_w,
-                                    rocblas_datatype_f32_r, K, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0,
-                                    0),
-                    "grad_w gemm");
   if (rc) return rc;
   return bias_grad();
 }
