@@ -281,57 +281,11 @@ __device__ __forceinline__ void tile_of(int nrt, int nct, int& rt, int& ct) {
   ct = v % nct;
 }
 
-// y = x W^T (+ bias) with the epilogue EPI, one 128 x BN tile per workgroup.
-// The K loop keeps the x fragments of the next two K steps in flight (a
-// two-slot register ring per wavefront) and double-buffers the shared W tile
-// in LDS.
-template <typename TX, int MATH, int BN, int EPI>
-__global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs g, int nrt, int nct) {
-  using T = typename Op<MATH>::T;
-  constexpr int S = lds_stride<MATH>();
-  constexpr int TN = BN / 16;
-  __shared__ __align__(16) T Bs[2][BN * S];
-  const int lane = lane_id();
-  const int wave = wave_id();
-  int rt, ct;
-  tile_of(nrt, nct, rt, ct);
-  const int64_t row0 = static_cast<int64_t>(rt) * kBM + wave * kRowsPerWave;
-  const int n0 = ct * BN;
-  const TX* x = static_cast<const TX*>(g.x);
-
-  f32x4 acc[2][TN];
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int f = 0; f < TN; ++f) acc[r][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  const int nk = (g.K + kBK - 1) / kBK;
-  XStep a0, a1;
-  WStage<MATH, BN> wst;
-  load_xstep<TX, MATH>(g, x, row0, 0, lane, a0);
-  if (nk > 1) load_xstep<TX, MATH>(g, x, row0, kBK, lane, a1);
-  wst.load(g, n0, 0);
-  wst.store(Bs[0]);
-  __syncthreads();
-  int buf = 0;
-  for (int s = 0; s < nk; s += 2) {
-    if (s + 1 < nk) wst.load(g, n0, (s + 1) * kBK);
-    mma_step<MATH, TN>(a0, Bs[buf], lane, acc);
-    if (s + 2 < nk) load_xstep<TX, MATH>(g, x, row0, (s + 2) * kBK, lane, a0);
-    if (s + 1 < nk) wst.store(Bs[buf ^ 1]);
-    __syncthreads();
-    buf ^= 1;
-    if (s + 1 >= nk) break;  // uniform
-    if (s + 2 < nk) wst.load(g, n0, (s + 2) * kBK);
-    mma_step<MATH, TN>(a1, Bs[buf], lane, acc);
-    if (s + 3 < nk) load_xstep<TX, MATH>(g, x, row0, (s + 3) * kBK, lane, a1);
-    if (s + 2 < nk) wst.store(Bs[buf ^ 1]);
-    __syncthreads();
-    buf ^= 1;
-  }
-
-  // Epilogue: lane holds row m = row0 + 16r + lane%16 and columns
-  // n = n0 + 16f + 4*(lane/16) + q, q < 4.
+// Epilogue of the swapped-operand layout: lane holds output row m = row0 +
+// 16r + lane%16 and columns n = n0 + 16f + 4*(lane/16) + q, q < 4.
+template <int EPI, int TN>
+__device__ __forceinline__ void epilogue_swapped(const GemmArgs& g, f32x4 (&acc)[2][TN], int64_t row0, int n0,
+                                                 int lane) {
   const int cg = (lane >> 4) * 4;
 #pragma unroll
   for (int f = 0; f < TN; ++f) {
@@ -436,6 +390,58 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs g, int nrt, 
   }
 }
 
+// y = x W^T (+ bias) with the epilogue EPI, one 128 x BN tile per workgroup.
+// The K loop keeps the x fragments of the next two K steps in flight (a
+// two-slot register ring per wavefront) and double-buffers the shared W tile
+// in LDS.
+template <typename TX, int MATH, int BN, int EPI>
+__global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs g, int nrt, int nct) {
+  using T = typename Op<MATH>::T;
+  constexpr int S = lds_stride<MATH>();
+  constexpr int TN = BN / 16;
+  __shared__ __align__(16) T Bs[2][BN * S];
+  const int lane = lane_id();
+  const int wave = wave_id();
+  int rt, ct;
+  tile_of(nrt, nct, rt, ct);
+  const int64_t row0 = static_cast<int64_t>(rt) * kBM + wave * kRowsPerWave;
+  const int n0 = ct * BN;
+  const TX* x = static_cast<const TX*>(g.x);
+
+  f32x4 acc[2][TN];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int f = 0; f < TN; ++f) acc[r][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int nk = (g.K + kBK - 1) / kBK;
+  XStep a0, a1;
+  WStage<MATH, BN> wst;
+  load_xstep<TX, MATH>(g, x, row0, 0, lane, a0);
+  if (nk > 1) load_xstep<TX, MATH>(g, x, row0, kBK, lane, a1);
+  wst.load(g, n0, 0);
+  wst.store(Bs[0]);
+  __syncthreads();
+  int buf = 0;
+  for (int s = 0; s < nk; s += 2) {
+    if (s + 1 < nk) wst.load(g, n0, (s + 1) * kBK);
+    mma_step<MATH, TN>(a0, Bs[buf], lane, acc);
+    if (s + 2 < nk) load_xstep<TX, MATH>(g, x, row0, (s + 2) * kBK, lane, a0);
+    if (s + 1 < nk) wst.store(Bs[buf ^ 1]);
+    __syncthreads();
+    buf ^= 1;
+    if (s + 1 >= nk) break;  // uniform
+    if (s + 2 < nk) wst.load(g, n0, (s + 2) * kBK);
+    mma_step<MATH, TN>(a1, Bs[buf], lane, acc);
+    if (s + 3 < nk) load_xstep<TX, MATH>(g, x, row0, (s + 3) * kBK, lane, a1);
+    if (s + 2 < nk) wst.store(Bs[buf ^ 1]);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  epilogue_swapped<EPI, TN>(g, acc, row0, n0, lane);
+}
+
 // ---------------------------------------------------------------------------
 // bf16 math: both operands staged through LDS
 // ---------------------------------------------------------------------------
@@ -492,7 +498,8 @@ struct LdsStage {
 };
 
 // MFMAs of one K step on the LDS tiles: the wave's 2 row tiles x TN column
-// tiles.
+// tiles, W as the first operand (the swapped-operand accumulator layout of
+// epilogue_swapped).
 template <int MATH, int TN>
 __device__ __forceinline__ void mma_step_lds(const typename Op<MATH>::T* As, const typename Op<MATH>::T* Bs, int wave,
                                          int lane, f32x4 (&acc)[2][TN]) {
@@ -507,7 +514,7 @@ __device__ __forceinline__ void mma_step_lds(const typename Op<MATH>::T* As, con
     for (int f = 0; f < TN; ++f) {
       const bf16x8 b = *reinterpret_cast<const bf16x8*>(Bs + (16 * f + rl) * S + ks * 8);
 #pragma unroll
-      for (int r = 0; r < 2; ++r) acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[r], b, acc[r][f], 0, 0, 0);
+      for (int r = 0; r < 2; ++r) acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, a[r], acc[r][f], 0, 0, 0);
     }
   } else {
     // Two 16-k halves; within a half, lane group ks supplies k = 4*ks .. +3
@@ -523,10 +530,10 @@ __device__ __forceinline__ void mma_step_lds(const typename Op<MATH>::T* As, con
         const float4 b = *reinterpret_cast<const float4*>(Bs + (16 * f + rl) * S + hk + ks * 4);
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r].x, b.x, acc[r][f], 0, 0, 0);
-          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r].y, b.y, acc[r][f], 0, 0, 0);
-          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r].z, b.z, acc[r][f], 0, 0, 0);
-          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r].w, b.w, acc[r][f], 0, 0, 0);
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(b.x, a[r].x, acc[r][f], 0, 0, 0);
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(b.y, a[r].y, acc[r][f], 0, 0, 0);
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(b.z, a[r].z, acc[r][f], 0, 0, 0);
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(b.w, a[r].w, acc[r][f], 0, 0, 0);
         }
       }
     }
@@ -569,86 +576,7 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_lds_kernel(GemmArgs g, int n
     buf ^= 1;
   }
 
-  // Epilogue: lane holds rows m0 + 32*wave + 16r + 4*(lane/16) + i of column
-  // n0 + 16f + lane%16.
-  const int cl = lane & 15;
-  const int rq = (lane >> 4) * 4;
-  const int64_t row0 = m0 + wave * kRowsPerWave;
-#pragma unroll
-  for (int f = 0; f < TN; ++f) {
-    const int n = n0 + 16 * f + cl;
-    const bool nv = n < g.N;
-    const float bv = (g.bias && nv) ? g.bias[n] : 0.0f;
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float v = acc[r][f][i] + bv;
-        if (g.round_bf16) v = round_bf16(v);
-        acc[r][f][i] = v;
-        const int64_t m = row0 + 16 * r + rq + i;
-        if (!nv || m >= g.M) continue;
-        const int64_t o = m * g.N + n;
-        g.y[o] = v;
-        if constexpr (EPI == kEpiGamma) {
-          const bool keep = block_keep(g.seed, static_cast<uint64_t>(o), g.p);
-          const float dv = keep ? (g.p > 0.0f ? v / (1.0f - g.p) : v) : 0.0f;
-          g.out[o] = g.h[o] + g.gamma[n] * dv;
-          g.mask[o] = keep ? 1 : 0;
-        }
-      }
-  }
-  if constexpr (EPI == kEpiLogits) {
-    // Heads of C columns lie whole inside the tile (host: BN % C == 0,
-    // C % 16 == 0). Sum over a head's fragments in the lane, then over the 16
-    // column lanes.
-    const int H = g.N / g.C;
-    const int fph = g.C / 16;
-    for (int h0 = 0; h0 < TN; h0 += fph) {
-      const int head = (n0 + 16 * h0) / g.C;
-      float ss[2][4], sd[2][4];
-#pragma unroll
-      for (int r = 0; r < 2; ++r)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ss[r][i] = sd[r][i] = 0.0f;
-#pragma unroll
-      for (int f = 0; f < TN; ++f) {
-        if (f < h0 || f >= h0 + fph) continue;
-        const int n = n0 + 16 * f + cl;
-        const int c = n - head * g.C;
-        const float as = n < g.N ? g.att_src[static_cast<int64_t>(head) * g.C + c] : 0.0f;
-        const float ad = n < g.N ? g.att_dst[static_cast<int64_t>(head) * g.C + c] : 0.0f;
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            ss[r][i] = fmaf(acc[r][f][i], as, ss[r][i]);
-            sd[r][i] = fmaf(acc[r][f][i], ad, sd[r][i]);
-          }
-      }
-#pragma unroll
-      for (int r = 0; r < 2; ++r)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int o = 1; o < 16; o <<= 1) {
-            ss[r][i] += shfl_xor(ss[r][i], o);
-            sd[r][i] += shfl_xor(sd[r][i], o);
-          }
-      if (cl == 0 && head < H) {
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int64_t m = row0 + 16 * r + rq + i;
-            if (m < g.M) {
-              g.alpha_src[m * H + head] = ss[r][i];
-              g.alpha_dst[m * H + head] = sd[r][i];
-            }
-          }
-      }
-    }
-  }
+  epilogue_swapped<EPI, TN>(g, acc, m0 + wave * kRowsPerWave, n0, lane);
 }
 
 // ---------------------------------------------------------------------------
