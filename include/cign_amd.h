@@ -299,10 +299,12 @@ int cign_linear_gamma_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t
 /* Workspace bytes of cign_linear_bwd. */
 int64_t cign_linear_bwd_workspace_bytes(int64_t M, int32_t N, int32_t K, int32_t with_bias);
 
-/* grad_x [M,K] = grad_y W (NULL to skip; bf16 MFMA when math = 1),
- * grad_w [N,K] = grad_y^T x and grad_b [N] = sum_m grad_y (NULL to skip) in
- * fp32 MFMA, deterministic. grad_y, x float32. Replaces the autograd backward
- * of the Linear layers above. */
+/* grad_x [M,K] = grad_y W (NULL to skip; a hipBLASLt GEMM), grad_w [N,K] =
+ * grad_y^T x (split-M MFMA partials summed in order) and grad_b [N] =
+ * sum_m grad_y (NULL to skip), fp32 accumulation, grad_w and grad_b
+ * deterministic; with math = 1 every product reads bf16-rounded operands (the
+ * autocast backward). N <= 16 runs two VALU streaming kernels instead. grad_y,
+ * x float32. Replaces the autograd backward of the Linear layers above. */
 int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math, const float* grad_y, const float* x,
                     const float* w, float* grad_x, float* grad_w, float* grad_b, void* workspace,
                     int64_t workspace_bytes);
