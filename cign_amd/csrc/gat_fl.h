@@ -66,9 +66,15 @@ constexpr int kFlHeads = 8;
 #ifndef CIGN_FL_COLS_U
 #define CIGN_FL_COLS_U 8
 #endif
+// Wide columns gather only grad_pre chunks (W floats each) per slot; this is
+// the number of gathered floats a lane holds per batch.
+#ifndef CIGN_FL_COLS_PAIR_FLOATS
+#define CIGN_FL_COLS_PAIR_FLOATS 16
+#endif
 constexpr int kFwdU = CIGN_FL_FWD_U;
 constexpr int kRowsU = CIGN_FL_ROWS_U;
 constexpr int kColsU = CIGN_FL_COLS_U;
+constexpr int kColsPairFloats = CIGN_FL_COLS_PAIR_FLOATS;
 
 // Batch cap for V chunks per lane: the largest power of two <= umax / V.
 constexpr int batch_cap(int umax, int v) {
@@ -230,7 +236,7 @@ struct FwdState {
   __device__ __forceinline__ void merge(int v, float m2, float s2, float bl2, const float (&acc2)[W],
                                         const float (&accl2)[W]) {
     const float mx = fmaxf(m[v], m2);
-    const float f1 = expf(m[v] - mx), f2 = expf(m2 - mx);
+    const float f1 = softmax_exp(m[v] - mx), f2 = softmax_exp(m2 - mx);
     s[v] = s[v] * f1 + s2 * f2;
     bl[v] = bl[v] * f1 + bl2 * f2;
 #pragma unroll
@@ -291,7 +297,7 @@ struct FwdBatches {
         sc[k][v] += ar[v];
         if (u < cnt) mx = fmaxf(mx, leaky(sc[k][v], a.slope));
       }
-      st.scale(v, expf(st.m[v] - mx));
+      st.scale(v, softmax_exp(st.m[v] - mx));
       st.m[v] = mx;
     }
 #pragma unroll
@@ -299,12 +305,12 @@ struct FwdBatches {
       const int u = first + (k0 + k) * step;
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        const float pk = u < cnt ? expf(leaky(sc[k][v], a.slope) - st.m[v]) : 0.0f;
+        const float pk = u < cnt ? softmax_exp(leaky(sc[k][v], a.slope) - st.m[v]) : 0.0f;
         const float lp = sc[k][v] < 0.0f ? a.slope : 1.0f;
         st.s[v] += pk;
         st.bl[v] = fmaf(pk, lp, st.bl[v]);
         float wk = pk;
-        if constexpr (DROP) wk = kb.get(k, ln.hq[v], ln.g) ? pk / (1.0f - a.p) : 0.0f;
+        if constexpr (DROP) wk = kb.get(k, ln.hq[v], ln.g) ? pk * (1.0f / (1.0f - a.p)) : 0.0f;
         const float wl = wk * lp;
         float xv[W];
         Chunk<T, W>::unpack(xb[k][v], xv);
@@ -390,10 +396,11 @@ __device__ __forceinline__ void fwd_emit(const GatFwdArgs<T>& a, const FlLane<L,
   if (!write) return;
   if (ln.qv[0] && ln.hq[0] == 0) {
     const int64_t base = static_cast<int64_t>(row) * a.C + ln.cw * W;
+    const float inv_h = 1.0f / static_cast<float>(a.H);
     float pr[W], o[W];
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      pr[w] = y[w] / static_cast<float>(a.H) + a.bias[ln.cw * W + w];
+      pr[w] = y[w] * inv_h + a.bias[ln.cw * W + w];
       o[w] = silu(pr[w]);
     }
     store_f32<W>(a.pre + base, pr);
@@ -639,9 +646,9 @@ struct RowBatches {
       for (int v = 0; v < V; ++v) {
         const float raw = rh.ar[v] + ab[k][v];
         const float lp = raw < 0.0f ? a.slope : 1.0f;
-        const float sm = u < cnt ? expf(leaky(raw, a.slope) - rh.em[v]) * rh.ies[v] : 0.0f;
+        const float sm = u < cnt ? softmax_exp(leaky(raw, a.slope) - rh.em[v]) * rh.ies[v] : 0.0f;
         float sk = sm;
-        if constexpr (DROP) sk = kb.get(k, ln.hq[v], ln.g) ? sm / (1.0f - a.p) : 0.0f;
+        if constexpr (DROP) sk = kb.get(k, ln.hq[v], ln.g) ? sm * (1.0f / (1.0f - a.p)) : 0.0f;
         const float skl = sk * lp;
         st.B[v] = fmaf(sm, lp, st.B[v]);
         float xv[W];
@@ -864,10 +871,14 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_agg_kernel(GatBwdArgs<T> 
 // ===========================================================================
 // Backward, columns (CSC)
 // ===========================================================================
+// ug = sum s kw g_pre and ua = sum s kw l' g_pre per owned chunk; t = sum s l'
+// wsum per owned chunk's head. Wide columns (pair weights) accumulate t per
+// pair lane in tp first and distribute it with cols_pair_t.
 template <int W, int V>
 struct ColAcc {
   float ug[V][W], ua[V][W];
   float t[V];
+  float tp;
   __device__ __forceinline__ void clear() {
 #pragma unroll
     for (int v = 0; v < V; ++v) {
@@ -875,8 +886,19 @@ struct ColAcc {
       for (int w = 0; w < W; ++w) ug[v][w] = ua[v][w] = 0.0f;
       t[v] = 0.0f;
     }
+    tp = 0.0f;
   }
 };
+
+// Columns whose lanes own several chunks (V > 1, a wavefront per column)
+// compute each (entry, head) weight once per wavefront: with every lane
+// evaluating the softmax weight of each of its heads, the exponentials, the
+// row-record loads and the dropout division were repeated cq times per pair
+// and bounded the kernel.
+template <int V>
+constexpr bool cols_pairwise() {
+  return V > 1;
+}
 
 // Batches of CSC entries of column j: slot u's destination row is held by
 // lane (base + u) in ii, its CSR edge id (used only with dropout) in ee. The
@@ -919,9 +941,9 @@ struct ColBatches {
       for (int v = 0; v < V; ++v) {
         const float raw = rs[k][v].x + ac[v];
         const float lp = raw < 0.0f ? a.slope : 1.0f;
-        const float sm = u < cnt ? expf(leaky(raw, a.slope) - rs[k][v].y) * rs[k][v].z : 0.0f;
+        const float sm = u < cnt ? softmax_exp(leaky(raw, a.slope) - rs[k][v].y) * rs[k][v].z : 0.0f;
         float w = sm;
-        if constexpr (DROP) w = kb.get(k, ln.hq[v], ln.g) ? sm / (1.0f - a.p) : 0.0f;
+        if constexpr (DROP) w = kb.get(k, ln.hq[v], ln.g) ? sm * (1.0f / (1.0f - a.p)) : 0.0f;
         const float wl = w * lp;
         st.t[v] = fmaf(sm * lp, rs[k][v].w, st.t[v]);
 #pragma unroll
@@ -934,22 +956,115 @@ struct ColBatches {
   }
 };
 
+// Pairwise batches: pair (slot k, head h) belongs to lane (k % SPR) * S + h of
+// the group in round k / SPR (the PairBits layout). The pair lane loads the
+// destination row's record and the mask byte, forms w = s kw and wl = w l'
+// and adds s l' wsum to its tp; every lane then reads the w, wl of its
+// chunks' heads by shuffle. acp is attn_col of the column for the lane's pair
+// head gl % S.
+template <typename T, int L, int V, bool DROP>
+struct ColPairBatches {
+  static constexpr int W = FlGeom<T>::W;
+  static constexpr int S = L < 8 ? L : 8;
+  static constexpr int SPR = L / S;
+  const GatBwdArgs<T>& a;
+  const FlLane<L, V>& ln;
+  int ii, ee, base, first, step, cnt;
+  float acp;
+  ColAcc<W, V>& st;
+
+  template <int U>
+  __device__ __forceinline__ void run(int k0) {
+    constexpr int R = (U + SPR - 1) / SPR;
+    float gb[U][W];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int u = first + (k0 + k) * step;
+      const int i = shfl(ii, (base + (u < cnt ? u : 0)) & (kWave - 1));
+      load_f32<W>(a.grad_pre + static_cast<int64_t>(i) * a.C + ln.cw * W, gb[k]);
+    }
+    const int h = ln.gl % S;
+    float pw[R], pwl[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int k = r * SPR + ln.gl / S;
+      const int u = first + (k0 + k) * step;
+      const bool own = h < a.H && k < U && u < cnt;
+      const int src = (base + (own ? u : 0)) & (kWave - 1);
+      const int i = shfl(ii, src);
+      float4 rs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (own) rs = a.rowstat[static_cast<int64_t>(i) * a.H + h];
+      bool keep = true;
+      if constexpr (DROP) {
+        const int e = shfl(ee, src);
+        keep = own && a.mask[static_cast<int64_t>(e) * a.H + h] != 0;
+      }
+      const float raw = rs.x + acp;
+      const float lp = raw < 0.0f ? a.slope : 1.0f;
+      const float sm = own ? softmax_exp(leaky(raw, a.slope) - rs.y) * rs.z : 0.0f;
+      float w = sm;
+      if constexpr (DROP) w = keep ? sm * (1.0f / (1.0f - a.p)) : 0.0f;
+      st.tp = fmaf(sm * lp, rs.w, st.tp);
+      pw[r] = w;
+      pwl[r] = w * lp;
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int src = ln.g * L + (k % SPR) * S + ln.hq[v];
+        const float w = shfl(pw[k / SPR], src);
+        const float wl = shfl(pwl[k / SPR], src);
+#pragma unroll
+        for (int q = 0; q < W; ++q) {
+          st.ug[v][q] = fmaf(w, gb[k][q], st.ug[v][q]);
+          st.ua[v][q] = fmaf(wl, gb[k][q], st.ua[v][q]);
+        }
+      }
+    }
+  }
+};
+
+// ac: attn_col of the column for the lane's chunks' heads (per-lane weights)
+// or, pairwise, ac[0] for the lane's pair head.
 template <typename T, int L, int V, bool DROP>
 __device__ __forceinline__ void cols_edges(const GatBwdArgs<T>& a, const FlLane<L, V>& ln, int ii, int ee, int base,
                                            int first, int step, int cnt, int need, const float (&ac)[V],
                                            ColAcc<FlGeom<T>::W, V>& st) {
-  ColBatches<T, L, V, DROP> cb{a, ln, ii, ee, base, first, step, cnt, ac, st};
-  for_batches<batch_cap(kColsU, V)>(need, cb);
+  if constexpr (cols_pairwise<V>()) {
+    ColPairBatches<T, L, V, DROP> cb{a, ln, ii, ee, base, first, step, cnt, ac[0], st};
+    for_batches<batch_cap(kColsPairFloats / FlGeom<T>::W, 1)>(need, cb);
+  } else {
+    ColBatches<T, L, V, DROP> cb{a, ln, ii, ee, base, first, step, cnt, ac, st};
+    for_batches<batch_cap(kColsU, V)>(need, cb);
+  }
 }
 
+// Pairwise t: the pair lanes' tp summed over the lanes sharing a pair head,
+// within the group (whole_wave false) or the wavefront, then read by each
+// owned chunk's head.
 template <int L, int W, int V>
-__device__ __forceinline__ void cols_group_sum(ColAcc<W, V>& st) {
+__device__ __forceinline__ void cols_pair_t(ColAcc<W, V>& st, const FlLane<L, V>& ln, bool whole_wave) {
+  constexpr int S = L < 8 ? L : 8;
+  float x = st.tp;
+  const int top = whole_wave ? kWave : L;
+  for (int o = S; o < top; o <<= 1) x += shfl_xor(x, o);
+  const int b = whole_wave ? 0 : ln.g * L;
+#pragma unroll
+  for (int v = 0; v < V; ++v) st.t[v] = shfl(x, b + ln.hq[v]);
+}
+
+// Sums of the wavefront's groups (mid and heavy columns split a column's
+// entries over the groups).
+template <int L, int W, int V>
+__device__ __forceinline__ void cols_group_sum(ColAcc<W, V>& st, const FlLane<L, V>& ln) {
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     group_sum<L, W>(st.ug[v]);
     group_sum<L, W>(st.ua[v]);
-    st.t[v] = group_sum1<L>(st.t[v]);
+    if constexpr (!cols_pairwise<V>()) st.t[v] = group_sum1<L>(st.t[v]);
   }
+  if constexpr (cols_pairwise<V>()) cols_pair_t<L, W, V>(st, ln, true);
 }
 
 // The column's own x chunks, needed after its entries: loaded before the
@@ -992,10 +1107,17 @@ __device__ __forceinline__ void cols_gac(const GatBwdArgs<T>& a, const FlLane<L,
   }
 }
 
+// attn_col[j] as cols_edges takes it.
 template <typename T, int L, int V>
 __device__ __forceinline__ void load_attn_col(const GatBwdArgs<T>& a, const FlLane<L, V>& ln, int j, float (&ac)[V]) {
+  if constexpr (cols_pairwise<V>()) {
+    constexpr int S = L < 8 ? L : 8;
+    const int h = ln.gl % S;
+    ac[0] = a.attn_col[static_cast<int64_t>(j) * a.H + (h < a.H ? h : a.H - 1)];
+  } else {
 #pragma unroll
-  for (int v = 0; v < V; ++v) ac[v] = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq[v]];
+    for (int v = 0; v < V; ++v) ac[v] = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq[v]];
+  }
 }
 
 template <typename T, int L, int V, bool DROP>
@@ -1047,9 +1169,10 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
     xc.prefetch(a, ln, j);
     if (tiny) {
       cols_edges<T, L, V, DROP>(a, ln, ii, ee, ln.g * L, 0, 1, deg, wave_group_max<L>(deg), ac, st);
+      if constexpr (cols_pairwise<V>()) cols_pair_t<L, W, V>(st, ln, false);
     } else {
       cols_edges<T, L, V, DROP>(a, ln, ii, ee, 0, ln.g, G, deg, (deg + G - 1) / G, ac, st);
-      cols_group_sum<L, W, V>(st);
+      cols_group_sum<L, W, V>(st, ln);
     }
     cols_gac(a, ln, st, xc, j, cq, gac);
     if (!(has && (tiny || ln.g == 0))) return;
@@ -1080,7 +1203,7 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
     const int ee = (DROP && own) ? a.perm[tb + ln.lane] : 0;
     cols_edges<T, L, V, DROP>(a, ln, ii, ee, 0, ln.g, G, cnt, (cnt + G - 1) / G, ac, st);
   }
-  cols_group_sum<L, W, V>(st);
+  cols_group_sum<L, W, V>(st, ln);
   cols_gac(a, ln, st, xc, j, cq, gac);
   if (ln.g == 0 && ln.cw == 0)
 #pragma unroll

@@ -60,7 +60,7 @@ constexpr int ilog2c(int v) { return v <= 1 ? 0 : 1 + ilog2c(v / 2); }
 // Softmax statistics merge: (m1, s1) <- (m1, s1) (+) (m2, s2).
 __device__ __forceinline__ void ms_merge(float& m1, float& s1, float m2, float s2) {
   const float M = fmaxf(m1, m2);
-  s1 = s1 * expf(m1 - M) + s2 * expf(m2 - M);
+  s1 = s1 * softmax_exp(m1 - M) + s2 * softmax_exp(m2 - M);
   m1 = M;
 }
 
@@ -239,7 +239,7 @@ struct FwdWave {
     for (int k = 0; k < N; ++k) m = v[k] ? fmaxf(m, sc[k]) : m;
     s = 0.0f;
 #pragma unroll
-    for (int k = 0; k < N; ++k) s += v[k] ? expf(sc[k] - m) : 0.0f;
+    for (int k = 0; k < N; ++k) s += v[k] ? softmax_exp(sc[k] - m) : 0.0f;
   }
 
   // Weight of one (edge, head): normalised softmax, or exp(sc - M) for a
@@ -254,9 +254,9 @@ struct FwdWave {
       if (write_mask) a.mask[idx] = keep ? 1 : 0;
     }
     if (!keep || (normalise && !(S > 0.0f))) return 0.0f;
-    float w = expf(sc[k] - M);
+    float w = softmax_exp(sc[k] - M);
     if (normalise) w = w / S;
-    if (a.p > 0.0f) w = w / (1.0f - a.p);
+    if (a.p > 0.0f) w = w * (1.0f / (1.0f - a.p));
     return w;
   }
 
@@ -439,7 +439,7 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_kernel(GatFwdArgs<T> a, Sched 
       float acch = 0.0f;
       for (int q = 0; q < hr.y; ++q) {
         const float* pq = a.partial + static_cast<int64_t>(hr.x + q) * stride;
-        acch += pq[hh * a.C + c] * expf(pq[HC + hh] - fin_m[hh]);
+        acch += pq[hh * a.C + c] * softmax_exp(pq[HC + hh] - fin_m[hh]);
       }
       if (fin_s[hh] > 0.0f) total += acch / fin_s[hh];
     }
@@ -547,8 +547,8 @@ __device__ __forceinline__ void bwd_row_wave(const GatBwdArgs<T>& a, const Lanes
 #pragma unroll
   for (int k = 0; k < N; ++k) {
     float ge = dot[k] * a.inv_h;
-    if (a.p > 0.0f) ge = (keep[k] ? ge : 0.0f) / (1.0f - a.p);
-    const float soft = S > 0.0f ? expf(leaky(raw[k], a.slope) - M) / S : 0.0f;
+    if (a.p > 0.0f) ge = (keep[k] ? ge : 0.0f) * (1.0f / (1.0f - a.p));
+    const float soft = S > 0.0f ? softmax_exp(leaky(raw[k], a.slope) - M) / S : 0.0f;
     const float lp = raw[k] < 0.0f ? a.slope : 1.0f;
     if (v[k]) {
       a.gscore[static_cast<int64_t>(t[k]) * a.H + L.h] = ge;
@@ -693,11 +693,11 @@ __device__ __forceinline__ float bwd_col_wave(const GatBwdArgs<T>& a, const Lane
     const float ws = a.wsum[ih];
     const float ge = a.gscore[eh];
     const bool keep = a.p > 0.0f ? a.mask[eh] != 0 : true;
-    const float soft = S > 0.0f ? expf(leaky(raw, a.slope) - M) / S : 0.0f;
+    const float soft = S > 0.0f ? softmax_exp(leaky(raw, a.slope) - M) / S : 0.0f;
     float ww = 0.0f;
     if (v[k] && keep) {
       ww = soft;
-      if (a.p > 0.0f) ww = ww / (1.0f - a.p);
+      if (a.p > 0.0f) ww = ww * (1.0f / (1.0f - a.p));
     }
     w[k] = ww;
     float g = soft * (ge - ws);
