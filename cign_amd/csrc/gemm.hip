@@ -56,10 +56,7 @@ enum Math : int { kMathF32 = 0, kMathBF16 = 1 };
 
 constexpr int kThreads = 256;
 constexpr int kBM = 128;
-#ifndef CIGN_GEMM_BK
-#define CIGN_GEMM_BK 32
-#endif
-constexpr int kBK = CIGN_GEMM_BK;  // K per LDS stage (a multiple of 32)
+constexpr int kBK = 32;  // K per step: one bf16 MFMA K (32), two fp32 halves of 16
 constexpr int kRowsPerWave = 32;
 
 struct GemmArgs {
@@ -142,6 +139,29 @@ __device__ __forceinline__ void gload(const TS* p, bool valid, int k, int K, boo
   }
 }
 
+// CNT values at element k of row p with one unconditional 16-byte load: the
+// caller has checked (wave-uniformly) that the whole K step is in bounds and
+// rows are aligned. Keeping these loads free of per-chunk branches lets a K
+// step issue all of its loads back to back; a guarded load in its own basic
+// block is followed by a wait for the previous one.
+template <typename TS, int CNT>
+__device__ __forceinline__ void gload_fast(const TS* p, int k, float (&v)[CNT]) {
+  if constexpr (std::is_same_v<TS, float>) {
+    static_assert(CNT == 4, "fp32 chunks are 4 values");
+    const float4 u = *reinterpret_cast<const float4*>(p + k);
+    v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+  } else {
+    static_assert(CNT == 8, "bf16 chunks are 8 values");
+    const uint4 u = *reinterpret_cast<const uint4*>(p + k);
+    const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w4[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w4[i] & 0xffff0000u);
+    }
+  }
+}
+
 // One vector LDS store of N values converted to the operand type (16 bytes
 // for fp32 x 4 and bf16 x 8, 8 bytes for bf16 x 4).
 template <typename T, int N>
@@ -165,11 +185,34 @@ __device__ __forceinline__ void st_lds(T* d, const float (&v)[N]) {
 // global memory into registers (a wavefront owns its rows, so x needs no LDS
 // staging): lane l holds row l%16 and, for bf16 math, k = 8*(l/16) .. +7;
 // for fp32 math, k = 4*(l/16) .. +3 and 16 + 4*(l/16) .. +3.
+// `fast`: the K step lies inside K and rows are aligned (wave-uniform); rows
+// past M then read row M-1, whose products land in output rows that are
+// never stored.
 template <typename TX, int MATH>
-__device__ __forceinline__ void load_x(const GemmArgs& g, const TX* x, int64_t m, int k0, int ks, float (&v)[8]) {
+__device__ __forceinline__ void load_x(const GemmArgs& g, const TX* x, int64_t m, int k0, int ks, bool fast,
+                                       float (&v)[8]) {
   const bool valid = m < g.M;
-  const TX* p = x + (valid ? m : 0) * g.K;
   float lo[CNT_OF<TX>], hi[CNT_OF<TX>];
+  if (fast) {
+    const TX* p = x + (valid ? m : g.M - 1) * g.K;
+    if constexpr (!std::is_same_v<TX, float>) {
+      gload_fast<TX, 8>(p, k0 + 8 * ks, lo);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = lo[q];
+    } else {
+      const int ka = MATH == kMathBF16 ? k0 + 8 * ks : k0 + 4 * ks;
+      const int kb = MATH == kMathBF16 ? ka + 4 : ka + 16;
+      gload_fast<float, 4>(p, ka, lo);
+      gload_fast<float, 4>(p, kb, hi);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v[q] = lo[q];
+        v[4 + q] = hi[q];
+      }
+    }
+    return;
+  }
+  const TX* p = x + (valid ? m : 0) * g.K;
   if constexpr (!std::is_same_v<TX, float>) {
     gload<TX, 8>(p, valid, k0 + 8 * ks, g.K, g.vec, lo);
 #pragma unroll
@@ -187,6 +230,9 @@ __device__ __forceinline__ void load_x(const GemmArgs& g, const TX* x, int64_t m
   }
 }
 
+// The K step starting at k0 can take the unconditional loads.
+__device__ __forceinline__ bool fast_step(const GemmArgs& g, int k0) { return g.vec && k0 + kBK <= g.K; }
+
 // One K step's x fragments of a wavefront: its two 16-row tiles.
 struct XStep {
   float v[2][8];
@@ -194,8 +240,9 @@ struct XStep {
 
 template <typename TX, int MATH>
 __device__ __forceinline__ void load_xstep(const GemmArgs& g, const TX* x, int64_t row0, int k0, int lane, XStep& a) {
+  const bool fast = fast_step(g, k0);
 #pragma unroll
-  for (int r = 0; r < 2; ++r) load_x<TX, MATH>(g, x, row0 + 16 * r + (lane & 15), k0, lane >> 4, a.v[r]);
+  for (int r = 0; r < 2; ++r) load_x<TX, MATH>(g, x, row0 + 16 * r + (lane & 15), k0, lane >> 4, fast, a.v[r]);
 }
 
 // W tile of one K step (BN rows x 32) held in registers between the global
@@ -207,6 +254,17 @@ struct WStage {
 
   __device__ __forceinline__ void load(const GemmArgs& g, int n0, int k0) {
     constexpr int CPR = kBK / 4;
+    if (fast_step(g, k0)) {
+      // Rows past N read row N-1; their output columns are never stored.
+#pragma unroll
+      for (int i = 0; i < CHUNKS; ++i) {
+        const int id = threadIdx.x + i * kThreads;
+        const int r = id / CPR, c = id % CPR;
+        const int n = n0 + r;
+        gload_fast<float, 4>(g.w + static_cast<int64_t>(n < g.N ? n : g.N - 1) * g.K, k0 + c * 4, b[i]);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < CHUNKS; ++i) {
       const int id = threadIdx.x + i * kThreads;
@@ -460,6 +518,25 @@ struct LdsStage {
 
   __device__ __forceinline__ void load(const GemmArgs& g, const TX* x, int64_t m0, int n0, int k0) {
     constexpr int ACPR = kBK / XC;  // chunks per A row
+    if (fast_step(g, k0)) {
+      // Rows past M (N) read row M-1 (N-1); their outputs are never stored.
+#pragma unroll
+      for (int i = 0; i < A_CHUNKS; ++i) {
+        const int id = threadIdx.x + i * kThreads;
+        const int r = id / ACPR, c = id % ACPR;
+        const int64_t m = m0 + r;
+        gload_fast<TX, XC>(x + (m < g.M ? m : g.M - 1) * g.K, k0 + c * XC, a[i]);
+      }
+      constexpr int BCPR = kBK / 4;
+#pragma unroll
+      for (int i = 0; i < B_CHUNKS; ++i) {
+        const int id = threadIdx.x + i * kThreads;
+        const int r = id / BCPR, c = id % BCPR;
+        const int n = n0 + r;
+        gload_fast<float, 4>(g.w + static_cast<int64_t>(n < g.N ? n : g.N - 1) * g.K, k0 + c * 4, b[i]);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < A_CHUNKS; ++i) {
       const int id = threadIdx.x + i * kThreads;
@@ -506,15 +583,18 @@ __device__ __forceinline__ void mma_step_lds(const typename Op<MATH>::T* As, con
   constexpr int S = lds_stride<MATH>();
   const int rl = lane & 15, ks = lane >> 4;
   if constexpr (MATH == kMathBF16) {
-    bf16x8 a[2];
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
-      a[r] = *reinterpret_cast<const bf16x8*>(As + (wave * kRowsPerWave + 16 * r + rl) * S + ks * 8);
+    for (int hk = 0; hk < kBK; hk += 32) {
+      bf16x8 a[2];
 #pragma unroll
-    for (int f = 0; f < TN; ++f) {
-      const bf16x8 b = *reinterpret_cast<const bf16x8*>(Bs + (16 * f + rl) * S + ks * 8);
+      for (int r = 0; r < 2; ++r)
+        a[r] = *reinterpret_cast<const bf16x8*>(As + (wave * kRowsPerWave + 16 * r + rl) * S + hk + ks * 8);
 #pragma unroll
-      for (int r = 0; r < 2; ++r) acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, a[r], acc[r][f], 0, 0, 0);
+      for (int f = 0; f < TN; ++f) {
+        const bf16x8 b = *reinterpret_cast<const bf16x8*>(Bs + (16 * f + rl) * S + hk + ks * 8);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, a[r], acc[r][f], 0, 0, 0);
+      }
     }
   } else {
     // Two 16-k halves; within a half, lane group ks supplies k = 4*ks .. +3
@@ -657,6 +737,17 @@ struct WgStage {
     const int r = threadIdx.x / 8;
     const int64_t m = m0 + r;
     const bool ok = m < m1;
+    if (vec && m0 + 32 <= m1 && c0 + 128 <= cmax) {
+      // Whole step in bounds (wave-uniform): unconditional loads, issued
+      // back to back.
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = ((threadIdx.x % 8) + 8 * i) * 4;
+        const float4 t = *reinterpret_cast<const float4*>(src + m * ld + c0 + c);
+        v[i][0] = t.x; v[i][1] = t.y; v[i][2] = t.z; v[i][3] = t.w;
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = ((threadIdx.x % 8) + 8 * i) * 4;
@@ -855,8 +946,6 @@ __global__ __launch_bounds__(kThreads) void small_n_grad_w_kernel(const float* g
 // ---------------------------------------------------------------------------
 inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
-// Column tile: 64 for N <= 64, else 128. For the logits epilogue the tile
-// must hold whole heads of 16..128 columns.
 // Column tile: fp32 math 64 (two waves per SIMD with the register-resident x
 // fragments); bf16 math 64 up to N = 256 (more workgroups for the skinny
 // shapes), else 128. For the logits epilogue the tile must hold whole heads
