@@ -27,17 +27,30 @@ from ._lib import load_library
 LIGHT_MAX = 64
 SEG_EDGES = 512       # smallest segment (small graphs)
 SEG_EDGES_MAX = 16384
+# Gathers of narrow rows (at most 256 bytes: D = 64 fp32, the c2/c3 GAT's
+# 4 x 16) carry little per edge, so their segments start at 1024 edges. At c2
+# (24.5K nodes, 211K edges) that took the SpMM hop from 9.9 to 9.2 us and the
+# GAT forward from 15.0 to 14.3 us, while the GAT backward (more work per
+# edge: 23.7 -> 25.4 us), the D = 512 hop and the 6 x 256 GAT forward of the
+# production block (55 -> 63 us, 240 -> 261 us) were faster at 512.
+SEG_EDGES_NARROW = 1024
+SEG_NARROW_ROW_BYTES = 256
 
 
-def segment_edges_for(nnz: int) -> int:
+def seg_floor_for(row_bytes: int) -> int:
+    """Smallest segment for gathers of rows of row_bytes bytes."""
+    return SEG_EDGES_NARROW if row_bytes <= SEG_NARROW_ROW_BYTES else SEG_EDGES
+
+
+def segment_edges_for(nnz: int, floor: int = SEG_EDGES) -> int:
     """Segment length for a graph of nnz edges: the power of two nearest
-    above nnz / 4096, clamped to [512, 16384]. One segment is then at most
+    above nnz / 4096, clamped to [floor, 16384]. One segment is then at most
     ~1/16 of the edges a CU handles, so the longest workgroup stays short
     against the whole launch, while rows that need a cross-workgroup merge
     become rare (at 62M edges a 512-edge segment leaves 9,250 merging rows
     and takes 2.2x longer per hop than 16,384)."""
     want = max(1, int(nnz) // 4096)
-    seg = SEG_EDGES
+    seg = floor
     while seg < want and seg < SEG_EDGES_MAX:
         seg *= 2
     return seg
@@ -65,9 +78,9 @@ class RowSchedule:
 
 
 def build_row_schedule(rowptr: torch.Tensor, device=None, light_max: int = LIGHT_MAX,
-                       seg_edges: int | None = None) -> RowSchedule:
+                       seg_edges: int | None = None, seg_floor: int = SEG_EDGES) -> RowSchedule:
     """Builds the schedule of a row pointer (any integer dtype, any device).
-    seg_edges None picks segment_edges_for(nnz). One host copy of the row
+    seg_edges None picks segment_edges_for(nnz, seg_floor). One host copy of the row
     pointer is taken (a synchronisation when it lives on the GPU); this
     happens once per graph, outside timed regions."""
     lib = load_library(require_gpu=False)
@@ -76,7 +89,7 @@ def build_row_schedule(rowptr: torch.Tensor, device=None, light_max: int = LIGHT
     if n_rows < 0:
         raise ValueError("row pointer must have at least one entry")
     if seg_edges is None:
-        seg_edges = segment_edges_for(int(rp[-1]) if rp.size else 0)
+        seg_edges = segment_edges_for(int(rp[-1]) if rp.size else 0, seg_floor)
     nl, ns, nh = C.c_int32(), C.c_int32(), C.c_int32()
     tot = C.c_int64()
     lib.call("cign_row_schedule_size", rp.ctypes.data, n_rows, light_max, seg_edges,
@@ -96,16 +109,17 @@ def build_row_schedule(rowptr: torch.Tensor, device=None, light_max: int = LIGHT
 _CACHE: dict[tuple, tuple[weakref.ref, int, RowSchedule]] = {}
 
 
-def cached_row_schedule(rowptr: torch.Tensor, light_max: int = LIGHT_MAX, seg_edges: int | None = None) -> RowSchedule:
+def cached_row_schedule(rowptr: torch.Tensor, light_max: int = LIGHT_MAX, seg_edges: int | None = None,
+                        seg_floor: int = SEG_EDGES) -> RowSchedule:
     """Schedule for a row-pointer tensor, built on first use and reused while
     the tensor is alive and unmodified (checked through its version counter)."""
-    key = (id(rowptr), int(light_max), None if seg_edges is None else int(seg_edges))
+    key = (id(rowptr), int(light_max), None if seg_edges is None else int(seg_edges), int(seg_floor))
     hit = _CACHE.get(key)
     if hit is not None:
         ref, version, sched = hit
         if ref() is rowptr and version == rowptr._version and sched.n_rows == rowptr.numel() - 1:
             return sched
-    sched = build_row_schedule(rowptr, light_max=light_max, seg_edges=seg_edges)
+    sched = build_row_schedule(rowptr, light_max=light_max, seg_edges=seg_edges, seg_floor=seg_floor)
     _CACHE[key] = (weakref.ref(rowptr, lambda _r, k=key: _CACHE.pop(k, None)), rowptr._version, sched)
     return sched
 
@@ -115,9 +129,13 @@ def gat_schedule(rowptr: torch.Tensor, pass_: int, dtype_code: int, heads: int, 
     1 = backward), with the geometry the library asks for that shape. When
     the library accepts any multiple of 256 as the segment length (its
     feature-layout kernels, seg_edges reported as 0 = "any"), the length
-    follows the graph size like the SpMM's."""
+    follows the graph size like the SpMM's, from 1024 edges for the forward
+    over narrow rows and from 512 otherwise."""
     lib = load_library(require_gpu=False)
     light, seg = C.c_int32(), C.c_int32()
     lib.call("cign_gat_schedule_params", int(pass_), int(dtype_code), int(heads), int(channels), C.byref(light),
              C.byref(seg))
-    return cached_row_schedule(rowptr, light.value, seg.value if seg.value > 0 else None)
+    if seg.value > 0:
+        return cached_row_schedule(rowptr, light.value, seg.value)
+    row_bytes = int(heads) * int(channels) * (2 if dtype_code == 1 else 4)
+    return cached_row_schedule(rowptr, light.value, None, seg_floor_for(row_bytes) if pass_ == 0 else SEG_EDGES)

@@ -271,7 +271,7 @@ def test_long_segments_multi_round(seg, dtype, p, agg_mode, monkeypatch):
     import cign_amd.schedule as S
 
     print(f"gat long segments seg={seg} dtype={dtype} p={p} agg={agg_mode}", flush=True)
-    monkeypatch.setattr(S, "segment_edges_for", lambda nnz: seg)
+    monkeypatch.setattr(S, "segment_edges_for", lambda nnz, floor=512: seg)
     S._CACHE.clear()
     rng = np.random.default_rng(seg)
     n, H, C = 7000, 4, 16
@@ -311,7 +311,7 @@ def test_wide_rows_long_segments(H, C, dtype, p, agg_mode, monkeypatch):
     import cign_amd.schedule as S
 
     print(f"gat wide long segments H={H} C={C} dtype={dtype} p={p} agg={agg_mode}", flush=True)
-    monkeypatch.setattr(S, "segment_edges_for", lambda nnz: 512)
+    monkeypatch.setattr(S, "segment_edges_for", lambda nnz, floor=512: 512)
     S._CACHE.clear()
     rng = np.random.default_rng(H * C)
     n = 2500

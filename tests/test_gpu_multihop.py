@@ -197,7 +197,7 @@ def test_plan_errors(c3):
         MultiHopCSR3GraphOperator(c3.operator, dense_cols=8, algorithm=4)
 
 
-@pytest.mark.parametrize("seg_edges", [256, 512, 2048])
+@pytest.mark.parametrize("seg_edges", [256, 512, 1024, 2048])
 @pytest.mark.parametrize("dtype,d", [(torch.float32, 64), (torch.float32, 1100), (torch.bfloat16, 256),
                                      (torch.bfloat16, 24)])
 def test_spmm_big_hubs_segment_sizes(seg_edges, dtype, d):

@@ -190,13 +190,16 @@ def test_gat_edge_index_reads_stay_in_bounds(rng):
 
 
 def test_segment_edges_for_graph_size():
-    """Segment length: 512 on small graphs (c2/c3), 16384 at c5 (62.4M edges),
-    a power of two in between that grows with nnz."""
-    from cign_amd.schedule import SEG_EDGES_MAX, segment_edges_for
+    """Segment length: 512 on small graphs (c2/c3), from 1024 for gathers of
+    rows of at most 256 bytes, 16384 at c5 (62.4M edges), a power of two in
+    between that grows with nnz."""
+    from cign_amd.schedule import SEG_EDGES_MAX, SEG_EDGES_NARROW, seg_floor_for, segment_edges_for
 
     assert segment_edges_for(0) == SEG_EDGES == 512
     assert segment_edges_for(210_592) == 512
-    assert segment_edges_for(62_400_000) == SEG_EDGES_MAX == 16384
+    assert segment_edges_for(210_592, seg_floor_for(256)) == SEG_EDGES_NARROW == 1024
+    assert seg_floor_for(257) == seg_floor_for(6144) == 512
+    assert segment_edges_for(62_400_000) == segment_edges_for(62_400_000, 1024) == SEG_EDGES_MAX == 16384
     prev = 0
     for nnz in np.logspace(3, 9, 40).astype(np.int64):
         s = segment_edges_for(int(nnz))
