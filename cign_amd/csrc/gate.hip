@@ -35,12 +35,60 @@ __device__ __forceinline__ void score_chunk(const float (&h)[W], const float (&c
   }
 }
 
-template <int LPR, int V, int W>
+// The lane's chunks (q = q0 + v*LPR) of the gate weight rows k: [weight[k,
+// :D] chunk, weight[k, D:] chunk]. With a compile-time hop count (KT > 0) they
+// are loaded once per thread into registers (chunks past the row read chunk
+// 0; they meet zero scores and are never stored); otherwise each use reads
+// global memory. Per-row weight loads, each in its own guarded block, had
+// made every row wait on K dependent loads.
+template <int LPR, int V, int W, int KT>
+struct GateW {
+  static constexpr int KR = KT > 0 ? KT : 1;
+  float a[KR][V][W], b[KR][V][W];
+  const float* wt;
+  int D, qd, q0;
+  __device__ __forceinline__ GateW(const float* w, int d, int q) : wt(w), D(d), qd(d / W), q0(q) {
+    if constexpr (KT > 0) {
+#pragma unroll
+      for (int k = 0; k < KT; ++k)
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const int qq = q0 + v * LPR;
+          const float* wk = wt + static_cast<int64_t>(k) * 2 * D + (qq < qd ? qq : 0) * W;
+          Chunk<float, W>::load(wk, a[k][v]);
+          Chunk<float, W>::load(wk + D, b[k][v]);
+        }
+    }
+  }
+  __device__ __forceinline__ void get(int k, int v, float (&x)[W], float (&y)[W]) const {
+    if constexpr (KT > 0) {
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        x[w] = a[k][v][w];
+        y[w] = b[k][v][w];
+      }
+    } else {
+      const float* wk = wt + static_cast<int64_t>(k) * 2 * D + (q0 + v * LPR) * W;
+      Chunk<float, W>::load(wk, x);
+      Chunk<float, W>::load(wk + D, y);
+    }
+  }
+};
+
+// Hop counts with a compile-time kernel (loop bound KC, weights in registers).
+template <int KT>
+constexpr int gate_kc() {
+  return KT > 0 ? KT : kMaxGateHops;
+}
+
+template <int LPR, int V, int W, int KT>
 __global__ __launch_bounds__(kBlock) void hop_gate_fwd_kernel(int64_t n, int D, int K, int mode, const float* H,
                                                               const float* C, const float* wt, const float* bias,
                                                               float* alpha) {
+  constexpr int KC = gate_kc<KT>();
   const Geo<LPR> g;
   const int qd = D / W;
+  const GateW<LPR, V, W, KT> gw(wt, D, g.q);
   const int64_t step = static_cast<int64_t>(gridDim.x) * Geo<LPR>::RPB;
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * Geo<LPR>::RPB + g.rl; r < n; r += step) {
     float s1[V][W], s2[V][W];
@@ -56,20 +104,18 @@ __global__ __launch_bounds__(kBlock) void hop_gate_fwd_kernel(int64_t n, int D, 
       }
       score_chunk<W>(h, c, mode, s1[v], s2[v]);
     }
-    float logit[kMaxGateHops];
+    float logit[KC];
     float m = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < kMaxGateHops; ++k) {
-      if (k < K) {
-        const float* wk = wt + static_cast<int64_t>(k) * 2 * D;
+    for (int k = 0; k < KC; ++k) {
+      if (KT > 0 || k < K) {
         float d = 0.0f;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           const int q = g.q + v * LPR;
-          if (q < qd) {
+          if (KT > 0 || q < qd) {
             float a[W], b[W];
-            Chunk<float, W>::load(wk + q * W, a);
-            Chunk<float, W>::load(wk + D + q * W, b);
+            gw.get(k, v, a, b);
 #pragma unroll
             for (int w = 0; w < W; ++w) d = fmaf(s1[v][w], a[w], fmaf(s2[v][w], b[w], d));
           }
@@ -80,40 +126,42 @@ __global__ __launch_bounds__(kBlock) void hop_gate_fwd_kernel(int64_t n, int D, 
     }
     float tot = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kMaxGateHops; ++k)
-      if (k < K) {
+    for (int k = 0; k < KC; ++k)
+      if (KT > 0 || k < K) {
         logit[k] = expf(logit[k] - m);
         tot += logit[k];
       }
 #pragma unroll
-    for (int k = 0; k < kMaxGateHops; ++k)
-      if (k < K && g.q == (k % LPR)) alpha[r * K + k] = logit[k] / tot;
+    for (int k = 0; k < KC; ++k)
+      if ((KT > 0 || k < K) && g.q == (k % LPR)) alpha[r * K + k] = logit[k] / tot;
   }
 }
 
 // Row part of the backward: gl (to the workspace), grad_H, grad_C.
-template <int LPR, int V, int W>
+template <int LPR, int V, int W, int KT>
 __global__ __launch_bounds__(kBlock) void hop_gate_bwd_rows_kernel(int64_t n, int D, int K, int mode, const float* H,
                                                                    const float* C, const float* wt, const float* alpha,
                                                                    const float* galpha, float* gl_out, float* gH,
                                                                    float* gC) {
+  constexpr int KC = gate_kc<KT>();
   const Geo<LPR> g;
   const int qd = D / W;
+  const GateW<LPR, V, W, KT> gw(wt, D, g.q);
   const int64_t step = static_cast<int64_t>(gridDim.x) * Geo<LPR>::RPB;
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * Geo<LPR>::RPB + g.rl; r < n; r += step) {
-    float gl[kMaxGateHops];
+    float gl[KC];
     float dot = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kMaxGateHops; ++k)
-      if (k < K) dot += alpha[r * K + k] * galpha[r * K + k];
+    for (int k = 0; k < KC; ++k)
+      if (KT > 0 || k < K) dot += alpha[r * K + k] * galpha[r * K + k];
 #pragma unroll
-    for (int k = 0; k < kMaxGateHops; ++k) {
+    for (int k = 0; k < KC; ++k) {
       gl[k] = 0.0f;
-      if (k < K) gl[k] = alpha[r * K + k] * (galpha[r * K + k] - dot);
+      if (KT > 0 || k < K) gl[k] = alpha[r * K + k] * (galpha[r * K + k] - dot);
     }
 #pragma unroll
-    for (int k = 0; k < kMaxGateHops; ++k)
-      if (k < K && g.q == (k % LPR)) gl_out[r * K + k] = gl[k];
+    for (int k = 0; k < KC; ++k)
+      if ((KT > 0 || k < K) && g.q == (k % LPR)) gl_out[r * K + k] = gl[k];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       const int q = g.q + v * LPR;
@@ -122,12 +170,10 @@ __global__ __launch_bounds__(kBlock) void hop_gate_bwd_rows_kernel(int64_t n, in
 #pragma unroll
         for (int w = 0; w < W; ++w) g1[w] = g2[w] = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kMaxGateHops; ++k) {
-          if (k < K) {
-            const float* wk = wt + static_cast<int64_t>(k) * 2 * D;
+        for (int k = 0; k < KC; ++k) {
+          if (KT > 0 || k < K) {
             float a[W], b[W];
-            Chunk<float, W>::load(wk + q * W, a);
-            Chunk<float, W>::load(wk + D + q * W, b);
+            gw.get(k, v, a, b);
 #pragma unroll
             for (int w = 0; w < W; ++w) {
               g1[w] = fmaf(gl[k], a[w], g1[w]);
@@ -163,48 +209,74 @@ __global__ __launch_bounds__(kBlock) void hop_gate_bwd_rows_kernel(int64_t n, in
 
 // Column part: row block blockIdx.x, tile blockIdx.y of kBlock chunks of the
 // 2D score columns. part_w [nb][K*2D] (column k*2D + j), part_b [nb][K].
-template <int W>
+// Rows go four at a time: their score chunks and gl values are all loaded
+// before any is used.
+template <int W, int KT>
 __global__ __launch_bounds__(kBlock) void hop_gate_bwd_cols_kernel(int64_t n, int D, int K, int mode,
                                                                    const float* H, const float* C, const float* gl,
                                                                    float* part_w, float* part_b, int nb) {
+  constexpr int KC = gate_kc<KT>();
+  constexpr int R = 4;
   const int qs = 2 * D / W;  // score chunks (D % W == 0, so no chunk straddles the halves)
   const int q = blockIdx.y * kBlock + threadIdx.x;
   int64_t r0, r1;
   block_rows(n, nb, blockIdx.x, r0, r1);
-  float acc[kMaxGateHops][W];
-#pragma unroll
-  for (int k = 0; k < kMaxGateHops; ++k)
-#pragma unroll
-    for (int w = 0; w < W; ++w) acc[k][w] = 0.0f;
-  float accb = 0.0f;
   const bool col = q < qs;
-  const bool second = col && q * W >= D;
-  const int d0 = col ? (second ? q * W - D : q * W) : 0;
-  for (int64_t r = r0; r < r1; ++r) {
-    if (col) {
-      float h[W], c[W], s1[W], s2[W];
-      Chunk<float, W>::load(H + r * D + d0, h);
-      Chunk<float, W>::load(C + r * D + d0, c);
-      score_chunk<W>(h, c, mode, s1, s2);
-#pragma unroll
-      for (int k = 0; k < kMaxGateHops; ++k)
-        if (k < K) {
-          const float glk = gl[r * K + k];
-#pragma unroll
-          for (int w = 0; w < W; ++w) acc[k][w] = fmaf(glk, second ? s2[w] : s1[w], acc[k][w]);
-        }
-    }
-    if (blockIdx.y == 0 && threadIdx.x < K) accb += gl[r * K + threadIdx.x];
-  }
   if (col) {
+    float acc[KC][W];
+#pragma unroll
+    for (int k = 0; k < KC; ++k)
+#pragma unroll
+      for (int w = 0; w < W; ++w) acc[k][w] = 0.0f;
+    const bool second = q * W >= D;
+    const int d0 = second ? q * W - D : q * W;
+    auto add_rows = [&](int64_t r, auto UC) {
+      constexpr int U = decltype(UC)::value;
+      float h[U][W], c[U][W], gk[U][KC];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        Chunk<float, W>::load(H + (r + u) * D + d0, h[u]);
+        Chunk<float, W>::load(C + (r + u) * D + d0, c[u]);
+#pragma unroll
+        for (int k = 0; k < KC; ++k) gk[u][k] = (KT > 0 || k < K) ? gl[(r + u) * K + k] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float s1[W], s2[W];
+        score_chunk<W>(h[u], c[u], mode, s1, s2);
+#pragma unroll
+        for (int k = 0; k < KC; ++k)
+#pragma unroll
+          for (int w = 0; w < W; ++w) acc[k][w] = fmaf(gk[u][k], second ? s2[w] : s1[w], acc[k][w]);
+      }
+    };
+    int64_t r = r0;
+    for (; r + R <= r1; r += R) add_rows(r, IC<R>());
+    for (; r < r1; ++r) add_rows(r, IC<1>());
     float* dst = part_w + static_cast<int64_t>(blockIdx.x) * K * 2 * D + q * W;
 #pragma unroll
-    for (int k = 0; k < kMaxGateHops; ++k)
-      if (k < K)
+    for (int k = 0; k < KC; ++k)
+      if (KT > 0 || k < K)
 #pragma unroll
         for (int w = 0; w < W; ++w) dst[static_cast<int64_t>(k) * 2 * D + w] = acc[k][w];
   }
-  if (blockIdx.y == 0 && threadIdx.x < K) part_b[static_cast<int64_t>(blockIdx.x) * K + threadIdx.x] = accb;
+  if (blockIdx.y == 0 && threadIdx.x < K) {
+    float accb = 0.0f;
+    for (int64_t r = r0; r < r1; ++r) accb += gl[r * K + threadIdx.x];
+    part_b[static_cast<int64_t>(blockIdx.x) * K + threadIdx.x] = accb;
+  }
+}
+
+// Runs f(IC<KT>()) with KT = K for the common hop counts 2..4 (kernels with
+// the weights in registers), KT = 0 (runtime K) otherwise.
+template <class F>
+void with_hops(int K, F&& f) {
+  switch (K) {
+    case 2: f(IC<2>()); break;
+    case 3: f(IC<3>()); break;
+    case 4: f(IC<4>()); break;
+    default: f(IC<0>()); break;
+  }
 }
 
 int check_gate(const char* who, int64_t n, int D, int K, int mode) {
@@ -251,11 +323,13 @@ int cign_hop_gate_fwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t sco
     constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
     const int grid = grid_for(n, Geo<L>::RPB);
     if (W == 4)
-      hipLaunchKernelGGL((hop_gate_fwd_kernel<L, V, 4>), dim3(grid), dim3(kBlock), 0, st, n, D, K, score_mode, H, C,
-                         weight, bias, alpha);
+      with_hops(K, [&](auto KC) {
+        hipLaunchKernelGGL((hop_gate_fwd_kernel<L, V, 4, decltype(KC)::value>), dim3(grid), dim3(kBlock), 0, st, n,
+                           D, K, score_mode, H, C, weight, bias, alpha);
+      });
     else
-      hipLaunchKernelGGL((hop_gate_fwd_kernel<L, V, 1>), dim3(grid), dim3(kBlock), 0, st, n, D, K, score_mode, H, C,
-                         weight, bias, alpha);
+      hipLaunchKernelGGL((hop_gate_fwd_kernel<L, V, 1, 0>), dim3(grid), dim3(kBlock), 0, st, n, D, K, score_mode, H,
+                         C, weight, bias, alpha);
     return check_launch("cign_hop_gate_fwd");
   });
   if (rc < 0) return set_error(kInvalid, "cign_hop_gate_fwd: D=%d too wide (max %d)", D, 256 * W);
@@ -280,11 +354,13 @@ int cign_hop_gate_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t sco
     constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
     const int grid = grid_for(n, Geo<L>::RPB);
     if (W == 4)
-      hipLaunchKernelGGL((hop_gate_bwd_rows_kernel<L, V, 4>), dim3(grid), dim3(kBlock), 0, st, n, D, K, score_mode, H,
-                         C, weight, alpha, grad_alpha, gl, grad_H, grad_C);
+      with_hops(K, [&](auto KC) {
+        hipLaunchKernelGGL((hop_gate_bwd_rows_kernel<L, V, 4, decltype(KC)::value>), dim3(grid), dim3(kBlock), 0, st,
+                           n, D, K, score_mode, H, C, weight, alpha, grad_alpha, gl, grad_H, grad_C);
+      });
     else
-      hipLaunchKernelGGL((hop_gate_bwd_rows_kernel<L, V, 1>), dim3(grid), dim3(kBlock), 0, st, n, D, K, score_mode, H,
-                         C, weight, alpha, grad_alpha, gl, grad_H, grad_C);
+      hipLaunchKernelGGL((hop_gate_bwd_rows_kernel<L, V, 1, 0>), dim3(grid), dim3(kBlock), 0, st, n, D, K,
+                         score_mode, H, C, weight, alpha, grad_alpha, gl, grad_H, grad_C);
     return check_launch("cign_hop_gate_bwd (rows)");
   });
   if (rc < 0) return set_error(kInvalid, "cign_hop_gate_bwd: D=%d too wide (max %d)", D, 256 * W);
@@ -292,10 +368,12 @@ int cign_hop_gate_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t sco
   const int qs = 2 * D / W;
   const dim3 cgrid(nb, (qs + kBlock - 1) / kBlock);
   if (W == 4)
-    hipLaunchKernelGGL((hop_gate_bwd_cols_kernel<4>), cgrid, dim3(kBlock), 0, st, n, D, K, score_mode, H, C, gl,
-                       part_w, part_b, nb);
+    with_hops(K, [&](auto KC) {
+      hipLaunchKernelGGL((hop_gate_bwd_cols_kernel<4, decltype(KC)::value>), cgrid, dim3(kBlock), 0, st, n, D, K,
+                         score_mode, H, C, gl, part_w, part_b, nb);
+    });
   else
-    hipLaunchKernelGGL((hop_gate_bwd_cols_kernel<1>), cgrid, dim3(kBlock), 0, st, n, D, K, score_mode, H, C, gl,
+    hipLaunchKernelGGL((hop_gate_bwd_cols_kernel<1, 0>), cgrid, dim3(kBlock), 0, st, n, D, K, score_mode, H, C, gl,
                        part_w, part_b, nb);
   if ((rc = check_launch("cign_hop_gate_bwd (cols)"))) return rc;
   if ((rc = launch_colsum(st, part_w, nb, K * 2 * D, 1, grad_weight, nullptr, "cign_hop_gate_bwd"))) return rc;

@@ -239,8 +239,8 @@ def test_block_ops_empty_rows_give_zero_parameter_grads():
 # ---------------------------------------------------------------------------
 # hop gate
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("n,D,K,mode", [(1000, 256, 3, 1), (1000, 256, 3, 0), (300, 32, 5, 1), (77, 7, 16, 1),
-                                        (50, 300, 1, 0), (10, 4, 2, 1)])
+@pytest.mark.parametrize("n,D,K,mode", [(1000, 256, 3, 1), (1000, 256, 3, 0), (1003, 256, 3, 1), (501, 64, 4, 0),
+                                        (300, 32, 5, 1), (77, 7, 16, 1), (50, 300, 1, 0), (10, 4, 2, 1)])
 def test_hop_gate_matches_oracle(n, D, K, mode):
     from cign_amd.hop_gate import HopGateFunction
 
