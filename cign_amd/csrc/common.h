@@ -161,6 +161,17 @@ __device__ __forceinline__ float sum_across(float v, int from) {
   return v;
 }
 
+// sum_across of every element of v, the butterflies interleaved step by step
+// so that their shuffles overlap instead of each waiting on the previous one.
+template <int N, int M>
+__device__ __forceinline__ void sum_across_n(float (&v)[N][M], int from) {
+  for (int o = from; o < kWave; o <<= 1)
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+      for (int j = 0; j < M; ++j) v[i][j] += shfl_xor(v[i][j], o);
+}
+
 // ---------------------------------------------------------------------------
 // Math helpers shared by the GAT, pack and block kernels.
 // ---------------------------------------------------------------------------

@@ -164,10 +164,16 @@ __device__ __forceinline__ float group_sum1(float v) {
   return v;
 }
 
-// Sum over the cq lanes of a head (lane bits below log2(cq)).
-__device__ __forceinline__ float head_sum(float v, int cq) {
-  for (int o = 1; o < cq; o <<= 1) v += shfl_xor(v, o);
-  return v;
+// Sums each of N values over the cq lanes of a head (lane bits below
+// log2(cq)). The N butterflies are interleaved step by step, so their
+// shuffles are in flight together; one value at a time made every shuffle
+// wait for the previous one (72 dependent round trips per row for the six
+// heads' two sums of a 6 x 256 row).
+template <int N>
+__device__ __forceinline__ void head_sum_n(float (&v)[N], int cq) {
+  for (int o = 1; o < cq; o <<= 1)
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += shfl_xor(v[i], o);
 }
 
 // Dropout keep bits of a batch's U x H (edge slot k, head h) pairs, each
@@ -699,6 +705,7 @@ __device__ __forceinline__ void grad_pre_chunk(const GatBwdArgs<T>& a, int row, 
 template <int W, int V>
 __device__ __forceinline__ void rows_dots(const RowAcc<W, V>& st, const float (&gp)[W], int cq, float inv_h,
                                           float (&wsum)[V], float (&A)[V]) {
+  float d[2 * V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     float d1 = 0.0f, d2 = 0.0f;
@@ -707,8 +714,14 @@ __device__ __forceinline__ void rows_dots(const RowAcc<W, V>& st, const float (&
       d1 = fmaf(gp[w], st.vs[v][w], d1);
       d2 = fmaf(gp[w], st.vsl[v][w], d2);
     }
-    wsum[v] = head_sum(d1, cq) * inv_h;
-    A[v] = head_sum(d2, cq) * inv_h;
+    d[v] = d1;
+    d[V + v] = d2;
+  }
+  head_sum_n<2 * V>(d, cq);
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    wsum[v] = d[v] * inv_h;
+    A[v] = d[V + v] * inv_h;
   }
 }
 
@@ -1096,15 +1109,18 @@ template <typename T, int L, int V>
 __device__ __forceinline__ void cols_gac(const GatBwdArgs<T>& a, const FlLane<L, V>& ln, const ColAcc<FlGeom<T>::W, V>& st,
                                          const XCol<T, V>& xc, int j, int cq, float (&gac)[V]) {
   constexpr int W = FlGeom<T>::W;
+  float d[V];
 #pragma unroll
   for (int v = 0; v < V; ++v) {
     float xj[W];
     xc.get(a, ln, j, v, xj);
-    float d = 0.0f;
+    d[v] = 0.0f;
 #pragma unroll
-    for (int w = 0; w < W; ++w) d = fmaf(st.ua[v][w], xj[w], d);
-    gac[v] = head_sum(d, cq) * a.inv_h - st.t[v];
+    for (int w = 0; w < W; ++w) d[v] = fmaf(st.ua[v][w], xj[w], d[v]);
   }
+  head_sum_n<V>(d, cq);
+#pragma unroll
+  for (int v = 0; v < V; ++v) gac[v] = d[v] * a.inv_h - st.t[v];
 }
 
 // attn_col[j] as cols_edges takes it.

@@ -589,9 +589,13 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_kernel(GatBwdArgs<T> a, S
         bwd_row_wave<T, HP, CP, decltype(NC)::value>(a, L, r.y, r.z, adst, M, S, gp[wave], wsum, A, B);
       };
       dispatch_n<1, NTL>(nt, body);
-      wsum = sum_across(wsum, HP);
-      A = sum_across(A, HP);
-      B = sum_across(B, HP);
+      {
+        float t[1][3] = {{wsum, A, B}};
+        sum_across_n(t, HP);
+        wsum = t[0][0];
+        A = t[0][1];
+        B = t[0][2];
+      }
       if (L.el == 0 && L.hv) {
         a.wsum[rh] = wsum;
         a.grad_attn_row[rh] = A - wsum * B;
@@ -620,9 +624,13 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_kernel(GatBwdArgs<T> a, S
   const int64_t rh = static_cast<int64_t>(row) * a.H + L.hc;
   float wsum, A, B;
   bwd_row_wave<T, HP, CP, NTL>(a, L, eb, ee, a.attn_row[rh], a.emax[rh], a.esum[rh], gp[0], wsum, A, B);
-  wsum = sum_across(wsum, HP);
-  A = sum_across(A, HP);
-  B = sum_across(B, HP);
+  {
+    float t[1][3] = {{wsum, A, B}};
+    sum_across_n(t, HP);
+    wsum = t[0][0];
+    A = t[0][1];
+    B = t[0][2];
+  }
   if (L.el == 0) {
     red[wave][0][L.h] = wsum;
     red[wave][1][L.h] = A;

@@ -185,10 +185,7 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a,
       const int jj = mine ? a.col[r.y + lane] : 0;
       const float vv = mine ? a.val[r.y + lane] : 0.0f;
       gather(a, jj, vv, 0, g, G, deg, (deg + G - 1) / G, gl, acc);
-#pragma unroll
-      for (int v = 0; v < VPL; ++v)
-#pragma unroll
-        for (int w = 0; w < W; ++w) acc[v][w] = sum_across(acc[v][w], a.L);
+      sum_across_n(acc, a.L);
       if (lane < a.L) write_row(a, r.x, gl, acc);
       return;
     }
@@ -219,10 +216,7 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a,
     const float vv = mine ? a.val[tb + lane] : 0.0f;
     gather(a, jj, vv, 0, g, G, cnt, (cnt + G - 1) / G, gl, acc);
   }
-#pragma unroll
-  for (int v = 0; v < VPL; ++v)
-#pragma unroll
-    for (int w = 0; w < W; ++w) acc[v][w] = sum_across(acc[v][w], a.L);
+  sum_across_n(acc, a.L);
   const int width = a.nch * W;
   if (lane < a.L) {
 #pragma unroll
