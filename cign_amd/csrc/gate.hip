@@ -267,18 +267,6 @@ __global__ __launch_bounds__(kBlock) void hop_gate_bwd_cols_kernel(int64_t n, in
   }
 }
 
-// Runs f(IC<KT>()) with KT = K for the common hop counts 2..4 (kernels with
-// the weights in registers), KT = 0 (runtime K) otherwise.
-template <class F>
-void with_hops(int K, F&& f) {
-  switch (K) {
-    case 2: f(IC<2>()); break;
-    case 3: f(IC<3>()); break;
-    case 4: f(IC<4>()); break;
-    default: f(IC<0>()); break;
-  }
-}
-
 int check_gate(const char* who, int64_t n, int D, int K, int mode) {
   if (n < 0 || D < 1) return set_error(kInvalid, "%s: bad shape n=%lld D=%d", who, static_cast<long long>(n), D);
   if (K < 1 || K > kMaxGateHops) return set_error(kInvalid, "%s: hop count %d outside [1, %d]", who, K, kMaxGateHops);

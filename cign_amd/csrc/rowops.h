@@ -111,6 +111,19 @@ int with_geo(int qc, F&& f) {
 
 inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// Runs f(IC<KT>()) with KT = K for the common hop counts 2..4 (kernels whose
+// per-hop loop is unrolled, so every hop's loads are issued before any hop's
+// arithmetic), KT = 0 (a runtime loop over K) otherwise.
+template <class F>
+void with_hops(int K, F&& f) {
+  switch (K) {
+    case 2: f(IC<2>()); break;
+    case 3: f(IC<3>()); break;
+    case 4: f(IC<4>()); break;
+    default: f(IC<0>()); break;
+  }
+}
+
 // Grid of a grid-stride loop over `items` units of `per_block` each.
 inline int grid_for(int64_t items, int per_block) {
   const int64_t g = (items + per_block - 1) / per_block;
