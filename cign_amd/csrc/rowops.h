@@ -111,9 +111,9 @@ int with_geo(int qc, F&& f) {
 
 inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
-// Runs f(IC<KT>()) with KT = K for the common hop counts 2..4 (kernels whose
-// per-hop loop is unrolled, so every hop's loads are issued before any hop's
-// arithmetic), KT = 0 (a runtime loop over K) otherwise.
+// Runs f(IC<KT>()) with KT = K for the common hop counts 2..4 (kernels
+// specialised on the hop count: per-hop state in registers, hop loops
+// unrolled), KT = 0 (a runtime loop over K) otherwise.
 template <class F>
 void with_hops(int K, F&& f) {
   switch (K) {
