@@ -509,10 +509,16 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
   const int row = sg.x;
   const int2 hr = s.hrow[sg.w];
   load_attn_row(a, ln, row, ar);
-  for (int tb = sg.y + wave * kWave; tb < sg.z; tb += kSegRound) {
+  // The next round's column indices are loaded before this round's gathers,
+  // so a round waits on one memory latency (the gathers) instead of two.
+  int tb = sg.y + wave * kWave;
+  int jj = tb + ln.lane < sg.z ? a.col[tb + ln.lane] : 0;
+  for (; tb < sg.z; tb += kSegRound) {
     const int cnt = min(kWave, sg.z - tb);
-    const int jj = ln.lane < cnt ? a.col[tb + ln.lane] : 0;
+    const int tn = tb + kSegRound + ln.lane;
+    const int jn = tn < sg.z ? a.col[tn] : 0;
     fwd_edges<T, L, V, DROP>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, ar, st);
+    jj = jn;
   }
   fwd_merge_groups<L, W, V>(st);
   fwd_merge_waves<W, V>(st, slot, wave, ln.gl, ln.g == 0);
@@ -802,10 +808,15 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a
   const int2 hr = s.hrow[sg.w];
   const RowHead<V> rh = row_head(a, row, ln);
   grad_pre_chunk(a, row, ln.cw, gp);
-  for (int tb = sg.y + wave * kWave; tb < sg.z; tb += kSegRound) {
+  // next round's indices loaded before this round's gathers, as in the forward
+  int tb = sg.y + wave * kWave;
+  int jj = tb + ln.lane < sg.z ? a.col[tb + ln.lane] : 0;
+  for (; tb < sg.z; tb += kSegRound) {
     const int cnt = min(kWave, sg.z - tb);
-    const int jj = ln.lane < cnt ? a.col[tb + ln.lane] : 0;
+    const int tn = tb + kSegRound + ln.lane;
+    const int jn = tn < sg.z ? a.col[tn] : 0;
     rows_edges<T, L, V, DROP>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, rh, st);
+    jj = jn;
   }
   rows_group_sum<L, W, V>(st);
   rows_dots<W, V>(st, gp, cq, a.inv_h, wsum, A);
@@ -1212,12 +1223,18 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
   load_attn_col(a, ln, j, ac);
   XCol<T, V> xc;
   xc.prefetch(a, ln, j);
-  for (int tb = sg.y + wave * kWave; tb < sg.z; tb += kSegRound) {
+  // next round's entries loaded before this round's gathers, as in the forward
+  int tb = sg.y + wave * kWave;
+  int ii = tb + ln.lane < sg.z ? a.rowind[tb + ln.lane] : 0;
+  int ee = DROP && tb + ln.lane < sg.z ? a.perm[tb + ln.lane] : 0;
+  for (; tb < sg.z; tb += kSegRound) {
     const int cnt = min(kWave, sg.z - tb);
-    const bool own = ln.lane < cnt;
-    const int ii = own ? a.rowind[tb + ln.lane] : 0;
-    const int ee = (DROP && own) ? a.perm[tb + ln.lane] : 0;
+    const int tn = tb + kSegRound + ln.lane;
+    const int in = tn < sg.z ? a.rowind[tn] : 0;
+    const int en = DROP && tn < sg.z ? a.perm[tn] : 0;
     cols_edges<T, L, V, DROP>(a, ln, ii, ee, 0, ln.g, G, cnt, (cnt + G - 1) / G, ac, st);
+    ii = in;
+    ee = en;
   }
   cols_group_sum<L, W, V>(st, ln);
   cols_gac(a, ln, st, xc, j, cq, gac);

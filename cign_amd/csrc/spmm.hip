@@ -209,12 +209,19 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a,
   const int4 sg = s.seg[b];
   const int row = sg.x;
   // Rounds of 4 x 64 edges when the schedule's segments are longer than 256.
-  for (int tb = sg.y + wave * kTile; tb < sg.z; tb += kSegEdges) {
+  // The next round's indices and weights are loaded before this round's
+  // gathers, so a round waits on one memory latency instead of two.
+  int tb = sg.y + wave * kTile;
+  int jj = tb + lane < sg.z ? a.col[tb + lane] : 0;
+  float vv = tb + lane < sg.z ? a.val[tb + lane] : 0.0f;
+  for (; tb < sg.z; tb += kSegEdges) {
     const int cnt = min(kTile, sg.z - tb);
-    const bool mine = lane < cnt;
-    const int jj = mine ? a.col[tb + lane] : 0;
-    const float vv = mine ? a.val[tb + lane] : 0.0f;
+    const int tn = tb + kSegEdges + lane;
+    const int jn = tn < sg.z ? a.col[tn] : 0;
+    const float vn = tn < sg.z ? a.val[tn] : 0.0f;
     gather(a, jj, vv, 0, g, G, cnt, (cnt + G - 1) / G, gl, acc);
+    jj = jn;
+    vv = vn;
   }
   sum_across_n(acc, a.L);
   const int width = a.nch * W;
