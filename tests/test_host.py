@@ -205,3 +205,21 @@ def test_segment_edges_for_graph_size():
         s = segment_edges_for(int(nnz))
         assert s >= prev and s & (s - 1) == 0 and s % 256 == 0
         prev = s
+
+
+def test_gat_schedules_pick_the_segment_floor(rng):
+    """The GAT forward over rows of at most 256 bytes gets 1024-edge segments
+    on a small graph; the backward's passes and wider rows keep 512 (header
+    word 3 is the schedule's segment length). The SpMM plan takes its floor
+    from the fp32 row width of its dense operand the same way."""
+    from cign_amd import schedule as S
+
+    deg = rng.integers(0, 30, 400)
+    deg[7] = 3000
+    rowptr = torch.from_numpy(np.concatenate([[0], np.cumsum(deg)]).astype(np.int32))
+    seg = lambda sch: int(sch.header[3])
+    assert seg(S.gat_schedule(rowptr, 0, 0, 4, 16)) == 1024  # 4 x 16 fp32: 256-byte rows
+    assert seg(S.gat_schedule(rowptr, 0, 1, 4, 32)) == 1024  # 4 x 32 bf16: 256-byte rows
+    assert seg(S.gat_schedule(rowptr, 0, 0, 6, 256)) == 512  # wide rows
+    assert seg(S.gat_schedule(rowptr, 1, 0, 4, 16)) == 512  # backward passes
+    assert S.seg_floor_for(4 * 64) == 1024 and S.seg_floor_for(4 * 512) == 512
