@@ -616,8 +616,8 @@ def main():
         return
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1 (multi-GPU sharding is "
-                                   "described in DESIGN.md and not run)"}), flush=True)
+        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1 (the path would shard by "
+                                   "destination rows with halo exchange; that is designed, not run)"}), flush=True)
         sys.exit(2)
     import torch
 
