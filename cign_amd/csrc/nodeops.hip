@@ -268,6 +268,15 @@ __global__ __launch_bounds__(kBlock) void ln_fwd_kernel(int64_t n, int D, const 
   const int qd = D / W;
   const float scale = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
   const float df = static_cast<float>(D);
+  // The lane's weight and bias chunks, loaded once (in flight with the first
+  // row's loads) instead of after each row's two reductions.
+  float wv[V][W], bv[V][W];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int c = g.q + v * LPR;
+    Chunk<float, W>::load(wt + (c < qd ? c : 0) * W, wv[v]);
+    Chunk<float, W>::load(bs + (c < qd ? c : 0) * W, bv[v]);
+  }
   const int64_t step = static_cast<int64_t>(gridDim.x) * Geo<LPR>::RPB;
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * Geo<LPR>::RPB + g.rl; r < n; r += step) {
     float qv[V][W];
@@ -311,11 +320,9 @@ __global__ __launch_bounds__(kBlock) void ln_fwd_kernel(int64_t n, int D, const 
     for (int v = 0; v < V; ++v) {
       const int c = g.q + v * LPR;
       if (c < qd) {
-        float wv[W], bv[W], o[W];
-        Chunk<float, W>::load(wt + c * W, wv);
-        Chunk<float, W>::load(bs + c * W, bv);
+        float o[W];
 #pragma unroll
-        for (int w = 0; w < W; ++w) o[w] = (qv[v][w] - mu) * rs * wv[w] + bv[w];
+        for (int w = 0; w < W; ++w) o[w] = (qv[v][w] - mu) * rs * wv[v][w] + bv[v][w];
         Chunk<float, W>::store(y + r * D + c * W, o);
       }
     }
