@@ -2,10 +2,12 @@
 CSR operator of the reference.
 
 Mirrors:
-  * build_sparse_normalized_adjacency / prepare_gat_edge_index
-    (generic_engine/train_cign.py:1558-1590, 1759-1771) and the PyG utilities
-    they call (to_undirected, add_self_loops, remove_self_loops, degree),
-    restated here with torch ops in the same order;
+  * build_sparse_normalized_adjacency / build_sparse_laplacian /
+    sparse_linear_combination / build_graph_operator / prepare_gat_edge_index
+    (generic_engine/train_cign.py:1518-1666, 1759-1771) and the PyG utilities
+    they call (to_undirected, get_laplacian, add_self_loops,
+    remove_self_loops, degree), restated here with torch ops in the same
+    order;
   * FixedCSRGraphOperator / prepare_fixed_csr_operator / fixed_sparse_mm /
     selected_sparse_powers / FixedCSRSpMMFunction (model.py:57-252);
   * GraphCliffordNet.prepare_fused_gat_graph (generic_engine/model_cign.py:
@@ -73,6 +75,91 @@ def build_sparse_normalized_adjacency(edge_index: torch.Tensor, num_nodes: int, 
     adjacency = torch.sparse_coo_tensor(indices=edge_index, values=edge_weight, size=(num_nodes, num_nodes),
                                         dtype=torch.float).coalesce()
     return edge_index, adjacency
+
+
+def get_laplacian(edge_index: torch.Tensor, num_nodes: int, normalization: str | None = "sym",
+                  edge_weight: torch.Tensor | None = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """PyG ``torch_geometric.utils.get_laplacian`` (the build_sparse_laplacian
+    call at generic_engine/train_cign.py:1541-1546), restated: self-loops
+    removed, unit weights, deg = weight sum over edge_index[0]; then
+      None:  L = D - A          (diagonal deg, off-diagonal -w)
+      "sym": L = I - D^-1/2 A D^-1/2  (deg^-1/2 of isolated nodes is 0)
+      "rw":  L = I - D^-1 A
+    with the diagonal entries appended after the off-diagonal ones."""
+    if normalization not in (None, "sym", "rw"):
+        raise ValueError(f"normalization must be None, 'sym' or 'rw', got {normalization!r}")
+    keep = edge_index[0] != edge_index[1]
+    edge_index = edge_index[:, keep]
+    if edge_weight is None:
+        edge_weight = torch.ones(edge_index.size(1), dtype=torch.float, device=edge_index.device)
+    else:
+        edge_weight = edge_weight[keep]
+    row, col = edge_index[0], edge_index[1]
+    deg = torch.zeros(num_nodes, dtype=edge_weight.dtype, device=edge_weight.device)
+    deg.scatter_add_(0, row.long(), edge_weight)
+    loop = torch.arange(num_nodes, dtype=edge_index.dtype, device=edge_index.device)
+    loops = torch.stack([loop, loop])
+    if normalization is None:
+        diag = deg
+        off = -edge_weight
+    elif normalization == "sym":
+        dis = deg.pow(-0.5)
+        dis = dis.masked_fill(dis == float("inf"), 0.0)
+        off = -(dis[row] * edge_weight * dis[col])
+        diag = torch.ones(num_nodes, dtype=edge_weight.dtype, device=edge_weight.device)
+    else:
+        dinv = 1.0 / deg
+        dinv = dinv.masked_fill(dinv == float("inf"), 0.0)
+        off = -(dinv[row] * edge_weight)
+        diag = torch.ones(num_nodes, dtype=edge_weight.dtype, device=edge_weight.device)
+    return torch.cat([edge_index, loops], dim=1), torch.cat([off, diag])
+
+
+def build_sparse_laplacian(edge_index: torch.Tensor, num_nodes: int, use_undirected: bool = True,
+                           normalization: str = "sym") -> Tuple[torch.Tensor, torch.Tensor]:
+    """L = I - D^-1/2 A D^-1/2 (normalization "sym") as a coalesced COO tensor,
+    and the (undirected) edge index both the GAT and the operator use
+    (generic_engine/train_cign.py:1518-1555)."""
+    if use_undirected:
+        edge_index = to_undirected(edge_index, num_nodes=num_nodes)
+    lap_index, lap_weight = get_laplacian(edge_index, num_nodes, normalization=normalization)
+    laplacian = torch.sparse_coo_tensor(indices=lap_index, values=lap_weight, size=(num_nodes, num_nodes),
+                                        dtype=torch.float).coalesce()
+    return edge_index, laplacian
+
+
+def sparse_linear_combination(A: torch.Tensor, B: torch.Tensor, alpha: float) -> torch.Tensor:
+    """alpha*A + (1-alpha)*B of two sparse COO matrices of one shape, merged
+    by coalescing (generic_engine/train_cign.py:1592-1610)."""
+    A = A.coalesce()
+    B = B.coalesce()
+    if A.shape != B.shape:
+        raise ValueError(f"Sparse matrices must have the same shape, got {A.shape} and {B.shape}.")
+    indices = torch.cat([A.indices(), B.indices()], dim=1)
+    values = torch.cat([alpha * A.values(), (1.0 - alpha) * B.values()], dim=0)
+    return torch.sparse_coo_tensor(indices=indices, values=values, size=A.shape, dtype=A.dtype,
+                                   device=A.device).coalesce()
+
+
+def build_graph_operator(edge_index: torch.Tensor, num_nodes: int, use_undirected: bool, operator_mode: str,
+                         hybrid_alpha: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The operator P of the Clifford block's powers P^s X
+    (generic_engine/train_cign.py:1613-1666): "laplacian" (L), "adjacency"
+    (D^-1/2 (A+I) D^-1/2) or "hybrid" (alpha L + (1-alpha) A_norm). Returns
+    (edge index used, P as a coalesced COO tensor)."""
+    if not (0.0 <= hybrid_alpha <= 1.0):
+        raise ValueError("hybrid_alpha must be in [0, 1].")
+    if operator_mode == "laplacian":
+        return build_sparse_laplacian(edge_index, num_nodes, use_undirected=use_undirected, normalization="sym")
+    if operator_mode == "adjacency":
+        return build_sparse_normalized_adjacency(edge_index, num_nodes, use_undirected=use_undirected,
+                                                 add_self_loop=True)
+    if operator_mode == "hybrid":
+        used, laplacian = build_sparse_laplacian(edge_index, num_nodes, use_undirected=use_undirected,
+                                                 normalization="sym")
+        _, adjacency = build_sparse_normalized_adjacency(used, num_nodes, use_undirected=False, add_self_loop=True)
+        return used, sparse_linear_combination(laplacian, adjacency, hybrid_alpha)
+    raise ValueError(f"Unknown operator_mode={operator_mode}.")
 
 
 def prepare_gat_edge_index(edge_index: torch.Tensor, num_nodes: int) -> torch.Tensor:

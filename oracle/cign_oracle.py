@@ -127,6 +127,43 @@ def normalized_adjacency(edge_index: np.ndarray, n: int, use_undirected: bool = 
     return np.stack([row, col]), (pr, pc, pv.astype(np.float32))
 
 
+def normalized_laplacian(edge_index: np.ndarray, n: int, use_undirected: bool = True):
+    """L = I - D^-1/2 A D^-1/2, generic_engine/train_cign.py:1518-1555 with
+    PyG get_laplacian(normalization="sym"): to_undirected (coalesced), self
+    loops dropped, deg = count of row entries (float32), deg^-1/2 (0 for
+    isolated nodes), off-diagonal -dis[row] * dis[col] (float32), a unit
+    diagonal appended, COO coalesce. Returns (edge_index_used, L as (row,
+    col, val float32)). Pinned by a dense float64 construction, L sqrt(deg)
+    = 0 and the spectrum in [0, 2] (tests)."""
+    row, col = edge_index[0].astype(np.int64), edge_index[1].astype(np.int64)
+    if use_undirected:
+        row, col, _ = coalesce(np.concatenate([row, col]), np.concatenate([col, row]), n)
+    used = np.stack([row, col])
+    keep = row != col
+    r, c = row[keep], col[keep]
+    deg = np.bincount(r, minlength=n).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        dis = (np.float32(1.0) / np.sqrt(deg)).astype(np.float32)
+    dis[deg == 0] = 0.0
+    off = -(dis[r] * dis[c]).astype(np.float32)
+    loop = np.arange(n, dtype=np.int64)
+    lr, lc, lv = coalesce(np.concatenate([r, loop]), np.concatenate([c, loop]), n,
+                          np.concatenate([off, np.ones(n, np.float32)]))
+    return used, (lr, lc, lv.astype(np.float32))
+
+
+def roc_auc_pairs(y_true: np.ndarray, score: np.ndarray) -> float:
+    """ROC AUC by its definition: the fraction of (positive, negative) pairs
+    ranked correctly, ties counted half (the quantity
+    generic_engine/train_cign.py:1810 takes from sklearn). O(P*N): small
+    inputs only."""
+    y_true = np.asarray(y_true)
+    pos = score[y_true == y_true.max()].astype(np.float64)
+    neg = score[y_true != y_true.max()].astype(np.float64)
+    d = pos[:, None] - neg[None, :]
+    return float(((d > 0).sum() + 0.5 * (d == 0).sum()) / d.size)
+
+
 def gat_edge_index(edge_index: np.ndarray, n: int) -> np.ndarray:
     """remove_self_loops + add_self_loops, generic_engine/train_cign.py:1759-1771."""
     row, col = edge_index[0].astype(np.int64), edge_index[1].astype(np.int64)
