@@ -23,6 +23,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -456,7 +457,7 @@ def run_block(args, torch):
     graph of 20 launches) and timed with HIP events against their own
     roofline: algorithmic bytes / HBM peak, or flops / MFMA peak for the
     projections (the lower of the two bounds)."""
-    from cign_amd import _lib, _pack, workloads
+    from cign_amd import _lib, workloads
     from cign_amd.model_cign import GraphCliffordBlock
     from cign_amd.multihop_csr_pipeline import MultiHopCSR3GraphOperator
 
@@ -508,9 +509,12 @@ def run_block(args, torch):
     alpha = torch.softmax(rnd(n, K), 1).contiguous()
     gate_w, gate_b = rnd(K, 2 * D) * 0.05, rnd(K)
     gate_ws = torch.empty(int(lib.cign_hop_gate_bwd_workspace_bytes(n, D, K)) + 256, dtype=torch.uint8, device=dev)
-    ga, gH_, gC_ = torch.empty(n, K, device=dev), torch.empty(n, D, device=dev), torch.empty(n, D, device=dev)
+    gH_, gC_ = torch.empty(n, D, device=dev), torch.empty(n, D, device=dev)
     gwt, gbt = torch.empty(K, 2 * D, device=dev), torch.empty(K, device=dev)
     gout = rnd(n, 2 * K * D)
+    gprops = [torch.empty(n, 2 * D, device=dev) for _ in range(K)]
+    parr = _lib.ptr_array([p.data_ptr() for p in props])
+    gparr = _lib.ptr_array([p.data_ptr() for p in gprops])
     Wp, bp = rnd(D, 2 * K * D) * 0.02, rnd(D)
     Wl = rnd(heads * D, D) * 0.05
     gp_out, yp = torch.empty(n, D, device=dev), torch.empty(n, D, device=dev)
@@ -536,16 +540,17 @@ def run_block(args, torch):
                                         lnw.data_ptr(), mean.data_ptr(), rstd.data_ptr(), y2.data_ptr(),
                                         gw_.data_ptr(), gb_.data_ptr(), ws.data_ptr(), ws.numel()),
                        16 * NDb + 8 * n, 0),
-        "hop_gate_fwd": (lambda: lib.call("cign_hop_gate_fwd", st(), n, D, K, 1, hh.data_ptr(), cc.data_ptr(),
-                                          gate_w.data_ptr(), gate_b.data_ptr(), alpha.data_ptr()),
-                         8 * NDb + 4 * n * K, 0),
-        "hop_gate_bwd": (lambda: lib.call("cign_hop_gate_bwd", st(), n, D, K, 1, hh.data_ptr(), cc.data_ptr(),
-                                          gate_w.data_ptr(), alpha.data_ptr(), ga.data_ptr(), gH_.data_ptr(),
-                                          gC_.data_ptr(), gwt.data_ptr(), gbt.data_ptr(), gate_ws.data_ptr(),
-                                          gate_ws.numel()), 16 * NDb + 8 * n * K, 0),
-        "pack_fwd": (lambda: _pack.forward_list(hh, cc, props, alpha, 1, 0), 8 * NDb + 16 * K * NDb + 4 * n * K, 0),
-        "pack_bwd": (lambda: _pack.backward_list(gout, hh, cc, props, alpha, 1, 0),
-                     24 * K * NDb + 16 * NDb + 8 * n * K, 0),
+        # the node hop gate fused into the pack, as the block runs them
+        "pack_gate_fwd": (lambda: lib.call("cign_pack_gate_fwd", st(), n, D, K, 1, 0, 1, hh.data_ptr(), cc.data_ptr(),
+                                           ctypes.addressof(parr), 2 * D, gate_w.data_ptr(), gate_b.data_ptr(),
+                                           alpha.data_ptr(), gout.data_ptr()),
+                          8 * NDb + 16 * K * NDb + 4 * n * K, 0),
+        "pack_gate_bwd": (lambda: lib.call("cign_pack_gate_bwd", st(), n, D, K, 1, 0, 1, gout.data_ptr(),
+                                           hh.data_ptr(), cc.data_ptr(), ctypes.addressof(parr), 2 * D,
+                                           alpha.data_ptr(), gate_w.data_ptr(), gH_.data_ptr(), gC_.data_ptr(),
+                                           ctypes.addressof(gparr), 2 * D, gwt.data_ptr(), gbt.data_ptr(),
+                                           gate_ws.data_ptr(), gate_ws.numel()),
+                          24 * K * NDb + 16 * NDb + 8 * n * K, 0),
         "proj_gamma_fwd": (lambda: lib.call("cign_linear_gamma_fwd", st(), n, D, 2 * K * D, 0, math, gout.data_ptr(),
                                             Wp.data_ptr(), bp.data_ptr(), hh.data_ptr(), lnw.data_ptr(), 0.28, 9,
                                             gp_out.data_ptr(), yp.data_ptr(), mask.data_ptr()),

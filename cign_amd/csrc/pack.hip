@@ -19,7 +19,7 @@
 // Forward: one thread per (node, 16-byte chunk of D), all K hops in registers.
 // Backward: a row's chunks on one lane group (rowops.h) so grad_alpha is a
 // butterfly; grad_H / grad_C accumulate over hops in registers (no atomics).
-#include "rowops.h"
+#include "clifford.h"
 
 namespace cign {
 namespace packk {
@@ -45,39 +45,6 @@ struct PackArgs {
   int64_t gp_stride;
   float* gA;
 };
-
-struct DW {
-  float Dv, Wv, dD_bhr, dD_brh, dW_bhr, dW_brh;
-};
-
-__device__ __forceinline__ DW interact(float bhr, float brh, int mode) {
-  DW r;
-  if (mode == 0) {
-    r.Dv = silu(bhr);
-    r.Wv = bhr - brh;
-    r.dD_bhr = silu_grad(bhr);
-    r.dD_brh = 0.0f;
-    r.dW_bhr = 1.0f;
-    r.dW_brh = -1.0f;
-  } else {
-    const float sym = 0.5f * (bhr + brh);
-    const float anti = 0.5f * (bhr - brh);
-    r.Dv = silu(sym);
-    const float ds = silu_grad(sym);
-    float dw = 1.0f;
-    if (mode == 2) {
-      r.Wv = tanhf(anti);
-      dw = 1.0f - r.Wv * r.Wv;
-    } else {
-      r.Wv = anti;
-    }
-    r.dD_bhr = 0.5f * ds;
-    r.dD_brh = 0.5f * ds;
-    r.dW_bhr = 0.5f * dw;
-    r.dW_brh = -0.5f * dw;
-  }
-  return r;
-}
 
 template <int W>
 __global__ __launch_bounds__(kBlock) void pack_fwd_kernel(PackArgs a) {

@@ -7,6 +7,8 @@ returns None, as in the reference.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 import torch.nn.functional as F
 
@@ -50,6 +52,77 @@ class HopGateFunction(torch.autograd.Function):
                  weight.data_ptr(), alpha.data_ptr(), g.data_ptr(), gH.data_ptr(), gC.data_ptr(), gW.data_ptr(),
                  gb.data_ptr(), ws.data_ptr(), ws_bytes)
         return gH, gC, gW, gb, None
+
+
+class PackGateFunction(torch.autograd.Function):
+    """The node-mode hop gate fused into the Clifford pack: G_raw from (H_norm,
+    C_norm, gate weight [K,2D], gate bias [K], K propagated [N,2D] tensors)
+    in one kernel each way (cign_pack_gate_fwd / cign_pack_gate_bwd). Alpha
+    exists only inside (saved for the backward); grad_H / grad_C come out
+    with the pack's and the gate's terms already summed."""
+
+    @staticmethod
+    def forward(ctx, interaction, weighting, score_mode, H, C, weight, bias, *props):
+        from ._pack import _out_width
+        for t, n in ((H, "H_norm"), (C, "C_norm"), (weight, "weight"), (bias, "bias")):
+            check_input(t, n)
+        for k, p in enumerate(props):
+            check_input(p, f"P{k}")
+        check(H.dim() == 2 and C.shape == H.shape, "H_norm/C_norm must be [N,D]")
+        N, D = H.shape
+        K = len(props)
+        check(1 <= K <= 16, "hop count must be in [1, 16]")
+        check(weight.dim() == 2 and tuple(weight.shape) == (K, 2 * D), "hop gate weight must be [K,2D]")
+        check(bias.dim() == 1 and bias.numel() == K, "hop gate bias must be [K]")
+        for k, p in enumerate(props):
+            check(tuple(p.shape) == (N, 2 * D), f"P{k} must be [N,2D]")
+        lib = _lib.load_library()
+        alpha = torch.empty((N, K), dtype=torch.float32, device=H.device)
+        out = torch.empty((N, _out_width(D, K, int(weighting))), dtype=torch.float32, device=H.device)
+        arr = _lib.ptr_array([p.data_ptr() for p in props])
+        lib.call("cign_pack_gate_fwd", _lib.stream_ptr(H.device), N, D, K, int(interaction), int(weighting),
+                 int(score_mode), H.data_ptr(), C.data_ptr(), ctypes.addressof(arr), 2 * D, weight.data_ptr(),
+                 bias.data_ptr(), alpha.data_ptr(), out.data_ptr())
+        ctx.modes = (int(interaction), int(weighting), int(score_mode))
+        ctx.save_for_backward(H, C, weight, alpha, *props)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        H, C, weight, alpha, *props = ctx.saved_tensors
+        interaction, weighting, score_mode = ctx.modes
+        N, D = H.shape
+        K = len(props)
+        lib = _lib.load_library()
+        g = grad_out.to(dtype=torch.float32).contiguous()
+        gH, gC = torch.empty_like(H), torch.empty_like(C)
+        gP = [torch.empty_like(p) for p in props]
+        gW = torch.empty_like(weight)
+        gb = torch.empty((K,), dtype=torch.float32, device=H.device)
+        ws_bytes = int(lib.cign_hop_gate_bwd_workspace_bytes(N, D, K))
+        ws = _lib.workspace(ws_bytes, H.device)
+        arr = _lib.ptr_array([p.data_ptr() for p in props])
+        garr = _lib.ptr_array([t.data_ptr() for t in gP])
+        lib.call("cign_pack_gate_bwd", _lib.stream_ptr(H.device), N, D, K, interaction, weighting, score_mode,
+                 g.data_ptr(), H.data_ptr(), C.data_ptr(), ctypes.addressof(arr), 2 * D, alpha.data_ptr(),
+                 weight.data_ptr(), gH.data_ptr(), gC.data_ptr(), ctypes.addressof(garr), 2 * D, gW.data_ptr(),
+                 gb.data_ptr(), ws.data_ptr(), ws_bytes)
+        return (None, None, None, gH, gC, gW, gb, *gP)
+
+
+def gated_clifford_pack(H_norm: torch.Tensor, C_norm: torch.Tensor, propagated, linear: torch.nn.Linear,
+                        score_mode: str, interaction: int, weighting: int) -> torch.Tensor:
+    """G_raw of the Clifford block with the node-mode gate: the same value as
+    clifford_pack_any(H_norm, C_norm, propagated, node_hop_gate(...)), from
+    one fused kernel per direction. Inputs become float32 as both of those
+    functions make them."""
+    mode = {"old": 0, "new": 1}[str(score_mode)]
+    H = H_norm.to(dtype=torch.float32).contiguous()
+    C = C_norm.to(dtype=torch.float32).contiguous()
+    props = [p.to(dtype=torch.float32).contiguous() for p in propagated]
+    bias = linear.bias if linear.bias is not None else torch.zeros(linear.out_features, device=H.device)
+    return PackGateFunction.apply(int(interaction), int(weighting), mode, H, C, linear.weight.float().contiguous(),
+                                  bias.float().contiguous(), *props)
 
 
 def node_hop_gate(H_norm: torch.Tensor, C_norm: torch.Tensor, linear: torch.nn.Linear, score_mode: str) -> torch.Tensor:

@@ -34,7 +34,7 @@ from . import _pack
 from .collapsed_gat import collapsed_gat_mean_bias_silu
 from .fused_block_ops import fused_add_layernorm, fused_dropout_layernorm
 from .graph import selected_sparse_powers
-from .hop_gate import global_hop_gate, node_hop_gate
+from .hop_gate import gated_clifford_pack, global_hop_gate, node_hop_gate
 from .linear import linear_attention_logits, linear_gamma_residual, mfma_linear
 
 
@@ -215,9 +215,15 @@ class GraphCliffordBlock(nn.Module):
         C_norm = fused_add_layernorm(C_gat, H_norm, self.c_norm.weight, self.c_norm.bias, self.c_norm.eps)
         HC_norm = torch.cat([H_norm, C_norm], dim=-1)
         propagated = selected_sparse_powers(operator=graph_operator, X=HC_norm, powers=self.order_set)
-        hop_gate = self.compute_hop_gate(H_norm, C_norm)
-        G_raw = _pack.clifford_pack_any(H_norm, C_norm, [propagated[s] for s in self.order_set], hop_gate,
-                                        self._interaction_code(), 0 if self.alpha_weighting_mode == "old" else 1)
+        props = [propagated[s] for s in self.order_set]
+        weighting = 0 if self.alpha_weighting_mode == "old" else 1
+        if self.hop_gate_mode == "node":
+            # the gate's only consumer is the pack: one fused kernel each way
+            G_raw = gated_clifford_pack(H_norm, C_norm, props, self.hop_gate_mlp, self.alpha_score_mode,
+                                        self._interaction_code(), weighting)
+        else:
+            G_raw = _pack.clifford_pack_any(H_norm, C_norm, props, self.compute_hop_gate(H_norm, C_norm),
+                                            self._interaction_code(), weighting)
         gamma = self.gamma if self.gamma_mode == "vector" else self.gamma.expand(self.hidden_dim)
         return linear_gamma_residual(H, G_raw, self.proj, gamma.contiguous(), p, self.use_selective_amp,
                                      self.selective_amp_dtype)

@@ -237,6 +237,27 @@ int cign_hop_gate_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t sco
                       const float* C, const float* weight, const float* alpha, const float* grad_alpha, float* grad_H,
                       float* grad_C, float* grad_weight, float* grad_bias, void* workspace, int64_t workspace_bytes);
 
+/* Node-mode hop gate fused into the Clifford pack (interaction and weighting
+ * codes of cign_pack_fwd): alpha [n,K] from (H, C, gate weight [K,2D], gate
+ * bias [K]) as cign_hop_gate_fwd computes it, written to `alpha`, and the
+ * pack of cign_pack_fwd with that alpha into `out`, in one pass over H and C.
+ * Replaces the compute_hop_gate + fused pack pair of GraphCliffordBlock.forward
+ * (generic_engine/model_cign.py:721-749 feeding :803-846, node hop gate). */
+int cign_pack_gate_fwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t interaction, int32_t weighting,
+                       int32_t score_mode, const float* H, const float* C, const float* const* props,
+                       int64_t prop_stride, const float* gate_weight, const float* gate_bias, float* alpha,
+                       float* out);
+
+/* Backward of cign_pack_gate_fwd given grad_out and its alpha: grad_H and
+ * grad_C (the pack's and the gate's terms summed), grad_props, grad_gate_weight
+ * [K,2D], grad_gate_bias [K]; workspace of cign_hop_gate_bwd_workspace_bytes.
+ * Replaces the autograd of the same lines. */
+int cign_pack_gate_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t interaction, int32_t weighting,
+                       int32_t score_mode, const float* grad_out, const float* H, const float* C,
+                       const float* const* props, int64_t prop_stride, const float* alpha, const float* gate_weight,
+                       float* grad_H, float* grad_C, float* const* grad_props, int64_t grad_prop_stride,
+                       float* grad_gate_weight, float* grad_gate_bias, void* workspace, int64_t workspace_bytes);
+
 /* ---- Clifford packs (float32) ------------------------------------------- */
 
 /* Fused Clifford interaction + alpha weighting over K <= 16 hops.

@@ -133,3 +133,65 @@ def test_pack_argument_errors_and_alpha_default():
     # alpha=None means all-ones weights
     out = fused_clifford_pack(Ht, Ct, Pt, None)
     assert_close(_n(out), O.clifford_pack_forward(H, C, props, np.ones((50, 3)), 0, 0), name="alpha ones", **T32)
+
+
+@pytest.mark.parametrize("n,D,K,interaction,weighting,score", [
+    (600, 256, 3, 1, 0, 1), (600, 256, 3, 2, 1, 1), (601, 256, 3, 0, 0, 0), (300, 64, 2, 1, 1, 0),
+    (200, 48, 4, 2, 0, 1), (150, 32, 5, 1, 0, 1), (90, 6, 3, 0, 1, 1), (40, 256, 1, 1, 0, 0)])
+def test_gated_pack_matches_oracle(n, D, K, interaction, weighting, score):
+    """The node-mode gate fused into the pack (cign_pack_gate_fwd/bwd) against
+    the oracle's gate followed by its pack: G_raw, and grad H / C (the pack's
+    and the gate's terms summed), grad P_k, grad gate weight and bias."""
+    from cign_amd.hop_gate import PackGateFunction
+
+    print(f"gated pack n={n} D={D} K={K} interaction={interaction} weighting={weighting} score={score}", flush=True)
+    rng = np.random.default_rng(n + D + K)
+    H, C, props, _ = _inputs(rng, n, D, K)
+    C[:, 0] = H[:, 0]  # ties of |H - C|: sign(0) = 0 in the gradient
+    W = (0.2 * rng.standard_normal((K, 2 * D))).astype(np.float32)
+    b = rng.standard_normal(K).astype(np.float32)
+    alpha = O.hop_gate_forward(H, C, W, b, score)
+    out = O.clifford_pack_forward(H, C, props, alpha, interaction, weighting)
+    g = rng.standard_normal(out.shape).astype(np.float32)
+    pH, pC, pP, pA = O.clifford_pack_backward(g, H, C, props, alpha, interaction, weighting)
+    gH, gC, gW, gb = O.hop_gate_backward(pA, H, C, W, b, score)
+
+    Ht, Ct, Wt, bt = (_t(a).requires_grad_() for a in (H, C, W, b))
+    Pt = [_t(p).requires_grad_() for p in props]
+    got = PackGateFunction.apply(interaction, weighting, score, Ht, Ct, Wt, bt, *Pt)
+    assert_close(_n(got), out, name="G_raw", **T32)
+    (got * _t(g)).sum().backward()
+    assert_close(_n(Ht.grad), pH + gH, name="grad H", **T32)
+    assert_close(_n(Ct.grad), pC + gC, name="grad C", **T32)
+    for k in range(K):
+        assert_close(_n(Pt[k].grad), pP[k], name=f"grad P{k}", **T32)
+    # parameter gradients sum over n rows
+    assert_close(_n(Wt.grad), gW, name="grad gate weight", rtol=1e-4, atol=1e-4)
+    assert_close(_n(bt.grad), gb, name="grad gate bias", rtol=1e-4, atol=1e-4)
+
+
+def test_gated_pack_equals_gate_then_pack():
+    """The fused path and the two-call path (node_hop_gate, then the pack) of
+    the block agree, value and gradients, within fp32 rounding."""
+    from cign_amd import _pack
+    from cign_amd.hop_gate import gated_clifford_pack, node_hop_gate
+
+    rng = np.random.default_rng(7)
+    n, D, K = 500, 256, 3
+    H, C, props, _ = _inputs(rng, n, D, K)
+    lin = torch.nn.Linear(2 * D, K).cuda()
+    g = _t(rng.standard_normal((n, 2 * K * D)))
+    res = []
+    for fused in (True, False):
+        Ht, Ct = _t(H).requires_grad_(), _t(C).requires_grad_()
+        Pt = [_t(p).requires_grad_() for p in props]
+        lin.zero_grad()
+        if fused:
+            out = gated_clifford_pack(Ht, Ct, Pt, lin, "new", 1, 0)
+        else:
+            out = _pack.clifford_pack_any(Ht, Ct, Pt, node_hop_gate(Ht, Ct, lin, "new"), 1, 0)
+        (out * g).sum().backward()
+        res.append([out.detach(), Ht.grad, Ct.grad, *[p.grad for p in Pt], lin.weight.grad.clone(),
+                    lin.bias.grad.clone()])
+    for i, (a, e) in enumerate(zip(*res)):
+        assert_close(_n(a), _n(e), name=f"output {i}", rtol=1e-4, atol=1e-4)
