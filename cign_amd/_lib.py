@@ -64,6 +64,8 @@ _SIGNATURES = {
     "cign_linear_bwd_workspace_bytes": (_I64, [_I64, _I32, _I32, _I32]),
     "cign_linear_bwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _I64]),
     # Clifford packs (pack.hip)
+    "cign_add_ln_cat_fwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _F32, _P, _P, _P, _P]),
+    "cign_add_ln_cat_bwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64]),
     "cign_pack_gate_fwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _I64, _P, _P, _P, _P]),
     "cign_pack_gate_bwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _I64, _P, _P, _P, _P,
                                      _P, _I64, _P, _P, _P, _I64]),

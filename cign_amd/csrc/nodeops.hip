@@ -263,7 +263,7 @@ template <int MODE, int LPR, int V, int W>
 __global__ __launch_bounds__(kBlock) void ln_fwd_kernel(int64_t n, int D, const float* x, const float* x2,
                                                         const float* wt, const float* bs, float p, float eps,
                                                         uint64_t seed, float* y, float* mean, float* rstd,
-                                                        uint8_t* mask) {
+                                                        uint8_t* mask, float* ycat) {
   const Geo<LPR> g;
   const int qd = D / W;
   const float scale = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
@@ -303,6 +303,7 @@ __global__ __launch_bounds__(kBlock) void ln_fwd_kernel(int64_t n, int D, const 
           Chunk<float, W>::load(x2 + base, bv);
 #pragma unroll
           for (int w = 0; w < W; ++w) qv[v][w] = xv[w] + bv[w];
+          if constexpr (MODE == 2) Chunk<float, W>::store(ycat + 2 * r * D + c * W, bv);
         }
 #pragma unroll
         for (int w = 0; w < W; ++w) s += qv[v][w];
@@ -324,6 +325,7 @@ __global__ __launch_bounds__(kBlock) void ln_fwd_kernel(int64_t n, int D, const 
 #pragma unroll
         for (int w = 0; w < W; ++w) o[w] = (qv[v][w] - mu) * rs * wv[v][w] + bv[v][w];
         Chunk<float, W>::store(y + r * D + c * W, o);
+        if constexpr (MODE == 2) Chunk<float, W>::store(ycat + 2 * r * D + D + c * W, o);
       }
     }
     if (g.q == 0) {
@@ -334,12 +336,14 @@ __global__ __launch_bounds__(kBlock) void ln_fwd_kernel(int64_t n, int D, const 
 }
 
 // dx (MODE 0) or dz (MODE 1) per row, and the row block's partial sums of
-// gy*xhat (weight) and gy (bias): part layout [2][nb][D].
+// gy*xhat (weight) and gy (bias): part layout [2][nb][D]. MODE 2 is MODE 1
+// for an output also read as the right half of [x2 | y] ([n, 2D], gradient
+// gcat): gy gains gcat's right half, and dx2 = dz + gcat's left half.
 template <int MODE, int LPR, int V, int W>
 __global__ __launch_bounds__(kBlock) void ln_bwd_kernel(int64_t n, int D, const float* gy, const float* x,
                                                         const float* x2, const float* wt, const float* mean,
                                                         const float* rstd, const uint8_t* mask, float p, float* dx,
-                                                        float* part, int nb) {
+                                                        float* part, int nb, const float* gcat, float* dx2) {
   __shared__ float lds[kBlock * V * W];
   const Geo<LPR> g;
   const int qd = D / W;
@@ -359,6 +363,7 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_kernel(int64_t n, int D, const 
     const float mu = mean[r];
     const float rs = rstd[r];
     float xh[V][W], dn[V][W], gv[V][W];
+    float gleft[MODE == 2 ? V : 1][W];
     bool keep[V][W];
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
@@ -374,6 +379,13 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_kernel(int64_t n, int D, const 
         float xv[W];
         Chunk<float, W>::load(x + base, xv);
         Chunk<float, W>::load(gy + base, gv[v]);
+        if constexpr (MODE == 2) {
+          float gr[W];
+          Chunk<float, W>::load(gcat + 2 * r * D + D + c * W, gr);
+          Chunk<float, W>::load(gcat + 2 * r * D + c * W, gleft[v]);
+#pragma unroll
+          for (int w = 0; w < W; ++w) gv[v][w] += gr[w];
+        }
         float qv[W];
         if constexpr (MODE == 0) {
           load_mask<W>(mask + base, keep[v]);
@@ -410,6 +422,11 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_kernel(int64_t n, int D, const 
           o[w] = MODE == 0 ? (keep[v][w] ? dq * scale : 0.0f) : dq;
         }
         Chunk<float, W>::store(dx + r * D + c * W, o);
+        if constexpr (MODE == 2) {
+#pragma unroll
+          for (int w = 0; w < W; ++w) o[w] += gleft[v][w];
+          Chunk<float, W>::store(dx2 + r * D + c * W, o);
+        }
       }
     }
   }
@@ -625,23 +642,25 @@ int cign_head_silu_bwd(void* stream, int64_t n, int32_t H, int32_t C, const floa
 // ---- block ops ------------------------------------------------------------
 static int ln_fwd(int mode, void* stream, int64_t n, int32_t D, const float* x, const float* x2, const float* w,
                   const float* b, float p, float eps, uint64_t seed, float* y, float* mean, float* rstd,
-                  uint8_t* mask, const char* who) {
+                  uint8_t* mask, const char* who, float* ycat = nullptr) {
   int rc = check_rows(who, n, D);
   if (rc) return rc;
   if (!(p >= 0.0f && p < 1.0f)) return set_error(kInvalid, "%s: dropout_p must be in [0,1)", who);
   if (n == 0) return kOk;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int W = chunk_width(D, {x, x2 ? x2 : x, w, b, y, mask ? static_cast<const void*>(mask) : x});
+  const int W = chunk_width(D, {x, x2 ? x2 : x, w, b, y, mask ? static_cast<const void*>(mask) : x, ycat ? ycat : y});
   return with_geo(D / W, [&](auto LC, auto VC) {
     constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
     const int grid = grid_for(n, Geo<L>::RPB);
 #define CIGN_LN_FWD(M, WW)                                                                                          \
   hipLaunchKernelGGL((ln_fwd_kernel<M, L, V, WW>), dim3(grid), dim3(kBlock), 0, st, n, D, x, x2, w, b, p, eps, seed, \
-                     y, mean, rstd, mask)
+                     y, mean, rstd, mask, ycat)
     if (mode == 0) {
       if (W == 4) CIGN_LN_FWD(0, 4); else CIGN_LN_FWD(0, 1);
-    } else {
+    } else if (mode == 1) {
       if (W == 4) CIGN_LN_FWD(1, 4); else CIGN_LN_FWD(1, 1);
+    } else {
+      if (W == 4) CIGN_LN_FWD(2, 4); else CIGN_LN_FWD(2, 1);
     }
 #undef CIGN_LN_FWD
     return check_launch(who);
@@ -650,7 +669,8 @@ static int ln_fwd(int mode, void* stream, int64_t n, int32_t D, const float* x, 
 
 static int ln_bwd(int mode, void* stream, int64_t n, int32_t D, const float* gy, const float* x, const float* x2,
                   const float* w, const float* mean, const float* rstd, const uint8_t* mask, float p, float* dx,
-                  float* dw, float* db, void* workspace, int64_t workspace_bytes, const char* who) {
+                  float* dw, float* db, void* workspace, int64_t workspace_bytes, const char* who,
+                  const float* gcat = nullptr, float* dx2 = nullptr) {
   int rc = check_rows(who, n, D);
   if (rc) return rc;
   if (workspace_bytes < colsum_bytes(n, D, 2)) return set_error(kInvalid, "%s: workspace too small", who);
@@ -658,16 +678,19 @@ static int ln_bwd(int mode, void* stream, int64_t n, int32_t D, const float* gy,
   const int nb = colsum_blocks(n);
   float* part = static_cast<float*>(workspace);
   if (n > 0) {
-    const int W = chunk_width(D, {gy, x, x2 ? x2 : x, w, dx, mask ? static_cast<const void*>(mask) : x});
+    const int W = chunk_width(D, {gy, x, x2 ? x2 : x, w, dx, mask ? static_cast<const void*>(mask) : x,
+                                  gcat ? gcat : gy, dx2 ? dx2 : dx});
     rc = with_geo(D / W, [&](auto LC, auto VC) {
       constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
 #define CIGN_LN_BWD(M, WW)                                                                                           \
   hipLaunchKernelGGL((ln_bwd_kernel<M, L, V, WW>), dim3(nb), dim3(kBlock), 0, st, n, D, gy, x, x2, w, mean, rstd, mask, \
-                     p, dx, part, nb)
+                     p, dx, part, nb, gcat, dx2)
       if (mode == 0) {
         if (W == 4) CIGN_LN_BWD(0, 4); else CIGN_LN_BWD(0, 1);
-      } else {
+      } else if (mode == 1) {
         if (W == 4) CIGN_LN_BWD(1, 4); else CIGN_LN_BWD(1, 1);
+      } else {
+        if (W == 4) CIGN_LN_BWD(2, 4); else CIGN_LN_BWD(2, 1);
       }
 #undef CIGN_LN_BWD
       return check_launch(who);
@@ -702,6 +725,19 @@ int cign_add_ln_bwd(void* stream, int64_t n, int32_t D, const float* grad_y, con
                     float* grad_bias, void* workspace, int64_t workspace_bytes) {
   return ln_bwd(1, stream, n, D, grad_y, a, b, weight, mean, rstd, nullptr, 0.0f, grad_z, grad_weight, grad_bias,
                 workspace, workspace_bytes, "cign_add_ln_bwd");
+}
+
+int cign_add_ln_cat_fwd(void* stream, int64_t n, int32_t D, const float* a, const float* b, const float* weight,
+                        const float* bias, float eps, float* y, float* cat, float* mean, float* rstd) {
+  return ln_fwd(2, stream, n, D, a, b, weight, bias, 0.0f, eps, 0, y, mean, rstd, nullptr, "cign_add_ln_cat_fwd",
+                cat);
+}
+
+int cign_add_ln_cat_bwd(void* stream, int64_t n, int32_t D, const float* grad_y, const float* grad_cat, const float* a,
+                        const float* b, const float* weight, const float* mean, const float* rstd, float* grad_a,
+                        float* grad_b, float* grad_weight, float* grad_bias, void* workspace, int64_t workspace_bytes) {
+  return ln_bwd(2, stream, n, D, grad_y, a, b, weight, mean, rstd, nullptr, 0.0f, grad_a, grad_weight, grad_bias,
+                workspace, workspace_bytes, "cign_add_ln_cat_bwd", grad_cat, grad_b);
 }
 
 int cign_gamma_residual_fwd(void* stream, int64_t n, int32_t D, const float* h, const float* g, const float* gamma,

@@ -237,6 +237,48 @@ class _AddLayerNormFn(torch.autograd.Function):
         return gz, gz, gw, gb, None
 
 
+class _AddLayerNormCatFn(torch.autograd.Function):
+    """y = LayerNorm(a + b) and cat = [b | y] from one kernel
+    (cign_add_ln_cat_fwd): the block's C_norm and HC_norm (model_cign.py:
+    781-792). The backward takes both outputs' gradients in one kernel
+    (cign_add_ln_cat_bwd), so neither the concatenation's gradient slices nor
+    the sums of y's two uses and of b's two uses pass through separate
+    additions."""
+
+    @staticmethod
+    def forward(ctx, a, b, weight, bias, eps):
+        for t, n in ((a, "a"), (b, "b"), (weight, "weight"), (bias, "bias")):
+            check_input(t, n)
+        N, D = a.shape
+        lib = _lib.load_library()
+        y = torch.empty_like(a)
+        cat = torch.empty((N, 2 * D), dtype=torch.float32, device=a.device)
+        mean = torch.empty((N,), dtype=torch.float32, device=a.device)
+        rstd = torch.empty_like(mean)
+        lib.call("cign_add_ln_cat_fwd", _lib.stream_ptr(a.device), N, D, a.data_ptr(), b.data_ptr(),
+                 weight.data_ptr(), bias.data_ptr(), float(eps), y.data_ptr(), cat.data_ptr(), mean.data_ptr(),
+                 rstd.data_ptr())
+        ctx.save_for_backward(a, b, weight, mean, rstd)
+        return y, cat
+
+    @staticmethod
+    def backward(ctx, grad_y, grad_cat):
+        a, b, weight, mean, rstd = ctx.saved_tensors
+        N, D = a.shape
+        lib = _lib.load_library()
+        gy = grad_y.to(dtype=torch.float32).contiguous()
+        gc = grad_cat.to(dtype=torch.float32).contiguous()
+        ga, gbb = torch.empty_like(a), torch.empty_like(b)
+        gw = torch.empty((D,), dtype=torch.float32, device=a.device)
+        gbias = torch.empty_like(gw)
+        ws_bytes = int(lib.cign_colsum_workspace_bytes(N, D, 2))
+        ws = _lib.workspace(ws_bytes, a.device)
+        lib.call("cign_add_ln_cat_bwd", _lib.stream_ptr(a.device), N, D, gy.data_ptr(), gc.data_ptr(), a.data_ptr(),
+                 b.data_ptr(), weight.data_ptr(), mean.data_ptr(), rstd.data_ptr(), ga.data_ptr(), gbb.data_ptr(),
+                 gw.data_ptr(), gbias.data_ptr(), ws.data_ptr(), ws_bytes)
+        return ga, gbb, gw, gbias, None
+
+
 class _DropoutGammaResidualFn(torch.autograd.Function):
     """fused_block_ops.py:90-106."""
 
@@ -283,6 +325,18 @@ def fused_add_layernorm(a, b, weight, bias, eps):
     if a.shape != b.shape or weight.numel() != D or bias.numel() != D:
         raise ValueError("Add+LayerNorm shapes do not match")
     return _AddLayerNormFn.apply(a, b, weight, bias, float(eps))
+
+
+def fused_add_layernorm_cat(a, b, weight, bias, eps):
+    """(LayerNorm(a + b), [b | LayerNorm(a + b)]): the add-LayerNorm and the
+    concatenation of GraphCliffordBlock.forward (model_cign.py:781-792) in
+    one kernel each way. Inputs become float32 contiguous tensors."""
+    D = _check_py_2d(a, "a")
+    _check_py_2d(b, "b")
+    if a.shape != b.shape or weight.numel() != D or bias.numel() != D:
+        raise ValueError("Add+LayerNorm shapes do not match")
+    f = lambda t: t.to(dtype=torch.float32).contiguous()
+    return _AddLayerNormCatFn.apply(f(a), f(b), f(weight), f(bias), float(eps))
 
 
 def fused_dropout_gamma_residual(h, g, gamma, dropout_p):

@@ -32,7 +32,7 @@ import torch.nn.functional as F
 
 from . import _pack
 from .collapsed_gat import collapsed_gat_mean_bias_silu
-from .fused_block_ops import fused_add_layernorm, fused_dropout_layernorm
+from .fused_block_ops import fused_add_layernorm_cat, fused_dropout_layernorm
 from .graph import selected_sparse_powers
 from .hop_gate import gated_clifford_pack, global_hop_gate, node_hop_gate
 from .linear import linear_attention_logits, linear_gamma_residual, mfma_linear
@@ -212,8 +212,8 @@ class GraphCliffordBlock(nn.Module):
                                "before training.")
         csr, csc, perm = fused_gat_graph
         C_gat = self.context_gat(H_norm, csr, csc, perm)
-        C_norm = fused_add_layernorm(C_gat, H_norm, self.c_norm.weight, self.c_norm.bias, self.c_norm.eps)
-        HC_norm = torch.cat([H_norm, C_norm], dim=-1)
+        C_norm, HC_norm = fused_add_layernorm_cat(C_gat, H_norm, self.c_norm.weight, self.c_norm.bias,
+                                                  self.c_norm.eps)
         propagated = selected_sparse_powers(operator=graph_operator, X=HC_norm, powers=self.order_set)
         props = [propagated[s] for s in self.order_set]
         weighting = 0 if self.alpha_weighting_mode == "old" else 1

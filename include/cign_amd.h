@@ -206,6 +206,20 @@ int cign_add_ln_bwd(void* stream, int64_t n, int32_t D, const float* grad_y, con
                     const float* weight, const float* mean, const float* rstd, float* grad_z, float* grad_weight,
                     float* grad_bias, void* workspace, int64_t workspace_bytes);
 
+/* y = LayerNorm(a + b) * weight + bias as cign_add_ln_fwd, also written with
+ * b into cat [n, 2D] = [b | y]. Replaces the add-LayerNorm and the
+ * concatenation of GraphCliffordBlock.forward (C_norm = LN(C_gat + H_norm),
+ * HC_norm = cat([H_norm, C_norm]); generic_engine/model_cign.py:781-792). */
+int cign_add_ln_cat_fwd(void* stream, int64_t n, int32_t D, const float* a, const float* b, const float* weight,
+                        const float* bias, float eps, float* y, float* cat, float* mean, float* rstd);
+
+/* Backward of cign_add_ln_cat_fwd given the gradients of y and cat: the LN
+ * backward of grad_y + grad_cat[:, D:] gives grad_a, and grad_b = grad_a +
+ * grad_cat[:, :D]; grad_weight, grad_bias; workspace as cign_add_ln_bwd. */
+int cign_add_ln_cat_bwd(void* stream, int64_t n, int32_t D, const float* grad_y, const float* grad_cat, const float* a,
+                        const float* b, const float* weight, const float* mean, const float* rstd, float* grad_a,
+                        float* grad_b, float* grad_weight, float* grad_bias, void* workspace, int64_t workspace_bytes);
+
 /* y = h + gamma * keep * g / (1-p); mask [n,D] u8. Replaces ext
  * dropout_gamma_residual_forward (fused_block_ops.cpp:74-81). */
 int cign_gamma_residual_fwd(void* stream, int64_t n, int32_t D, const float* h, const float* g, const float* gamma,

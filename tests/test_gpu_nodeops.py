@@ -259,3 +259,30 @@ def test_hop_gate_matches_oracle(n, D, K, mode):
     assert_close(_n(Ct.grad), gC, name="grad C", **T32)
     assert_close(_n(Wt.grad), gW, name="grad weight", rtol=1e-4, atol=1e-4)
     assert_close(_n(bt.grad), gb, name="grad bias", rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("n,D", [(1000, 256), (333, 100), (50, 6)])
+def test_add_layernorm_cat_matches_oracle(n, D):
+    """(LN(a + b), [b | LN(a + b)]) and the backward given both outputs'
+    gradients (cign_add_ln_cat_fwd/bwd) against the oracle's add+LayerNorm:
+    grad a = the LN backward of grad_y + grad_cat[:, D:], grad b = grad a +
+    grad_cat[:, :D]; weight and bias gradients from the summed grad_y."""
+    from cign_amd.fused_block_ops import fused_add_layernorm_cat
+
+    print(f"add+ln+cat n={n} D={D}", flush=True)
+    rng = np.random.default_rng(n + D)
+    a, b = rng.standard_normal((n, D)).astype(np.float32), rng.standard_normal((n, D)).astype(np.float32)
+    w, bias = (1 + 0.3 * rng.standard_normal(D)).astype(np.float32), rng.standard_normal(D).astype(np.float32)
+    gy, gcat = rng.standard_normal((n, D)).astype(np.float32), rng.standard_normal((n, 2 * D)).astype(np.float32)
+    at, bt, wt, bst = (_t(x).requires_grad_() for x in (a, b, w, bias))
+    y, cat = fused_add_layernorm_cat(at, bt, wt, bst, 1e-5)
+    ey = O.add_layernorm_forward(a, b, w, bias, 1e-5)[0]
+    assert_close(_n(y), ey, name="y", **T32)
+    assert_close(_n(cat[:, D:]), ey, name="cat right", **T32)
+    assert np.array_equal(_n(cat[:, :D]), b.astype(np.float64))
+    ((y * _t(gy)).sum() + (cat * _t(gcat)).sum()).backward()
+    dz, gw, gb = O.add_layernorm_backward(gy + gcat[:, D:], a, b, w, 1e-5)
+    assert_close(_n(at.grad), dz, name="grad a", **T32)
+    assert_close(_n(bt.grad), dz + gcat[:, :D], name="grad b", **T32)
+    assert_close(_n(wt.grad), gw, name="grad weight", rtol=1e-4, atol=1e-4)
+    assert_close(_n(bst.grad), gb, name="grad bias", rtol=1e-4, atol=1e-4)
