@@ -25,7 +25,6 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
-import os
 import sys
 import time
 from pathlib import Path
