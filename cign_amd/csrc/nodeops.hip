@@ -21,9 +21,12 @@ namespace rowops {
 // a workgroup of kColsumThreads covers 64 columns; thread (c, s) sums the
 // partials b = s, s + 16, ... with four independent accumulators (combined in
 // a fixed order), then the 16 slices are added in order through LDS.
+template <int kCols>
 __global__ __launch_bounds__(kColsumThreads) void colsum_kernel(const float* part, int nb, int width, float* out0,
                                                                 float* out1) {
-  constexpr int kCols = 64;
+  // kCols columns x kSlices partial slices per workgroup; a slice thread
+  // keeps eight partial rows in flight, then the slices meet in an LDS tree
+  // (a fixed order, so the sums are deterministic).
   constexpr int kSlices = kColsumThreads / kCols;
   __shared__ float red[kColsumThreads];
   const float* src = part + static_cast<int64_t>(blockIdx.y) * nb * width;
@@ -31,24 +34,23 @@ __global__ __launch_bounds__(kColsumThreads) void colsum_kernel(const float* par
   const int t = threadIdx.x;
   const int c = blockIdx.x * kCols + t % kCols;
   const int s = t / kCols;
-  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  float acc[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
   if (c < width) {
     int b = s;
-    for (; b + 3 * kSlices < nb; b += 4 * kSlices) {
-      a0 += src[static_cast<int64_t>(b) * width + c];
-      a1 += src[static_cast<int64_t>(b + kSlices) * width + c];
-      a2 += src[static_cast<int64_t>(b + 2 * kSlices) * width + c];
-      a3 += src[static_cast<int64_t>(b + 3 * kSlices) * width + c];
-    }
-    for (; b < nb; b += kSlices) a0 += src[static_cast<int64_t>(b) * width + c];
+    for (; b + 7 * kSlices < nb; b += 8 * kSlices)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc[u] += src[static_cast<int64_t>(b + u * kSlices) * width + c];
+    for (; b < nb; b += kSlices) acc[0] += src[static_cast<int64_t>(b) * width + c];
   }
-  red[t] = (a0 + a1) + (a2 + a3);
+  red[t] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
-  if (s == 0 && c < width) {
-    float tot = 0.0f;
-    for (int k = 0; k < kSlices; ++k) tot += red[k * kCols + t];
-    out[c] = tot;
+  for (int h = kSlices / 2; h > 0; h >>= 1) {
+    if (s < h) red[t] += red[t + h * kCols];
+    __syncthreads();
   }
+  if (s == 0 && c < width) out[c] = red[t];
 }
 
 __global__ void zero_kernel(float* a, int na, float* b, int nbv) {
@@ -67,8 +69,15 @@ int zero_outputs(hipStream_t st, float* a, int na, float* b, int nbv, const char
 int launch_colsum(hipStream_t st, const float* part, int nb, int width, int quantities, float* out0, float* out1,
                   const char* who) {
   if (width <= 0) return kOk;
-  hipLaunchKernelGGL(colsum_kernel, dim3((width + 63) / 64, quantities), dim3(kColsumThreads), 0, st, part, nb,
-                     width, out0, out1);
+  // Narrow outputs over many partial rows (LayerNorm and bias gradients):
+  // 16 columns x 64 slices, so more workgroups share the rows; wide outputs
+  // (weight gradients) already have enough columns: 64 x 16.
+  if (width <= 4096 && nb >= 256)
+    hipLaunchKernelGGL(colsum_kernel<16>, dim3((width + 15) / 16, quantities), dim3(kColsumThreads), 0, st, part, nb,
+                       width, out0, out1);
+  else
+    hipLaunchKernelGGL(colsum_kernel<64>, dim3((width + 63) / 64, quantities), dim3(kColsumThreads), 0, st, part, nb,
+                       width, out0, out1);
   return check_launch(who);
 }
 

@@ -31,7 +31,8 @@ inline int colsum_blocks(int64_t n) {
   return static_cast<int>(b < 1 ? 1 : (b < 1024 ? b : 1024));
 }
 
-// Threads of the colsum_kernel workgroup (64 columns x 16 partial slices).
+// Threads of the colsum_kernel workgroup (16 or 64 columns x 64 or 16
+// partial slices).
 constexpr int kColsumThreads = 1024;
 
 template <int LPR>
@@ -82,7 +83,6 @@ __device__ __forceinline__ void block_colsum(const float (&acc)[V][W], float* ld
 // selecting one of two outputs. Each workgroup covers up to 256 columns; its
 // threads split the nb partial rows into S interleaved slices whose sums are
 // then added in slice order.
-__global__ void colsum_kernel(const float* part, int nb, int width, float* out0, float* out1);
 
 // Zero-fills a[0..na) and b[0..nbv) (b may be null): the parameter
 // gradients of an empty row set.
