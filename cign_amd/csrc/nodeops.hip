@@ -53,6 +53,37 @@ __global__ __launch_bounds__(kColsumThreads) void colsum_kernel(const float* par
   if (s == 0 && c < width) out[c] = red[t];
 }
 
+// Wide outputs over few partial rows (weight gradients): one thread per four
+// columns walks every partial row in order, eight rows in flight.
+__global__ __launch_bounds__(kBlock) void colsum_wide_kernel(const float* part, int nb, int width, float* out0,
+                                                             float* out1) {
+  const int64_t c = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 4;
+  if (c >= width) return;
+  const float* src = part + static_cast<int64_t>(blockIdx.y) * nb * width + c;
+  float* out = blockIdx.y == 0 ? out0 : out1;
+  float4 acc[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) acc[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  int b = 0;
+  for (; b + 8 <= nb; b += 8)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float4 v = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(b + u) * width);
+      acc[u].x += v.x; acc[u].y += v.y; acc[u].z += v.z; acc[u].w += v.w;
+    }
+  for (; b < nb; ++b) {
+    const float4 v = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(b) * width);
+    acc[0].x += v.x; acc[0].y += v.y; acc[0].z += v.z; acc[0].w += v.w;
+  }
+#pragma unroll
+  for (int h = 4; h > 0; h >>= 1)
+#pragma unroll
+    for (int u = 0; u < h; ++u) {
+      acc[u].x += acc[u + h].x; acc[u].y += acc[u + h].y; acc[u].z += acc[u + h].z; acc[u].w += acc[u + h].w;
+    }
+  *reinterpret_cast<float4*>(out + c) = acc[0];
+}
+
 __global__ void zero_kernel(float* a, int na, float* b, int nbv) {
   const int i = blockIdx.x * kBlock + threadIdx.x;
   if (i < na) a[i] = 0.0f;
@@ -72,7 +103,11 @@ int launch_colsum(hipStream_t st, const float* part, int nb, int width, int quan
   // Narrow outputs over many partial rows (LayerNorm and bias gradients):
   // 16 columns x 64 slices, so more workgroups share the rows; wide outputs
   // (weight gradients) already have enough columns: 64 x 16.
-  if (width <= 4096 && nb >= 256)
+  const bool vec = width % 4 == 0 && aligned16(part) && aligned16(out0) && (!out1 || aligned16(out1));
+  if (width > 4096 && nb <= 128 && vec)
+    hipLaunchKernelGGL(colsum_wide_kernel, dim3((width / 4 + kBlock - 1) / kBlock, quantities), dim3(kBlock), 0, st,
+                       part, nb, width, out0, out1);
+  else if (width <= 4096 && nb >= 256)
     hipLaunchKernelGGL(colsum_kernel<16>, dim3((width + 15) / 16, quantities), dim3(kColsumThreads), 0, st, part, nb,
                        width, out0, out1);
   else
