@@ -32,6 +32,7 @@ _SIGNATURES = {
     "cign_spmm": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "cign_spmm_fwd3": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "cign_spmm_bwd3": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "cign_spmm_fwd3_noalloc": (C.c_int, [_P, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P]),
     "cign_gat_schedule_params": (C.c_int, [_I32, _I32, _I32, _I32, _P, _P]),
     "cign_gat_fwd_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "cign_gat_fwd": (C.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _F32, _P, _P, _F32, _U64,

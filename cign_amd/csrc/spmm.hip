@@ -25,6 +25,8 @@
 // A batch's gathers are unconditional (indices clamped to a valid edge,
 // weight zero) so they all issue before the first is consumed; its size is
 // the wavefront's largest per-group edge count rounded up to a power of two.
+#include <mutex>
+
 #include "common.h"
 #include "schedule.h"
 
@@ -344,6 +346,52 @@ int spmm_dispatch(hipStream_t stream, const Sched& s, const SchedInfo& info, int
   return launch_all<T, 1>(stream, s, info, d, col, val, xt, at, yt, partial, counters);
 }
 
+__global__ __launch_bounds__(kBlock) void zero_i32_kernel(int32_t* p, int n) {
+  const int i = blockIdx.x * kBlock + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+}  // namespace
+}  // namespace cign
+
+// Scratch of cign_spmm_fwd3_noalloc: kNoAllocCounterInts int32 merge
+// counters, then the segment partial sums of multi-segment rows. Each GPU
+// the library runs on holds its own copy until the process ends. In host
+// code `scratch` names a host-side stand-in, never the device memory: host
+// code uses only the address hipGetSymbolAddress returns for the current
+// device (noalloc_scratch below).
+constexpr int64_t kNoAllocScratchBytes = 16ll << 20;
+constexpr int64_t kNoAllocCounterInts = 1ll << 18;
+constexpr int64_t kNoAllocPartialBytes = kNoAllocScratchBytes - kNoAllocCounterInts * 4;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace cign {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up once per device.
+int noalloc_scratch(const char* what, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(kHipError, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(kInvalid, "%s: device ordinal %d out of range", what, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      return set_error(kHipError, "%s: hipGetSymbolAddress(scratch) on device %d: %s", what, dev,
+                       hipGetErrorString(e));
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return kOk;
+}
+
 }  // namespace
 }  // namespace cign
 
@@ -400,6 +448,40 @@ int cign_spmm_bwd3(void* stream, int32_t dtype, int32_t n_rows, int32_t d, const
   rc = cign_spmm(stream, dtype, n_rows, d, col, val, sched, sched_info, t2, g1, t1, partial, counters);
   if (rc) return rc;
   return cign_spmm(stream, dtype, n_rows, d, col, val, sched, sched_info, t1, nullptr, gx, partial, counters);
+}
+
+// cign_spmm_fwd3 with its partial sums and merge counters in the library's
+// own per-GPU scratch, so the call allocates nothing. The counters are
+// cleared by a fill kernel on `stream` first. Calls that overlap on one GPU
+// (different streams or threads) share the scratch and race.
+int cign_spmm_fwd3_noalloc(void* stream, int32_t dtype, int32_t n_rows, int32_t d, const int32_t* col,
+                           const float* val, const int32_t* sched, const int32_t* sched_info, const void* x,
+                           void* y1, void* y2, void* y3) {
+  static const char* kWhat = "cign_spmm_fwd3_noalloc";
+  if (!sched_info) return set_error(kInvalid, "%s: null schedule header", kWhat);
+  if (d <= 0) return set_error(kInvalid, "%s: bad dense width d=%d", kWhat, d);
+  const SchedInfo info = read_info(sched_info);
+  if (info.n_seg < 0 || info.n_hrow < 0) return set_error(kInvalid, "%s: corrupt schedule header", kWhat);
+  const int64_t counter_ints = static_cast<int64_t>(info.n_hrow) + 1;
+  const int64_t partial_bytes = cign_spmm_partial_bytes(info.n_seg, d);
+  if (counter_ints > kNoAllocCounterInts || partial_bytes > kNoAllocPartialBytes) {
+    return set_error(kInvalid,
+                     "%s: this schedule needs %lld merge counters and %lld bytes of partial sums; the built-in "
+                     "scratch holds %lld counters and %lld bytes (use cign_spmm_fwd3 with caller workspace)",
+                     kWhat, static_cast<long long>(counter_ints), static_cast<long long>(partial_bytes),
+                     static_cast<long long>(kNoAllocCounterInts), static_cast<long long>(kNoAllocPartialBytes));
+  }
+  void* base = nullptr;
+  int rc = noalloc_scratch(kWhat, &base);
+  if (rc) return rc;
+  int32_t* counters = static_cast<int32_t*>(base);
+  float* partial = reinterpret_cast<float*>(static_cast<unsigned char*>(base) + kNoAllocCounterInts * 4);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nc = static_cast<int>(counter_ints);
+  hipLaunchKernelGGL(zero_i32_kernel, dim3((nc + kBlock - 1) / kBlock), dim3(kBlock), 0, st, counters, nc);
+  rc = check_launch(kWhat);
+  if (rc) return rc;
+  return cign_spmm_fwd3(stream, dtype, n_rows, d, col, val, sched, sched_info, x, y1, y2, y3, partial, counters);
 }
 
 }  // extern "C"

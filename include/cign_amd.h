@@ -78,6 +78,19 @@ int cign_spmm_bwd3(void* stream, int32_t dtype, int32_t n_rows, int32_t d, const
                    const int32_t* sched, const int32_t* sched_info, const void* g1, const void* g2, const void* g3,
                    void* t2, void* t1, void* gx, float* partial, int32_t* counters);
 
+/* cign_spmm_fwd3 without caller workspace: the partial sums and merge
+ * counters live in a 16 MiB array of the library's own (per GPU, held until
+ * the process ends), so the call allocates nothing. No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc). Limits: the
+ * schedule's n_hrow + 1 <= 262144 and cign_spmm_partial_bytes(n_seg, d) <=
+ * 15 MiB, else status 1 with the sizes in cign_last_error(). Results are
+ * bit-identical to cign_spmm_fwd3. Calls that overlap on one GPU share the
+ * scratch and race: keep them stream-ordered. */
+int cign_spmm_fwd3_noalloc(void* stream, int32_t dtype, int32_t n_rows, int32_t d, const int32_t* col,
+                           const float* val, const int32_t* sched, const int32_t* sched_info, const void* x,
+                           void* y1, void* y2, void* y3);
+
 /* ---- collapsed GAT ------------------------------------------------------- */
 
 /* Schedule geometry (light_max, seg_edges) to build the schedules of a GAT

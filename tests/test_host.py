@@ -223,3 +223,17 @@ def test_gat_schedules_pick_the_segment_floor(rng):
     assert seg(S.gat_schedule(rowptr, 0, 0, 6, 256)) == 512  # wide rows
     assert seg(S.gat_schedule(rowptr, 1, 0, 4, 16)) == 512  # backward passes
     assert S.seg_floor_for(4 * 64) == 1024 and S.seg_floor_for(4 * 512) == 512
+
+
+def test_spmm_noalloc_rejects_schedules_beyond_its_scratch():
+    """The no-allocation SpMM checks its fixed scratch size on the host, before
+    any HIP call: a schedule needing more partial sums or counters is refused
+    with the sizes in the error text."""
+    lib = _lib.load_library(require_gpu=False)
+    hdr = np.zeros(12, dtype=np.int32)
+    hdr[0], hdr[1], hdr[2] = 10, 1_000_000, 10  # 10^6 segments x 512 columns of fp32 partials
+    rc = lib.cign_spmm_fwd3_noalloc(None, 0, 20, 512, None, None, None, hdr.ctypes.data, None, None, None, None)
+    assert rc == 1 and b"scratch holds" in lib.cign_last_error()
+    hdr[1], hdr[2] = 1, 300_000  # more merge counters than the scratch holds
+    rc = lib.cign_spmm_fwd3_noalloc(None, 0, 300_010, 4, None, None, None, hdr.ctypes.data, None, None, None, None)
+    assert rc == 1 and b"262144 counters" in lib.cign_last_error()
