@@ -357,9 +357,16 @@ def prepare_fixed_csr_operator(operator: torch.Tensor) -> FixedCSRGraphOperator:
         raise TypeError("FixedCSRSpMM expects a sparse COO or sparse CSR graph operator; "
                         f"got layout={operator.layout}.")
     csr = _clone_csr_storage(coo.to_sparse_csr())
-    idx_t = coo.indices().flip(0).contiguous()
-    coo_t = torch.sparse_coo_tensor(idx_t, coo.values(), size=(coo.size(1), coo.size(0)), dtype=coo.dtype,
-                                    device=coo.device).coalesce()
+    # P^T: the flipped indices of a coalesced tensor are distinct, so
+    # coalescing them is a stable sort by (column, row) with nothing to sum.
+    # One key sort does it, in a fraction of sparse coalesce()'s time on the
+    # host (62M entries: 1 s against 20 s), with the same result.
+    idx = coo.indices()
+    n_rows = max(int(coo.size(0)), 1)
+    order = torch.sort(idx[1] * n_rows + idx[0], stable=True).indices
+    idx_t = idx.flip(0)[:, order].contiguous()
+    coo_t = torch.sparse_coo_tensor(idx_t, coo.values()[order], size=(coo.size(1), coo.size(0)), dtype=coo.dtype,
+                                    device=coo.device, is_coalesced=True)
     csr_t = _clone_csr_storage(coo_t.to_sparse_csr())
     return FixedCSRGraphOperator(csr=csr, csr_t=csr_t)
 
