@@ -351,7 +351,11 @@ __device__ __forceinline__ void epilogue_swapped(const GemmArgs& g, f32x4 (&acc)
     const bool full4 = g.vec4 && nb + 4 <= g.N;
     float bv[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) bv[q] = (g.bias && nb + q < g.N) ? g.bias[nb + q] : 0.0f;
+    for (int q = 0; q < 4; ++q) {
+      // Autocast casts the bias to bf16 with the other operands.
+      const float b = (g.bias && nb + q < g.N) ? g.bias[nb + q] : 0.0f;
+      bv[q] = g.round_bf16 ? round_bf16(b) : b;
+    }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int64_t m = row0 + 16 * r + (lane & 15);

@@ -5,7 +5,7 @@ GEMM epilogue. Drop-in for the reference's ``_local_amp_linear``
 follow its calls in the block:
 
 * ``mfma_linear(linear, x, amp, amp_dtype)``: ``y = x W^T + b`` returned as
-  float32. With ``amp`` (the reference's local bf16 autocast) the inputs are
+  float32. With ``amp`` (the reference's local bf16 autocast) x, W and b are
   rounded to bf16 in registers, the products run on bf16 MFMA with fp32
   accumulation and the output is rounded to bf16 (autocast's output dtype)
   before it is returned as float32; without it the GEMM is exact fp32 MFMA.

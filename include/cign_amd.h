@@ -315,8 +315,8 @@ int cign_pack_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t interac
 /* ---- dense projections on MFMA ------------------------------------------ */
 
 /* math: 0 = float32 (fp32 MFMA, exact fp32 products), 1 = bf16 autocast
- * (inputs rounded to bf16, bf16 MFMA with fp32 accumulation, output rounded to
- * bf16 and stored as float32). x [M,K] float32 or bfloat16 (x_dtype; bf16
+ * (x, weight and bias rounded to bf16, bf16 MFMA with fp32 accumulation,
+ * output rounded to bf16 and stored as float32). x [M,K] float32 or bfloat16 (x_dtype; bf16
  * needs math 1), weight [N,K] float32 (nn.Linear layout), bias [N] or NULL.
  * Any M, N, K; rows that start 16-byte aligned are read with vector loads. */
 

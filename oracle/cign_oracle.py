@@ -373,6 +373,103 @@ def collapsed_gat_backward(attn_row, attn_col, rowptr, col, slope, x, bias, grad
             "grad_pre": g_pre, "grad_raw": g_raw}
 
 
+def _sub_rows(rowptr, rows):
+    """Row pointer [len(rows)+1] and CSR edge ids of the given rows."""
+    rows = np.asarray(rows, dtype=np.int64)
+    deg = rowptr[rows + 1] - rowptr[rows]
+    sub = np.zeros(len(rows) + 1, dtype=np.int64)
+    sub[1:] = np.cumsum(deg)
+    start = np.repeat(rowptr[rows] - sub[:-1], deg)
+    return sub, start + np.arange(sub[-1], dtype=np.int64)
+
+
+def _rows_softmax_agg(attn_row, attn_col, rowptr, col, slope, x, rows):
+    """Softmax statistics and the aggregates sum_e s x[j] and sum_e s l' x[j]
+    ([R,H,C]) of the given destination rows, over their complete in-edge
+    lists, with the edge arrays of those rows only (no [E,C] gathers)."""
+    x = np.asarray(x, dtype=np.float64)
+    n, H, C = x.shape
+    sub, eid = _sub_rows(rowptr, rows)
+    cols = np.asarray(col, dtype=np.int64)[eid]
+    ar = np.asarray(attn_row, np.float64)[np.asarray(rows, dtype=np.int64)]
+    # Local destinations 0..R-1 over the sources' global ids.
+    raw, soft, emax, esum = gat_softmax(ar, np.asarray(attn_col, np.float64), sub, cols, slope)
+    lp = np.where(raw < 0, slope, 1.0)
+    R = len(sub) - 1
+    agg = np.zeros((R, H, C))
+    agg_l = np.zeros((R, H, C))
+    for h in range(H):
+        agg[:, h, :] = sp.csr_matrix((soft[:, h], cols, sub), shape=(R, n)) @ x[:, h, :]
+        agg_l[:, h, :] = sp.csr_matrix((soft[:, h] * lp[:, h], cols, sub), shape=(R, n)) @ x[:, h, :]
+    return dict(sub=sub, cols=cols, raw=raw, soft=soft, lp=lp, emax=emax, esum=esum, agg=agg, agg_l=agg_l)
+
+
+def collapsed_gat_forward_rows(attn_row, attn_col, rowptr, col, slope, x, bias, rows):
+    """collapsed_gat_forward (p = 0) evaluated at the given destination rows
+    only: each row's output needs only its own in-edges, so the cost is that
+    of those rows' edges (for full-size graphs). Returns dict(out, pre, emax,
+    esum) of shape [len(rows), ...]. Pinned against collapsed_gat_forward on
+    graphs with hubs and empty rows (tests)."""
+    H = np.asarray(x).shape[1]
+    r = _rows_softmax_agg(attn_row, attn_col, rowptr, col, slope, x, rows)
+    pre = r["agg"].sum(axis=1) / H + np.asarray(bias, dtype=np.float64)
+    return {"out": _silu(pre), "pre": pre, "emax": r["emax"], "esum": r["esum"]}
+
+
+def collapsed_gat_backward_columns(attn_row, attn_col, rowptr, col, slope, x, bias, grad_y, cols):
+    """collapsed_gat_backward (p = 0) evaluated at the given source columns:
+    grad_feat and grad_attn_col of those columns, plus grad_attn_row and
+    grad_pre of every destination row that reads one of them. The rows that
+    read a column are found by scanning `col`; their complete in-edge lists
+    give the softmax, pre and grad_pre; then, with g = grad_pre[i],
+      wsum[i,h]  = <g, sum_e s x[j_e,h]>/H,
+      g_raw[e,h] = l'_e s_e (<g, x[j_e,h]>/H - wsum[i,h]),
+      grad_attn_row[i,h] = <g, sum_e s l' x[j_e,h]>/H - wsum[i,h] sum_e s l',
+    and each requested column sums s g/H (grad_feat) and g_raw (grad_attn_col)
+    over its edges. Returns dict(cols, grad_feat [J,H,C], grad_attn_col [J,H],
+    rows, grad_attn_row [R,H], grad_pre [R,C]). Pinned against
+    collapsed_gat_backward on graphs with hubs and empty rows (tests)."""
+    x = np.asarray(x, dtype=np.float64)
+    n, H, C = x.shape
+    cols = np.asarray(cols, dtype=np.int64)
+    col = np.asarray(col, dtype=np.int64)
+    want = np.zeros(n, dtype=bool)
+    want[cols] = True
+    all_rows = np.repeat(np.arange(n, dtype=np.int64), np.diff(rowptr))
+    rows = np.unique(all_rows[want[col]])
+    r = _rows_softmax_agg(attn_row, attn_col, rowptr, col, slope, x, rows)
+    pre = r["agg"].sum(axis=1) / H + np.asarray(bias, dtype=np.float64)
+    g_pre = np.asarray(grad_y, dtype=np.float64)[rows] * _silu_grad(pre)
+    wsum = np.einsum("rc,rhc->rh", g_pre, r["agg"]) / H
+    b_l = _segment_reduce(np.add, r["soft"] * r["lp"], r["sub"], 0.0)
+    g_row = np.einsum("rc,rhc->rh", g_pre, r["agg_l"]) / H - wsum * b_l
+    # Edges of those rows whose source is a requested column.
+    local = np.repeat(np.arange(len(rows), dtype=np.int64), np.diff(r["sub"]))
+    hit = np.nonzero(want[r["cols"]])[0]
+    ei, ej = local[hit], r["cols"][hit]
+    s, lp = r["soft"][hit], r["lp"][hit]
+    dot = np.einsum("ec,ehc->eh", g_pre[ei], x[ej]) / H
+    g_raw = lp * s * (dot - wsum[ei])
+    slot = np.searchsorted(np.sort(cols), ej)
+    order = np.argsort(cols)
+    g_feat = np.zeros((len(cols), H, C))
+    g_col = np.zeros((len(cols), H))
+    np.add.at(g_feat, order[slot], s[:, :, None] * g_pre[ei][:, None, :] / H)
+    np.add.at(g_col, order[slot], g_raw)
+    return {"cols": cols, "grad_feat": g_feat, "grad_attn_col": g_col, "rows": rows, "grad_attn_row": g_row,
+            "grad_pre": g_pre}
+
+
+def spmm_rows(rowptr, col, val, x, rows, add=None):
+    """Rows `rows` of spmm(rowptr, col, val, x, add) from those rows' edges."""
+    sub, eid = _sub_rows(rowptr, rows)
+    n_src = np.asarray(x).shape[0]
+    m = sp.csr_matrix((np.asarray(val, np.float64)[eid], np.asarray(col, np.int64)[eid], sub),
+                      shape=(len(sub) - 1, n_src))
+    y = m @ np.asarray(x, dtype=np.float64)
+    return y if add is None else y + np.asarray(add, np.float64)[np.asarray(rows, dtype=np.int64)]
+
+
 def collapsed_gat_row_aggregates(attn_row, attn_col, rowptr, col, slope, x, p=0.0, keep=None):
     """Per-destination-row aggregates the feature-layout forward saves for its
     backward (no reference counterpart; they regroup the sums of

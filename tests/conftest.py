@@ -56,3 +56,42 @@ def random_gat_graph(rng, n, avg_deg=6, hubs=None):
     ei = O.gat_edge_index(np.stack([np.array(src, dtype=np.int64), np.array(dst, dtype=np.int64)]), n)
     r, c, _ = O.coalesce(ei[0], ei[1], n)
     return np.stack([r, c])
+
+
+def assert_close_fp32_derived(actual, expected64, expected32, name="", rtol=1e-4, atol=1e-5, k=4.0):
+    """Tolerance for float32 results that sum over many nodes (parameter
+    gradients): |a - e64| <= atol + rtol |e64| + k |e32 - e64| elementwise,
+    where e32 is the same oracle computation carried out in float32 on the
+    same inputs. |e32 - e64| is the rounding error float32 arithmetic incurs
+    on exactly this computation; k allows for a different summation order."""
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected64, dtype=np.float64)
+    e32 = np.asarray(expected32, dtype=np.float64)
+    assert a.shape == e.shape == e32.shape, f"{name}: shapes {a.shape} {e.shape} {e32.shape}"
+    bound = atol + rtol * np.abs(e) + k * np.abs(e32 - e)
+    err = np.abs(a - e)
+    bad = err > bound
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - bound), a.shape)
+        raise AssertionError(f"{name}: {int(bad.sum())} of {a.size} outside the fp32-derived bound; worst at {i}: "
+                             f"got {a[i]!r} expected {e[i]!r} (fp32 oracle {e32[i]!r}, bound {bound[i]!r})")
+
+
+def colsum_atol(terms_abs_sum, n_rows):
+    """Absolute error bound of a float32 sum over n_rows rows whose terms have
+    the given sum of magnitudes (per output element): the kernels add rows in
+    chunks and then the chunk partials in order, so the longest chain of
+    dependent float32 additions is at most about 2 sqrt(n) + 8 long, each
+    adding at most 2^-24 of the running magnitude; plus 1e-5 absolute."""
+    return 1e-5 + (2.0 * np.sqrt(max(int(n_rows), 1)) + 8.0) * 2.0 ** -24 * np.asarray(terms_abs_sum, np.float64)
+
+
+def bf16_flip_atol(expected):
+    """Extra absolute tolerance of a selective-bf16 result compared with an
+    oracle that rounds to bf16 at the same points: where fp32 (GPU) and fp64
+    (oracle) accumulation put a value on different sides of a bf16 rounding
+    boundary, that value differs by one bf16 ulp, at most 2^-7 of the largest
+    magnitude in its tensor, and the difference carries on to everything
+    computed from it (which may cancel to far smaller values)."""
+    e = np.asarray(expected, dtype=np.float64)
+    return 2.0 ** -7 * (float(np.abs(e).max()) if e.size else 0.0)

@@ -1,0 +1,198 @@
+"""Full-size c5: Chung-Lu graph of 2.4M nodes and 62.4M
+edges (exponent 2.2, hubs of ~44.6K in-edges), hidden 128 as GAT 4 heads x
+32 channels, K=3 hops. The whole-graph oracle does not fit here, so the HIP
+layer is checked by
+  * size-independent properties: P sqrt(deg) = sqrt(deg) through forward3
+    and backward3 (P = D^-1/2 (A+I) D^-1/2, symmetric); the adjoint identity
+    sum_k <y_k, g_k> = <x, grad_x>; constant features give pre = 1 + bias
+    and zero attention gradients;
+  * the oracle at sampled rows and columns (cign_oracle.*_rows / *_columns,
+    pinned against the whole-graph oracle): every hop's rows (hubs
+    included) from that hop's own input, the GAT forward at the three
+    largest hubs (three 16,384-edge segments each) and 200 random rows, the
+    GAT backward at a two-segment hub column, two mid-degree columns and 100
+    random columns, and grad_bias against the sum of grad_y SiLU'(pre).
+Tolerances: fp32 1e-4 rel / 1e-5 abs; bf16 2e-2 (inputs rounded to bf16
+first; the oracle runs on the rounded values)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cign_oracle as O
+from tests.conftest import assert_close
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
+
+F32_TOL = dict(rtol=1e-4, atol=1e-5)
+BF16_TOL = dict(rtol=2e-2, atol=2e-2)
+SLOPE = 0.2
+
+
+def _say(request, msg):
+    """Progress line on the real stdout, past pytest's output capture (the
+    graph build and the sampled oracle take tens of seconds each)."""
+    capman = request.config.pluginmanager.getplugin("capturemanager")
+    if capman is None:
+        print(f"[c5] {msg}", flush=True)
+        return
+    with capman.global_and_fixture_disabled():
+        print(f"[c5] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def c5(request):
+    import time
+
+    from cign_amd import workloads
+
+    t0 = time.perf_counter()
+    _say(request, "building the 2.4M-node / 62.4M-edge graph on the host (about a minute)")
+    w = workloads.build(workloads.C5, device="cuda")
+    (rowptr, col), (row, colptr), perm = w.gat_graph
+    host = {"rowptr": rowptr.cpu().numpy().astype(np.int64), "col": col.cpu().numpy().astype(np.int64),
+            "colptr": colptr.cpu().numpy().astype(np.int64)}
+    csr, csr_t = w.operator.csr, w.operator.csr_t
+    host["p"] = (csr.crow_indices().cpu().numpy().astype(np.int64), csr.col_indices().cpu().numpy().astype(np.int64),
+                 csr.values().cpu().numpy().astype(np.float64))
+    host["pt"] = (csr_t.crow_indices().cpu().numpy().astype(np.int64),
+                  csr_t.col_indices().cpu().numpy().astype(np.int64), csr_t.values().cpu().numpy().astype(np.float64))
+    _say(request, f"graph ready in {time.perf_counter() - t0:.0f} s: n={w.n} nnz={w.nnz_gat}")
+    return w, host
+
+
+def _rand(shape, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(dtype).cuda()
+
+
+def _np(t):
+    return t.detach().double().cpu().numpy()
+
+
+def _sample_rows(host, k, seed):
+    n = len(host["rowptr"]) - 1
+    rng = np.random.default_rng(seed)
+    return np.unique(np.concatenate([[0, 1, 2], rng.choice(n, k, replace=False)]))
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 256), (torch.float32, 128)])
+def test_c5_multihop_fixed_point_and_sampled_rows(request, c5, dtype, d):
+    from cign_amd.graph import _hip_parts
+    from cign_amd.multihop_csr_pipeline import MultiHopCSR3GraphOperator
+
+    w, host = c5
+    _say(request, f"multihop {dtype} D={d}: fixed point, sampled rows of every hop")
+    tol = F32_TOL if dtype == torch.float32 else BF16_TOL
+    plan = MultiHopCSR3GraphOperator(w.operator, dense_cols=d, dense_dtype=dtype).plan
+    deg = torch.diff(w.operator.csr.crow_indices()).double()
+    xs = deg.sqrt()[:, None].expand(w.n, d).contiguous().to(dtype)
+    ref = xs.double()
+    for k, y in enumerate(plan.forward3(xs)):
+        err = float(((y.double() - ref).abs() - tol["rtol"] * ref.abs()).max())
+        assert err <= tol["atol"], f"P^{k + 1} sqrt(deg) != sqrt(deg): excess {err}"
+    z = torch.zeros_like(xs)
+    gx = plan.backward3(z, z, xs)
+    assert float(((gx.double() - ref).abs() - tol["rtol"] * ref.abs()).max()) <= tol["atol"]
+    # Random inputs: each hop's sampled rows from that hop's own (stored) input.
+    rows = _sample_rows(host, 300, 7)
+    x = _rand((w.n, d), dtype, 1)
+    y1, y2, y3 = plan.forward3(x)
+    g1, g2, g3 = (_rand((w.n, d), dtype, 2 + k) for k in range(3))
+    gxr = plan.backward3(g1, g2, g3)
+    p, pt = host["p"], host["pt"]
+    for name, out, inp in (("y1", y1, x), ("y2", y2, y1), ("y3", y3, y2)):
+        assert_close(_np(out[rows]), O.spmm_rows(*p, _np(inp), rows), name=name, **tol)
+    if dtype == torch.float32:
+        # backward3 = P^T applied three times with the adds; by the adjoint
+        # identity (fp64 sums of the fp32 results).
+        lhs = sum(float((yk.double() * gk.double()).sum()) for yk, gk in zip((y1, y2, y3), (g1, g2, g3)))
+        rhs = float((x.double() * gxr.double()).sum())
+        assert abs(lhs - rhs) <= 1e-4 * abs(lhs), (lhs, rhs)
+    # backward3 against its three hops run one by one on P^T (cign_spmm),
+    # each hop's sampled rows checked from that hop's own input.
+    ht = _hip_parts(w.operator.csr_t)
+    t2 = ht.spmm(g3, add=g2)
+    t1 = ht.spmm(t2, add=g1)
+    gx1 = ht.spmm(t1)
+    for name, out, inp, add in (("t2", t2, g3, g2), ("t1", t1, t2, g1), ("gx", gx1, t1, None)):
+        assert_close(_np(out[rows]), O.spmm_rows(*pt, _np(inp), rows, add=None if add is None else _np(add)),
+                     name=name, **tol)
+    excess = float(((gxr.double() - gx1.double()).abs() - tol["rtol"] * gx1.double().abs()).max())
+    assert excess <= tol["atol"], f"backward3 differs from its hop chain: excess {excess}"
+
+
+def test_c5_gat_constant_features(request, c5):
+    from cign_amd.collapsed_gat import ensure_collapsed_gat_loaded
+
+    w, _ = c5
+    _say(request, "GAT bf16 4x32: constant features")
+    (rowptr, col), (row, colptr), perm = w.gat_graph
+    ext = ensure_collapsed_gat_loaded()
+    ones = torch.ones(w.n, 4, 32, device="cuda", dtype=torch.bfloat16)
+    ar, ac, bias = _rand((w.n, 4), torch.float32, 11), _rand((w.n, 4), torch.float32, 12), _rand((32,), torch.float32, 13)
+    gy = _rand((w.n, 32), torch.bfloat16, 14)
+    (out, pre, emax, esum, mask), agg = ext.forward_agg(ar, ac, rowptr, col, SLOPE, ones, bias, 0.0, 0, True)
+    assert_close(_np(pre), np.broadcast_to(1.0 + _np(bias), (w.n, 32)), name="pre", **F32_TOL)
+    gf, gar, gac, gb = ext.backward(SLOPE, 0.0, rowptr, col, colptr, row, perm, emax, esum, mask, ones, ar, ac, pre,
+                                    gy, agg)
+    scale = float(gf.float().abs().max())
+    assert float(gar.abs().max()) <= 1e-4 * scale and float(gac.abs().max()) <= 1e-4 * scale
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_c5_gat_sampled_rows_and_columns_match_oracle(request, c5, dtype):
+    from cign_amd.collapsed_gat import ensure_collapsed_gat_loaded
+    from cign_amd.schedule import gat_schedule
+
+    w, host = c5
+    H, C = 4, 32
+    tol = F32_TOL if dtype == torch.float32 else BF16_TOL
+    (rowptr, col), (row, colptr), perm = w.gat_graph
+    ext = ensure_collapsed_gat_loaded()
+    x = _rand((w.n, H, C), dtype, 21)
+    ar, ac, bias = _rand((w.n, H), torch.float32, 22), _rand((w.n, H), torch.float32, 23), _rand((C,), torch.float32, 24)
+    gy = _rand((w.n, C), dtype, 25)
+    code = 0 if dtype == torch.float32 else 1
+    seg_fwd = int(gat_schedule(rowptr, 0, code, H, C).header[3])
+    seg_bwd = int(gat_schedule(colptr, 1, code, H, C).header[3])
+    cdeg = np.diff(host["colptr"])
+    two_seg = int(np.nonzero((cdeg > seg_bwd) & (cdeg <= 2 * seg_bwd))[0][-1])
+    assert np.diff(host["rowptr"])[0] > 2 * seg_fwd, "the top hub must span three forward segments"
+    _say(request, f"GAT {dtype}: forward/backward on the GPU (segments {seg_fwd}/{seg_bwd}; two-segment column "
+                  f"{two_seg} of degree {cdeg[two_seg]})")
+    (out, pre, emax, esum, mask), agg = ext.forward_agg(ar, ac, rowptr, col, SLOPE, x, bias, 0.0, 0, True)
+    grads_agg = ext.backward(SLOPE, 0.0, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar, ac, pre, gy, agg)
+    grads_gather = ext.backward(SLOPE, 0.0, rowptr, col, colptr, row, perm, emax, esum, mask, x, ar, ac, pre, gy,
+                                None)
+    torch.cuda.synchronize()
+
+    xs, ars, acs, bs, gys = _np(x).reshape(w.n, H, C), _np(ar), _np(ac), _np(bias), _np(gy)
+    rows = _sample_rows(host, 200, 31)
+    _say(request, f"oracle forward at {len(rows)} rows (three hubs)")
+    f = O.collapsed_gat_forward_rows(ars, acs, host["rowptr"], host["col"], SLOPE, xs, bs, rows)
+    assert_close(_np(pre[rows]), f["pre"], name="pre", **tol)
+    assert_close(_np(out[rows]), f["out"], name="out", **tol)
+    assert_close(_np(emax[rows]), f["emax"], name="edge_max", **F32_TOL)
+    assert_close(_np(esum[rows]), f["esum"], name="edge_sum", **F32_TOL)
+
+    rng = np.random.default_rng(32)
+    cols = np.unique(np.concatenate([[two_seg, 1000, 3000], rng.choice(w.n, 100, replace=False)]))
+    _say(request, f"oracle backward at {len(cols)} columns (their 2-hop rows)")
+    gc = O.collapsed_gat_backward_columns(ars, acs, host["rowptr"], host["col"], SLOPE, xs, bs, gys, cols)
+    _say(request, f"oracle done: {len(gc['rows'])} rows read those columns")
+    pre_np = _np(pre)
+    sig = 1.0 / (1.0 + np.exp(-pre_np))
+    g_pre_gpu = gys * sig * (1.0 + pre_np * (1.0 - sig))
+    bias_ref = g_pre_gpu.sum(axis=0)
+    # fp32 summation of 2.4M terms: bound the error by 1e-5 of the sum of
+    # magnitudes per channel (a tree sum of n terms errs by at most
+    # ~log2(n) * 6e-8 of it).
+    bias_atol = 1e-5 * np.abs(g_pre_gpu).sum(axis=0)
+    for label, (gf, gar, gac, gb) in (("agg", grads_agg), ("gather", grads_gather)):
+        assert_close(_np(gf[cols]), gc["grad_feat"], name=f"{label} grad_feat", **tol)
+        assert_close(_np(gac[cols]), gc["grad_attn_col"], name=f"{label} grad_attn_col", **tol)
+        assert_close(_np(gar[gc["rows"]]), gc["grad_attn_row"], name=f"{label} grad_attn_row", **tol)
+        # grad_bias = sum_n grad_y SiLU'(pre): the 2.4M-row reduction against
+        # fp64 sums over the GPU's own pre (checked at the sampled rows above).
+        err = np.abs(_np(gb) - bias_ref)
+        assert (err <= bias_atol + 1e-4 * np.abs(bias_ref)).all(), f"{label} grad_bias: {err.max()}"

@@ -183,6 +183,42 @@ def test_gat_dense_textbook_single_head(rng):
     assert_close(got["out"], pre / (1 + np.exp(-pre)), 1e-12, 1e-12, "out")
 
 
+def test_gat_sampled_rows_and_columns_match_full_oracle(rng):
+    """The row-sampled forward and column-sampled backward (used at full
+    size, where the whole-graph oracle does not fit) equal the whole-graph
+    oracle at the sampled rows/columns, including hubs, rows with empty
+    in-lists (rowptr plateaus) and columns no row reads."""
+    n, H, C = 160, 3, 5
+    d = _gat_inputs(rng, n, H, C, hubs={4: 120, 9: 90})
+    rp, cl = d["rowptr"].copy(), d["col"].copy()
+    # Empty rows 20..23: drop their edges.
+    keep = ~np.isin(np.repeat(np.arange(n), np.diff(rp)), [20, 21, 22, 23])
+    rows_all = np.repeat(np.arange(n), np.diff(rp))[keep]
+    cl = cl[keep]
+    rp = np.concatenate([[0], np.cumsum(np.bincount(rows_all, minlength=n))])
+    gy = rng.standard_normal((n, C))
+    f = O.collapsed_gat_forward(d["ar"], d["ac"], rp, cl, 0.2, d["x"], d["b"])
+    g = O.collapsed_gat_backward(d["ar"], d["ac"], rp, cl, 0.2, d["x"], d["b"], gy)
+    rows = np.array([4, 9, 0, 21, 37, 159, 100])
+    fr = O.collapsed_gat_forward_rows(d["ar"], d["ac"], rp, cl, 0.2, d["x"], d["b"], rows)
+    for k in ("out", "pre", "emax", "esum"):
+        assert_close(fr[k], f[k][rows], 1e-12, 1e-12, k)
+    unread = np.setdiff1d(np.arange(n), cl)
+    cols = np.array([9, 4, 55, 0, 158] + ([int(unread[0])] if unread.size else []))
+    gc = O.collapsed_gat_backward_columns(d["ar"], d["ac"], rp, cl, 0.2, d["x"], d["b"], gy, cols)
+    assert_close(gc["grad_feat"], g["grad_feat"][cols], 1e-12, 1e-12, "grad_feat")
+    assert_close(gc["grad_attn_col"], g["grad_attn_col"][cols], 1e-12, 1e-12, "grad_attn_col")
+    assert_close(gc["grad_attn_row"], g["grad_attn_row"][gc["rows"]], 1e-12, 1e-12, "grad_attn_row")
+    assert_close(gc["grad_pre"], g["grad_pre"][gc["rows"]], 1e-12, 1e-12, "grad_pre")
+    assert set(gc["rows"].tolist()) == set(np.repeat(np.arange(n), np.diff(rp))[np.isin(cl, cols)].tolist())
+    # Row-sampled SpMM.
+    val = rng.standard_normal(len(cl))
+    X = rng.standard_normal((n, 7))
+    A = rng.standard_normal((n, 7))
+    assert_close(O.spmm_rows(rp, cl, val, X, rows, add=A), O.spmm(rp, cl, val, X, add=A)[rows], 1e-12, 1e-12,
+                 "spmm_rows")
+
+
 def test_gat_closed_forms(rng):
     n, H, C = 20, 3, 4
     d = _gat_inputs(rng, n, H, C)
@@ -553,3 +589,24 @@ def test_net_oracle_closed_forms():
     h = F.silu(x @ g["input_proj_0.weight"].T + g["input_proj_0.bias"])
     z = F.layer_norm(h, (D,), g2["output_norm.weight"], g2["output_norm.bias"], 1e-5)
     assert torch.allclose(got2, z @ g2["classifier.weight"].T + g["classifier.bias"], rtol=1e-10, atol=1e-10)
+
+
+def test_block_oracle_amp_linear_matches_autocast_rounding_points():
+    """block_oracle._AmpLinear (the selective-AMP projections of the block and
+    net oracles) equals the pinned O.linear_forward(amp=True) forward and the
+    bf16-operand O.linear_backward, in float64."""
+    import torch
+
+    from oracle import block_oracle as B
+
+    rng = np.random.default_rng(9)
+    x, w, b = rng.standard_normal((37, 19)), rng.standard_normal((11, 19)), rng.standard_normal(11)
+    gy = rng.standard_normal((37, 11))
+    xt, wt, bt = (torch.from_numpy(v).requires_grad_() for v in (x, w, b))
+    y = B._AmpLinear.apply(xt, wt, bt)
+    assert np.array_equal(y.detach().numpy(), O.linear_forward(x, w, b, amp=True))
+    y.backward(torch.from_numpy(gy))
+    gx, gw, _ = O.linear_backward(O.bf16_round(gy), O.bf16_round(x), O.bf16_round(w))
+    assert_close(xt.grad.numpy(), gx, 1e-12, 1e-12, "grad x")
+    assert_close(wt.grad.numpy(), gw, 1e-12, 1e-12, "grad w")
+    assert_close(bt.grad.numpy(), gy.sum(0), 1e-12, 1e-12, "grad b")
