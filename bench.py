@@ -14,11 +14,18 @@ of the step captured as a HIP graph, or with --eager the four drop-in API
 calls). The roofline object is computed for the dominant kernel from HIP
 events recorded on the launch stream in a second timed region, where each
 phase is launched back to back (captured as one graph of 20 launches and
-replayed), which is the per-kernel average rocprofv3 reports. The CPU
-baseline times the numpy oracle on the host (a bounded sample of the same
-workload).
+replayed), which is the per-kernel average rocprofv3 reports.
+The same run then adds
+  * cpu_baseline: the reference's CPU path on the same layer (float32 torch
+    on the host's cores, oracle/cpu_path.py), a bounded sample;
+  * cpu_baseline_c1 / c1_gpu: BASELINE config 1, the full 2-layer model's
+    training step on the host and on the GPU;
+  * scale: the layer at BASELINE config 5 (2.4M nodes, 62.4M edges, GAT 4 x
+    32 + SpMM D=256, bf16, eager launches) with its roofline and full-size
+    invariants (--no-scale skips it).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--eager] [--dtype f32|bf16]
+                       [--no-scale] [--workload layer|scale|block|train]
 """
 from __future__ import annotations
 
@@ -40,13 +47,16 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 disables)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="bounded sample of each CPU baseline, seconds (0 disables)")
     ap.add_argument("--workload", choices=["layer", "scale", "block", "train"], default="layer",
                     help="layer: the headline c2+c3 layer (24,492 nodes); scale: the same layer at c5 size "
                          "(2.4M nodes, ~62M edges, GAT 4x32 + SpMM D=256, bf16 by default); block: the full "
                          "Clifford block forward+backward at the production shape (D=256, 6 GAT heads, hops 1-3) "
                          "with every component kernel timed against its own roofline (bf16 = selective AMP GEMMs)")
     ap.add_argument("--dtype", choices=["f32", "bf16"], default=None)
+    ap.add_argument("--no-scale", action="store_true",
+                    help="default workload: skip the c5 measurement that follows the headline c2+c3 layer")
     ap.add_argument("--eager", action="store_true",
                     help="launch every step through the Python drop-in API instead of replaying it as a HIP graph")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -56,53 +66,30 @@ def parse():
 
 
 def cpu_baseline(w, seconds: float, H: int, C: int, D: int):
-    """Times the numpy oracle (single thread) on the same c2/c3 layer."""
-    import numpy as np
+    """The reference's CPU path on the same c2+c3 layer (oracle/cpu_path.py:
+    float32 torch, GATConv-style scatter softmax and torch.sparse.mm hops,
+    autograd backward) on the host's cores, timed for about `seconds`:
+    median step time after 3 warmup steps (backend_autotune_cign.py:228-229)."""
+    import torch
 
+    from oracle import cpu_path
+
+    threads = cpu_path.host_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
     try:
-        from threadpoolctl import threadpool_limits
-    except Exception:  # pragma: no cover
-        threadpool_limits = None
-    from oracle import cign_oracle as O
-
-    (rowptr, col), _, _ = w.gat_graph
-    rp, cl = rowptr.cpu().numpy().astype(np.int64), col.cpu().numpy().astype(np.int64)
-    n = w.n
-    rng = np.random.default_rng(0)
-    x = rng.standard_normal((n, H, C)).astype(np.float32)
-    ar, ac = rng.standard_normal((n, H)).astype(np.float32), rng.standard_normal((n, H)).astype(np.float32)
-    b, gy = rng.standard_normal(C).astype(np.float32), rng.standard_normal((n, C)).astype(np.float32)
-    csr, csr_t = w.operator.csr, w.operator.csr_t
-    p = (csr.crow_indices().cpu().numpy(), csr.col_indices().cpu().numpy(), csr.values().cpu().numpy())
-    pt = (csr_t.crow_indices().cpu().numpy(), csr_t.col_indices().cpu().numpy(), csr_t.values().cpu().numpy())
-    X = rng.standard_normal((n, D)).astype(np.float32)
-    G = [rng.standard_normal((n, D)).astype(np.float32) for _ in range(3)]
-
-    def one():
-        O.collapsed_gat_forward(ar, ac, rp, cl, 0.2, x, b)
-        O.collapsed_gat_backward(ar, ac, rp, cl, 0.2, x, b, gy)
-        O.multihop3_forward(p, X)
-        O.multihop3_backward(pt, *G)
-
-    ctx = threadpool_limits(limits=1) if threadpool_limits else None
-    try:
-        if ctx:
-            ctx.__enter__()
-        one()  # warmup
-        t0 = time.perf_counter()
-        k = 0
-        while True:
-            one()
-            k += 1
-            if time.perf_counter() - t0 >= seconds:
-                break
-        dt = time.perf_counter() - t0
+        (rowptr, col), _, _ = w.gat_graph
+        csr, csr_t = w.operator.csr, w.operator.csr_t
+        host = lambda c: (c.crow_indices().cpu().numpy(), c.col_indices().cpu().numpy(), c.values().cpu().numpy())
+        layer = cpu_path.LayerCPU(rowptr.cpu().numpy(), col.cpu().numpy(), host(csr), host(csr_t), w.n, H, C, D)
+        med, k = cpu_path.time_steps(layer.step, seconds)
     finally:
-        if ctx:
-            ctx.__exit__(None, None, None)
-    return {"value": w.nnz_gat * k / dt, "unit": "edges/s", "cores": 1, "kind": "port",
-            "sample": f"{k} full c2+c3 layer fwd+bwd steps of the numpy/scipy oracle (float64) in {dt:.1f} s, "
-                      f"1 thread"}
+        torch.set_num_threads(prev)
+    return {"value": w.nnz_gat / med, "unit": "edges/s", "cores": threads, "kind": "port",
+            "ms_per_step": round(1e3 * med, 3),
+            "sample": f"median of {k} c2+c3 layer fwd+bwd steps (GAT {H}x{C} + 3 hops D={D}) of the reference's CPU "
+                      f"path restated in float32 torch (GATConv scatter softmax, torch.sparse.mm, autograd), "
+                      f"{threads} threads"}
 
 
 def invariants(torch, w, ext, plan, H, C, D, dt):
@@ -299,17 +286,18 @@ def time_components(comps: dict, dtype: str, torch):
 
 def cpu_train_baseline(seconds: float, torch):
     """The reference's CPU case (BASELINE config c1): the full CIGN model
-    forward + cross-entropy + backward + Adam step, restated in float64 torch
-    on the host (oracle/block_oracle.net_forward; the torch/PyG fallback
-    path of the reference, eval-mode numerics), on N=2000 nodes with
-    out-degree 8 uniform-random edges (symmetrised, as the reference's
-    default use_undirected) plus self-loops, 64-dim features, 2 layers, 4
-    heads x 64, hops (1, 2), 5 classes, seed 0. Times whole steps for about
-    `seconds` with every host thread torch uses."""
+    forward + cross-entropy + backward + Adam step, restated in float32 torch
+    on the host (oracle/block_oracle.net_forward: the torch/PyG fallback path
+    of the reference, eval-mode numerics), on N=2000 nodes with out-degree 8
+    uniform-random edges (symmetrised, as the reference's default
+    use_undirected) plus self-loops, 64-dim features, 2 layers, 4 heads x 64,
+    hops (1, 2), 5 classes, seed 0. Median step time over about `seconds`
+    with the host's cores (oracle.cpu_path.host_threads)."""
     import numpy as np
 
     from cign_amd import workloads
     from oracle import block_oracle as B
+    from oracle import cpu_path
 
     d, hidden, heads, classes = 64, 64, 4, 5
     w = workloads.build(workloads.C1, device="cpu")
@@ -319,9 +307,9 @@ def cpu_train_baseline(seconds: float, torch):
     Pc = w.operator.csr
     p_np = (Pc.crow_indices().numpy(), Pc.col_indices().numpy(), Pc.values().double().numpy())
     g = torch.Generator().manual_seed(0)
-    t = lambda *s: (torch.randn(*s, generator=g, dtype=torch.float64) * 0.1).requires_grad_()
+    t = lambda *s: (torch.randn(*s, generator=g) * 0.1).requires_grad_()
     params = {"input_proj_0.weight": t(hidden, d), "input_proj_0.bias": t(hidden), "input_proj_1.weight": t(hidden, d),
-              "input_proj_1.bias": t(hidden), "input_eta": torch.tensor(0.1, dtype=torch.float64, requires_grad=True),
+              "input_proj_1.bias": t(hidden), "input_eta": torch.tensor(0.1, requires_grad=True),
               "output_norm.weight": t(3 * hidden), "output_norm.bias": t(3 * hidden),
               "classifier.weight": t(classes, 3 * hidden), "classifier.bias": t(classes)}
     for i in range(2):
@@ -331,7 +319,7 @@ def cpu_train_baseline(seconds: float, torch):
                          "context_gat.bias": (hidden,), "proj.weight": (hidden, 4 * hidden), "proj.bias": (hidden,),
                          "hop_gate_mlp.weight": (2, 2 * hidden), "hop_gate_mlp.bias": (2,), "gamma": (hidden,)}.items():
             params[f"blocks.{i}.{k}"] = t(*shape)
-    x = torch.randn(n, d, generator=g, dtype=torch.float64)
+    x = torch.randn(n, d, generator=g)
     y = torch.randint(0, classes, (n,), generator=g)
     mask = torch.rand(n, generator=g) < 0.5
     opt = torch.optim.Adam(list(params.values()), lr=3e-3, weight_decay=1e-5)
@@ -343,19 +331,79 @@ def cpu_train_baseline(seconds: float, torch):
         torch.nn.functional.cross_entropy(logits[mask], y[mask]).backward()
         opt.step()
 
-    step()
+    threads = cpu_path.host_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        med, k = cpu_path.time_steps(step, seconds)
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": int(col.numel()) / med, "unit": "edges/s", "cores": threads, "kind": "port",
+            "ms_per_step": round(1e3 * med, 3),
+            "sample": f"median of {k} c1 training steps (N=2000, E_nnz={int(col.numel())}, in 64, hidden 64, 2 layers, "
+                      f"4 heads, hops 1-2; float32 torch restatement of the reference's CPU path + Adam), "
+                      f"{threads} threads"}
+
+
+def make_train_step(torch, w, in_dim, hidden, heads, layers, order_set, amp, dev):
+    """One training step of GraphCliffordNet (zero_grad, forward,
+    cross-entropy over a 50% train mask, backward, Adam lr 3e-3 / weight
+    decay 1e-5) on workload w, as generic_engine/train_cign.py:2103-2148
+    times it; returns the step callable (it returns the loss)."""
+    import torch.nn.functional as F
+
+    from cign_amd.model_cign import GraphCliffordNet
+    from cign_amd.multihop_csr_pipeline import prepare_multihop_csr_operator
+
+    torch.manual_seed(0)
+    model = GraphCliffordNet(in_dim, hidden, 5, num_layers=layers, order_set=order_set, gat_heads=heads,
+                             use_selective_amp=amp).to(dev).train()
+    model._fused_gat_graph = w.gat_graph
+    # the operator the reference's driver prepares for these hops
+    mh = prepare_multihop_csr_operator(w.operator, dense_cols=2 * hidden, powers=order_set)
+    g = torch.Generator(device="cpu").manual_seed(0)
+    x = torch.randn(w.n, in_dim, generator=g).to(dev)
+    y = torch.randint(0, 5, (w.n,), generator=g).to(dev)
+    mask = (torch.rand(w.n, generator=g) < 0.5).to(dev)
+    opt = torch.optim.Adam(model.parameters(), lr=3e-3, weight_decay=1e-5)
+
+    def step():
+        opt.zero_grad()
+        logits = model(x, None, mh)
+        loss = F.cross_entropy(logits[mask], y[mask])
+        loss.backward()
+        opt.step()
+        return loss
+
+    return step
+
+
+def time_train(torch, step, steps, warmup):
+    """(wall seconds of `steps` steps, GPU ms per step) after `warmup` steps."""
+    for _ in range(max(1, warmup)):
+        loss = step()
+    torch.cuda.synchronize()
+    if not torch.isfinite(loss):
+        raise SystemExit("non-finite training loss")
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    k = 0
-    while True:
+    a0.record()
+    for _ in range(steps):
         step()
-        k += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": int(col.numel()) * k / dt, "unit": "edges/s", "cores": torch.get_num_threads(), "kind": "port",
-            "ms_per_step": 1e3 * dt / k,
-            "sample": f"{k} c1 training steps (N=2000, E_nnz={int(col.numel())}, in 64, hidden 64, 2 layers, 4 heads, "
-                      f"hops 1-2, float64 torch restatement + Adam) in {dt:.1f} s"}
+    a1.record()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, a0.elapsed_time(a1) / steps
+
+
+def c1_gpu(torch, dev, steps=20):
+    """The reference's CPU case c1 (N=2000, 64-dim, 4 heads x 64, hops 1-2,
+    2 layers) as a training step on the GPU, fp32."""
+    from cign_amd import workloads
+
+    w1 = workloads.build(workloads.C1, device=dev)
+    e1, gms = time_train(torch, make_train_step(torch, w1, 64, 64, 4, 2, (1, 2), False, dev), steps, 3)
+    return {"ms_per_step": round(1e3 * e1 / steps, 4), "gpu_ms_per_step": round(gms, 4), "edges_nnz": w1.nnz_gat,
+            "edges_per_s": w1.nnz_gat * steps / e1}
 
 
 def run_train(args, torch):
@@ -368,58 +416,16 @@ def run_train(args, torch):
     self-loops) per second of training. The CPU baseline is the reference's
     own CPU case c1 (cpu_train_baseline); the same model at c1 is also timed
     on the GPU for a like-for-like ratio."""
-    import torch.nn.functional as F
-
     from cign_amd import workloads
-    from cign_amd.model_cign import GraphCliffordNet
-    from cign_amd.multihop_csr_pipeline import prepare_multihop_csr_operator
 
     dev = torch.device("cuda:0")
     amp = args.dtype != "f32"
 
-    def make(w, in_dim, hidden, heads, layers, order_set):
-        torch.manual_seed(0)
-        model = GraphCliffordNet(in_dim, hidden, 5, num_layers=layers, order_set=order_set, gat_heads=heads,
-                                 use_selective_amp=amp).to(dev).train()
-        model._fused_gat_graph = w.gat_graph
-        # the operator the reference's driver prepares for these hops
-        mh = prepare_multihop_csr_operator(w.operator, dense_cols=2 * hidden, powers=order_set)
-        g = torch.Generator(device="cpu").manual_seed(0)
-        x = torch.randn(w.n, in_dim, generator=g).to(dev)
-        y = torch.randint(0, 5, (w.n,), generator=g).to(dev)
-        mask = (torch.rand(w.n, generator=g) < 0.5).to(dev)
-        opt = torch.optim.Adam(model.parameters(), lr=3e-3, weight_decay=1e-5)
-
-        def step():
-            opt.zero_grad()
-            logits = model(x, None, mh)
-            loss = F.cross_entropy(logits[mask], y[mask])
-            loss.backward()
-            opt.step()
-            return loss
-
-        return step
-
-    def timed(step, steps, warmup):
-        for _ in range(max(1, warmup)):
-            loss = step()
-        torch.cuda.synchronize()
-        if not torch.isfinite(loss):
-            raise SystemExit("non-finite training loss")
-        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        a0.record()
-        for _ in range(steps):
-            step()
-        a1.record()
-        torch.cuda.synchronize()
-        return time.perf_counter() - t0, a0.elapsed_time(a1) / steps
-
     w = workloads.build(workloads.C2, device=dev)
-    elapsed, gpu_ms = timed(make(w, 256, 256, 6, 2, (1, 2, 3)), args.steps, args.warmup)
+    elapsed, gpu_ms = time_train(torch, make_train_step(torch, w, 256, 256, 6, 2, (1, 2, 3), amp, dev), args.steps,
+                                 args.warmup)
     # The reference's CPU case on the GPU (c1: N=2000, 64-dim, 4 heads, hops 1-2).
-    w1 = workloads.build(workloads.C1, device=dev)
-    e1, _ = timed(make(w1, 64, 64, 4, 2, (1, 2)), 20, 3)
+    c1 = c1_gpu(torch, dev)
     cpu = cpu_train_baseline(args.cpu_seconds, torch) if args.cpu_seconds > 0 else None
     line = {
         "metric": "CIGN 2-layer training step edges/sec (zero_grad, forward, cross-entropy, backward, Adam)",
@@ -439,8 +445,7 @@ def run_train(args, torch):
         "config": {"workload": "c4 training step: GraphCliffordNet in 256, hidden 256, 2 layers, 6 GAT heads x 256, "
                                "hops 1-3, dropout 0.28 / GAT 0.32, concat, Adam",
                    "nodes": w.n, "edges_nnz": w.nnz_gat},
-        "c1_gpu": {"ms_per_step": 1e3 * e1 / 20, "edges_nnz": w1.nnz_gat,
-                   "edges_per_s": w1.nnz_gat * 20 / e1},
+        "c1_gpu": c1,
         "roofline": None,
         "cpu_baseline": cpu,
     }
@@ -625,10 +630,6 @@ def main():
         sys.exit(2)
     import torch
 
-    from cign_amd import workloads
-    from cign_amd.collapsed_gat import ensure_collapsed_gat_loaded
-    from cign_amd.multihop_csr_pipeline import MultiHopCSR3GraphOperator
-
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.workload == "block":
@@ -641,17 +642,57 @@ def main():
             args.dtype = "bf16"
         run_train(args, torch)
         return
-    scale = args.workload == "scale"
-    if args.dtype is None:
-        args.dtype = "bf16" if scale else "f32"
+    layer_only = args.workload == "scale"
+    if layer_only:
+        line, _ = measure_layer(torch, True, args.dtype or "bf16", args.steps, args.warmup, args.eager,
+                                args.calibrate_copy)
+        print(json.dumps(line), flush=True)
+        return
+    line, w = measure_layer(torch, False, args.dtype or "f32", args.steps, args.warmup, args.eager,
+                            args.calibrate_copy)
+    print(f"c2+c3 layer: {line['ms_per_step']:.4f} ms/step", file=sys.stderr, flush=True)
+    # The GPU c1 step is launch-bound host code: time it before the CPU
+    # baselines leave their worker threads spinning.
+    line["c1_gpu"] = c1_gpu(torch, torch.device("cuda:0"))
+    if args.cpu_seconds > 0:
+        line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds, 4, 16, 64)
+        print("cpu baseline done", file=sys.stderr, flush=True)
+        line["cpu_baseline_c1"] = cpu_train_baseline(args.cpu_seconds, torch)
+        print("c1 model step on the host done", file=sys.stderr, flush=True)
+    else:
+        line["cpu_baseline"] = None
+    del w
+    if not args.no_scale:
+        # BASELINE config 5 in the same run: the layer at 2.4M nodes / 62.4M
+        # edges (bf16, 4 x 32 heads, D = 256), the true HBM-bound case.
+        sc, _ = measure_layer(torch, True, "bf16", max(3, min(args.steps, 20)), 2)
+        line["scale"] = {k: sc[k] for k in ("value", "unit", "ms_per_step", "gpu_ms_per_step", "dtype", "config",
+                                           "layer_GB_s", "layer_roofline_frac", "algorithmic_bytes_per_step",
+                                           "layer_own_roofline_frac", "breakdown", "roofline", "invariants")}
+        line["scale"]["steps"] = max(3, min(args.steps, 20))
+    print(json.dumps(line), flush=True)
+
+
+def measure_layer(torch, scale: bool, dtype: str, steps: int, warmup: int, eager: bool = False,
+                  calibrate_copy: bool = False):
+    """The layer step (collapsed GAT + 3-hop SpMM, forward + backward) at c2+c3
+    (scale False: H=4 x C=16, D=64) or c5 (scale True: H=4 x C=32, D=256,
+    eager launches, full-size invariants), timed over `steps` steps after
+    `warmup`, with the per-phase roofline. Returns (JSON line without CPU
+    baselines, workload)."""
+    from cign_amd import workloads
+    from cign_amd.collapsed_gat import ensure_collapsed_gat_loaded
+    from cign_amd.multihop_csr_pipeline import MultiHopCSR3GraphOperator
+
+    dev = torch.device("cuda:0")
     H, C, D = (4, 32, 256) if scale else (4, 16, 64)
-    dt = torch.float32 if args.dtype == "f32" else torch.bfloat16
+    dt = torch.float32 if dtype == "f32" else torch.bfloat16
+    # Captured graphs would keep one output set per captured launch; at c5
+    # the GPU is the bottleneck, so its launches stay eager.
+    eager = eager or scale
     t_build = time.perf_counter()
     if scale:
-        print("building the c5 graph on the host (about 1.5 minutes)...", file=sys.stderr, flush=True)
-        # Captured graphs would keep one output set per captured launch; at
-        # this size the GPU is the bottleneck, so launches stay eager.
-        args.eager = True
+        print("building the c5 graph on the host (under a minute)...", file=sys.stderr, flush=True)
     w = workloads.build(workloads.C5 if scale else workloads.C2, device=dev)
     if scale:
         print(f"graph built in {time.perf_counter() - t_build:.0f} s", file=sys.stderr, flush=True)
@@ -688,7 +729,7 @@ def main():
         else:
             fwd_out["mh_bwd"] = [plan.backward3(g1, g2, g3)]
 
-    if args.calibrate_copy:
+    if calibrate_copy:
         src = torch.ones(64 << 20, dtype=torch.float32, device=dev)  # 256 MiB
         dst = torch.empty_like(src)
         for _ in range(3):
@@ -698,7 +739,7 @@ def main():
 
     # Eager warmup: builds the row schedules (one host copy of each row
     # pointer) and the workspaces, and gives the reference outputs.
-    for _ in range(max(1, args.warmup)):
+    for _ in range(max(1, warmup)):
         for p in phases:
             run_phase(p)
     torch.cuda.synchronize()
@@ -720,20 +761,20 @@ def main():
         for p in phases:
             run_phase(p)
 
-    if args.eager:
+    if eager:
         launch_step = whole_step
     else:
-        eager = {k: [t.clone() for t in v] for k, v in fwd_out.items()}
+        eager_out = {k: [t.clone() for t in v] for k, v in fwd_out.items()}
         # The step as one HIP graph: its host work is one launch, and every
         # replay recomputes every kernel of the four phases.
         launch_step = capture(whole_step).replay
-        for _ in range(max(1, args.warmup)):
+        for _ in range(max(1, warmup)):
             launch_step()
         torch.cuda.synchronize()
         # Replays reproduce the eager results bit for bit (the GAT forward's
         # edge_mask, output 4, is only written when attn_drop > 0).
         for k, v in fwd_out.items():
-            for i, (a_, b_) in enumerate(zip(v, eager[k])):
+            for i, (a_, b_) in enumerate(zip(v, eager_out[k])):
                 if not (k == "gat" and i == 4) and not torch.equal(a_, b_):
                     raise SystemExit(f"graph replay of {k}[{i}] differs from the eager result")
 
@@ -742,20 +783,20 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         launch_step()
     stop.record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    gpu_step_ms = start.elapsed_time(stop) / args.steps
+    gpu_step_ms = start.elapsed_time(stop) / steps
 
     # Per-phase kernel durations: each phase launched R times back to back
     # (one HIP graph, or R drop-in calls with --eager) and timed with HIP
     # events on the launch stream.
-    R, M = (1, max(2, args.steps)) if scale else (20, max(2, args.steps // 10))
+    R, M = (1, max(2, steps)) if scale else (20, max(2, steps // 10))
     phase_ms = {}
     for p in phases:
-        if args.eager:
+        if eager:
             rep = lambda p=p: [run_phase(p) for _ in range(R)]
         else:
             gp = capture(lambda p=p: [run_phase(p) for _ in range(R)])
@@ -772,7 +813,7 @@ def main():
 
     s = 2 if dt == torch.bfloat16 else 4
     B = workloads.algorithmic_bytes(n, E, H, C, D, s_gat=s, s_mh=s)
-    ms = 1e3 * elapsed / args.steps
+    ms = 1e3 * elapsed / steps
     # One "launch" of the GAT backward is one cign_gat_bwd call (its rows and
     # columns kernels back to back on the stream).
     launches = {"gat_fwd": 1, "spmm_fwd3": 3, "gat_bwd": 1, "spmm_bwd3": 3}
@@ -792,34 +833,30 @@ def main():
                    "gat_bwd": ("cign_gat_bwd (gat_bwd_rows_agg_kernel + gat_bwd_cols_fl_kernel)" if agg_path else
                                "cign_gat_bwd (gat_bwd_rows_fl_kernel + gat_bwd_cols_fl_kernel)"),
                    "spmm_bwd3": "spmm_kernel (bwd hop, fused add)"}[dom]
-    traffic, traffic_src = measured_traffic(f"layer_{'c5' if scale else 'c2c3'}_{args.dtype}", dom)
+    traffic, traffic_src = measured_traffic(f"layer_{'c5' if scale else 'c2c3'}_{dtype}", dom)
     layer_gbs = B["layer"] / (ms * 1e-3) / 1e9
     layer_own_gbs = B["layer" + gkey] / (ms * 1e-3) / 1e9
 
     checks = invariants(torch, w, ext, plan, H, C, D, dt) if scale else None
 
-    cpu = None
-    if args.cpu_seconds > 0 and not scale:
-        cpu = cpu_baseline(w, args.cpu_seconds, H, C, D)
-
     line = {
         "metric": "GAT+multihop layer fwd+bwd edges/sec; achieved HBM GB/s as % of roofline",
-        "value": E * args.steps / elapsed,
+        "value": E * steps / elapsed,
         "unit": "edges/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": ms,
         "gpu_ms_per_step": round(gpu_step_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": args.dtype,
+        "dtype": dtype,
         "data": (f"synthetic: seeded Chung-Lu power-law graph (gamma {2.2 if scale else 2.5}), N(0,1) features "
                  "and gradient probes"),
         "config": {"workload": (f"{'c5 scale' if scale else 'c2+c3'} layer: collapsed GAT H={H} x C={C} + 3-hop "
                                 f"CSR SpMM D={D}, forward+backward"),
-                   "launch": "eager" if args.eager else "hip_graph_per_step",
+                   "launch": "eager" if eager else "hip_graph_per_step",
                    "nodes": n, "edges_nnz": E, "heads": H, "channels": C, "dense_cols": D, "hops": 3,
                    "max_in_degree": int(torch.diff(rowptr.long()).max())},
         "layer_GB_s": round(layer_gbs, 1),
@@ -834,11 +871,12 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_source": traffic_src, "bytes_per_launch": bytes_per_launch[dom],
                      "avg_launch_ms": round(dom_ms, 5)},
-        "cpu_baseline": cpu,
     }
     if checks is not None:
         line["invariants"] = checks
-    print(json.dumps(line), flush=True)
+    return line, w
+
+
 
 
 if __name__ == "__main__":

@@ -678,3 +678,34 @@ def test_block_oracle_amp_linear_matches_autocast_rounding_points():
     assert_close(xt.grad.numpy(), gx, 1e-12, 1e-12, "grad x")
     assert_close(wt.grad.numpy(), gw, 1e-12, 1e-12, "grad w")
     assert_close(bt.grad.numpy(), gy.sum(0), 1e-12, 1e-12, "grad b")
+
+
+def test_cpu_path_layer_matches_oracle(rng):
+    """The float32 torch restatement of the reference's CPU path (the timed
+    CPU baseline) computes the oracle's GAT and three hops, forward and
+    backward, to float32 accuracy."""
+    import torch
+
+    from oracle import cpu_path
+
+    n, H, C, D = 120, 3, 5, 7
+    ei = random_gat_graph(rng, n, avg_deg=6, hubs={2: 90})
+    rowptr, col, _, _, _ = O.gat_graph_format(ei, n)
+    val = rng.random(len(col))
+    p_csr = (rowptr, col, val)
+    pt_csr = O.transpose_csr(rowptr, col, val, n)
+    L = cpu_path.LayerCPU(rowptr, col, p_csr, pt_csr, n, H, C, D, seed=3)
+    L.step()
+    d = lambda t: t.detach().double().numpy()
+    f = O.collapsed_gat_forward(d(L.ar), d(L.ac), rowptr, col, 0.2, d(L.x), d(L.b))
+    y = cpu_path.gat_concat_false(L.x, L.ac, L.ar, L.rows, L.src, n, 0.2, L.b)
+    assert_close(d(y), f["out"], 1e-4, 1e-5, "gat out")
+    g = O.collapsed_gat_backward(d(L.ar), d(L.ac), rowptr, col, 0.2, d(L.x), d(L.b), d(L.gy))
+    for name, t in (("grad_feat", L.x), ("grad_attn_row", L.ar), ("grad_attn_col", L.ac), ("grad_bias", L.b)):
+        assert_close(d(t.grad), g[name], 1e-4, 1e-5, name)
+    ys = O.multihop3_forward(p_csr, d(L.X))
+    gx = O.multihop3_backward(pt_csr, *(d(t) for t in L.G))
+    assert_close(d(L.X.grad), gx, 1e-4, 1e-5, "multihop grad_x")
+    y1 = cpu_path._FixedCsrMM.apply(L.X, L.P, L.PT)
+    assert_close(d(y1), ys[0], 1e-4, 1e-5, "hop 1")
+    assert cpu_path.host_threads() >= 1
