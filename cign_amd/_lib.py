@@ -53,6 +53,8 @@ _SIGNATURES = {
     "cign_add_ln_bwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64]),
     "cign_gamma_residual_fwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _F32, _U64, _P, _P]),
     "cign_gamma_residual_bwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _F32, _P, _P, _P, _I64]),
+    "cign_add_ln_cat_fwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _F32, _P, _P, _P, _P]),
+    "cign_add_ln_cat_bwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64]),
     # hop gate (gate.hip)
     "cign_hop_gate_bwd_workspace_bytes": (_I64, [_I64, _I32, _I32]),
     "cign_hop_gate_fwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P]),
@@ -64,9 +66,7 @@ _SIGNATURES = {
                                         _P]),
     "cign_linear_bwd_workspace_bytes": (_I64, [_I64, _I32, _I32, _I32]),
     "cign_linear_bwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _I64]),
-    # Clifford packs (pack.hip)
-    "cign_add_ln_cat_fwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _F32, _P, _P, _P, _P]),
-    "cign_add_ln_cat_bwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64]),
+    # Clifford packs (pack.hip) and the gate fused into them (gate.hip)
     "cign_pack_gate_fwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _I64, _P, _P, _P, _P]),
     "cign_pack_gate_bwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _I64, _P, _P, _P, _P,
                                      _P, _I64, _P, _P, _P, _I64]),

@@ -18,9 +18,10 @@ namespace cign {
 namespace rowops {
 
 // out[c] = sum_b part[b][c] over the nb row-block partials, in a fixed order:
-// a workgroup of kColsumThreads covers 64 columns; thread (c, s) sums the
-// partials b = s, s + 16, ... with four independent accumulators (combined in
-// a fixed order), then the 16 slices are added in order through LDS.
+// a workgroup of kColsumThreads covers kCols columns (16 or 64) in
+// kColsumThreads / kCols slices; thread (c, s) sums the partials b = s,
+// s + slices, ... with eight independent accumulators (combined in a fixed
+// order), then the slices are added through an LDS tree.
 template <int kCols>
 __global__ __launch_bounds__(kColsumThreads) void colsum_kernel(const float* part, int nb, int width, float* out0,
                                                                 float* out1) {
@@ -100,9 +101,12 @@ int zero_outputs(hipStream_t st, float* a, int na, float* b, int nbv, const char
 int launch_colsum(hipStream_t st, const float* part, int nb, int width, int quantities, float* out0, float* out1,
                   const char* who) {
   if (width <= 0) return kOk;
-  // Narrow outputs over many partial rows (LayerNorm and bias gradients):
-  // 16 columns x 64 slices, so more workgroups share the rows; wide outputs
-  // (weight gradients) already have enough columns: 64 x 16.
+  // Three fixed-order paths: outputs wider than 4096 columns over at most 128
+  // partial rows (weight gradients) take colsum_wide_kernel, one thread per
+  // four columns walking the rows in order; narrow outputs over at least 256
+  // partial rows (LayerNorm and bias gradients at large n) take 16 columns x
+  // 64 slices, so more workgroups share the rows; the rest 64 columns x 16
+  // slices.
   const bool vec = width % 4 == 0 && aligned16(part) && aligned16(out0) && (!out1 || aligned16(out1));
   if (width > 4096 && nb <= 128 && vec)
     hipLaunchKernelGGL(colsum_wide_kernel, dim3((width / 4 + kBlock - 1) / kBlock, quantities), dim3(kBlock), 0, st,

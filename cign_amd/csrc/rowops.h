@@ -79,16 +79,13 @@ __device__ __forceinline__ void block_colsum(const float (&acc)[V][W], float* ld
   __syncthreads();
 }
 
-// out_y[c] = sum over b < nb of part[(y * nb + b) * width + c], y = blockIdx.y
-// selecting one of two outputs. Each workgroup covers up to 256 columns; its
-// threads split the nb partial rows into S interleaved slices whose sums are
-// then added in slice order.
-
 // Zero-fills a[0..na) and b[0..nbv) (b may be null): the parameter
 // gradients of an empty row set.
 int zero_outputs(hipStream_t st, float* a, int na, float* b, int nbv, const char* who);
 
-// Launches colsum_kernel for `quantities` (1 or 2) outputs.
+// out_y[c] = sum over b < nb of part[(y * nb + b) * width + c] for
+// `quantities` (1 or 2) outputs y, in a fixed order (colsum_kernel or
+// colsum_wide_kernel by shape).
 int launch_colsum(hipStream_t st, const float* part, int nb, int width, int quantities, float* out0, float* out1,
                   const char* who);
 

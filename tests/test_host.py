@@ -6,6 +6,7 @@ import re
 from pathlib import Path
 
 import numpy as np
+import pytest
 import torch
 
 from cign_amd import _lib, graph, graphgen
@@ -237,3 +238,29 @@ def test_spmm_noalloc_rejects_schedules_beyond_its_scratch():
     hdr[1], hdr[2] = 1, 300_000  # more merge counters than the scratch holds
     rc = lib.cign_spmm_fwd3_noalloc(None, 0, 300_010, 4, None, None, None, hdr.ctypes.data, None, None, None, None)
     assert rc == 1 and b"262144 counters" in lib.cign_last_error()
+
+
+def test_dispatch_signatures_match_reference_vectors(monkeypatch):
+    """canonical_config / cign_speed_signature give the reference's keys and
+    dicts (vectors recorded from the reference by
+    tests/golden/make_dispatch_signatures.py): option forms --a v / --a=v,
+    list options, booleans, repeated options, the switch environment."""
+    import json
+
+    from cign_amd.cign_dispatch_utils import cign_speed_signature
+    from cign_amd.generic_dispatch import canonical_config
+
+    cases = json.loads((ROOT / "tests" / "golden" / "dispatch_signatures.json").read_text())["cases"]
+    assert len(cases) >= 20
+    keys = ("CIGN_ALPHA_SCORE_MODE", "CIGN_INTERACTION_MODE", "CIGN_ALPHA_WEIGHTING_MODE", "CIGN_OUTER_NONLINEARITY",
+            "CLIFFORD_EDGE_DROP_RATIO")
+    for c in cases:
+        for k in keys:
+            monkeypatch.delenv(k, raising=False)
+        for k, v in c["env"].items():
+            monkeypatch.setenv(k, v)
+        assert canonical_config(c["argv"]) == (c["canonical_key"], c["canonical_cfg"]), c["argv"]
+        assert cign_speed_signature(c["argv"]) == (c["cign_key"], c["cign_cfg"]), (c["argv"], c["env"])
+    monkeypatch.setenv("CIGN_INTERACTION_MODE", "sideways")
+    with pytest.raises(ValueError, match="old/new"):
+        cign_speed_signature([])
