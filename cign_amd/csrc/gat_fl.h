@@ -560,23 +560,28 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
 
 template <typename T, int L, int V>
 struct FwdFlLauncher {
-  static int run(hipStream_t st, const GatFwdArgs<T>& a, const Sched& s, const int32_t* hdr, int lgcq) {
-    constexpr int G = kWave / L;
-    const int n_mid = G > 1 ? sched_count_gt(hdr, L) : s.n_light;
-    const int mid_blocks = (n_mid + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int n_tiny = s.n_light - n_mid;
-    const int blocks = s.n_seg + mid_blocks + (n_tiny + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
-    if (blocks > 0) {
-      if (a.p > 0.0f)
-        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, true>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
-                           mid_blocks, lgcq);
-      else
-        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, false>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
-                           mid_blocks, lgcq);
-    }
-    return check_launch("cign_gat_fwd (feature layout)");
-  }
+  static int run(hipStream_t st, const GatFwdArgs<T>& a, const Sched& s, const int32_t* hdr, int lgcq);
 };
+
+// Out of class, so that the extern template declarations of the
+// translation units that only call a launcher also suppress its kernels.
+template <typename T, int L, int V>
+int FwdFlLauncher<T, L, V>::run(hipStream_t st, const GatFwdArgs<T>& a, const Sched& s, const int32_t* hdr, int lgcq) {
+  constexpr int G = kWave / L;
+  const int n_mid = G > 1 ? sched_count_gt(hdr, L) : s.n_light;
+  const int mid_blocks = (n_mid + kWavesPerBlock - 1) / kWavesPerBlock;
+  const int n_tiny = s.n_light - n_mid;
+  const int blocks = s.n_seg + mid_blocks + (n_tiny + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
+  if (blocks > 0) {
+    if (a.p > 0.0f)
+      hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, true>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
+                         mid_blocks, lgcq);
+    else
+      hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, false>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
+                         mid_blocks, lgcq);
+  }
+  return check_launch("cign_gat_fwd (feature layout)");
+}
 
 // ===========================================================================
 // Backward, rows (CSR)
@@ -1282,51 +1287,60 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
 
 template <typename T, int L, int V>
 struct BwdFlLauncher {
-  static int row_blocks(const Sched& rs, const int32_t* rhdr) {
-    constexpr int G = kWave / L;
-    const int r_mid = G > 1 ? sched_count_gt(rhdr, L) : rs.n_light;
-    return rs.n_seg + (r_mid + kWavesPerBlock - 1) / kWavesPerBlock +
-           (rs.n_light - r_mid + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
-  }
+  static int row_blocks(const Sched& rs, const int32_t* rhdr);
 
   static int run(hipStream_t st, const GatBwdArgs<T>& a, const Sched& rs, const int32_t* rhdr, const Sched& cs,
-                 const int32_t* chdr, int lgcq) {
-    constexpr int G = kWave / L;
-    const int r_mid = G > 1 ? sched_count_gt(rhdr, L) : rs.n_light;
-    const int r_mid_blocks = (r_mid + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int rb = row_blocks(rs, rhdr);
-    if (a.agg) {
-      const int ab = (a.n + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
-      if (ab > 0) {
-        hipLaunchKernelGGL((gat_bwd_rows_agg_kernel<T, L, V>), dim3(ab), dim3(kBlock), 0, st, a, lgcq);
-        const int rc = check_launch("cign_gat_bwd (rows from aggregates, feature layout)");
-        if (rc) return rc;
-      }
-    } else if (rb > 0) {
-      if (a.p > 0.0f)
-        hipLaunchKernelGGL((gat_bwd_rows_fl_kernel<T, L, V, true>), dim3(rb), dim3(kBlock), 0, st, a, rs, r_mid,
-                           r_mid_blocks, lgcq);
-      else
-        hipLaunchKernelGGL((gat_bwd_rows_fl_kernel<T, L, V, false>), dim3(rb), dim3(kBlock), 0, st, a, rs, r_mid,
-                           r_mid_blocks, lgcq);
-      const int rc = check_launch("cign_gat_bwd (rows, feature layout)");
+                 const int32_t* chdr, int lgcq);
+};
+
+// Out of class, so that the extern template declarations of the
+// translation units that only call a launcher also suppress its kernels.
+template <typename T, int L, int V>
+int BwdFlLauncher<T, L, V>::row_blocks(const Sched& rs, const int32_t* rhdr) {
+  constexpr int G = kWave / L;
+  const int r_mid = G > 1 ? sched_count_gt(rhdr, L) : rs.n_light;
+  return rs.n_seg + (r_mid + kWavesPerBlock - 1) / kWavesPerBlock +
+         (rs.n_light - r_mid + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
+}
+
+template <typename T, int L, int V>
+int BwdFlLauncher<T, L, V>::run(hipStream_t st, const GatBwdArgs<T>& a, const Sched& rs, const int32_t* rhdr, const Sched& cs,
+                                const int32_t* chdr, int lgcq) {
+  constexpr int G = kWave / L;
+  const int r_mid = G > 1 ? sched_count_gt(rhdr, L) : rs.n_light;
+  const int r_mid_blocks = (r_mid + kWavesPerBlock - 1) / kWavesPerBlock;
+  const int rb = row_blocks(rs, rhdr);
+  if (a.agg) {
+    const int ab = (a.n + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
+    if (ab > 0) {
+      hipLaunchKernelGGL((gat_bwd_rows_agg_kernel<T, L, V>), dim3(ab), dim3(kBlock), 0, st, a, lgcq);
+      const int rc = check_launch("cign_gat_bwd (rows from aggregates, feature layout)");
       if (rc) return rc;
     }
-    const int c_mid = G > 1 ? sched_count_gt(chdr, L) : cs.n_light;
-    const int c_mid_blocks = (c_mid + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int cb = cs.n_seg + c_mid_blocks + (cs.n_light - c_mid + kWavesPerBlock * G - 1) / (kWavesPerBlock * G) +
-                   a.n_l2;
-    if (cb > 0) {
-      if (a.p > 0.0f)
-        hipLaunchKernelGGL((gat_bwd_cols_fl_kernel<T, L, V, true>), dim3(cb), dim3(kBlock), 0, st, a, cs, c_mid,
-                           c_mid_blocks, lgcq);
-      else
-        hipLaunchKernelGGL((gat_bwd_cols_fl_kernel<T, L, V, false>), dim3(cb), dim3(kBlock), 0, st, a, cs, c_mid,
-                           c_mid_blocks, lgcq);
-    }
-    return check_launch("cign_gat_bwd (cols, feature layout)");
+  } else if (rb > 0) {
+    if (a.p > 0.0f)
+      hipLaunchKernelGGL((gat_bwd_rows_fl_kernel<T, L, V, true>), dim3(rb), dim3(kBlock), 0, st, a, rs, r_mid,
+                         r_mid_blocks, lgcq);
+    else
+      hipLaunchKernelGGL((gat_bwd_rows_fl_kernel<T, L, V, false>), dim3(rb), dim3(kBlock), 0, st, a, rs, r_mid,
+                         r_mid_blocks, lgcq);
+    const int rc = check_launch("cign_gat_bwd (rows, feature layout)");
+    if (rc) return rc;
   }
-};
+  const int c_mid = G > 1 ? sched_count_gt(chdr, L) : cs.n_light;
+  const int c_mid_blocks = (c_mid + kWavesPerBlock - 1) / kWavesPerBlock;
+  const int cb = cs.n_seg + c_mid_blocks + (cs.n_light - c_mid + kWavesPerBlock * G - 1) / (kWavesPerBlock * G) +
+                 a.n_l2;
+  if (cb > 0) {
+    if (a.p > 0.0f)
+      hipLaunchKernelGGL((gat_bwd_cols_fl_kernel<T, L, V, true>), dim3(cb), dim3(kBlock), 0, st, a, cs, c_mid,
+                         c_mid_blocks, lgcq);
+    else
+      hipLaunchKernelGGL((gat_bwd_cols_fl_kernel<T, L, V, false>), dim3(cb), dim3(kBlock), 0, st, a, cs, c_mid,
+                         c_mid_blocks, lgcq);
+  }
+  return check_launch("cign_gat_bwd (cols, feature layout)");
+}
 
 // Narrow rows: one chunk per lane, groups of 1..64 lanes.
 #define CIGN_GAT_FL_LIST_NARROW(X, T) \

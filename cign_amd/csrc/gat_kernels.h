@@ -922,28 +922,38 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_kernel(GatBwdArgs<T> a, S
 // ---------------------------------------------------------------------------
 template <typename T, int HP, int CP>
 struct FwdLauncher {
-  static int run(hipStream_t st, const GatFwdArgs<T>& a, const Sched& s) {
-    const int blocks = sched_blocks(s);
-    if (blocks > 0)
-      hipLaunchKernelGGL((gat_fwd_kernel<T, HP, CP>), dim3(blocks), dim3(kBlock), 0, st, a, s);
-    return check_launch("cign_gat_fwd");
-  }
+  static int run(hipStream_t st, const GatFwdArgs<T>& a, const Sched& s);
 };
+
+// Out of class, so that the extern template declarations of the
+// translation units that only call a launcher also suppress its kernels.
+template <typename T, int HP, int CP>
+int FwdLauncher<T, HP, CP>::run(hipStream_t st, const GatFwdArgs<T>& a, const Sched& s) {
+  const int blocks = sched_blocks(s);
+  if (blocks > 0)
+    hipLaunchKernelGGL((gat_fwd_kernel<T, HP, CP>), dim3(blocks), dim3(kBlock), 0, st, a, s);
+  return check_launch("cign_gat_fwd");
+}
 
 template <typename T, int HP, int CP>
 struct BwdLauncher {
-  static int run(hipStream_t st, const GatBwdArgs<T>& a, const Sched& rs, const Sched& cs) {
-    const int rb = sched_blocks(rs);
-    if (rb > 0) {
-      hipLaunchKernelGGL((gat_bwd_rows_kernel<T, HP, CP>), dim3(rb), dim3(kBlock), 0, st, a, rs);
-      const int rc = check_launch("cign_gat_bwd (rows)");
-      if (rc) return rc;
-    }
-    const int cb = sched_blocks(cs) + a.n_l2;
-    if (cb > 0) hipLaunchKernelGGL((gat_bwd_cols_kernel<T, HP, CP>), dim3(cb), dim3(kBlock), 0, st, a, cs);
-    return check_launch("cign_gat_bwd (cols)");
-  }
+  static int run(hipStream_t st, const GatBwdArgs<T>& a, const Sched& rs, const Sched& cs);
 };
+
+// Out of class, so that the extern template declarations of the
+// translation units that only call a launcher also suppress its kernels.
+template <typename T, int HP, int CP>
+int BwdLauncher<T, HP, CP>::run(hipStream_t st, const GatBwdArgs<T>& a, const Sched& rs, const Sched& cs) {
+  const int rb = sched_blocks(rs);
+  if (rb > 0) {
+    hipLaunchKernelGGL((gat_bwd_rows_kernel<T, HP, CP>), dim3(rb), dim3(kBlock), 0, st, a, rs);
+    const int rc = check_launch("cign_gat_bwd (rows)");
+    if (rc) return rc;
+  }
+  const int cb = sched_blocks(cs) + a.n_l2;
+  if (cb > 0) hipLaunchKernelGGL((gat_bwd_cols_kernel<T, HP, CP>), dim3(cb), dim3(kBlock), 0, st, a, cs);
+  return check_launch("cign_gat_bwd (cols)");
+}
 
 #define CIGN_GAT_INSTANTIATE(T, HP)                        \
   template struct ::cign::gatk::FwdLauncher<T, HP, 8>;     \
