@@ -47,6 +47,8 @@
 // trailing workgroups, so the rows pass has no block barrier on light rows.
 #pragma once
 
+#include <utility>
+
 #include "gat_kernels.h"
 
 namespace cign {
@@ -254,10 +256,51 @@ struct FwdState {
   }
 };
 
+// The R lanes of a quad (R = 4) or pair (R = 2) that hold chunks of one
+// head split the per-(edge, head) work of a batch and exchange its results
+// through DPP: broadcast of lane S, max and sum over the R lanes.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int R, int S>
+__device__ __forceinline__ float quad_bcast(float v) {
+  if constexpr (R == 1) return v;
+  else if constexpr (R == 2) return dpp<(S == 0 ? 0xA0 : 0xF5)>(v);  // [S, S, 2 + S, 2 + S]
+  else return dpp<0x55 * S>(v);                                        // [S, S, S, S]
+}
+// f(integral_constant<int, i>) for i = 0 .. N-1 (compile-time indices).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+template <int R>
+__device__ __forceinline__ float quad_max(float v) {
+  if constexpr (R >= 2) v = fmaxf(v, dpp<0xB1>(v));  // xor 1
+  if constexpr (R >= 4) v = fmaxf(v, dpp<0x4E>(v));  // xor 2
+  return v;
+}
+template <int R>
+__device__ __forceinline__ float quad_sum(float v) {
+  if constexpr (R >= 2) v += dpp<0xB1>(v);
+  if constexpr (R >= 4) v += dpp<0x4E>(v);
+  return v;
+}
+
 // Batches of U edge slots of a lane group: slot u = first + (k0 + k) * step,
 // valid while u < cnt; its column index is held by lane (base + u) of the
 // wavefront, its CSR edge id is ebase + u. DROP: edge dropout (p > 0).
-template <typename T, int L, int V, bool DROP>
+// Every lane gathers its chunks of all U source rows. The softmax work of
+// each (edge, head) pair -- the source logit, LeakyReLU, exponential, slope,
+// dropout bit and mask byte -- is done once per R lanes of the head: lane r of
+// an R-lane set takes slots r, r + R, ...; the weights of slot k then come
+// from lane k % R by a DPP broadcast. The running max is shared by the R
+// lanes; the sums s and bl are per-lane partials until quad_reduce().
+template <typename T, int L, int V, bool DROP, int R>
 struct FwdBatches {
   static constexpr int W = FlGeom<T>::W;
   const GatFwdArgs<T>& a;
@@ -268,75 +311,94 @@ struct FwdBatches {
 
   template <int U>
   __device__ __forceinline__ void run(int k0) {
-    const int F = a.H * a.C;
+    constexpr int NT = (U + R - 1) / R;  // slots whose weights this lane computes
+    const uint32_t rowB = static_cast<uint32_t>(a.H * a.C) * sizeof(T);
     typename Chunk<T, W>::Raw xb[U][V];
-    float sc[U][V];
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
-      const int j = shfl(jj, (base + (u < cnt ? u : 0)) & (kWave - 1));
+      const uint64_t j = static_cast<uint32_t>(shfl(jj, (base + (u < cnt ? u : 0)) & (kWave - 1)));
 #pragma unroll
-      for (int v = 0; v < V; ++v) {
-        sc[k][v] = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq[v]];
-        xb[k][v] = Chunk<T, W>::load_raw(a.x + static_cast<int64_t>(j) * F + ln.q[v] * W);
-      }
+      for (int v = 0; v < V; ++v)
+        xb[k][v] = *reinterpret_cast<const typename Chunk<T, W>::Raw*>(
+            reinterpret_cast<const char*>(a.x + ln.q[v] * W) + j * rowB);
     }
-    // Dropout: each (edge, head) pair hashed once, its mask byte written by
-    // the lane that hashed it.
-    PairBits<(DROP ? U : 1), L> kb;
-    if constexpr (DROP)
-      kb.compute(a.H, ln.gl, [&](int k, int h, bool own) {
-        const int u = first + (k0 + k) * step;
-        if (!own || u >= cnt) return false;
-        const int64_t idx = static_cast<int64_t>(ebase + u) * a.H + h;
-        const bool keep = gat_keep(a.seed, static_cast<uint64_t>(idx), a.p);
-        a.mask[idx] = keep ? 1 : 0;
-        return keep;
-      });
-    // sc becomes the raw score (before LeakyReLU): its sign gives l'.
+    const int r = ln.gl & (R - 1);
+    float sc[NT][V];
+    bool own[NT];
+    int uo[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int kk = R * t + r;
+      uo[t] = first + (k0 + kk) * step;
+      own[t] = kk < U && uo[t] < cnt;
+      const uint64_t j = static_cast<uint32_t>(shfl(jj, (base + (own[t] ? uo[t] : 0)) & (kWave - 1)));
+#pragma unroll
+      for (int v = 0; v < V; ++v) sc[t][v] = a.attn_col[j * a.H + ln.hq[v]] + ar[v];  // raw score
+    }
+    float wk[NT][V], wl[NT][V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       float mx = st.m[v];
 #pragma unroll
-      for (int k = 0; k < U; ++k) {
-        const int u = first + (k0 + k) * step;
-        sc[k][v] += ar[v];
-        if (u < cnt) mx = fmaxf(mx, leaky(sc[k][v], a.slope));
-      }
-      st.scale(v, softmax_exp(st.m[v] - mx));
+      for (int t = 0; t < NT; ++t)
+        if (own[t]) mx = fmaxf(mx, leaky(sc[t][v], a.slope));
+      mx = quad_max<R>(mx);
+      if (__any(mx != st.m[v])) st.scale(v, softmax_exp(st.m[v] - mx));
       st.m[v] = mx;
-    }
 #pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int u = first + (k0 + k) * step;
-#pragma unroll
-      for (int v = 0; v < V; ++v) {
-        const float pk = u < cnt ? softmax_exp(leaky(sc[k][v], a.slope) - st.m[v]) : 0.0f;
-        const float lp = sc[k][v] < 0.0f ? a.slope : 1.0f;
+      for (int t = 0; t < NT; ++t) {
+        const float pk = own[t] ? softmax_exp(leaky(sc[t][v], a.slope) - mx) : 0.0f;
+        const float lp = sc[t][v] < 0.0f ? a.slope : 1.0f;
         st.s[v] += pk;
         st.bl[v] = fmaf(pk, lp, st.bl[v]);
-        float wk = pk;
-        if constexpr (DROP) wk = kb.get(k, ln.hq[v], ln.g) ? pk * (1.0f / (1.0f - a.p)) : 0.0f;
-        const float wl = wk * lp;
+        float w = pk;
+        if constexpr (DROP) {
+          const int64_t idx = static_cast<int64_t>(ebase + uo[t]) * a.H + ln.hq[v];
+          const bool keep = gat_keep(a.seed, static_cast<uint64_t>(idx), a.p);
+          if (own[t] && ln.qv[v]) a.mask[idx] = keep ? 1 : 0;
+          w = keep ? pk * (1.0f / (1.0f - a.p)) : 0.0f;
+        }
+        wk[t][v] = w;
+        wl[t][v] = w * lp;
+      }
+    }
+    static_for<U>([&](auto KC) {
+      constexpr int k = decltype(KC)::value;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float w = quad_bcast<R, k % R>(wk[k / R][v]);
+        const float wlk = quad_bcast<R, k % R>(wl[k / R][v]);
         float xv[W];
         Chunk<T, W>::unpack(xb[k][v], xv);
 #pragma unroll
-        for (int w = 0; w < W; ++w) {
-          st.acc[v][w] = fmaf(wk, xv[w], st.acc[v][w]);
-          st.accl[v][w] = fmaf(wl, xv[w], st.accl[v][w]);
+        for (int q = 0; q < W; ++q) {
+          st.acc[v][q] = fmaf(w, xv[q], st.acc[v][q]);
+          st.accl[v][q] = fmaf(wlk, xv[q], st.accl[v][q]);
         }
       }
-    }
+    });
   }
 };
 
 // All edge slots of a lane group: `need` (wave-uniform) slots per group.
-template <typename T, int L, int V, bool DROP>
+template <typename T, int L, int V, bool DROP, int R>
 __device__ __forceinline__ void fwd_edges(const GatFwdArgs<T>& a, const FlLane<L, V>& ln, int jj, int base, int first,
                                           int step, int cnt, int need, int ebase, const float (&ar)[V],
                                           FwdState<FlGeom<T>::W, V>& st) {
-  FwdBatches<T, L, V, DROP> fb{a, ln, jj, base, first, step, cnt, ebase, ar, st};
+  FwdBatches<T, L, V, DROP, R> fb{a, ln, jj, base, first, step, cnt, ebase, ar, st};
   for_batches<batch_cap(kFwdU, V)>(need, fb);
+}
+
+// The per-lane partial sums s, bl of each R-lane set, summed (after a row's
+// or segment's last batch).
+template <int R, int W, int V>
+__device__ __forceinline__ void quad_reduce(FwdState<W, V>& st) {
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    st.s[v] = quad_sum<R>(st.s[v]);
+    st.bl[v] = quad_sum<R>(st.bl[v]);
+  }
 }
 
 template <int L, int W, int V>
@@ -457,7 +519,7 @@ __device__ __forceinline__ void fwd_merge_waves(FwdState<W, V>& st, float* slot,
   }
 }
 
-template <typename T, int L, int V, bool DROP>
+template <typename T, int L, int V, bool DROP, int R>
 __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sched s, int n_mid, int mid_blocks,
                                                             int lgcq) {
   constexpr int W = FlGeom<T>::W;
@@ -483,7 +545,8 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
       const int jj = ln.gl < deg ? a.col[r.y + ln.gl] : 0;
       load_attn_row(a, ln, r.x, ar);
       const int need = wave_group_max<L>(deg);
-      fwd_edges<T, L, V, DROP>(a, ln, jj, ln.g * L, 0, 1, deg, need, r.y, ar, st);
+      fwd_edges<T, L, V, DROP, R>(a, ln, jj, ln.g * L, 0, 1, deg, need, r.y, ar, st);
+      quad_reduce<R>(st);
       fwd_emit<T, L, V>(a, ln, cq, r.x, has, st);
       return;
     }
@@ -495,7 +558,8 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
     const int deg = r.z - r.y;
     const int jj = ln.lane < deg ? a.col[r.y + ln.lane] : 0;
     load_attn_row(a, ln, r.x, ar);
-    fwd_edges<T, L, V, DROP>(a, ln, jj, 0, ln.g, G, deg, (deg + G - 1) / G, r.y, ar, st);
+    fwd_edges<T, L, V, DROP, R>(a, ln, jj, 0, ln.g, G, deg, (deg + G - 1) / G, r.y, ar, st);
+    quad_reduce<R>(st);
     fwd_merge_groups<L, W, V>(st);
     fwd_emit<T, L, V>(a, ln, cq, r.x, ln.g == 0, st);
     return;
@@ -517,9 +581,10 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
     const int cnt = min(kWave, sg.z - tb);
     const int tn = tb + kSegRound + ln.lane;
     const int jn = tn < sg.z ? a.col[tn] : 0;
-    fwd_edges<T, L, V, DROP>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, ar, st);
+    fwd_edges<T, L, V, DROP, R>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, ar, st);
     jj = jn;
   }
+  quad_reduce<R>(st);
   fwd_merge_groups<L, W, V>(st);
   fwd_merge_waves<W, V>(st, slot, wave, ln.gl, ln.g == 0);
   if (hr.y == 1) {
@@ -572,13 +637,26 @@ int FwdFlLauncher<T, L, V>::run(hipStream_t st, const GatFwdArgs<T>& a, const Sc
   const int mid_blocks = (n_mid + kWavesPerBlock - 1) / kWavesPerBlock;
   const int n_tiny = s.n_light - n_mid;
   const int blocks = s.n_seg + mid_blocks + (n_tiny + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
-  if (blocks > 0) {
+  if (blocks <= 0) return kOk;
+  // R lanes per head share the softmax work: min(cq, 4) (cq <= L).
+  auto launch = [&](auto RC) {
+    constexpr int R = decltype(RC)::value;
     if (a.p > 0.0f)
-      hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, true>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
+      hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, true, R>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
                          mid_blocks, lgcq);
     else
-      hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, false>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
+      hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, false, R>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
                          mid_blocks, lgcq);
+  };
+  if constexpr (L >= 4) {
+    if (lgcq >= 2) launch(std::integral_constant<int, 4>());
+    else if (lgcq == 1) launch(std::integral_constant<int, 2>());
+    else launch(std::integral_constant<int, 1>());
+  } else if constexpr (L == 2) {
+    if (lgcq >= 1) launch(std::integral_constant<int, 2>());
+    else launch(std::integral_constant<int, 1>());
+  } else {
+    launch(std::integral_constant<int, 1>());
   }
   return check_launch("cign_gat_fwd (feature layout)");
 }
