@@ -236,7 +236,7 @@ int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
   auto fill = [&](auto* xt, auto* ot) {
     using T = std::remove_cv_t<std::remove_pointer_t<decltype(ot)>>;
     GatFwdArgs<T> a;
-    a.n = n; a.H = heads; a.C = channels;
+    a.n = n; a.H = heads; a.C = channels; a.nnz = nnz;
     a.slope = negative_slope; a.p = attn_drop; a.seed = seed;
     a.vec = aligned16(xt) && (channels * static_cast<int>(sizeof(T))) % 16 == 0;
     a.attn_row = attn_row; a.attn_col = attn_col; a.col = col;

@@ -47,6 +47,7 @@
 // trailing workgroups, so the rows pass has no block barrier on light rows.
 #pragma once
 
+#include <cstdlib>
 #include <utility>
 
 #include "gat_kernels.h"
@@ -59,9 +60,27 @@ constexpr int kFlHeads = 8;
 // Largest batch (edge slots gathered per lane before any is consumed, times
 // the chunks per lane) of each kernel; the cap trades loads in flight per
 // wave for waves per SIMD.
+// The forward has two caps: 16 edge slots for graphs below kFwdBigGraph
+// edges, where a launch is a few dependent memory rounds and more loads per
+// round shorten it, and 8 above, where the smaller register footprint (one
+// more wavefront per SIMD) keeps more bytes in flight: at 62.4M edges (bf16,
+// 4 x 32) the forward took 3.43 ms with 8 against 4.84 ms with 16, at 211K
+// edges (fp32, 4 x 16) 14.7 us against 13.5 us.
 #ifndef CIGN_FL_FWD_U
 #define CIGN_FL_FWD_U 16
 #endif
+#ifndef CIGN_FL_FWD_U_BIG
+#define CIGN_FL_FWD_U_BIG 8
+#endif
+constexpr int64_t kFwdBigGraph = 1 << 22;
+
+// Edge count from which the large-graph variants run: kFwdBigGraph, or the
+// value of CIGN_GAT_BIG_GRAPH_EDGES (read at every launch; the tests set it to
+// 0 to run every shape through the large-graph variants at small sizes).
+inline int64_t big_graph_edges() {
+  const char* e = getenv("CIGN_GAT_BIG_GRAPH_EDGES");
+  return (e && *e) ? atoll(e) : kFwdBigGraph;
+}
 #ifndef CIGN_FL_ROWS_U
 #define CIGN_FL_ROWS_U 16
 #endif
@@ -74,8 +93,12 @@ constexpr int kFlHeads = 8;
 #define CIGN_FL_COLS_PAIR_FLOATS 16
 #endif
 constexpr int kFwdU = CIGN_FL_FWD_U;
+constexpr int kFwdUBig = CIGN_FL_FWD_U_BIG;
 constexpr int kRowsU = CIGN_FL_ROWS_U;
 constexpr int kColsU = CIGN_FL_COLS_U;
+// Batch cap of the shared-weight columns batches (large graphs): 4 slots
+// measured 3.54 ms at 62.4M edges against 3.90 ms for 8 and 5.55 ms for 16.
+constexpr int kColsUShared = 4;
 constexpr int kColsPairFloats = CIGN_FL_COLS_PAIR_FLOATS;
 
 // Batch cap for V chunks per lane: the largest power of two <= umax / V.
@@ -382,12 +405,12 @@ struct FwdBatches {
 };
 
 // All edge slots of a lane group: `need` (wave-uniform) slots per group.
-template <typename T, int L, int V, bool DROP, int R>
+template <typename T, int L, int V, bool DROP, int R, int UM>
 __device__ __forceinline__ void fwd_edges(const GatFwdArgs<T>& a, const FlLane<L, V>& ln, int jj, int base, int first,
                                           int step, int cnt, int need, int ebase, const float (&ar)[V],
                                           FwdState<FlGeom<T>::W, V>& st) {
   FwdBatches<T, L, V, DROP, R> fb{a, ln, jj, base, first, step, cnt, ebase, ar, st};
-  for_batches<batch_cap(kFwdU, V)>(need, fb);
+  for_batches<batch_cap(UM, V)>(need, fb);
 }
 
 // The per-lane partial sums s, bl of each R-lane set, summed (after a row's
@@ -519,7 +542,7 @@ __device__ __forceinline__ void fwd_merge_waves(FwdState<W, V>& st, float* slot,
   }
 }
 
-template <typename T, int L, int V, bool DROP, int R>
+template <typename T, int L, int V, bool DROP, int R, int UM>
 __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sched s, int n_mid, int mid_blocks,
                                                             int lgcq) {
   constexpr int W = FlGeom<T>::W;
@@ -545,7 +568,7 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
       const int jj = ln.gl < deg ? a.col[r.y + ln.gl] : 0;
       load_attn_row(a, ln, r.x, ar);
       const int need = wave_group_max<L>(deg);
-      fwd_edges<T, L, V, DROP, R>(a, ln, jj, ln.g * L, 0, 1, deg, need, r.y, ar, st);
+      fwd_edges<T, L, V, DROP, R, UM>(a, ln, jj, ln.g * L, 0, 1, deg, need, r.y, ar, st);
       quad_reduce<R>(st);
       fwd_emit<T, L, V>(a, ln, cq, r.x, has, st);
       return;
@@ -558,7 +581,7 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
     const int deg = r.z - r.y;
     const int jj = ln.lane < deg ? a.col[r.y + ln.lane] : 0;
     load_attn_row(a, ln, r.x, ar);
-    fwd_edges<T, L, V, DROP, R>(a, ln, jj, 0, ln.g, G, deg, (deg + G - 1) / G, r.y, ar, st);
+    fwd_edges<T, L, V, DROP, R, UM>(a, ln, jj, 0, ln.g, G, deg, (deg + G - 1) / G, r.y, ar, st);
     quad_reduce<R>(st);
     fwd_merge_groups<L, W, V>(st);
     fwd_emit<T, L, V>(a, ln, cq, r.x, ln.g == 0, st);
@@ -581,7 +604,7 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
     const int cnt = min(kWave, sg.z - tb);
     const int tn = tb + kSegRound + ln.lane;
     const int jn = tn < sg.z ? a.col[tn] : 0;
-    fwd_edges<T, L, V, DROP, R>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, ar, st);
+    fwd_edges<T, L, V, DROP, R, UM>(a, ln, jj, 0, ln.g, G, cnt, (cnt + G - 1) / G, tb, ar, st);
     jj = jn;
   }
   quad_reduce<R>(st);
@@ -639,14 +662,24 @@ int FwdFlLauncher<T, L, V>::run(hipStream_t st, const GatFwdArgs<T>& a, const Sc
   const int blocks = s.n_seg + mid_blocks + (n_tiny + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
   if (blocks <= 0) return kOk;
   // R lanes per head share the softmax work: min(cq, 4) (cq <= L).
+  const bool big = a.nnz >= big_graph_edges();
   auto launch = [&](auto RC) {
     constexpr int R = decltype(RC)::value;
-    if (a.p > 0.0f)
-      hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, true, R>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
-                         mid_blocks, lgcq);
-    else
-      hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, false, R>), dim3(blocks), dim3(kBlock), 0, st, a, s, n_mid,
-                         mid_blocks, lgcq);
+    if (a.p > 0.0f) {
+      if (big)
+        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, true, R, kFwdUBig>), dim3(blocks), dim3(kBlock), 0, st, a, s,
+                           n_mid, mid_blocks, lgcq);
+      else
+        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, true, R, kFwdU>), dim3(blocks), dim3(kBlock), 0, st, a, s,
+                           n_mid, mid_blocks, lgcq);
+    } else {
+      if (big)
+        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, false, R, kFwdUBig>), dim3(blocks), dim3(kBlock), 0, st, a, s,
+                           n_mid, mid_blocks, lgcq);
+      else
+        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, false, R, kFwdU>), dim3(blocks), dim3(kBlock), 0, st, a, s,
+                           n_mid, mid_blocks, lgcq);
+    }
   };
   if constexpr (L >= 4) {
     if (lgcq >= 2) launch(std::integral_constant<int, 4>());
@@ -1063,6 +1096,80 @@ struct ColBatches {
   }
 };
 
+template <typename T, int L, int V, bool DROP, int R>
+struct ColSharedBatches {
+  static constexpr int W = FlGeom<T>::W;
+  const GatBwdArgs<T>& a;
+  const FlLane<L, V>& ln;
+  int ii, ee, base, first, step, cnt;
+  const float (&ac)[V];
+  ColAcc<W, V>& st;
+
+  // Every lane gathers its g_pre chunk of all U destination rows; the row
+  // record, the exponential and the dropout byte of each (entry, head) pair
+  // are handled once per R lanes of the head (slots r, r + R, ... by lane r,
+  // weights shared by DPP broadcast, t a per-lane partial until
+  // cols_quad_reduce), as in the forward.
+  template <int U>
+  __device__ __forceinline__ void run(int k0) {
+    constexpr int NT = (U + R - 1) / R;
+    float gb[U][W];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int u = first + (k0 + k) * step;
+      const uint64_t i = static_cast<uint32_t>(shfl(ii, (base + (u < cnt ? u : 0)) & (kWave - 1)));
+      load_f32<W>(a.grad_pre + i * a.C + ln.cw * W, gb[k]);
+    }
+    const int r = ln.gl & (R - 1);
+    float wk[NT][V], wl[NT][V];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int kk = R * t + r;
+      const int u = first + (k0 + kk) * step;
+      const bool own = kk < U && u < cnt;
+      const int src = (base + (own ? u : 0)) & (kWave - 1);
+      const uint64_t i = static_cast<uint32_t>(shfl(ii, src));
+      int e = 0;
+      if constexpr (DROP) e = shfl(ee, src);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float4 rs = a.rowstat[i * a.H + ln.hq[v]];
+        const float raw = rs.x + ac[v];
+        const float lp = raw < 0.0f ? a.slope : 1.0f;
+        const float sm = own ? softmax_exp(leaky(raw, a.slope) - rs.y) * rs.z : 0.0f;
+        float w = sm;
+        if constexpr (DROP)
+          w = (own && a.mask[static_cast<int64_t>(e) * a.H + ln.hq[v]] != 0) ? sm * (1.0f / (1.0f - a.p)) : 0.0f;
+        st.t[v] = fmaf(sm * lp, rs.w, st.t[v]);
+        wk[t][v] = w;
+        wl[t][v] = w * lp;
+      }
+    }
+    static_for<U>([&](auto KC) {
+      constexpr int k = decltype(KC)::value;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float w = quad_bcast<R, k % R>(wk[k / R][v]);
+        const float wlk = quad_bcast<R, k % R>(wl[k / R][v]);
+#pragma unroll
+        for (int q = 0; q < W; ++q) {
+          st.ug[v][q] = fmaf(w, gb[k][q], st.ug[v][q]);
+          st.ua[v][q] = fmaf(wlk, gb[k][q], st.ua[v][q]);
+        }
+      }
+    });
+  }
+};
+
+// t of each R-lane set summed (per-lane partials of ColBatches), after a
+// column's or segment's last batch.
+template <int R, int W, int V>
+__device__ __forceinline__ void cols_quad_reduce(ColAcc<W, V>& st) {
+  if constexpr (!cols_pairwise<V>())
+#pragma unroll
+    for (int v = 0; v < V; ++v) st.t[v] = quad_sum<R>(st.t[v]);
+}
+
 // Pairwise batches: pair (slot k, head h) belongs to lane (k % SPR) * S + h of
 // the group in round k / SPR (the PairBits layout). The pair lane loads the
 // destination row's record and the mask byte, forms w = s kw and wl = w l'
@@ -1134,16 +1241,19 @@ struct ColPairBatches {
 
 // ac: attn_col of the column for the lane's chunks' heads (per-lane weights)
 // or, pairwise, ac[0] for the lane's pair head.
-template <typename T, int L, int V, bool DROP>
+template <typename T, int L, int V, bool DROP, int R>
 __device__ __forceinline__ void cols_edges(const GatBwdArgs<T>& a, const FlLane<L, V>& ln, int ii, int ee, int base,
                                            int first, int step, int cnt, int need, const float (&ac)[V],
                                            ColAcc<FlGeom<T>::W, V>& st) {
   if constexpr (cols_pairwise<V>()) {
     ColPairBatches<T, L, V, DROP> cb{a, ln, ii, ee, base, first, step, cnt, ac[0], st};
     for_batches<batch_cap(kColsPairFloats / FlGeom<T>::W, 1)>(need, cb);
-  } else {
+  } else if constexpr (R == 1) {
     ColBatches<T, L, V, DROP> cb{a, ln, ii, ee, base, first, step, cnt, ac, st};
     for_batches<batch_cap(kColsU, V)>(need, cb);
+  } else {
+    ColSharedBatches<T, L, V, DROP, R> cb{a, ln, ii, ee, base, first, step, cnt, ac, st};
+    for_batches<batch_cap(kColsUShared, V)>(need, cb);
   }
 }
 
@@ -1230,7 +1340,7 @@ __device__ __forceinline__ void load_attn_col(const GatBwdArgs<T>& a, const FlLa
   }
 }
 
-template <typename T, int L, int V, bool DROP>
+template <typename T, int L, int V, bool DROP, int R>
 __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a, Sched s, int n_mid, int mid_blocks,
                                                                  int lgcq) {
   constexpr int W = FlGeom<T>::W;
@@ -1278,10 +1388,12 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
     XCol<T, V> xc;
     xc.prefetch(a, ln, j);
     if (tiny) {
-      cols_edges<T, L, V, DROP>(a, ln, ii, ee, ln.g * L, 0, 1, deg, wave_group_max<L>(deg), ac, st);
+      cols_edges<T, L, V, DROP, R>(a, ln, ii, ee, ln.g * L, 0, 1, deg, wave_group_max<L>(deg), ac, st);
+      cols_quad_reduce<R>(st);
       if constexpr (cols_pairwise<V>()) cols_pair_t<L, W, V>(st, ln, false);
     } else {
-      cols_edges<T, L, V, DROP>(a, ln, ii, ee, 0, ln.g, G, deg, (deg + G - 1) / G, ac, st);
+      cols_edges<T, L, V, DROP, R>(a, ln, ii, ee, 0, ln.g, G, deg, (deg + G - 1) / G, ac, st);
+      cols_quad_reduce<R>(st);
       cols_group_sum<L, W, V>(st, ln);
     }
     cols_gac(a, ln, st, xc, j, cq, gac);
@@ -1315,10 +1427,11 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
     const int tn = tb + kSegRound + ln.lane;
     const int in = tn < sg.z ? a.rowind[tn] : 0;
     const int en = DROP && tn < sg.z ? a.perm[tn] : 0;
-    cols_edges<T, L, V, DROP>(a, ln, ii, ee, 0, ln.g, G, cnt, (cnt + G - 1) / G, ac, st);
+    cols_edges<T, L, V, DROP, R>(a, ln, ii, ee, 0, ln.g, G, cnt, (cnt + G - 1) / G, ac, st);
     ii = in;
     ee = en;
   }
+  cols_quad_reduce<R>(st);
   cols_group_sum<L, W, V>(st, ln);
   cols_gac(a, ln, st, xc, j, cq, gac);
   if (ln.g == 0 && ln.cw == 0)
@@ -1410,12 +1523,32 @@ int BwdFlLauncher<T, L, V>::run(hipStream_t st, const GatBwdArgs<T>& a, const Sc
   const int cb = cs.n_seg + c_mid_blocks + (cs.n_light - c_mid + kWavesPerBlock * G - 1) / (kWavesPerBlock * G) +
                  a.n_l2;
   if (cb > 0) {
-    if (a.p > 0.0f)
-      hipLaunchKernelGGL((gat_bwd_cols_fl_kernel<T, L, V, true>), dim3(cb), dim3(kBlock), 0, st, a, cs, c_mid,
-                         c_mid_blocks, lgcq);
-    else
-      hipLaunchKernelGGL((gat_bwd_cols_fl_kernel<T, L, V, false>), dim3(cb), dim3(kBlock), 0, st, a, cs, c_mid,
-                         c_mid_blocks, lgcq);
+    // R lanes per head share the per-entry work of narrow columns (wide
+    // columns have their pairwise batches).
+    auto launch = [&](auto RC) {
+      constexpr int R = decltype(RC)::value;
+      if (a.p > 0.0f)
+        hipLaunchKernelGGL((gat_bwd_cols_fl_kernel<T, L, V, true, R>), dim3(cb), dim3(kBlock), 0, st, a, cs, c_mid,
+                           c_mid_blocks, lgcq);
+      else
+        hipLaunchKernelGGL((gat_bwd_cols_fl_kernel<T, L, V, false, R>), dim3(cb), dim3(kBlock), 0, st, a, cs, c_mid,
+                           c_mid_blocks, lgcq);
+    };
+    // Below kFwdBigGraph edges the columns pass is a few dependent memory
+    // rounds and the exchange costs more than it saves (c2: 25.1 us with it,
+    // 23.7 us without), so every lane keeps its own weights there.
+    const bool share = a.nnz >= big_graph_edges();
+    if constexpr (V == 1 && L >= 4) {
+      if (!share) launch(std::integral_constant<int, 1>());
+      else if (lgcq >= 2) launch(std::integral_constant<int, 4>());
+      else if (lgcq == 1) launch(std::integral_constant<int, 2>());
+      else launch(std::integral_constant<int, 1>());
+    } else if constexpr (V == 1 && L == 2) {
+      if (share && lgcq >= 1) launch(std::integral_constant<int, 2>());
+      else launch(std::integral_constant<int, 1>());
+    } else {
+      launch(std::integral_constant<int, 1>());
+    }
   }
   return check_launch("cign_gat_bwd (cols, feature layout)");
 }

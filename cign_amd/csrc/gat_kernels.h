@@ -145,6 +145,7 @@ struct Lanes {
 template <typename T>
 struct GatFwdArgs {
   int n, H, C;
+  int64_t nnz;
   float slope, p;
   uint64_t seed;
   bool vec;  // 16-byte loads of x rows are legal

@@ -78,13 +78,19 @@ def _forward(ext, agg_mode, *args):
     return ext.forward(*args), None
 
 
+@pytest.mark.parametrize("big", [False, True], ids=["small-graph-kernels", "large-graph-kernels"])
 @pytest.mark.parametrize("agg_mode", [False, True])
 @pytest.mark.parametrize("H,C,p,dtype,n,hubs", CASES)
-def test_ext_forward_backward_matches_oracle(H, C, p, dtype, n, hubs, agg_mode):
+def test_ext_forward_backward_matches_oracle(H, C, p, dtype, n, hubs, agg_mode, big, monkeypatch):
+    """big: the kernel variants the library runs from 4M edges up (the lanes
+    of a head sharing the softmax work, other batch caps), forced at these
+    sizes through CIGN_GAT_BIG_GRAPH_EDGES=0."""
     from cign_amd import _lib
     from cign_amd.collapsed_gat import ensure_collapsed_gat_loaded
 
-    print(f"gat ext H={H} C={C} p={p} dtype={dtype} n={n} agg={agg_mode}", flush=True)
+    if big:
+        monkeypatch.setenv("CIGN_GAT_BIG_GRAPH_EDGES", "0")
+    print(f"gat ext H={H} C={C} p={p} dtype={dtype} n={n} agg={agg_mode} big={big}", flush=True)
     rng = np.random.default_rng(H * 1000 + C)
     ei = _graph(rng, n, hubs)
     rowptr, col, row, colptr, perm = _dev_graph(ei, n)
@@ -262,15 +268,18 @@ def test_argument_errors(c2):
                                      torch.zeros(n, 4, 4, device="cuda"), None, 0.0)
 
 
+@pytest.mark.parametrize("big", [False, True], ids=["small-graph-kernels", "large-graph-kernels"])
 @pytest.mark.parametrize("agg_mode", [False, True])
 @pytest.mark.parametrize("seg", [256, 1024, 4096])
 @pytest.mark.parametrize("dtype,p", [(torch.float32, 0.0), (torch.float32, 0.2), (torch.bfloat16, 0.0)])
-def test_long_segments_multi_round(seg, dtype, p, agg_mode, monkeypatch):
+def test_long_segments_multi_round(seg, dtype, p, agg_mode, big, monkeypatch):
     """Hub rows/columns of 2,500-6,000 edges cut into segments of `seg` edges
     (several 256-edge rounds per workgroup, several workgroups per row)."""
     import cign_amd.schedule as S
 
-    print(f"gat long segments seg={seg} dtype={dtype} p={p} agg={agg_mode}", flush=True)
+    if big:
+        monkeypatch.setenv("CIGN_GAT_BIG_GRAPH_EDGES", "0")
+    print(f"gat long segments seg={seg} dtype={dtype} p={p} agg={agg_mode} big={big}", flush=True)
     monkeypatch.setattr(S, "segment_edges_for", lambda nnz, floor=512: seg)
     S._CACHE.clear()
     rng = np.random.default_rng(seg)
