@@ -178,8 +178,10 @@ def summarize(prof_dir: str, name: str, command: str) -> None:
         lines.append(f"{_short(r['Name'])[:72]:72s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} "
                      f"{float(r['MinNs']) / 1e3:9.2f} {float(r['MaxNs']) / 1e3:9.2f} {float(r['Percentage']):6.2f}")
     (out / f"{name}_kernel_stats.txt").write_text("\n".join(lines) + "\n")
+    if (prof / "mfma").exists():
+        _summarize_mfma(prof, name, command, {_short(r["Name"]): float(r["AverageNs"]) for r in stats})
     if not (prof / "fetch").exists():
-        print(f"wrote profiles/{name}_kernel_stats.txt (no counter runs)")
+        print(f"wrote profiles/{name}_kernel_stats.txt (no traffic counter runs)")
         return
 
     def counters(sub, counter):
@@ -224,6 +226,41 @@ def summarize(prof_dir: str, name: str, command: str) -> None:
 
 
 MFMA_PEAK = {"f32": 157.3, "bf16": 2500.0}  # MI355X dense matrix TFLOP/s
+
+
+def _summarize_mfma(prof: Path, name: str, command: str, avg_ns: dict) -> None:
+    """profiles/<name>_mfma.txt from <prof>/mfma (rocprofv3 --pmc MfmaUtil
+    SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_INSTS_VALU_MFMA_MOPS_F32): per MFMA kernel
+    the matrix-core busy share (MfmaUtil, percent of SIMD cycles while the
+    kernel ran), the flops it issued (MOPS x 512) and those flops over the
+    kernel's average duration from the kernel trace, against the dense peak
+    of its operand type."""
+    import csv
+    import glob
+    import statistics
+
+    per = {}
+    f = glob.glob(str(prof / "mfma" / "*_counter_collection.csv"))[0]
+    for r in csv.DictReader(open(f)):
+        per.setdefault(_short(r["Kernel_Name"]), {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    lines = [f"# rocprofv3 --pmc MfmaUtil SQ_INSTS_VALU_MFMA_MOPS_BF16 SQ_INSTS_VALU_MFMA_MOPS_F32: {name}", "",
+             "Command (from the repository root, GPU box):", "", "    " + command.replace("\n", "\n    "), "",
+             "MfmaUtil = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x SIMDs), percent; flops = MOPS x 512 per",
+             "dispatch (median); TFLOP/s = flops / the kernel trace's average duration; peak = dense MI355X",
+             "(bf16 2500, fp32 157.3 TFLOP/s).", "",
+             f"{'kernel':56s} {'MfmaUtil%':>9s} {'GFLOP':>8s} {'avg_us':>8s} {'TFLOP/s':>8s} {'of peak':>8s}"]
+    for k, c in sorted(per.items()):
+        bf = statistics.median(c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", [0.0])) * 512
+        f32 = statistics.median(c.get("SQ_INSTS_VALU_MFMA_MOPS_F32", [0.0])) * 512
+        if bf + f32 == 0 or k not in avg_ns:
+            continue
+        util = statistics.median(c.get("MfmaUtil", [float("nan")]))
+        tf = (bf + f32) / (avg_ns[k] * 1e-9) / 1e12
+        peak = MFMA_PEAK["bf16"] if bf >= f32 else MFMA_PEAK["f32"]
+        lines.append(f"{k[:56]:56s} {util:9.1f} {(bf + f32) / 1e9:8.2f} {avg_ns[k] / 1e3:8.2f} {tf:8.1f} "
+                     f"{100 * tf / peak:7.1f}%")
+    (ROOT / "profiles" / f"{name}_mfma.txt").write_text("\n".join(lines) + "\n")
+    print(f"wrote profiles/{name}_mfma.txt")
 
 
 def time_components(comps: dict, dtype: str, torch):

@@ -10,9 +10,10 @@
 //   proj + dropout-gamma-residual          g = x W^T + b, out = h + gamma * drop(g)
 //                                          (model_cign.py:927-933, fused_block_ops
 //                                          gamma residual, keep = 53-bit splitmix64)
-//   backward                               grad_x = grad_y W, grad_W = grad_y^T x
-//                                          (plain GEMMs, rocBLAS), grad_b = sum_n
-//                                          grad_y (chunked column sums)
+//   backward                               grad_x = grad_y W (the forward kernel
+//                                          against W^T), grad_W = grad_y^T x
+//                                          (split-M MFMA partials), grad_b =
+//                                          sum_n grad_y (chunked column sums)
 //
 // Math: fp32 (v_mfma_f32_16x16x4_f32, exact fp32 products) or bf16
 // (v_mfma_f32_16x16x32_bf16, the autocast path of _local_amp_linear: operands
@@ -34,13 +35,7 @@
 // column l%16 and the same k-slice, D holds rows 4*(l/16)+i, i < 4, of
 // column l%16.
 #include <algorithm>
-#include <mutex>
 #include <type_traits>
-
-#include <hipblaslt/hipblaslt.h>
-#include <rocblas/rocblas.h>
-
-#include <vector>
 
 #include "rowops.h"
 
@@ -695,11 +690,26 @@ __global__ __launch_bounds__(kThreads) void bias_grad_kernel(const float* gy, in
     part[static_cast<int64_t>(blockIdx.y) * N + n] = red[t] + red[t + 64] + red[t + 128] + red[t + 192];
 }
 
-// dst[i] = bf16(src[i])
-__global__ void to_bf16_kernel(const float* src, int64_t n, __bf16* dst) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    dst[i] = static_cast<__bf16>(src[i]);
+// wt [K, N] = w [N, K]^T through a 32 x 32 LDS tile (row stride 33 floats,
+// so the column reads of the transposed store fall on distinct banks). Grid
+// (ceil(K/32), ceil(N/32)), 256 threads, four rows each; reads and writes are
+// 128-byte row segments.
+__global__ void __launch_bounds__(256) transpose_w_kernel(const float* __restrict__ w, int N, int K,
+                                                         float* __restrict__ wt) {
+  __shared__ float tile[32][33];
+  const int k0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
+  const int c = threadIdx.x & 31, r0 = threadIdx.x >> 5;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = r0 + 8 * i;
+    if (n0 + r < N && k0 + c < K) tile[r][c] = w[static_cast<int64_t>(n0 + r) * K + k0 + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = r0 + 8 * i;
+    if (k0 + r < K && n0 + c < N) wt[static_cast<int64_t>(k0 + r) * N + n0 + c] = tile[c][r];
+  }
 }
 
 // ---- grad_W = grad_y^T x of the larger projections: a reduction over the
@@ -1014,34 +1024,13 @@ inline bool rows_aligned(const void* x, int x_dtype, const float* w, int K) {
   return aligned16(x) && aligned16(w) && xrow % 16 == 0 && (K * 4) % 16 == 0;
 }
 
-// One rocBLAS handle per device, created on first use.
-rocblas_handle blas_handle(int& rc) {
-  static std::mutex mu;
-  static rocblas_handle handles[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
-    rc = set_error(kHipError, "cign_linear_bwd: no current HIP device");
-    return nullptr;
-  }
-  std::lock_guard<std::mutex> lock(mu);
-  if (!handles[dev] && rocblas_create_handle(&handles[dev]) != rocblas_status_success) {
-    handles[dev] = nullptr;
-    rc = set_error(kHipError, "cign_linear_bwd: rocblas_create_handle failed");
-    return nullptr;
-  }
-  rc = kOk;
-  return handles[dev];
-}
-
 // Workspace layout of cign_linear_bwd.
 struct BwdWs {
   int chunks, wg_chunks;
-  int64_t chunk, wg_chunk, part_b, part_w, gy16, w16, lt, total;
+  int64_t chunk, wg_chunk, part_b, part_w, wt, total;
 };
 
-constexpr int64_t kLtWs = 16 << 20;  // hipBLASLt workspace carved from the caller's
-
-inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias, int math) {
+inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias) {
   BwdWs L;
   // row chunks of the bias (and, for few outputs, grad_W) partials: 64 rows,
   // or 16 for few outputs (more workgroups for the per-chunk VALU sums)
@@ -1063,99 +1052,10 @@ inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias, int math) {
   wgc = M > 0 ? (M + L.wg_chunk - 1) / L.wg_chunk : 1;
   L.wg_chunks = static_cast<int>(wgc);
   L.part_w = off; off = al(off + 4LL * (small ? chunks : wgc) * N * K);
-  // grad_x on the library GEMM: bf16 copies of grad_y and W under autocast
-  const bool b16 = math == kMathBF16 && !small;
-  L.gy16 = off; off = al(off + (b16 ? 2LL * M * N : 0));
-  L.w16 = off; off = al(off + (b16 ? 2LL * N * K : 0));
-  L.lt = off; off = al(off + (small ? 0 : kLtWs));
+  // grad_x = grad_y W runs on the forward NT kernel against W^T [K, N]
+  L.wt = off; off = al(off + (small ? 0 : 4LL * N * K));
   L.total = off;
   return L;
-}
-
-// ---- hipBLASLt for the backward's plain GEMMs (D = op(A) op(B), column
-// major, fp32 accumulation and output), one handle per device and one
-// heuristic choice per problem, cached; problems it has no kernel for fall
-// back to rocBLAS.
-
-struct LtPlan {
-  int dev, ta, tb, in_t;
-  int64_t m, n, k, lda, ldb, ldd;
-  bool ok;
-  hipblasLtMatmulDesc_t desc;
-  hipblasLtMatrixLayout_t a, b, d;
-  hipblasLtMatmulAlgo_t algo;
-  size_t ws;
-};
-
-hipblasLtHandle_t lt_handle(int dev) {
-  static std::mutex mu;
-  static hipblasLtHandle_t handles[64] = {};
-  if (dev < 0 || dev >= 64) return nullptr;
-  std::lock_guard<std::mutex> lock(mu);
-  if (!handles[dev] && hipblasLtCreate(&handles[dev]) != HIPBLAS_STATUS_SUCCESS) handles[dev] = nullptr;
-  return handles[dev];
-}
-
-// The cached plan of a problem (ok = false: no hipBLASLt kernel for it).
-const LtPlan* lt_plan(int dev, hipblasLtHandle_t h, int ta, int tb, int64_t m, int64_t n, int64_t k, int in_t,
-                      int64_t lda, int64_t ldb, int64_t ldd) {
-  static std::mutex mu;
-  static std::vector<LtPlan*> cache;
-  std::lock_guard<std::mutex> lock(mu);
-  for (const LtPlan* p : cache)
-    if (p->dev == dev && p->ta == ta && p->tb == tb && p->m == m && p->n == n && p->k == k && p->in_t == in_t &&
-        p->lda == lda && p->ldb == ldb && p->ldd == ldd)
-      return p;
-  LtPlan* p = new LtPlan{dev, ta, tb, in_t, m, n, k, lda, ldb, ldd, false, nullptr, nullptr, nullptr, nullptr, {}, 0};
-  cache.push_back(p);
-  const hipDataType it = static_cast<hipDataType>(in_t);
-  const hipblasOperation_t oa = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, ob = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
-  if (hipblasLtMatmulDescCreate(&p->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return p;
-  if (hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &oa, sizeof(oa)) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &ob, sizeof(ob)) != HIPBLAS_STATUS_SUCCESS)
-    return p;
-  if (hipblasLtMatrixLayoutCreate(&p->a, it, ta ? k : m, ta ? m : k, lda) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatrixLayoutCreate(&p->b, it, tb ? n : k, tb ? k : n, ldb) != HIPBLAS_STATUS_SUCCESS ||
-      hipblasLtMatrixLayoutCreate(&p->d, HIP_R_32F, m, n, ldd) != HIPBLAS_STATUS_SUCCESS)
-    return p;
-  hipblasLtMatmulPreference_t pref;
-  if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return p;
-  const uint64_t max_ws = kLtWs;
-  hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &max_ws, sizeof(max_ws));
-  hipblasLtMatmulHeuristicResult_t res[1];
-  int count = 0;
-  if (hipblasLtMatmulAlgoGetHeuristic(h, p->desc, p->a, p->b, p->d, p->d, pref, 1, res, &count) ==
-          HIPBLAS_STATUS_SUCCESS &&
-      count > 0 && res[0].state == HIPBLAS_STATUS_SUCCESS && static_cast<int64_t>(res[0].workspaceSize) <= kLtWs) {
-    p->algo = res[0].algo;
-    p->ws = res[0].workspaceSize;
-    p->ok = true;
-  }
-  hipblasLtMatmulPreferenceDestroy(pref);
-  return p;
-}
-
-// D (fp32) = op(A) op(B) through hipBLASLt; false when it has no kernel (the
-// caller then uses rocBLAS), an error code in rc when the call fails.
-bool lt_gemm(hipStream_t st, int ta, int tb, int64_t m, int64_t n, int64_t k, const void* A, int64_t lda,
-             const void* B, int64_t ldb, float* D, int64_t ldd, int in_t, void* ws, int& rc) {
-  rc = kOk;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return false;
-  hipblasLtHandle_t h = lt_handle(dev);
-  if (!h) return false;
-  const LtPlan* p = lt_plan(dev, h, ta, tb, m, n, k, in_t, lda, ldb, ldd);
-  if (!p->ok) return false;
-  const float one = 1.0f, zero = 0.0f;
-  if (hipblasLtMatmul(h, p->desc, &one, A, p->a, B, p->b, &zero, D, p->d, D, p->d, &p->algo, ws, p->ws, st) !=
-      HIPBLAS_STATUS_SUCCESS)
-    rc = set_error(kHipError, "cign_linear_bwd: hipblasLtMatmul failed");
-  return true;
-}
-
-inline int blas_check(rocblas_status s, const char* what) {
-  return s == rocblas_status_success ? kOk
-                                     : set_error(kHipError, "cign_linear_bwd: %s failed (rocblas %d)", what, static_cast<int>(s));
 }
 
 }  // namespace gemm
@@ -1221,8 +1121,7 @@ int cign_linear_gamma_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t
 }
 
 int64_t cign_linear_bwd_workspace_bytes(int64_t M, int32_t N, int32_t K, int32_t with_bias) {
-  // sized for either math (the bf16 operand copies are used with math = 1)
-  return bwd_ws(M, N, K, with_bias != 0, kMathBF16).total;
+  return bwd_ws(M, N, K, with_bias != 0).total;
 }
 
 int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math, const float* grad_y, const float* x,
@@ -1232,7 +1131,7 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
   if (!w || !grad_w || (M > 0 && (!grad_y || !x))) return set_error(kInvalid, "cign_linear_bwd: null pointer");
   if (math != kMathF32 && math != kMathBF16) return set_error(kInvalid, "cign_linear_bwd: math must be 0 or 1");
   if (M > 0x7fffffff) return set_error(kInvalid, "cign_linear_bwd: M too large");
-  const BwdWs L = bwd_ws(M, N, K, grad_b != nullptr, math);
+  const BwdWs L = bwd_ws(M, N, K, grad_b != nullptr);
   if (workspace_bytes < L.total || (L.total > 0 && !workspace))
     return set_error(kInvalid, "cign_linear_bwd: workspace too small (%lld < %lld)",
                      static_cast<long long>(workspace_bytes), static_cast<long long>(L.total));
@@ -1287,37 +1186,19 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
       return rc;
   }
   if (!grad_x) return bias_grad();
-  // grad_x [M,K] = grad_y [M,N] W [N,K] on the library GEMM. Row-major C = A B
-  // is column-major C^T = B^T A^T: (K x M) = W_cm (K x N) * gy_cm (N x M).
-  const void *gy_op = grad_y, *w_op = w;
-  rocblas_datatype in_t = rocblas_datatype_f32_r;
-  if (math == kMathBF16) {
-    // autocast semantics: the backward GEMM reads bf16 operands
-    __bf16* gy16 = reinterpret_cast<__bf16*>(ws + L.gy16);
-    __bf16* w16 = reinterpret_cast<__bf16*>(ws + L.w16);
-    auto conv = [&](const float* src, int64_t n, __bf16* d) {
-      const int64_t gb = std::min<int64_t>((n + 255) / 256, 8192);
-      hipLaunchKernelGGL(to_bf16_kernel, dim3(static_cast<unsigned>(gb)), dim3(256), 0, st, src, n, d);
-      return check_launch("cign_linear_bwd (bf16 operands)");
-    };
-    if ((rc = conv(grad_y, M * N, gy16)) || (rc = conv(w, static_cast<int64_t>(N) * K, w16))) return rc;
-    gy_op = gy16;
-    w_op = w16;
-    in_t = rocblas_datatype_bf16_r;
-  }
-  const int lt_t = math == kMathBF16 ? HIP_R_16BF : HIP_R_32F;
-  if (!lt_gemm(st, 0, 0, K, M, N, w_op, K, gy_op, N, grad_x, K, lt_t, ws + L.lt, rc)) {
-    rocblas_handle hdl = blas_handle(rc);
-    if (!hdl) return rc;
-    if ((rc = blas_check(rocblas_set_stream(hdl, st), "rocblas_set_stream"))) return rc;
-    const float one = 1.0f, zero = 0.0f;
-    rc = blas_check(rocblas_gemm_ex(hdl, rocblas_operation_none, rocblas_operation_none, K, static_cast<int>(M), N,
-                                    &one, w_op, in_t, K, gy_op, in_t, N, &zero, grad_x, rocblas_datatype_f32_r, K,
-                                    grad_x, rocblas_datatype_f32_r, K, rocblas_datatype_f32_r,
-                                    rocblas_gemm_algo_standard, 0, 0),
-                    "grad_x gemm");
-  }
-  if (rc) return rc;
+  // grad_x [M,K] = grad_y [M,N] W [N,K] = grad_y (W^T)^T: the forward NT
+  // kernel with W^T [K,N] as its weight. Under bf16 math it rounds both
+  // operands to bf16 as autocast's backward GEMM reads them; the output stays
+  // fp32 (not rounded).
+  float* wt = reinterpret_cast<float*>(ws + L.wt);
+  hipLaunchKernelGGL(transpose_w_kernel, dim3((K + 31) / 32, (N + 31) / 32), dim3(256), 0, st, w, N, K, wt);
+  if ((rc = check_launch("cign_linear_bwd (W^T)"))) return rc;
+  GemmArgs g{};
+  g.M = M; g.N = K; g.K = N; g.x = grad_y; g.w = wt; g.y = grad_x;
+  g.vec = rows_aligned(grad_y, kF32, wt, N);
+  g.vec4 = K % 4 == 0 && aligned16(grad_x);
+  g.round_bf16 = false;
+  if ((rc = dispatch_nt<kEpiStore>(st, g, kF32, math, pick_bn(K, 0, math)))) return rc;
   return bias_grad();
 }
 

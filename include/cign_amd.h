@@ -347,7 +347,8 @@ int cign_linear_gamma_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t
 /* Workspace bytes of cign_linear_bwd. */
 int64_t cign_linear_bwd_workspace_bytes(int64_t M, int32_t N, int32_t K, int32_t with_bias);
 
-/* grad_x [M,K] = grad_y W (NULL to skip; a hipBLASLt GEMM), grad_w [N,K] =
+/* grad_x [M,K] = grad_y W (NULL to skip; the forward MFMA kernel against
+ * W^T, which the workspace holds), grad_w [N,K] =
  * grad_y^T x (split-M MFMA partials summed in order) and grad_b [N] =
  * sum_m grad_y (NULL to skip), fp32 accumulation, grad_w and grad_b
  * deterministic; with math = 1 every product reads bf16-rounded operands (the
