@@ -41,6 +41,10 @@ _SIGNATURES = {
     "cign_gat_bwd_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32, _I32, _I32]),
     "cign_gat_bwd": (C.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _F32, _F32] + [_P] * 11
                      + [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P]),
+    "cign_gat_fwd_shard": (C.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _F32, _P, _P, _F32,
+                                     _U64, _P, _P, _P, _P, _P, _P, _I64, _P, _I64, _I64]),
+    "cign_gat_bwd_shard": (C.c_int, [_P, _I32, _I32, _I32, _I32, _I32, _F32, _F32] + [_P] * 11
+                           + [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _I32, _I32, _I64]),
     # GAT side ops and block ops (nodeops.hip)
     "cign_colsum_workspace_bytes": (_I64, [_I64, _I32, _I32]),
     "cign_attn_logits_fwd": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P]),

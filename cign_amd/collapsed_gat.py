@@ -225,8 +225,14 @@ def collapsed_gat_mean_bias_silu(attn_row: torch.Tensor, attn_col: torch.Tensor,
     if not (1 <= H <= 32):
         raise ValueError(f"collapsed GAT requires 1<=H<=32; got H={H}")
     (rowptr, col), (row, colptr) = csr, csc
+    return _CollapsedGATFn.apply(attn_row, attn_col, rowptr, col, colptr, row, perm, float(negative_slope), in_feat,
+                                 bias, float(attn_drop), next_seed(attn_drop))
+
+
+def next_seed(attn_drop: float) -> int:
+    """Dropout seed of the next collapsed-GAT call (collapsed_gat.py:204-211):
+    torch.initial_seed() plus a per-process call counter that only advances
+    when attn_drop > 0; 0 without dropout."""
     base_seed = int(torch.initial_seed()) & ((1 << 63) - 1)
     call_id = next(_CALL_COUNTER) if float(attn_drop) > 0.0 else -1
-    seed = 0 if call_id < 0 else (base_seed + 0x9E3779B97F4A7C15 * (call_id + 1)) & ((1 << 63) - 1)
-    return _CollapsedGATFn.apply(attn_row, attn_col, rowptr, col, colptr, row, perm, float(negative_slope), in_feat,
-                                 bias, float(attn_drop), int(seed))
+    return 0 if call_id < 0 else (base_seed + 0x9E3779B97F4A7C15 * (call_id + 1)) & ((1 << 63) - 1)

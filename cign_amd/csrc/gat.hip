@@ -213,11 +213,18 @@ int64_t cign_gat_row_agg_floats(int32_t dtype, int32_t n, int32_t heads, int32_t
 
 // Collapsed GAT forward. Replaces the ext `forward` of the reference
 // (collapsed_gat_ext/collapsed_gat.cpp:45-72 -> collapsed_gat_cuda.cu:434-478).
-int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
+}  // extern "C"
+
+namespace {
+
+// cign_gat_fwd over the whole graph (edge_base 0, graph_nnz = nnz) or one
+// destination-row shard of it.
+int gat_fwd_impl(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
                  const float* attn_row, const float* attn_col, const int32_t* col, const int32_t* row_sched,
                  const int32_t* row_sched_info, int32_t* row_counters, float negative_slope, const void* in_feat,
                  const float* bias, float attn_drop, uint64_t seed, void* out, float* pre, float* edge_max,
-                 float* edge_sum, uint8_t* edge_mask, void* workspace, int64_t workspace_bytes, float* row_agg) {
+                 float* edge_sum, uint8_t* edge_mask, void* workspace, int64_t workspace_bytes, float* row_agg,
+                 int64_t edge_base, int64_t graph_nnz) {
   int rc = check_shape("cign_gat_fwd", n, nnz, heads, channels);
   if (rc) return rc;
   if (!(attn_drop >= 0.0f && attn_drop < 1.0f)) return set_error(kInvalid, "cign_gat_fwd: attn_drop must be in [0,1)");
@@ -236,7 +243,7 @@ int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
   auto fill = [&](auto* xt, auto* ot) {
     using T = std::remove_cv_t<std::remove_pointer_t<decltype(ot)>>;
     GatFwdArgs<T> a;
-    a.n = n; a.H = heads; a.C = channels; a.nnz = nnz;
+    a.n = n; a.H = heads; a.C = channels; a.graph_nnz = graph_nnz; a.mask_base = edge_base * heads;
     a.slope = negative_slope; a.p = attn_drop; a.seed = seed;
     a.vec = aligned16(xt) && (channels * static_cast<int>(sizeof(T))) % 16 == 0;
     a.attn_row = attn_row; a.attn_col = attn_col; a.col = col;
@@ -261,21 +268,55 @@ int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
   return set_error(kInvalid, "cign_gat_fwd: unsupported dtype %d", dtype);
 }
 
+}  // namespace
+
+extern "C" {
+
+int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
+                 const float* attn_row, const float* attn_col, const int32_t* col, const int32_t* row_sched,
+                 const int32_t* row_sched_info, int32_t* row_counters, float negative_slope, const void* in_feat,
+                 const float* bias, float attn_drop, uint64_t seed, void* out, float* pre, float* edge_max,
+                 float* edge_sum, uint8_t* edge_mask, void* workspace, int64_t workspace_bytes, float* row_agg) {
+  return gat_fwd_impl(stream, dtype, n, nnz, heads, channels, attn_row, attn_col, col, row_sched, row_sched_info,
+                      row_counters, negative_slope, in_feat, bias, attn_drop, seed, out, pre, edge_max, edge_sum,
+                      edge_mask, workspace, workspace_bytes, row_agg, 0, nnz);
+}
+
+int cign_gat_fwd_shard(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
+                       const float* attn_row, const float* attn_col, const int32_t* col, const int32_t* row_sched,
+                       const int32_t* row_sched_info, int32_t* row_counters, float negative_slope,
+                       const void* in_feat, const float* bias, float attn_drop, uint64_t seed, void* out, float* pre,
+                       float* edge_max, float* edge_sum, uint8_t* edge_mask, void* workspace,
+                       int64_t workspace_bytes, float* row_agg, int64_t edge_base, int64_t graph_nnz) {
+  if (edge_base < 0 || graph_nnz < nnz || edge_base > graph_nnz - nnz)
+    return set_error(kInvalid, "cign_gat_fwd_shard: edges [%lld, %lld) outside a graph of %lld edges",
+                     static_cast<long long>(edge_base), static_cast<long long>(edge_base) + nnz,
+                     static_cast<long long>(graph_nnz));
+  return gat_fwd_impl(stream, dtype, n, nnz, heads, channels, attn_row, attn_col, col, row_sched, row_sched_info,
+                      row_counters, negative_slope, in_feat, bias, attn_drop, seed, out, pre, edge_max, edge_sum,
+                      edge_mask, workspace, workspace_bytes, row_agg, edge_base, graph_nnz);
+}
+
 int64_t cign_gat_bwd_workspace_bytes(int32_t n, int32_t nnz, int32_t heads, int32_t channels, int32_t row_blocks,
                                      int32_t n_seg_rows, int32_t n_seg_cols) {
   return bwd_layout(n, nnz, heads, channels, row_blocks, n_seg_rows, n_seg_cols).total;
 }
 
-// Collapsed GAT backward. Replaces the ext `backward` of the reference
-// (collapsed_gat_ext/collapsed_gat.cpp:74-102 -> collapsed_gat_cuda.cu:480-545).
-int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
+}  // extern "C"
+
+namespace {
+
+// cign_gat_bwd over the whole graph (bias rows [0, n), graph_nnz = nnz) or
+// one source-column shard of it.
+int gat_bwd_impl(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
                  float negative_slope, float attn_drop, const int32_t* col, const int32_t* rowind,
                  const int32_t* perm, const float* edge_max, const float* edge_sum, const uint8_t* edge_mask,
                  const void* in_feat, const float* attn_row, const float* attn_col, const float* pre,
                  const void* grad_y, const int32_t* row_sched, const int32_t* row_sched_info,
                  int32_t* row_counters, const int32_t* col_sched, const int32_t* col_sched_info,
                  int32_t* col_counters, void* workspace, int64_t workspace_bytes, void* grad_feat,
-                 float* grad_attn_row, float* grad_attn_col, float* grad_bias, const float* row_agg) {
+                 float* grad_attn_row, float* grad_attn_col, float* grad_bias, const float* row_agg,
+                 int32_t bias_lo, int32_t bias_n, int64_t graph_nnz) {
   int rc = check_shape("cign_gat_bwd", n, nnz, heads, channels);
   if (row_agg && (cign_gat_row_agg_floats(dtype, n, heads, channels) == 0 || !aligned16(row_agg)))
     return set_error(kInvalid, "cign_gat_bwd: row_agg must be null for this shape (cign_gat_row_agg_floats) or "
@@ -303,6 +344,7 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
     using T = std::remove_cv_t<std::remove_pointer_t<decltype(gxt)>>;
     GatBwdArgs<T> a;
     a.n = n; a.nnz = nnz; a.H = heads; a.C = channels;
+    a.graph_nnz = graph_nnz; a.bias_lo = bias_lo; a.bias_n = bias_n;
     a.slope = negative_slope; a.p = attn_drop; a.inv_h = 1.0f / static_cast<float>(heads);
     a.vec_x = aligned16(xt) && (channels * static_cast<int>(sizeof(T))) % 16 == 0;
     a.vec_gp = (channels % 4) == 0;
@@ -329,7 +371,7 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
       auto go = [&](auto LC, auto VC) {
         constexpr int LL = decltype(LC)::value, VV = decltype(VC)::value;
         a.rows_blocks = BwdFlLauncher<T, LL, VV>::row_blocks(rs, row_sched_info);
-        a.n_l2 = fl_bias_blocks(n);
+        a.n_l2 = fl_bias_blocks(bias_n);
         return BwdFlLauncher<T, LL, VV>::run(st, a, rs, row_sched_info, cs, col_sched_info, lgcq);
       };
       return fl_dispatch(L, V, go);
@@ -343,6 +385,49 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
   if (dtype == kBF16)
     return fill(static_cast<const bf16*>(in_feat), static_cast<const bf16*>(grad_y), static_cast<bf16*>(grad_feat));
   return set_error(kInvalid, "cign_gat_bwd: unsupported dtype %d", dtype);
+}
+
+}  // namespace
+
+extern "C" {
+
+// Collapsed GAT backward. Replaces the ext `backward` of the reference
+// (collapsed_gat_ext/collapsed_gat.cpp:74-102 -> collapsed_gat_cuda.cu:480-545).
+int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
+                 float negative_slope, float attn_drop, const int32_t* col, const int32_t* rowind,
+                 const int32_t* perm, const float* edge_max, const float* edge_sum, const uint8_t* edge_mask,
+                 const void* in_feat, const float* attn_row, const float* attn_col, const float* pre,
+                 const void* grad_y, const int32_t* row_sched, const int32_t* row_sched_info,
+                 int32_t* row_counters, const int32_t* col_sched, const int32_t* col_sched_info,
+                 int32_t* col_counters, void* workspace, int64_t workspace_bytes, void* grad_feat,
+                 float* grad_attn_row, float* grad_attn_col, float* grad_bias, const float* row_agg) {
+  return gat_bwd_impl(stream, dtype, n, nnz, heads, channels, negative_slope, attn_drop, col, rowind, perm, edge_max,
+                      edge_sum, edge_mask, in_feat, attn_row, attn_col, pre, grad_y, row_sched, row_sched_info,
+                      row_counters, col_sched, col_sched_info, col_counters, workspace, workspace_bytes, grad_feat,
+                      grad_attn_row, grad_attn_col, grad_bias, row_agg, 0, n, nnz);
+}
+
+int cign_gat_bwd_shard(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
+                       float negative_slope, float attn_drop, const int32_t* col, const int32_t* rowind,
+                       const int32_t* perm, const float* edge_max, const float* edge_sum, const uint8_t* edge_mask,
+                       const void* in_feat, const float* attn_row, const float* attn_col, const float* pre,
+                       const void* grad_y, const int32_t* row_sched, const int32_t* row_sched_info,
+                       int32_t* row_counters, const int32_t* col_sched, const int32_t* col_sched_info,
+                       int32_t* col_counters, void* workspace, int64_t workspace_bytes, void* grad_feat,
+                       float* grad_attn_row, float* grad_attn_col, float* grad_bias, const float* row_agg,
+                       int32_t bias_row_lo, int32_t bias_rows, int64_t graph_nnz) {
+  if (!row_agg || cign_gat_row_agg_floats(dtype, n, heads, channels) == 0)
+    return set_error(kInvalid, "cign_gat_bwd_shard: needs the forward's row_agg (a feature-layout shape): the halo "
+                     "destination rows have only part of their in-edges in a column shard");
+  if (bias_row_lo < 0 || bias_rows < 0 || bias_row_lo > n - bias_rows)
+    return set_error(kInvalid, "cign_gat_bwd_shard: bias rows [%d, %d) outside [0, %d)", bias_row_lo,
+                     bias_row_lo + bias_rows, n);
+  if (graph_nnz < nnz) return set_error(kInvalid, "cign_gat_bwd_shard: graph_nnz %lld < shard edges %d",
+                                        static_cast<long long>(graph_nnz), nnz);
+  return gat_bwd_impl(stream, dtype, n, nnz, heads, channels, negative_slope, attn_drop, col, rowind, perm, edge_max,
+                      edge_sum, edge_mask, in_feat, attn_row, attn_col, pre, grad_y, row_sched, row_sched_info,
+                      row_counters, col_sched, col_sched_info, col_counters, workspace, workspace_bytes, grad_feat,
+                      grad_attn_row, grad_attn_col, grad_bias, row_agg, bias_row_lo, bias_rows, graph_nnz);
 }
 
 }  // extern "C"

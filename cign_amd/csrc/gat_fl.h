@@ -378,7 +378,7 @@ struct FwdBatches {
         float w = pk;
         if constexpr (DROP) {
           const int64_t idx = static_cast<int64_t>(ebase + uo[t]) * a.H + ln.hq[v];
-          const bool keep = gat_keep(a.seed, static_cast<uint64_t>(idx), a.p);
+          const bool keep = gat_keep(a.seed, static_cast<uint64_t>(idx + a.mask_base), a.p);
           if (own[t] && ln.qv[v]) a.mask[idx] = keep ? 1 : 0;
           w = keep ? pk * (1.0f / (1.0f - a.p)) : 0.0f;
         }
@@ -662,7 +662,7 @@ int FwdFlLauncher<T, L, V>::run(hipStream_t st, const GatFwdArgs<T>& a, const Sc
   const int blocks = s.n_seg + mid_blocks + (n_tiny + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
   if (blocks <= 0) return kOk;
   // R lanes per head share the softmax work: min(cq, 4) (cq <= L).
-  const bool big = a.nnz >= big_graph_edges();
+  const bool big = a.graph_nnz >= big_graph_edges();
   auto launch = [&](auto RC) {
     constexpr int R = decltype(RC)::value;
     if (a.p > 0.0f) {
@@ -1537,7 +1537,7 @@ int BwdFlLauncher<T, L, V>::run(hipStream_t st, const GatBwdArgs<T>& a, const Sc
     // Below kFwdBigGraph edges the columns pass is a few dependent memory
     // rounds and the exchange costs more than it saves (c2: 25.1 us with it,
     // 23.7 us without), so every lane keeps its own weights there.
-    const bool share = a.nnz >= big_graph_edges();
+    const bool share = a.graph_nnz >= big_graph_edges();
     if constexpr (V == 1 && L >= 4) {
       if (!share) launch(std::integral_constant<int, 1>());
       else if (lgcq >= 2) launch(std::integral_constant<int, 4>());

@@ -145,7 +145,13 @@ struct Lanes {
 template <typename T>
 struct GatFwdArgs {
   int n, H, C;
-  int64_t nnz;
+  // Edges of the whole graph: selects the large-graph kernel variants, so a
+  // launch over one row shard computes each row as the whole-graph launch.
+  int64_t graph_nnz;
+  // Dropout hash index offset: H x the CSR id, in the whole graph, of the
+  // launch's first edge (0 for a whole-graph launch). The mask is stored at
+  // the launch's own edge ids.
+  int64_t mask_base;
   float slope, p;
   uint64_t seed;
   bool vec;  // 16-byte loads of x rows are legal
@@ -251,7 +257,7 @@ struct FwdWave {
     bool keep = true;
     if (a.p > 0.0f) {
       const int64_t idx = static_cast<int64_t>(t[k]) * a.H + h;
-      keep = gat_keep(a.seed, static_cast<uint64_t>(idx), a.p);
+      keep = gat_keep(a.seed, static_cast<uint64_t>(idx + a.mask_base), a.p);
       if (write_mask) a.mask[idx] = keep ? 1 : 0;
     }
     if (!keep || (normalise && !(S > 0.0f))) return 0.0f;
@@ -455,6 +461,10 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_kernel(GatFwdArgs<T> a, Sched 
 template <typename T>
 struct GatBwdArgs {
   int n, nnz, H, C;
+  int64_t graph_nnz;  // edges of the whole graph (variant selection, as GatFwdArgs)
+  // grad_bias sums grad_pre rows [bias_lo, bias_lo + bias_n) (0, n for a
+  // whole-graph launch; a shard's own rows otherwise)
+  int bias_lo, bias_n;
   float slope, p, inv_h;
   bool vec_x;   // 16-byte loads of x rows are legal
   bool vec_gp;  // 16-byte loads of grad_pre rows are legal
@@ -767,8 +777,9 @@ __device__ __forceinline__ void bias_reduce(const GatBwdArgs<T>& a, int q, int* 
   reduce(a.bias_l2, 0, a.n_l2, a.grad_bias);
 }
 
-// grad_bias = sum_n grad_pre[n, :] in two deterministic levels: workgroup q
-// of a.n_l2 sums rows [q*R, q*R + R) (R = ceil(n / n_l2)) into bias_l2[q];
+// grad_bias = sum_n grad_pre[n, :] over rows [bias_lo, bias_lo + bias_n) in
+// two deterministic levels: workgroup q of a.n_l2 sums rows [q*R, q*R + R) of
+// that range (R = ceil(bias_n / n_l2)) into bias_l2[q];
 // the last one to finish sums the n_l2 partials in order. Threads own a
 // (row, 4-channel chunk) pair and read float4 (C % 4 == 0, rows 16-byte
 // aligned), 256 / (C/4) rows per step.
@@ -806,9 +817,9 @@ __device__ __forceinline__ void bias_from_grad_pre(const GatBwdArgs<T>& a, int q
     }
     __syncthreads();
   };
-  const int R = (a.n + a.n_l2 - 1) / a.n_l2;
-  const int lo = min(a.n, q * R), hi = min(a.n, lo + R);
-  reduce(a.grad_pre, lo, hi, a.bias_l2 + static_cast<int64_t>(q) * C);
+  const int R = (a.bias_n + a.n_l2 - 1) / a.n_l2;
+  const int lo = min(a.bias_n, q * R), hi = min(a.bias_n, lo + R);
+  reduce(a.grad_pre + static_cast<int64_t>(a.bias_lo) * C, lo, hi, a.bias_l2 + static_cast<int64_t>(q) * C);
   if (!arrive_last(counter, a.n_l2, flag)) return;
   reduce(a.bias_l2, 0, a.n_l2, a.grad_bias);
 }

@@ -18,8 +18,10 @@ The reference picks between PyG / dgNN / CUDA / torch paths with its
   epilogue (one MFMA kernel, cign_linear_gamma_fwd).
 
 The flags are accepted for signature compatibility and validated like the
-reference's. ``use_chunked_fused_gat`` (the dgNN chunking backend) is out of
-scope and raises.
+reference's. ``use_chunked_fused_gat`` (the reference's dgNN chunking backend,
+chunked_dgnn_gat.py) runs the same collapsed GAT shard by shard over the
+row-nnz partition of cign_amd.partition, with ``dgnn_chunk_target_nodes`` and
+``dgnn_chunk_max_nodes`` as its knobs.
 """
 from __future__ import annotations
 
@@ -36,6 +38,7 @@ from .fused_block_ops import fused_add_layernorm_cat, fused_dropout_layernorm
 from .graph import selected_sparse_powers
 from .hop_gate import gated_clifford_pack, global_hop_gate, node_hop_gate
 from .linear import linear_attention_logits, linear_gamma_residual, mfma_linear
+from .partition import ShardedGAT, prepare_sharded_gat_graph, sharded_collapsed_gat_mean_bias_silu
 
 
 def cign_outer_difference(b_hr, b_rh, mode):
@@ -121,6 +124,10 @@ class CompatibleCollapsedFusedGATConv(nn.Module):
         xp, alpha_src, alpha_dst = linear_attention_logits(x, self.lin.weight, self.att_src, self.att_dst, H,
                                                            amp_enabled, amp_dtype)
         dropout = self.dropout if self.training else 0.0
+        if isinstance(csr, ShardedGAT):
+            # the partitioned graph (model_cign.py:462 dispatches on ChunkedDgNNGraph alike)
+            return sharded_collapsed_gat_mean_bias_silu(alpha_dst, alpha_src, csr, self.negative_slope, xp,
+                                                        self.bias, dropout)
         return collapsed_gat_mean_bias_silu(attn_row=alpha_dst, attn_col=alpha_src, csr=csr, csc=csc, perm=perm,
                                             negative_slope=self.negative_slope, in_feat=xp, bias=self.bias,
                                             attn_drop=dropout)
@@ -145,8 +152,6 @@ class GraphCliffordBlock(nn.Module):
             raise ValueError("gamma_mode must be either 'scalar' or 'vector'.")
         if hop_gate_mode not in {"none", "global", "node"}:
             raise ValueError("hop_gate_mode must be one of {'none', 'global', 'node'}.")
-        if use_chunked_fused_gat:
-            raise ValueError("the chunked dgNN GAT backend is not part of the HIP route")
         self.hidden_dim = hidden_dim
         self.order_set = [int(s) for s in order_set]
         self.num_hops = len(self.order_set)
@@ -158,7 +163,7 @@ class GraphCliffordBlock(nn.Module):
         self.alpha_weighting_mode = _resolve_old_new_mode(alpha_weighting_mode, "CIGN_ALPHA_WEIGHTING_MODE", "old")
         self.use_fused_gat = bool(use_fused_gat)
         self.use_fused_gat_sideops = bool(use_fused_gat_sideops)
-        self.use_chunked_fused_gat = False
+        self.use_chunked_fused_gat = bool(use_chunked_fused_gat)
         self.use_collapsed_fused_gat = bool(use_collapsed_fused_gat)
         self.outer_nonlinearity = os.environ.get("CIGN_OUTER_NONLINEARITY", "none").strip().lower()
         if self.outer_nonlinearity not in {"tanh", "none"}:
@@ -210,8 +215,11 @@ class GraphCliffordBlock(nn.Module):
         if fused_gat_graph is None:
             raise RuntimeError("The GAT graph format cache was not prepared. Call prepare_fused_gat_graph(...) once "
                                "before training.")
-        csr, csc, perm = fused_gat_graph
-        C_gat = self.context_gat(H_norm, csr, csc, perm)
+        if isinstance(fused_gat_graph, ShardedGAT):
+            C_gat = self.context_gat(H_norm, fused_gat_graph, None, None)  # model_cign.py:773-774
+        else:
+            csr, csc, perm = fused_gat_graph
+            C_gat = self.context_gat(H_norm, csr, csc, perm)
         C_norm, HC_norm = fused_add_layernorm_cat(C_gat, H_norm, self.c_norm.weight, self.c_norm.bias,
                                                   self.c_norm.eps)
         propagated = selected_sparse_powers(operator=graph_operator, X=HC_norm, powers=self.order_set)
@@ -301,6 +309,7 @@ class GraphCliffordNet(nn.Module):
             GraphCliffordBlock(hidden_dim=hidden_dim, order_set=order_set, dropout=dropout, gat_heads=gat_heads,
                                gat_dropout=gat_dropout, use_fused_gat=self.use_fused_gat,
                                use_fused_gat_sideops=self.use_fused_gat_sideops,
+                               use_chunked_fused_gat=self.use_chunked_fused_gat,
                                use_collapsed_fused_gat=self.use_collapsed_fused_gat,
                                use_fused_clifford_pack=self.use_fused_clifford_pack,
                                use_fused_block_ops=self.use_fused_block_ops,
@@ -330,6 +339,14 @@ class GraphCliffordNet(nn.Module):
         (rowptr, col), (row, colptr), perm = prepare_fused_gat_graph(edge_index, int(num_nodes))
         dev = self.classifier.weight.device
         rowptr, col, row, colptr, perm = (t.to(dev) for t in (rowptr, col, row, colptr, perm))
+        if self.use_chunked_fused_gat:
+            # model_cign.py:1105-1115: the partitioned graph and its info
+            conv = self.blocks[0].context_gat
+            graph = prepare_sharded_gat_graph(((rowptr, col), (row, colptr), perm), conv.heads, conv.out_channels,
+                                              torch.float32, self.dgnn_chunk_max_nodes, self.dgnn_chunk_target_nodes)
+            self._fused_gat_graph = graph
+            self._fused_gat_graph_info = dict(graph.info)
+            return dict(self._fused_gat_graph_info)
         self._fused_gat_graph = ((rowptr, col), (row, colptr), perm)
         self._fused_gat_graph_info = {
             "num_nodes": int(num_nodes), "num_edges": int(col.numel()),

@@ -153,6 +153,45 @@ int cign_gat_bwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
                  int32_t* col_counters, void* workspace, int64_t workspace_bytes, void* grad_feat,
                  float* grad_attn_row, float* grad_attn_col, float* grad_bias, const float* row_agg);
 
+/* cign_gat_fwd over one destination-row shard of a larger graph, the
+ * partitioned execution that replaces run_chunked_dgnn_op
+ * (chunked_dgnn_gat.py:214-252): n and col are the shard's rows and its
+ * in-edges with source ids local to the gathered in_feat / attn_col (its own
+ * rows and its source halo); attn_row and the outputs are the shard's rows.
+ * edge_base = the CSR id, in the whole graph, of the shard's first edge: the
+ * dropout mask is hashed on whole-graph edge ids (and stored at the shard's
+ * own). graph_nnz = the whole graph's edges: the kernels run the variant the
+ * whole-graph call runs, so with the whole graph's schedule geometry every
+ * row's outputs are bit-identical to cign_gat_fwd's. */
+int cign_gat_fwd_shard(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
+                       const float* attn_row, const float* attn_col, const int32_t* col, const int32_t* row_sched,
+                       const int32_t* row_sched_info, int32_t* row_counters, float negative_slope,
+                       const void* in_feat, const float* bias, float attn_drop, uint64_t seed, void* out, float* pre,
+                       float* edge_max, float* edge_sum, uint8_t* edge_mask, void* workspace,
+                       int64_t workspace_bytes, float* row_agg, int64_t edge_base, int64_t graph_nnz);
+
+/* cign_gat_bwd over one source-column shard: the graph holds the shard's
+ * source nodes with all their out-edges and the destination rows those
+ * reach (the halo), every per-row input (edge_max, edge_sum, attn_row, pre,
+ * grad_y, row_agg) gathered for those rows from the whole-graph forward.
+ * row_agg is required: the halo rows have only part of their in-edges here,
+ * so their row sums come from the aggregates. grad_feat and grad_attn_col are
+ * complete (bit-identical to cign_gat_bwd's) for the shard's sources, and
+ * grad_attn_row for every row; grad_bias sums grad_pre rows [bias_row_lo,
+ * bias_row_lo + bias_rows) only (the shard's own nodes; the whole graph's is
+ * the sum over shards). graph_nnz as in cign_gat_fwd_shard. No counterpart
+ * in the reference, whose chunked path leaves the source gradients of
+ * overlapping chunks to autograd's scatter-add. */
+int cign_gat_bwd_shard(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
+                       float negative_slope, float attn_drop, const int32_t* col, const int32_t* rowind,
+                       const int32_t* perm, const float* edge_max, const float* edge_sum, const uint8_t* edge_mask,
+                       const void* in_feat, const float* attn_row, const float* attn_col, const float* pre,
+                       const void* grad_y, const int32_t* row_sched, const int32_t* row_sched_info,
+                       int32_t* row_counters, const int32_t* col_sched, const int32_t* col_sched_info,
+                       int32_t* col_counters, void* workspace, int64_t workspace_bytes, void* grad_feat,
+                       float* grad_attn_row, float* grad_attn_col, float* grad_bias, const float* row_agg,
+                       int32_t bias_row_lo, int32_t bias_rows, int64_t graph_nnz);
+
 /* ---- GAT side ops (float32) ---------------------------------------------- */
 
 /* Workspace bytes of a backward entry point below whose parameter gradient

@@ -196,3 +196,20 @@ def test_c5_gat_sampled_rows_and_columns_match_oracle(request, c5, dtype):
         # fp64 sums over the GPU's own pre (checked at the sampled rows above).
         err = np.abs(_np(gb) - bias_ref)
         assert (err <= bias_atol + 1e-4 * np.abs(bias_ref)).all(), f"{label} grad_bias: {err.max()}"
+
+
+def test_c5_sharded_layer_bit_identical(request, c5):
+    """The c5 layer (bf16 GAT 4 x 32 with edge dropout, 3 hops over D = 256) in
+    16 nnz-balanced shards, each below the large-graph threshold the whole
+    graph is above, against the unsharded layer bit for bit
+    (tests/test_gpu_partition.py states the checks)."""
+    from cign_amd.partition import partition_rows
+    from tests.test_gpu_partition import check_sharded_layer
+
+    w, _ = c5
+    (rowptr, _), (_, colptr), _ = w.gat_graph
+    ranges = partition_rows([rowptr, colptr, w.operator.csr.crow_indices()], 16)
+    _say(request, f"sharded layer: {len(ranges)} shards, largest {max(hi - lo for lo, hi in ranges)} rows")
+    check_sharded_layer(w, ranges, torch.bfloat16, 4, 32, 256, 0.3)
+    _say(request, "sharded layer matches")
+
