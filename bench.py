@@ -563,6 +563,10 @@ def run_block(args, torch):
     lin_ws = torch.empty(int(lib.cign_linear_bwd_workspace_bytes(n, D, 2 * K * D, 1)), dtype=torch.uint8, device=dev)
     gxp, gWp, gbp = torch.empty(n, 2 * K * D, device=dev), torch.empty(D, 2 * K * D, device=dev), torch.empty(D, device=dev)
     math = 1 if amp else 0
+    galpha = torch.empty(n, K, device=dev)
+    pp_ws = torch.empty(int(lib.cign_pack_proj_bwd_workspace_bytes(n, D, K)), dtype=torch.uint8, device=dev)
+    pf_ws = torch.empty(max(1, int(lib.cign_pack_proj_fwd_workspace_bytes(D, K, math))), dtype=torch.uint8,
+                        device=dev)
     s4 = 4
     NDb = n * D
     comps = {
@@ -600,6 +604,20 @@ def run_block(args, torch):
                                       Wp.data_ptr(), gxp.data_ptr(), gWp.data_ptr(), gbp.data_ptr(),
                                       lin_ws.data_ptr(), lin_ws.numel()),
                      2 * s4 * n * 2 * K * D + 2 * 4 * NDb, 4 * n * 2 * K * D * D),
+        # the pack built inside proj (the block's tail as it runs): G_raw never stored
+        "pack_proj_fwd": (lambda: lib.call("cign_pack_proj_fwd", st(), n, D, K, 1, math, hh.data_ptr(),
+                                           cc.data_ptr(), ctypes.addressof(parr), 2 * D, alpha.data_ptr(), K,
+                                           Wp.data_ptr(), bp.data_ptr(), x.data_ptr(), lnw.data_ptr(), 0.28, 9,
+                                           gp_out.data_ptr(), yp.data_ptr(), mask.data_ptr(),
+                                           pf_ws.data_ptr(), pf_ws.numel()),
+                          (21 + 8 * K) * NDb + 4 * n * K, 2 * n * 2 * K * D * D),
+        "pack_proj_bwd": (lambda: lib.call("cign_pack_proj_bwd", st(), n, D, K, 1, math, x.data_ptr(),
+                                           hh.data_ptr(), cc.data_ptr(), ctypes.addressof(parr), 2 * D,
+                                           alpha.data_ptr(), K, Wp.data_ptr(), 1, gate_w.data_ptr(),
+                                           gH_.data_ptr(), gC_.data_ptr(), ctypes.addressof(gparr), 2 * D,
+                                           galpha.data_ptr(), gWp.data_ptr(), gbp.data_ptr(), gwt.data_ptr(),
+                                           gbt.data_ptr(), pp_ws.data_ptr(), pp_ws.numel()),
+                          (20 + 16 * K) * NDb + 8 * n * K, 4 * n * 2 * K * D * D),
         "gat_lin_fwd": (lambda: lib.call("cign_linear_fwd", st(), n, heads * D, D, 0, math, x.data_ptr(),
                                          Wl.data_ptr(), None, xl.data_ptr()),
                         4 * NDb + 4 * n * heads * D, 2 * n * D * heads * D),

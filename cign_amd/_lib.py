@@ -70,6 +70,12 @@ _SIGNATURES = {
                                         _P]),
     "cign_linear_bwd_workspace_bytes": (_I64, [_I64, _I32, _I32, _I32]),
     "cign_linear_bwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _I64]),
+    "cign_pack_proj_fwd_workspace_bytes": (_I64, [_I32, _I32, _I32]),
+    "cign_pack_proj_fwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _I64, _P, _I64, _P, _P, _P, _P,
+                                     _F32, _U64, _P, _P, _P, _P, _I64]),
+    "cign_pack_proj_bwd_workspace_bytes": (_I64, [_I64, _I32, _I32]),
+    "cign_pack_proj_bwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _I64, _P, _I64, _P, _I32, _P,
+                                     _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64]),
     # Clifford packs (pack.hip) and the gate fused into them (gate.hip)
     "cign_pack_gate_fwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _I64, _P, _P, _P, _P]),
     "cign_pack_gate_bwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _I64, _P, _P, _P, _P,

@@ -183,7 +183,14 @@ __device__ __forceinline__ float leaky(float x, float slope) { return x > 0.0f ?
 // result leaves the normal range; results below 2^-126 flush to zero. Three
 // instructions instead of the dozen of the correctly rounded expf.
 __device__ __forceinline__ float softmax_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+// 1 / (1 + e^-x) from the hardware exponential and reciprocal (v_exp_f32,
+// v_rcp_f32, 1 ulp each; the product -x * log2(e) adds a relative error of
+// at most |x| * 2^-24 to e^-x): a few ulp against the correctly rounded
+// expf and IEEE division, in four instructions instead of about twenty.
+// Saturates to 0 (e^-x overflows to inf) and 1 (e^-x underflows) as those do.
+__device__ __forceinline__ float sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
+}
 __device__ __forceinline__ float silu(float x) { return x * sigmoid(x); }
 __device__ __forceinline__ float silu_grad(float x) {
   const float s = sigmoid(x);

@@ -13,6 +13,7 @@
 // lane group (rowops.h); the parameter gradients are deterministic row-block
 // partials added by colsum_kernel.
 #include "clifford.h"
+#include "gate.h"
 
 namespace cign {
 namespace gate {
@@ -137,8 +138,9 @@ __global__ __launch_bounds__(kBlock) void hop_gate_fwd_kernel(int64_t n, int D, 
   }
 }
 
-// Row part of the backward: gl (to the workspace), grad_H, grad_C.
-template <int LPR, int V, int W, int KT>
+// Row part of the backward: gl (to the workspace), grad_H, grad_C (added to
+// what they hold when ACC).
+template <int LPR, int V, int W, int KT, bool ACC>
 __global__ __launch_bounds__(kBlock) void hop_gate_bwd_rows_kernel(int64_t n, int D, int K, int mode, const float* H,
                                                                    const float* C, const float* wt, const float* alpha,
                                                                    const float* galpha, float* gl_out, float* gH,
@@ -198,6 +200,16 @@ __global__ __launch_bounds__(kBlock) void hop_gate_bwd_rows_kernel(int64_t n, in
             const float sg = d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f);
             oh[w] = g1[w] + sg * g2[w];
             oc[w] = g1[w] - sg * g2[w];
+          }
+        }
+        if constexpr (ACC) {
+          float ph[W], pc[W];
+          Chunk<float, W>::load(gH + r * D + q * W, ph);
+          Chunk<float, W>::load(gC + r * D + q * W, pc);
+#pragma unroll
+          for (int w = 0; w < W; ++w) {
+            oh[w] = ph[w] + oh[w];
+            oc[w] = pc[w] + oc[w];
           }
         }
         Chunk<float, W>::store(gH + r * D + q * W, oh);
@@ -566,6 +578,46 @@ int gate_param_grads(hipStream_t st, int64_t n, int D, int K, int mode, int W, c
   return launch_colsum(st, part_b, nb, K, 1, grad_bias, nullptr, who);
 }
 
+}  // namespace gate
+
+int64_t gate::node_gate_ws_bytes(int64_t n, int D, int K) { return 4LL * gate_ws_floats(n, D, K); }
+
+// Backward of the node hop gate given grad_alpha (gate.h).
+int gate::node_gate_bwd(hipStream_t st, int64_t n, int D, int K, int score_mode, const float* H, const float* C,
+                        const float* weight, const float* alpha, const float* grad_alpha, float* grad_H,
+                        float* grad_C, float* grad_weight, float* grad_bias, void* workspace,
+                        int64_t workspace_bytes, bool accumulate, const char* who) {
+  int rc = check_gate(who, n, D, K, score_mode);
+  if (rc) return rc;
+  if (workspace_bytes < 4LL * gate_ws_floats(n, D, K)) return set_error(kInvalid, "%s: workspace too small", who);
+  if (n == 0) return zero_outputs(st, grad_weight, K * 2 * D, grad_bias, K, who);
+  float* gl = static_cast<float*>(workspace);
+  const int W = gate_width(D, {H, C, weight, grad_H, grad_C});
+  rc = with_geo(D / W, [&](auto LC, auto VC) {
+    constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
+    const int grid = grid_for(n, Geo<L>::RPB);
+    auto go = [&](auto AC) {
+      constexpr bool A = decltype(AC)::value;
+      if (W == 4)
+        with_hops(K, [&](auto KC) {
+          hipLaunchKernelGGL((hop_gate_bwd_rows_kernel<L, V, 4, decltype(KC)::value, A>), dim3(grid), dim3(kBlock), 0,
+                             st, n, D, K, score_mode, H, C, weight, alpha, grad_alpha, gl, grad_H, grad_C);
+        });
+      else
+        hipLaunchKernelGGL((hop_gate_bwd_rows_kernel<L, V, 1, 0, A>), dim3(grid), dim3(kBlock), 0, st, n, D, K,
+                           score_mode, H, C, weight, alpha, grad_alpha, gl, grad_H, grad_C);
+    };
+    if (accumulate) go(std::true_type());
+    else go(std::false_type());
+    return check_launch(who);
+  });
+  if (rc < 0) return set_error(kInvalid, "%s: D=%d too wide (max %d)", who, D, 256 * W);
+  if (rc) return rc;
+  return gate_param_grads(st, n, D, K, score_mode, W, H, C, workspace, grad_weight, grad_bias, who);
+}
+
+namespace gate {
+
 int check_pack_gate(const char* who, int64_t n, int D, int K, int interaction, int weighting, int mode) {
   int rc = check_gate(who, n, D, K, mode);
   if (rc) return rc;
@@ -650,30 +702,9 @@ int cign_hop_gate_fwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t sco
 int cign_hop_gate_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t score_mode, const float* H,
                       const float* C, const float* weight, const float* alpha, const float* grad_alpha, float* grad_H,
                       float* grad_C, float* grad_weight, float* grad_bias, void* workspace, int64_t workspace_bytes) {
-  int rc = check_gate("cign_hop_gate_bwd", n, D, K, score_mode);
-  if (rc) return rc;
-  if (workspace_bytes < 4LL * gate_ws_floats(n, D, K))
-    return set_error(kInvalid, "cign_hop_gate_bwd: workspace too small");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (n == 0) return zero_outputs(st, grad_weight, K * 2 * D, grad_bias, K, "cign_hop_gate_bwd");
-  float* gl = static_cast<float*>(workspace);
-  const int W = gate_width(D, {H, C, weight, grad_H, grad_C});
-  rc = with_geo(D / W, [&](auto LC, auto VC) {
-    constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
-    const int grid = grid_for(n, Geo<L>::RPB);
-    if (W == 4)
-      with_hops(K, [&](auto KC) {
-        hipLaunchKernelGGL((hop_gate_bwd_rows_kernel<L, V, 4, decltype(KC)::value>), dim3(grid), dim3(kBlock), 0, st,
-                           n, D, K, score_mode, H, C, weight, alpha, grad_alpha, gl, grad_H, grad_C);
-      });
-    else
-      hipLaunchKernelGGL((hop_gate_bwd_rows_kernel<L, V, 1, 0>), dim3(grid), dim3(kBlock), 0, st, n, D, K,
-                         score_mode, H, C, weight, alpha, grad_alpha, gl, grad_H, grad_C);
-    return check_launch("cign_hop_gate_bwd (rows)");
-  });
-  if (rc < 0) return set_error(kInvalid, "cign_hop_gate_bwd: D=%d too wide (max %d)", D, 256 * W);
-  if (rc) return rc;
-  return gate_param_grads(st, n, D, K, score_mode, W, H, C, workspace, grad_weight, grad_bias, "cign_hop_gate_bwd");
+  return cign::gate::node_gate_bwd(static_cast<hipStream_t>(stream), n, D, K, score_mode, H, C, weight, alpha,
+                                   grad_alpha, grad_H, grad_C, grad_weight, grad_bias, workspace, workspace_bytes,
+                                   false, "cign_hop_gate_bwd");
 }
 
 int cign_pack_gate_fwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t interaction, int32_t weighting,

@@ -37,6 +37,8 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "clifford.h"
+#include "gate.h"
 #include "rowops.h"
 
 namespace cign {
@@ -161,9 +163,14 @@ __device__ __forceinline__ void gload_fast(const TS* p, int k, float (&v)[CNT]) 
 // for fp32 x 4 and bf16 x 8, 8 bytes for bf16 x 4).
 template <typename T, int N>
 __device__ __forceinline__ void st_lds(T* d, const float (&v)[N]) {
-  if constexpr (std::is_same_v<T, float>) {
-    static_assert(N == 4, "fp32 LDS chunks are 4 values");
+  if constexpr (std::is_same_v<T, float> && N == 2) {
+    *reinterpret_cast<float2*>(d) = make_float2(v[0], v[1]);
+  } else if constexpr (std::is_same_v<T, float>) {
+    static_assert(N == 4, "fp32 LDS chunks are 2 or 4 values");
     *reinterpret_cast<float4*>(d) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if constexpr (N == 2) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<bf16x2*>(d) = bf16x2{static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1])};
   } else if constexpr (N == 4) {
     *reinterpret_cast<bf16x4*>(d) = bf16x4{static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1]),
                                            static_cast<__bf16>(v[2]), static_cast<__bf16>(v[3])};
@@ -335,9 +342,9 @@ __device__ __forceinline__ void tile_of(int nrt, int nct, int& rt, int& ct) {
 }
 
 // Epilogue of the swapped-operand layout: lane holds output row m = row0 +
-// 16r + lane%16 and columns n = n0 + 16f + 4*(lane/16) + q, q < 4.
-template <int EPI, int TN>
-__device__ __forceinline__ void epilogue_swapped(const GemmArgs& g, f32x4 (&acc)[2][TN], int64_t row0, int n0,
+// 16r + lane%16 (r < RT) and columns n = n0 + 16f + 4*(lane/16) + q, q < 4.
+template <int EPI, int TN, int RT = 2>
+__device__ __forceinline__ void epilogue_swapped(const GemmArgs& g, f32x4 (&acc)[RT][TN], int64_t row0, int n0,
                                                  int lane) {
   const int cg = (lane >> 4) * 4;
 #pragma unroll
@@ -352,7 +359,7 @@ __device__ __forceinline__ void epilogue_swapped(const GemmArgs& g, f32x4 (&acc)
       bv[q] = g.round_bf16 ? round_bf16(b) : b;
     }
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < RT; ++r) {
       const int64_t m = row0 + 16 * r + (lane & 15);
       float v[4];
 #pragma unroll
@@ -409,7 +416,9 @@ __device__ __forceinline__ void epilogue_swapped(const GemmArgs& g, f32x4 (&acc)
     const int fph = g.C / 16;
     for (int h0 = 0; h0 < TN; h0 += fph) {
       const int head = (n0 + 16 * h0) / g.C;
-      float ss[2] = {0.0f, 0.0f}, sd[2] = {0.0f, 0.0f};
+      float ss[RT], sd[RT];
+#pragma unroll
+      for (int r = 0; r < RT; ++r) ss[r] = sd[r] = 0.0f;
 #pragma unroll
       for (int f = 0; f < TN; ++f) {
         if (f < h0 || f >= h0 + fph) continue;
@@ -420,14 +429,14 @@ __device__ __forceinline__ void epilogue_swapped(const GemmArgs& g, f32x4 (&acc)
           const float as = n < g.N ? g.att_src[static_cast<int64_t>(head) * g.C + c] : 0.0f;
           const float ad = n < g.N ? g.att_dst[static_cast<int64_t>(head) * g.C + c] : 0.0f;
 #pragma unroll
-          for (int r = 0; r < 2; ++r) {
+          for (int r = 0; r < RT; ++r) {
             ss[r] = fmaf(acc[r][f][q], as, ss[r]);
             sd[r] = fmaf(acc[r][f][q], ad, sd[r]);
           }
         }
       }
 #pragma unroll
-      for (int r = 0; r < 2; ++r)
+      for (int r = 0; r < RT; ++r)
 #pragma unroll
         for (int o = 16; o < kWave; o <<= 1) {
           ss[r] += shfl_xor(ss[r], o);
@@ -435,7 +444,7 @@ __device__ __forceinline__ void epilogue_swapped(const GemmArgs& g, f32x4 (&acc)
         }
       if (lane < 16 && head < H) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < RT; ++r) {
           const int64_t m = row0 + 16 * r + lane;
           if (m < g.M) {
             g.alpha_src[m * H + head] = ss[r];
@@ -956,6 +965,580 @@ __global__ __launch_bounds__(kThreads) void small_n_grad_w_kernel(const float* g
 }
 
 // ---------------------------------------------------------------------------
+// Clifford pack inside the projection (weighting old). The block's
+//   G[m, kk*2D + j]     = alpha[m,kk] W(bhr, brh),
+//   G[m, kk*2D + D + j] = alpha[m,kk] D(bhr, brh),   bhr = H[m,j] P_kk[m,D+j],
+//                                                   brh = C[m,j] P_kk[m,j]
+// (packk::interact, the pack kernels' own formula) feeds proj only, so the
+// kernels below build G's tiles from H, C, the hops and alpha where the
+// projection GEMMs load their operands, and G [n, 2KD] is never stored:
+//   forward   g = G Wp^T + bp, out = h + gamma * drop(g)  (the gamma epilogue);
+//   backward  grad_G = grad_g Wp per 32-channel block of every hop and half,
+//             consumed by the pack's backward in the epilogue (grad_H, grad_C,
+//             grad_P_k, grad_alpha), and grad_Wp = grad_g^T G with G rebuilt
+//             in the reduction's operand load.
+// The reduction over G's columns runs hop by hop over 16 (forward) or 64
+// (grad_Wp) channels at a time, W half then D half, so one load of H, C and
+// the hop's two halves yields both halves' values.
+constexpr int kPackMaxHops = 4;
+constexpr int kPpBM = 64;  // rows per workgroup of the pack-projection kernels
+
+struct PackArgs {
+  int64_t M;
+  int D, K, mode;  // mode: interaction code (packk::interact)
+  const float* H;
+  const float* C;
+  const float* P[kPackMaxHops];
+  int64_t p_stride;  // row stride of the hops (>= 2D)
+  const float* alpha;
+  int64_t a_stride;  // row stride of alpha: K, or 0 for one row shared by all nodes
+  const __bf16* w16;  // bf16 math: Wp rounded to bf16 once per call [D, 2KD]
+};
+
+// Forward A tile of one K step (hop kk, channels j0 .. j0+15): BM rows x 32
+// columns, tile column c < 16 = W value of channel j0 + c, c >= 16 = D value
+// of channel j0 + c - 16. Thread: row tid / (16/CPT), CPT = BM/16 channels.
+template <int BM>
+struct PackAStage {
+  static constexpr int CPT = BM / 16;  // channels per thread: 4 (64 rows) or 2 (32 rows)
+  static constexpr int TPR = 16 / CPT; // threads per row
+  float hv[CPT], cv[CPT], th[CPT], tc[CPT], al;
+
+  template <int N>
+  __device__ __forceinline__ static void ld(const float* p, int j, float (&v)[N]) {
+    if constexpr (N == 4) {
+      gload_fast<float, 4>(p, j, v);
+    } else {
+      const float2 u = *reinterpret_cast<const float2*>(p + j);
+      v[0] = u.x;
+      v[1] = u.y;
+    }
+  }
+
+  __device__ __forceinline__ void load(const PackArgs& a, int64_t m0, int kk, int j0) {
+    const int r = threadIdx.x / TPR, j = j0 + CPT * (threadIdx.x % TPR);
+    const int64_t m = m0 + r < a.M ? m0 + r : a.M - 1;  // rows past M: outputs never stored
+    ld(a.H + m * a.D, j, hv);
+    ld(a.C + m * a.D, j, cv);
+    const float* pk = a.P[kk] + m * a.p_stride;
+    ld(pk, j, th);
+    ld(pk, a.D + j, tc);
+    al = a.alpha[m * a.a_stride + kk];
+  }
+
+  template <typename T>
+  __device__ __forceinline__ void store(T* As, int S, int mode) const {
+    const int r = threadIdx.x / TPR, c = CPT * (threadIdx.x % TPR);
+    float w[CPT], d[CPT];
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+      const packk::DW e = packk::interact(hv[q] * tc[q], cv[q] * th[q], mode);
+      w[q] = al * e.Wv;
+      d[q] = al * e.Dv;
+    }
+    st_lds<T, CPT>(As + r * S + c, w);
+    st_lds<T, CPT>(As + r * S + 16 + c, d);
+  }
+};
+
+// Forward W tile of the same K step: BN rows (all D outputs) x 32, tile
+// column c < 16 from Wp column kk*2D + j0 + c, c >= 16 from kk*2D + D + j0 +
+// c - 16. fp32 math reads Wp; bf16 math its bf16 copy (half the bytes, no
+// conversion per step), 16-byte chunks either way.
+template <int MATH, int BN>
+struct PackBStage {
+  static constexpr int CHUNKS = BN * kBK / 4 / kThreads;
+  float b[CHUNKS][4];
+
+  __device__ __forceinline__ void load(const GemmArgs& g, const PackArgs&, int kk, int j0, int D) {
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      const int r = id >> 3, c = id & 7;
+      const int col = kk * 2 * D + (c < 4 ? j0 + 4 * c : D + j0 + 4 * (c - 4));
+      gload_fast<float, 4>(g.w + static_cast<int64_t>(r) * g.K, col, b[i]);
+    }
+  }
+  template <typename T>
+  __device__ __forceinline__ void store(T* Bs, int S) const {
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      st_lds<T, 4>(Bs + (id >> 3) * S + 4 * (id & 7), b[i]);
+    }
+  }
+};
+
+template <int BN>
+struct PackBStage<kMathBF16, BN> {
+  static constexpr int CHUNKS = BN * kBK / 8 / kThreads;
+  bf16x8 b[CHUNKS];
+
+  __device__ __forceinline__ void load(const GemmArgs& g, const PackArgs& a, int kk, int j0, int D) {
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      const int r = id >> 2, c = id & 3;
+      const int col = kk * 2 * D + (c < 2 ? j0 + 8 * c : D + j0 + 8 * (c - 2));
+      b[i] = *reinterpret_cast<const bf16x8*>(a.w16 + static_cast<int64_t>(r) * g.K + col);
+    }
+  }
+  __device__ __forceinline__ void store(__bf16* Bs, int S) const {
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      *reinterpret_cast<bf16x8*>(Bs + (id >> 2) * S + 8 * (id & 3)) = b[i];
+    }
+  }
+};
+
+// MFMAs of one K step: the wave's columns [wave*TNW*16, +TNW*16) of all four
+// 16-row tiles (W tile first operand: the swapped accumulator layout).
+template <int MATH, int TNW, int RT>
+__device__ __forceinline__ void mma_step_pp(const typename Op<MATH>::T* As, const typename Op<MATH>::T* Bs, int wave,
+                                            int lane, f32x4 (&acc)[RT][TNW]) {
+  constexpr int S = lds_stride<MATH>();
+  const int rl = lane & 15, ks = lane >> 4;
+  const int nb = wave * TNW * 16;
+  if constexpr (MATH == kMathBF16) {
+    bf16x8 a[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) a[r] = *reinterpret_cast<const bf16x8*>(As + (16 * r + rl) * S + ks * 8);
+#pragma unroll
+    for (int f = 0; f < TNW; ++f) {
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(Bs + (nb + 16 * f + rl) * S + ks * 8);
+#pragma unroll
+      for (int r = 0; r < RT; ++r) acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, a[r], acc[r][f], 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int hk = 0; hk < kBK; hk += 16) {
+      float4 a[RT];
+#pragma unroll
+      for (int r = 0; r < RT; ++r) a[r] = *reinterpret_cast<const float4*>(As + (16 * r + rl) * S + hk + ks * 4);
+#pragma unroll
+      for (int f = 0; f < TNW; ++f) {
+        const float4 b = *reinterpret_cast<const float4*>(Bs + (nb + 16 * f + rl) * S + hk + ks * 4);
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(b.x, a[r].x, acc[r][f], 0, 0, 0);
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(b.y, a[r].y, acc[r][f], 0, 0, 0);
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(b.z, a[r].z, acc[r][f], 0, 0, 0);
+          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(b.w, a[r].w, acc[r][f], 0, 0, 0);
+        }
+      }
+    }
+  }
+}
+
+// g = G Wp^T + bp and the gamma epilogue; a workgroup owns 64 rows and all
+// BN = D outputs (each wavefront BN/4 of them), so every G value is built
+// once; the next K step's rows and W tile load while the current one runs.
+// The host checks D in {64, 128, 256}, K <= kPackMaxHops, 16-byte aligned
+// rows (H, C, hops, Wp, g_out, h, out).
+template <int MATH, int BN, int BM>
+__global__ __launch_bounds__(kThreads) void pack_proj_fwd_kernel(GemmArgs g, PackArgs a) {
+  using T = typename Op<MATH>::T;
+  constexpr int S = lds_stride<MATH>();
+  constexpr int TNW = BN / 64;
+  constexpr int RT = BM / 16;
+  __shared__ __align__(16) T As[2][BM * S];
+  __shared__ __align__(16) T Bs[2][BN * S];
+  const int lane = lane_id();
+  const int wave = wave_id();
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * BM;
+
+  f32x4 acc[RT][TNW];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int f = 0; f < TNW; ++f) acc[r][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int jq = a.D / 16;
+  const int steps = a.K * jq;
+  PackAStage<BM> pa;
+  PackBStage<MATH, BN> pb;
+  pa.load(a, m0, 0, 0);
+  pb.load(g, a, 0, 0, a.D);
+  pa.store(As[0], S, a.mode);
+  pb.store(Bs[0], S);
+  __syncthreads();
+  int buf = 0;
+  for (int s = 0; s < steps; ++s) {
+    const bool more = s + 1 < steps;
+    if (more) {
+      const int kk = (s + 1) / jq, j0 = ((s + 1) % jq) * 16;
+      pa.load(a, m0, kk, j0);
+      pb.load(g, a, kk, j0, a.D);
+    }
+    mma_step_pp<MATH, TNW, RT>(As[buf], Bs[buf], wave, lane, acc);
+    if (more) {
+      pa.store(As[buf ^ 1], S, a.mode);
+      pb.store(Bs[buf ^ 1], S);
+    }
+    __syncthreads();
+    buf ^= 1;
+  }
+  epilogue_swapped<kEpiGamma, TNW, RT>(g, acc, m0, wave * TNW * 16, lane);
+}
+
+// dst[i] = bf16(src[i]) (round to nearest even, as the MFMA operand stores)
+__global__ void to_bf16_kernel(const float* src, int64_t n, __bf16* dst) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    dst[i] = static_cast<__bf16>(src[i]);
+}
+
+// ---- backward: grad_G and the pack's backward --------------------------------
+struct PackBwdArgs {
+  PackArgs a;
+  const float* gg;     // grad_g [M, D]
+  const void* wt;      // Wp^T [2KD, D]: bf16 with bf16 math, else fp32
+  float* gH;
+  float* gC;
+  float* gP[kPackMaxHops];
+  int64_t gp_stride;
+  float* galpha_part;  // [M, K, D/CBW]: grad_alpha per channel block
+};
+
+// A workgroup owns 64 rows (a wavefront 16) and one block cb of CBW channels:
+// grad_G for the 2K groups (hop kk, half) of those channels, 2K x CBW
+// columns, over the D-long reduction. The Wp^T rows of those columns sit in
+// LDS for the whole reduction and the wavefront's grad_g fragments in
+// registers, so the only global loads are issued up front, together with
+// the rows of H, C and the hops its epilogue needs. The epilogue is the
+// pack's backward: the lane holds, for its row, channels cb*CBW + 16 fh +
+// 4*(lane/16) + q of every group. CBW = 32 (bf16) writes whole 128-byte row
+// segments of every gradient; fp32 takes CBW = 16 (its Wp^T rows would not
+// fit LDS). Grid (ceil(M/64), D/CBW).
+template <int MATH, int KC, int DD>
+__global__ __launch_bounds__(kThreads) void pack_proj_bwd_kernel(PackBwdArgs b) {
+  using T = typename Op<MATH>::T;
+  constexpr int CBW = MATH == kMathBF16 ? 32 : 16;  // channels per block
+  constexpr int NFH = CBW / 16;                     // 16-column tiles per group
+  constexpr int TF = 2 * KC * NFH;                  // tile f = group * NFH + fh
+  constexpr int NCOL = TF * 16;
+  constexpr int CE = 16 / sizeof(T);                // elements per 16-byte chunk
+  constexpr int SB = DD + CE;                       // LDS row stride, padded by 16 bytes
+  constexpr int NT = DD / kBK;
+  constexpr int CHUNKS = NCOL * DD / CE / kThreads;
+  // loads per round: the largest of 8, 6, 4, 3, 2, 1 dividing CHUNKS
+  constexpr int ROUND = CHUNKS % 8 == 0 ? 8 : CHUNKS % 6 == 0 ? 6 : CHUNKS % 4 == 0 ? 4 : CHUNKS % 3 == 0 ? 3
+                        : CHUNKS % 2 == 0 ? 2 : 1;
+  __shared__ __align__(16) T Bs[NCOL * SB];
+  const PackArgs& a = b.a;
+  const int lane = lane_id(), wave = wave_id();
+  const int rl = lane & 15, ks = lane >> 4;
+  const int cb = blockIdx.y;
+  const int64_t mrow = static_cast<int64_t>(blockIdx.x) * kPpBM + 16 * wave + rl;
+  const bool valid = mrow < a.M;
+  const int64_t mr = valid ? mrow : a.M - 1;
+
+  // the epilogue's rows, first in the queue
+  float h[NFH][4], c[NFH][4], th[KC][NFH][4], tc[KC][NFH][4], al[KC];
+#pragma unroll
+  for (int fh = 0; fh < NFH; ++fh) {
+    const int j = cb * CBW + 16 * fh + 4 * ks;
+    gload_fast<float, 4>(a.H + mr * DD, j, h[fh]);
+    gload_fast<float, 4>(a.C + mr * DD, j, c[fh]);
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      const float* pk = a.P[k] + mr * a.p_stride;
+      gload_fast<float, 4>(pk, j, th[k][fh]);
+      gload_fast<float, 4>(pk, DD + j, tc[k][fh]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < KC; ++k) al[k] = a.alpha[mr * a.a_stride + k];
+  // grad_g fragments of the wavefront's 16 rows over all D (MFMA second
+  // operand), in the operand type: bf16 k = 32t + 8*(lane/16) .. +7; fp32
+  // k = 32t + 4*(lane/16) .. +3 and 32t + 16 + 4*(lane/16) .. +3.
+  using XF = std::conditional_t<MATH == kMathBF16, bf16x8, float[8]>;
+  XF xf[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    float lo[4], hi[4];
+    const int ka = MATH == kMathBF16 ? kBK * t + 8 * ks : kBK * t + 4 * ks;
+    const int kb = MATH == kMathBF16 ? ka + 4 : ka + 16;
+    gload_fast<float, 4>(b.gg + mr * DD, ka, lo);
+    gload_fast<float, 4>(b.gg + mr * DD, kb, hi);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if constexpr (MATH == kMathBF16) {
+        xf[t][q] = static_cast<__bf16>(lo[q]);
+        xf[t][4 + q] = static_cast<__bf16>(hi[q]);
+      } else {
+        xf[t][q] = lo[q];
+        xf[t][4 + q] = hi[q];
+      }
+    }
+  }
+  // Wp^T rows of the block's columns: tile column col = CBW gi + cc is group
+  // gi (hop gi/2, half gi%2), channel cb*CBW + cc.
+  {
+    const T* wt = static_cast<const T*>(b.wt);
+    constexpr int CPR = DD / CE;  // chunks per row
+#pragma unroll 1
+    for (int r0 = 0; r0 < CHUNKS; r0 += ROUND) {
+      uint4 v[ROUND];
+#pragma unroll
+      for (int i = 0; i < ROUND; ++i) {
+        const int id = threadIdx.x + (r0 + i) * kThreads;
+        const int col = id / CPR, k = (id % CPR) * CE;
+        const int gi = col / CBW;
+        const int64_t gcol = (gi >> 1) * 2 * DD + (gi & 1) * DD + cb * CBW + (col % CBW);
+        v[i] = *reinterpret_cast<const uint4*>(wt + gcol * DD + k);
+      }
+#pragma unroll
+      for (int i = 0; i < ROUND; ++i) {
+        const int id = threadIdx.x + (r0 + i) * kThreads;
+        *reinterpret_cast<uint4*>(Bs + (id / CPR) * SB + (id % CPR) * CE) = v[i];
+      }
+    }
+  }
+  __syncthreads();
+
+  f32x4 acc[TF];
+#pragma unroll
+  for (int f = 0; f < TF; ++f) acc[f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if constexpr (MATH == kMathBF16) {
+#pragma unroll
+      for (int f = 0; f < TF; ++f) {
+        const bf16x8 wb = *reinterpret_cast<const bf16x8*>(Bs + (16 * f + rl) * SB + kBK * t + ks * 8);
+        acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb, xf[t], acc[f], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int f = 0; f < TF; ++f) {
+          const float4 wb = *reinterpret_cast<const float4*>(Bs + (16 * f + rl) * SB + kBK * t + 16 * hh + ks * 4);
+          const float* xv = xf[t] + 4 * hh;
+          acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.x, xv[0], acc[f], 0, 0, 0);
+          acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.y, xv[1], acc[f], 0, 0, 0);
+          acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.z, xv[2], acc[f], 0, 0, 0);
+          acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.w, xv[3], acc[f], 0, 0, 0);
+        }
+    }
+  }
+
+  // the pack's backward (fused_clifford_cign_pack backward_main_kernel, as
+  // cign_pack_gate_bwd); acc[gi * NFH + fh][q] = grad_G[mrow, channel
+  // cb*CBW + 16 fh + 4 ks + q of group gi]
+  float gsum[KC];
+#pragma unroll
+  for (int k = 0; k < KC; ++k) gsum[k] = 0.0f;
+#pragma unroll
+  for (int fh = 0; fh < NFH; ++fh) {
+    const int j = cb * CBW + 16 * fh + 4 * ks;
+    float gh[4], gc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) gh[q] = gc[q] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      float gpt[4], gpc[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float goW = acc[(2 * k) * NFH + fh][q];
+        const float goD = acc[(2 * k + 1) * NFH + fh][q];
+        const packk::DW e = packk::interact(h[fh][q] * tc[k][fh][q], c[fh][q] * th[k][fh][q], a.mode);
+        const float gD = goD * al[k];
+        const float gW = goW * al[k];
+        const float gbhr = gD * e.dD_bhr + gW * e.dW_bhr;
+        const float gbrh = gD * e.dD_brh + gW * e.dW_brh;
+        gh[q] += gbhr * tc[k][fh][q];
+        gc[q] += gbrh * th[k][fh][q];
+        gpt[q] = gbrh * c[fh][q];
+        gpc[q] = gbhr * h[fh][q];
+        gsum[k] += goW * e.Wv + goD * e.Dv;
+      }
+      if (valid) {
+        float* gp = b.gP[k] + mrow * b.gp_stride;
+        *reinterpret_cast<float4*>(gp + j) = make_float4(gpt[0], gpt[1], gpt[2], gpt[3]);
+        *reinterpret_cast<float4*>(gp + DD + j) = make_float4(gpc[0], gpc[1], gpc[2], gpc[3]);
+      }
+    }
+    if (valid) {
+      *reinterpret_cast<float4*>(b.gH + mrow * DD + j) = make_float4(gh[0], gh[1], gh[2], gh[3]);
+      *reinterpret_cast<float4*>(b.gC + mrow * DD + j) = make_float4(gc[0], gc[1], gc[2], gc[3]);
+    }
+  }
+  // grad_alpha of the block: the four lane groups of a row
+#pragma unroll
+  for (int k = 0; k < KC; ++k) {
+    gsum[k] += shfl_xor(gsum[k], 16);
+    gsum[k] += shfl_xor(gsum[k], 32);
+  }
+  if (valid && ks == 0)
+#pragma unroll
+    for (int k = 0; k < KC; ++k) b.galpha_part[(mrow * a.K + k) * (DD / CBW) + cb] = gsum[k];
+}
+
+// grad_alpha[m, k] = sum of the nb channel blocks' partials, in block order.
+__global__ void galpha_sum_kernel(const float* part, int64_t mk, int nb, float* galpha) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= mk) return;
+  float s = 0.0f;
+  for (int q = 0; q < nb; ++q) s += part[i * nb + q];
+  galpha[i] = s;
+}
+
+// W^T in bf16 for the backward's operand tiles: wt [K, N] = bf16(w [N, K])^T.
+__global__ void __launch_bounds__(256) transpose_w_bf16_kernel(const float* __restrict__ w, int N, int K,
+                                                              __bf16* __restrict__ wt) {
+  __shared__ float tile[32][33];
+  const int k0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
+  const int c = threadIdx.x & 31, r0 = threadIdx.x >> 5;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = r0 + 8 * i;
+    if (n0 + r < N && k0 + c < K) tile[r][c] = w[static_cast<int64_t>(n0 + r) * K + k0 + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = r0 + 8 * i;
+    if (k0 + r < K && n0 + c < N) wt[static_cast<int64_t>(k0 + r) * N + n0 + c] = static_cast<__bf16>(tile[c][r]);
+  }
+}
+
+// grad_Wp [D, 2KD] partials: the wgrad kernel's tiling (128 x 128 tile of
+// grad_Wp per workgroup, a chunk of rows) with the x operand = G rebuilt per
+// 32-row step: tile k = kt covers hop kk = kt / (D/64), channels j0 = 64 *
+// (kt % (D/64)) .. +63, tile column c < 64 = W value of channel j0 + c,
+// c >= 64 = D value of channel j0 + c - 64. Rows past the chunk are zero.
+template <int MATH>
+struct PackWgStage : WgStage<MATH> {
+  // WgStage's register layout: row tid / 8, tile column quads (tid % 8 + 8 i) * 4
+  using WgStage<MATH>::v;
+
+  __device__ __forceinline__ void load_pack(const PackArgs& a, int64_t m0, int64_t m1, int kk, int j0) {
+    const int r = threadIdx.x / 8;
+    const int64_t m = m0 + r;
+    if (m >= m1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[i][q] = 0.0f;
+      return;
+    }
+    const float al = a.alpha[m * a.a_stride + kk];
+    const float* pk = a.P[kk] + m * a.p_stride;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int j = j0 + ((threadIdx.x % 8) + 8 * i) * 4;
+      float h[4], c[4], th[4], tc[4];
+      gload_fast<float, 4>(a.H + m * a.D, j, h);
+      gload_fast<float, 4>(a.C + m * a.D, j, c);
+      gload_fast<float, 4>(pk, j, th);
+      gload_fast<float, 4>(pk, a.D + j, tc);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const packk::DW e = packk::interact(h[q] * tc[q], c[q] * th[q], a.mode);
+        v[i][q] = al * e.Wv;
+        v[i + 2][q] = al * e.Dv;
+      }
+    }
+  }
+};
+
+template <int MATH>
+__global__ __launch_bounds__(kThreads) void pack_wgrad_kernel(const float* gy, PackArgs a, int64_t chunk, int ntk,
+                                                              float* part) {
+  using T = typename Op<MATH>::T;
+  using Lay = WgLayout<MATH>;
+  __shared__ __align__(16) T Gs[2][kWgT * kWgM];
+  __shared__ __align__(16) T Xs[2][kWgT * kWgM];
+  const int N = a.D, KW = 2 * a.K * a.D;
+  const int lane = lane_id();
+  const int wave = wave_id();
+  const int kt = blockIdx.x % ntk;
+  const int n0 = (blockIdx.x / ntk) * kWgT;
+  const int kk = kt / (a.D / 64), j0 = 64 * (kt % (a.D / 64));
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * chunk;
+  const int64_t m1 = m0 + chunk < a.M ? m0 + chunk : a.M;
+  const int wn = (wave >> 1) * 64, wk = (wave & 1) * 64;
+  const int rl = lane & 15, ks = lane >> 4;
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  WgStage<MATH> sg;
+  PackWgStage<MATH> sx;
+  sg.load(gy, N, m0, m1, n0, N, true);
+  sx.load_pack(a, m0, m1, kk, j0);
+  sg.store(Gs[0]);
+  sx.store(Xs[0]);
+  __syncthreads();
+  int buf = 0;
+  for (int64_t mb = m0; mb < m1; mb += kWgM) {
+    const bool more = mb + kWgM < m1;
+    if (more) {
+      sg.load(gy, N, mb + kWgM, m1, n0, N, true);
+      sx.load_pack(a, mb + kWgM, m1, kk, j0);
+    }
+    const T* G = Gs[buf];
+    const T* X = Xs[buf];
+    if constexpr (MATH == kMathBF16) {
+      bf16x8 xb[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xb[j] = *reinterpret_cast<const bf16x8*>(X + Lay::frag(wk + 16 * j + rl, ks));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bf16x8 gb = *reinterpret_cast<const bf16x8*>(G + Lay::frag(wn + 16 * i + rl, ks));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gb, xb[j], acc[i][j], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float4 xb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          xb[j] = *reinterpret_cast<const float4*>(X + Lay::frag(wk + 16 * j + rl, 4 * h + ks));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 gb = *reinterpret_cast<const float4*>(G + Lay::frag(wn + 16 * i + rl, 4 * h + ks));
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.x, xb[j].x, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.y, xb[j].y, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.z, xb[j].z, acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.w, xb[j].w, acc[i][j], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (more) {
+      sg.store(Gs[buf ^ 1]);
+      sx.store(Xs[buf ^ 1]);
+    }
+    __syncthreads();
+    buf ^= 1;
+  }
+  // lane holds grad_Wp rows n = n0 + wn + 16i + 4*(lane/16) + q of tile
+  // column wk + 16j + lane%16: G column kk*2D + (wk/64)*D + j0 + 16j + lane%16
+  float* out = part + static_cast<int64_t>(blockIdx.y) * N * KW;
+  const int gbase = kk * 2 * a.D + (wk / 64) * a.D + j0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = gbase + 16 * j + rl;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn + 16 * i + 4 * ks + q;
+        if (n < N) out[static_cast<int64_t>(n) * KW + k] = acc[i][j][q];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -1056,6 +1639,69 @@ inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias) {
   L.wt = off; off = al(off + (small ? 0 : 4LL * N * K));
   L.total = off;
   return L;
+}
+
+
+// ---- pack projection (host) --------------------------------------------------
+// Workspace of cign_pack_proj_bwd: Wp^T [2KD, D] (fp32, or bf16 in its
+// first half) | grad_Wp partials per row chunk | grad_b partials per row
+// chunk | grad_alpha partials per 16-channel block | the node gate's backward.
+struct PpWs {
+  int wg_chunks, b_chunks;
+  int64_t wg_chunk, b_chunk, wt, part_w, part_b, part_a, gate, total;
+};
+
+inline int pp_ntk(int D, int K) { return K * (D / 64); }
+
+inline PpWs pp_ws(int64_t M, int D, int K) {
+  PpWs L;
+  auto al = [](int64_t v) { return (v + 255) & ~int64_t(255); };
+  const int64_t kw = 2LL * K * D;
+  const int64_t tiles = static_cast<int64_t>((D + kWgT - 1) / kWgT) * pp_ntk(D, K);
+  int64_t wgc = std::max<int64_t>(1, std::min<int64_t>((M + 255) / 256, std::max<int64_t>(1, 512 / tiles)));
+  L.wg_chunk = std::max<int64_t>(kWgM, ((M + wgc - 1) / wgc + kWgM - 1) / kWgM * kWgM);
+  L.wg_chunks = static_cast<int>(M > 0 ? (M + L.wg_chunk - 1) / L.wg_chunk : 1);
+  int64_t bc = std::max<int64_t>(1, std::min<int64_t>(1024, (M + 63) / 64));
+  L.b_chunk = std::max<int64_t>(1, (M + bc - 1) / bc);
+  L.b_chunks = static_cast<int>(M > 0 ? (M + L.b_chunk - 1) / L.b_chunk : 1);
+  int64_t off = 0;
+  L.wt = off; off = al(off + 4 * kw * D);
+  L.part_w = off; off = al(off + 4LL * L.wg_chunks * D * kw);
+  L.part_b = off; off = al(off + 4LL * L.b_chunks * D);
+  L.part_a = off; off = al(off + 4LL * M * K * (D / 16));
+  L.gate = off; off = al(off + gate::node_gate_ws_bytes(M, D, K));
+  L.total = off;
+  return L;
+}
+
+inline int pp_check(const char* who, int64_t n, int D, int K, int interaction, int math, const float* H,
+                    const float* C, const float* const* props, int64_t prop_stride, const float* alpha,
+                    int64_t alpha_stride, const float* w) {
+  if (n < 0) return set_error(kInvalid, "%s: n=%lld", who, static_cast<long long>(n));
+  if (D != 64 && D != 128 && D != 256)
+    return set_error(kInvalid, "%s: D=%d; the fused pack projection takes D = 64, 128 or 256 (else cign_pack_gate_fwd "
+                     "+ cign_linear_gamma_fwd)", who, D);
+  if (K < 1 || K > kPackMaxHops) return set_error(kInvalid, "%s: K=%d outside [1, %d]", who, K, kPackMaxHops);
+  if (interaction < 0 || interaction > 2) return set_error(kInvalid, "%s: interaction must be 0, 1 or 2", who);
+  if (math != kMathF32 && math != kMathBF16) return set_error(kInvalid, "%s: math must be 0 or 1", who);
+  if (n > 0x7fffffffLL * kPpBM) return set_error(kInvalid, "%s: n too large", who);
+  if (!w || !alpha || !props || (n > 0 && (!H || !C))) return set_error(kInvalid, "%s: null pointer", who);
+  if (alpha_stride != 0 && alpha_stride < K) return set_error(kInvalid, "%s: alpha_stride must be 0 or >= K", who);
+  if (prop_stride < 2LL * D || prop_stride % 4 != 0)
+    return set_error(kInvalid, "%s: prop_stride must be a multiple of 4 and >= 2D", who);
+  bool ok = aligned16(H) && aligned16(C) && aligned16(w);
+  for (int k = 0; k < K; ++k) ok = ok && props[k] && aligned16(props[k]);
+  if (!ok) return set_error(kInvalid, "%s: H, C, every hop and the weight must be 16-byte aligned, non-null", who);
+  return kOk;
+}
+
+inline PackArgs pp_args(int64_t n, int D, int K, int interaction, const float* H, const float* C,
+                        const float* const* props, int64_t prop_stride, const float* alpha, int64_t alpha_stride) {
+  PackArgs a{};
+  a.M = n; a.D = D; a.K = K; a.mode = interaction; a.H = H; a.C = C; a.p_stride = prop_stride;
+  a.alpha = alpha; a.a_stride = alpha_stride;
+  for (int k = 0; k < K; ++k) a.P[k] = props[k];
+  return a;
 }
 
 }  // namespace gemm
@@ -1200,6 +1846,148 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
   g.round_bf16 = false;
   if ((rc = dispatch_nt<kEpiStore>(st, g, kF32, math, pick_bn(K, 0, math)))) return rc;
   return bias_grad();
+}
+
+int64_t cign_pack_proj_fwd_workspace_bytes(int32_t D, int32_t K, int32_t math) {
+  if (K < 1 || K > kPackMaxHops || (D != 64 && D != 128 && D != 256)) return 0;
+  return math == kMathBF16 ? 2LL * D * 2 * K * D : 0;
+}
+
+int cign_pack_proj_fwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t interaction, int32_t math,
+                       const float* H, const float* C, const float* const* props, int64_t prop_stride,
+                       const float* alpha, int64_t alpha_stride, const float* w, const float* bias, const float* h,
+                       const float* gamma, float dropout_p, uint64_t seed, float* g_out, float* out, uint8_t* mask,
+                       void* workspace, int64_t workspace_bytes) {
+  const char* who = "cign_pack_proj_fwd";
+  int rc = pp_check(who, n, D, K, interaction, math, H, C, props, prop_stride, alpha, alpha_stride, w);
+  if (rc) return rc;
+  const int64_t need = cign_pack_proj_fwd_workspace_bytes(D, K, math);
+  if (workspace_bytes < need || (need > 0 && (!workspace || !aligned16(workspace))))
+    return set_error(kInvalid, "%s: workspace too small or unaligned (%lld < %lld)", who,
+                     static_cast<long long>(workspace_bytes), static_cast<long long>(need));
+  if (!gamma || (n > 0 && (!h || !g_out || !out || !mask))) return set_error(kInvalid, "%s: null pointer", who);
+  if (!(dropout_p >= 0.0f && dropout_p < 1.0f)) return set_error(kInvalid, "%s: dropout_p must be in [0,1)", who);
+  if (!aligned16(h) || !aligned16(g_out) || !aligned16(out) || reinterpret_cast<uintptr_t>(mask) % 4 != 0)
+    return set_error(kInvalid, "%s: h, g_out and out must be 16-byte aligned, mask 4-byte", who);
+  if (n == 0) return kOk;
+  GemmArgs g{};
+  g.M = n; g.N = D; g.K = 2 * K * D; g.w = w; g.bias = bias; g.y = g_out;
+  g.vec = true; g.vec4 = true; g.round_bf16 = math == kMathBF16;
+  g.h = h; g.gamma = gamma; g.p = dropout_p; g.seed = seed; g.out = out; g.mask = mask;
+  PackArgs a = pp_args(n, D, K, interaction, H, C, props, prop_stride, alpha, alpha_stride);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (math == kMathBF16) {
+    __bf16* w16 = static_cast<__bf16*>(workspace);
+    const int64_t nw = 2LL * K * D * D;
+    hipLaunchKernelGGL(to_bf16_kernel, dim3(static_cast<unsigned>(std::min<int64_t>((nw + 255) / 256, 2048))),
+                       dim3(256), 0, st, w, nw, w16);
+    if ((rc = check_launch("cign_pack_proj_fwd (bf16 weight)"))) return rc;
+    a.w16 = w16;
+  }
+  // 64-row tiles: at the c2 block (24.5K rows, D = 256, bf16) 119 us against
+  // 146 us with 32-row tiles (twice the workgroups, twice the W tile loads)
+  const dim3 grid(static_cast<unsigned>((n + kPpBM - 1) / kPpBM));
+  auto go = [&](auto MC) {
+    constexpr int M_ = decltype(MC)::value;
+    if (D == 64) hipLaunchKernelGGL((pack_proj_fwd_kernel<M_, 64, kPpBM>), grid, dim3(kThreads), 0, st, g, a);
+    else if (D == 128) hipLaunchKernelGGL((pack_proj_fwd_kernel<M_, 128, kPpBM>), grid, dim3(kThreads), 0, st, g, a);
+    else hipLaunchKernelGGL((pack_proj_fwd_kernel<M_, 256, kPpBM>), grid, dim3(kThreads), 0, st, g, a);
+  };
+  if (math == kMathBF16) go(std::integral_constant<int, kMathBF16>());
+  else go(std::integral_constant<int, kMathF32>());
+  return check_launch(who);
+}
+
+int64_t cign_pack_proj_bwd_workspace_bytes(int64_t n, int32_t D, int32_t K) {
+  if (n < 0 || K < 1 || K > kPackMaxHops || (D != 64 && D != 128 && D != 256)) return 0;
+  return pp_ws(n, D, K).total;
+}
+
+int cign_pack_proj_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t interaction, int32_t math,
+                       const float* grad_g, const float* H, const float* C, const float* const* props,
+                       int64_t prop_stride, const float* alpha, int64_t alpha_stride, const float* w,
+                       int32_t score_mode, const float* gate_weight, float* grad_H, float* grad_C,
+                       float* const* grad_props, int64_t grad_prop_stride, float* grad_alpha, float* grad_w,
+                       float* grad_b, float* grad_gate_weight, float* grad_gate_bias, void* workspace,
+                       int64_t workspace_bytes) {
+  const char* who = "cign_pack_proj_bwd";
+  int rc = pp_check(who, n, D, K, interaction, math, H, C, props, prop_stride, alpha, alpha_stride, w);
+  if (rc) return rc;
+  if (!grad_w || !grad_props || (n > 0 && (!grad_g || !grad_H || !grad_C || !grad_alpha)))
+    return set_error(kInvalid, "%s: null pointer", who);
+  if (gate_weight && (!grad_gate_weight || !grad_gate_bias || alpha_stride != K))
+    return set_error(kInvalid, "%s: the node gate needs its gradient outputs and a per-node alpha (stride K)", who);
+  if (grad_prop_stride < 2LL * D || grad_prop_stride % 4 != 0)
+    return set_error(kInvalid, "%s: grad_prop_stride must be a multiple of 4 and >= 2D", who);
+  bool ok = aligned16(grad_g) && aligned16(grad_H) && aligned16(grad_C);
+  for (int k = 0; k < K; ++k) ok = ok && grad_props[k] && aligned16(grad_props[k]);
+  if (!ok) return set_error(kInvalid, "%s: grad_g, grad_H, grad_C and every grad_prop must be 16-byte aligned", who);
+  const PpWs L = pp_ws(n, D, K);
+  if (workspace_bytes < L.total || !workspace)
+    return set_error(kInvalid, "%s: workspace too small (%lld < %lld)", who, static_cast<long long>(workspace_bytes),
+                     static_cast<long long>(L.total));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int kw = 2 * K * D;
+  if (n == 0) {
+    if ((rc = rowops::zero_outputs(st, grad_w, D * kw, grad_b, grad_b ? D : 0, who))) return rc;
+    return gate_weight ? rowops::zero_outputs(st, grad_gate_weight, K * 2 * D, grad_gate_bias, K, who) : kOk;
+  }
+  char* ws = static_cast<char*>(workspace);
+  const dim3 tgrid((kw + 31) / 32, (D + 31) / 32);
+  if (math == kMathBF16)
+    hipLaunchKernelGGL(transpose_w_bf16_kernel, tgrid, dim3(256), 0, st, w, D, kw,
+                       reinterpret_cast<__bf16*>(ws + L.wt));
+  else
+    hipLaunchKernelGGL(transpose_w_kernel, tgrid, dim3(256), 0, st, w, D, kw, reinterpret_cast<float*>(ws + L.wt));
+  if ((rc = check_launch("cign_pack_proj_bwd (Wp^T)"))) return rc;
+  PackBwdArgs b{};
+  b.a = pp_args(n, D, K, interaction, H, C, props, prop_stride, alpha, alpha_stride);
+  b.gg = grad_g; b.wt = ws + L.wt; b.gH = grad_H; b.gC = grad_C; b.gp_stride = grad_prop_stride;
+  b.galpha_part = reinterpret_cast<float*>(ws + L.part_a);
+  for (int k = 0; k < K; ++k) b.gP[k] = grad_props[k];
+  const int cbw = math == kMathBF16 ? 32 : 16;  // channel block of pack_proj_bwd_kernel
+  const dim3 grid(static_cast<unsigned>((n + kPpBM - 1) / kPpBM), static_cast<unsigned>(D / cbw));
+  auto go = [&](auto MC) {
+    constexpr int M_ = decltype(MC)::value;
+    auto with_d = [&](auto KC) {
+      constexpr int K_ = decltype(KC)::value;
+      if (D == 64) hipLaunchKernelGGL((pack_proj_bwd_kernel<M_, K_, 64>), grid, dim3(kThreads), 0, st, b);
+      else if (D == 128) hipLaunchKernelGGL((pack_proj_bwd_kernel<M_, K_, 128>), grid, dim3(kThreads), 0, st, b);
+      else hipLaunchKernelGGL((pack_proj_bwd_kernel<M_, K_, 256>), grid, dim3(kThreads), 0, st, b);
+    };
+    switch (K) {
+      case 1: with_d(std::integral_constant<int, 1>()); break;
+      case 2: with_d(std::integral_constant<int, 2>()); break;
+      case 3: with_d(std::integral_constant<int, 3>()); break;
+      default: with_d(std::integral_constant<int, 4>()); break;
+    }
+    const int64_t mk = n * K;
+    hipLaunchKernelGGL(galpha_sum_kernel, dim3(static_cast<unsigned>((mk + 255) / 256)), dim3(256), 0, st,
+                       b.galpha_part, mk, D / cbw, grad_alpha);
+    const int ntk = pp_ntk(D, K);
+    const dim3 wgrid(static_cast<unsigned>(((D + kWgT - 1) / kWgT) * ntk), static_cast<unsigned>(L.wg_chunks));
+    hipLaunchKernelGGL((pack_wgrad_kernel<M_>), wgrid, dim3(kThreads), 0, st, grad_g, b.a, L.wg_chunk, ntk,
+                       reinterpret_cast<float*>(ws + L.part_w));
+  };
+  if (math == kMathBF16) go(std::integral_constant<int, kMathBF16>());
+  else go(std::integral_constant<int, kMathF32>());
+  if ((rc = check_launch(who))) return rc;
+  if ((rc = rowops::launch_colsum(st, reinterpret_cast<float*>(ws + L.part_w), L.wg_chunks, D * kw, 1, grad_w,
+                                  nullptr, "cign_pack_proj_bwd (grad_Wp)")))
+    return rc;
+  if (grad_b) {
+    float* part = reinterpret_cast<float*>(ws + L.part_b);
+    hipLaunchKernelGGL(bias_grad_kernel, dim3((D + 63) / 64, L.b_chunks), dim3(kThreads), 0, st, grad_g, n, D,
+                       L.b_chunk, part);
+    if ((rc = check_launch("cign_pack_proj_bwd (bias partials)"))) return rc;
+    if ((rc = rowops::launch_colsum(st, part, L.b_chunks, D, 1, grad_b, nullptr, "cign_pack_proj_bwd (bias)")))
+      return rc;
+  }
+  if (!gate_weight) return kOk;
+  // the node gate's backward, its input gradients added to the pack's
+  return gate::node_gate_bwd(st, n, D, K, score_mode, H, C, gate_weight, alpha, grad_alpha, grad_H, grad_C,
+                             grad_gate_weight, grad_gate_bias, ws + L.gate, L.total - L.gate, true,
+                             "cign_pack_proj_bwd (node gate)");
 }
 
 }  // extern "C"

@@ -15,7 +15,9 @@ The reference picks between PyG / dgNN / CUDA / torch paths with its
 - the hop gate kernel;
 - the fused Clifford pack for any interaction x weighting x K;
 - the projection ``proj`` with bias, dropout and the gamma residual in its
-  epilogue (one MFMA kernel, cign_linear_gamma_fwd).
+  epilogue (one MFMA kernel, cign_linear_gamma_fwd); with weighting old and
+  hidden 64, 128 or 256 the pack is built inside that kernel's operand load
+  (cign_pack_proj_fwd / _bwd) and G_raw is never stored.
 
 The flags are accepted for signature compatibility and validated like the
 reference's. ``use_chunked_fused_gat`` (the reference's dgNN chunking backend,
@@ -32,7 +34,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import _pack
+from . import _pack, pack_proj
 from .collapsed_gat import collapsed_gat_mean_bias_silu
 from .fused_block_ops import fused_add_layernorm_cat, fused_dropout_layernorm
 from .graph import selected_sparse_powers
@@ -225,6 +227,13 @@ class GraphCliffordBlock(nn.Module):
         propagated = selected_sparse_powers(operator=graph_operator, X=HC_norm, powers=self.order_set)
         props = [propagated[s] for s in self.order_set]
         weighting = 0 if self.alpha_weighting_mode == "old" else 1
+        gamma = self.gamma if self.gamma_mode == "vector" else self.gamma.expand(self.hidden_dim)
+        if pack_proj.use_fused(self.hidden_dim, self.num_hops, weighting, self.use_selective_amp):
+            # the pack built inside proj's MFMA kernels: G_raw is never stored
+            return pack_proj.pack_proj_gamma_residual(H, H_norm, C_norm, props, self.hop_gate_mode,
+                                                      self.hop_gate_mlp, self.hop_gate_logits, self.alpha_score_mode,
+                                                      self._interaction_code(), self.proj, gamma, p,
+                                                      self.use_selective_amp, self.selective_amp_dtype)
         if self.hop_gate_mode == "node":
             # the gate's only consumer is the pack: one fused kernel each way
             G_raw = gated_clifford_pack(H_norm, C_norm, props, self.hop_gate_mlp, self.alpha_score_mode,
@@ -232,7 +241,6 @@ class GraphCliffordBlock(nn.Module):
         else:
             G_raw = _pack.clifford_pack_any(H_norm, C_norm, props, self.compute_hop_gate(H_norm, C_norm),
                                             self._interaction_code(), weighting)
-        gamma = self.gamma if self.gamma_mode == "vector" else self.gamma.expand(self.hidden_dim)
         return linear_gamma_residual(H, G_raw, self.proj, gamma.contiguous(), p, self.use_selective_amp,
                                      self.selective_amp_dtype)
 

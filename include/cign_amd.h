@@ -324,6 +324,46 @@ int cign_pack_gate_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t in
                        float* grad_H, float* grad_C, float* const* grad_props, int64_t grad_prop_stride,
                        float* grad_gate_weight, float* grad_gate_bias, void* workspace, int64_t workspace_bytes);
 
+/* The Clifford pack (weighting old: G = cat_k alpha_k [W_k, D_k], [n, 2KD])
+ * built inside the projection's MFMA operand load, with the gamma epilogue
+ * of cign_linear_gamma_fwd: g_out = G Wp^T + bias, out = h + gamma *
+ * drop(g_out), mask. G is never stored. Replaces the pack feeding `proj`
+ * (generic_engine/model_cign.py:803-846 then :927-933). D in {64, 128, 256},
+ * 1 <= K <= 4, interaction as cign_pack_fwd, math as cign_linear_fwd; props:
+ * HOST array of K device row pointers (row stride prop_stride floats, >= 2D);
+ * alpha [n,K] with row stride alpha_stride (K), or one row for every node
+ * (stride 0: the global gate, or ones without a gate); w = Wp [D, 2KD];
+ * workspace of cign_pack_proj_fwd_workspace_bytes. */
+int cign_pack_proj_fwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t interaction, int32_t math,
+                       const float* H, const float* C, const float* const* props, int64_t prop_stride,
+                       const float* alpha, int64_t alpha_stride, const float* w, const float* bias, const float* h,
+                       const float* gamma, float dropout_p, uint64_t seed, float* g_out, float* out, uint8_t* mask,
+                       void* workspace, int64_t workspace_bytes);
+
+/* Workspace bytes of cign_pack_proj_fwd (with math = 1, the bf16 copy of w
+ * the kernel reads; 0 with math = 0 or for shapes it does not take). */
+int64_t cign_pack_proj_fwd_workspace_bytes(int32_t D, int32_t K, int32_t math);
+
+/* Workspace bytes of cign_pack_proj_bwd (0 for shapes it does not take). */
+int64_t cign_pack_proj_bwd_workspace_bytes(int64_t n, int32_t D, int32_t K);
+
+/* Backward of cign_pack_proj_fwd from grad_g = d out / d g_out (as
+ * cign_gamma_residual_bwd gives it): grad_G = grad_g Wp computed per block of
+ * 32 channels of every hop and half and consumed in the same kernel by the
+ * pack's backward (grad_H, grad_C, grad_props [n,2D] each, grad_alpha [n,K]),
+ * grad_w [D,2KD] = grad_g^T G with G rebuilt in the reduction's operand load,
+ * grad_b (NULL to skip) = sum_n grad_g. With gate_weight (the node gate of
+ * cign_hop_gate_fwd that produced alpha, stride K), the gate's backward is
+ * added: its input terms into grad_H / grad_C, grad_gate_weight [K,2D],
+ * grad_gate_bias [K]. Replaces the autograd of the same lines. */
+int cign_pack_proj_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t interaction, int32_t math,
+                       const float* grad_g, const float* H, const float* C, const float* const* props,
+                       int64_t prop_stride, const float* alpha, int64_t alpha_stride, const float* w,
+                       int32_t score_mode, const float* gate_weight, float* grad_H, float* grad_C,
+                       float* const* grad_props, int64_t grad_prop_stride, float* grad_alpha, float* grad_w,
+                       float* grad_b, float* grad_gate_weight, float* grad_gate_bias, void* workspace,
+                       int64_t workspace_bytes);
+
 /* ---- Clifford packs (float32) ------------------------------------------- */
 
 /* Fused Clifford interaction + alpha weighting over K <= 16 hops.

@@ -60,15 +60,21 @@ def random_gat_graph(rng, n, avg_deg=6, hubs=None):
 
 def assert_close_fp32_derived(actual, expected64, expected32, name="", rtol=1e-4, atol=1e-5, k=4.0):
     """Tolerance for float32 results that sum over many nodes (parameter
-    gradients): |a - e64| <= atol + rtol |e64| + k |e32 - e64| elementwise,
-    where e32 is the same oracle computation carried out in float32 on the
-    same inputs. |e32 - e64| is the rounding error float32 arithmetic incurs
-    on exactly this computation; k allows for a different summation order."""
+    gradients): |a - e64| <= atol + rtol |e64| + k |e32 - e64| + max |e32 -
+    e64| elementwise, where e32 is the same oracle computation carried out in
+    float32 on the same inputs. |e32 - e64| is the rounding error float32
+    arithmetic incurs on exactly this computation; k allows for a different
+    summation order, and the tensor's largest such error covers the elements
+    where the oracle's own order happened to round well (the GPU's order
+    rounds differently: at D = 128 a GAT attention gradient the fp32 oracle
+    got within 7e-6 was 2.3e-4 off on the GPU, inside the 5.6e-4 the oracle
+    itself missed by elsewhere in that tensor)."""
     a = np.asarray(actual, dtype=np.float64)
     e = np.asarray(expected64, dtype=np.float64)
     e32 = np.asarray(expected32, dtype=np.float64)
     assert a.shape == e.shape == e32.shape, f"{name}: shapes {a.shape} {e.shape} {e32.shape}"
-    bound = atol + rtol * np.abs(e) + k * np.abs(e32 - e)
+    err32 = np.abs(e32 - e)
+    bound = atol + rtol * np.abs(e) + k * err32 + (err32.max() if err32.size else 0.0)
     err = np.abs(a - e)
     bad = err > bound
     if bad.any():

@@ -3,9 +3,11 @@ GraphCliffordBlock on the HIP route) against the float64 torch restatement of
 the reference block (oracle/block_oracle.py), forward output and the
 gradients of the input and of every parameter, in eval mode (no dropout; the
 dropout masks are pinned op by op in test_gpu_nodeops / test_gpu_gat).
-fp32 tolerance 1e-4 rel / 1e-5 abs on the output and grad H; parameter
-gradients (sums over nodes) within 1e-4 rel / 1e-5 abs plus four times the
-rounding error of the same oracle run in float32; bf16 selective AMP 2e-2."""
+fp32 tolerance 1e-4 rel / 1e-5 abs on the output and (D = 32) grad H;
+parameter gradients (sums over nodes), and grad H at D >= 64, within 1e-4
+rel / 1e-5 abs plus four times the rounding error of the same oracle run in
+float32; bf16 selective AMP 2e-2. Widths 64, 128 and 256 (the production
+block, 6 GAT heads x 256) run the fused pack projection."""
 import numpy as np
 import pytest
 import torch
@@ -66,13 +68,36 @@ MODES = [
 
 @pytest.mark.parametrize("score,interaction,weighting,gate,outer", MODES)
 def test_block_forward_backward_matches_oracle(score, interaction, weighting, gate, outer, monkeypatch):
+    _check_block(score, interaction, weighting, gate, outer, 300, 32, 4, monkeypatch)
+
+
+# Widths the fused pack projection takes (weighting old): its kernels build
+# G_raw inside proj; D = 256 with 6 heads x 256 is the production block.
+WIDE = [
+    ("new", "new", "old", "node", "none", 64, 4),
+    ("old", "old", "old", "global", "tanh", 64, 4),
+    ("new", "new", "old", "none", "none", 128, 2),
+    ("new", "new", "old", "node", "none", 256, 6),
+]
+
+
+@pytest.mark.parametrize("pack_proj", ["all", "none"])
+@pytest.mark.parametrize("score,interaction,weighting,gate,outer,D,heads", WIDE)
+def test_block_fused_pack_projection_matches_oracle(score, interaction, weighting, gate, outer, D, heads, pack_proj,
+                                                    monkeypatch):
+    """Both tails at the widths the fused kernels take: fused (G_raw never
+    stored) and the pack + projection pair (CIGN_PACK_PROJ)."""
+    monkeypatch.setenv("CIGN_PACK_PROJ", pack_proj)
+    _check_block(score, interaction, weighting, gate, outer, 300, D, heads, monkeypatch)
+
+
+def _check_block(score, interaction, weighting, gate, outer, n, D, heads, monkeypatch):
     from cign_amd.model_cign import GraphCliffordBlock
     from oracle import block_oracle as B
 
-    print(f"block score={score} interaction={interaction} weighting={weighting} gate={gate} outer={outer}",
-          flush=True)
+    print(f"block score={score} interaction={interaction} weighting={weighting} gate={gate} outer={outer} D={D} "
+          f"heads={heads}", flush=True)
     monkeypatch.setenv("CIGN_OUTER_NONLINEARITY", outer)
-    n, D, heads = 300, 32, 4
     mh, gat_graph, (rp, cl), p_np = _setup(n, D)
     block = GraphCliffordBlock(D, order_set=(1, 2, 3), gat_heads=heads, hop_gate_mode=gate, alpha_score_mode=score,
                                interaction_mode=interaction, alpha_weighting_mode=weighting).cuda().eval()
@@ -93,10 +118,19 @@ def test_block_forward_backward_matches_oracle(score, interaction, weighting, ga
         (ref * G.to(dt)).sum().backward()
         refs[dt] = (ref, Hr, params)
     ref, H64, params = refs[torch.float64]
-    params32 = refs[torch.float32][2]
-    _close(out, ref, "out")
+    ref32, H32, params32 = refs[torch.float32]
     (out * G.cuda()).sum().backward()
-    _close(H.grad, H64.grad, "grad H")
+    if D <= 32:
+        _close(out, ref, "out")
+        _close(H.grad, H64.grad, "grad H")
+    else:
+        # From D = 128 the float32 restatement itself misses 1e-4 / 1e-5 (D =
+        # 256: 2.1e-5 on the output, 5.1e-4 on grad H at |grad H| <= 67, from
+        # the sums over 6 x 256 GAT channels, 1536 proj inputs and the
+        # LayerNorm rows), and so does the unfused GPU path by the same
+        # amount; the bound is then the fp32-derived one.
+        _close_param_grad(out, ref, ref32, "out")
+        _close_param_grad(H.grad, H64.grad, H32.grad, "grad H")
     for name, p in block.named_parameters():
         assert p.grad is not None, name
         _close_param_grad(p.grad, params[name].grad, params32[name].grad, f"grad {name}")
@@ -110,7 +144,20 @@ def test_block_selective_amp_bf16():
     from cign_amd.model_cign import GraphCliffordBlock
     from oracle import block_oracle as B
 
-    n, D, heads = 300, 32, 4
+    _check_block_amp(300, 32, 4)
+
+
+def test_block_selective_amp_bf16_production_width():
+    """The same at the production width (D = 256, 6 GAT heads x 256), where
+    proj runs as the fused pack projection."""
+    _check_block_amp(300, 256, 6)
+
+
+def _check_block_amp(n, D, heads):
+    from cign_amd.model_cign import GraphCliffordBlock
+    from oracle import block_oracle as B
+
+    print(f"block amp D={D} heads={heads}", flush=True)
     mh, gat_graph, (rp, cl), p_np = _setup(n, D, seed=3)
     block = GraphCliffordBlock(D, gat_heads=heads, use_selective_amp=True, alpha_score_mode="new",
                                interaction_mode="new", alpha_weighting_mode="old").cuda().eval()
