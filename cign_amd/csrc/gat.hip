@@ -43,7 +43,7 @@ int dispatch_hc(int H, int C, Args&&... args) {
 }
 
 struct BwdLayout {
-  int64_t grad_pre, gscore, wsum, rowstat, bias_part, bias_l2, part_row, part_col, total;
+  int64_t grad_pre, gscore, wsum, bias_part, bias_l2, part_row, part_col, total;
 };
 
 inline int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
@@ -59,10 +59,11 @@ inline BwdLayout bwd_layout(int n, int nnz, int H, int C, int row_blocks, int n_
   // (partials of grad_pre rows).
   const int n_l2 = max((row_blocks + 63) / 64, kFlBiasBlocks);
   int64_t off = 0;
-  L.grad_pre = off; off = align256(off + 4LL * n * C);
+  // grad_pre rows of C + 4H floats: the feature layout keeps each row's
+  // softmax record after its g_pre; the pair layout uses the first n*C.
+  L.grad_pre = off; off = align256(off + 4LL * n * (C + 4LL * H));
   L.gscore = off; off = align256(off + 4LL * nnz * H);
   L.wsum = off; off = align256(off + 4LL * n * H);
-  L.rowstat = off; off = align256(off + 16LL * n * H);
   L.bias_part = off; off = align256(off + 4LL * row_blocks * C);
   L.bias_l2 = off; off = align256(off + 4LL * n_l2 * C);
   L.part_row = off; off = align256(off + 4LL * n_seg_rows * 3 * H);
@@ -352,9 +353,11 @@ int gat_bwd_impl(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
     a.emax = edge_max; a.esum = edge_sum; a.mask = edge_mask; a.x = xt;
     a.attn_row = attn_row; a.attn_col = attn_col; a.pre = pre; a.grad_y = gyt; a.agg = row_agg;
     a.grad_pre = reinterpret_cast<float*>(ws + L.grad_pre);
+    a.gp_stride = channels;
+    a.rowstat = nullptr;
+    a.rs_stride = 0;
     a.gscore = reinterpret_cast<float*>(ws + L.gscore);
     a.wsum = reinterpret_cast<float*>(ws + L.wsum);
-    a.rowstat = reinterpret_cast<float4*>(ws + L.rowstat);
     a.bias_part = reinterpret_cast<float*>(ws + L.bias_part);
     a.bias_l2 = reinterpret_cast<float*>(ws + L.bias_l2);
     a.part_row = reinterpret_cast<float*>(ws + L.part_row);
@@ -365,6 +368,10 @@ int gat_bwd_impl(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
       if (!aligned16(xt) || !aligned16(gyt) || !aligned16(gxt) || !aligned16(pre) || !aligned16(grad_bias))
         return set_error(kInvalid, "cign_gat_bwd: in_feat, pre, grad_y, grad_feat and grad_bias must be 16-byte "
                                    "aligned");
+      // one contiguous record per destination row: g_pre, then H float4s
+      a.gp_stride = channels + 4 * heads;
+      a.rowstat = reinterpret_cast<float4*>(a.grad_pre + channels);
+      a.rs_stride = a.gp_stride / 4;
       const int lgcq = fl_lgcq(dtype, channels);
       int L, V;
       fl_geom(dtype, heads, channels, L, V);

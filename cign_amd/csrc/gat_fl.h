@@ -850,9 +850,8 @@ __device__ __forceinline__ void rows_dots(const RowAcc<W, V>& st, const float (&
 template <typename T>
 __device__ __forceinline__ void rows_store(const GatBwdArgs<T>& a, int row, int hq, float ar, float em, float ies,
                                            float wsum, float A, float B) {
-  const int64_t idx = static_cast<int64_t>(row) * a.H + hq;
-  a.grad_attn_row[idx] = A - wsum * B;
-  a.rowstat[idx] = make_float4(ar, em, ies, wsum);
+  a.grad_attn_row[static_cast<int64_t>(row) * a.H + hq] = A - wsum * B;
+  a.rowstat[static_cast<int64_t>(row) * a.rs_stride + hq] = make_float4(ar, em, ies, wsum);
 }
 
 // Lane stores of a finished light row: grad_attn_row / rowstat of its heads
@@ -866,7 +865,7 @@ __device__ __forceinline__ void rows_emit(const GatBwdArgs<T>& a, const FlLane<L
 #pragma unroll
     for (int v = 0; v < V; ++v)
       if (ln.qv[v]) rows_store(a, row, ln.hq[v], rh.ar[v], rh.em[v], rh.ies[v], wsum[v], A[v], B[v]);
-  if (ln.qv[0] && ln.hq[0] == 0) store_f32<W>(a.grad_pre + static_cast<int64_t>(row) * a.C + ln.cw * W, gp);
+  if (ln.qv[0] && ln.hq[0] == 0) store_f32<W>(a.grad_pre + static_cast<int64_t>(row) * a.gp_stride + ln.cw * W, gp);
 }
 
 template <typename T, int L, int V, bool DROP>
@@ -946,7 +945,7 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a
       }
   // The row's g_pre is published once, by its first segment.
   if (b == hr.x && wave == 0 && ln.g == 0 && ln.qv[0] && ln.hq[0] == 0)
-    store_f32<W>(a.grad_pre + static_cast<int64_t>(row) * a.C + ln.cw * W, gp);
+    store_f32<W>(a.grad_pre + static_cast<int64_t>(row) * a.gp_stride + ln.cw * W, gp);
   __syncthreads();
   if (threadIdx.x < 3 * kFlHeads) {
     const int k = threadIdx.x / kFlHeads, h = threadIdx.x % kFlHeads;
@@ -1040,6 +1039,22 @@ constexpr bool cols_pairwise() {
   return V > 1;
 }
 
+// Softmax weight e^(leaky(raw) - max) / sum of a CSC entry from its
+// destination row's record rs = {attn_row, max, 1/sum, wsum}; 0 for an unused
+// slot. Branch-free: an unused slot's record (some valid row's) is loaded
+// like the others and the selects leave nothing to do conditionally, so the
+// whole record arrives in one 16-byte load instead of a second load issued
+// behind a branch once the first has returned.
+__device__ __forceinline__ float col_weight(const float4& rs, float raw, float slope, bool own) {
+  return softmax_exp(own ? leaky(raw, slope) - rs.y : -__builtin_inff()) * (own ? rs.z : 0.0f);
+}
+
+// Float offset of record row i (i < 2^31, stride < 2^31): one 32 x 32 -> 64
+// bit multiply.
+__device__ __forceinline__ uint64_t rec_off(uint32_t i, int stride) {
+  return static_cast<uint64_t>(i) * static_cast<uint32_t>(stride);
+}
+
 // Batches of CSC entries of column j: slot u's destination row is held by
 // lane (base + u) in ii, its CSR edge id (used only with dropout) in ee. The
 // g_pre chunk of a destination row is shared by the lane's V heads.
@@ -1060,10 +1075,10 @@ struct ColBatches {
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
       const int src = (base + (u < cnt ? u : 0)) & (kWave - 1);
-      const int i = shfl(ii, src);
-      load_f32<W>(a.grad_pre + static_cast<int64_t>(i) * a.C + ln.cw * W, gb[k]);
+      const uint32_t i = shfl(ii, src);
+      load_f32<W>(a.grad_pre + rec_off(i, a.gp_stride) + ln.cw * W, gb[k]);
 #pragma unroll
-      for (int v = 0; v < V; ++v) rs[k][v] = a.rowstat[static_cast<int64_t>(i) * a.H + ln.hq[v]];
+      for (int v = 0; v < V; ++v) rs[k][v] = a.rowstat[rec_off(i, a.rs_stride) + ln.hq[v]];
     }
     // Dropout mask bytes (CSR edge id from perm): each (entry, head) pair
     // loaded once.
@@ -1081,7 +1096,7 @@ struct ColBatches {
       for (int v = 0; v < V; ++v) {
         const float raw = rs[k][v].x + ac[v];
         const float lp = raw < 0.0f ? a.slope : 1.0f;
-        const float sm = u < cnt ? softmax_exp(leaky(raw, a.slope) - rs[k][v].y) * rs[k][v].z : 0.0f;
+        const float sm = col_weight(rs[k][v], raw, a.slope, u < cnt);
         float w = sm;
         if constexpr (DROP) w = kb.get(k, ln.hq[v], ln.g) ? sm * (1.0f / (1.0f - a.p)) : 0.0f;
         const float wl = w * lp;
@@ -1117,8 +1132,8 @@ struct ColSharedBatches {
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
-      const uint64_t i = static_cast<uint32_t>(shfl(ii, (base + (u < cnt ? u : 0)) & (kWave - 1)));
-      load_f32<W>(a.grad_pre + i * a.C + ln.cw * W, gb[k]);
+      const uint32_t i = shfl(ii, (base + (u < cnt ? u : 0)) & (kWave - 1));
+      load_f32<W>(a.grad_pre + rec_off(i, a.gp_stride) + ln.cw * W, gb[k]);
     }
     const int r = ln.gl & (R - 1);
     float wk[NT][V], wl[NT][V];
@@ -1128,18 +1143,20 @@ struct ColSharedBatches {
       const int u = first + (k0 + kk) * step;
       const bool own = kk < U && u < cnt;
       const int src = (base + (own ? u : 0)) & (kWave - 1);
-      const uint64_t i = static_cast<uint32_t>(shfl(ii, src));
+      const uint32_t i = shfl(ii, src);
       int e = 0;
       if constexpr (DROP) e = shfl(ee, src);
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        const float4 rs = a.rowstat[i * a.H + ln.hq[v]];
+        const float4 rs = a.rowstat[rec_off(i, a.rs_stride) + ln.hq[v]];
         const float raw = rs.x + ac[v];
         const float lp = raw < 0.0f ? a.slope : 1.0f;
-        const float sm = own ? softmax_exp(leaky(raw, a.slope) - rs.y) * rs.z : 0.0f;
+        const float sm = col_weight(rs, raw, a.slope, own);
         float w = sm;
+        // (an unused slot's e is a valid edge id: its mask byte is read and
+        // ignored)
         if constexpr (DROP)
-          w = (own && a.mask[static_cast<int64_t>(e) * a.H + ln.hq[v]] != 0) ? sm * (1.0f / (1.0f - a.p)) : 0.0f;
+          w = (a.mask[static_cast<int64_t>(e) * a.H + ln.hq[v]] != 0) ? sm * (1.0f / (1.0f - a.p)) : 0.0f;
         st.t[v] = fmaf(sm * lp, rs.w, st.t[v]);
         wk[t][v] = w;
         wl[t][v] = w * lp;
@@ -1194,8 +1211,8 @@ struct ColPairBatches {
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
-      const int i = shfl(ii, (base + (u < cnt ? u : 0)) & (kWave - 1));
-      load_f32<W>(a.grad_pre + static_cast<int64_t>(i) * a.C + ln.cw * W, gb[k]);
+      const uint32_t i = shfl(ii, (base + (u < cnt ? u : 0)) & (kWave - 1));
+      load_f32<W>(a.grad_pre + rec_off(i, a.gp_stride) + ln.cw * W, gb[k]);
     }
     const int h = ln.gl % S;
     float pw[R], pwl[R];
@@ -1205,17 +1222,17 @@ struct ColPairBatches {
       const int u = first + (k0 + k) * step;
       const bool own = h < a.H && k < U && u < cnt;
       const int src = (base + (own ? u : 0)) & (kWave - 1);
-      const int i = shfl(ii, src);
-      float4 rs = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (own) rs = a.rowstat[static_cast<int64_t>(i) * a.H + h];
+      const uint32_t i = shfl(ii, src);
+      const int hc = h < a.H ? h : a.H - 1;  // pair lanes past the heads read head H-1's record, unused
+      const float4 rs = a.rowstat[rec_off(i, a.rs_stride) + hc];
       bool keep = true;
       if constexpr (DROP) {
         const int e = shfl(ee, src);
-        keep = own && a.mask[static_cast<int64_t>(e) * a.H + h] != 0;
+        keep = a.mask[static_cast<int64_t>(e) * a.H + hc] != 0;
       }
       const float raw = rs.x + acp;
       const float lp = raw < 0.0f ? a.slope : 1.0f;
-      const float sm = own ? softmax_exp(leaky(raw, a.slope) - rs.y) * rs.z : 0.0f;
+      const float sm = col_weight(rs, raw, a.slope, own);
       float w = sm;
       if constexpr (DROP) w = keep ? sm * (1.0f / (1.0f - a.p)) : 0.0f;
       st.tp = fmaf(sm * lp, rs.w, st.tp);

@@ -481,10 +481,15 @@ struct GatBwdArgs {
   const T* grad_y;
   const float* agg;  // per-row aggregates written by the forward, or null
   // workspace
-  float* grad_pre;   // [n, C]
+  float* grad_pre;   // [n, gp_stride]: g_pre in the row's first C floats
+  int gp_stride;     // floats per grad_pre row: C (pair layout) or C + 4H
   float* gscore;     // [nnz, H]: ge' = keep/(1-p) * <g_pre, x>/H
   float* wsum;       // [n, H]: sum_e s ge'
-  float4* rowstat;   // [n, H]: {attn_row, edge_max, 1/edge_sum, wsum} (feature layout)
+  // Feature layout: {attn_row, edge_max, 1/edge_sum, wsum} per head, stored
+  // after the row's g_pre (rowstat = grad_pre + C, rs_stride = gp_stride / 4
+  // float4s per row), so a column's entry gathers one contiguous record.
+  float4* rowstat;
+  int rs_stride;
   float* bias_part;  // [rows_blocks, C]
   float* bias_l2;    // [n_l2, C]
   float* part_row;   // [n_seg_rows, 3H]
@@ -514,7 +519,7 @@ __device__ __forceinline__ void bwd_grad_pre(const GatBwdArgs<T>& a, int row, in
     const int64_t idx = static_cast<int64_t>(row) * a.C + c;
     const float g = to_f32(a.grad_y[idx]) * silu_grad(a.pre[idx]);
     gp[c] = g;
-    if (publish) a.grad_pre[idx] = g;
+    if (publish) a.grad_pre[static_cast<int64_t>(row) * a.gp_stride + c] = g;
   }
 }
 
@@ -733,7 +738,7 @@ __device__ __forceinline__ void bwd_col_gather(const GatBwdArgs<T>& a, int cb, c
   float gv[N][CP];
 #pragma unroll
   for (int k = 0; k < N; ++k)
-    load_run<float, CP>(a.grad_pre + static_cast<int64_t>(i[k]) * a.C + cb * CP, nvalid, a.vec_gp, gv[k]);
+    load_run<float, CP>(a.grad_pre + static_cast<int64_t>(i[k]) * a.gp_stride + cb * CP, nvalid, a.vec_gp, gv[k]);
 #pragma unroll
   for (int c = 0; c < CP; ++c) acc[c] = 0.0f;
 #pragma unroll
@@ -782,7 +787,7 @@ __device__ __forceinline__ void bias_reduce(const GatBwdArgs<T>& a, int q, int* 
 // that range (R = ceil(bias_n / n_l2)) into bias_l2[q];
 // the last one to finish sums the n_l2 partials in order. Threads own a
 // (row, 4-channel chunk) pair and read float4 (C % 4 == 0, rows 16-byte
-// aligned), 256 / (C/4) rows per step.
+// aligned; grad_pre rows gp_stride floats apart), 256 / (C/4) rows per step.
 template <typename T>
 __device__ __forceinline__ void bias_from_grad_pre(const GatBwdArgs<T>& a, int q, int* counter, int* flag) {
   __shared__ float4 red[kBlock];
@@ -792,11 +797,11 @@ __device__ __forceinline__ void bias_from_grad_pre(const GatBwdArgs<T>& a, int q
   const int tid = threadIdx.x;
   const int c4 = tid % c4n;
   const int r0 = tid / c4n;
-  auto reduce = [&](const float* src, int lo, int hi, float* dst) {
+  auto reduce = [&](const float* src, int stride, int lo, int hi, float* dst) {
     float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll 4
     for (int r = lo + r0; r < hi; r += rpi) {
-      const float4 v = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(r) * C + c4 * 4);
+      const float4 v = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(r) * stride + c4 * 4);
       t.x += v.x;
       t.y += v.y;
       t.z += v.z;
@@ -819,9 +824,10 @@ __device__ __forceinline__ void bias_from_grad_pre(const GatBwdArgs<T>& a, int q
   };
   const int R = (a.bias_n + a.n_l2 - 1) / a.n_l2;
   const int lo = min(a.bias_n, q * R), hi = min(a.bias_n, lo + R);
-  reduce(a.grad_pre + static_cast<int64_t>(a.bias_lo) * C, lo, hi, a.bias_l2 + static_cast<int64_t>(q) * C);
+  reduce(a.grad_pre + static_cast<int64_t>(a.bias_lo) * a.gp_stride, a.gp_stride, lo, hi,
+         a.bias_l2 + static_cast<int64_t>(q) * C);
   if (!arrive_last(counter, a.n_l2, flag)) return;
-  reduce(a.bias_l2, 0, a.n_l2, a.grad_bias);
+  reduce(a.bias_l2, C, 0, a.n_l2, a.grad_bias);
 }
 
 template <typename T, int HP, int CP>
