@@ -284,7 +284,9 @@ struct FwdState {
 // through DPP: broadcast of lane S, max and sum over the R lanes.
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+  // bound_ctrl: a lane reading a disabled lane gets 0 (as from an old value
+  // of 0) and the destination needs no initialisation.
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 template <int R, int S>
 __device__ __forceinline__ float quad_bcast(float v) {
@@ -1493,6 +1495,349 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
   }
 }
 
+// ===========================================================================
+// Backward, columns, channel-major lanes
+// ===========================================================================
+// Narrow rows of H = 4 heads and C = 4 LC channels (LC in {4, 8, 16}): a
+// group of LC lanes owns a column and lane c the channels [4c, 4c + 4) of
+// every head, so a destination row's g_pre chunk is gathered once per entry
+// rather than once per head as in the head-major lanes above (at 62.4M edges
+// those gathers kept the address units 78% busy and the VALU 58%). Lane r of
+// the column's first quad loads head r's part of each slot's row record and
+// computes its softmax weight; DPP row shifts pass the weights to the other
+// quads and quad broadcasts to every lane. Light columns
+// (degree <= kFlLightMax) run one per group, G = 64 / LC per wavefront (the
+// light list is sorted by degree, so a wavefront's columns need about the
+// same number of batches), in batches of U slots whose row indices are loaded
+// one batch ahead; heavy columns are segments, as in the head-major kernel.
+// Large graphs only (the same threshold as the forward's): a group streams
+// all of a light column's entries in sequence, up to 16 dependent batches,
+// which bounds a small graph's launch (c2: 30.9 us against 23.1 us for the
+// head-major kernel, whose wavefront splits a column of more than L entries
+// over its groups).
+// 4 slots per batch: at 62.4M edges 2.85 ms for the backward against 3.06 ms
+// with 8 (138 VGPRs, one wavefront per SIMD fewer).
+#ifndef CIGN_FL_COLS_CM_U
+#define CIGN_FL_COLS_CM_U 4
+#endif
+constexpr int kColsCmHeads = 4;
+
+inline bool cols_cm_ok(int H, int C) { return H == kColsCmHeads && (C == 16 || C == 32 || C == 64); }
+
+// Four consecutive elements of T (16 bytes of fp32, 8 of bf16), kept raw
+// while loads are in flight and unpacked on use.
+template <typename T>
+struct Four;
+template <>
+struct Four<float> {
+  using Raw = float4;
+  static __device__ __forceinline__ Raw load(const float* p) { return *reinterpret_cast<const float4*>(p); }
+  static __device__ __forceinline__ void unpack(const Raw& q, float (&v)[4]) {
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  }
+};
+template <>
+struct Four<bf16> {
+  using Raw = uint2;
+  static __device__ __forceinline__ Raw load(const bf16* p) { return *reinterpret_cast<const uint2*>(p); }
+  static __device__ __forceinline__ void unpack(const Raw& q, float (&v)[4]) {
+    v[0] = __uint_as_float(q.x << 16);
+    v[1] = __uint_as_float(q.x & 0xffff0000u);
+    v[2] = __uint_as_float(q.y << 16);
+    v[3] = __uint_as_float(q.y & 0xffff0000u);
+  }
+};
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const float (&v)[4]);
+template <>
+__device__ __forceinline__ void store4<float>(float* p, const float (&v)[4]) {
+  Chunk<float, 4>::store(p, v);
+}
+template <>
+__device__ __forceinline__ void store4<bf16>(bf16* p, const float (&v)[4]) {
+  const uint32_t w0 = from_f32<bf16>(v[0]).bits | (static_cast<uint32_t>(from_f32<bf16>(v[1]).bits) << 16);
+  const uint32_t w1 = from_f32<bf16>(v[2]).bits | (static_cast<uint32_t>(from_f32<bf16>(v[3]).bits) << 16);
+  *reinterpret_cast<uint2*>(p) = make_uint2(w0, w1);
+}
+
+// Sums over a column's entries held by one lane: ug[h] = sum s kw g_pre
+// chunk, ua[h] = sum s kw l' g_pre chunk for every head h; t = sum s l' wsum
+// for the lane's quad head.
+template <int HH>
+struct CmAcc {
+  float ug[HH][4], ua[HH][4];
+  float t;
+  __device__ __forceinline__ void clear() {
+#pragma unroll
+    for (int h = 0; h < HH; ++h)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ug[h][q] = ua[h][q] = 0.0f;
+    t = 0.0f;
+  }
+};
+
+// One batch of U slots of a group: slot k's destination row index (and CSR
+// edge id, with dropout) is held by lane src0 + k; slots k >= cnt are unused
+// (their lanes hold index 0, a valid row and edge, read and ignored). c: the
+// lane's channel chunk; hl: its quad lane (the head whose weights it
+// computes); ac: attn_col of the column for head min(hl, HH - 1).
+#ifndef CIGN_FL_COLS_CM_SHARE
+#define CIGN_FL_COLS_CM_SHARE 1
+#endif
+// Whether only the first quad of a column loads the rows' records and
+// computes the weights, the other quads receiving them by DPP row shifts
+// (LC >= 8; otherwise every quad loads them): the repeated record loads were
+// a quarter of the gathered bytes (62.4M edges: columns kernel 2.198 ms
+// against 2.215 ms).
+template <int LC>
+constexpr bool cm_share() {
+  return LC >= 8 && CIGN_FL_COLS_CM_SHARE;
+}
+// v of the column's first quad in every quad of the column: row_shr by 4, 8,
+// 12 lanes into DPP banks 1, 2, 3 (a bank is a quad of a 16-lane row; an
+// 8-lane column is banks 0-1 or 2-3 of its row), the other banks keeping
+// their value.
+template <int LC>
+__device__ __forceinline__ float from_quad0(float v) {
+  int x = __float_as_int(v);
+  if constexpr (LC == 8) {
+    x = __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0xA, false);
+  } else if constexpr (LC == 16) {
+    x = __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0x2, false);
+    x = __builtin_amdgcn_update_dpp(x, x, 0x118, 0xF, 0x4, false);
+    x = __builtin_amdgcn_update_dpp(x, x, 0x11C, 0xF, 0x8, false);
+  }
+  return __int_as_float(x);
+}
+
+template <typename T, int LC, int HH, bool DROP, int U>
+__device__ __forceinline__ void cm_batch(const GatBwdArgs<T>& a, int c, int hl, int ii, int ee, int src0, int cnt,
+                                         float ac, CmAcc<HH>& st) {
+  constexpr bool kShare = cm_share<LC>();
+  const int hc = hl < HH ? hl : HH - 1;
+  const bool q0 = !kShare || c < 4;
+  float gk[U][4];
+  float4 rs[U];
+  int mk[DROP ? U : 1];
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const uint32_t i = shfl(ii, src0 + k);
+    load_f32<4>(a.grad_pre + rec_off(i, a.gp_stride) + 4 * c, gk[k]);
+    rs[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if constexpr (DROP) mk[k] = 0;
+    if (q0) {
+      rs[k] = a.rowstat[rec_off(i, a.rs_stride) + hc];
+      if constexpr (DROP) mk[k] = a.mask[static_cast<int64_t>(shfl(ee, src0 + k)) * HH + hc];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const float raw = rs[k].x + ac;
+    const float lp = raw < 0.0f ? a.slope : 1.0f;
+    const float sm = col_weight(rs[k], raw, a.slope, k < cnt && hl < HH && q0);
+    float w = sm;
+    if constexpr (DROP) w = mk[k] != 0 ? sm * (1.0f / (1.0f - a.p)) : 0.0f;
+    float wl = w * lp;
+    st.t = fmaf(sm * lp, rs[k].w, st.t);
+    if constexpr (kShare) {
+      w = from_quad0<LC>(w);
+      wl = from_quad0<LC>(wl);
+    }
+    static_for<HH>([&](auto HC) {
+      constexpr int h = decltype(HC)::value;
+      const float wh = quad_bcast<4, h>(w);
+      const float wlh = quad_bcast<4, h>(wl);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        st.ug[h][q] = fmaf(wh, gk[k][q], st.ug[h][q]);
+        st.ua[h][q] = fmaf(wlh, gk[k][q], st.ua[h][q]);
+      }
+    });
+  }
+}
+
+// d[h] = <ua[h], x[j, h] chunk c> summed over the LC lanes of the group.
+template <typename T, int LC, int HH>
+__device__ __forceinline__ void cm_dots(const CmAcc<HH>& st, const typename Four<T>::Raw (&xr)[HH], float (&d)[HH]) {
+#pragma unroll
+  for (int h = 0; h < HH; ++h) {
+    float xj[4];
+    Four<T>::unpack(xr[h], xj);
+    d[h] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) d[h] = fmaf(st.ua[h][q], xj[q], d[h]);
+  }
+#pragma unroll
+  for (int o = 1; o < LC; o <<= 1)
+#pragma unroll
+    for (int h = 0; h < HH; ++h) d[h] += shfl_xor(d[h], o);
+}
+
+template <typename T, int LC, int HH, bool DROP, int U>
+__global__ __launch_bounds__(kBlock) void gat_bwd_cols_cm_kernel(GatBwdArgs<T> a, Sched s, int light_blocks) {
+  static_assert(LC >= 4 && LC <= 16 && U <= LC && HH <= 4, "channel-major geometry");
+  constexpr int G = kWave / LC;
+  const int C = a.C;
+  const int F = HH * C;
+  const int wave = wave_id();
+  const int lane = lane_id();
+  const int g = lane / LC;
+  const int c = lane & (LC - 1);
+  const int hl = lane & 3;
+  const int hc = hl < HH ? hl : HH - 1;
+  __shared__ float red[kWavesPerBlock][LC][HH * 4];
+  __shared__ float gred[kWavesPerBlock][HH];
+  __shared__ int flag;
+  int b = blockIdx.x;
+  if (b >= s.n_seg + light_blocks) {
+    bias_from_grad_pre(a, b - s.n_seg - light_blocks, a.col_counters + s.n_hrow, &flag);
+    return;
+  }
+  CmAcc<HH> st;
+  st.clear();
+  typename Four<T>::Raw xr[HH];
+
+  if (b >= s.n_seg) {
+    // Light columns: group g of the wavefront owns light column li. Groups
+    // exchange nothing (every shuffle and DPP read below stays within a
+    // group), so each runs its own number of batches.
+    const int li = ((b - s.n_seg) * kWavesPerBlock + wave) * G + g;
+    if (li >= s.n_light) return;
+    const int4 r = s.light[li];
+    const int j = r.x;
+    const int deg = r.z - r.y;
+    const int nb = (deg + U - 1) / U;
+    const float ac = a.attn_col[static_cast<int64_t>(j) * HH + hc];
+    int ii = c < U && c < deg ? a.rowind[r.y + c] : 0;
+    int ee = DROP && c < U && c < deg ? a.perm[r.y + c] : 0;
+#pragma unroll
+    for (int h = 0; h < HH; ++h) xr[h] = Four<T>::load(a.x + static_cast<int64_t>(j) * F + h * C + 4 * c);
+    for (int bb = 0; bb < nb; ++bb) {
+      const int k0 = bb * U;
+      const int kn = k0 + U + c;
+      const int in = c < U && kn < deg ? a.rowind[r.y + kn] : 0;
+      const int en = DROP && c < U && kn < deg ? a.perm[r.y + kn] : 0;
+      cm_batch<T, LC, HH, DROP, U>(a, c, hl, ii, ee, g * LC, deg - k0, ac, st);
+      ii = in;
+      ee = en;
+    }
+    float d[HH];
+    cm_dots<T, LC, HH>(st, xr, d);
+    float gac = 0.0f;
+    static_for<HH>([&](auto HC) {
+      constexpr int h = decltype(HC)::value;
+      const float th = quad_bcast<4, h>(st.t);
+      if (c == h) gac = d[h] * a.inv_h - th;
+    });
+#pragma unroll
+    for (int h = 0; h < HH; ++h) {
+      float o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = st.ug[h][q] * a.inv_h;
+      store4<T>(a.grad_feat + static_cast<int64_t>(j) * F + h * C + 4 * c, o);
+    }
+    if (c < HH) a.grad_attn_col[static_cast<int64_t>(j) * HH + c] = gac;
+    return;
+  }
+
+  // Heavy column segment: group gid = wave * G + g takes slots [gid U, gid U
+  // + U) of every round of 4 G U entries; the groups' sums are added by
+  // butterflies within the wavefront, then wave by wave through LDS.
+  constexpr int E = kWavesPerBlock * G * U;
+  const int4 sg = s.seg[b];
+  const int j = sg.x;
+  const int2 hr = s.hrow[sg.w];
+  const int gid = wave * G + g;
+  const float ac = a.attn_col[static_cast<int64_t>(j) * HH + hc];
+#pragma unroll
+  for (int h = 0; h < HH; ++h) xr[h] = Four<T>::load(a.x + static_cast<int64_t>(j) * F + h * C + 4 * c);
+  int tb = sg.y;
+  int t0 = tb + gid * U + c;
+  int ii = c < U && t0 < sg.z ? a.rowind[t0] : 0;
+  int ee = DROP && c < U && t0 < sg.z ? a.perm[t0] : 0;
+  for (; tb < sg.z; tb += E) {
+    const int tn = tb + E + gid * U + c;
+    const int in = c < U && tn < sg.z ? a.rowind[tn] : 0;
+    const int en = DROP && c < U && tn < sg.z ? a.perm[tn] : 0;
+    cm_batch<T, LC, HH, DROP, U>(a, c, hl, ii, ee, g * LC, sg.z - (tb + gid * U), ac, st);
+    ii = in;
+    ee = en;
+  }
+  float d[HH];
+  cm_dots<T, LC, HH>(st, xr, d);
+#pragma unroll
+  for (int o = LC; o < kWave; o <<= 1) {
+#pragma unroll
+    for (int h = 0; h < HH; ++h) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) st.ug[h][q] += shfl_xor(st.ug[h][q], o);
+      d[h] += shfl_xor(d[h], o);
+    }
+    st.t += shfl_xor(st.t, o);
+  }
+  float gac = 0.0f;
+  static_for<HH>([&](auto HC) {
+    constexpr int h = decltype(HC)::value;
+    const float th = quad_bcast<4, h>(st.t);
+    if (c == h) gac = d[h] * a.inv_h - th;
+  });
+  if (g == 0) {
+#pragma unroll
+    for (int h = 0; h < HH; ++h)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) red[wave][c][h * 4 + q] = st.ug[h][q];
+    if (c < HH) gred[wave][c] = gac;
+  }
+  __syncthreads();
+  const bool single = hr.y == 1;
+  const int stride = F + HH;
+  float* mine = a.part_col + static_cast<int64_t>(b) * stride;
+  if (threadIdx.x < LC * HH * 4) {
+    const int cc = threadIdx.x / (HH * 4), h = (threadIdx.x / 4) % HH, q = threadIdx.x % 4;
+    const float v = red[0][cc][h * 4 + q] + red[1][cc][h * 4 + q] + red[2][cc][h * 4 + q] + red[3][cc][h * 4 + q];
+    const int k = h * C + 4 * cc + q;
+    if (single) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<T>(v * a.inv_h);
+    else mine[k] = v;
+  }
+  if (threadIdx.x < HH) {
+    const int h = threadIdx.x;
+    const float v = gred[0][h] + gred[1][h] + gred[2][h] + gred[3][h];
+    if (single) a.grad_attn_col[static_cast<int64_t>(j) * HH + h] = v;
+    else mine[F + h] = v;
+  }
+  if (single) return;
+  if (!arrive_last(a.col_counters + sg.w, hr.y, &flag)) return;
+  for (int k = threadIdx.x; k < stride; k += kBlock) {
+    float v = 0.0f;
+    for (int z = 0; z < hr.y; ++z) v += a.part_col[static_cast<int64_t>(hr.x + z) * stride + k];
+    if (k < F) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<T>(v * a.inv_h);
+    else a.grad_attn_col[static_cast<int64_t>(j) * HH + (k - F)] = v;
+  }
+}
+
+// Launches the channel-major columns kernel for LC = C / 4.
+template <typename T>
+int launch_cols_cm(hipStream_t st, const GatBwdArgs<T>& a, const Sched& cs) {
+  auto go = [&](auto LCC) {
+    constexpr int LC = decltype(LCC)::value;
+    constexpr int G = kWave / LC;
+    constexpr int U = LC < CIGN_FL_COLS_CM_U ? LC : CIGN_FL_COLS_CM_U;
+    const int light_blocks = (cs.n_light + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
+    const int cb = cs.n_seg + light_blocks + a.n_l2;
+    if (cb == 0) return static_cast<int>(kOk);
+    if (a.p > 0.0f)
+      hipLaunchKernelGGL((gat_bwd_cols_cm_kernel<T, LC, kColsCmHeads, true, U>), dim3(cb), dim3(kBlock), 0, st, a,
+                         cs, light_blocks);
+    else
+      hipLaunchKernelGGL((gat_bwd_cols_cm_kernel<T, LC, kColsCmHeads, false, U>), dim3(cb), dim3(kBlock), 0, st, a,
+                         cs, light_blocks);
+    return check_launch("cign_gat_bwd (cols, channel-major)");
+  };
+  if (a.C == 16) return go(std::integral_constant<int, 4>());
+  if (a.C == 32) return go(std::integral_constant<int, 8>());
+  return go(std::integral_constant<int, 16>());
+}
+
 template <typename T, int L, int V>
 struct BwdFlLauncher {
   static int row_blocks(const Sched& rs, const int32_t* rhdr);
@@ -1534,6 +1879,9 @@ int BwdFlLauncher<T, L, V>::run(hipStream_t st, const GatBwdArgs<T>& a, const Sc
                          r_mid_blocks, lgcq);
     const int rc = check_launch("cign_gat_bwd (rows, feature layout)");
     if (rc) return rc;
+  }
+  if constexpr (V == 1) {
+    if (cols_cm_ok(a.H, a.C) && a.graph_nnz >= big_graph_edges()) return launch_cols_cm<T>(st, a, cs);
   }
   const int c_mid = G > 1 ? sched_count_gt(chdr, L) : cs.n_light;
   const int c_mid_blocks = (c_mid + kWavesPerBlock - 1) / kWavesPerBlock;
