@@ -180,6 +180,8 @@ def summarize(prof_dir: str, name: str, command: str) -> None:
     (out / f"{name}_kernel_stats.txt").write_text("\n".join(lines) + "\n")
     if (prof / "mfma").exists():
         _summarize_mfma(prof, name, command, {_short(r["Name"]): float(r["AverageNs"]) for r in stats})
+    if (prof / "valu").exists():
+        _summarize_valu(prof, name, command, {_short(r["Name"]): float(r["AverageNs"]) for r in stats})
     if not (prof / "fetch").exists():
         print(f"wrote profiles/{name}_kernel_stats.txt (no traffic counter runs)")
         return
@@ -223,6 +225,35 @@ def summarize(prof_dir: str, name: str, command: str) -> None:
         lines.append(f"{k[:60]:60s} {v['fetch_kib']:10.0f} {v['write_kib']:10.0f} {v['bytes'] / 1e6:11.2f}")
     (out / f"{name}_traffic.txt").write_text("\n".join(lines) + "\n")
     print(f"wrote profiles/{name}_kernel_stats.txt, _traffic.txt, _traffic.json")
+
+
+def _summarize_valu(prof: Path, name: str, command: str, avg_ns: dict) -> None:
+    """profiles/<name>_valu.txt from <prof>/valu (rocprofv3 --pmc
+    SQ_INSTS_VALU SQ_INSTS_VMEM_RD VALUBusy): per kernel of this library the
+    wavefront VALU and vector-memory-read instructions one dispatch issues
+    (median over dispatches) and the VALU busy share (VALUBusy: percent of
+    SIMD cycles issuing VALU while the kernel ran)."""
+    import csv
+    import glob
+    import statistics
+
+    per = {}
+    f = glob.glob(str(prof / "valu" / "*_counter_collection.csv"))[0]
+    for r in csv.DictReader(open(f)):
+        if "cign" in r["Kernel_Name"]:
+            per.setdefault(_short(r["Kernel_Name"]), {}).setdefault(r["Counter_Name"], []).append(
+                float(r["Counter_Value"]))
+    lines = [f"# rocprofv3 --pmc SQ_INSTS_VALU SQ_INSTS_VMEM_RD VALUBusy: {name}", "",
+             "Command (from the repository root, GPU box):", "", "    " + command.replace("\n", "\n    "), "",
+             "Per dispatch (median): wavefront instructions issued; VALUBusy = percent of SIMD cycles issuing VALU;",
+             "avg_us from the kernel trace.", "",
+             f"{'kernel':64s} {'VALU M':>9s} {'VMEM_RD M':>10s} {'VALUBusy%':>9s} {'avg_us':>9s}"]
+    for k, c in sorted(per.items()):
+        med = {n: statistics.median(v) for n, v in c.items()}
+        lines.append(f"{k[:64]:64s} {med.get('SQ_INSTS_VALU', 0) / 1e6:9.2f} {med.get('SQ_INSTS_VMEM_RD', 0) / 1e6:10.3f} "
+                     f"{med.get('VALUBusy', float('nan')):9.1f} {avg_ns.get(k, float('nan')) / 1e3:9.2f}")
+    (ROOT / "profiles" / f"{name}_valu.txt").write_text("\n".join(lines) + "\n")
+    print(f"wrote profiles/{name}_valu.txt")
 
 
 MFMA_PEAK = {"f32": 157.3, "bf16": 2500.0}  # MI355X dense matrix TFLOP/s
