@@ -1203,124 +1203,142 @@ struct PackBwdArgs {
 
 // A workgroup owns 64 rows (a wavefront 16) and one block cb of CBW channels:
 // grad_G for the 2K groups (hop kk, half) of those channels, 2K x CBW
-// columns, over the D-long reduction. The Wp^T rows of those columns sit in
-// LDS for the whole reduction and the wavefront's grad_g fragments in
-// registers, so the only global loads are issued up front, together with
-// the rows of H, C and the hops its epilogue needs. The epilogue is the
-// pack's backward: the lane holds, for its row, channels cb*CBW + 16 fh +
-// 4*(lane/16) + q of every group. CBW = 32 (bf16) writes whole 128-byte row
-// segments of every gradient; fp32 takes CBW = 16 (its Wp^T rows would not
-// fit LDS). Grid (ceil(M/64), D/CBW).
+// columns, over the D-long reduction, taken in phases of at most 128: each
+// phase stages the Wp^T rows of the block's columns for its K range in LDS
+// and loads the wavefront's grad_g fragments for it (about 52 KB of LDS at
+// D = 256 bf16, where the whole reduction's rows took 101 KB and left one
+// workgroup per CU). The last phase also issues the loads of the rows of H,
+// C and the hops the epilogue needs. The epilogue is the pack's backward:
+// the lane holds, for its row, channels cb*CBW + 16 fh + 4*(lane/16) + q of
+// every group. CBW = 32 (bf16) writes whole 128-byte row segments of every
+// gradient; fp32 takes CBW = 16. One-dimensional grid of 8 ceil(row_tiles /
+// 8) x D/CBW workgroups: workgroup ids go round-robin over the 8 XCDs, and
+// the mapping below gives the D/CBW channel blocks of a row tile to one XCD
+// one after another, so the tile's grad_g rows, read by each of them, come
+// from that XCD's L2 after the first.
 template <int MATH, int KC, int DD>
-__global__ __launch_bounds__(kThreads) void pack_proj_bwd_kernel(PackBwdArgs b) {
+__global__ __launch_bounds__(kThreads) void pack_proj_bwd_kernel(PackBwdArgs b, int row_tiles) {
   using T = typename Op<MATH>::T;
   constexpr int CBW = MATH == kMathBF16 ? 32 : 16;  // channels per block
+  constexpr int NCB = DD / CBW;                     // channel blocks
   constexpr int NFH = CBW / 16;                     // 16-column tiles per group
   constexpr int TF = 2 * KC * NFH;                  // tile f = group * NFH + fh
   constexpr int NCOL = TF * 16;
   constexpr int CE = 16 / sizeof(T);                // elements per 16-byte chunk
-  constexpr int SB = DD + CE;                       // LDS row stride, padded by 16 bytes
-  constexpr int NT = DD / kBK;
-  constexpr int CHUNKS = NCOL * DD / CE / kThreads;
+  constexpr int KP = DD < 128 ? DD : 128;           // K per phase
+  constexpr int PH = DD / KP;
+  constexpr int SB = KP + CE;                       // LDS row stride, padded by 16 bytes
+  constexpr int NTP = KP / kBK;                     // K steps per phase
+  constexpr int CHUNKS = NCOL * KP / CE / kThreads;
+  static_assert(NCOL * KP % (CE * kThreads) == 0, "whole staging rounds");
   // loads per round: the largest of 8, 6, 4, 3, 2, 1 dividing CHUNKS
   constexpr int ROUND = CHUNKS % 8 == 0 ? 8 : CHUNKS % 6 == 0 ? 6 : CHUNKS % 4 == 0 ? 4 : CHUNKS % 3 == 0 ? 3
                         : CHUNKS % 2 == 0 ? 2 : 1;
   __shared__ __align__(16) T Bs[NCOL * SB];
+  const int xcd = blockIdx.x % 8, jw = blockIdx.x / 8;
+  const int rt = (jw / NCB) * 8 + xcd;
+  const int cb = jw % NCB;
+  if (rt >= row_tiles) return;  // whole workgroup, before any barrier
   const PackArgs& a = b.a;
   const int lane = lane_id(), wave = wave_id();
   const int rl = lane & 15, ks = lane >> 4;
-  const int cb = blockIdx.y;
-  const int64_t mrow = static_cast<int64_t>(blockIdx.x) * kPpBM + 16 * wave + rl;
+  const int64_t mrow = static_cast<int64_t>(rt) * kPpBM + 16 * wave + rl;
   const bool valid = mrow < a.M;
   const int64_t mr = valid ? mrow : a.M - 1;
 
-  // the epilogue's rows, first in the queue
   float h[NFH][4], c[NFH][4], th[KC][NFH][4], tc[KC][NFH][4], al[KC];
-#pragma unroll
-  for (int fh = 0; fh < NFH; ++fh) {
-    const int j = cb * CBW + 16 * fh + 4 * ks;
-    gload_fast<float, 4>(a.H + mr * DD, j, h[fh]);
-    gload_fast<float, 4>(a.C + mr * DD, j, c[fh]);
-#pragma unroll
-    for (int k = 0; k < KC; ++k) {
-      const float* pk = a.P[k] + mr * a.p_stride;
-      gload_fast<float, 4>(pk, j, th[k][fh]);
-      gload_fast<float, 4>(pk, DD + j, tc[k][fh]);
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < KC; ++k) al[k] = a.alpha[mr * a.a_stride + k];
-  // grad_g fragments of the wavefront's 16 rows over all D (MFMA second
-  // operand), in the operand type: bf16 k = 32t + 8*(lane/16) .. +7; fp32
-  // k = 32t + 4*(lane/16) .. +3 and 32t + 16 + 4*(lane/16) .. +3.
-  using XF = std::conditional_t<MATH == kMathBF16, bf16x8, float[8]>;
-  XF xf[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    float lo[4], hi[4];
-    const int ka = MATH == kMathBF16 ? kBK * t + 8 * ks : kBK * t + 4 * ks;
-    const int kb = MATH == kMathBF16 ? ka + 4 : ka + 16;
-    gload_fast<float, 4>(b.gg + mr * DD, ka, lo);
-    gload_fast<float, 4>(b.gg + mr * DD, kb, hi);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if constexpr (MATH == kMathBF16) {
-        xf[t][q] = static_cast<__bf16>(lo[q]);
-        xf[t][4 + q] = static_cast<__bf16>(hi[q]);
-      } else {
-        xf[t][q] = lo[q];
-        xf[t][4 + q] = hi[q];
-      }
-    }
-  }
-  // Wp^T rows of the block's columns: tile column col = CBW gi + cc is group
-  // gi (hop gi/2, half gi%2), channel cb*CBW + cc.
-  {
-    const T* wt = static_cast<const T*>(b.wt);
-    constexpr int CPR = DD / CE;  // chunks per row
-#pragma unroll 1
-    for (int r0 = 0; r0 < CHUNKS; r0 += ROUND) {
-      uint4 v[ROUND];
-#pragma unroll
-      for (int i = 0; i < ROUND; ++i) {
-        const int id = threadIdx.x + (r0 + i) * kThreads;
-        const int col = id / CPR, k = (id % CPR) * CE;
-        const int gi = col / CBW;
-        const int64_t gcol = (gi >> 1) * 2 * DD + (gi & 1) * DD + cb * CBW + (col % CBW);
-        v[i] = *reinterpret_cast<const uint4*>(wt + gcol * DD + k);
-      }
-#pragma unroll
-      for (int i = 0; i < ROUND; ++i) {
-        const int id = threadIdx.x + (r0 + i) * kThreads;
-        *reinterpret_cast<uint4*>(Bs + (id / CPR) * SB + (id % CPR) * CE) = v[i];
-      }
-    }
-  }
-  __syncthreads();
-
   f32x4 acc[TF];
 #pragma unroll
   for (int f = 0; f < TF; ++f) acc[f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  using XF = std::conditional_t<MATH == kMathBF16, bf16x8, float[8]>;
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    if constexpr (MATH == kMathBF16) {
+  for (int ph = 0; ph < PH; ++ph) {
+    // grad_g fragments of the wavefront's 16 rows over the phase's K range
+    // (MFMA second operand), in the operand type: bf16 k = 32t + 8*(lane/16)
+    // .. +7; fp32 k = 32t + 4*(lane/16) .. +3 and 32t + 16 + 4*(lane/16) .. +3.
+    XF xf[NTP];
 #pragma unroll
-      for (int f = 0; f < TF; ++f) {
-        const bf16x8 wb = *reinterpret_cast<const bf16x8*>(Bs + (16 * f + rl) * SB + kBK * t + ks * 8);
-        acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb, xf[t], acc[f], 0, 0, 0);
+    for (int t = 0; t < NTP; ++t) {
+      float lo[4], hi[4];
+      const int k0 = ph * KP + kBK * t;
+      const int ka = MATH == kMathBF16 ? k0 + 8 * ks : k0 + 4 * ks;
+      const int kb = MATH == kMathBF16 ? ka + 4 : ka + 16;
+      gload_fast<float, 4>(b.gg + mr * DD, ka, lo);
+      gload_fast<float, 4>(b.gg + mr * DD, kb, hi);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if constexpr (MATH == kMathBF16) {
+          xf[t][q] = static_cast<__bf16>(lo[q]);
+          xf[t][4 + q] = static_cast<__bf16>(hi[q]);
+        } else {
+          xf[t][q] = lo[q];
+          xf[t][4 + q] = hi[q];
+        }
       }
-    } else {
+    }
+    if (ph == PH - 1) {
+      // the epilogue's rows, in flight during the last phase's products
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
+      for (int fh = 0; fh < NFH; ++fh) {
+        const int j = cb * CBW + 16 * fh + 4 * ks;
+        gload_fast<float, 4>(a.H + mr * DD, j, h[fh]);
+        gload_fast<float, 4>(a.C + mr * DD, j, c[fh]);
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+          const float* pk = a.P[k] + mr * a.p_stride;
+          gload_fast<float, 4>(pk, j, th[k][fh]);
+          gload_fast<float, 4>(pk, DD + j, tc[k][fh]);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < KC; ++k) al[k] = a.alpha[mr * a.a_stride + k];
+    }
+    if (ph > 0) __syncthreads();  // the previous phase's products have read Bs
+    // Wp^T rows of the block's columns over the phase's K range: tile column
+    // col = CBW gi + cc is group gi (hop gi/2, half gi%2), channel cb*CBW + cc.
+    {
+      const T* wt = static_cast<const T*>(b.wt);
+      constexpr int CPR = KP / CE;  // chunks per row
+#pragma unroll 1
+      for (int r0 = 0; r0 < CHUNKS; r0 += ROUND) {
+        uint4 v[ROUND];
+#pragma unroll
+        for (int i = 0; i < ROUND; ++i) {
+          const int id = threadIdx.x + (r0 + i) * kThreads;
+          const int col = id / CPR, k = ph * KP + (id % CPR) * CE;
+          const int gi = col / CBW;
+          const int64_t gcol = (gi >> 1) * 2 * DD + (gi & 1) * DD + cb * CBW + (col % CBW);
+          v[i] = *reinterpret_cast<const uint4*>(wt + gcol * DD + k);
+        }
+#pragma unroll
+        for (int i = 0; i < ROUND; ++i) {
+          const int id = threadIdx.x + (r0 + i) * kThreads;
+          *reinterpret_cast<uint4*>(Bs + (id / CPR) * SB + (id % CPR) * CE) = v[i];
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NTP; ++t) {
+      if constexpr (MATH == kMathBF16) {
 #pragma unroll
         for (int f = 0; f < TF; ++f) {
-          const float4 wb = *reinterpret_cast<const float4*>(Bs + (16 * f + rl) * SB + kBK * t + 16 * hh + ks * 4);
-          const float* xv = xf[t] + 4 * hh;
-          acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.x, xv[0], acc[f], 0, 0, 0);
-          acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.y, xv[1], acc[f], 0, 0, 0);
-          acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.z, xv[2], acc[f], 0, 0, 0);
-          acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.w, xv[3], acc[f], 0, 0, 0);
+          const bf16x8 wb = *reinterpret_cast<const bf16x8*>(Bs + (16 * f + rl) * SB + kBK * t + ks * 8);
+          acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb, xf[t], acc[f], 0, 0, 0);
         }
+      } else {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int f = 0; f < TF; ++f) {
+            const float4 wb = *reinterpret_cast<const float4*>(Bs + (16 * f + rl) * SB + kBK * t + 16 * hh + ks * 4);
+            const float* xv = xf[t] + 4 * hh;
+            acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.x, xv[0], acc[f], 0, 0, 0);
+            acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.y, xv[1], acc[f], 0, 0, 0);
+            acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.z, xv[2], acc[f], 0, 0, 0);
+            acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.w, xv[3], acc[f], 0, 0, 0);
+          }
+      }
     }
   }
 
@@ -1946,14 +1964,16 @@ int cign_pack_proj_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t in
   b.galpha_part = reinterpret_cast<float*>(ws + L.part_a);
   for (int k = 0; k < K; ++k) b.gP[k] = grad_props[k];
   const int cbw = math == kMathBF16 ? 32 : 16;  // channel block of pack_proj_bwd_kernel
-  const dim3 grid(static_cast<unsigned>((n + kPpBM - 1) / kPpBM), static_cast<unsigned>(D / cbw));
+  const int row_tiles = static_cast<int>((n + kPpBM - 1) / kPpBM);
+  const dim3 grid(static_cast<unsigned>((row_tiles + 7) / 8 * 8 * (D / cbw)));
   auto go = [&](auto MC) {
     constexpr int M_ = decltype(MC)::value;
     auto with_d = [&](auto KC) {
       constexpr int K_ = decltype(KC)::value;
-      if (D == 64) hipLaunchKernelGGL((pack_proj_bwd_kernel<M_, K_, 64>), grid, dim3(kThreads), 0, st, b);
-      else if (D == 128) hipLaunchKernelGGL((pack_proj_bwd_kernel<M_, K_, 128>), grid, dim3(kThreads), 0, st, b);
-      else hipLaunchKernelGGL((pack_proj_bwd_kernel<M_, K_, 256>), grid, dim3(kThreads), 0, st, b);
+      if (D == 64) hipLaunchKernelGGL((pack_proj_bwd_kernel<M_, K_, 64>), grid, dim3(kThreads), 0, st, b, row_tiles);
+      else if (D == 128)
+        hipLaunchKernelGGL((pack_proj_bwd_kernel<M_, K_, 128>), grid, dim3(kThreads), 0, st, b, row_tiles);
+      else hipLaunchKernelGGL((pack_proj_bwd_kernel<M_, K_, 256>), grid, dim3(kThreads), 0, st, b, row_tiles);
     };
     switch (K) {
       case 1: with_d(std::integral_constant<int, 1>()); break;
