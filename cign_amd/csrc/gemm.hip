@@ -796,17 +796,51 @@ struct WgStage {
   }
 };
 
+// Workgroup -> (tile, row chunk) of the split-M weight-gradient kernels.
+// Workgroup ids go round-robin over the 8 XCDs. With `xcd` (bf16 operands),
+// a one-dimensional grid of `tiles` x (row chunks rounded up to 8) gives
+// every tile of a row chunk to one XCD, so the chunk's rows of both operands
+// reach that XCD's L2 once and its tiles share them: at the production block
+// (M = 24.5K, 24 tiles) grad_W of proj took 155 against 169 us, the pack
+// projection's backward 302 against 313 us. fp32 operands (twice the LDS,
+// two workgroups per CU) ran slower that way (446 against 391 us, and 16
+// chunks to avoid a second round still 433), so they keep chunk-major ids.
+// False for the padding workgroups.
+__device__ __forceinline__ bool wg_tile_chunk(int tiles, int chunks, bool xcd, int& tile, int& chunk) {
+  if (xcd) {
+    const int x = blockIdx.x % 8, j = blockIdx.x / 8;
+    chunk = (j / tiles) * 8 + x;
+    tile = j % tiles;
+  } else {
+    chunk = blockIdx.x / tiles;
+    tile = blockIdx.x % tiles;
+  }
+  return chunk < chunks;
+}
+inline unsigned wg_grid(int tiles, int chunks, bool xcd) {
+  return static_cast<unsigned>(tiles * (xcd ? (chunks + 7) / 8 * 8 : chunks));
+}
+// Row chunks of those kernels: about `target`; with `xcd` a multiple of 8
+// (one per XCD each round) once there are at least 8.
+inline int64_t wg_chunk_count(int64_t M, int64_t target, bool xcd) {
+  const int64_t c = std::max<int64_t>(1, std::min<int64_t>((M + 255) / 256, target));
+  return xcd && c >= 8 ? (c + 7) / 8 * 8 : c;
+}
+
 template <int MATH>
 __global__ __launch_bounds__(kThreads) void wgrad_kernel(const float* gy, const float* x, int64_t M, int N, int K,
-                                                         int64_t chunk, int ntk, bool vec, float* part) {
+                                                         int64_t chunk, int nchunks, int ntk, bool vec, float* part) {
+  constexpr bool kXcd = MATH == kMathBF16;
   using T = typename Op<MATH>::T;
   using Lay = WgLayout<MATH>;
   __shared__ __align__(16) T Gs[2][kWgT * kWgM];
   __shared__ __align__(16) T Xs[2][kWgT * kWgM];
   const int lane = lane_id();
   const int wave = wave_id();
-  const int n0 = (blockIdx.x / ntk) * kWgT, k0 = (blockIdx.x % ntk) * kWgT;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * chunk;
+  int tile, cy;
+  if (!wg_tile_chunk(((N + kWgT - 1) / kWgT) * ntk, nchunks, kXcd, tile, cy)) return;  // whole workgroup
+  const int n0 = (tile / ntk) * kWgT, k0 = (tile % ntk) * kWgT;
+  const int64_t m0 = static_cast<int64_t>(cy) * chunk;
   const int64_t m1 = m0 + chunk < M ? m0 + chunk : M;
   const int wn = (wave >> 1) * 64, wk = (wave & 1) * 64;  // the wave's 64 x 64 quadrant
   const int rl = lane & 15, ks = lane >> 4;
@@ -871,7 +905,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(const float* gy, const 
   }
   // lane holds grad_W rows n = n0 + wn + 16i + 4*(lane/16) + q of column
   // k = k0 + wk + 16j + lane%16
-  float* out = part + static_cast<int64_t>(blockIdx.y) * N * K;
+  float* out = part + static_cast<int64_t>(cy) * N * K;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1463,8 +1497,8 @@ struct PackWgStage : WgStage<MATH> {
 };
 
 template <int MATH>
-__global__ __launch_bounds__(kThreads) void pack_wgrad_kernel(const float* gy, PackArgs a, int64_t chunk, int ntk,
-                                                              float* part) {
+__global__ __launch_bounds__(kThreads) void pack_wgrad_kernel(const float* gy, PackArgs a, int64_t chunk, int nchunks,
+                                                              int ntk, float* part) {
   using T = typename Op<MATH>::T;
   using Lay = WgLayout<MATH>;
   __shared__ __align__(16) T Gs[2][kWgT * kWgM];
@@ -1472,10 +1506,12 @@ __global__ __launch_bounds__(kThreads) void pack_wgrad_kernel(const float* gy, P
   const int N = a.D, KW = 2 * a.K * a.D;
   const int lane = lane_id();
   const int wave = wave_id();
-  const int kt = blockIdx.x % ntk;
-  const int n0 = (blockIdx.x / ntk) * kWgT;
+  int tile, cy;
+  if (!wg_tile_chunk(((N + kWgT - 1) / kWgT) * ntk, nchunks, MATH == kMathBF16, tile, cy)) return;  // whole workgroup
+  const int kt = tile % ntk;
+  const int n0 = (tile / ntk) * kWgT;
   const int kk = kt / (a.D / 64), j0 = 64 * (kt % (a.D / 64));
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * chunk;
+  const int64_t m0 = static_cast<int64_t>(cy) * chunk;
   const int64_t m1 = m0 + chunk < a.M ? m0 + chunk : a.M;
   const int wn = (wave >> 1) * 64, wk = (wave & 1) * 64;
   const int rl = lane & 15, ks = lane >> 4;
@@ -1541,7 +1577,7 @@ __global__ __launch_bounds__(kThreads) void pack_wgrad_kernel(const float* gy, P
   }
   // lane holds grad_Wp rows n = n0 + wn + 16i + 4*(lane/16) + q of tile
   // column wk + 16j + lane%16: G column kk*2D + (wk/64)*D + j0 + 16j + lane%16
-  float* out = part + static_cast<int64_t>(blockIdx.y) * N * KW;
+  float* out = part + static_cast<int64_t>(cy) * N * KW;
   const int gbase = kk * 2 * a.D + (wk / 64) * a.D + j0;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -1631,7 +1667,9 @@ struct BwdWs {
   int64_t chunk, wg_chunk, part_b, part_w, wt, total;
 };
 
-inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias) {
+// xcd: the chunking of bf16 operands (wg_tile_chunk); the workspace size
+// query takes it (the larger layout) for either math.
+inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias, bool xcd = true) {
   BwdWs L;
   // row chunks of the bias (and, for few outputs, grad_W) partials: 64 rows,
   // or 16 for few outputs (more workgroups for the per-chunk VALU sums)
@@ -1648,7 +1686,7 @@ inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias) {
   // workgroups over its 128 x 128 tiles
   const bool small = N <= kSmallN;
   const int64_t tiles = static_cast<int64_t>((N + kWgT - 1) / kWgT) * ((K + kWgT - 1) / kWgT);
-  int64_t wgc = std::max<int64_t>(1, std::min<int64_t>((M + 255) / 256, 512 / tiles));
+  int64_t wgc = wg_chunk_count(M, std::max<int64_t>(1, 512 / tiles), xcd);
   L.wg_chunk = std::max<int64_t>(kWgM, ((M + wgc - 1) / wgc + kWgM - 1) / kWgM * kWgM);
   wgc = M > 0 ? (M + L.wg_chunk - 1) / L.wg_chunk : 1;
   L.wg_chunks = static_cast<int>(wgc);
@@ -1671,12 +1709,12 @@ struct PpWs {
 
 inline int pp_ntk(int D, int K) { return K * (D / 64); }
 
-inline PpWs pp_ws(int64_t M, int D, int K) {
+inline PpWs pp_ws(int64_t M, int D, int K, bool xcd = true) {
   PpWs L;
   auto al = [](int64_t v) { return (v + 255) & ~int64_t(255); };
   const int64_t kw = 2LL * K * D;
   const int64_t tiles = static_cast<int64_t>((D + kWgT - 1) / kWgT) * pp_ntk(D, K);
-  int64_t wgc = std::max<int64_t>(1, std::min<int64_t>((M + 255) / 256, std::max<int64_t>(1, 512 / tiles)));
+  int64_t wgc = wg_chunk_count(M, std::max<int64_t>(1, 512 / tiles), xcd);
   L.wg_chunk = std::max<int64_t>(kWgM, ((M + wgc - 1) / wgc + kWgM - 1) / kWgM * kWgM);
   L.wg_chunks = static_cast<int>(M > 0 ? (M + L.wg_chunk - 1) / L.wg_chunk : 1);
   int64_t bc = std::max<int64_t>(1, std::min<int64_t>(1024, (M + 63) / 64));
@@ -1795,7 +1833,7 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
   if (!w || !grad_w || (M > 0 && (!grad_y || !x))) return set_error(kInvalid, "cign_linear_bwd: null pointer");
   if (math != kMathF32 && math != kMathBF16) return set_error(kInvalid, "cign_linear_bwd: math must be 0 or 1");
   if (M > 0x7fffffff) return set_error(kInvalid, "cign_linear_bwd: M too large");
-  const BwdWs L = bwd_ws(M, N, K, grad_b != nullptr);
+  const BwdWs L = bwd_ws(M, N, K, grad_b != nullptr, math == kMathBF16);
   if (workspace_bytes < L.total || (L.total > 0 && !workspace))
     return set_error(kInvalid, "cign_linear_bwd: workspace too small (%lld < %lld)",
                      static_cast<long long>(workspace_bytes), static_cast<long long>(L.total));
@@ -1836,15 +1874,15 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
   // grad_W [N,K] = grad_y^T x: split-M MFMA partials, then chunk sums.
   {
     const int ntk = (K + kWgT - 1) / kWgT;
-    const dim3 grid(static_cast<unsigned>(((N + kWgT - 1) / kWgT) * ntk), static_cast<unsigned>(L.wg_chunks));
+    const dim3 grid(wg_grid(((N + kWgT - 1) / kWgT) * ntk, L.wg_chunks, math == kMathBF16));
     const bool vec = N % 4 == 0 && K % 4 == 0 && aligned16(grad_y) && aligned16(x);
     float* part = reinterpret_cast<float*>(ws + L.part_w);
     if (math == kMathBF16)
-      hipLaunchKernelGGL(wgrad_kernel<kMathBF16>, grid, dim3(kThreads), 0, st, grad_y, x, M, N, K, L.wg_chunk, ntk,
-                         vec, part);
+      hipLaunchKernelGGL(wgrad_kernel<kMathBF16>, grid, dim3(kThreads), 0, st, grad_y, x, M, N, K, L.wg_chunk,
+                         L.wg_chunks, ntk, vec, part);
     else
-      hipLaunchKernelGGL(wgrad_kernel<kMathF32>, grid, dim3(kThreads), 0, st, grad_y, x, M, N, K, L.wg_chunk, ntk,
-                         vec, part);
+      hipLaunchKernelGGL(wgrad_kernel<kMathF32>, grid, dim3(kThreads), 0, st, grad_y, x, M, N, K, L.wg_chunk,
+                         L.wg_chunks, ntk, vec, part);
     if ((rc = check_launch("cign_linear_bwd (grad_W partials)"))) return rc;
     if ((rc = rowops::launch_colsum(st, part, L.wg_chunks, N * K, 1, grad_w, nullptr, "cign_linear_bwd (grad_W)")))
       return rc;
@@ -1940,7 +1978,7 @@ int cign_pack_proj_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t in
   bool ok = aligned16(grad_g) && aligned16(grad_H) && aligned16(grad_C);
   for (int k = 0; k < K; ++k) ok = ok && grad_props[k] && aligned16(grad_props[k]);
   if (!ok) return set_error(kInvalid, "%s: grad_g, grad_H, grad_C and every grad_prop must be 16-byte aligned", who);
-  const PpWs L = pp_ws(n, D, K);
+  const PpWs L = pp_ws(n, D, K, math == kMathBF16);
   if (workspace_bytes < L.total || !workspace)
     return set_error(kInvalid, "%s: workspace too small (%lld < %lld)", who, static_cast<long long>(workspace_bytes),
                      static_cast<long long>(L.total));
@@ -1985,8 +2023,8 @@ int cign_pack_proj_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t in
     hipLaunchKernelGGL(galpha_sum_kernel, dim3(static_cast<unsigned>((mk + 255) / 256)), dim3(256), 0, st,
                        b.galpha_part, mk, D / cbw, grad_alpha);
     const int ntk = pp_ntk(D, K);
-    const dim3 wgrid(static_cast<unsigned>(((D + kWgT - 1) / kWgT) * ntk), static_cast<unsigned>(L.wg_chunks));
-    hipLaunchKernelGGL((pack_wgrad_kernel<M_>), wgrid, dim3(kThreads), 0, st, grad_g, b.a, L.wg_chunk, ntk,
+    const dim3 wgrid(wg_grid(((D + kWgT - 1) / kWgT) * ntk, L.wg_chunks, math == kMathBF16));
+    hipLaunchKernelGGL((pack_wgrad_kernel<M_>), wgrid, dim3(kThreads), 0, st, grad_g, b.a, L.wg_chunk, L.wg_chunks, ntk,
                        reinterpret_cast<float*>(ws + L.part_w));
   };
   if (math == kMathBF16) go(std::integral_constant<int, kMathBF16>());
