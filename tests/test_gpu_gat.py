@@ -59,6 +59,11 @@ CASES = [
     (1, 4, 0.1, torch.float32, 300, {2: 400}),
     (4, 4, 0.0, torch.float32, 300, {1: 700}),
     (2, 8, 0.2, torch.bfloat16, 300, {1: 500}),
+    # four heads of 32 and 64 channels: the channel-major columns kernel with
+    # 8 and 16 lanes per column (large-graph kernels)
+    (4, 32, 0.0, torch.float32, 400, {2: 900}),
+    (4, 64, 0.1, torch.float32, 300, {1: 700}),
+    (4, 64, 0.0, torch.bfloat16, 300, {0: 600, 5: 70}),
     # wide rows (several chunks per lane): V = H*C/(W*64) = 4, 4, 8, 2, 2 and
     # a narrow bf16 row of 64 chunks
     (4, 256, 0.1, torch.float32, 300, {2: 700}),
