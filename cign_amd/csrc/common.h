@@ -54,6 +54,21 @@ __device__ __forceinline__ bf16 from_f32<bf16>(float f) {
   return r;
 }
 
+// bf16 storage that a kernel reads and writes four values (8 bytes) per lane
+// instead of eight: the feature-layout GAT kernels of small graphs take bf16
+// features this way, so a row spreads over as many lanes as an fp32 row and
+// each lane of a latency-bound launch has half the work.
+struct bf16h {
+  uint16_t bits;
+};
+__device__ __forceinline__ float to_f32(bf16h v) { return __uint_as_float(static_cast<uint32_t>(v.bits) << 16); }
+template <>
+__device__ __forceinline__ bf16h from_f32<bf16h>(float f) {
+  bf16h r;
+  r.bits = from_f32<bf16>(f).bits;
+  return r;
+}
+
 // A 16-byte (or 1-element) vector chunk of T, unpacked to fp32 registers.
 // W = elements per chunk: 4 (fp32 x4), 8 (bf16 x8) or 1 (scalar fallback).
 template <typename T, int W>
@@ -108,6 +123,25 @@ struct Chunk<bf16, 8> {
       w[i] = lo | (hi << 16);
     }
     *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+
+template <>
+struct Chunk<bf16h, 4> {
+  using Raw = uint2;
+  static __device__ __forceinline__ Raw load_raw(const bf16h* p) { return *reinterpret_cast<const uint2*>(p); }
+  static __device__ __forceinline__ Raw zero_raw() { return make_uint2(0u, 0u); }
+  static __device__ __forceinline__ void unpack(const Raw& q, float (&v)[4]) {
+    v[0] = __uint_as_float(q.x << 16);
+    v[1] = __uint_as_float(q.x & 0xffff0000u);
+    v[2] = __uint_as_float(q.y << 16);
+    v[3] = __uint_as_float(q.y & 0xffff0000u);
+  }
+  static __device__ __forceinline__ void load(const bf16h* p, float (&v)[4]) { unpack(load_raw(p), v); }
+  static __device__ __forceinline__ void store(bf16h* p, const float (&v)[4]) {
+    const uint32_t w0 = from_f32<bf16>(v[0]).bits | (static_cast<uint32_t>(from_f32<bf16>(v[1]).bits) << 16);
+    const uint32_t w1 = from_f32<bf16>(v[2]).bits | (static_cast<uint32_t>(from_f32<bf16>(v[3]).bits) << 16);
+    *reinterpret_cast<uint2*>(p) = make_uint2(w0, w1);
   }
 };
 

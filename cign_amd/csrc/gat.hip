@@ -12,6 +12,7 @@ CIGN_GAT_DECLARE(bf16, 8)
 CIGN_GAT_DECLARE(bf16, 32)
 CIGN_GAT_FL_DECLARE(float)
 CIGN_GAT_FL_DECLARE(bf16)
+CIGN_GAT_FL_DECLARE_NARROW(bf16h)
 }  // namespace gatk
 }  // namespace cign
 
@@ -92,8 +93,7 @@ __global__ void zero_floats(float* p, int n) {
 // over lane bits); narrow rows (H*cq <= 64 chunks) take L = pow2ceil(H*cq),
 // V = 1; wide rows take L = 64 and V = H*cq/64 in {2, 3, 4, 6, 8} (cq <= 64
 // divides 64, so a lane's chunks share one channel chunk).
-inline bool fl_geom(int dtype, int H, int C, int& L, int& V) {
-  const int W = dtype == kBF16 ? 8 : 4;
+inline bool fl_geom_w(int W, int H, int C, int& L, int& V) {
   const int cq = C / W;
   if (H < 1 || H > kFlHeads || C % W != 0 || cq < 1 || (cq & (cq - 1)) != 0) return false;
   const int nq = H * cq;
@@ -109,9 +109,22 @@ inline bool fl_geom(int dtype, int H, int C, int& L, int& V) {
   return V == 2 || V == 3 || V == 4 || V == 6 || V == 8;
 }
 
+inline bool fl_geom(int dtype, int H, int C, int& L, int& V) { return fl_geom_w(dtype == kBF16 ? 8 : 4, H, C, L, V); }
+
 inline bool fl_ok(int dtype, int H, int C) {
   int L, V;
   return fl_geom(dtype, H, C, L, V);
+}
+
+// Whether bf16 features run the feature-layout kernels four values per lane
+// (bf16h): graphs below the large-graph threshold, shapes whose rows stay
+// narrow that way. At 211K edges (4 x 16 channels) a row then takes 16 lanes
+// like fp32 instead of 8, each with half the work, which a launch of a few
+// dependent memory rounds is bound by.
+inline bool fl_half(int dtype, int H, int C, int64_t graph_nnz) {
+  int L, V;
+  return dtype == kBF16 && graph_nnz < big_graph_edges() && fl_ok(dtype, H, C) && fl_geom_w(4, H, C, L, V) &&
+         V == 1;
 }
 
 // Calls go(integral_constant<L>, integral_constant<V>) for an instantiated
@@ -139,8 +152,22 @@ int fl_dispatch(int L, int V, Go&& go) {
   }
 }
 
-inline int fl_lgcq(int dtype, int C) {
-  const int W = dtype == kBF16 ? 8 : 4;
+// fl_dispatch for the narrow rows (V = 1) only.
+template <typename Go>
+int fl_dispatch_narrow(int L, Go&& go) {
+  using std::integral_constant;
+  switch (L) {
+    case 1: return go(integral_constant<int, 1>(), integral_constant<int, 1>());
+    case 2: return go(integral_constant<int, 2>(), integral_constant<int, 1>());
+    case 4: return go(integral_constant<int, 4>(), integral_constant<int, 1>());
+    case 8: return go(integral_constant<int, 8>(), integral_constant<int, 1>());
+    case 16: return go(integral_constant<int, 16>(), integral_constant<int, 1>());
+    case 32: return go(integral_constant<int, 32>(), integral_constant<int, 1>());
+    default: return go(integral_constant<int, 64>(), integral_constant<int, 1>());
+  }
+}
+
+inline int fl_lgcq_w(int W, int C) {
   int lg = 0;
   while ((1 << lg) < C / W) ++lg;
   return lg;
@@ -251,20 +278,23 @@ int gat_fwd_impl(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
     a.x = xt; a.bias = bias; a.out = ot; a.pre = pre; a.emax = edge_max; a.esum = edge_sum;
     a.mask = edge_mask; a.partial = static_cast<float*>(workspace); a.counters = row_counters;
     a.agg = row_agg;
-    if (fl_ok(dtype, heads, channels)) {
+    int L, V;
+    if (fl_geom_w(FlGeom<T>::W, heads, channels, L, V)) {
       if (!aligned16(xt) || !aligned16(ot) || !aligned16(pre))
         return set_error(kInvalid, "cign_gat_fwd: in_feat, out and pre must be 16-byte aligned");
-      const int lgcq = fl_lgcq(dtype, channels);
-      int L, V;
-      fl_geom(dtype, heads, channels, L, V);
+      const int lgcq = fl_lgcq_w(FlGeom<T>::W, channels);
       auto go = [&](auto LC, auto VC) {
         return FwdFlLauncher<T, decltype(LC)::value, decltype(VC)::value>::run(st, a, s, row_sched_info, lgcq);
       };
-      return fl_dispatch(L, V, go);
+      if constexpr (std::is_same_v<T, bf16h>) return fl_dispatch_narrow(L, go);  // fl_half: V = 1
+      else return fl_dispatch(L, V, go);
     }
-    return dispatch_hc<FwdLauncher, T>(heads, channels, st, a, s);
+    if constexpr (std::is_same_v<T, bf16h>) return set_error(kInvalid, "cign_gat_fwd: bf16h needs a narrow shape");
+    else return dispatch_hc<FwdLauncher, T>(heads, channels, st, a, s);
   };
   if (dtype == kF32) return fill(static_cast<const float*>(in_feat), static_cast<float*>(out));
+  if (dtype == kBF16 && fl_half(dtype, heads, channels, graph_nnz))
+    return fill(static_cast<const bf16h*>(in_feat), static_cast<bf16h*>(out));
   if (dtype == kBF16) return fill(static_cast<const bf16*>(in_feat), static_cast<bf16*>(out));
   return set_error(kInvalid, "cign_gat_fwd: unsupported dtype %d", dtype);
 }
@@ -364,7 +394,8 @@ int gat_bwd_impl(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
     a.part_col = reinterpret_cast<float*>(ws + L.part_col);
     a.row_counters = row_counters; a.col_counters = col_counters;
     a.grad_feat = gxt; a.grad_attn_row = grad_attn_row; a.grad_attn_col = grad_attn_col; a.grad_bias = grad_bias;
-    if (fl_ok(dtype, heads, channels)) {
+    int FL, FV;
+    if (fl_geom_w(FlGeom<T>::W, heads, channels, FL, FV)) {
       if (!aligned16(xt) || !aligned16(gyt) || !aligned16(gxt) || !aligned16(pre) || !aligned16(grad_bias))
         return set_error(kInvalid, "cign_gat_bwd: in_feat, pre, grad_y, grad_feat and grad_bias must be 16-byte "
                                    "aligned");
@@ -372,23 +403,25 @@ int gat_bwd_impl(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
       a.gp_stride = channels + 4 * heads;
       a.rowstat = reinterpret_cast<float4*>(a.grad_pre + channels);
       a.rs_stride = a.gp_stride / 4;
-      const int lgcq = fl_lgcq(dtype, channels);
-      int L, V;
-      fl_geom(dtype, heads, channels, L, V);
+      const int lgcq = fl_lgcq_w(FlGeom<T>::W, channels);
       auto go = [&](auto LC, auto VC) {
         constexpr int LL = decltype(LC)::value, VV = decltype(VC)::value;
         a.rows_blocks = BwdFlLauncher<T, LL, VV>::row_blocks(rs, row_sched_info);
         a.n_l2 = fl_bias_blocks(bias_n);
         return BwdFlLauncher<T, LL, VV>::run(st, a, rs, row_sched_info, cs, col_sched_info, lgcq);
       };
-      return fl_dispatch(L, V, go);
+      if constexpr (std::is_same_v<T, bf16h>) return fl_dispatch_narrow(FL, go);  // fl_half: V = 1
+      else return fl_dispatch(FL, FV, go);
     }
     a.rows_blocks = row_blocks;
     a.n_l2 = (row_blocks + 63) / 64;
-    return dispatch_hc<BwdLauncher, T>(heads, channels, st, a, rs, cs);
+    if constexpr (std::is_same_v<T, bf16h>) return set_error(kInvalid, "cign_gat_bwd: bf16h needs a narrow shape");
+    else return dispatch_hc<BwdLauncher, T>(heads, channels, st, a, rs, cs);
   };
   if (dtype == kF32)
     return fill(static_cast<const float*>(in_feat), static_cast<const float*>(grad_y), static_cast<float*>(grad_feat));
+  if (dtype == kBF16 && fl_half(dtype, heads, channels, graph_nnz))
+    return fill(static_cast<const bf16h*>(in_feat), static_cast<const bf16h*>(grad_y), static_cast<bf16h*>(grad_feat));
   if (dtype == kBF16)
     return fill(static_cast<const bf16*>(in_feat), static_cast<const bf16*>(grad_y), static_cast<bf16*>(grad_feat));
   return set_error(kInvalid, "cign_gat_bwd: unsupported dtype %d", dtype);

@@ -124,6 +124,10 @@ template <typename T>
 struct FlGeom {
   static constexpr int W = 16 / sizeof(T);
 };
+template <>
+struct FlGeom<bf16h> {
+  static constexpr int W = 4;
+};
 
 // Lane geometry of a group of L lanes (one row) owning V chunks per lane.
 template <int L, int V>
@@ -1880,7 +1884,7 @@ int BwdFlLauncher<T, L, V>::run(hipStream_t st, const GatBwdArgs<T>& a, const Sc
     const int rc = check_launch("cign_gat_bwd (rows, feature layout)");
     if (rc) return rc;
   }
-  if constexpr (V == 1) {
+  if constexpr (V == 1 && !std::is_same_v<T, bf16h>) {  // (bf16h runs on small graphs only)
     if (cols_cm_ok(a.H, a.C) && a.graph_nnz >= big_graph_edges()) return launch_cols_cm<T>(st, a, cs);
   }
   const int c_mid = G > 1 ? sched_count_gt(chdr, L) : cs.n_light;
@@ -1935,6 +1939,7 @@ int BwdFlLauncher<T, L, V>::run(hipStream_t st, const GatBwdArgs<T>& a, const Sc
 #define CIGN_GAT_FLW_INSTANTIATE(T) CIGN_GAT_FL_LIST_WIDE(CIGN_GAT_FL_INST_ONE, T)
 #define CIGN_GAT_FL_DECLARE(T) \
   CIGN_GAT_FL_LIST_NARROW(CIGN_GAT_FL_DECL_ONE, T) CIGN_GAT_FL_LIST_WIDE(CIGN_GAT_FL_DECL_ONE, T)
+#define CIGN_GAT_FL_DECLARE_NARROW(T) CIGN_GAT_FL_LIST_NARROW(CIGN_GAT_FL_DECL_ONE, T)
 
 }  // namespace gatk
 }  // namespace cign
