@@ -343,10 +343,13 @@ struct FwdBatches {
     constexpr int NT = (U + R - 1) / R;  // slots whose weights this lane computes
     const uint32_t rowB = static_cast<uint32_t>(a.H * a.C) * sizeof(T);
     typename Chunk<T, W>::Raw xb[U][V];
+    // Slot u's index is held by lane (base + u) mod 64. Every lane holds a
+    // valid column index (0 where it has no edge), so a slot past cnt reads
+    // some valid row, weighted 0, and needs no clamp.
+    const int ub = base + first + k0 * step;
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-      const int u = first + (k0 + k) * step;
-      const uint64_t j = static_cast<uint32_t>(shfl(jj, (base + (u < cnt ? u : 0)) & (kWave - 1)));
+      const uint64_t j = static_cast<uint32_t>(shfl(jj, (ub + k * step) & (kWave - 1)));
 #pragma unroll
       for (int v = 0; v < V; ++v)
         xb[k][v] = *reinterpret_cast<const typename Chunk<T, W>::Raw*>(
@@ -361,7 +364,7 @@ struct FwdBatches {
       const int kk = R * t + r;
       uo[t] = first + (k0 + kk) * step;
       own[t] = kk < U && uo[t] < cnt;
-      const uint64_t j = static_cast<uint32_t>(shfl(jj, (base + (own[t] ? uo[t] : 0)) & (kWave - 1)));
+      const uint64_t j = static_cast<uint32_t>(shfl(jj, (base + uo[t]) & (kWave - 1)));
 #pragma unroll
       for (int v = 0; v < V; ++v) sc[t][v] = a.attn_col[j * a.H + ln.hq[v]] + ar[v];  // raw score
     }
@@ -759,7 +762,7 @@ struct RowBatches {
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
-      const int j = shfl(jj, (base + (u < cnt ? u : 0)) & (kWave - 1));
+      const int j = shfl(jj, (base + u) & (kWave - 1));
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         ab[k][v] = a.attn_col[static_cast<int64_t>(j) * a.H + ln.hq[v]];
@@ -1062,7 +1065,9 @@ __device__ __forceinline__ uint64_t rec_off(uint32_t i, int stride) {
 }
 
 // Batches of CSC entries of column j: slot u's destination row is held by
-// lane (base + u) in ii, its CSR edge id (used only with dropout) in ee. The
+// lane (base + u) mod 64 in ii, its CSR edge id (used only with dropout) in
+// ee. Every lane holds a valid row and edge id (0 where it has no entry), so
+// a slot past cnt reads some valid record, weighted 0, without a clamp. The
 // g_pre chunk of a destination row is shared by the lane's V heads.
 template <typename T, int L, int V, bool DROP>
 struct ColBatches {
@@ -1080,7 +1085,7 @@ struct ColBatches {
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
-      const int src = (base + (u < cnt ? u : 0)) & (kWave - 1);
+      const int src = (base + u) & (kWave - 1);
       const uint32_t i = shfl(ii, src);
       load_f32<W>(a.grad_pre + rec_off(i, a.gp_stride) + ln.cw * W, gb[k]);
 #pragma unroll
@@ -1092,7 +1097,7 @@ struct ColBatches {
     if constexpr (DROP)
       kb.compute(a.H, ln.gl, [&](int k, int h, bool own) {
         const int u = first + (k0 + k) * step;
-        const int e = shfl(ee, (base + (u < cnt ? u : 0)) & (kWave - 1));
+        const int e = shfl(ee, (base + u) & (kWave - 1));
         return own && u < cnt && a.mask[static_cast<int64_t>(e) * a.H + h] != 0;
       });
 #pragma unroll
@@ -1138,7 +1143,7 @@ struct ColSharedBatches {
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
-      const uint32_t i = shfl(ii, (base + (u < cnt ? u : 0)) & (kWave - 1));
+      const uint32_t i = shfl(ii, (base + u) & (kWave - 1));
       load_f32<W>(a.grad_pre + rec_off(i, a.gp_stride) + ln.cw * W, gb[k]);
     }
     const int r = ln.gl & (R - 1);
@@ -1148,7 +1153,7 @@ struct ColSharedBatches {
       const int kk = R * t + r;
       const int u = first + (k0 + kk) * step;
       const bool own = kk < U && u < cnt;
-      const int src = (base + (own ? u : 0)) & (kWave - 1);
+      const int src = (base + u) & (kWave - 1);
       const uint32_t i = shfl(ii, src);
       int e = 0;
       if constexpr (DROP) e = shfl(ee, src);
@@ -1217,7 +1222,7 @@ struct ColPairBatches {
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       const int u = first + (k0 + k) * step;
-      const uint32_t i = shfl(ii, (base + (u < cnt ? u : 0)) & (kWave - 1));
+      const uint32_t i = shfl(ii, (base + u) & (kWave - 1));
       load_f32<W>(a.grad_pre + rec_off(i, a.gp_stride) + ln.cw * W, gb[k]);
     }
     const int h = ln.gl % S;
@@ -1227,7 +1232,7 @@ struct ColPairBatches {
       const int k = r * SPR + ln.gl / S;
       const int u = first + (k0 + k) * step;
       const bool own = h < a.H && k < U && u < cnt;
-      const int src = (base + (own ? u : 0)) & (kWave - 1);
+      const int src = (base + u) & (kWave - 1);
       const uint32_t i = shfl(ii, src);
       const int hc = h < a.H ? h : a.H - 1;  // pair lanes past the heads read head H-1's record, unused
       const float4 rs = a.rowstat[rec_off(i, a.rs_stride) + hc];
