@@ -55,6 +55,10 @@ def parse():
                          "Clifford block forward+backward at the production shape (D=256, 6 GAT heads, hops 1-3) "
                          "with every component kernel timed against its own roofline (bf16 = selective AMP GEMMs)")
     ap.add_argument("--dtype", choices=["f32", "bf16"], default=None)
+    ap.add_argument("--layers", type=int, default=2,
+                    help="--workload train: GraphCliffordNet layers (2: BASELINE config c4; 4 with --in-dim 300: the "
+                         "Amazon-ratings production model of the reference's published step times)")
+    ap.add_argument("--in-dim", type=int, default=256, help="--workload train: input feature width")
     ap.add_argument("--no-scale", action="store_true",
                     help="default workload: skip the c5 measurement that follows the headline c2+c3 layer")
     ap.add_argument("--eager", action="store_true",
@@ -490,13 +494,14 @@ def run_train(args, torch):
     amp = args.dtype != "f32"
 
     w = workloads.build(workloads.C2, device=dev)
-    elapsed, gpu_ms = time_train(torch, make_train_step(torch, w, 256, 256, 6, 2, (1, 2, 3), amp, dev), args.steps,
+    L, ind = int(args.layers), int(args.in_dim)
+    elapsed, gpu_ms = time_train(torch, make_train_step(torch, w, ind, 256, 6, L, (1, 2, 3), amp, dev), args.steps,
                                  args.warmup)
     # The reference's CPU case on the GPU (c1: N=2000, 64-dim, 4 heads, hops 1-2).
     c1 = c1_gpu(torch, dev)
     cpu = cpu_train_baseline(args.cpu_seconds, torch) if args.cpu_seconds > 0 else None
     line = {
-        "metric": "CIGN 2-layer training step edges/sec (zero_grad, forward, cross-entropy, backward, Adam)",
+        "metric": f"CIGN {L}-layer training step edges/sec (zero_grad, forward, cross-entropy, backward, Adam)",
         "value": w.nnz_gat * args.steps / elapsed,
         "unit": "edges/s",
         "n_gpus": 1,
@@ -510,8 +515,9 @@ def run_train(args, torch):
         "dtype": "bf16-gemm" if amp else "f32",
         "data": "synthetic: seeded Chung-Lu power-law graph (gamma 2.5), N(0,1) features, uniform 5-class labels, "
                 "random-init model",
-        "config": {"workload": "c4 training step: GraphCliffordNet in 256, hidden 256, 2 layers, 6 GAT heads x 256, "
-                               "hops 1-3, dropout 0.28 / GAT 0.32, concat, Adam",
+        "config": {"workload": f"{'c4 ' if (L, ind) == (2, 256) else ''}training step: GraphCliffordNet in {ind}, "
+                               f"hidden 256, {L} layers, 6 GAT heads x 256, hops 1-3, dropout 0.28 / GAT 0.32, "
+                               "concat, Adam",
                    "nodes": w.n, "edges_nnz": w.nnz_gat},
         "c1_gpu": c1,
         "roofline": None,
