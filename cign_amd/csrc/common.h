@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace cign {
 
 constexpr int kWave = 64;
@@ -166,6 +168,42 @@ __device__ __forceinline__ float shfl(float v, int src) { return __shfl(v, src, 
 __device__ __forceinline__ int shfl(int v, int src) { return __shfl(v, src, kWave); }
 
 __device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, kWave); }
+
+// DPP move with control CTRL, all rows and banks. bound_ctrl: a lane reading a
+// disabled lane gets 0 (as from an old value of 0) and the destination needs
+// no initialisation.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// v of lane (lane ^ O), O a compile-time power of two below 64, the value
+// shfl_xor(v, O) returns: DPP inside a 16-lane row for O <= 8 (quad permutes
+// for 1 and 2; a row half-mirror then a quad reverse for 4, as 7 - (3 - i) =
+// i ^ 4 within 8 lanes; a row rotation by 8 for 8), a swizzle inside 32 lanes
+// for 16 and a backward permute for 32. Butterflies over low lane bits then
+// run on the VALU instead of waiting on LDS-pipe permutes. The partner lane
+// must be active.
+template <int O>
+__device__ __forceinline__ float xor_shfl(float v) {
+  static_assert(O > 0 && O < kWave && (O & (O - 1)) == 0, "lane offset");
+  if constexpr (O == 1) return dpp<0xB1>(v);               // quad_perm [1,0,3,2]
+  else if constexpr (O == 2) return dpp<0x4E>(v);          // quad_perm [2,3,0,1]
+  else if constexpr (O == 4) return dpp<0x1B>(dpp<0x141>(v));  // row_half_mirror, quad_perm [3,2,1,0]
+  else if constexpr (O == 8) return dpp<0x128>(v);         // row_ror:8
+  else if constexpr (O == 16) return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+  else return shfl_xor(v, O);
+}
+
+// f(integral_constant<int, O>) for O = 1, 2, 4, ..., 32 with FROM <= O < TO
+// (compile-time lane offsets of a butterfly).
+template <int FROM, int TO, typename F>
+__device__ __forceinline__ void for_offsets(F&& f) {
+  if constexpr (FROM < TO) {
+    f(std::integral_constant<int, FROM>{});
+    for_offsets<FROM * 2, TO>(f);
+  }
+}
 
 // Edge-batch driver of the gather kernels: runs fn.template run<U>(k0) for
 // k0 = 0, U, 2U, ... < need, with U the smallest power of two >= need, capped

@@ -180,16 +180,15 @@ __device__ __forceinline__ int wave_group_max(int v) {
 
 template <int L, int W>
 __device__ __forceinline__ void group_sum(float (&v)[W]) {
+  for_offsets<L, kWave>([&](auto OC) {
 #pragma unroll
-  for (int o = L; o < kWave; o <<= 1)
-#pragma unroll
-    for (int w = 0; w < W; ++w) v[w] += shfl_xor(v[w], o);
+    for (int w = 0; w < W; ++w) v[w] += xor_shfl<decltype(OC)::value>(v[w]);
+  });
 }
 
 template <int L>
 __device__ __forceinline__ float group_sum1(float v) {
-#pragma unroll
-  for (int o = L; o < kWave; o <<= 1) v += shfl_xor(v, o);
+  for_offsets<L, kWave>([&](auto OC) { v += xor_shfl<decltype(OC)::value>(v); });
   return v;
 }
 
@@ -200,9 +199,12 @@ __device__ __forceinline__ float group_sum1(float v) {
 // heads' two sums of a 6 x 256 row).
 template <int N>
 __device__ __forceinline__ void head_sum_n(float (&v)[N], int cq) {
-  for (int o = 1; o < cq; o <<= 1)
+  for_offsets<1, kWave>([&](auto OC) {
+    constexpr int o = decltype(OC)::value;
+    if (o < cq)
 #pragma unroll
-    for (int i = 0; i < N; ++i) v[i] += shfl_xor(v[i], o);
+      for (int i = 0; i < N; ++i) v[i] += xor_shfl<o>(v[i]);
+  });
 }
 
 // Dropout keep bits of a batch's U x H (edge slot k, head h) pairs, each
@@ -286,12 +288,6 @@ struct FwdState {
 // The R lanes of a quad (R = 4) or pair (R = 2) that hold chunks of one
 // head split the per-(edge, head) work of a batch and exchange its results
 // through DPP: broadcast of lane S, max and sum over the R lanes.
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  // bound_ctrl: a lane reading a disabled lane gets 0 (as from an old value
-  // of 0) and the destination needs no initialisation.
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
-}
 template <int R, int S>
 __device__ __forceinline__ float quad_bcast(float v) {
   if constexpr (R == 1) return v;
@@ -435,19 +431,20 @@ __device__ __forceinline__ void quad_reduce(FwdState<W, V>& st) {
 
 template <int L, int W, int V>
 __device__ __forceinline__ void fwd_merge_groups(FwdState<W, V>& st) {
-#pragma unroll
-  for (int o = L; o < kWave; o <<= 1)
+  for_offsets<L, kWave>([&](auto OC) {
+    constexpr int o = decltype(OC)::value;
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       float a2[W], l2[W];
 #pragma unroll
       for (int w = 0; w < W; ++w) {
-        a2[w] = shfl_xor(st.acc[v][w], o);
-        l2[w] = shfl_xor(st.accl[v][w], o);
+        a2[w] = xor_shfl<o>(st.acc[v][w]);
+        l2[w] = xor_shfl<o>(st.accl[v][w]);
       }
-      const float m2 = shfl_xor(st.m[v], o), s2 = shfl_xor(st.s[v], o), b2 = shfl_xor(st.bl[v], o);
+      const float m2 = xor_shfl<o>(st.m[v]), s2 = xor_shfl<o>(st.s[v]), b2 = xor_shfl<o>(st.bl[v]);
       st.merge(v, m2, s2, b2, a2, l2);
     }
+  });
 }
 
 template <typename T, int L, int V>
@@ -490,9 +487,12 @@ __device__ __forceinline__ void fwd_emit(const GatFwdArgs<T>& a, const FlLane<L,
       if (ln.cw == 0) a.agg[2 * nF + static_cast<int64_t>(row) * a.H + ln.hq[v]] = st.bl[v] * inv;
     }
   }
-  for (int o = cq; o < L; o <<= 1)
+  for_offsets<1, L>([&](auto OC) {
+    constexpr int o = decltype(OC)::value;
+    if (o >= cq)
 #pragma unroll
-    for (int w = 0; w < W; ++w) y[w] += shfl_xor(y[w], o);
+      for (int w = 0; w < W; ++w) y[w] += xor_shfl<o>(y[w]);
+  });
   if (!write) return;
   if (ln.qv[0] && ln.hq[0] == 0) {
     const int64_t base = static_cast<int64_t>(row) * a.C + ln.cw * W;
@@ -1676,10 +1676,10 @@ __device__ __forceinline__ void cm_dots(const CmAcc<HH>& st, const typename Four
 #pragma unroll
     for (int q = 0; q < 4; ++q) d[h] = fmaf(st.ua[h][q], xj[q], d[h]);
   }
+  for_offsets<1, LC>([&](auto OC) {
 #pragma unroll
-  for (int o = 1; o < LC; o <<= 1)
-#pragma unroll
-    for (int h = 0; h < HH; ++h) d[h] += shfl_xor(d[h], o);
+    for (int h = 0; h < HH; ++h) d[h] += xor_shfl<decltype(OC)::value>(d[h]);
+  });
 }
 
 template <typename T, int LC, int HH, bool DROP, int U>
@@ -1774,16 +1774,16 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_cm_kernel(GatBwdArgs<T> a
   }
   float d[HH];
   cm_dots<T, LC, HH>(st, xr, d);
-#pragma unroll
-  for (int o = LC; o < kWave; o <<= 1) {
+  for_offsets<LC, kWave>([&](auto OC) {
+    constexpr int o = decltype(OC)::value;
 #pragma unroll
     for (int h = 0; h < HH; ++h) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) st.ug[h][q] += shfl_xor(st.ug[h][q], o);
-      d[h] += shfl_xor(d[h], o);
+      for (int q = 0; q < 4; ++q) st.ug[h][q] += xor_shfl<o>(st.ug[h][q]);
+      d[h] += xor_shfl<o>(d[h]);
     }
-    st.t += shfl_xor(st.t, o);
-  }
+    st.t += xor_shfl<o>(st.t);
+  });
   float gac = 0.0f;
   static_for<HH>([&](auto HC) {
     constexpr int h = decltype(HC)::value;
