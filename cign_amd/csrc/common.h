@@ -229,7 +229,10 @@ __device__ __forceinline__ void for_batches(int need, Fn& fn) {
 // Sum over lanes whose ids differ only in bits >= `from` (all lanes sharing
 // lane % from); every such lane receives the total.
 __device__ __forceinline__ float sum_across(float v, int from) {
-  for (int o = from; o < kWave; o <<= 1) v += shfl_xor(v, o);
+  for_offsets<1, kWave>([&](auto OC) {
+    constexpr int o = decltype(OC)::value;
+    if (o >= from) v += xor_shfl<o>(v);
+  });
   return v;
 }
 
@@ -237,11 +240,14 @@ __device__ __forceinline__ float sum_across(float v, int from) {
 // so that their shuffles overlap instead of each waiting on the previous one.
 template <int N, int M>
 __device__ __forceinline__ void sum_across_n(float (&v)[N][M], int from) {
-  for (int o = from; o < kWave; o <<= 1)
+  for_offsets<1, kWave>([&](auto OC) {
+    constexpr int o = decltype(OC)::value;
+    if (o >= from)
 #pragma unroll
-    for (int i = 0; i < N; ++i)
+      for (int i = 0; i < N; ++i)
 #pragma unroll
-      for (int j = 0; j < M; ++j) v[i][j] += shfl_xor(v[i][j], o);
+        for (int j = 0; j < M; ++j) v[i][j] += xor_shfl<o>(v[i][j]);
+  });
 }
 
 // ---------------------------------------------------------------------------
