@@ -1084,13 +1084,13 @@ struct PackBStage {
   static constexpr int CHUNKS = BN * kBK / 4 / kThreads;
   float b[CHUNKS][4];
 
-  __device__ __forceinline__ void load(const GemmArgs& g, const PackArgs&, int kk, int j0, int D) {
+  __device__ __forceinline__ void load(const GemmArgs& g, const PackArgs&, int kk, int j0, int D, int n0) {
 #pragma unroll
     for (int i = 0; i < CHUNKS; ++i) {
       const int id = threadIdx.x + i * kThreads;
       const int r = id >> 3, c = id & 7;
       const int col = kk * 2 * D + (c < 4 ? j0 + 4 * c : D + j0 + 4 * (c - 4));
-      gload_fast<float, 4>(g.w + static_cast<int64_t>(r) * g.K, col, b[i]);
+      gload_fast<float, 4>(g.w + static_cast<int64_t>(n0 + r) * g.K, col, b[i]);
     }
   }
   template <typename T>
@@ -1108,13 +1108,13 @@ struct PackBStage<kMathBF16, BN> {
   static constexpr int CHUNKS = BN * kBK / 8 / kThreads;
   bf16x8 b[CHUNKS];
 
-  __device__ __forceinline__ void load(const GemmArgs& g, const PackArgs& a, int kk, int j0, int D) {
+  __device__ __forceinline__ void load(const GemmArgs& g, const PackArgs& a, int kk, int j0, int D, int n0) {
 #pragma unroll
     for (int i = 0; i < CHUNKS; ++i) {
       const int id = threadIdx.x + i * kThreads;
       const int r = id >> 2, c = id & 3;
       const int col = kk * 2 * D + (c < 2 ? j0 + 8 * c : D + j0 + 8 * (c - 2));
-      b[i] = *reinterpret_cast<const bf16x8*>(a.w16 + static_cast<int64_t>(r) * g.K + col);
+      b[i] = *reinterpret_cast<const bf16x8*>(a.w16 + static_cast<int64_t>(n0 + r) * g.K + col);
     }
   }
   __device__ __forceinline__ void store(__bf16* Bs, int S) const {
@@ -1165,22 +1165,32 @@ __device__ __forceinline__ void mma_step_pp(const typename Op<MATH>::T* As, cons
   }
 }
 
-// g = G Wp^T + bp and the gamma epilogue; a workgroup owns 64 rows and all
-// BN = D outputs (each wavefront BN/4 of them), so every G value is built
-// once; the next K step's rows and W tile load while the current one runs.
+// g = G Wp^T + bp and the gamma epilogue; a workgroup owns BM rows and BN of
+// the D outputs (each wavefront BN/4 of them); the next K step's rows and W
+// tile load while the current one runs. With BN < D the D/BN workgroups of a
+// row tile each build its G tiles: with one workgroup per 64 rows, c2's 383
+// workgroups left the GPU at 1.5 wavefronts per SIMD, too few to cover each
+// K step's load latency. One-dimensional grid of 8 ceil(row_tiles / 8) x
+// D/BN workgroups, the column blocks of a row tile on one XCD one after
+// another (ids go round-robin over the 8 XCDs), so they share its rows in L2.
 // The host checks D in {64, 128, 256}, K <= kPackMaxHops, 16-byte aligned
 // rows (H, C, hops, Wp, g_out, h, out).
 template <int MATH, int BN, int BM>
-__global__ __launch_bounds__(kThreads) void pack_proj_fwd_kernel(GemmArgs g, PackArgs a) {
+__global__ __launch_bounds__(kThreads) void pack_proj_fwd_kernel(GemmArgs g, PackArgs a, int row_tiles) {
   using T = typename Op<MATH>::T;
   constexpr int S = lds_stride<MATH>();
   constexpr int TNW = BN / 64;
   constexpr int RT = BM / 16;
   __shared__ __align__(16) T As[2][BM * S];
   __shared__ __align__(16) T Bs[2][BN * S];
+  const int ncb = a.D / BN;
+  const int xcd = blockIdx.x % 8, jw = blockIdx.x / 8;
+  const int rt = (jw / ncb) * 8 + xcd;
+  const int n0 = (jw % ncb) * BN;
+  if (rt >= row_tiles) return;  // whole workgroup, before any barrier
   const int lane = lane_id();
   const int wave = wave_id();
-  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * BM;
+  const int64_t m0 = static_cast<int64_t>(rt) * BM;
 
   f32x4 acc[RT][TNW];
 #pragma unroll
@@ -1193,7 +1203,7 @@ __global__ __launch_bounds__(kThreads) void pack_proj_fwd_kernel(GemmArgs g, Pac
   PackAStage<BM> pa;
   PackBStage<MATH, BN> pb;
   pa.load(a, m0, 0, 0);
-  pb.load(g, a, 0, 0, a.D);
+  pb.load(g, a, 0, 0, a.D, n0);
   pa.store(As[0], S, a.mode);
   pb.store(Bs[0], S);
   __syncthreads();
@@ -1203,7 +1213,7 @@ __global__ __launch_bounds__(kThreads) void pack_proj_fwd_kernel(GemmArgs g, Pac
     if (more) {
       const int kk = (s + 1) / jq, j0 = ((s + 1) % jq) * 16;
       pa.load(a, m0, kk, j0);
-      pb.load(g, a, kk, j0, a.D);
+      pb.load(g, a, kk, j0, a.D, n0);
     }
     mma_step_pp<MATH, TNW, RT>(As[buf], Bs[buf], wave, lane, acc);
     if (more) {
@@ -1213,7 +1223,7 @@ __global__ __launch_bounds__(kThreads) void pack_proj_fwd_kernel(GemmArgs g, Pac
     __syncthreads();
     buf ^= 1;
   }
-  epilogue_swapped<kEpiGamma, TNW, RT>(g, acc, m0, wave * TNW * 16, lane);
+  epilogue_swapped<kEpiGamma, TNW, RT>(g, acc, m0, n0 + wave * TNW * 16, lane);
 }
 
 // dst[i] = bf16(src[i]) (round to nearest even, as the MFMA operand stores)
@@ -1942,12 +1952,22 @@ int cign_pack_proj_fwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t in
   }
   // 64-row tiles: at the c2 block (24.5K rows, D = 256, bf16) 119 us against
   // 146 us with 32-row tiles (twice the workgroups, twice the W tile loads)
-  const dim3 grid(static_cast<unsigned>((n + kPpBM - 1) / kPpBM));
   auto go = [&](auto MC) {
     constexpr int M_ = decltype(MC)::value;
-    if (D == 64) hipLaunchKernelGGL((pack_proj_fwd_kernel<M_, 64, kPpBM>), grid, dim3(kThreads), 0, st, g, a);
-    else if (D == 128) hipLaunchKernelGGL((pack_proj_fwd_kernel<M_, 128, kPpBM>), grid, dim3(kThreads), 0, st, g, a);
-    else hipLaunchKernelGGL((pack_proj_fwd_kernel<M_, 256, kPpBM>), grid, dim3(kThreads), 0, st, g, a);
+    const int row_tiles = static_cast<int>((n + kPpBM - 1) / kPpBM);
+    auto launch = [&](auto BNC) {
+      constexpr int BN = decltype(BNC)::value;
+      const dim3 grid1(static_cast<unsigned>((row_tiles + 7) / 8 * 8 * (D / BN)));
+      hipLaunchKernelGGL((pack_proj_fwd_kernel<M_, BN, kPpBM>), grid1, dim3(kThreads), 0, st, g, a, row_tiles);
+    };
+    // Column block: all D outputs with bf16 math (at the production block
+    // 120 us against 122 us with 128 and 153 us with 64), 64 with fp32 math,
+    // whose double-buffered fp32 tiles of all 256 outputs took 92 KB of LDS
+    // and one workgroup per CU (229 us against 237 us with 128 and 317 us
+    // with 256).
+    if (D == 64 || M_ == kMathF32) launch(std::integral_constant<int, 64>());
+    else if (D == 128) launch(std::integral_constant<int, 128>());
+    else launch(std::integral_constant<int, 256>());
   };
   if (math == kMathBF16) go(std::integral_constant<int, kMathBF16>());
   else go(std::integral_constant<int, kMathF32>());
