@@ -655,30 +655,44 @@ def run_block(args, torch):
                                            galpha.data_ptr(), gWp.data_ptr(), gbp.data_ptr(), gwt.data_ptr(),
                                            gbt.data_ptr(), pp_ws.data_ptr(), pp_ws.numel()),
                           (20 + 16 * K) * NDb + 8 * n * K, 4 * n * 2 * K * D * D),
-        "gat_lin_fwd": (lambda: lib.call("cign_linear_fwd", st(), n, heads * D, D, 0, math, x.data_ptr(),
-                                         Wl.data_ptr(), None, xl.data_ptr()),
-                        4 * NDb + 4 * n * heads * D, 2 * n * D * heads * D),
     }
-    # The block's collapsed GAT (H=6 x C=256, fp32 projections) and one hop
-    # of its multihop SpMM (D = 2 x 256), as the block runs them.
+    # The GAT lin: under AMP its bf16 output is held in bf16 (amp_gat), as the
+    # block runs it; fp32 otherwise.
+    if amp:
+        xl16 = torch.empty(n, heads * D, dtype=torch.bfloat16, device=dev)
+        comps["gat_lin_fwd"] = (lambda: lib.call("cign_linear_fwd_bf16y", st(), n, heads * D, D, 0, x.data_ptr(),
+                                                 Wl.data_ptr(), None, xl16.data_ptr()),
+                                4 * NDb + 2 * n * heads * D, 2 * n * D * heads * D)
+    else:
+        comps["gat_lin_fwd"] = (lambda: lib.call("cign_linear_fwd", st(), n, heads * D, D, 0, math, x.data_ptr(),
+                                                 Wl.data_ptr(), None, xl.data_ptr()),
+                                4 * NDb + 4 * n * heads * D, 2 * n * D * heads * D)
+    # The block's collapsed GAT (H=6 x C=256; under AMP on the bf16-held
+    # projection output with fp32 outputs and gradients, as amp_gat runs it)
+    # and one hop of its multihop SpMM (D = 2 x 256), as the block runs them.
     from cign_amd.collapsed_gat import ensure_collapsed_gat_loaded
 
     ext = ensure_collapsed_gat_loaded()
     (rowptr, col), (row_, colptr), perm = w.gat_graph
     xg = rnd(n, heads, D)
+    if amp:
+        xg = xg.to(torch.bfloat16)
     ar_, ac_, bg_ = rnd(n, heads) * 0.1, rnd(n, heads) * 0.1, rnd(D)
     gyg = rnd(n, D)
     gat_state = {}
 
     def gat_fwd():
-        gat_state["f"] = ext.forward_agg(ar_, ac_, rowptr, col, 0.2, xg, bg_, 0.32, 5, True)
+        gat_state["f"] = ext.forward_agg(ar_, ac_, rowptr, col, 0.2, xg, bg_, 0.32, 5, True, f32_out=amp)
 
     def gat_bwd():
         (_, pre_, em_, es_, mk_), agg_ = gat_state["f"]
-        ext.backward(0.2, 0.32, rowptr, col, colptr, row_, perm, em_, es_, mk_, xg, ar_, ac_, pre_, gyg, agg_)
+        ext.backward(0.2, 0.32, rowptr, col, colptr, row_, perm, em_, es_, mk_, xg, ar_, ac_, pre_, gyg, agg_,
+                     f32_out=amp)
 
     gat_fwd()
-    Bg = workloads.algorithmic_bytes(n, E, heads, D, 2 * D, dropout=True)
+    Bg = workloads.algorithmic_bytes(n, E, heads, D, 2 * D, s_gat=2 if amp else 4, dropout=True)
+    if amp:
+        Bg["gat_bwd_agg"] += 2 * n * heads * D  # grad_feat is written as fp32
     Xs = rnd(n, 2 * D)
     comps["gat_fwd"] = (gat_fwd, Bg["gat_fwd_agg"], 0)
     comps["gat_bwd"] = (gat_bwd, Bg["gat_bwd_agg"], 0)

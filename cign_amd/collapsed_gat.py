@@ -42,6 +42,23 @@ _F32 = (torch.float32,)
 _FEAT = (torch.float32, torch.bfloat16)
 _I32 = (torch.int32,)
 
+# Library dtype of bf16 features with float32 outputs and gradients.
+GAT_BF16_F32 = 2
+
+
+def _gat_code(in_feat: torch.Tensor, f32_out: bool) -> int:
+    if not f32_out:
+        return _lib.dtype_code(in_feat)
+    _check(in_feat.dtype == torch.bfloat16, "f32_out takes bfloat16 in_feat")
+    return GAT_BF16_F32
+
+
+def bf16_f32_supported(heads: int, channels: int) -> bool:
+    """Whether the library runs bf16 features with float32 outputs for this
+    shape (its feature-layout kernels)."""
+    lib = _lib.load_library(require_gpu=False)
+    return int(lib.cign_gat_row_agg_floats(GAT_BF16_F32, 1, int(heads), int(channels))) > 0
+
 
 class _CollapsedGATExt:
     """Extension object with the reference binding's two entry points."""
@@ -53,10 +70,12 @@ class _CollapsedGATExt:
 
     @staticmethod
     def forward_agg(attn_row, attn_col, row_ptr, col_ind, negative_slope, in_feat, bias, attn_drop, seed,
-                    want_agg):
+                    want_agg, f32_out=False):
         """forward() plus, with ``want_agg`` on shapes that support it, the
         per-row aggregate buffer that lets backward() skip its second gather
-        of in_feat (None otherwise)."""
+        of in_feat (None otherwise). ``f32_out`` with bfloat16 in_feat: the
+        output is float32 (library dtype 2; feature-layout shapes only), the
+        results of float32 in_feat holding the same values."""
         for t, n in ((attn_row, "attn_row"), (attn_col, "attn_col"), (bias, "bias")):
             _check_dev(t, n, _F32)
         _check_dev(row_ptr, "row_ptr", _I32)
@@ -76,8 +95,9 @@ class _CollapsedGATExt:
         dev = in_feat.device
         if in_feat.data_ptr() % 16:
             in_feat = in_feat.clone()
-        sched = gat_schedule(row_ptr, 0, _lib.dtype_code(in_feat), H, C)
-        out = torch.empty((n, C), dtype=in_feat.dtype, device=dev)
+        code = _gat_code(in_feat, f32_out)
+        sched = gat_schedule(row_ptr, 0, code, H, C)
+        out = torch.empty((n, C), dtype=torch.float32 if code == 2 else in_feat.dtype, device=dev)
         pre = torch.empty((n, C), dtype=torch.float32, device=dev)
         edge_max = torch.empty((n, H), dtype=torch.float32, device=dev)
         edge_sum = torch.empty((n, H), dtype=torch.float32, device=dev)
@@ -86,10 +106,10 @@ class _CollapsedGATExt:
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         agg = None
         if want_agg:
-            agg_floats = int(lib.cign_gat_row_agg_floats(_lib.dtype_code(in_feat), n, H, C))
+            agg_floats = int(lib.cign_gat_row_agg_floats(code, n, H, C))
             if agg_floats > 0:
                 agg = torch.empty(agg_floats, dtype=torch.float32, device=dev)
-        lib.call("cign_gat_fwd", _lib.stream_ptr(dev), _lib.dtype_code(in_feat), n, nnz, H, C, attn_row.data_ptr(),
+        lib.call("cign_gat_fwd", _lib.stream_ptr(dev), code, n, nnz, H, C, attn_row.data_ptr(),
                  attn_col.data_ptr(), col_ind.data_ptr(), *sched.args(),
                  sched.counters.data_ptr(), float(negative_slope), in_feat.data_ptr(), bias.data_ptr(),
                  float(attn_drop), int(seed) & ((1 << 64) - 1), out.data_ptr(), pre.data_ptr(), edge_max.data_ptr(),
@@ -98,9 +118,10 @@ class _CollapsedGATExt:
 
     @staticmethod
     def backward(negative_slope, attn_drop, row_ptr, col_ind, col_ptr, row_ind, permute, edge_max, edge_sum,
-                 edge_mask, in_feat, attn_row, attn_col, pre, grad_y, row_agg=None):
+                 edge_mask, in_feat, attn_row, attn_col, pre, grad_y, row_agg=None, f32_out=False):
         """``row_agg``: the buffer forward_agg() returned for the same inputs,
-        or None (the rows pass then gathers in_feat per edge)."""
+        or None (the rows pass then gathers in_feat per edge). ``f32_out``
+        as in forward_agg: grad_y and grad_feat are float32."""
         for t, n in ((row_ptr, "row_ptr"), (col_ind, "col_ind"), (col_ptr, "col_ptr"), (row_ind, "row_ind"),
                      (permute, "permute")):
             _check_dev(t, n, _I32)
@@ -109,7 +130,8 @@ class _CollapsedGATExt:
             _check_dev(t, n, _F32)
         _check_dev(edge_mask, "edge_mask", (torch.uint8,))
         _check_dev(in_feat, "in_feat", _FEAT)
-        _check_dev(grad_y, "grad_y", (in_feat.dtype,))
+        code = _gat_code(in_feat, f32_out)
+        _check_dev(grad_y, "grad_y", (torch.float32,) if code == 2 else (in_feat.dtype,))
         _check(in_feat.dim() == 3 and 1 <= in_feat.size(1) <= 32 and 1 <= in_feat.size(2) <= 256,
                "collapsed GAT requires in_feat [N,H,C] with 1<=H<=32, 1<=C<=256")
         _check(pre.shape == grad_y.shape, "pre and grad_y must match")
@@ -117,17 +139,16 @@ class _CollapsedGATExt:
         n, H, C = (int(v) for v in in_feat.shape)
         nnz = int(col_ind.numel())
         dev = in_feat.device
-        code = _lib.dtype_code(in_feat)
         rs = gat_schedule(row_ptr, 1, code, H, C)
         cs = gat_schedule(col_ptr, 1, code, H, C)
         row_blocks = rs.n_seg + (rs.n_light + 3) // 4
         ws_bytes = int(lib.cign_gat_bwd_workspace_bytes(n, nnz, H, C, row_blocks, rs.n_seg, cs.n_seg))
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-        grad_feat = torch.empty_like(in_feat)
+        grad_feat = torch.empty_like(in_feat, dtype=torch.float32 if code == 2 else in_feat.dtype)
         grad_attn_row = torch.empty_like(attn_row)
         grad_attn_col = torch.empty_like(attn_col)
         grad_bias = torch.empty((C,), dtype=torch.float32, device=dev)
-        lib.call("cign_gat_bwd", _lib.stream_ptr(dev), _lib.dtype_code(in_feat), n, nnz, H, C, float(negative_slope),
+        lib.call("cign_gat_bwd", _lib.stream_ptr(dev), code, n, nnz, H, C, float(negative_slope),
                  float(attn_drop), col_ind.data_ptr(), row_ind.data_ptr(),
                  permute.data_ptr(), edge_max.data_ptr(), edge_sum.data_ptr(), edge_mask.data_ptr(),
                  in_feat.data_ptr(), attn_row.data_ptr(), attn_col.data_ptr(), pre.data_ptr(), grad_y.data_ptr(),

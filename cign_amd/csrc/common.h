@@ -17,8 +17,9 @@ constexpr int kWave = 64;
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
 
-// dtype codes used on the C-ABI.
-enum DType : int { kF32 = 0, kBF16 = 1 };
+// dtype codes used on the C-ABI. kBF16F32: bf16 features (values a bf16
+// projection produced, so exact in bf16) with fp32 outputs and gradients.
+enum DType : int { kF32 = 0, kBF16 = 1, kBF16F32 = 2 };
 
 // Return codes used on the C-ABI.
 enum Status : int { kOk = 0, kInvalid = 1, kHipError = 2 };
@@ -70,6 +71,27 @@ __device__ __forceinline__ bf16h from_f32<bf16h>(float f) {
   r.bits = from_f32<bf16>(f).bits;
   return r;
 }
+
+// Features stored as bf16 whose results and gradients are fp32 (the
+// collapsed GAT on a bf16 projection under selective AMP, whose fp32 input
+// holds bf16 values exactly): loads are those of bf16, every output type is
+// float (GatOut).
+struct bf16x {
+  uint16_t bits;
+};
+__device__ __forceinline__ float to_f32(bf16x v) { return __uint_as_float(static_cast<uint32_t>(v.bits) << 16); }
+
+// Type of the outputs and incoming gradients of kernels whose inputs are T.
+template <typename T>
+struct GatOutOf {
+  using type = T;
+};
+template <>
+struct GatOutOf<bf16x> {
+  using type = float;
+};
+template <typename T>
+using GatOut = typename GatOutOf<T>::type;
 
 // A 16-byte (or 1-element) vector chunk of T, unpacked to fp32 registers.
 // W = elements per chunk: 4 (fp32 x4), 8 (bf16 x8) or 1 (scalar fallback).
@@ -144,6 +166,37 @@ struct Chunk<bf16h, 4> {
     const uint32_t w0 = from_f32<bf16>(v[0]).bits | (static_cast<uint32_t>(from_f32<bf16>(v[1]).bits) << 16);
     const uint32_t w1 = from_f32<bf16>(v[2]).bits | (static_cast<uint32_t>(from_f32<bf16>(v[3]).bits) << 16);
     *reinterpret_cast<uint2*>(p) = make_uint2(w0, w1);
+  }
+};
+
+template <>
+struct Chunk<bf16x, 8> {
+  using Raw = uint4;
+  static __device__ __forceinline__ Raw load_raw(const bf16x* p) { return *reinterpret_cast<const uint4*>(p); }
+  static __device__ __forceinline__ Raw zero_raw() { return make_uint4(0u, 0u, 0u, 0u); }
+  static __device__ __forceinline__ void unpack(const Raw& q, float (&v)[8]) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  static __device__ __forceinline__ void load(const bf16x* p, float (&v)[8]) { unpack(load_raw(p), v); }
+};
+
+// Eight fp32 values (the outputs of a bf16x chunk): two 16-byte accesses.
+template <>
+struct Chunk<float, 8> {
+  static __device__ __forceinline__ void load(const float* p, float (&v)[8]) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&v)[8]) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
   }
 };
 

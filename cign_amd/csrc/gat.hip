@@ -13,6 +13,7 @@ CIGN_GAT_DECLARE(bf16, 32)
 CIGN_GAT_FL_DECLARE(float)
 CIGN_GAT_FL_DECLARE(bf16)
 CIGN_GAT_FL_DECLARE_NARROW(bf16h)
+CIGN_GAT_FL_DECLARE(bf16x)
 }  // namespace gatk
 }  // namespace cign
 
@@ -109,7 +110,9 @@ inline bool fl_geom_w(int W, int H, int C, int& L, int& V) {
   return V == 2 || V == 3 || V == 4 || V == 6 || V == 8;
 }
 
-inline bool fl_geom(int dtype, int H, int C, int& L, int& V) { return fl_geom_w(dtype == kBF16 ? 8 : 4, H, C, L, V); }
+inline bool fl_geom(int dtype, int H, int C, int& L, int& V) {
+  return fl_geom_w(dtype == kBF16 || dtype == kBF16F32 ? 8 : 4, H, C, L, V);
+}
 
 inline bool fl_ok(int dtype, int H, int C) {
   int L, V;
@@ -269,7 +272,7 @@ int gat_fwd_impl(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
   const Sched s = make_sched(row_sched, hd.n_light, hd.n_seg, hd.n_hrow);
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto fill = [&](auto* xt, auto* ot) {
-    using T = std::remove_cv_t<std::remove_pointer_t<decltype(ot)>>;
+    using T = std::remove_cv_t<std::remove_pointer_t<decltype(xt)>>;
     GatFwdArgs<T> a;
     a.n = n; a.H = heads; a.C = channels; a.graph_nnz = graph_nnz; a.mask_base = edge_base * heads;
     a.slope = negative_slope; a.p = attn_drop; a.seed = seed;
@@ -290,12 +293,16 @@ int gat_fwd_impl(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
       else return fl_dispatch(L, V, go);
     }
     if constexpr (std::is_same_v<T, bf16h>) return set_error(kInvalid, "cign_gat_fwd: bf16h needs a narrow shape");
+    else if constexpr (std::is_same_v<T, bf16x>)
+      return set_error(kInvalid, "cign_gat_fwd: dtype 2 (bf16 features, fp32 outputs) needs a feature-layout shape "
+                       "(cign_gat_row_agg_floats > 0)");
     else return dispatch_hc<FwdLauncher, T>(heads, channels, st, a, s);
   };
   if (dtype == kF32) return fill(static_cast<const float*>(in_feat), static_cast<float*>(out));
   if (dtype == kBF16 && fl_half(dtype, heads, channels, graph_nnz))
     return fill(static_cast<const bf16h*>(in_feat), static_cast<bf16h*>(out));
   if (dtype == kBF16) return fill(static_cast<const bf16*>(in_feat), static_cast<bf16*>(out));
+  if (dtype == kBF16F32) return fill(static_cast<const bf16x*>(in_feat), static_cast<float*>(out));
   return set_error(kInvalid, "cign_gat_fwd: unsupported dtype %d", dtype);
 }
 
@@ -372,7 +379,7 @@ int gat_bwd_impl(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
   }
   char* ws = static_cast<char*>(workspace);
   auto fill = [&](auto* xt, auto* gyt, auto* gxt) {
-    using T = std::remove_cv_t<std::remove_pointer_t<decltype(gxt)>>;
+    using T = std::remove_cv_t<std::remove_pointer_t<decltype(xt)>>;
     GatBwdArgs<T> a;
     a.n = n; a.nnz = nnz; a.H = heads; a.C = channels;
     a.graph_nnz = graph_nnz; a.bias_lo = bias_lo; a.bias_n = bias_n;
@@ -416,6 +423,9 @@ int gat_bwd_impl(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
     a.rows_blocks = row_blocks;
     a.n_l2 = (row_blocks + 63) / 64;
     if constexpr (std::is_same_v<T, bf16h>) return set_error(kInvalid, "cign_gat_bwd: bf16h needs a narrow shape");
+    else if constexpr (std::is_same_v<T, bf16x>)
+      return set_error(kInvalid, "cign_gat_bwd: dtype 2 (bf16 features, fp32 outputs) needs a feature-layout shape "
+                       "(cign_gat_row_agg_floats > 0)");
     else return dispatch_hc<BwdLauncher, T>(heads, channels, st, a, rs, cs);
   };
   if (dtype == kF32)
@@ -424,6 +434,8 @@ int gat_bwd_impl(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t he
     return fill(static_cast<const bf16h*>(in_feat), static_cast<const bf16h*>(grad_y), static_cast<bf16h*>(grad_feat));
   if (dtype == kBF16)
     return fill(static_cast<const bf16*>(in_feat), static_cast<const bf16*>(grad_y), static_cast<bf16*>(grad_feat));
+  if (dtype == kBF16F32)
+    return fill(static_cast<const bf16x*>(in_feat), static_cast<const float*>(grad_y), static_cast<float*>(grad_feat));
   return set_error(kInvalid, "cign_gat_bwd: unsupported dtype %d", dtype);
 }
 

@@ -504,7 +504,7 @@ __device__ __forceinline__ void fwd_emit(const GatFwdArgs<T>& a, const FlLane<L,
       o[w] = silu(pr[w]);
     }
     store_f32<W>(a.pre + base, pr);
-    Chunk<T, W>::store(a.out + base, o);
+    Chunk<GatOut<T>, W>::store(a.out + base, o);
   }
   if (ln.cw == 0)
 #pragma unroll
@@ -825,7 +825,7 @@ __device__ __forceinline__ void grad_pre_chunk(const GatBwdArgs<T>& a, int row, 
   constexpr int W = FlGeom<T>::W;
   const int64_t base = static_cast<int64_t>(row) * a.C + cw * W;
   float gy[W], pr[W];
-  Chunk<T, W>::load(a.grad_y + base, gy);
+  Chunk<GatOut<T>, W>::load(a.grad_y + base, gy);
   load_f32<W>(a.pre + base, pr);
 #pragma unroll
   for (int w = 0; w < W; ++w) gp[w] = gy[w] * silu_grad(pr[w]);
@@ -1432,7 +1432,7 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
       float o[W];
 #pragma unroll
       for (int w = 0; w < W; ++w) o[w] = st.ug[v][w] * a.inv_h;
-      Chunk<T, W>::store(a.grad_feat + static_cast<int64_t>(j) * F + ln.q[v] * W, o);
+      Chunk<GatOut<T>, W>::store(a.grad_feat + static_cast<int64_t>(j) * F + ln.q[v] * W, o);
       if (ln.cw == 0) a.grad_attn_col[static_cast<int64_t>(j) * a.H + ln.hq[v]] = gac[v];
     }
     return;
@@ -1485,7 +1485,7 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
   float* mine = a.part_col + static_cast<int64_t>(b) * stride;
   for (int k = threadIdx.x; k < F; k += kBlock) {
     const float v = red[k];
-    if (single) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<T>(v * a.inv_h);
+    if (single) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<GatOut<T>>(v * a.inv_h);
     else mine[k] = v;
   }
   if (threadIdx.x < a.H) {
@@ -1499,7 +1499,7 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
   for (int k = threadIdx.x; k < stride; k += kBlock) {
     float v = 0.0f;
     for (int z = 0; z < hr.y; ++z) v += a.part_col[static_cast<int64_t>(hr.x + z) * stride + k];
-    if (k < F) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<T>(v * a.inv_h);
+    if (k < F) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<GatOut<T>>(v * a.inv_h);
     else a.grad_attn_col[static_cast<int64_t>(j) * a.H + (k - F)] = v;
   }
 }
@@ -1555,6 +1555,12 @@ struct Four<bf16> {
     v[2] = __uint_as_float(q.y << 16);
     v[3] = __uint_as_float(q.y & 0xffff0000u);
   }
+};
+template <>
+struct Four<bf16x> {
+  using Raw = uint2;
+  static __device__ __forceinline__ Raw load(const bf16x* p) { return *reinterpret_cast<const uint2*>(p); }
+  static __device__ __forceinline__ void unpack(const Raw& q, float (&v)[4]) { Four<bf16>::unpack(q, v); }
 };
 template <typename T>
 __device__ __forceinline__ void store4(T* p, const float (&v)[4]);
@@ -1743,7 +1749,7 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_cm_kernel(GatBwdArgs<T> a
       float o[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) o[q] = st.ug[h][q] * a.inv_h;
-      store4<T>(a.grad_feat + static_cast<int64_t>(j) * F + h * C + 4 * c, o);
+      store4<GatOut<T>>(a.grad_feat + static_cast<int64_t>(j) * F + h * C + 4 * c, o);
     }
     if (c < HH) a.grad_attn_col[static_cast<int64_t>(j) * HH + c] = gac;
     return;
@@ -1805,7 +1811,7 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_cm_kernel(GatBwdArgs<T> a
     const int cc = threadIdx.x / (HH * 4), h = (threadIdx.x / 4) % HH, q = threadIdx.x % 4;
     const float v = red[0][cc][h * 4 + q] + red[1][cc][h * 4 + q] + red[2][cc][h * 4 + q] + red[3][cc][h * 4 + q];
     const int k = h * C + 4 * cc + q;
-    if (single) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<T>(v * a.inv_h);
+    if (single) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<GatOut<T>>(v * a.inv_h);
     else mine[k] = v;
   }
   if (threadIdx.x < HH) {
@@ -1819,7 +1825,7 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_cm_kernel(GatBwdArgs<T> a
   for (int k = threadIdx.x; k < stride; k += kBlock) {
     float v = 0.0f;
     for (int z = 0; z < hr.y; ++z) v += a.part_col[static_cast<int64_t>(hr.x + z) * stride + k];
-    if (k < F) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<T>(v * a.inv_h);
+    if (k < F) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<GatOut<T>>(v * a.inv_h);
     else a.grad_attn_col[static_cast<int64_t>(j) * HH + (k - F)] = v;
   }
 }

@@ -160,7 +160,7 @@ struct GatFwdArgs {
   const int32_t* col;
   const T* x;
   const float* bias;
-  T* out;
+  GatOut<T>* out;
   float* pre;
   float* emax;
   float* esum;
@@ -478,7 +478,7 @@ struct GatBwdArgs {
   const float* attn_row;
   const float* attn_col;
   const float* pre;
-  const T* grad_y;
+  const GatOut<T>* grad_y;
   const float* agg;  // per-row aggregates written by the forward, or null
   // workspace
   float* grad_pre;   // [n, gp_stride]: g_pre in the row's first C floats
@@ -499,7 +499,7 @@ struct GatBwdArgs {
   int rows_blocks;
   int n_l2;
   // outputs
-  T* grad_feat;
+  GatOut<T>* grad_feat;
   float* grad_attn_row;
   float* grad_attn_col;
   float* grad_bias;

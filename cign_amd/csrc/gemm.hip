@@ -66,6 +66,7 @@ struct GemmArgs {
   const float* bias;  // [N] or null
   float* y;           // [M, N]
   bool round_bf16;    // y holds bf16-rounded values (autocast output)
+  bool y_bf16;        // y is bf16 storage (with round_bf16: the same values, exactly)
   // logits epilogue: heads of C columns, alpha_* [M, N / C]
   int C;
   const float* att_src;
@@ -370,7 +371,17 @@ __device__ __forceinline__ void epilogue_swapped(const GemmArgs& g, f32x4 (&acc)
       }
       if (m >= g.M) continue;
       const int64_t o = m * g.N + nb;
-      if (full4) {
+      if (g.y_bf16) {
+        __bf16* yb = reinterpret_cast<__bf16*>(g.y);
+        if (full4) {
+          *reinterpret_cast<bf16x4*>(yb + o) = bf16x4{static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1]),
+                                                      static_cast<__bf16>(v[2]), static_cast<__bf16>(v[3])};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (nb + q < g.N) yb[o + q] = static_cast<__bf16>(v[q]);
+        }
+      } else if (full4) {
         *reinterpret_cast<float4*>(g.y + o) = make_float4(v[0], v[1], v[2], v[3]);
       } else {
 #pragma unroll
@@ -1811,6 +1822,46 @@ int cign_linear_logits_fwd(void* stream, int64_t M, int32_t heads, int32_t chann
   g.round_bf16 = math == kMathBF16;
   g.C = channels; g.att_src = att_src; g.att_dst = att_dst; g.alpha_src = alpha_src; g.alpha_dst = alpha_dst;
   return dispatch_nt<kEpiLogits>(static_cast<hipStream_t>(stream), g, x_dtype, math, bn);
+}
+
+// cign_linear_fwd / cign_linear_logits_fwd with bf16 math whose y is stored
+// as bf16: the values the float32 output would hold (they are bf16-rounded),
+// in half the bytes.
+int cign_linear_fwd_bf16y(void* stream, int64_t M, int32_t N, int32_t K, int32_t x_dtype, const void* x,
+                          const float* w, const float* bias, void* y) {
+  int rc = check_common("cign_linear_fwd_bf16y", M, N, K, x, w, y);
+  if (rc) return rc;
+  if (M == 0) return kOk;
+  GemmArgs g{};
+  g.M = M; g.N = N; g.K = K; g.x = x; g.w = w; g.bias = bias; g.y = static_cast<float*>(y);
+  g.vec = rows_aligned(x, x_dtype, w, K);
+  g.vec4 = N % 4 == 0 && aligned16(y);
+  g.round_bf16 = true;
+  g.y_bf16 = true;
+  return dispatch_nt<kEpiStore>(static_cast<hipStream_t>(stream), g, x_dtype, kMathBF16, pick_bn(N, 0, kMathBF16));
+}
+
+int cign_linear_logits_fwd_bf16y(void* stream, int64_t M, int32_t heads, int32_t channels, int32_t K,
+                                 int32_t x_dtype, const void* x, const float* w, const float* att_src,
+                                 const float* att_dst, void* y, float* alpha_src, float* alpha_dst) {
+  const int N = heads * channels;
+  int rc = check_common("cign_linear_logits_fwd_bf16y", M, N, K, x, w, y);
+  if (rc) return rc;
+  if (!att_src || !att_dst || (M > 0 && (!alpha_src || !alpha_dst)))
+    return set_error(kInvalid, "cign_linear_logits_fwd_bf16y: null pointer");
+  const int bn = pick_bn(N, channels, kMathBF16);
+  if (bn == 0)
+    return set_error(kInvalid, "cign_linear_logits_fwd_bf16y: channels=%d must be 16, 32, 64 or 128 (use "
+                     "cign_linear_fwd_bf16y + cign_attn_logits_fwd_bf16)", channels);
+  if (M == 0) return kOk;
+  GemmArgs g{};
+  g.M = M; g.N = N; g.K = K; g.x = x; g.w = w; g.y = static_cast<float*>(y);
+  g.vec = rows_aligned(x, x_dtype, w, K);
+  g.vec4 = N % 4 == 0 && aligned16(y);
+  g.round_bf16 = true;
+  g.y_bf16 = true;
+  g.C = channels; g.att_src = att_src; g.att_dst = att_dst; g.alpha_src = alpha_src; g.alpha_dst = alpha_dst;
+  return dispatch_nt<kEpiLogits>(static_cast<hipStream_t>(stream), g, x_dtype, kMathBF16, bn);
 }
 
 int cign_linear_gamma_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t x_dtype, int32_t math,

@@ -128,9 +128,10 @@ using namespace rowops;
 // ---------------------------------------------------------------------------
 // Attention logits.
 // ---------------------------------------------------------------------------
-// Rows r of x viewed as [n*H, C]; head h = r % H.
-template <int LPR, int V, int W>
-__global__ __launch_bounds__(kBlock) void attn_fwd_kernel(int64_t rows, int H, int C, const float* x,
+// Rows r of x viewed as [n*H, C]; head h = r % H. x is float32, or bf16
+// storage (TX = bf16h: W values per 2W-byte load).
+template <int LPR, int V, int W, typename TX = float>
+__global__ __launch_bounds__(kBlock) void attn_fwd_kernel(int64_t rows, int H, int C, const TX* x,
                                                           const float* as, const float* ad, float* os, float* od) {
   const Geo<LPR> g;
   const int qc = C / W;
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(int64_t rows, int H, i
       const int c = g.q + v * LPR;
       if (c < qc) {
         float xv[W], av[W], dv[W];
-        Chunk<float, W>::load(x + r * C + c * W, xv);
+        Chunk<TX, W>::load(x + r * C + c * W, xv);
         Chunk<float, W>::load(as + static_cast<int64_t>(h) * C + c * W, av);
         Chunk<float, W>::load(ad + static_cast<int64_t>(h) * C + c * W, dv);
 #pragma unroll
@@ -163,12 +164,13 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(int64_t rows, int H, i
 }
 
 // Rows = nodes of width F = H*C; column tile blockIdx.y of LPR*V chunks.
-// Writes g_x and the tile's partial sums of gs*x and gd*x for row block
-// blockIdx.x (part layout [2][nb][F]).
-template <int LPR, int V, int W>
+// Writes g_x (plus gx_in, the gradient x receives from its other consumer,
+// when not null; it may alias gx) and the tile's partial sums of gs*x and
+// gd*x for row block blockIdx.x (part layout [2][nb][F]).
+template <int LPR, int V, int W, typename TX = float>
 __global__ __launch_bounds__(kBlock) void attn_bwd_kernel(int64_t n, int H, int C, const float* gs, const float* gd,
-                                                          const float* x, const float* as, const float* ad, float* gx,
-                                                          float* part, int nb) {
+                                                          const TX* x, const float* as, const float* ad,
+                                                          const float* gx_in, float* gx, float* part, int nb) {
   __shared__ float lds[kBlock * V * W];
   const Geo<LPR> g;
   const int F = H * C;
@@ -196,11 +198,13 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kernel(int64_t n, int H, int 
       if (c < qf) {
         const float s = gs[r * H + hv[v]];
         const float d = gd[r * H + hv[v]];
-        float xv[W], o[W];
-        Chunk<float, W>::load(x + r * F + c * W, xv);
+        float xv[W], o[W], gi[W];
+        Chunk<TX, W>::load(x + r * F + c * W, xv);
+        if (gx_in) Chunk<float, W>::load(gx_in + r * F + c * W, gi);
 #pragma unroll
         for (int w = 0; w < W; ++w) {
           o[w] = s * av[v][w] + d * dv[v][w];
+          if (gx_in) o[w] = gi[w] + o[w];
           accs[v][w] = fmaf(s, xv[w], accs[v][w]);
           accd[v][w] = fmaf(d, xv[w], accd[v][w]);
         }
@@ -573,6 +577,67 @@ int64_t colsum_bytes(int64_t n, int width, int quantities) {
   return 4LL * quantities * colsum_blocks(n) * width;
 }
 
+// Attention logits over float32 or bf16-stored x (TX = bf16h).
+template <typename TX>
+int attn_fwd_impl(const char* who, void* stream, int64_t n, int32_t H, int32_t C, const TX* x, const float* att_src,
+                  const float* att_dst, float* alpha_src, float* alpha_dst) {
+  if (n < 0 || H < 1 || C < 1)
+    return set_error(kInvalid, "%s: bad shape n=%lld H=%d C=%d", who, static_cast<long long>(n), H, C);
+  if (n == 0) return kOk;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int W = chunk_width(C, {x, att_src, att_dst});
+  const int64_t rows = n * H;
+  const int rc = with_geo(C / W, [&](auto LC, auto VC) {
+    constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
+    const int grid = grid_for(rows, Geo<L>::RPB);
+    if (W == 4)
+      hipLaunchKernelGGL((attn_fwd_kernel<L, V, 4, TX>), dim3(grid), dim3(kBlock), 0, st, rows, H, C, x, att_src,
+                         att_dst, alpha_src, alpha_dst);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<L, V, 1, TX>), dim3(grid), dim3(kBlock), 0, st, rows, H, C, x, att_src,
+                         att_dst, alpha_src, alpha_dst);
+    return check_launch(who);
+  });
+  if (rc < 0) return set_error(kInvalid, "%s: channels=%d too wide (max %d)", who, C, 256 * W);
+  return rc;
+}
+
+// Attention logits backward; grad_x = grad_x_in (when not null; it may alias
+// grad_x) + the logits' term.
+template <typename TX>
+int attn_bwd_impl(const char* who, void* stream, int64_t n, int32_t H, int32_t C, const float* grad_src,
+                  const float* grad_dst, const TX* x, const float* att_src, const float* att_dst,
+                  const float* grad_x_in, float* grad_x, float* grad_att_src, float* grad_att_dst, void* workspace,
+                  int64_t workspace_bytes) {
+  if (n < 0 || H < 1 || C < 1) return set_error(kInvalid, "%s: bad shape", who);
+  const int F = H * C;
+  if (workspace_bytes < colsum_bytes(n, F, 2)) return set_error(kInvalid, "%s: workspace too small", who);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nb = colsum_blocks(n);
+  float* part = static_cast<float*>(workspace);
+  const int W = grad_x_in ? chunk_width(C, {x, att_src, att_dst, grad_x, grad_x_in})
+                          : chunk_width(C, {x, att_src, att_dst, grad_x});
+  const int qf = F / W;
+  if (n > 0) {
+    auto launch = [&](auto LC, auto VC) {
+      constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
+      const dim3 grid(nb, (qf + L * V - 1) / (L * V));
+      if (W == 4)
+        hipLaunchKernelGGL((attn_bwd_kernel<L, V, 4, TX>), grid, dim3(kBlock), 0, st, n, H, C, grad_src, grad_dst, x,
+                           att_src, att_dst, grad_x_in, grad_x, part, nb);
+      else
+        hipLaunchKernelGGL((attn_bwd_kernel<L, V, 1, TX>), grid, dim3(kBlock), 0, st, n, H, C, grad_src, grad_dst, x,
+                           att_src, att_dst, grad_x_in, grad_x, part, nb);
+      return check_launch(who);
+    };
+    const int rc = qf > 256 ? launch(IC<64>(), IC<4>()) : with_geo(qf, launch);
+    if (rc) return rc;
+  } else {
+    return zero_outputs(st, grad_att_src, F, grad_att_dst, F, who);
+  }
+  return launch_colsum(st, part, nb, F, 2, grad_att_src, grad_att_dst, who);
+}
+
 }  // namespace nodeops
 }  // namespace cign
 
@@ -591,56 +656,28 @@ int64_t cign_colsum_workspace_bytes(int64_t n, int32_t width, int32_t quantities
 // ---- attention logits --------------------------------------------------------
 int cign_attn_logits_fwd(void* stream, int64_t n, int32_t H, int32_t C, const float* x, const float* att_src,
                          const float* att_dst, float* alpha_src, float* alpha_dst) {
-  if (n < 0 || H < 1 || C < 1) return set_error(kInvalid, "cign_attn_logits_fwd: bad shape n=%lld H=%d C=%d",
-                                                static_cast<long long>(n), H, C);
-  if (n == 0) return kOk;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int W = chunk_width(C, {x, att_src, att_dst});
-  const int64_t rows = n * H;
-  const int rc = with_geo(C / W, [&](auto LC, auto VC) {
-    constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
-    const int grid = grid_for(rows, Geo<L>::RPB);
-    if (W == 4)
-      hipLaunchKernelGGL((attn_fwd_kernel<L, V, 4>), dim3(grid), dim3(kBlock), 0, st, rows, H, C, x, att_src, att_dst,
-                         alpha_src, alpha_dst);
-    else
-      hipLaunchKernelGGL((attn_fwd_kernel<L, V, 1>), dim3(grid), dim3(kBlock), 0, st, rows, H, C, x, att_src, att_dst,
-                         alpha_src, alpha_dst);
-    return check_launch("cign_attn_logits_fwd");
-  });
-  if (rc < 0) return set_error(kInvalid, "cign_attn_logits_fwd: channels=%d too wide (max %d)", C, 256 * W);
-  return rc;
+  return attn_fwd_impl("cign_attn_logits_fwd", stream, n, H, C, x, att_src, att_dst, alpha_src, alpha_dst);
+}
+
+int cign_attn_logits_fwd_bf16(void* stream, int64_t n, int32_t H, int32_t C, const void* x, const float* att_src,
+                              const float* att_dst, float* alpha_src, float* alpha_dst) {
+  return attn_fwd_impl("cign_attn_logits_fwd_bf16", stream, n, H, C, static_cast<const bf16h*>(x), att_src, att_dst,
+                       alpha_src, alpha_dst);
 }
 
 int cign_attn_logits_bwd(void* stream, int64_t n, int32_t H, int32_t C, const float* grad_src, const float* grad_dst,
                          const float* x, const float* att_src, const float* att_dst, float* grad_x,
                          float* grad_att_src, float* grad_att_dst, void* workspace, int64_t workspace_bytes) {
-  if (n < 0 || H < 1 || C < 1) return set_error(kInvalid, "cign_attn_logits_bwd: bad shape");
-  const int F = H * C;
-  if (workspace_bytes < colsum_bytes(n, F, 2)) return set_error(kInvalid, "cign_attn_logits_bwd: workspace too small");
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int nb = colsum_blocks(n);
-  float* part = static_cast<float*>(workspace);
-  const int W = chunk_width(C, {x, att_src, att_dst, grad_x});
-  const int qf = F / W;
-  if (n > 0) {
-    auto launch = [&](auto LC, auto VC) {
-      constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
-      const dim3 grid(nb, (qf + L * V - 1) / (L * V));
-      if (W == 4)
-        hipLaunchKernelGGL((attn_bwd_kernel<L, V, 4>), grid, dim3(kBlock), 0, st, n, H, C, grad_src, grad_dst, x,
-                           att_src, att_dst, grad_x, part, nb);
-      else
-        hipLaunchKernelGGL((attn_bwd_kernel<L, V, 1>), grid, dim3(kBlock), 0, st, n, H, C, grad_src, grad_dst, x,
-                           att_src, att_dst, grad_x, part, nb);
-      return check_launch("cign_attn_logits_bwd");
-    };
-    const int rc = qf > 256 ? launch(IC<64>(), IC<4>()) : with_geo(qf, launch);
-    if (rc) return rc;
-  } else {
-    return zero_outputs(st, grad_att_src, F, grad_att_dst, F, "cign_attn_logits_bwd");
-  }
-  return launch_colsum(st, part, nb, F, 2, grad_att_src, grad_att_dst, "cign_attn_logits_bwd");
+  return attn_bwd_impl("cign_attn_logits_bwd", stream, n, H, C, grad_src, grad_dst, x, att_src, att_dst, nullptr,
+                       grad_x, grad_att_src, grad_att_dst, workspace, workspace_bytes);
+}
+
+int cign_attn_logits_bwd_bf16(void* stream, int64_t n, int32_t H, int32_t C, const float* grad_src,
+                              const float* grad_dst, const void* x, const float* att_src, const float* att_dst,
+                              const float* grad_x_in, float* grad_x, float* grad_att_src, float* grad_att_dst,
+                              void* workspace, int64_t workspace_bytes) {
+  return attn_bwd_impl("cign_attn_logits_bwd_bf16", stream, n, H, C, grad_src, grad_dst, static_cast<const bf16h*>(x),
+                       att_src, att_dst, grad_x_in, grad_x, grad_att_src, grad_att_dst, workspace, workspace_bytes);
 }
 
 // ---- head mean + bias + SiLU ----------------------------------------------

@@ -19,9 +19,9 @@ follow its calls in the block:
   fused_block_ops.fused_dropout_gamma_residual), the dropout mask drawn with
   the reference's block-op seed stream.
 
-Backward (all three): grad_x = grad_y W on hipBLASLt, grad_W = grad_y^T x on
-a split-M MFMA kernel (the reduction over nodes that the libraries run
-slowly), grad_b = sum_n grad_y; with ``amp`` every product reads
+Backward (all three): grad_x = grad_y W on the forward's MFMA kernel against
+a transposed W, grad_W = grad_y^T x on a split-M MFMA kernel, grad_b =
+sum_n grad_y; with ``amp`` every product reads
 bf16-rounded operands with fp32 accumulation, as autocast's backward does;
 grad_W and grad_b are deterministic (chunk partials summed in order). The
 logits and gamma-residual parts run on their existing kernels

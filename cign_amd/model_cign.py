@@ -34,7 +34,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import _pack, pack_proj
+from . import _pack, amp_gat, pack_proj
 from .collapsed_gat import collapsed_gat_mean_bias_silu
 from .fused_block_ops import fused_add_layernorm_cat, fused_dropout_layernorm
 from .graph import selected_sparse_powers
@@ -51,6 +51,12 @@ def cign_outer_difference(b_hr, b_rh, mode):
     if mode == "none":
         return raw
     raise ValueError(f"Invalid outer nonlinearity: {mode}")
+
+
+def _bf16_proj_enabled() -> bool:
+    """CIGN_GAT_BF16_PROJ (default 1): under selective bf16 AMP the GAT's
+    projection output is held in bf16 (amp_gat); 0 keeps it float32."""
+    return os.environ.get("CIGN_GAT_BF16_PROJ", "1").strip() != "0"
 
 
 def _resolve_selective_amp_dtype(name: str):
@@ -123,9 +129,14 @@ class CompatibleCollapsedFusedGATConv(nn.Module):
             raise RuntimeError(f"Generalized collapsed GAT requires 1<=heads<=32 and 1<=channels<=256; got H={H},C={C}")
         amp_enabled = bool(getattr(self, "_selective_amp_enabled", False))
         amp_dtype = getattr(self, "_selective_amp_dtype", torch.bfloat16)
+        dropout = self.dropout if self.training else 0.0
+        if (amp_enabled and self.bias is not None and not isinstance(csr, ShardedGAT) and _bf16_proj_enabled()
+                and amp_gat.supported(H, C, amp_dtype)):
+            # x_proj held in bf16 (the values the float32 result holds)
+            return amp_gat.amp_lin_gat(x, self.lin.weight, self.att_src, self.att_dst, self.bias, csr, csc, perm,
+                                       self.negative_slope, dropout, H)
         xp, alpha_src, alpha_dst = linear_attention_logits(x, self.lin.weight, self.att_src, self.att_dst, H,
                                                            amp_enabled, amp_dtype)
-        dropout = self.dropout if self.training else 0.0
         if isinstance(csr, ShardedGAT):
             # the partitioned graph (model_cign.py:462 dispatches on ChunkedDgNNGraph alike)
             return sharded_collapsed_gat_mean_bias_silu(alpha_dst, alpha_src, csr, self.negative_slope, xp,

@@ -137,5 +137,5 @@ def gat_schedule(rowptr: torch.Tensor, pass_: int, dtype_code: int, heads: int, 
              C.byref(seg))
     if seg.value > 0:
         return cached_row_schedule(rowptr, light.value, seg.value)
-    row_bytes = int(heads) * int(channels) * (2 if dtype_code == 1 else 4)
+    row_bytes = int(heads) * int(channels) * (2 if dtype_code in (1, 2) else 4)
     return cached_row_schedule(rowptr, light.value, None, seg_floor_for(row_bytes) if pass_ == 0 else SEG_EDGES)

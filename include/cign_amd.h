@@ -9,7 +9,9 @@
  *     of the last error of the calling thread is cign_last_error().
  *   - All tensors are device pointers to contiguous row-major memory owned by
  *     the caller (inputs borrowed, outputs and workspaces preallocated).
- *   - dtype: 0 = float32, 1 = bfloat16 (storage only; math is float32).
+ *   - dtype: 0 = float32, 1 = bfloat16 (storage only; math is float32);
+ *     the collapsed GAT also takes 2 = bfloat16 features with float32
+ *     outputs and gradients (see cign_gat_fwd).
  *   - Row schedules (cign_amd/csrc/schedule.h) are built on the host once per
  *     CSR/CSC row pointer with cign_row_schedule_size / _build and replace the
  *     row pointer in every launch: the caller uploads the buffer and passes it
@@ -124,7 +126,11 @@ int64_t cign_gat_row_agg_floats(int32_t dtype, int32_t n, int32_t heads, int32_t
  * Outputs: out [n,C] (dtype), pre [n,C] f32, edge_max/edge_sum [n,H] f32,
  * edge_mask [nnz,H] u8 (written only when attn_drop > 0). row_agg: null, or
  * cign_gat_row_agg_floats() floats (16-byte aligned) to receive the per-row
- * aggregates of the backward. */
+ * aggregates of the backward. dtype 2 (shapes with cign_gat_row_agg_floats
+ * > 0): in_feat bf16, out (and, in cign_gat_bwd, grad_y and grad_feat)
+ * float32: the results of dtype 0 on the same values when in_feat holds the
+ * bf16 output of an autocast projection, which _local_amp_linear returns as
+ * float32 (model_cign.py:86-103, :546-553), in half the gathered bytes. */
 int cign_gat_fwd(void* stream, int32_t dtype, int32_t n, int32_t nnz, int32_t heads, int32_t channels,
                  const float* attn_row, const float* attn_col, const int32_t* col, const int32_t* row_sched,
                  const int32_t* row_sched_info, int32_t* row_counters, float negative_slope, const void* in_feat,
@@ -216,6 +222,19 @@ int cign_attn_logits_bwd(void* stream, int64_t n, int32_t heads, int32_t channel
                          const float* grad_dst, const float* x, const float* att_src, const float* att_dst,
                          float* grad_x, float* grad_att_src, float* grad_att_dst, void* workspace,
                          int64_t workspace_bytes);
+
+/* cign_attn_logits_fwd / _bwd on x stored as bf16 [n,H,C] (the GAT lin's
+ * bf16 output, see cign_linear_fwd_bf16y); the backward writes grad_x =
+ * grad_x_in + the logits' term, grad_x_in being the gradient x receives from
+ * the collapsed GAT (null for none; it may alias grad_x), so the sum of the
+ * two consumers' gradients that autograd forms in float32 takes no pass of
+ * its own. No counterpart in the reference (its x is float32). */
+int cign_attn_logits_fwd_bf16(void* stream, int64_t n, int32_t heads, int32_t channels, const void* x,
+                              const float* att_src, const float* att_dst, float* alpha_src, float* alpha_dst);
+int cign_attn_logits_bwd_bf16(void* stream, int64_t n, int32_t heads, int32_t channels, const float* grad_src,
+                              const float* grad_dst, const void* x, const float* att_src, const float* att_dst,
+                              const float* grad_x_in, float* grad_x, float* grad_att_src, float* grad_att_dst,
+                              void* workspace, int64_t workspace_bytes);
 
 /* pre = sum_h out[n,h,:] / H + bias, y = SiLU(pre). Replaces ext
  * head_silu_forward (fused_gat_sideops.cpp:68-76; kernel
@@ -413,6 +432,18 @@ int cign_linear_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t x_dty
 int cign_linear_logits_fwd(void* stream, int64_t M, int32_t heads, int32_t channels, int32_t K, int32_t x_dtype,
                            int32_t math, const void* x, const float* w, const float* att_src, const float* att_dst,
                            float* y, float* alpha_src, float* alpha_dst);
+
+/* cign_linear_fwd / cign_linear_logits_fwd with math 1 whose y is stored as
+ * bf16 [M,N]: the same values (math 1 rounds the output to bf16), half the
+ * bytes. For a projection whose only consumers read bf16 (the collapsed GAT
+ * with dtype 2, cign_attn_logits_*_bf16): the GAT lin of
+ * CompatibleCollapsedFusedGATConv under selective AMP (model_cign.py:546-553),
+ * whose float32 result holds bf16 values. */
+int cign_linear_fwd_bf16y(void* stream, int64_t M, int32_t N, int32_t K, int32_t x_dtype, const void* x,
+                          const float* w, const float* bias, void* y);
+int cign_linear_logits_fwd_bf16y(void* stream, int64_t M, int32_t heads, int32_t channels, int32_t K,
+                                 int32_t x_dtype, const void* x, const float* w, const float* att_src,
+                                 const float* att_dst, void* y, float* alpha_src, float* alpha_dst);
 
 /* Projection + dropout-gamma-residual: g_out [M,N] = x W^T + b,
  * y = h + gamma * keep * g_out / (1-p), mask [M,N] u8 (keep = 53-bit
