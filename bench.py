@@ -656,7 +656,7 @@ def run_block(args, torch):
                                            gbt.data_ptr(), pp_ws.data_ptr(), pp_ws.numel()),
                           (20 + 16 * K) * NDb + 8 * n * K, 4 * n * 2 * K * D * D),
     }
-    # The GAT lin: under AMP its bf16 output is held in bf16 (amp_gat), as the
+    # The GAT lin: under AMP its bf16 output is held in bf16 (lin_gat), as the
     # block runs it; fp32 otherwise.
     if amp:
         xl16 = torch.empty(n, heads * D, dtype=torch.bfloat16, device=dev)
@@ -668,7 +668,7 @@ def run_block(args, torch):
                                                  Wl.data_ptr(), None, xl.data_ptr()),
                                 4 * NDb + 4 * n * heads * D, 2 * n * D * heads * D)
     # The block's collapsed GAT (H=6 x C=256; under AMP on the bf16-held
-    # projection output with fp32 outputs and gradients, as amp_gat runs it)
+    # projection output with fp32 outputs and gradients, as lin_gat runs it)
     # and one hop of its multihop SpMM (D = 2 x 256), as the block runs them.
     from cign_amd.collapsed_gat import ensure_collapsed_gat_loaded
 

@@ -672,12 +672,18 @@ int cign_attn_logits_bwd(void* stream, int64_t n, int32_t H, int32_t C, const fl
                        grad_x, grad_att_src, grad_att_dst, workspace, workspace_bytes);
 }
 
-int cign_attn_logits_bwd_bf16(void* stream, int64_t n, int32_t H, int32_t C, const float* grad_src,
-                              const float* grad_dst, const void* x, const float* att_src, const float* att_dst,
-                              const float* grad_x_in, float* grad_x, float* grad_att_src, float* grad_att_dst,
-                              void* workspace, int64_t workspace_bytes) {
-  return attn_bwd_impl("cign_attn_logits_bwd_bf16", stream, n, H, C, grad_src, grad_dst, static_cast<const bf16h*>(x),
-                       att_src, att_dst, grad_x_in, grad_x, grad_att_src, grad_att_dst, workspace, workspace_bytes);
+int cign_attn_logits_bwd_acc(void* stream, int64_t n, int32_t H, int32_t C, int32_t x_dtype, const float* grad_src,
+                             const float* grad_dst, const void* x, const float* att_src, const float* att_dst,
+                             const float* grad_x_in, float* grad_x, float* grad_att_src, float* grad_att_dst,
+                             void* workspace, int64_t workspace_bytes) {
+  const char* who = "cign_attn_logits_bwd_acc";
+  if (x_dtype == kF32)
+    return attn_bwd_impl(who, stream, n, H, C, grad_src, grad_dst, static_cast<const float*>(x), att_src, att_dst,
+                         grad_x_in, grad_x, grad_att_src, grad_att_dst, workspace, workspace_bytes);
+  if (x_dtype == kBF16)
+    return attn_bwd_impl(who, stream, n, H, C, grad_src, grad_dst, static_cast<const bf16h*>(x), att_src, att_dst,
+                         grad_x_in, grad_x, grad_att_src, grad_att_dst, workspace, workspace_bytes);
+  return set_error(kInvalid, "%s: x_dtype must be 0 (float32) or 1 (bf16), got %d", who, x_dtype);
 }
 
 // ---- head mean + bias + SiLU ----------------------------------------------

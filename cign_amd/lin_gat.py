@@ -1,0 +1,136 @@
+"""The context GAT's projection, attention logits and collapsed GAT as one
+autograd function (CompatibleCollapsedFusedGATConv.forward,
+generic_engine/model_cign.py:546-566).
+
+The reference runs three functions: ``_local_amp_linear`` (the ``lin``,
+model_cign.py:86-103), the attention logits (fused_gat_sideops.py:94-97) and
+the collapsed GAT (collapsed_gat.py:164-225). x_proj feeds both the logits
+and the GAT, so autograd sums their two gradients of it in a pass of its own
+before the projection's backward; here the logits' backward adds the GAT's
+gradient as it writes its own (cign_attn_logits_bwd_acc), which is that sum.
+
+Under selective bf16 AMP the ``lin`` returns ``.float()`` of a bf16 result,
+so x_proj holds bf16 values. Where the library runs the GAT on bf16 features
+with fp32 outputs and gradients (its feature-layout shapes, dtype 2) the
+projection stores those values as bf16 and every consumer reads them so
+with fp32 math: the forward computes what the fp32 x_proj gives, in half the
+bytes, and the backward rounds where the reference does (the two gradients
+summed in fp32, then rounded to bf16 by the projection's backward, as
+autocast's backward does). That needs one function: autograd would round
+each consumer's gradient to the dtype of a bf16 x_proj before summing.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .collapsed_gat import _check, bf16_f32_supported, ensure_collapsed_gat_loaded, next_seed
+from .linear import _linear_bwd, _math_code, _prep_x
+from .schedule import gat_schedule
+
+_FUSED_LOGITS_C = (16, 32, 64, 128)
+
+
+def holds_bf16(heads: int, channels: int, math: int) -> bool:
+    """Whether x_proj is held in bf16: bf16 autocast (math 1) on a shape the
+    library runs with bf16 features and fp32 outputs."""
+    return math == 1 and bf16_f32_supported(heads, channels)
+
+
+class _LinGatFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, att_src, att_dst, bias, rowptr, col, colptr, row, perm, negative_slope, attn_drop,
+                seed, heads, math):
+        lib = _lib.load_library()
+        x2 = _prep_x(x)
+        w = weight.detach().float().contiguous()
+        M, K = x2.shape
+        H = int(heads)
+        C = w.size(0) // H
+        dev = x2.device
+        st = _lib.stream_ptr(dev)
+        hold = holds_bf16(H, C, math)
+        xp = torch.empty((M, H, C), dtype=torch.bfloat16 if hold else torch.float32, device=dev)
+        a_src = torch.empty((M, H), dtype=torch.float32, device=dev)
+        a_dst = torch.empty((M, H), dtype=torch.float32, device=dev)
+        s = att_src.detach().float().contiguous()
+        d = att_dst.detach().float().contiguous()
+        xd = _lib.dtype_code(x2)
+        if C in _FUSED_LOGITS_C:
+            if hold:
+                lib.call("cign_linear_logits_fwd_bf16y", st, M, H, C, K, xd, x2.data_ptr(), w.data_ptr(),
+                         s.data_ptr(), d.data_ptr(), xp.data_ptr(), a_src.data_ptr(), a_dst.data_ptr())
+            else:
+                lib.call("cign_linear_logits_fwd", st, M, H, C, K, xd, math, x2.data_ptr(), w.data_ptr(),
+                         s.data_ptr(), d.data_ptr(), xp.data_ptr(), a_src.data_ptr(), a_dst.data_ptr())
+        else:
+            if hold:
+                lib.call("cign_linear_fwd_bf16y", st, M, H * C, K, xd, x2.data_ptr(), w.data_ptr(), None,
+                         xp.data_ptr())
+                lib.call("cign_attn_logits_fwd_bf16", st, M, H, C, xp.data_ptr(), s.data_ptr(), d.data_ptr(),
+                         a_src.data_ptr(), a_dst.data_ptr())
+            else:
+                lib.call("cign_linear_fwd", st, M, H * C, K, xd, math, x2.data_ptr(), w.data_ptr(), None,
+                         xp.data_ptr())
+                lib.call("cign_attn_logits_fwd", st, M, H, C, xp.data_ptr(), s.data_ptr(), d.data_ptr(),
+                         a_src.data_ptr(), a_dst.data_ptr())
+        rowptr, col, colptr, row, perm = (t.contiguous() for t in (rowptr, col, colptr, row, perm))
+        bias_c = bias.detach().float().contiguous()
+        # the backward's schedules, built now so the backward never synchronises
+        code = 2 if hold else 0
+        gat_schedule(rowptr, 1, code, H, C)
+        gat_schedule(colptr, 1, code, H, C)
+        ext = ensure_collapsed_gat_loaded(False)
+        (y, pre, edge_max, edge_sum, edge_mask), agg = ext.forward_agg(
+            a_dst, a_src, rowptr, col, float(negative_slope), xp, bias_c, float(attn_drop), int(seed), True,
+            f32_out=hold)
+        ctx.save_for_backward(x2, w, s, d, xp, a_src, a_dst, col, row, perm, edge_max, edge_sum, edge_mask, pre,
+                              agg)
+        ctx.graph = (rowptr, colptr)
+        ctx.negative_slope = float(negative_slope)
+        ctx.attn_drop = float(attn_drop)
+        ctx.hold = hold
+        ctx.math = int(math)
+        ctx.x_dtype = x.dtype
+        ctx.in_shape = x.shape
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        (x2, w, s, d, xp, a_src, a_dst, col, row, perm, edge_max, edge_sum, edge_mask, pre,
+         agg) = ctx.saved_tensors
+        rowptr, colptr = ctx.graph
+        lib = _lib.load_library()
+        ext = ensure_collapsed_gat_loaded(False)
+        M, H, C = xp.shape
+        dev = xp.device
+        grad_feat, g_attn_row, g_attn_col, g_bias = ext.backward(
+            ctx.negative_slope, ctx.attn_drop, rowptr, col, colptr, row, perm, edge_max, edge_sum, edge_mask, xp,
+            a_dst, a_src, pre, grad_y.float().contiguous(), agg, f32_out=ctx.hold)
+        # d alpha_src is the GAT's attn_col gradient, d alpha_dst its attn_row
+        # gradient; the logits' term is added to grad_feat in place.
+        g_s = torch.empty_like(s)
+        g_d = torch.empty_like(d)
+        ws_bytes = int(lib.cign_colsum_workspace_bytes(M, H * C, 2))
+        ws = _lib.workspace(ws_bytes, dev)
+        lib.call("cign_attn_logits_bwd_acc", _lib.stream_ptr(dev), M, H, C, 1 if ctx.hold else 0,
+                 g_attn_col.data_ptr(), g_attn_row.data_ptr(), xp.data_ptr(), s.data_ptr(), d.data_ptr(),
+                 grad_feat.data_ptr(), grad_feat.data_ptr(), g_s.data_ptr(), g_d.data_ptr(), ws.data_ptr(), ws_bytes)
+        gx, gw, _ = _linear_bwd(grad_feat, x2, w, False, ctx.math, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+        if gx is not None:
+            gx = gx.reshape(ctx.in_shape).to(ctx.x_dtype)
+        return (gx, gw, g_s, g_d, g_bias) + (None,) * 10
+
+
+def lin_gat(x: torch.Tensor, weight: torch.Tensor, att_src: torch.Tensor, att_dst: torch.Tensor,
+            bias: torch.Tensor, csr, csc, perm: torch.Tensor, negative_slope: float, attn_drop: float, heads: int,
+            amp: bool = False, amp_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """SiLU(mean_h GAT_h(x_proj) + bias) with x_proj = lin(x) (bf16 autocast
+    with ``amp``) and its attention logits (model_cign.py:546-566). Dropout
+    seeds as collapsed_gat_mean_bias_silu: one per call."""
+    _check(bias is not None, "collapsed GAT currently requires bias=True")
+    _check(x.dim() == 2, f"FusedGAT expects a 2-D node feature tensor, got {tuple(x.shape)}")
+    math = _math_code(bool(amp), amp_dtype)
+    (rowptr, col), (row, colptr) = csr, csc
+    return _LinGatFn.apply(x, weight, att_src, att_dst, bias, rowptr, col, colptr, row, perm, float(negative_slope),
+                           float(attn_drop), next_seed(attn_drop), int(heads), math)

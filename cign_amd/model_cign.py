@@ -34,7 +34,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import _pack, amp_gat, pack_proj
+from . import _pack, lin_gat, pack_proj
 from .collapsed_gat import collapsed_gat_mean_bias_silu
 from .fused_block_ops import fused_add_layernorm_cat, fused_dropout_layernorm
 from .graph import selected_sparse_powers
@@ -53,10 +53,12 @@ def cign_outer_difference(b_hr, b_rh, mode):
     raise ValueError(f"Invalid outer nonlinearity: {mode}")
 
 
-def _bf16_proj_enabled() -> bool:
-    """CIGN_GAT_BF16_PROJ (default 1): under selective bf16 AMP the GAT's
-    projection output is held in bf16 (amp_gat); 0 keeps it float32."""
-    return os.environ.get("CIGN_GAT_BF16_PROJ", "1").strip() != "0"
+def _fused_lin_gat() -> bool:
+    """CIGN_GAT_FUSED_LIN (default 1): the GAT's lin, logits and collapsed GAT
+    run as one autograd function (lin_gat: the two gradients of x_proj summed
+    inside the logits' backward, x_proj held in bf16 under bf16 AMP); 0 runs
+    them as three."""
+    return os.environ.get("CIGN_GAT_FUSED_LIN", "1").strip() != "0"
 
 
 def _resolve_selective_amp_dtype(name: str):
@@ -130,11 +132,9 @@ class CompatibleCollapsedFusedGATConv(nn.Module):
         amp_enabled = bool(getattr(self, "_selective_amp_enabled", False))
         amp_dtype = getattr(self, "_selective_amp_dtype", torch.bfloat16)
         dropout = self.dropout if self.training else 0.0
-        if (amp_enabled and self.bias is not None and not isinstance(csr, ShardedGAT) and _bf16_proj_enabled()
-                and amp_gat.supported(H, C, amp_dtype)):
-            # x_proj held in bf16 (the values the float32 result holds)
-            return amp_gat.amp_lin_gat(x, self.lin.weight, self.att_src, self.att_dst, self.bias, csr, csc, perm,
-                                       self.negative_slope, dropout, H)
+        if self.bias is not None and not isinstance(csr, ShardedGAT) and _fused_lin_gat():
+            return lin_gat.lin_gat(x, self.lin.weight, self.att_src, self.att_dst, self.bias, csr, csc, perm,
+                                   self.negative_slope, dropout, H, amp_enabled, amp_dtype)
         xp, alpha_src, alpha_dst = linear_attention_logits(x, self.lin.weight, self.att_src, self.att_dst, H,
                                                            amp_enabled, amp_dtype)
         if isinstance(csr, ShardedGAT):

@@ -223,18 +223,22 @@ int cign_attn_logits_bwd(void* stream, int64_t n, int32_t heads, int32_t channel
                          float* grad_x, float* grad_att_src, float* grad_att_dst, void* workspace,
                          int64_t workspace_bytes);
 
-/* cign_attn_logits_fwd / _bwd on x stored as bf16 [n,H,C] (the GAT lin's
- * bf16 output, see cign_linear_fwd_bf16y); the backward writes grad_x =
- * grad_x_in + the logits' term, grad_x_in being the gradient x receives from
- * the collapsed GAT (null for none; it may alias grad_x), so the sum of the
- * two consumers' gradients that autograd forms in float32 takes no pass of
- * its own. No counterpart in the reference (its x is float32). */
+/* cign_attn_logits_fwd on x stored as bf16 [n,H,C] (the GAT lin's bf16
+ * output, see cign_linear_fwd_bf16y). No counterpart in the reference (its x
+ * is float32). */
 int cign_attn_logits_fwd_bf16(void* stream, int64_t n, int32_t heads, int32_t channels, const void* x,
                               const float* att_src, const float* att_dst, float* alpha_src, float* alpha_dst);
-int cign_attn_logits_bwd_bf16(void* stream, int64_t n, int32_t heads, int32_t channels, const float* grad_src,
-                              const float* grad_dst, const void* x, const float* att_src, const float* att_dst,
-                              const float* grad_x_in, float* grad_x, float* grad_att_src, float* grad_att_dst,
-                              void* workspace, int64_t workspace_bytes);
+
+/* cign_attn_logits_bwd that also adds the gradient x receives from its other
+ * consumer, the collapsed GAT: grad_x = grad_x_in + gs*att_src + gd*att_dst
+ * (grad_x_in may alias grad_x; null for none), the sum autograd forms between
+ * ext attention_backward (fused_gat_sideops.cpp:54-66) and the GAT's
+ * backward, without a pass of its own. x_dtype: 0 = float32, 1 = bf16
+ * storage (as cign_attn_logits_fwd_bf16). */
+int cign_attn_logits_bwd_acc(void* stream, int64_t n, int32_t heads, int32_t channels, int32_t x_dtype,
+                             const float* grad_src, const float* grad_dst, const void* x, const float* att_src,
+                             const float* att_dst, const float* grad_x_in, float* grad_x, float* grad_att_src,
+                             float* grad_att_dst, void* workspace, int64_t workspace_bytes);
 
 /* pre = sum_h out[n,h,:] / H + bias, y = SiLU(pre). Replaces ext
  * head_silu_forward (fused_gat_sideops.cpp:68-76; kernel

@@ -1,14 +1,15 @@
 """bf16 features with fp32 outputs and gradients (library dtype 2) and the
-AMP context GAT that holds its projection output in bf16 (amp_gat).
+context GAT's lin + logits + collapsed GAT as one autograd function
+(lin_gat), which under bf16 AMP holds its projection output in bf16.
 
 Dtype 2 runs the bf16 kernels' lane geometry with fp32 outputs, so on the
 same values it must give the bf16 (dtype 1) launch's fp32 results bit for
 bit and its bf16 outputs before rounding; against fp32 features holding the
 same values (dtype 0, another lane geometry) it agrees to the fp32
-tolerance. The AMP module path is checked against the float32-held path it
-replaces (CIGN_GAT_BF16_PROJ=0): the same rounding points, so the fp32
-tolerance plus, where an operand is rounded to bf16, one bf16 ulp; against
-the oracle it is covered by the block and net tests."""
+tolerance. The module path is checked against the three autograd functions
+it replaces (CIGN_GAT_FUSED_LIN=0): the same rounding points, so the fp32
+tolerance plus, under AMP where an operand is rounded to bf16, one bf16 ulp;
+against the oracle it is covered by the block and net tests."""
 import numpy as np
 import pytest
 import torch
@@ -120,10 +121,12 @@ def test_gat_bf16_f32_rejects_pair_layout_shapes():
     assert _lib.load_library() is not None
 
 
-@pytest.mark.parametrize("C", [256, 64])
-def test_amp_context_gat_matches_float32_held_projection(C, monkeypatch):
-    """The module forward + backward with the projection output held in bf16
-    against the float32-held path, under bf16 AMP with GAT dropout. The GAT
+@pytest.mark.parametrize("C,amp", [(256, True), (64, True), (256, False), (64, False), (40, False), (40, True)])
+def test_lin_gat_matches_three_functions(C, amp, monkeypatch):
+    """The module forward + backward as one function against the lin, the
+    logits and the collapsed GAT as three, with GAT dropout, in fp32 and
+    under bf16 AMP (x_proj held in bf16 where the shape allows: C 256 and 64;
+    C = 40 takes the pair-layout GAT on a float32 x_proj). Under AMP the GAT
     runs another lane geometry on each path (fp32 reassociation), so grad x
     and grad W, which round their operand to bf16, also allow one bf16 ulp."""
     import itertools
@@ -142,13 +145,13 @@ def test_amp_context_gat_matches_float32_held_projection(C, monkeypatch):
     mod = CompatibleCollapsedFusedGATConv(K, C, heads=H, dropout=0.32).cuda().train()
     with torch.no_grad():
         mod.bias.normal_()
-    mod._selective_amp_enabled = True
+    mod._selective_amp_enabled = amp
     mod._selective_amp_dtype = torch.bfloat16
     x0 = torch.from_numpy(rng.standard_normal((n, K)).astype(np.float32)).cuda()
     gy = torch.from_numpy(rng.standard_normal((n, C)).astype(np.float32)).cuda()
     res = {}
     for mode in ("1", "0"):
-        monkeypatch.setenv("CIGN_GAT_BF16_PROJ", mode)
+        monkeypatch.setenv("CIGN_GAT_FUSED_LIN", mode)
         # the same dropout seed for both runs
         torch.manual_seed(5)
         monkeypatch.setattr(collapsed_gat, "_CALL_COUNTER", itertools.count())
@@ -161,5 +164,5 @@ def test_amp_context_gat_matches_float32_held_projection(C, monkeypatch):
     assert set(res["1"]) == {"y", "x", "lin.weight", "att_src", "att_dst", "bias"}
     for k, e in res["0"].items():
         a = res["1"][k]
-        extra = bf16_flip_atol(e.cpu().numpy()) if k in ("x", "lin.weight") else 0.0
+        extra = bf16_flip_atol(e.cpu().numpy()) if amp and k in ("x", "lin.weight") else 0.0
         assert_close(a, e, rtol=1e-4, atol=1e-5 * max(1.0, float(e.abs().max())) + extra, name=k)
