@@ -100,6 +100,11 @@ def test_gat_bf16_f32_dtype(H, C, p, n, hubs, big, monkeypatch):
     assert b2[0].dtype == torch.float32
     for a, e in zip(b2, b1):
         _match(a, e, same_lanes)
+    # without the aggregates: the rows pass gathers x again (another order)
+    b2g = ext.backward(0.2, p, rowptr, col, colptr, row, perm, f2[2], f2[3], f2[4], x16, ar, ac, f2[1], gy, None,
+                       f32_out=True)
+    for a, e in zip(b2g, b2):
+        assert_close(a, e, **F32)
     for a, e in zip(b2, b0):
         assert_close(a, e, **F32)
 
