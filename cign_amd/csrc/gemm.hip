@@ -233,17 +233,23 @@ __device__ __forceinline__ void load_x(const GemmArgs& g, const TX* x, int64_t m
   }
 }
 
-// The K step starting at k0 can take the unconditional loads.
-__device__ __forceinline__ bool fast_step(const GemmArgs& g, int k0) { return g.vec && k0 + kBK <= g.K; }
+// The K step starting at k0 can take the unconditional loads. FULL: the host
+// has checked that every step can (aligned rows, K a multiple of kBK), so the
+// guarded loads are not compiled: a guarded path in the loop makes the
+// compiler wait for every load in flight before the step's MFMAs.
+template <bool FULL = false>
+__device__ __forceinline__ bool fast_step(const GemmArgs& g, int k0) {
+  return FULL || (g.vec && k0 + kBK <= g.K);
+}
 
 // One K step's x fragments of a wavefront: its two 16-row tiles.
 struct XStep {
   float v[2][8];
 };
 
-template <typename TX, int MATH>
+template <typename TX, int MATH, bool FULL = false>
 __device__ __forceinline__ void load_xstep(const GemmArgs& g, const TX* x, int64_t row0, int k0, int lane, XStep& a) {
-  const bool fast = fast_step(g, k0);
+  const bool fast = fast_step<FULL>(g, k0);
 #pragma unroll
   for (int r = 0; r < 2; ++r) load_x<TX, MATH>(g, x, row0 + 16 * r + (lane & 15), k0, lane >> 4, fast, a.v[r]);
 }
@@ -255,9 +261,10 @@ struct WStage {
   static constexpr int CHUNKS = BN * kBK / 4 / kThreads;  // 16-byte fp32 chunks per thread
   float b[CHUNKS][4];
 
+  template <bool FULL = false>
   __device__ __forceinline__ void load(const GemmArgs& g, int n0, int k0) {
     constexpr int CPR = kBK / 4;
-    if (fast_step(g, k0)) {
+    if (fast_step<FULL>(g, k0)) {
       // Rows past N read row N-1; their output columns are never stored.
 #pragma unroll
       for (int i = 0; i < CHUNKS; ++i) {
@@ -288,10 +295,71 @@ struct WStage {
   }
 };
 
+#ifndef CIGN_GEMM_ASM_MFMA
+#define CIGN_GEMM_ASM_MFMA 1
+#endif
+// MFMAs accumulating in place (vdst == srcC), for the K loops of the
+// unguarded (FULL) kernels. With the builtins the compiler allocates each
+// result apart from its accumulator and copies it back every iteration (two
+// moves per MFMA in the bf16 loop, as many VALU cycles as the MFMAs take);
+// here the accumulators stay put. Their operands come straight from global
+// or LDS loads, whose waits the compiler inserts; the compiler does not see
+// these as MFMAs, so mfma_settle puts the wait states an MFMA result needs
+// between the accumulators' initialisation, the K loop and the epilogue.
+// The guarded kernels, whose operands pass through selects, keep the
+// builtins.
+__device__ __forceinline__ void mfma_bf16_acc(f32x4& c, const bf16x8& a, const bf16x8& b) {
+  asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_f32_acc(f32x4& c, float a, float b) {
+  asm("v_mfma_f32_16x16x4_f32 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
+
+// Wait states between MFMAs writing the accumulators and any other
+// instruction reading or writing them (at most 18 for any MFMA): every
+// accumulator passes through an empty statement before and after the nops.
+template <int R, int TN>
+__device__ __forceinline__ void mfma_settle(f32x4 (&acc)[R][TN]) {
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int f = 0; f < TN; ++f) asm volatile("" : "+v"(acc[r][f]));
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 4");
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int f = 0; f < TN; ++f) asm volatile("" : "+v"(acc[r][f]));
+}
+
+// One bf16 MFMA, or the four fp32 MFMAs of a 16-wide k chunk (k slices x, y,
+// z, w), accumulating into c: in place when ASM (operands from LDS reads).
+template <bool ASM>
+__device__ __forceinline__ void mma_bf16(f32x4& c, const bf16x8& a, const bf16x8& b) {
+  if constexpr (ASM) mfma_bf16_acc(c, a, b);
+  else c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+template <bool ASM>
+__device__ __forceinline__ void mma_f32x4(f32x4& c, const float4& a, const float4& b) {
+  if constexpr (ASM) {
+    mfma_f32_acc(c, a.x, b.x);
+    mfma_f32_acc(c, a.y, b.y);
+    mfma_f32_acc(c, a.z, b.z);
+    mfma_f32_acc(c, a.w, b.w);
+  } else {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, c, 0, 0, 0);
+  }
+}
+// Kernels whose MFMA operands all come from LDS reads take the in-place
+// form whether or not their global loads are guarded.
+constexpr bool kLdsAsm = CIGN_GEMM_ASM_MFMA;
+
 // MFMAs of one K step. The W tile is the MFMA's first operand and x the
 // second, so D = W x^T: lane l holds output rows (of y) 16r + l%16 and, per
 // 16-column tile f, the four consecutive columns 16f + 4*(l/16) + q.
-template <int MATH, int TN>
+template <int MATH, int TN, bool ASM = false>
 __device__ __forceinline__ void mma_step(const XStep& a, const typename Op<MATH>::T* Bs, int lane,
                                          f32x4 (&acc)[2][TN]) {
   constexpr int S = lds_stride<MATH>();
@@ -319,10 +387,17 @@ __device__ __forceinline__ void mma_step(const XStep& a, const typename Op<MATH>
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
           const float* xv = a.v[r] + 4 * h;
-          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.x, xv[0], acc[r][f], 0, 0, 0);
-          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.y, xv[1], acc[r][f], 0, 0, 0);
-          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.z, xv[2], acc[r][f], 0, 0, 0);
-          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.w, xv[3], acc[r][f], 0, 0, 0);
+          if constexpr (ASM) {
+            mfma_f32_acc(acc[r][f], wb.x, xv[0]);
+            mfma_f32_acc(acc[r][f], wb.y, xv[1]);
+            mfma_f32_acc(acc[r][f], wb.z, xv[2]);
+            mfma_f32_acc(acc[r][f], wb.w, xv[3]);
+          } else {
+            acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.x, xv[0], acc[r][f], 0, 0, 0);
+            acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.y, xv[1], acc[r][f], 0, 0, 0);
+            acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.z, xv[2], acc[r][f], 0, 0, 0);
+            acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(wb.w, xv[3], acc[r][f], 0, 0, 0);
+          }
         }
       }
   }
@@ -471,7 +546,7 @@ __device__ __forceinline__ void epilogue_swapped(const GemmArgs& g, f32x4 (&acc)
 // The K loop keeps the x fragments of the next two K steps in flight (a
 // two-slot register ring per wavefront) and double-buffers the shared W tile
 // in LDS.
-template <typename TX, int MATH, int BN, int EPI>
+template <typename TX, int MATH, int BN, int EPI, bool FULL>
 __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs g, int nrt, int nct) {
   using T = typename Op<MATH>::T;
   constexpr int S = lds_stride<MATH>();
@@ -492,30 +567,41 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs g, int nrt, 
     for (int f = 0; f < TN; ++f) acc[r][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   const int nk = (g.K + kBK - 1) / kBK;
+  constexpr bool ASM = FULL && CIGN_GEMM_ASM_MFMA && MATH == kMathF32;
+  if constexpr (ASM) mfma_settle(acc);
   XStep a0, a1;
   WStage<MATH, BN> wst;
-  load_xstep<TX, MATH>(g, x, row0, 0, lane, a0);
-  if (nk > 1) load_xstep<TX, MATH>(g, x, row0, kBK, lane, a1);
-  wst.load(g, n0, 0);
+  // With FULL every prefetch is issued, past the end as a repeat of the last
+  // step (in bounds, unused), so no load sits behind a branch and each wait
+  // covers only the loads it needs.
+  const int last = (nk - 1) * kBK;
+  load_xstep<TX, MATH, FULL>(g, x, row0, 0, lane, a0);
+  if (FULL || nk > 1) load_xstep<TX, MATH, FULL>(g, x, row0, min(kBK, last), lane, a1);
+  wst.template load<FULL>(g, n0, 0);
   wst.store(Bs[0]);
   __syncthreads();
   int buf = 0;
   for (int s = 0; s < nk; s += 2) {
-    if (s + 1 < nk) wst.load(g, n0, (s + 1) * kBK);
-    mma_step<MATH, TN>(a0, Bs[buf], lane, acc);
-    if (s + 2 < nk) load_xstep<TX, MATH>(g, x, row0, (s + 2) * kBK, lane, a0);
-    if (s + 1 < nk) wst.store(Bs[buf ^ 1]);
+    if (FULL || s + 1 < nk) wst.template load<FULL>(g, n0, min((s + 1) * kBK, last));
+    // keep the W loads ahead of the MFMAs (the scheduler sinks them below,
+    // exposing their latency at the LDS store)
+    __builtin_amdgcn_sched_barrier(0);
+    mma_step<MATH, TN, ASM>(a0, Bs[buf], lane, acc);
+    if (FULL || s + 2 < nk) load_xstep<TX, MATH, FULL>(g, x, row0, min((s + 2) * kBK, last), lane, a0);
+    if (FULL || s + 1 < nk) wst.store(Bs[buf ^ 1]);
     __syncthreads();
     buf ^= 1;
     if (s + 1 >= nk) break;  // uniform
-    if (s + 2 < nk) wst.load(g, n0, (s + 2) * kBK);
-    mma_step<MATH, TN>(a1, Bs[buf], lane, acc);
-    if (s + 3 < nk) load_xstep<TX, MATH>(g, x, row0, (s + 3) * kBK, lane, a1);
-    if (s + 2 < nk) wst.store(Bs[buf ^ 1]);
+    if (FULL || s + 2 < nk) wst.template load<FULL>(g, n0, min((s + 2) * kBK, last));
+    __builtin_amdgcn_sched_barrier(0);
+    mma_step<MATH, TN, ASM>(a1, Bs[buf], lane, acc);
+    if (FULL || s + 3 < nk) load_xstep<TX, MATH, FULL>(g, x, row0, min((s + 3) * kBK, last), lane, a1);
+    if (FULL || s + 2 < nk) wst.store(Bs[buf ^ 1]);
     __syncthreads();
     buf ^= 1;
   }
 
+  if constexpr (ASM) mfma_settle(acc);
   epilogue_swapped<EPI, TN>(g, acc, row0, n0, lane);
 }
 
@@ -535,9 +621,10 @@ struct LdsStage {
   float a[A_CHUNKS][XC];
   float b[B_CHUNKS][4];
 
+  template <bool FULL = false>
   __device__ __forceinline__ void load(const GemmArgs& g, const TX* x, int64_t m0, int n0, int k0) {
     constexpr int ACPR = kBK / XC;  // chunks per A row
-    if (fast_step(g, k0)) {
+    if (fast_step<FULL>(g, k0)) {
       // Rows past M (N) read row M-1 (N-1); their outputs are never stored.
 #pragma unroll
       for (int i = 0; i < A_CHUNKS; ++i) {
@@ -596,9 +683,9 @@ struct LdsStage {
 // MFMAs of one K step on the LDS tiles: the wave's 2 row tiles x TN column
 // tiles, W as the first operand (the swapped-operand accumulator layout of
 // epilogue_swapped).
-template <int MATH, int TN>
+template <int MATH, int TN, bool ASM = false>
 __device__ __forceinline__ void mma_step_lds(const typename Op<MATH>::T* As, const typename Op<MATH>::T* Bs, int wave,
-                                         int lane, f32x4 (&acc)[2][TN]) {
+                                             int lane, f32x4 (&acc)[2][TN]) {
   constexpr int S = lds_stride<MATH>();
   const int rl = lane & 15, ks = lane >> 4;
   if constexpr (MATH == kMathBF16) {
@@ -612,7 +699,10 @@ __device__ __forceinline__ void mma_step_lds(const typename Op<MATH>::T* As, con
       for (int f = 0; f < TN; ++f) {
         const bf16x8 b = *reinterpret_cast<const bf16x8*>(Bs + (16 * f + rl) * S + hk + ks * 8);
 #pragma unroll
-        for (int r = 0; r < 2; ++r) acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, a[r], acc[r][f], 0, 0, 0);
+        for (int r = 0; r < 2; ++r) {
+          if constexpr (ASM) mfma_bf16_acc(acc[r][f], b, a[r]);
+          else acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, a[r], acc[r][f], 0, 0, 0);
+        }
       }
     }
   } else {
@@ -640,7 +730,7 @@ __device__ __forceinline__ void mma_step_lds(const typename Op<MATH>::T* As, con
 }
 
 
-template <typename TX, int MATH, int BN, int EPI>
+template <typename TX, int MATH, int BN, int EPI, bool FULL>
 __global__ __launch_bounds__(kThreads) void gemm_nt_lds_kernel(GemmArgs g, int nrt, int nct) {
   using T = typename Op<MATH>::T;
   constexpr int S = lds_stride<MATH>();
@@ -661,20 +751,27 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_lds_kernel(GemmArgs g, int n
 #pragma unroll
     for (int f = 0; f < TN; ++f) acc[r][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+  constexpr bool ASM = FULL && CIGN_GEMM_ASM_MFMA && MATH == kMathBF16;
+  if constexpr (ASM) mfma_settle(acc);
   LdsStage<TX, MATH, BN> regs;
-  regs.load(g, x, m0, n0, 0);
+  regs.template load<FULL>(g, x, m0, n0, 0);
   regs.store(As[0], Bs[0]);
   __syncthreads();
   int buf = 0;
   for (int k0 = 0; k0 < g.K; k0 += kBK) {
+    // with FULL the last step loads itself again (in bounds, unused): no
+    // load behind a branch
     const bool more = k0 + kBK < g.K;
-    if (more) regs.load(g, x, m0, n0, k0 + kBK);
-    mma_step_lds<MATH, TN>(As[buf], Bs[buf], wave, lane, acc);
-    if (more) regs.store(As[buf ^ 1], Bs[buf ^ 1]);
+    if (FULL || more) regs.template load<FULL>(g, x, m0, n0, more ? k0 + kBK : k0);
+    __builtin_amdgcn_sched_barrier(0);  // the next step's loads ahead of the MFMAs,
+    mma_step_lds<MATH, TN, ASM>(As[buf], Bs[buf], wave, lane, acc);
+    __builtin_amdgcn_sched_barrier(0);  // and the MFMAs ahead of the wait for them
+    if (FULL || more) regs.store(As[buf ^ 1], Bs[buf ^ 1]);
     __syncthreads();
     buf ^= 1;
   }
 
+  if constexpr (ASM) mfma_settle(acc);
   epilogue_swapped<EPI, TN>(g, acc, m0 + wave * kRowsPerWave, n0, lane);
 }
 
@@ -861,6 +958,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(const float* gy, const 
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (kLdsAsm) mfma_settle(acc);
 
   WgStage<MATH> sg, sx;
   sg.load(gy, N, m0, m1, n0, N, vec);
@@ -885,7 +983,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(const float* gy, const 
       for (int i = 0; i < 4; ++i) {
         const bf16x8 gb = *reinterpret_cast<const bf16x8*>(G + Lay::frag(wn + 16 * i + rl, ks));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gb, xb[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 4; ++j) mma_bf16<kLdsAsm>(acc[i][j], gb, xb[j]);
       }
     } else {
 #pragma unroll
@@ -898,12 +996,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(const float* gy, const 
         for (int i = 0; i < 4; ++i) {
           const float4 gb = *reinterpret_cast<const float4*>(G + Lay::frag(wn + 16 * i + rl, 4 * h + ks));
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.x, xb[j].x, acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.y, xb[j].y, acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.z, xb[j].z, acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.w, xb[j].w, acc[i][j], 0, 0, 0);
-          }
+          for (int j = 0; j < 4; ++j) mma_f32x4<kLdsAsm>(acc[i][j], gb, xb[j]);
         }
       }
     }
@@ -914,6 +1007,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(const float* gy, const 
     __syncthreads();
     buf ^= 1;
   }
+  if constexpr (kLdsAsm) mfma_settle(acc);
   // lane holds grad_W rows n = n0 + wn + 16i + 4*(lane/16) + q of column
   // k = k0 + wk + 16j + lane%16
   float* out = part + static_cast<int64_t>(cy) * N * K;
@@ -1153,7 +1247,7 @@ __device__ __forceinline__ void mma_step_pp(const typename Op<MATH>::T* As, cons
     for (int f = 0; f < TNW; ++f) {
       const bf16x8 b = *reinterpret_cast<const bf16x8*>(Bs + (nb + 16 * f + rl) * S + ks * 8);
 #pragma unroll
-      for (int r = 0; r < RT; ++r) acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, a[r], acc[r][f], 0, 0, 0);
+      for (int r = 0; r < RT; ++r) mma_bf16<kLdsAsm>(acc[r][f], b, a[r]);
     }
   } else {
 #pragma unroll
@@ -1165,12 +1259,7 @@ __device__ __forceinline__ void mma_step_pp(const typename Op<MATH>::T* As, cons
       for (int f = 0; f < TNW; ++f) {
         const float4 b = *reinterpret_cast<const float4*>(Bs + (nb + 16 * f + rl) * S + hk + ks * 4);
 #pragma unroll
-        for (int r = 0; r < RT; ++r) {
-          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(b.x, a[r].x, acc[r][f], 0, 0, 0);
-          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(b.y, a[r].y, acc[r][f], 0, 0, 0);
-          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(b.z, a[r].z, acc[r][f], 0, 0, 0);
-          acc[r][f] = __builtin_amdgcn_mfma_f32_16x16x4f32(b.w, a[r].w, acc[r][f], 0, 0, 0);
-        }
+        for (int r = 0; r < RT; ++r) mma_f32x4<kLdsAsm>(acc[r][f], b, a[r]);
       }
     }
   }
@@ -1208,6 +1297,7 @@ __global__ __launch_bounds__(kThreads) void pack_proj_fwd_kernel(GemmArgs g, Pac
   for (int r = 0; r < RT; ++r)
 #pragma unroll
     for (int f = 0; f < TNW; ++f) acc[r][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (kLdsAsm) mfma_settle(acc);
 
   const int jq = a.D / 16;
   const int steps = a.K * jq;
@@ -1234,6 +1324,7 @@ __global__ __launch_bounds__(kThreads) void pack_proj_fwd_kernel(GemmArgs g, Pac
     __syncthreads();
     buf ^= 1;
   }
+  if constexpr (kLdsAsm) mfma_settle(acc);
   epilogue_swapped<kEpiGamma, TNW, RT>(g, acc, m0, n0 + wave * TNW * 16, lane);
 }
 
@@ -1542,6 +1633,7 @@ __global__ __launch_bounds__(kThreads) void pack_wgrad_kernel(const float* gy, P
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (kLdsAsm) mfma_settle(acc);
 
   WgStage<MATH> sg;
   PackWgStage<MATH> sx;
@@ -1567,7 +1659,7 @@ __global__ __launch_bounds__(kThreads) void pack_wgrad_kernel(const float* gy, P
       for (int i = 0; i < 4; ++i) {
         const bf16x8 gb = *reinterpret_cast<const bf16x8*>(G + Lay::frag(wn + 16 * i + rl, ks));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(gb, xb[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 4; ++j) mma_bf16<kLdsAsm>(acc[i][j], gb, xb[j]);
       }
     } else {
 #pragma unroll
@@ -1580,12 +1672,7 @@ __global__ __launch_bounds__(kThreads) void pack_wgrad_kernel(const float* gy, P
         for (int i = 0; i < 4; ++i) {
           const float4 gb = *reinterpret_cast<const float4*>(G + Lay::frag(wn + 16 * i + rl, 4 * h + ks));
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.x, xb[j].x, acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.y, xb[j].y, acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.z, xb[j].z, acc[i][j], 0, 0, 0);
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(gb.w, xb[j].w, acc[i][j], 0, 0, 0);
-          }
+          for (int j = 0; j < 4; ++j) mma_f32x4<kLdsAsm>(acc[i][j], gb, xb[j]);
         }
       }
     }
@@ -1598,6 +1685,7 @@ __global__ __launch_bounds__(kThreads) void pack_wgrad_kernel(const float* gy, P
   }
   // lane holds grad_Wp rows n = n0 + wn + 16i + 4*(lane/16) + q of tile
   // column wk + 16j + lane%16: G column kk*2D + (wk/64)*D + j0 + 16j + lane%16
+  if constexpr (kLdsAsm) mfma_settle(acc);
   float* out = part + static_cast<int64_t>(cy) * N * KW;
   const int gbase = kk * 2 * a.D + (wk / 64) * a.D + j0;
 #pragma unroll
@@ -1632,6 +1720,22 @@ inline int pick_bn(int N, int C, int math) {
   return bn;
 }
 
+template <typename TX, int MATH, int EPI, bool FULL>
+void launch_nt_bn(hipStream_t st, const GemmArgs& g, int bn, int64_t blocks, int nrt, int nct) {
+  const dim3 grid(static_cast<unsigned>(blocks));
+  if constexpr (MATH == kMathBF16) {
+    if (bn == 64)
+      hipLaunchKernelGGL((gemm_nt_lds_kernel<TX, MATH, 64, EPI, FULL>), grid, dim3(kThreads), 0, st, g, nrt, nct);
+    else
+      hipLaunchKernelGGL((gemm_nt_lds_kernel<TX, MATH, 128, EPI, FULL>), grid, dim3(kThreads), 0, st, g, nrt, nct);
+  } else {
+    if (bn == 64)
+      hipLaunchKernelGGL((gemm_nt_kernel<TX, MATH, 64, EPI, FULL>), grid, dim3(kThreads), 0, st, g, nrt, nct);
+    else
+      hipLaunchKernelGGL((gemm_nt_kernel<TX, MATH, 128, EPI, FULL>), grid, dim3(kThreads), 0, st, g, nrt, nct);
+  }
+}
+
 template <typename TX, int MATH, int EPI>
 int launch_nt(hipStream_t st, const GemmArgs& g, int bn) {
   const int nrt = static_cast<int>((g.M + kBM - 1) / kBM);
@@ -1639,21 +1743,9 @@ int launch_nt(hipStream_t st, const GemmArgs& g, int bn) {
   const int64_t blocks = static_cast<int64_t>(nrt) * nct;
   if (blocks == 0) return kOk;
   if (blocks > 0x7fffffff) return set_error(kInvalid, "cign linear: too many tiles");
-  if constexpr (MATH == kMathBF16) {
-    if (bn == 64)
-      hipLaunchKernelGGL((gemm_nt_lds_kernel<TX, MATH, 64, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
-                         0, st, g, nrt, nct);
-    else
-      hipLaunchKernelGGL((gemm_nt_lds_kernel<TX, MATH, 128, EPI>), dim3(static_cast<unsigned>(blocks)),
-                         dim3(kThreads), 0, st, g, nrt, nct);
-  } else {
-    if (bn == 64)
-      hipLaunchKernelGGL((gemm_nt_kernel<TX, MATH, 64, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
-                         st, g, nrt, nct);
-    else
-      hipLaunchKernelGGL((gemm_nt_kernel<TX, MATH, 128, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
-                         0, st, g, nrt, nct);
-  }
+  // every K step takes the unguarded loads
+  if (g.vec && g.K % kBK == 0) launch_nt_bn<TX, MATH, EPI, true>(st, g, bn, blocks, nrt, nct);
+  else launch_nt_bn<TX, MATH, EPI, false>(st, g, bn, blocks, nrt, nct);
   return check_launch("cign linear");
 }
 
