@@ -950,6 +950,9 @@ def measure_layer(torch, scale: bool, dtype: str, steps: int, warmup: int, eager
     layer_own_gbs = B["layer" + gkey] / (ms * 1e-3) / 1e9
 
     checks = invariants(torch, w, ext, plan, H, C, D, dt) if scale else None
+    projected = None
+    if not scale and not eager:
+        projected = projected_layer(torch, w, dtype, steps, warmup, plan, X, (g1, g2, g3), capture, ev)
 
     line = {
         "metric": "GAT+multihop layer fwd+bwd edges/sec; achieved HBM GB/s as % of roofline",
@@ -986,7 +989,66 @@ def measure_layer(torch, scale: bool, dtype: str, steps: int, warmup: int, eager
     }
     if checks is not None:
         line["invariants"] = checks
+    if projected is not None:
+        line["c2_with_projection"] = projected
     return line, w
+
+
+def projected_layer(torch, w, dtype, steps, warmup, plan, X, grads, capture, ev):
+    """The c2 layer as BASELINE config 2 states it, the GAT's input 300-dim
+    features projected to 4 heads x 16 (the GAT lin on MFMA, fp32 or bf16
+    autocast, with the attention logits; backward: the weight and logit
+    gradients, the input being data) plus the same 3-hop SpMM, one step per
+    HIP graph replay, timed as the headline step. The projection runs as
+    CompatibleCollapsedFusedGATConv runs it (lin_gat's forward and backward,
+    called without autograd so the step captures as one graph)."""
+    from cign_amd.lin_gat import _LinGatFn
+
+    dev = torch.device("cuda:0")
+    H, C, K_in = 4, 16, 300
+    (rowptr, col), (row, colptr), perm = w.gat_graph
+    gen = torch.Generator(device="cpu").manual_seed(1)
+    x300 = torch.randn(w.n, K_in, generator=gen).to(dev)
+    Wl = (torch.randn(H * C, K_in, generator=gen) / K_in ** 0.5).to(dev)
+    att_s = (torch.randn(1, H, C, generator=gen) * 0.1).to(dev)
+    att_d = (torch.randn(1, H, C, generator=gen) * 0.1).to(dev)
+    bias = (torch.randn(C, generator=gen) * 0.1).to(dev)
+    gy = torch.randn(w.n, C, generator=gen).to(dev)
+    math = 1 if dtype == "bf16" else 0
+
+    class Ctx:
+        needs_input_grad = (False, True, True, True, True) + (False,) * 10
+
+        def save_for_backward(self, *t):
+            self.saved_tensors = t
+
+    def step():
+        ctx = Ctx()
+        _LinGatFn.forward(ctx, x300, Wl, att_s, att_d, bias, rowptr, col, colptr, row, perm, 0.2, 0.0, 0, H, math)
+        plan.forward3(X)
+        _LinGatFn.backward(ctx, gy)
+        plan.backward3(*grads)
+
+    for _ in range(max(1, warmup)):
+        step()
+    torch.cuda.synchronize()
+    replay = capture(step).replay
+    for _ in range(max(1, warmup)):
+        replay()
+    torch.cuda.synchronize()
+    a0, a1 = ev(), ev()
+    t0 = time.perf_counter()
+    a0.record()
+    for _ in range(steps):
+        replay()
+    a1.record()
+    torch.cuda.synchronize()
+    ms = 1e3 * (time.perf_counter() - t0) / steps
+    E = w.nnz_gat
+    return {"ms_per_step": round(ms, 5), "gpu_ms_per_step": round(a0.elapsed_time(a1) / steps, 5),
+            "edges_per_s": E / (ms * 1e-3),
+            "projection": f"GAT lin {K_in} -> {H} x {C} on MFMA ({'bf16 autocast' if math else 'fp32'}) with the "
+                          "attention logits, forward + weight and logit gradients"}
 
 
 

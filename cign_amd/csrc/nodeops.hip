@@ -101,14 +101,19 @@ int zero_outputs(hipStream_t st, float* a, int na, float* b, int nbv, const char
 int launch_colsum(hipStream_t st, const float* part, int nb, int width, int quantities, float* out0, float* out1,
                   const char* who) {
   if (width <= 0) return kOk;
-  // Three fixed-order paths: outputs wider than 4096 columns over at most 128
-  // partial rows (weight gradients) take colsum_wide_kernel, one thread per
-  // four columns walking the rows in order; narrow outputs over at least 256
-  // partial rows (LayerNorm and bias gradients at large n) take 16 columns x
-  // 64 slices, so more workgroups share the rows; the rest 64 columns x 16
-  // slices.
+  // Three fixed-order paths: outputs of at least 65536 columns over at most
+  // 128 partial rows (weight gradients) take colsum_wide_kernel, one thread
+  // per four columns walking the rows in order (16K threads and more);
+  // outputs of at most 4096 columns over at least 256 partial rows
+  // (LayerNorm and bias gradients at large n), and mid-width outputs (the
+  // 64 x 300 weight gradient of the c2 projection: 4800 threads of the wide
+  // kernel walking 128 rows took 26 us), take 16 columns x 64 slices, so more
+  // workgroups share the rows; the rest 64 columns x 16 slices.
   const bool vec = width % 4 == 0 && aligned16(part) && aligned16(out0) && (!out1 || aligned16(out1));
-  if (width > 4096 && nb <= 128 && vec)
+  if (width > 4096 && width < 65536 && nb >= 16)
+    hipLaunchKernelGGL(colsum_kernel<16>, dim3((width + 15) / 16, quantities), dim3(kColsumThreads), 0, st, part, nb,
+                       width, out0, out1);
+  else if (width > 4096 && nb <= 128 && vec)
     hipLaunchKernelGGL(colsum_wide_kernel, dim3((width / 4 + kBlock - 1) / kBlock, quantities), dim3(kBlock), 0, st,
                        part, nb, width, out0, out1);
   else if (width <= 4096 && nb >= 256)
