@@ -1577,34 +1577,37 @@ template <int MATH>
 struct PackWgStage : WgStage<MATH> {
   // WgStage's register layout: row tid / 8, tile column quads (tid % 8 + 8 i) * 4
   using WgStage<MATH>::v;
+  // The raw inputs of a step, loaded before the current step's MFMAs and
+  // packed after them (finish), so the loads' latency overlaps the MFMAs.
+  float h[2][4], c[2][4], th[2][4], tc[2][4];
+  float al;
+  bool ok;
 
   __device__ __forceinline__ void load_pack(const PackArgs& a, int64_t m0, int64_t m1, int kk, int j0) {
     const int r = threadIdx.x / 8;
     const int64_t m = m0 + r;
-    if (m >= m1) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[i][q] = 0.0f;
-      return;
-    }
-    const float al = a.alpha[m * a.a_stride + kk];
-    const float* pk = a.P[kk] + m * a.p_stride;
+    ok = m < m1;
+    const int64_t mm = ok ? m : m1 - 1;  // a row past m1 reads row m1 - 1 (m0 < m1), packed as zeros
+    al = a.alpha[mm * a.a_stride + kk];
+    const float* pk = a.P[kk] + mm * a.p_stride;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int j = j0 + ((threadIdx.x % 8) + 8 * i) * 4;
-      float h[4], c[4], th[4], tc[4];
-      gload_fast<float, 4>(a.H + m * a.D, j, h);
-      gload_fast<float, 4>(a.C + m * a.D, j, c);
-      gload_fast<float, 4>(pk, j, th);
-      gload_fast<float, 4>(pk, a.D + j, tc);
+      gload_fast<float, 4>(a.H + mm * a.D, j, h[i]);
+      gload_fast<float, 4>(a.C + mm * a.D, j, c[i]);
+      gload_fast<float, 4>(pk, j, th[i]);
+      gload_fast<float, 4>(pk, a.D + j, tc[i]);
+    }
+  }
+  __device__ __forceinline__ void finish(int mode) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const packk::DW e = packk::interact(h[q] * tc[q], c[q] * th[q], a.mode);
-        v[i][q] = al * e.Wv;
-        v[i + 2][q] = al * e.Dv;
+        const packk::DW e = packk::interact(h[i][q] * tc[i][q], c[i][q] * th[i][q], mode);
+        v[i][q] = ok ? al * e.Wv : 0.0f;
+        v[i + 2][q] = ok ? al * e.Dv : 0.0f;
       }
-    }
   }
 };
 
@@ -1639,6 +1642,7 @@ __global__ __launch_bounds__(kThreads) void pack_wgrad_kernel(const float* gy, P
   PackWgStage<MATH> sx;
   sg.load(gy, N, m0, m1, n0, N, true);
   sx.load_pack(a, m0, m1, kk, j0);
+  sx.finish(a.mode);
   sg.store(Gs[0]);
   sx.store(Xs[0]);
   __syncthreads();
@@ -1649,6 +1653,7 @@ __global__ __launch_bounds__(kThreads) void pack_wgrad_kernel(const float* gy, P
       sg.load(gy, N, mb + kWgM, m1, n0, N, true);
       sx.load_pack(a, mb + kWgM, m1, kk, j0);
     }
+    __builtin_amdgcn_sched_barrier(0);  // the next step's loads ahead of the MFMAs
     const T* G = Gs[buf];
     const T* X = Xs[buf];
     if constexpr (MATH == kMathBF16) {
@@ -1676,8 +1681,10 @@ __global__ __launch_bounds__(kThreads) void pack_wgrad_kernel(const float* gy, P
         }
       }
     }
+    __builtin_amdgcn_sched_barrier(0);  // and its packing after them
     if (more) {
       sg.store(Gs[buf ^ 1]);
+      sx.finish(a.mode);
       sx.store(Xs[buf ^ 1]);
     }
     __syncthreads();
