@@ -590,8 +590,21 @@ int attn_fwd_impl(const char* who, void* stream, int64_t n, int32_t H, int32_t C
     return set_error(kInvalid, "%s: bad shape n=%lld H=%d C=%d", who, static_cast<long long>(n), H, C);
   if (n == 0) return kOk;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int W = chunk_width(C, {x, att_src, att_dst});
   const int64_t rows = n * H;
+  if constexpr (std::is_same_v<TX, bf16h>) {
+    // bf16 rows eight values (16 bytes) per lane
+    if (C % 8 == 0 && aligned16(x) && aligned16(att_src) && aligned16(att_dst)) {
+      const bf16* xb = reinterpret_cast<const bf16*>(x);
+      const int rc = with_geo(C / 8, [&](auto LC, auto VC) {
+        constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
+        hipLaunchKernelGGL((attn_fwd_kernel<L, V, 8, bf16>), dim3(grid_for(rows, Geo<L>::RPB)), dim3(kBlock), 0, st,
+                           rows, H, C, xb, att_src, att_dst, alpha_src, alpha_dst);
+        return check_launch(who);
+      });
+      if (rc >= 0) return rc;
+    }
+  }
+  const int W = chunk_width(C, {x, att_src, att_dst});
   const int rc = with_geo(C / W, [&](auto LC, auto VC) {
     constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
     const int grid = grid_for(rows, Geo<L>::RPB);
@@ -620,6 +633,26 @@ int attn_bwd_impl(const char* who, void* stream, int64_t n, int32_t H, int32_t C
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nb = colsum_blocks(n);
   float* part = static_cast<float*>(workspace);
+  if constexpr (std::is_same_v<TX, bf16h>) {
+    // bf16 rows eight values (16 bytes) per lane
+    if (n > 0 && C % 8 == 0 && aligned16(x) && aligned16(att_src) && aligned16(att_dst) && aligned16(grad_x) &&
+        (!grad_x_in || aligned16(grad_x_in))) {
+      const bf16* xb = reinterpret_cast<const bf16*>(x);
+      const int qf8 = F / 8;
+      auto launch8 = [&](auto LC, auto VC) {
+        constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
+        const dim3 grid(nb, (qf8 + L * V - 1) / (L * V));
+        hipLaunchKernelGGL((attn_bwd_kernel<L, V, 8, bf16>), grid, dim3(kBlock), 0, st, n, H, C, grad_src, grad_dst,
+                           xb, att_src, att_dst, grad_x_in, grad_x, part, nb);
+        return check_launch(who);
+      };
+      // rows of more than 128 chunks take column tiles of 128 (two chunks per
+      // lane): four chunks of eight values held 197 VGPRs, two waves per SIMD
+      const int rc = qf8 > 128 ? launch8(IC<64>(), IC<2>()) : with_geo(qf8, launch8);
+      if (rc) return rc;
+      return launch_colsum(st, part, nb, F, 2, grad_att_src, grad_att_dst, who);
+    }
+  }
   const int W = grad_x_in ? chunk_width(C, {x, att_src, att_dst, grad_x, grad_x_in})
                           : chunk_width(C, {x, att_src, att_dst, grad_x});
   const int qf = F / W;
