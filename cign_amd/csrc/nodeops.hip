@@ -603,6 +603,18 @@ int attn_fwd_impl(const char* who, void* stream, int64_t n, int32_t H, int32_t C
       });
       if (rc >= 0) return rc;
     }
+  } else {
+    // fp32 rows of at least 128 values eight per lane (two 16-byte loads):
+    // two rows per wavefront instead of one
+    if (C % 8 == 0 && C >= 128 && aligned16(x) && aligned16(att_src) && aligned16(att_dst)) {
+      const int rc = with_geo(C / 8, [&](auto LC, auto VC) {
+        constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
+        hipLaunchKernelGGL((attn_fwd_kernel<L, V, 8, float>), dim3(grid_for(rows, Geo<L>::RPB)), dim3(kBlock), 0,
+                           st, rows, H, C, x, att_src, att_dst, alpha_src, alpha_dst);
+        return check_launch(who);
+      });
+      if (rc >= 0) return rc;
+    }
   }
   const int W = chunk_width(C, {x, att_src, att_dst});
   const int rc = with_geo(C / W, [&](auto LC, auto VC) {
