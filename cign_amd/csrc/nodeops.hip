@@ -297,7 +297,14 @@ __global__ __launch_bounds__(kBlock) void head_silu_bwd_kernel(int64_t n, int H,
 // ---------------------------------------------------------------------------
 template <int W>
 __device__ __forceinline__ void store_mask(uint8_t* m, const bool (&k)[W]) {
-  if constexpr (W == 4) {
+  if constexpr (W == 8) {
+    uint32_t v[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      v[h] = (k[4 * h] ? 1u : 0u) | (k[4 * h + 1] ? 1u << 8 : 0u) | (k[4 * h + 2] ? 1u << 16 : 0u) |
+             (k[4 * h + 3] ? 1u << 24 : 0u);
+    *reinterpret_cast<uint2*>(m) = make_uint2(v[0], v[1]);
+  } else if constexpr (W == 4) {
     const uint32_t v = (k[0] ? 1u : 0u) | (k[1] ? 1u << 8 : 0u) | (k[2] ? 1u << 16 : 0u) | (k[3] ? 1u << 24 : 0u);
     *reinterpret_cast<uint32_t*>(m) = v;
   } else {
@@ -307,7 +314,14 @@ __device__ __forceinline__ void store_mask(uint8_t* m, const bool (&k)[W]) {
 
 template <int W>
 __device__ __forceinline__ void load_mask(const uint8_t* m, bool (&k)[W]) {
-  if constexpr (W == 4) {
+  if constexpr (W == 8) {
+    const uint2 v = *reinterpret_cast<const uint2*>(m);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      k[w] = ((v.x >> (8 * w)) & 0xffu) != 0;
+      k[4 + w] = ((v.y >> (8 * w)) & 0xffu) != 0;
+    }
+  } else if constexpr (W == 4) {
     const uint32_t v = *reinterpret_cast<const uint32_t*>(m);
 #pragma unroll
     for (int w = 0; w < 4; ++w) k[w] = ((v >> (8 * w)) & 0xffu) != 0;
@@ -572,6 +586,10 @@ inline int chunk_width(int width, std::initializer_list<const void*> ptrs) {
   return 4;
 }
 
+// Rows of at least 128 aligned floats: eight values per lane (two 16-byte
+// accesses), so a wavefront holds two rows of 256 instead of one.
+inline int wide_chunks(int width, int w) { return w == 4 && width % 8 == 0 && width >= 128 ? 8 : w; }
+
 int check_rows(const char* who, int64_t n, int D) {
   if (n < 0) return set_error(kInvalid, "%s: negative row count", who);
   if (D < 1 || D > 256) return set_error(kInvalid, "%s: requires 1<=D<=256, got %d", who, D);
@@ -789,7 +807,8 @@ static int ln_fwd(int mode, void* stream, int64_t n, int32_t D, const float* x, 
   if (!(p >= 0.0f && p < 1.0f)) return set_error(kInvalid, "%s: dropout_p must be in [0,1)", who);
   if (n == 0) return kOk;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int W = chunk_width(D, {x, x2 ? x2 : x, w, b, y, mask ? static_cast<const void*>(mask) : x, ycat ? ycat : y});
+  const int W = wide_chunks(D, chunk_width(D, {x, x2 ? x2 : x, w, b, y, mask ? static_cast<const void*>(mask) : x,
+                                                ycat ? ycat : y}));
   return with_geo(D / W, [&](auto LC, auto VC) {
     constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
     const int grid = grid_for(n, Geo<L>::RPB);
@@ -797,11 +816,11 @@ static int ln_fwd(int mode, void* stream, int64_t n, int32_t D, const float* x, 
   hipLaunchKernelGGL((ln_fwd_kernel<M, L, V, WW>), dim3(grid), dim3(kBlock), 0, st, n, D, x, x2, w, b, p, eps, seed, \
                      y, mean, rstd, mask, ycat)
     if (mode == 0) {
-      if (W == 4) CIGN_LN_FWD(0, 4); else CIGN_LN_FWD(0, 1);
+      if (W == 8) CIGN_LN_FWD(0, 8); else if (W == 4) CIGN_LN_FWD(0, 4); else CIGN_LN_FWD(0, 1);
     } else if (mode == 1) {
-      if (W == 4) CIGN_LN_FWD(1, 4); else CIGN_LN_FWD(1, 1);
+      if (W == 8) CIGN_LN_FWD(1, 8); else if (W == 4) CIGN_LN_FWD(1, 4); else CIGN_LN_FWD(1, 1);
     } else {
-      if (W == 4) CIGN_LN_FWD(2, 4); else CIGN_LN_FWD(2, 1);
+      if (W == 8) CIGN_LN_FWD(2, 8); else if (W == 4) CIGN_LN_FWD(2, 4); else CIGN_LN_FWD(2, 1);
     }
 #undef CIGN_LN_FWD
     return check_launch(who);
@@ -819,19 +838,19 @@ static int ln_bwd(int mode, void* stream, int64_t n, int32_t D, const float* gy,
   const int nb = colsum_blocks(n);
   float* part = static_cast<float*>(workspace);
   if (n > 0) {
-    const int W = chunk_width(D, {gy, x, x2 ? x2 : x, w, dx, mask ? static_cast<const void*>(mask) : x,
-                                  gcat ? gcat : gy, dx2 ? dx2 : dx});
+    const int W = wide_chunks(D, chunk_width(D, {gy, x, x2 ? x2 : x, w, dx, mask ? static_cast<const void*>(mask) : x,
+                                                 gcat ? gcat : gy, dx2 ? dx2 : dx}));
     rc = with_geo(D / W, [&](auto LC, auto VC) {
       constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
 #define CIGN_LN_BWD(M, WW)                                                                                           \
   hipLaunchKernelGGL((ln_bwd_kernel<M, L, V, WW>), dim3(nb), dim3(kBlock), 0, st, n, D, gy, x, x2, w, mean, rstd, mask, \
                      p, dx, part, nb, gcat, dx2)
       if (mode == 0) {
-        if (W == 4) CIGN_LN_BWD(0, 4); else CIGN_LN_BWD(0, 1);
+        if (W == 8) CIGN_LN_BWD(0, 8); else if (W == 4) CIGN_LN_BWD(0, 4); else CIGN_LN_BWD(0, 1);
       } else if (mode == 1) {
-        if (W == 4) CIGN_LN_BWD(1, 4); else CIGN_LN_BWD(1, 1);
+        if (W == 8) CIGN_LN_BWD(1, 8); else if (W == 4) CIGN_LN_BWD(1, 4); else CIGN_LN_BWD(1, 1);
       } else {
-        if (W == 4) CIGN_LN_BWD(2, 4); else CIGN_LN_BWD(2, 1);
+        if (W == 8) CIGN_LN_BWD(2, 8); else if (W == 4) CIGN_LN_BWD(2, 4); else CIGN_LN_BWD(2, 1);
       }
 #undef CIGN_LN_BWD
       return check_launch(who);
