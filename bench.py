@@ -554,7 +554,14 @@ def run_block(args, torch):
     H0 = torch.randn(n, D, generator=g).to(dev).requires_grad_(True)
     G0 = torch.randn(n, D, generator=g).to(dev)
 
+    params = list(block.parameters())
+
     def step():
+        # gradients produced, not accumulated across steps (zero_grad with
+        # set_to_none, as the training loop does before each backward)
+        for prm in params:
+            prm.grad = None
+        H0.grad = None
         out = block(H0, None, mh, w.gat_graph)
         out.backward(G0)
 
