@@ -50,8 +50,8 @@ _SIGNATURES = {
     "cign_attn_logits_fwd": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P]),
     "cign_attn_logits_bwd": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64]),
     "cign_attn_logits_fwd_bf16": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P]),
-    "cign_attn_logits_bwd_acc": (C.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                                           _I64]),
+    "cign_attn_logits_bwd_acc": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                           _P, _I64]),
     "cign_head_silu_fwd": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P]),
     "cign_head_silu_bwd": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _I64]),
     "cign_dropout_ln_fwd": (C.c_int, [_P, _I64, _I32, _P, _P, _P, _F32, _F32, _U64, _P, _P, _P, _P]),
@@ -75,6 +75,7 @@ _SIGNATURES = {
                                         _P]),
     "cign_linear_bwd_workspace_bytes": (_I64, [_I64, _I32, _I32, _I32]),
     "cign_linear_bwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _I64]),
+    "cign_linear_bwd_bf16gy": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _I64]),
     "cign_pack_proj_fwd_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "cign_pack_proj_fwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _I64, _P, _I64, _P, _P, _P, _P,
                                      _F32, _U64, _P, _P, _P, _P, _I64]),

@@ -859,11 +859,13 @@ struct WgLayout {
 
 template <int MATH>
 struct WgStage {
-  // 128 columns x 32 rows of one operand: 1024 float4, four per thread.
-  // Thread id takes row id / 8 and column quads id % 8 + 8i, so a
-  // wavefront's load covers 8 rows x 128 contiguous bytes.
+  // 128 columns x 32 rows of one operand: 1024 four-value chunks, four per
+  // thread. Thread id takes row id / 8 and column quads id % 8 + 8i, so a
+  // wavefront's load covers 8 rows x 128 contiguous values. The source is
+  // fp32, or bf16 storage (TS = bf16h, four values per 8-byte load).
   float v[4][4];
-  __device__ __forceinline__ void load(const float* src, int64_t ld, int64_t m0, int64_t m1, int c0, int cmax,
+  template <typename TS = float>
+  __device__ __forceinline__ void load(const TS* src, int64_t ld, int64_t m0, int64_t m1, int c0, int cmax,
                                        bool vec) {
     const int r = threadIdx.x / 8;
     const int64_t m = m0 + r;
@@ -874,21 +876,19 @@ struct WgStage {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int c = ((threadIdx.x % 8) + 8 * i) * 4;
-        const float4 t = *reinterpret_cast<const float4*>(src + m * ld + c0 + c);
-        v[i][0] = t.x; v[i][1] = t.y; v[i][2] = t.z; v[i][3] = t.w;
+        Chunk<TS, 4>::load(src + m * ld + c0 + c, v[i]);
       }
       return;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = ((threadIdx.x % 8) + 8 * i) * 4;
-      const float* p = src + (ok ? m : 0) * ld + c0 + c;
+      const TS* p = src + (ok ? m : 0) * ld + c0 + c;
       if (vec && ok && c0 + c + 4 <= cmax) {
-        const float4 t = *reinterpret_cast<const float4*>(p);
-        v[i][0] = t.x; v[i][1] = t.y; v[i][2] = t.z; v[i][3] = t.w;
+        Chunk<TS, 4>::load(p, v[i]);
       } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[i][q] = (ok && c0 + c + q < cmax) ? p[q] : 0.0f;
+        for (int q = 0; q < 4; ++q) v[i][q] = (ok && c0 + c + q < cmax) ? to_f32(p[q]) : 0.0f;
       }
     }
   }
@@ -935,8 +935,10 @@ inline int64_t wg_chunk_count(int64_t M, int64_t target, bool xcd) {
   return xcd && c >= 8 ? (c + 7) / 8 * 8 : c;
 }
 
-template <int MATH>
-__global__ __launch_bounds__(kThreads) void wgrad_kernel(const float* gy, const float* x, int64_t M, int N, int K,
+// gy: fp32, or bf16 storage (TG = bf16h: a gradient the caller has rounded to
+// bf16, as bf16 math rounds it anyway).
+template <int MATH, typename TG = float>
+__global__ __launch_bounds__(kThreads) void wgrad_kernel(const TG* gy, const float* x, int64_t M, int N, int K,
                                                          int64_t chunk, int nchunks, int ntk, bool vec, float* part) {
   constexpr bool kXcd = MATH == kMathBF16;
   using T = typename Op<MATH>::T;
@@ -961,7 +963,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(const float* gy, const 
   if constexpr (kLdsAsm) mfma_settle(acc);
 
   WgStage<MATH> sg, sx;
-  sg.load(gy, N, m0, m1, n0, N, vec);
+  sg.template load<TG>(gy, N, m0, m1, n0, N, vec);
   sx.load(x, K, m0, m1, k0, K, vec);
   sg.store(Gs[0]);
   sx.store(Xs[0]);
@@ -970,7 +972,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(const float* gy, const 
   for (int64_t mb = m0; mb < m1; mb += kWgM) {
     const bool more = mb + kWgM < m1;
     if (more) {
-      sg.load(gy, N, mb + kWgM, m1, n0, N, vec);
+      sg.template load<TG>(gy, N, mb + kWgM, m1, n0, N, vec);
       sx.load(x, K, mb + kWgM, m1, k0, K, vec);
     }
     const T* G = Gs[buf];
@@ -1984,6 +1986,48 @@ int cign_linear_gamma_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t
 
 int64_t cign_linear_bwd_workspace_bytes(int64_t M, int32_t N, int32_t K, int32_t with_bias) {
   return bwd_ws(M, N, K, with_bias != 0).total;
+}
+
+// cign_linear_bwd with bf16 math (no bias) whose grad_y is bf16 storage: the
+// values bf16 math rounds it to, in half the bytes (the GAT lin's backward,
+// whose gradient the logits backward writes rounded).
+int cign_linear_bwd_bf16gy(void* stream, int64_t M, int32_t N, int32_t K, const void* grad_y, const float* x,
+                           const float* w, float* grad_x, float* grad_w, void* workspace, int64_t workspace_bytes) {
+  if (M < 0 || N <= kSmallN || K <= 0)
+    return set_error(kInvalid, "cign_linear_bwd_bf16gy: bad sizes (N must exceed %d)", kSmallN);
+  if (!w || !grad_w || (M > 0 && (!grad_y || !x))) return set_error(kInvalid, "cign_linear_bwd_bf16gy: null pointer");
+  if (M > 0x7fffffff) return set_error(kInvalid, "cign_linear_bwd_bf16gy: M too large");
+  const BwdWs L = bwd_ws(M, N, K, false, true);
+  if (workspace_bytes < L.total || (L.total > 0 && !workspace))
+    return set_error(kInvalid, "cign_linear_bwd_bf16gy: workspace too small (%lld < %lld)",
+                     static_cast<long long>(workspace_bytes), static_cast<long long>(L.total));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  int rc;
+  if (M == 0) return rowops::zero_outputs(st, grad_w, N * K, nullptr, 0, "cign_linear_bwd_bf16gy");
+  const bf16h* gy = static_cast<const bf16h*>(grad_y);
+  {
+    const int ntk = (K + kWgT - 1) / kWgT;
+    const dim3 grid(wg_grid(((N + kWgT - 1) / kWgT) * ntk, L.wg_chunks, true));
+    const bool vec = N % 4 == 0 && K % 4 == 0 && aligned16(grad_y) && aligned16(x);
+    float* part = reinterpret_cast<float*>(ws + L.part_w);
+    hipLaunchKernelGGL((wgrad_kernel<kMathBF16, bf16h>), grid, dim3(kThreads), 0, st, gy, x, M, N, K, L.wg_chunk,
+                       L.wg_chunks, ntk, vec, part);
+    if ((rc = check_launch("cign_linear_bwd_bf16gy (grad_W partials)"))) return rc;
+    if ((rc = rowops::launch_colsum(st, part, L.wg_chunks, N * K, 1, grad_w, nullptr,
+                                    "cign_linear_bwd_bf16gy (grad_W)")))
+      return rc;
+  }
+  if (!grad_x) return kOk;
+  float* wt = reinterpret_cast<float*>(ws + L.wt);
+  hipLaunchKernelGGL(transpose_w_kernel, dim3((K + 31) / 32, (N + 31) / 32), dim3(256), 0, st, w, N, K, wt);
+  if ((rc = check_launch("cign_linear_bwd_bf16gy (W^T)"))) return rc;
+  GemmArgs g{};
+  g.M = M; g.N = K; g.K = N; g.x = grad_y; g.w = wt; g.y = grad_x;
+  g.vec = rows_aligned(grad_y, kBF16, wt, N);
+  g.vec4 = K % 4 == 0 && aligned16(grad_x);
+  g.round_bf16 = false;
+  return dispatch_nt<kEpiStore>(st, g, kBF16, kMathBF16, pick_bn(K, 0, kMathBF16));
 }
 
 int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math, const float* grad_y, const float* x,

@@ -172,10 +172,10 @@ __global__ __launch_bounds__(kBlock) void attn_fwd_kernel(int64_t rows, int H, i
 // Writes g_x (plus gx_in, the gradient x receives from its other consumer,
 // when not null; it may alias gx) and the tile's partial sums of gs*x and
 // gd*x for row block blockIdx.x (part layout [2][nb][F]).
-template <int LPR, int V, int W, typename TX = float>
+template <int LPR, int V, int W, typename TX = float, typename TO = float>
 __global__ __launch_bounds__(kBlock) void attn_bwd_kernel(int64_t n, int H, int C, const float* gs, const float* gd,
                                                           const TX* x, const float* as, const float* ad,
-                                                          const float* gx_in, float* gx, float* part, int nb) {
+                                                          const float* gx_in, TO* gx, float* part, int nb) {
   __shared__ float lds[kBlock * V * W];
   const Geo<LPR> g;
   const int F = H * C;
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(kBlock) void attn_bwd_kernel(int64_t n, int H, int 
           accs[v][w] = fmaf(s, xv[w], accs[v][w]);
           accd[v][w] = fmaf(d, xv[w], accd[v][w]);
         }
-        Chunk<float, W>::store(gx + r * F + c * W, o);
+        Chunk<TO, W>::store(gx + r * F + c * W, o);
       }
     }
   }
@@ -656,7 +656,7 @@ template <typename TX>
 int attn_bwd_impl(const char* who, void* stream, int64_t n, int32_t H, int32_t C, const float* grad_src,
                   const float* grad_dst, const TX* x, const float* att_src, const float* att_dst,
                   const float* grad_x_in, float* grad_x, float* grad_att_src, float* grad_att_dst, void* workspace,
-                  int64_t workspace_bytes) {
+                  int64_t workspace_bytes, bool grad_x_bf16 = false) {
   if (n < 0 || H < 1 || C < 1) return set_error(kInvalid, "%s: bad shape", who);
   const int F = H * C;
   if (workspace_bytes < colsum_bytes(n, F, 2)) return set_error(kInvalid, "%s: workspace too small", who);
@@ -672,8 +672,12 @@ int attn_bwd_impl(const char* who, void* stream, int64_t n, int32_t H, int32_t C
       auto launch8 = [&](auto LC, auto VC) {
         constexpr int L = decltype(LC)::value, V = decltype(VC)::value;
         const dim3 grid(nb, (qf8 + L * V - 1) / (L * V));
-        hipLaunchKernelGGL((attn_bwd_kernel<L, V, 8, bf16>), grid, dim3(kBlock), 0, st, n, H, C, grad_src, grad_dst,
-                           xb, att_src, att_dst, grad_x_in, grad_x, part, nb);
+        if (grad_x_bf16)
+          hipLaunchKernelGGL((attn_bwd_kernel<L, V, 8, bf16, bf16>), grid, dim3(kBlock), 0, st, n, H, C, grad_src,
+                             grad_dst, xb, att_src, att_dst, grad_x_in, reinterpret_cast<bf16*>(grad_x), part, nb);
+        else
+          hipLaunchKernelGGL((attn_bwd_kernel<L, V, 8, bf16>), grid, dim3(kBlock), 0, st, n, H, C, grad_src, grad_dst,
+                             xb, att_src, att_dst, grad_x_in, grad_x, part, nb);
         return check_launch(who);
       };
       // rows of more than 128 chunks take column tiles of 128 (two chunks per
@@ -683,6 +687,9 @@ int attn_bwd_impl(const char* who, void* stream, int64_t n, int32_t H, int32_t C
       return launch_colsum(st, part, nb, F, 2, grad_att_src, grad_att_dst, who);
     }
   }
+  if (grad_x_bf16 && n > 0)
+    return set_error(kInvalid, "%s: a bf16 grad_x needs bf16 x with channels a multiple of 8 and 16-byte aligned "
+                     "rows", who);
   const int W = grad_x_in ? chunk_width(C, {x, att_src, att_dst, grad_x, grad_x_in})
                           : chunk_width(C, {x, att_src, att_dst, grad_x});
   const int qf = F / W;
@@ -740,17 +747,23 @@ int cign_attn_logits_bwd(void* stream, int64_t n, int32_t H, int32_t C, const fl
                        grad_x, grad_att_src, grad_att_dst, workspace, workspace_bytes);
 }
 
-int cign_attn_logits_bwd_acc(void* stream, int64_t n, int32_t H, int32_t C, int32_t x_dtype, const float* grad_src,
-                             const float* grad_dst, const void* x, const float* att_src, const float* att_dst,
-                             const float* grad_x_in, float* grad_x, float* grad_att_src, float* grad_att_dst,
-                             void* workspace, int64_t workspace_bytes) {
+int cign_attn_logits_bwd_acc(void* stream, int64_t n, int32_t H, int32_t C, int32_t x_dtype, int32_t grad_x_dtype,
+                             const float* grad_src, const float* grad_dst, const void* x, const float* att_src,
+                             const float* att_dst, const float* grad_x_in, void* grad_x, float* grad_att_src,
+                             float* grad_att_dst, void* workspace, int64_t workspace_bytes) {
   const char* who = "cign_attn_logits_bwd_acc";
+  if (grad_x_dtype != kF32 && !(grad_x_dtype == kBF16 && x_dtype == kBF16))
+    return set_error(kInvalid, "%s: grad_x_dtype must be 0 (float32), or 1 (bf16) with bf16 x", who);
+  if (grad_x_dtype == kBF16 && grad_x_in == grad_x)
+    return set_error(kInvalid, "%s: a bf16 grad_x cannot alias the float32 grad_x_in", who);
+  float* gx = static_cast<float*>(grad_x);
   if (x_dtype == kF32)
     return attn_bwd_impl(who, stream, n, H, C, grad_src, grad_dst, static_cast<const float*>(x), att_src, att_dst,
-                         grad_x_in, grad_x, grad_att_src, grad_att_dst, workspace, workspace_bytes);
+                         grad_x_in, gx, grad_att_src, grad_att_dst, workspace, workspace_bytes);
   if (x_dtype == kBF16)
     return attn_bwd_impl(who, stream, n, H, C, grad_src, grad_dst, static_cast<const bf16h*>(x), att_src, att_dst,
-                         grad_x_in, grad_x, grad_att_src, grad_att_dst, workspace, workspace_bytes);
+                         grad_x_in, gx, grad_att_src, grad_att_dst, workspace, workspace_bytes,
+                         grad_x_dtype == kBF16);
   return set_error(kInvalid, "%s: x_dtype must be 0 (float32) or 1 (bf16), got %d", who, x_dtype);
 }
 

@@ -32,6 +32,8 @@ _FUSED_LOGITS_C = (16, 32, 64, 128)
 # Largest average degree at which bf16 x_proj is gathered again in the
 # backward instead of saving per-row aggregates.
 _GATHER_MAX_DEGREE = 12
+# cign_linear_bwd runs outputs up to this many on VALU kernels
+_SMALL_N = 16
 
 
 def holds_bf16(heads: int, channels: int, math: int) -> bool:
@@ -120,12 +122,29 @@ class _LinGatFn(torch.autograd.Function):
         # gradient; the logits' term is added to grad_feat in place.
         g_s = torch.empty_like(s)
         g_d = torch.empty_like(d)
+        st = _lib.stream_ptr(dev)
+        # With x_proj held in bf16 the sum is written rounded to bf16, the
+        # values the projection's bf16-math backward reads of it.
+        gy16 = ctx.hold and C % 8 == 0 and H * C > _SMALL_N
+        gy = torch.empty((M, H, C), dtype=torch.bfloat16, device=dev) if gy16 else grad_feat
         ws_bytes = int(lib.cign_colsum_workspace_bytes(M, H * C, 2))
         ws = _lib.workspace(ws_bytes, dev)
-        lib.call("cign_attn_logits_bwd_acc", _lib.stream_ptr(dev), M, H, C, 1 if ctx.hold else 0,
+        lib.call("cign_attn_logits_bwd_acc", st, M, H, C, 1 if ctx.hold else 0, 1 if gy16 else 0,
                  g_attn_col.data_ptr(), g_attn_row.data_ptr(), xp.data_ptr(), s.data_ptr(), d.data_ptr(),
-                 grad_feat.data_ptr(), grad_feat.data_ptr(), g_s.data_ptr(), g_d.data_ptr(), ws.data_ptr(), ws_bytes)
-        gx, gw, _ = _linear_bwd(grad_feat, x2, w, False, ctx.math, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+                 grad_feat.data_ptr(), gy.data_ptr(), g_s.data_ptr(), g_d.data_ptr(), ws.data_ptr(), ws_bytes)
+        if gy16:
+            K = x2.size(1)
+            xf = x2 if x2.dtype == torch.float32 else x2.float()
+            gx = torch.empty((M, K), dtype=torch.float32, device=dev) if ctx.needs_input_grad[0] else None
+            gw = torch.empty((H * C, K), dtype=torch.float32, device=dev)
+            lws_bytes = int(lib.cign_linear_bwd_workspace_bytes(M, H * C, K, 0))
+            lws = _lib.workspace(lws_bytes, dev)
+            lib.call("cign_linear_bwd_bf16gy", st, M, H * C, K, gy.data_ptr(), xf.data_ptr(), w.data_ptr(),
+                     _lib.ptr(gx), gw.data_ptr(), lws.data_ptr(), lws_bytes)
+            gw = gw if ctx.needs_input_grad[1] else None
+        else:
+            gx, gw, _ = _linear_bwd(grad_feat, x2, w, False, ctx.math, ctx.needs_input_grad[0],
+                                    ctx.needs_input_grad[1])
         if gx is not None:
             gx = gx.reshape(ctx.in_shape).to(ctx.x_dtype)
         return (gx, gw, g_s, g_d, g_bias) + (None,) * 10

@@ -234,11 +234,14 @@ int cign_attn_logits_fwd_bf16(void* stream, int64_t n, int32_t heads, int32_t ch
  * (grad_x_in may alias grad_x; null for none), the sum autograd forms between
  * ext attention_backward (fused_gat_sideops.cpp:54-66) and the GAT's
  * backward, without a pass of its own. x_dtype: 0 = float32, 1 = bf16
- * storage (as cign_attn_logits_fwd_bf16). */
+ * storage (as cign_attn_logits_fwd_bf16). grad_x_dtype: 0 = float32, 1 =
+ * bf16 (x_dtype 1 with channels a multiple of 8 only; the sum rounded to
+ * nearest even, what a bf16-math GEMM reads of it; grad_x_in must not alias
+ * it). */
 int cign_attn_logits_bwd_acc(void* stream, int64_t n, int32_t heads, int32_t channels, int32_t x_dtype,
-                             const float* grad_src, const float* grad_dst, const void* x, const float* att_src,
-                             const float* att_dst, const float* grad_x_in, float* grad_x, float* grad_att_src,
-                             float* grad_att_dst, void* workspace, int64_t workspace_bytes);
+                             int32_t grad_x_dtype, const float* grad_src, const float* grad_dst, const void* x,
+                             const float* att_src, const float* att_dst, const float* grad_x_in, void* grad_x,
+                             float* grad_att_src, float* grad_att_dst, void* workspace, int64_t workspace_bytes);
 
 /* pre = sum_h out[n,h,:] / H + bias, y = SiLU(pre). Replaces ext
  * head_silu_forward (fused_gat_sideops.cpp:68-76; kernel
@@ -471,6 +474,15 @@ int64_t cign_linear_bwd_workspace_bytes(int64_t M, int32_t N, int32_t K, int32_t
 int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math, const float* grad_y, const float* x,
                     const float* w, float* grad_x, float* grad_w, float* grad_b, void* workspace,
                     int64_t workspace_bytes);
+
+/* cign_linear_bwd with math = 1, no bias and N > 16, whose grad_y is bf16
+ * storage [M,N]: the values bf16 math rounds a float32 grad_y to, read in half
+ * the bytes; results equal cign_linear_bwd's on the float32 grad_y. Workspace:
+ * cign_linear_bwd_workspace_bytes(M, N, K, 0). No counterpart in the
+ * reference; the GAT lin's backward under AMP, whose gradient
+ * cign_attn_logits_bwd_acc writes as bf16. */
+int cign_linear_bwd_bf16gy(void* stream, int64_t M, int32_t N, int32_t K, const void* grad_y, const float* x,
+                           const float* w, float* grad_x, float* grad_w, void* workspace, int64_t workspace_bytes);
 
 #ifdef __cplusplus
 }

@@ -28,12 +28,13 @@ def gpu_available() -> bool:
 
 
 def assert_close(actual, expected, rtol, atol, name=""):
-    """|a - e| <= atol + rtol * |e| elementwise (the torch.allclose rule)."""
+    """|a - e| <= atol + rtol * |e| elementwise (the torch.allclose rule); a
+    NaN matches only a NaN."""
     a = np.asarray(actual, dtype=np.float64)
     e = np.asarray(expected, dtype=np.float64)
     assert a.shape == e.shape, f"{name}: shape {a.shape} != {e.shape}"
     err = np.abs(a - e)
-    bad = err > atol + rtol * np.abs(e)
+    bad = ~(err <= atol + rtol * np.abs(e)) & ~(np.isnan(a) & np.isnan(e))
     if bad.any():
         i = np.unravel_index(np.argmax(err - (atol + rtol * np.abs(e))), a.shape)
         raise AssertionError(f"{name}: {int(bad.sum())} of {a.size} outside rtol={rtol} atol={atol}; "

@@ -171,3 +171,103 @@ def test_lin_gat_matches_three_functions(C, amp, monkeypatch):
         a = res["1"][k]
         extra = bf16_flip_atol(e.cpu().numpy()) if amp and k in ("x", "lin.weight") else 0.0
         assert_close(a, e, rtol=1e-4, atol=1e-5 * max(1.0, float(e.abs().max())) + extra, name=k)
+
+
+@pytest.mark.parametrize("M,N,K", [(1000, 256, 48), (777, 1536, 256), (130, 64, 300), (37, 24, 20), (0, 64, 32)])
+def test_linear_bwd_bf16_grad_y(M, N, K):
+    """cign_linear_bwd_bf16gy on bf16 grad_y against cign_linear_bwd (math 1)
+    on the same values in float32: bit for bit (both GEMMs read the bf16
+    values and run the same tiles)."""
+    from cign_amd import _lib
+
+    print(f"linear bwd bf16 grad_y M={M} N={N} K={K}", flush=True)
+    lib = _lib.load_library()
+    rng = np.random.default_rng(M + N + K)
+    gy16 = torch.from_numpy((rng.standard_normal((M, N)) / 30).astype(np.float32)).cuda().to(torch.bfloat16)
+    gy = gy16.float()
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()
+    w = torch.from_numpy((rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32)).cuda()
+    st = _lib.stream_ptr(x.device)
+    ws_bytes = int(lib.cign_linear_bwd_workspace_bytes(M, N, K, 0))
+    ws = _lib.workspace(ws_bytes, x.device)
+    outs = []
+    for name, g in (("cign_linear_bwd", gy), ("cign_linear_bwd_bf16gy", gy16)):
+        gx = torch.full((M, K), float("nan"), device="cuda")
+        gw = torch.full((N, K), float("nan"), device="cuda")
+        args = (g.data_ptr(), x.data_ptr(), w.data_ptr(), gx.data_ptr(), gw.data_ptr())
+        if name == "cign_linear_bwd":
+            lib.call(name, st, M, N, K, 1, *args, None, ws.data_ptr(), ws_bytes)
+        else:
+            lib.call(name, st, M, N, K, *args, ws.data_ptr(), ws_bytes)
+        outs.append((gx, gw))
+    torch.cuda.synchronize()
+    for a, e, what in ((outs[1][0], outs[0][0], "grad_x"), (outs[1][1], outs[0][1], "grad_w")):
+        assert torch.equal(a, e), what
+    # grad_x may be skipped
+    gw = torch.empty((N, K), device="cuda")
+    lib.call("cign_linear_bwd_bf16gy", st, M, N, K, gy16.data_ptr(), x.data_ptr(), w.data_ptr(), None,
+             gw.data_ptr(), ws.data_ptr(), ws_bytes)
+    torch.cuda.synchronize()
+    assert torch.equal(gw, outs[0][1])
+
+
+@pytest.mark.parametrize("H,C", [(6, 256), (4, 64), (2, 8), (3, 1040)])
+def test_attn_logits_bwd_acc_bf16_grad_x(H, C):
+    """cign_attn_logits_bwd_acc writing a bf16 grad_x: the float32 grad_x of
+    the same call rounded to nearest even, bit for bit; the logits'
+    gradients unchanged."""
+    from cign_amd import _lib
+
+    print(f"logits bwd acc bf16 grad_x H={H} C={C}", flush=True)
+    lib = _lib.load_library()
+    n = 517
+    rng = np.random.default_rng(H * C)
+    xp = torch.from_numpy(rng.standard_normal((n, H, C)).astype(np.float32)).cuda().to(torch.bfloat16)
+    s = torch.from_numpy(rng.standard_normal((H, C)).astype(np.float32)).cuda()
+    d = torch.from_numpy(rng.standard_normal((H, C)).astype(np.float32)).cuda()
+    gs = torch.from_numpy(rng.standard_normal((n, H)).astype(np.float32)).cuda()
+    gd = torch.from_numpy(rng.standard_normal((n, H)).astype(np.float32)).cuda()
+    gin = torch.from_numpy((rng.standard_normal((n, H, C)) / 7).astype(np.float32)).cuda()
+    st = _lib.stream_ptr(xp.device)
+    ws_bytes = int(lib.cign_colsum_workspace_bytes(n, H * C, 2))
+    ws = _lib.workspace(ws_bytes, xp.device)
+    res = []
+    for code, dt in ((0, torch.float32), (1, torch.bfloat16)):
+        gx = torch.empty((n, H, C), dtype=dt, device="cuda")
+        g_s, g_d = torch.empty_like(s), torch.empty_like(d)
+        lib.call("cign_attn_logits_bwd_acc", st, n, H, C, 1, code, gs.data_ptr(), gd.data_ptr(), xp.data_ptr(),
+                 s.data_ptr(), d.data_ptr(), gin.data_ptr(), gx.data_ptr(), g_s.data_ptr(), g_d.data_ptr(),
+                 ws.data_ptr(), ws_bytes)
+        res.append((gx, g_s, g_d))
+    torch.cuda.synchronize()
+    assert torch.equal(res[1][0], res[0][0].to(torch.bfloat16))
+    assert torch.equal(res[1][1], res[0][1]) and torch.equal(res[1][2], res[0][2])
+
+
+def test_bf16_gradient_entry_points_reject():
+    from cign_amd import _lib
+
+    lib = _lib.load_library()
+    n, H, C = 10, 2, 12
+    x32 = torch.zeros((n, H, C), device="cuda")
+    x16 = x32.to(torch.bfloat16)
+    v = torch.zeros((H, C), device="cuda")
+    g = torch.zeros((n, H), device="cuda")
+    out16 = torch.empty_like(x16)
+    ws = _lib.workspace(int(lib.cign_colsum_workspace_bytes(n, H * C, 2)), x32.device)
+    st = _lib.stream_ptr(x32.device)
+    for xd, x, gin, gdt in ((0, x32, x32, 1), (1, x16, x32, 1), (1, x16, x32, 2)):
+        # float32 x, channels not a multiple of 8, an unknown code
+        with pytest.raises(RuntimeError):
+            lib.call("cign_attn_logits_bwd_acc", st, n, H, C, xd, gdt, g.data_ptr(), g.data_ptr(), x.data_ptr(),
+                     v.data_ptr(), v.data_ptr(), gin.data_ptr(), out16.data_ptr(), v.data_ptr(), v.data_ptr(),
+                     ws.data_ptr(), ws.numel())
+    w = torch.zeros((16, 8), device="cuda")
+    gw = torch.empty_like(w)
+    lws = _lib.workspace(int(lib.cign_linear_bwd_workspace_bytes(n, 16, 8, 0)), w.device)
+    with pytest.raises(RuntimeError, match="N must exceed"):
+        lib.call("cign_linear_bwd_bf16gy", st, n, 16, 8, x16.data_ptr(), w.data_ptr(), w.data_ptr(), None,
+                 gw.data_ptr(), lws.data_ptr(), lws.numel())
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        lib.call("cign_linear_bwd_bf16gy", st, n, 24, 8, x16.data_ptr(), torch.zeros((n, 8), device="cuda").data_ptr(),
+                 torch.zeros((24, 8), device="cuda").data_ptr(), None, gw.data_ptr(), lws.data_ptr(), 0)
