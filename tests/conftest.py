@@ -77,7 +77,7 @@ def assert_close_fp32_derived(actual, expected64, expected32, name="", rtol=1e-4
     err32 = np.abs(e32 - e)
     bound = atol + rtol * np.abs(e) + k * err32 + (err32.max() if err32.size else 0.0)
     err = np.abs(a - e)
-    bad = err > bound
+    bad = ~(err <= bound) & ~(np.isnan(a) & np.isnan(e))
     if bad.any():
         i = np.unravel_index(np.argmax(err - bound), a.shape)
         raise AssertionError(f"{name}: {int(bad.sum())} of {a.size} outside the fp32-derived bound; worst at {i}: "

@@ -709,3 +709,19 @@ def test_cpu_path_layer_matches_oracle(rng):
     y1 = cpu_path._FixedCsrMM.apply(L.X, L.P, L.PT)
     assert_close(d(y1), ys[0], 1e-4, 1e-5, "hop 1")
     assert cpu_path.host_threads() >= 1
+
+
+def test_assert_close_rejects_nan():
+    """The comparison helpers fail on a NaN where a number is expected (a
+    NaN compares false against any tolerance); assert_close accepts NaN
+    against NaN."""
+    from tests.conftest import assert_close, assert_close_fp32_derived
+
+    e = np.array([1.0, 2.0, 3.0])
+    a = e.copy()
+    a[1] = np.nan
+    with pytest.raises(AssertionError):
+        assert_close(a, e, rtol=1e-4, atol=1e-5)
+    with pytest.raises(AssertionError):
+        assert_close_fp32_derived(a, e, e)
+    assert_close(a, a, rtol=1e-4, atol=1e-5)
