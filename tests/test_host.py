@@ -264,3 +264,45 @@ def test_dispatch_signatures_match_reference_vectors(monkeypatch):
     monkeypatch.setenv("CIGN_INTERACTION_MODE", "sideways")
     with pytest.raises(ValueError, match="old/new"):
         cign_speed_signature([])
+
+
+def _header_prototypes():
+    """{name: (return type, [parameter types])} of include/cign_amd.h."""
+    text = (ROOT / "include" / "cign_amd.h").read_text()
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", " ", text)
+    protos = {}
+    for ret, name, params in re.findall(r"([A-Za-z_][\w ]*?\**)\s*\b(cign_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = " ".join(params.split())
+        types = [] if params in ("", "void") else [p.strip().rsplit(" ", 1)[0] if "*" not in p.rsplit(" ", 1)[-1]
+                                                  else p.strip() for p in params.split(",")]
+        protos[name] = (" ".join(ret.split()), types)
+    return protos
+
+
+def test_ctypes_signatures_match_header():
+    """Every entry point's ctypes argument list has the header's length and,
+    argument by argument, the same kind (pointer, int32, int64, uint64,
+    float), and the same return kind: a mismatch would pass arguments in the
+    wrong registers without any error."""
+    def kind(t):
+        t = t.replace("const ", "").strip()
+        if "*" in t:
+            return C.c_void_p
+        return {"int": C.c_int32, "int32_t": C.c_int32, "int64_t": C.c_int64, "uint64_t": C.c_uint64,
+                "float": C.c_float}[t]
+
+    import ctypes as C
+
+    protos = _header_prototypes()
+    assert set(protos) == set(_lib._SIGNATURES), set(protos) ^ set(_lib._SIGNATURES)
+    for name, (ret, params) in protos.items():
+        sig_ret, sig_args = _lib._SIGNATURES[name]
+        assert len(params) == len(sig_args), f"{name}: header {len(params)} arguments, ctypes {len(sig_args)}"
+        for i, (p, a) in enumerate(zip(params, sig_args)):
+            assert C.sizeof(kind(p)) == C.sizeof(a) and (kind(p) is C.c_float) == (a is C.c_float), \
+                f"{name} argument {i}: header {p!r}, ctypes {a}"
+        if ret.endswith("*"):
+            assert sig_ret in (C.c_void_p, C.c_char_p), name
+        else:
+            assert C.sizeof(kind(ret)) == C.sizeof(sig_ret), f"{name}: returns {ret}, ctypes {sig_ret}"
