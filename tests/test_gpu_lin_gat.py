@@ -9,7 +9,11 @@ same values (dtype 0, another lane geometry) it agrees to the fp32
 tolerance. The module path is checked against the three autograd functions
 it replaces (CIGN_GAT_FUSED_LIN=0): the same rounding points, so the fp32
 tolerance plus, under AMP where an operand is rounded to bf16, one bf16 ulp;
-against the oracle it is covered by the block and net tests."""
+against the oracle it is covered by the block and net tests. Its backward's
+bf16 gradient entry points are checked bit for bit against their float32
+counterparts on the same values: the logits backward's bf16 grad_x against
+its float32 grad_x rounded to nearest even, and cign_linear_bwd_bf16gy
+against cign_linear_bwd with bf16 math."""
 import numpy as np
 import pytest
 import torch
