@@ -781,9 +781,11 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_lds_kernel(GemmArgs g, int n
 // Backward helpers
 // ---------------------------------------------------------------------------
 // part[c][n] = sum of grad_y rows of chunk c (a workgroup: 64 columns x 4 row
-// slices, four accumulators per thread, slices combined in order).
+// slices, four accumulators per thread, slices combined in order). With rb
+// (bf16 autocast) each grad_y value is rounded to bf16 first: the bf16
+// Linear's backward sums its bf16 incoming gradient.
 __global__ __launch_bounds__(kThreads) void bias_grad_kernel(const float* gy, int64_t M, int N, int64_t chunk,
-                                                             float* part) {
+                                                             float* part, bool rb) {
   __shared__ float red[kThreads];
   const int t = threadIdx.x;
   const int n = blockIdx.x * 64 + (t & 63);
@@ -793,13 +795,14 @@ __global__ __launch_bounds__(kThreads) void bias_grad_kernel(const float* gy, in
   float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
   if (n < N) {
     int64_t r = r0 + s;
+    auto v = [&](int64_t i) { const float t = gy[i * N + n]; return rb ? round_bf16(t) : t; };
     for (; r + 12 < r1; r += 16) {
-      a0 += gy[r * N + n];
-      a1 += gy[(r + 4) * N + n];
-      a2 += gy[(r + 8) * N + n];
-      a3 += gy[(r + 12) * N + n];
+      a0 += v(r);
+      a1 += v(r + 4);
+      a2 += v(r + 8);
+      a3 += v(r + 12);
     }
-    for (; r < r1; r += 4) a0 += gy[r * N + n];
+    for (; r < r1; r += 4) a0 += v(r);
   }
   red[t] = (a0 + a1) + (a2 + a3);
   __syncthreads();
@@ -1060,6 +1063,8 @@ __global__ __launch_bounds__(kThreads) void small_n_grad_x_kernel(const float* g
     }
   }
   float* o = gx + m * K + k;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) acc[q] = rb_if(RB, acc[q]);
   if (full) {
     *reinterpret_cast<float4*>(o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
   } else {
@@ -1507,8 +1512,10 @@ __global__ __launch_bounds__(kThreads) void pack_proj_bwd_kernel(PackBwdArgs b, 
       float gpt[4], gpc[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float goW = acc[(2 * k) * NFH + fh][q];
-        const float goD = acc[(2 * k + 1) * NFH + fh][q];
+        // bf16 math: grad_G is the bf16 output of autocast's Linear backward
+        const float goW = MATH == kMathBF16 ? round_bf16(acc[(2 * k) * NFH + fh][q]) : acc[(2 * k) * NFH + fh][q];
+        const float goD =
+            MATH == kMathBF16 ? round_bf16(acc[(2 * k + 1) * NFH + fh][q]) : acc[(2 * k + 1) * NFH + fh][q];
         const packk::DW e = packk::interact(h[fh][q] * tc[k][fh][q], c[fh][q] * th[k][fh][q], a.mode);
         const float gD = goD * al[k];
         const float gW = goW * al[k];
@@ -2015,7 +2022,7 @@ int cign_linear_bwd_bf16gy(void* stream, int64_t M, int32_t N, int32_t K, const 
                        L.wg_chunks, ntk, vec, part);
     if ((rc = check_launch("cign_linear_bwd_bf16gy (grad_W partials)"))) return rc;
     if ((rc = rowops::launch_colsum(st, part, L.wg_chunks, N * K, 1, grad_w, nullptr,
-                                    "cign_linear_bwd_bf16gy (grad_W)")))
+                                    "cign_linear_bwd_bf16gy (grad_W)", true)))
       return rc;
   }
   if (!grad_x) return kOk;
@@ -2026,7 +2033,7 @@ int cign_linear_bwd_bf16gy(void* stream, int64_t M, int32_t N, int32_t K, const 
   g.M = M; g.N = K; g.K = N; g.x = grad_y; g.w = wt; g.y = grad_x;
   g.vec = rows_aligned(grad_y, kBF16, wt, N);
   g.vec4 = K % 4 == 0 && aligned16(grad_x);
-  g.round_bf16 = false;
+  g.round_bf16 = true;  // grad_x is the bf16 output of autocast's Linear backward
   return dispatch_nt<kEpiStore>(st, g, kBF16, kMathBF16, pick_bn(K, 0, kMathBF16));
 }
 
@@ -2045,16 +2052,18 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
   char* ws = static_cast<char*>(workspace);
   int rc;
   if (M == 0) return rowops::zero_outputs(st, grad_w, N * K, grad_b, grad_b ? N : 0, "cign_linear_bwd");
+  // Under bf16 math (autocast) grad_x, grad_W and grad_b are rounded to bf16:
+  // they are the bf16 outputs of the autocast Linear's backward.
+  const bool rb = math == kMathBF16;
   auto bias_grad = [&]() -> int {
     if (!grad_b) return kOk;
     float* part = reinterpret_cast<float*>(ws + L.part_b);
     hipLaunchKernelGGL(bias_grad_kernel, dim3((N + 63) / 64, L.chunks), dim3(kThreads), 0, st, grad_y, M, N, L.chunk,
-                       part);
+                       part, rb);
     const int r = check_launch("cign_linear_bwd (bias partials)");
-    return r ? r : rowops::launch_colsum(st, part, L.chunks, N, 1, grad_b, nullptr, "cign_linear_bwd (bias)");
+    return r ? r : rowops::launch_colsum(st, part, L.chunks, N, 1, grad_b, nullptr, "cign_linear_bwd (bias)", rb);
   };
   if (N <= kSmallN) {
-    const bool rb = math == kMathBF16;
     const int K4 = (K + 3) / 4;
     if (grad_x) {
       const dim3 gxg((K4 + 63) / 64, static_cast<unsigned>((M + 3) / 4));
@@ -2071,7 +2080,7 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
     else
       hipLaunchKernelGGL(small_n_grad_w_kernel<false>, grid, dim3(kThreads), 0, st, grad_y, x, M, N, K, L.chunk, part);
     if ((rc = check_launch("cign_linear_bwd (grad_W partials, few outputs)"))) return rc;
-    if ((rc = rowops::launch_colsum(st, part, L.chunks, N * K, 1, grad_w, nullptr, "cign_linear_bwd (grad_W)")))
+    if ((rc = rowops::launch_colsum(st, part, L.chunks, N * K, 1, grad_w, nullptr, "cign_linear_bwd (grad_W)", rb)))
       return rc;
     return bias_grad();
   }
@@ -2088,14 +2097,15 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
       hipLaunchKernelGGL(wgrad_kernel<kMathF32>, grid, dim3(kThreads), 0, st, grad_y, x, M, N, K, L.wg_chunk,
                          L.wg_chunks, ntk, vec, part);
     if ((rc = check_launch("cign_linear_bwd (grad_W partials)"))) return rc;
-    if ((rc = rowops::launch_colsum(st, part, L.wg_chunks, N * K, 1, grad_w, nullptr, "cign_linear_bwd (grad_W)")))
+    if ((rc = rowops::launch_colsum(st, part, L.wg_chunks, N * K, 1, grad_w, nullptr, "cign_linear_bwd (grad_W)",
+                                    rb)))
       return rc;
   }
   if (!grad_x) return bias_grad();
   // grad_x [M,K] = grad_y [M,N] W [N,K] = grad_y (W^T)^T: the forward NT
   // kernel with W^T [K,N] as its weight. Under bf16 math it rounds both
-  // operands to bf16 as autocast's backward GEMM reads them; the output stays
-  // fp32 (not rounded).
+  // operands to bf16 as autocast's backward GEMM reads them, and the output
+  // to bf16.
   float* wt = reinterpret_cast<float*>(ws + L.wt);
   hipLaunchKernelGGL(transpose_w_kernel, dim3((K + 31) / 32, (N + 31) / 32), dim3(256), 0, st, w, N, K, wt);
   if ((rc = check_launch("cign_linear_bwd (W^T)"))) return rc;
@@ -2103,7 +2113,7 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
   g.M = M; g.N = K; g.K = N; g.x = grad_y; g.w = wt; g.y = grad_x;
   g.vec = rows_aligned(grad_y, kF32, wt, N);
   g.vec4 = K % 4 == 0 && aligned16(grad_x);
-  g.round_bf16 = false;
+  g.round_bf16 = rb;
   if ((rc = dispatch_nt<kEpiStore>(st, g, kF32, math, pick_bn(K, 0, math)))) return rc;
   return bias_grad();
 }
@@ -2244,15 +2254,17 @@ int cign_pack_proj_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t in
   if (math == kMathBF16) go(std::integral_constant<int, kMathBF16>());
   else go(std::integral_constant<int, kMathF32>());
   if ((rc = check_launch(who))) return rc;
+  // bf16 math: grad_Wp and grad_b are the bf16 outputs of autocast's backward
+  const bool rb = math == kMathBF16;
   if ((rc = rowops::launch_colsum(st, reinterpret_cast<float*>(ws + L.part_w), L.wg_chunks, D * kw, 1, grad_w,
-                                  nullptr, "cign_pack_proj_bwd (grad_Wp)")))
+                                  nullptr, "cign_pack_proj_bwd (grad_Wp)", rb)))
     return rc;
   if (grad_b) {
     float* part = reinterpret_cast<float*>(ws + L.part_b);
     hipLaunchKernelGGL(bias_grad_kernel, dim3((D + 63) / 64, L.b_chunks), dim3(kThreads), 0, st, grad_g, n, D,
-                       L.b_chunk, part);
+                       L.b_chunk, part, rb);
     if ((rc = check_launch("cign_pack_proj_bwd (bias partials)"))) return rc;
-    if ((rc = rowops::launch_colsum(st, part, L.b_chunks, D, 1, grad_b, nullptr, "cign_pack_proj_bwd (bias)")))
+    if ((rc = rowops::launch_colsum(st, part, L.b_chunks, D, 1, grad_b, nullptr, "cign_pack_proj_bwd (bias)", rb)))
       return rc;
   }
   if (!gate_weight) return kOk;

@@ -17,14 +17,19 @@
 namespace cign {
 namespace rowops {
 
-// out[c] = sum_b part[b][c] over the nb row-block partials, in a fixed order:
+// v rounded to bf16 (nearest even), as a float: parameter gradients under
+// bf16 autocast are the bf16 outputs of its Linear backward.
+__device__ __forceinline__ float bf16_rounded(float v) { return to_f32(from_f32<bf16>(v)); }
+
+// out[c] = sum_b part[b][c] over the nb row-block partials, in a fixed order
+// (rounded to bf16 when rb):
 // a workgroup of kColsumThreads covers kCols columns (16 or 64) in
 // kColsumThreads / kCols slices; thread (c, s) sums the partials b = s,
 // s + slices, ... with eight independent accumulators (combined in a fixed
 // order), then the slices are added through an LDS tree.
 template <int kCols>
 __global__ __launch_bounds__(kColsumThreads) void colsum_kernel(const float* part, int nb, int width, float* out0,
-                                                                float* out1) {
+                                                                float* out1, bool rb) {
   // kCols columns x kSlices partial slices per workgroup; a slice thread
   // keeps eight partial rows in flight, then the slices meet in an LDS tree
   // (a fixed order, so the sums are deterministic).
@@ -51,13 +56,13 @@ __global__ __launch_bounds__(kColsumThreads) void colsum_kernel(const float* par
     if (s < h) red[t] += red[t + h * kCols];
     __syncthreads();
   }
-  if (s == 0 && c < width) out[c] = red[t];
+  if (s == 0 && c < width) out[c] = rb ? bf16_rounded(red[t]) : red[t];
 }
 
 // Wide outputs over few partial rows (weight gradients): one thread per four
 // columns walks every partial row in order, eight rows in flight.
 __global__ __launch_bounds__(kBlock) void colsum_wide_kernel(const float* part, int nb, int width, float* out0,
-                                                             float* out1) {
+                                                             float* out1, bool rb) {
   const int64_t c = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 4;
   if (c >= width) return;
   const float* src = part + static_cast<int64_t>(blockIdx.y) * nb * width + c;
@@ -82,6 +87,8 @@ __global__ __launch_bounds__(kBlock) void colsum_wide_kernel(const float* part, 
     for (int u = 0; u < h; ++u) {
       acc[u].x += acc[u + h].x; acc[u].y += acc[u + h].y; acc[u].z += acc[u + h].z; acc[u].w += acc[u + h].w;
     }
+  if (rb)
+    acc[0] = make_float4(bf16_rounded(acc[0].x), bf16_rounded(acc[0].y), bf16_rounded(acc[0].z), bf16_rounded(acc[0].w));
   *reinterpret_cast<float4*>(out + c) = acc[0];
 }
 
@@ -99,7 +106,7 @@ int zero_outputs(hipStream_t st, float* a, int na, float* b, int nbv, const char
 }
 
 int launch_colsum(hipStream_t st, const float* part, int nb, int width, int quantities, float* out0, float* out1,
-                  const char* who) {
+                  const char* who, bool round_bf16_out) {
   if (width <= 0) return kOk;
   // Three fixed-order paths: outputs of at least 65536 columns over at most
   // 128 partial rows (weight gradients) take colsum_wide_kernel, one thread
@@ -112,16 +119,16 @@ int launch_colsum(hipStream_t st, const float* part, int nb, int width, int quan
   const bool vec = width % 4 == 0 && aligned16(part) && aligned16(out0) && (!out1 || aligned16(out1));
   if (width > 4096 && width < 65536 && nb >= 16)
     hipLaunchKernelGGL(colsum_kernel<16>, dim3((width + 15) / 16, quantities), dim3(kColsumThreads), 0, st, part, nb,
-                       width, out0, out1);
+                       width, out0, out1, round_bf16_out);
   else if (width > 4096 && nb <= 128 && vec)
     hipLaunchKernelGGL(colsum_wide_kernel, dim3((width / 4 + kBlock - 1) / kBlock, quantities), dim3(kBlock), 0, st,
-                       part, nb, width, out0, out1);
+                       part, nb, width, out0, out1, round_bf16_out);
   else if (width <= 4096 && nb >= 256)
     hipLaunchKernelGGL(colsum_kernel<16>, dim3((width + 15) / 16, quantities), dim3(kColsumThreads), 0, st, part, nb,
-                       width, out0, out1);
+                       width, out0, out1, round_bf16_out);
   else
     hipLaunchKernelGGL(colsum_kernel<64>, dim3((width + 63) / 64, quantities), dim3(kColsumThreads), 0, st, part, nb,
-                       width, out0, out1);
+                       width, out0, out1, round_bf16_out);
   return check_launch(who);
 }
 

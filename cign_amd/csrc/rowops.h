@@ -85,9 +85,9 @@ int zero_outputs(hipStream_t st, float* a, int na, float* b, int nbv, const char
 
 // out_y[c] = sum over b < nb of part[(y * nb + b) * width + c] for
 // `quantities` (1 or 2) outputs y, in a fixed order (colsum_kernel or
-// colsum_wide_kernel by shape).
+// colsum_wide_kernel by shape), each sum rounded to bf16 when round_bf16_out.
 int launch_colsum(hipStream_t st, const float* part, int nb, int width, int quantities, float* out0, float* out1,
-                  const char* who);
+                  const char* who, bool round_bf16_out = false);
 
 // Calls f(IC<LPR>, IC<V>) for a row of qc chunks: LPR = next power of two
 // >= qc up to 64, then V = 2 or 4 chunks per lane (qc <= 256). Returns -1 when

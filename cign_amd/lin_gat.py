@@ -17,7 +17,8 @@ with fp32 math: the forward computes what the fp32 x_proj gives, in half the
 bytes, and the backward rounds where the reference does (the two gradients
 summed in fp32, then rounded to bf16 for the projection's backward, as
 autocast's backward does; the logits' backward stores the sum so rounded,
-and cign_linear_bwd_bf16gy reads it in half the bytes). That needs one
+and cign_linear_bwd_bf16gy reads it in half the bytes and returns grad_x and
+grad_W rounded to bf16, the bf16 Linear's backward outputs). That needs one
 function: autograd would round each consumer's gradient to the dtype of a
 bf16 x_proj before summing.
 """

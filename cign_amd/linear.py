@@ -22,8 +22,10 @@ follow its calls in the block:
 Backward (all three): grad_x = grad_y W on the forward's MFMA kernel against
 a transposed W, grad_W = grad_y^T x on a split-M MFMA kernel, grad_b =
 sum_n grad_y; with ``amp`` every product reads
-bf16-rounded operands with fp32 accumulation, as autocast's backward does;
-grad_W and grad_b are deterministic (chunk partials summed in order). The
+bf16-rounded operands with fp32 accumulation and grad_x, grad_W and grad_b
+are rounded to bf16 (grad_b the sum of the bf16-rounded grad_y), as the bf16
+Linear's backward under autocast returns them; grad_W and grad_b are
+deterministic (chunk partials summed in order). The
 logits and gamma-residual parts run on their existing kernels
 (cign_attn_logits_bwd, cign_gamma_residual_bwd).
 """

@@ -26,8 +26,10 @@ class _AmpLinear(torch.autograd.Function):
     (generic_engine/model_cign.py:86-103), rounding where the GPU path rounds:
     x, W and b to bf16, the output to bf16 (autocast's output dtype, handed on
     as float32); backward products on bf16-rounded operands (grad_y, W, x),
-    grad_b the sum of the unrounded grad_y. Arithmetic between the rounding
-    points is exact in the tensors' dtype."""
+    grad_b the sum of the rounded grad_y, and grad_x, grad_W, grad_b each
+    rounded to bf16 (the bf16 Linear's backward outputs, which the casts of
+    x, W and b back to float32 hand on unchanged). Arithmetic between the
+    rounding points is exact in the tensors' dtype."""
 
     @staticmethod
     def forward(ctx, x, w, b):
@@ -43,7 +45,7 @@ class _AmpLinear(torch.autograd.Function):
     def backward(ctx, gy):
         xr, wr = ctx.saved_tensors
         gr = _bf16(gy)
-        return gr @ wr, gr.T @ xr, (gy.sum(0) if ctx.has_bias else None)
+        return _bf16(gr @ wr), _bf16(gr.T @ xr), (_bf16(gr.sum(0)) if ctx.has_bias else None)
 
 
 def _linear(x, w, b, amp):

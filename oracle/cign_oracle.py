@@ -760,7 +760,16 @@ def linear_forward(x, w, b=None, amp=False):
     return bf16_round(y) if amp else y
 
 
-def linear_backward(gy, x, w):
-    """grad_x = gy W, grad_W = gy^T x, grad_b = sum_n gy (float64)."""
+def linear_backward(gy, x, w, amp=False):
+    """grad_x = gy W, grad_W = gy^T x, grad_b = sum_n gy (float64). With amp
+    (the backward of _local_amp_linear's autocast region): y.float()'s
+    backward hands the bf16 Linear a bf16 gradient, so gy, x and W enter the
+    products rounded to bf16, and the bf16 Linear's backward returns bf16
+    grad_x, grad_W and grad_b (each a float64 sum rounded once to bf16), which
+    the casts of x, W and b back to float32 pass on unchanged. Pinned against
+    torch CPU autocast of nn.Linear in tests/test_oracle.py."""
     gy, x, w = (np.asarray(v, np.float64) for v in (gy, x, w))
-    return gy @ w, gy.T @ x, gy.sum(axis=0)
+    if not amp:
+        return gy @ w, gy.T @ x, gy.sum(axis=0)
+    gy, x, w = bf16_round(gy), bf16_round(x), bf16_round(w)
+    return bf16_round(gy @ w), bf16_round(gy.T @ x), bf16_round(gy.sum(axis=0))

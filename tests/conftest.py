@@ -93,6 +93,30 @@ def colsum_atol(terms_abs_sum, n_rows):
     return 1e-5 + (2.0 * np.sqrt(max(int(n_rows), 1)) + 8.0) * 2.0 ** -24 * np.asarray(terms_abs_sum, np.float64)
 
 
+def assert_bf16_sum_close(actual, expected_rounded, abs_terms_sum, n_terms, name=""):
+    """A sum formed in float32 and rounded once to bf16 (the GPU) against the
+    same sum formed in float64 and rounded once to bf16 (the oracle). With
+    s32, s64 the two unrounded sums, |s32 - s64| <= d = n 2^-24 sum|terms|
+    (the float32 summation bound gamma_n; the products of bf16 operands are
+    exact in float32), and rounding to nearest moves each by at most half a
+    bf16 spacing, at most 2^-8 of its magnitude, so |a - e| <= 2^-7 |s64| +
+    1.01 d <= 2^-7 (1 + 2^-8) |e| + 1.01 d elementwise. Both sides must be
+    bf16 values."""
+    from oracle import cign_oracle as O
+
+    a = np.asarray(actual, np.float64)
+    e = np.asarray(expected_rounded, np.float64)
+    assert np.array_equal(O.bf16_round(a), a), f"{name}: not bf16-valued"
+    d = float(n_terms) * 2.0 ** -24 * np.asarray(abs_terms_sum, np.float64)
+    bound = 2.0 ** -7 * (1 + 2.0 ** -8) * np.abs(e) + 1.01 * d
+    err = np.abs(a - e)
+    bad = ~(err <= bound)
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - bound), a.shape)
+        raise AssertionError(f"{name}: {int(bad.sum())} of {a.size} outside the bf16 sum bound; worst at {i}: "
+                             f"got {a[i]!r} expected {e[i]!r} bound {bound[i]!r}")
+
+
 def bf16_flip_atol(expected):
     """Extra absolute tolerance of a selective-bf16 result compared with an
     oracle that rounds to bf16 at the same points: where fp32 (GPU) and fp64

@@ -2,17 +2,19 @@
 attention logits, fused dropout-gamma-residual) and their backward against
 the float64 oracle, through the drop-in Python API (cign_amd.linear) and the
 C-ABI. Tolerances: fp32 math 1e-4 rel / 1e-5 abs; bf16 autocast math 2e-2
-rel / 2e-2 abs against the float64 oracle (the backward GEMMs read bf16
-operands, as autocast's do, and also match the oracle of the bf16-rounded
-operands to 1e-4 / 1e-5). Dropout masks
-are bit-exact against the splitmix64 oracle."""
+rel / 2e-2 abs against the float64 oracle. Under autocast the backward reads
+bf16 operands and returns bf16 grad_x, grad_W and grad_b, as the bf16
+Linear's backward does: they are bf16 values, and within one bf16 rounding
+of the float64 oracle with the same rounding points (O.linear_backward(amp=
+True), conftest.assert_bf16_sum_close). Dropout masks are bit-exact against
+the splitmix64 oracle."""
 import numpy as np
 import pytest
 import torch
 import torch.nn as nn
 
 from oracle import cign_oracle as O
-from tests.conftest import assert_close
+from tests.conftest import assert_bf16_sum_close, assert_close
 
 pytestmark = pytest.mark.gpu
 F32 = dict(rtol=1e-4, atol=1e-5)
@@ -54,12 +56,23 @@ def test_linear_forward_backward(M, N, K, amp):
     gx, gw, gb = O.linear_backward(gy, _np(x), _np(lin.weight))
     assert_close(_np(x.grad), gx, name="grad_x", **tol)
     assert_close(_np(lin.weight.grad), gw, name="grad_w", **tol)
-    assert_close(_np(lin.bias.grad), gb, name="grad_b", **F32)
+    assert_close(_np(lin.bias.grad), gb, name="grad_b", **tol)
     if amp:
-        # autocast backward: bf16 operands, fp32 accumulation
-        gx16, gw16, _ = O.linear_backward(O.bf16_round(gy), O.bf16_round(_np(x)), O.bf16_round(_np(lin.weight)))
-        assert_close(_np(x.grad), gx16, name="grad_x (bf16 operands)", **F32)
-        assert_close(_np(lin.weight.grad), gw16, name="grad_w (bf16 operands)", **F32)
+        # autocast backward: bf16 operands, fp32 accumulation, bf16 results
+        _check_amp_backward(gy, _np(x), _np(lin.weight), _np(x.grad), _np(lin.weight.grad), _np(lin.bias.grad))
+
+
+def _check_amp_backward(gy, x, w, gx, gw, gb):
+    """The bf16-autocast backward against O.linear_backward(amp=True): each
+    gradient a float32 sum of products of bf16 operands rounded once to bf16
+    (conftest.assert_bf16_sum_close)."""
+    gyr, xr, wr = O.bf16_round(gy), O.bf16_round(x), O.bf16_round(w)
+    ex, ew, eb = O.linear_backward(gy, x, w, amp=True)
+    M, N = gy.shape
+    assert_bf16_sum_close(gx, ex, np.abs(gyr) @ np.abs(wr), N, "grad_x (amp)")
+    assert_bf16_sum_close(gw, ew, np.abs(gyr).T @ np.abs(xr), M, "grad_w (amp)")
+    if gb is not None:
+        assert_bf16_sum_close(gb, eb, np.abs(gyr).sum(0), M, "grad_b (amp)")
 
 
 def test_linear_bf16_input():
@@ -103,6 +116,9 @@ def test_linear_attention_logits(H, C, K, amp):
     gx, gw, _ = O.linear_backward(g_tot, _np(x), _np(W))
     assert_close(_np(x.grad), gx, name="grad_x", **tol)
     assert_close(_np(W.grad), gw, name="grad_w", **tol)
+    if amp:  # the bf16 Linear's backward outputs
+        assert np.array_equal(O.bf16_round(_np(x.grad)), _np(x.grad))
+        assert np.array_equal(O.bf16_round(_np(W.grad)), _np(W.grad))
     assert_close(_np(s.grad).reshape(H, C), gs_ref.reshape(H, C), name="grad_att_src", **F32)
     assert_close(_np(d.grad).reshape(H, C), gd_ref.reshape(H, C), name="grad_att_dst", **F32)
 
@@ -134,8 +150,11 @@ def test_linear_gamma_residual(M, N, K, p, amp):
     assert_close(_np(h.grad), gy, name="grad_h", rtol=0, atol=0)
     assert_close(_np(x.grad), gx, name="grad_x", **tol)
     assert_close(_np(lin.weight.grad), gw, name="grad_w", **tol)
-    assert_close(_np(lin.bias.grad), gb, name="grad_b", **F32)
+    assert_close(_np(lin.bias.grad), gb, name="grad_b", **tol)
     assert_close(_np(gamma.grad), ggamma, name="grad_gamma", **tol)
+    if amp:  # the bf16 Linear's backward outputs
+        for name, t in (("grad_x", x.grad), ("grad_w", lin.weight.grad), ("grad_b", lin.bias.grad)):
+            assert np.array_equal(O.bf16_round(_np(t)), _np(t)), name
 
 
 def test_linear_gamma_mask_bits():

@@ -608,6 +608,34 @@ def test_linear_oracle_amp_rounding_points():
     np.testing.assert_allclose(gx, np.tile(w.astype(np.float64).sum(0), (64, 1)), rtol=1e-12)
 
 
+def test_linear_oracle_amp_backward_matches_torch_autocast():
+    """amp backward: torch CPU autocast of nn.Linear, whose output goes on as
+    float32 (y.float(), as _local_amp_linear returns it), gives bf16-valued
+    grad_x, grad_W and grad_b, grad_b being the sum of the bf16-rounded
+    grad_y. O.linear_backward(amp=True) matches grad_x and grad_b bit for bit
+    and grad_W within one bf16 ulp (torch accumulates the 64 rows in another
+    order); an oracle that left the gradients unrounded, or summed the
+    unrounded grad_y for grad_b, fails this."""
+    import torch
+
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(48, 24)
+    x = torch.randn(64, 48, requires_grad=True)
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        y = lin(x)
+    gy = torch.randn(64, 24)
+    y.float().backward(gy)
+    gx, gw, gb = O.linear_backward(gy.numpy(), x.detach().numpy(), lin.weight.detach().numpy(), amp=True)
+    for name, got in (("grad_x", gx), ("grad_w", gw), ("grad_b", gb)):
+        assert np.array_equal(O.bf16_round(got), got), name
+    assert np.array_equal(gx, x.grad.double().numpy())
+    assert np.array_equal(gb, lin.bias.grad.double().numpy())
+    assert not np.array_equal(O.bf16_round(gy.double().numpy().sum(0)), gb)
+    tw = lin.weight.grad.double().numpy()
+    assert np.mean(gw == tw) > 0.99
+    assert np.all(np.abs(gw - tw) <= 2.0 ** -7 * np.abs(tw))
+
+
 def test_net_oracle_closed_forms():
     """net_forward's outer composition: with gamma = 0 every block is the
     identity (H + 0 * G), so the logits are classifier(LN([H0]*(L+1))) with H0
@@ -661,8 +689,8 @@ def test_net_oracle_closed_forms():
 
 def test_block_oracle_amp_linear_matches_autocast_rounding_points():
     """block_oracle._AmpLinear (the selective-AMP projections of the block and
-    net oracles) equals the pinned O.linear_forward(amp=True) forward and the
-    bf16-operand O.linear_backward, in float64."""
+    net oracles) equals the pinned O.linear_forward(amp=True) forward and
+    O.linear_backward(amp=True), in float64."""
     import torch
 
     from oracle import block_oracle as B
@@ -674,10 +702,10 @@ def test_block_oracle_amp_linear_matches_autocast_rounding_points():
     y = B._AmpLinear.apply(xt, wt, bt)
     assert np.array_equal(y.detach().numpy(), O.linear_forward(x, w, b, amp=True))
     y.backward(torch.from_numpy(gy))
-    gx, gw, _ = O.linear_backward(O.bf16_round(gy), O.bf16_round(x), O.bf16_round(w))
-    assert_close(xt.grad.numpy(), gx, 1e-12, 1e-12, "grad x")
-    assert_close(wt.grad.numpy(), gw, 1e-12, 1e-12, "grad w")
-    assert_close(bt.grad.numpy(), gy.sum(0), 1e-12, 1e-12, "grad b")
+    gx, gw, gb = O.linear_backward(gy, x, w, amp=True)
+    assert np.array_equal(xt.grad.numpy(), gx)
+    assert np.array_equal(wt.grad.numpy(), gw)
+    assert np.array_equal(bt.grad.numpy(), gb)
 
 
 def test_cpu_path_layer_matches_oracle(rng):
