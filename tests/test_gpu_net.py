@@ -71,9 +71,6 @@ CASES = [
 
 @pytest.mark.parametrize("case,layers,combine,dual,amp", CASES)
 def test_net_training_step_matches_oracle(case, layers, combine, dual, amp):
-    from cign_amd.model_cign import GraphCliffordNet
-    from oracle import block_oracle as B
-
     print(f"net {case} layers={layers} combine={combine} dual={dual} amp={amp}", flush=True)
     if case == "c1":
         n, mh, gat_graph, (rp, cl), p_np = _c1_setup()
@@ -84,6 +81,23 @@ def test_net_training_step_matches_oracle(case, layers, combine, dual, amp):
     else:
         n, D, heads, in_dim, classes, order_set, seed = 300, 32, 4, 20, 5, (1, 2, 3), 4
         mh, gat_graph, (rp, cl), p_np = _setup(n, D)
+    check_training_step(n, mh, gat_graph, rp, cl, p_np, D=D, heads=heads, in_dim=in_dim, classes=classes,
+                        order_set=order_set, seed=seed, layers=layers, combine=combine, dual=dual, amp=amp,
+                        all_rows=case == "c1", derived_logits=case == "prod",
+                        adam_from_oracle=not (amp or case in ("c1", "prod")))
+
+
+def check_training_step(n, mh, gat_graph, rp, cl, p_np, *, D, heads, in_dim, classes, order_set, seed, layers,
+                        combine, dual, amp, all_rows, derived_logits, adam_from_oracle):
+    """One eval-mode training step of GraphCliffordNet on the GPU against
+    block_oracle.net_forward in float64 (and float32, for the derived
+    bounds): logits, the loss over a train mask (every row when all_rows),
+    every parameter gradient, and the parameters after one Adam step.
+    derived_logits: logits and loss take the fp32-derived bound (widths
+    where the float32 restatement itself misses 1e-5)."""
+    from cign_amd.model_cign import GraphCliffordNet
+    from oracle import block_oracle as B
+
     model = GraphCliffordNet(in_dim, D, classes, num_layers=layers, order_set=order_set, gat_heads=heads,
                              use_selective_amp=amp, layer_combine=combine, use_dual_input_projection=dual).cuda()
     model.eval()
@@ -92,7 +106,7 @@ def test_net_training_step_matches_oracle(case, layers, combine, dual, amp):
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(n, in_dim, generator=g)
     y = torch.randint(0, classes, (n,), generator=g)
-    mask = torch.rand(n, generator=g) < 0.5 if case != "c1" else torch.ones(n, dtype=torch.bool)
+    mask = torch.ones(n, dtype=torch.bool) if all_rows else torch.rand(n, generator=g) < 0.5
 
     logits = model(x.cuda(), None, mh)
     loss = F.cross_entropy(logits[mask.cuda()], y.cuda()[mask.cuda()])
@@ -105,42 +119,48 @@ def test_net_training_step_matches_oracle(case, layers, combine, dual, amp):
                                heads=heads, amp=amp)
         loss_dt = F.cross_entropy(ref_dt[mask], y[mask])
         loss_dt.backward()
-        refs[dt] = (ref_dt, loss_dt, params_dt)
-    ref, ref_loss, params = refs[torch.float64]
-    params32 = refs[torch.float32][2]
+        refs[dt] = (ref_dt.detach(), loss_dt.detach(), {k: v.grad for k, v in params_dt.items()})
+        del ref_dt, loss_dt, params_dt
+    ref, ref_loss, grads = refs[torch.float64]
+    grads32 = refs[torch.float32][2]
     # amp: the oracle rounds to bf16 where the GPU path does, so the bf16
     # bar (2e-2 relative) covers the rare bf16 roundings that fall the other
     # way after fp32 (GPU) instead of fp64 (oracle) accumulation.
     rtol = 2e-2 if amp else 1e-4
-    flip = (lambda e: bf16_flip_atol(e.detach().numpy())) if amp else (lambda e: 0.0)
-    if case == "prod":
+    flip = (lambda e: bf16_flip_atol(e.numpy())) if amp else (lambda e: 0.0)
+    if derived_logits:
         ref32, loss32 = refs[torch.float32][0], refs[torch.float32][1]
-        assert_close_fp32_derived(logits.detach().double().cpu().numpy(), ref.detach().numpy(),
-                                  ref32.detach().double().numpy(), name="logits", rtol=rtol, atol=1e-5 + flip(ref))
-        assert_close_fp32_derived(loss.detach().double().cpu().numpy(), ref_loss.detach().numpy(),
-                                  loss32.detach().double().numpy(), name="loss", rtol=rtol, atol=1e-5 + flip(ref_loss))
+        assert_close_fp32_derived(logits.detach().double().cpu().numpy(), ref.numpy(),
+                                  ref32.double().numpy(), name="logits", rtol=rtol, atol=1e-5 + flip(ref))
+        assert_close_fp32_derived(loss.detach().double().cpu().numpy(), ref_loss.numpy(),
+                                  loss32.double().numpy(), name="loss", rtol=rtol, atol=1e-5 + flip(ref_loss))
     else:
         _close(logits, ref, "logits", rtol, 1e-5 + flip(ref))
         _close(loss, ref_loss, "loss", rtol, 1e-5 + flip(ref_loss))
     for name, p in model.named_parameters():
-        e = params[name].grad
-        assert_close_fp32_derived(p.grad.double().cpu().numpy(), e.numpy(), params32[name].grad.double().numpy(),
+        e = grads[name]
+        assert_close_fp32_derived(p.grad.double().cpu().numpy(), e.numpy(), grads32[name].double().numpy(),
                                   name=f"grad {name}", rtol=rtol, atol=1e-5 + flip(e))
 
     # One Adam step on the GPU, against the same step on the host from (a)
-    # the oracle's gradients (fp32 only: Adam's first step moves each weight
-    # by about lr * sign(g), so a bf16-sized gradient error on a near-zero
-    # gradient flips a whole step) and (b) the GPU's own gradients.
+    # the oracle's gradients (fp32 at small sizes only: Adam's first step
+    # moves each weight by about lr * sign(g), so a gradient error on a
+    # near-zero gradient flips a whole step) and (b) the GPU's own gradients.
     mine = {k: (v.detach().double().cpu().requires_grad_(), v.grad.detach().double().cpu())
             for k, v in model.named_parameters()}
     opt = torch.optim.Adam(model.parameters(), lr=3e-3, weight_decay=1e-5)
     opt.step()
-    refs = [] if (amp or case in ("c1", "prod")) else [params]
+    steps = []
+    if adam_from_oracle:
+        oracle_params = {k: v.detach().clone().requires_grad_() for k, (v, _) in mine.items()}
+        for k, v in oracle_params.items():
+            v.grad = grads[k]
+        steps.append(oracle_params)
     own = {k: v for k, (v, _) in mine.items()}
     for k, (v, gr) in mine.items():
         v.grad = gr
-    refs.append(own)
-    for ref_params in refs:
+    steps.append(own)
+    for ref_params in steps:
         torch.optim.Adam(list(ref_params.values()), lr=3e-3, weight_decay=1e-5).step()
         for name, p in model.named_parameters():
             _close(p, ref_params[name], f"param after Adam {name}", 1e-5, 1e-6)
