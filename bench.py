@@ -20,12 +20,20 @@ The same run then adds
     on the host's cores, oracle/cpu_path.py), a bounded sample;
   * cpu_baseline_c1 / c1_gpu: BASELINE config 1, the full 2-layer model's
     training step on the host and on the GPU;
+  * c3_multihop: BASELINE config 3, the 3-hop SpMM pipeline alone at D = 64,
+    256 and 512 in fp32 and bf16 (forward3 + backward3, per-hop GB/s);
+  * c2c3_bf16: the headline layer with bf16 features;
+  * c4_pack: BASELINE config 4's pack and side ops at N = 24,492, D = 256
+    (switch pack K=3 forward + backward against its 351.4 / 552.3 MB byte
+    model; dropout-LN, add-LN, dropout-gamma-residual at p = 0.5);
   * scale: the layer at BASELINE config 5 (2.4M nodes, 62.4M edges, GAT 4 x
     32 + SpMM D=256, bf16, eager launches) with its roofline and full-size
     invariants (--no-scale skips it).
+Every step time also comes as the median of per-step HIP event pairs
+(median_gpu_ms_per_step, BASELINE's method) beside the mean.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S] [--eager] [--dtype f32|bf16]
-                       [--no-scale] [--workload layer|scale|block|train]
+                       [--no-scale] [--workload layer|scale|block|train|c3|c4pack]
 """
 from __future__ import annotations
 
@@ -49,9 +57,11 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="bounded sample of each CPU baseline, seconds (0 disables)")
-    ap.add_argument("--workload", choices=["layer", "scale", "block", "train"], default="layer",
+    ap.add_argument("--workload", choices=["layer", "scale", "block", "train", "c3", "c4pack"], default="layer",
                     help="layer: the headline c2+c3 layer (24,492 nodes); scale: the same layer at c5 size "
-                         "(2.4M nodes, ~62M edges, GAT 4x32 + SpMM D=256, bf16 by default); block: the full "
+                         "(2.4M nodes, ~62M edges, GAT 4x32 + SpMM D=256, bf16 by default); c3: the 3-hop SpMM "
+                         "pipeline alone at D = 64, 256, 512 in fp32 and bf16; c4pack: the Clifford pack and the "
+                         "side ops of BASELINE config c4 (N=24,492, D=256, p=0.5); block: the full "
                          "Clifford block forward+backward at the production shape (D=256, 6 GAT heads, hops 1-3) "
                          "with every component kernel timed against its own roofline (bf16 = selective AMP GEMMs)")
     ap.add_argument("--dtype", choices=["f32", "bf16"], default=None)
@@ -761,6 +771,16 @@ def main():
             args.dtype = "bf16"
         run_train(args, torch)
         return
+    if args.workload in ("c3", "c4pack"):
+        from cign_amd import workloads
+
+        if args.workload == "c3":
+            w = workloads.build(workloads.C2, device=dev)
+            res = {"c3_multihop": [measure_multihop(torch, w, D, dt) for D in (64, 256, 512) for dt in ("f32", "bf16")]}
+        else:
+            res = {"c4_pack": measure_c4_pack(torch)}
+        print(json.dumps(res), flush=True)
+        return
     layer_only = args.workload == "scale"
     if layer_only:
         line, _ = measure_layer(torch, True, args.dtype or "bf16", args.steps, args.warmup, args.eager,
@@ -780,12 +800,26 @@ def main():
         print("c1 model step on the host done", file=sys.stderr, flush=True)
     else:
         line["cpu_baseline"] = None
+    # The other BASELINE rows in the same run: c3 (the SpMM pipeline alone at
+    # D = 64, 256, 512, fp32 and bf16), the c2+c3 layer in bf16, and the c4
+    # pack + side ops.
+    line["c3_multihop"] = [measure_multihop(torch, w, D, dt) for D in (64, 256, 512) for dt in ("f32", "bf16")]
+    print("c3 done", file=sys.stderr, flush=True)
     del w
+    lb, _ = measure_layer(torch, False, "bf16", args.steps, args.warmup, args.eager)
+    line["c2c3_bf16"] = {k: lb[k] for k in ("value", "unit", "ms_per_step", "median_gpu_ms_per_step", "dtype",
+                                           "layer_GB_s", "layer_roofline_frac", "algorithmic_bytes_per_step",
+                                           "layer_own_roofline_frac", "breakdown", "roofline") if k in lb}
+    if "c2_with_projection" in lb:
+        line["c2c3_bf16"]["c2_with_projection"] = lb["c2_with_projection"]
+    line["c4_pack"] = measure_c4_pack(torch)
+    print("c2+c3 bf16 and c4 pack done", file=sys.stderr, flush=True)
     if not args.no_scale:
         # BASELINE config 5 in the same run: the layer at 2.4M nodes / 62.4M
         # edges (bf16, 4 x 32 heads, D = 256), the true HBM-bound case.
         sc, _ = measure_layer(torch, True, "bf16", max(3, min(args.steps, 20)), 2)
-        line["scale"] = {k: sc[k] for k in ("value", "unit", "ms_per_step", "gpu_ms_per_step", "dtype", "config",
+        line["scale"] = {k: sc[k] for k in ("value", "unit", "ms_per_step", "gpu_ms_per_step",
+                                           "median_gpu_ms_per_step", "dtype", "config",
                                            "layer_GB_s", "layer_roofline_frac", "algorithmic_bytes_per_step",
                                            "layer_own_roofline_frac", "breakdown", "roofline", "invariants")}
         line["scale"]["steps"] = max(3, min(args.steps, 20))
@@ -908,6 +942,17 @@ def measure_layer(torch, scale: bool, dtype: str, steps: int, warmup: int, eager
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     gpu_step_ms = start.elapsed_time(stop) / steps
+    # The median step (BASELINE's method: a HIP event pair around each of
+    # the K steps), in a second pass after the timed region.
+    import statistics
+
+    evs = [(ev(), ev()) for _ in range(steps)]
+    for a_, b_ in evs:
+        a_.record()
+        launch_step()
+        b_.record()
+    torch.cuda.synchronize()
+    median_step_ms = statistics.median(a_.elapsed_time(b_) for a_, b_ in evs)
 
     # Per-phase kernel durations: each phase launched R times back to back
     # (one HIP graph, or R drop-in calls with --eager) and timed with HIP
@@ -970,6 +1015,7 @@ def measure_layer(torch, scale: bool, dtype: str, steps: int, warmup: int, eager
         "warmup": warmup,
         "ms_per_step": ms,
         "gpu_ms_per_step": round(gpu_step_ms, 5),
+        "median_gpu_ms_per_step": round(median_step_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -999,6 +1045,130 @@ def measure_layer(torch, scale: bool, dtype: str, steps: int, warmup: int, eager
     if projected is not None:
         line["c2_with_projection"] = projected
     return line, w
+
+
+def _graph_time(torch, fn, R=10, M=20):
+    """Per-call milliseconds of fn(): R calls captured as one HIP graph (its
+    allocations settled by an eager call on a side stream first), replayed
+    M times with a HIP event pair on the launch stream around each replay.
+    Returns (mean, median) over the replays."""
+    import statistics
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(R):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(M)]
+    for a, b in evs:
+        a.record()
+        g.replay()
+        b.record()
+    torch.cuda.synchronize()
+    per = [a.elapsed_time(b) / R for a, b in evs]
+    return sum(per) / len(per), statistics.median(per)
+
+
+def measure_multihop(torch, w, D: int, dtype: str):
+    """BASELINE config c3: the 3-hop CSR SpMM pipeline alone (MultiHopCsrPlan
+    forward3 then backward3, every hop's output retained) on the c2 graph's
+    normalized adjacency at D columns, fp32 or bf16 storage (fp32 math). One
+    call of each is timed from HIP graph replays; per-hop GB/s against the
+    survey byte model (a hop 4(N+1) + 8E + s E D + s N D; the backward's two
+    hops that add g_k read s N D more)."""
+    from cign_amd import workloads
+    from cign_amd.multihop_csr_pipeline import MultiHopCSR3GraphOperator
+
+    dev = torch.device("cuda:0")
+    dt = torch.float32 if dtype == "f32" else torch.bfloat16
+    s = 4 if dtype == "f32" else 2
+    n, E = w.n, w.nnz_p
+    g = torch.Generator(device="cpu").manual_seed(3)
+    X, g1, g2, g3 = (torch.randn(n, D, generator=g).to(dev).to(dt) for _ in range(4))
+    plan = MultiHopCSR3GraphOperator(w.operator, dense_cols=D, dense_dtype=dt).plan
+    plan.forward3(X)
+    plan.backward3(g1, g2, g3)
+    fwd, fwd_med = _graph_time(torch, lambda: plan.forward3(X))
+    bwd, bwd_med = _graph_time(torch, lambda: plan.backward3(g1, g2, g3))
+    step, step_med = _graph_time(torch, lambda: (plan.forward3(X), plan.backward3(g1, g2, g3)))
+    B = workloads.algorithmic_bytes(n, E, 1, 1, D, s_mh=s)
+    hop_f = B["spmm"] / (fwd / 3 * 1e-3) / 1e9
+    hop_b = (B["spmm"] + s * n * D * 2 / 3) / (bwd / 3 * 1e-3) / 1e9
+    gbs = B["multihop"] / (step * 1e-3) / 1e9
+    return {"D": D, "dtype": dtype, "ms_per_step": round(step, 5), "median_ms_per_step": round(step_med, 5),
+            "fwd3_ms": round(fwd, 5), "bwd3_ms": round(bwd, 5), "edges_per_s": E / (step * 1e-3),
+            "algorithmic_bytes_per_step": B["multihop"], "GB_s": round(gbs, 1),
+            "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "hop_fwd_GB_s": round(hop_f, 1), "hop_bwd_GB_s": round(hop_b, 1),
+            "hop_roofline_frac": round(max(hop_f, hop_b) / HBM_PEAK_GBS, 4)}
+
+
+C4_N, C4_D = 24492, 256
+
+
+def measure_c4_pack(torch):
+    """BASELINE config c4's first half at N = 24,492, D = 256 (8 blades x 32
+    channels), K = 3, fp32 N(0,1): the production Clifford pack (CIGN switch
+    pack, interaction new, weighting old: out [N, 6D]) forward and backward
+    through the drop-in extension object, and the block's side ops with
+    dropout p = 0.5 (dropout + LayerNorm, add + LayerNorm, dropout-gamma
+    residual, each forward and backward). Each call is timed from HIP graph
+    replays and priced by its streamed bytes: the pack forward reads H, C
+    (4ND each), the three hops (8ND each) and alpha (12N) and writes 24ND
+    (351.4 MB); the backward reads grad_out (24ND) and the forward's inputs
+    and writes their gradients (552.3 MB)."""
+    from cign_amd.fused_block_ops import ensure_fused_block_ops_loaded
+    from cign_amd.fused_clifford_cign_pack import ensure_fused_clifford_switch_pack_loaded
+
+    dev = torch.device("cuda:0")
+    N, D, K, p = C4_N, C4_D, 3, 0.5
+    g = torch.Generator(device="cpu").manual_seed(4)
+    r = lambda *sh: torch.randn(*sh, generator=g).to(dev)
+    H, C, h2 = r(N, D), r(N, D), r(N, D)
+    P = [r(N, 2 * D) for _ in range(K)]
+    alpha = torch.softmax(r(N, K), -1).contiguous()
+    G6 = r(N, 2 * K * D)
+    gy = r(N, D)
+    w, b, gamma = r(D), r(D), r(D)
+    pack = ensure_fused_clifford_switch_pack_loaded()
+    ops = ensure_fused_block_ops_loaded()
+    y_ln, mu, rs, m_ln = ops.dropout_layernorm_forward(H, w, b, p, 1e-5, 11)
+    y_a, mu_a, rs_a = ops.add_layernorm_forward(H, C, w, b, 1e-5)
+    y_g, m_g = ops.dropout_gamma_residual_forward(h2, C, gamma, p, 12)
+    ND = N * D
+    calls = {
+        "pack_fwd": (lambda: pack.forward(H, C, *P, alpha, 1, 0), 4 * N * 14 * D + 12 * N),
+        "pack_bwd": (lambda: pack.backward(G6, H, C, *P, alpha, 1, 0), 4 * N * 22 * D + 24 * N),
+        "dropout_ln_fwd": (lambda: ops.dropout_layernorm_forward(H, w, b, p, 1e-5, 11), 9 * ND + 8 * N + 8 * D),
+        "dropout_ln_bwd": (lambda: ops.dropout_layernorm_backward(gy, H, w, mu, rs, m_ln, p),
+                           13 * ND + 8 * N + 12 * D),
+        "add_ln_fwd": (lambda: ops.add_layernorm_forward(H, C, w, b, 1e-5), 12 * ND + 8 * N + 8 * D),
+        "add_ln_bwd": (lambda: ops.add_layernorm_backward(gy, H, C, w, mu_a, rs_a), 16 * ND + 8 * N + 12 * D),
+        "gamma_residual_fwd": (lambda: ops.dropout_gamma_residual_forward(h2, C, gamma, p, 12), 13 * ND + 4 * D),
+        "gamma_residual_bwd": (lambda: ops.dropout_gamma_residual_backward(gy, C, gamma, m_g, p), 13 * ND + 8 * D),
+    }
+    out, total_ms, total_b = {}, 0.0, 0
+    for k, (fn, nbytes) in calls.items():
+        fn()
+        mean, med = _graph_time(torch, fn)
+        gbs = nbytes / (mean * 1e-3) / 1e9
+        out[k] = {"ms": round(mean, 5), "median_ms": round(med, 5), "bytes": nbytes, "GB_s": round(gbs, 1),
+                  "roofline_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        total_ms += mean
+        total_b += nbytes
+    step = total_ms
+    return {"workload": "c4 pack + side ops: CIGN switch pack (new interaction, old weighting) K=3 + dropout-LN, "
+                        "add-LN, dropout-gamma-residual at p=0.5, forward + backward",
+            "nodes": N, "dim": D, "hops": K, "dtype": "f32", "ms_per_step": round(step, 5),
+            "algorithmic_bytes_per_step": total_b, "GB_s": round(total_b / (step * 1e-3) / 1e9, 1),
+            "roofline_frac": round(total_b / (step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "calls": out}
 
 
 def projected_layer(torch, w, dtype, steps, warmup, plan, X, grads, capture, ev):
