@@ -69,6 +69,11 @@ def parse():
                     help="--workload train: GraphCliffordNet layers (2: BASELINE config c4; 4 with --in-dim 300: the "
                          "Amazon-ratings production model of the reference's published step times)")
     ap.add_argument("--in-dim", type=int, default=256, help="--workload train: input feature width")
+    ap.add_argument("--dims", default="64,256,512",
+                    help="--workload c3: comma-separated feature widths (with --dtype: that dtype only)")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="default workload: skip the c3, c2+c3 bf16 and c4 rows that follow the headline layer "
+                         "(for profiles of the headline alone)")
     ap.add_argument("--no-scale", action="store_true",
                     help="default workload: skip the c5 measurement that follows the headline c2+c3 layer")
     ap.add_argument("--eager", action="store_true",
@@ -774,9 +779,12 @@ def main():
     if args.workload in ("c3", "c4pack"):
         from cign_amd import workloads
 
+        if args.calibrate_copy:
+            calibration_copy(torch, dev)
         if args.workload == "c3":
             w = workloads.build(workloads.C2, device=dev)
-            res = {"c3_multihop": [measure_multihop(torch, w, D, dt) for D in (64, 256, 512) for dt in ("f32", "bf16")]}
+            dts = (args.dtype,) if args.dtype else ("f32", "bf16")
+            res = {"c3_multihop": [measure_multihop(torch, w, int(D), dt) for D in args.dims.split(",") for dt in dts]}
         else:
             res = {"c4_pack": measure_c4_pack(torch)}
         print(json.dumps(res), flush=True)
@@ -803,17 +811,20 @@ def main():
     # The other BASELINE rows in the same run: c3 (the SpMM pipeline alone at
     # D = 64, 256, 512, fp32 and bf16), the c2+c3 layer in bf16, and the c4
     # pack + side ops.
-    line["c3_multihop"] = [measure_multihop(torch, w, D, dt) for D in (64, 256, 512) for dt in ("f32", "bf16")]
-    print("c3 done", file=sys.stderr, flush=True)
+    if not args.headline_only:
+        line["c3_multihop"] = [measure_multihop(torch, w, D, dt) for D in (64, 256, 512)
+                               for dt in ("f32", "bf16")]
+        print("c3 done", file=sys.stderr, flush=True)
     del w
-    lb, _ = measure_layer(torch, False, "bf16", args.steps, args.warmup, args.eager)
-    line["c2c3_bf16"] = {k: lb[k] for k in ("value", "unit", "ms_per_step", "median_gpu_ms_per_step", "dtype",
-                                           "layer_GB_s", "layer_roofline_frac", "algorithmic_bytes_per_step",
-                                           "layer_own_roofline_frac", "breakdown", "roofline") if k in lb}
-    if "c2_with_projection" in lb:
-        line["c2c3_bf16"]["c2_with_projection"] = lb["c2_with_projection"]
-    line["c4_pack"] = measure_c4_pack(torch)
-    print("c2+c3 bf16 and c4 pack done", file=sys.stderr, flush=True)
+    if not args.headline_only:
+        lb, _ = measure_layer(torch, False, "bf16", args.steps, args.warmup, args.eager)
+        line["c2c3_bf16"] = {k: lb[k] for k in ("value", "unit", "ms_per_step", "median_gpu_ms_per_step", "dtype",
+                                               "layer_GB_s", "layer_roofline_frac", "algorithmic_bytes_per_step",
+                                               "layer_own_roofline_frac", "breakdown", "roofline") if k in lb}
+        if "c2_with_projection" in lb:
+            line["c2c3_bf16"]["c2_with_projection"] = lb["c2_with_projection"]
+        line["c4_pack"] = measure_c4_pack(torch)
+        print("c2+c3 bf16 and c4 pack done", file=sys.stderr, flush=True)
     if not args.no_scale:
         # BASELINE config 5 in the same run: the layer at 2.4M nodes / 62.4M
         # edges (bf16, 4 x 32 heads, D = 256), the true HBM-bound case.
@@ -824,6 +835,17 @@ def main():
                                            "layer_own_roofline_frac", "breakdown", "roofline", "invariants")}
         line["scale"]["steps"] = max(3, min(args.steps, 20))
     print(json.dumps(line), flush=True)
+
+
+def calibration_copy(torch, dev):
+    """Three plain 256 MiB elementwise copies (x * 1 -> y, fp32) whose
+    FETCH_SIZE / WRITE_SIZE counters calibrate the per-kernel traffic."""
+    src = torch.ones(64 << 20, dtype=torch.float32, device=dev)  # 256 MiB
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
 
 
 def measure_layer(torch, scale: bool, dtype: str, steps: int, warmup: int, eager: bool = False,
@@ -883,12 +905,7 @@ def measure_layer(torch, scale: bool, dtype: str, steps: int, warmup: int, eager
             fwd_out["mh_bwd"] = [plan.backward3(g1, g2, g3)]
 
     if calibrate_copy:
-        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)  # 256 MiB
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            torch.mul(src, 1.0, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
+        calibration_copy(torch, dev)
 
     # Eager warmup: builds the row schedules (one host copy of each row
     # pointer) and the workspaces, and gives the reference outputs.

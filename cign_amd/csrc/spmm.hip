@@ -372,7 +372,10 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices];
 
-// Device address of `scratch` on the current device, looked up once per device.
+// Device address of `scratch` on the current device, looked up once per device
+// and kept for the life of the process: a hipDeviceReset (or unloading the
+// library's code object) invalidates it, and the entry point must not be
+// called on that device afterwards.
 int noalloc_scratch(const char* what, void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);

@@ -113,12 +113,20 @@ def test_sharded_gat_runs_the_whole_graphs_variant(c2, monkeypatch):
     check_sharded_layer(c2, ranges, torch.bfloat16, 4, 32, 256, 0.3, hops=False)
 
 
-def test_net_with_chunked_gat_matches_whole_graph():
+@pytest.mark.parametrize("amp", [False, True])
+def test_net_with_chunked_gat_matches_whole_graph(amp):
     """GraphCliffordNet at c1 with use_chunked_fused_gat (the graph prepared
     as nnz-balanced shards by its dgnn_chunk_* knobs) against the same model on
     the whole graph: logits, loss and every parameter gradient bit for bit,
     except the GAT biases (sums over all nodes, combined across shards), which
-    agree to fp32 rounding."""
+    agree to fp32 rounding. Under selective AMP the whole graph holds x_proj
+    in bf16 and runs the bf16-feature GAT kernels (lin_gat), while the shards
+    take float32 features holding the same bf16 values: the two sum in other
+    lane orders, so they agree to fp32 reassociation carried through the
+    later bf16 roundings, the bf16 bar (2e-2 relative plus one bf16 ulp of
+    each tensor's scale)."""
+    from tests.conftest import assert_close, bf16_flip_atol
+
     import torch.nn.functional as F
 
     from cign_amd import graph as G
@@ -136,7 +144,7 @@ def test_net_with_chunked_gat_matches_whole_graph():
     for chunked in (False, True):
         m = GraphCliffordNet(in_dim, D, classes, num_layers=2, order_set=(1, 2), gat_heads=heads, use_fused_gat=True,
                              use_chunked_fused_gat=chunked, dgnn_chunk_max_nodes=1500,
-                             dgnn_chunk_target_nodes=300).cuda().eval()
+                             dgnn_chunk_target_nodes=300, use_selective_amp=amp).cuda().eval()
         _randomize(m, 3)
         info = m.prepare_fused_gat_graph(gat_ei, n)
         if chunked:
@@ -153,6 +161,15 @@ def test_net_with_chunked_gat_matches_whole_graph():
         loss.backward()
         outs.append((logits, loss))
     torch.cuda.synchronize()
+    if amp:
+        np_ = lambda t: t.detach().double().cpu().numpy()
+        for i, name in enumerate(("logits", "loss")):
+            e = np_(outs[0][i])
+            assert_close(np_(outs[1][i]), e, rtol=2e-2, atol=1e-5 + bf16_flip_atol(e), name=name)
+        for (name, a), (_, b) in zip(models[0].named_parameters(), models[1].named_parameters()):
+            e = np_(a.grad)
+            assert_close(np_(b.grad), e, rtol=2e-2, atol=1e-5 + bf16_flip_atol(e), name=f"grad {name}")
+        return
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
     for (name, a), (_, b) in zip(models[0].named_parameters(), models[1].named_parameters()):
         if name.endswith("context_gat.bias"):

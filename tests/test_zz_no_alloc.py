@@ -58,14 +58,3 @@ def test_spmm_fwd3_noalloc_matches_workspace_entry(dtype):
     print(f"noalloc fwd3 {dtype}: n=4000 d=256 hub 3000, then n=900 d=64 hub 850", flush=True)
     _run_pair(lib, _graph(4000, 3000, 1), 256, dtype, 11)
     _run_pair(lib, _graph(900, 850, 2), 64, dtype, 12)
-
-
-def test_spmm_fwd3_noalloc_rejects_oversized_schedule():
-    from cign_amd import _lib
-
-    lib = _lib.load_library()
-    hdr = np.zeros(12, dtype=np.int32)
-    hdr[0], hdr[1], hdr[2] = 10, 1_000_000, 10  # a million segments of 512 columns: far beyond 15 MiB
-    rc = lib.cign_spmm_fwd3_noalloc(_lib.stream_ptr(), 0, 20, 512, None, None, None, hdr.ctypes.data, None, None,
-                                    None, None)
-    assert rc == 1 and b"scratch holds" in lib.cign_last_error()
