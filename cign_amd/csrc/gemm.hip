@@ -1029,6 +1029,305 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(const TG* gy, const flo
     }
 }
 
+// ---- Narrow projections (kSmallN < N <= 64 outputs: the c2 GAT lin, 300 -> 64)
+// The 128-row tiles above leave such a shape short of work: at the c2 lin
+// (M = 24,492) 192 workgroups, under one wavefront per SIMD, each a chain of
+// ten dependent K steps. Here a workgroup owns 32 rows and all (at most 64)
+// columns; wavefront w owns column tile w (16 columns) over all of K. The
+// 32 rows of x are one contiguous block of memory, staged through LDS in
+// chunks of 128 k by fully coalesced 16-byte loads (a direct fragment load
+// touches 16 rows per instruction and kept the texture units, not the
+// MFMAs, busy); W fragments come straight from L2, clamped in K where the
+// staged x is zero.
+constexpr int kNarrowN = 64;
+constexpr int kNarrowRows = 32;
+constexpr int kNarrowKC = 128;             // k per staged chunk (four K steps)
+constexpr int kNarrowLS = kNarrowKC + 4;   // LDS row stride: 132 = 4 mod 64 banks
+
+// W fragment of one K step for the wave's 16-column tile, laid out as the LDS
+// tile reads of mma_step give them: lane l holds W row n0 + l%16 (row N-1
+// past N: output columns that are never stored) at k0 + 4*(l/16) .. +3 and
+// k0 + 16 + 4*(l/16) .. +3 (fp32 math) or k0 + 8*(l/16) .. +7 (bf16 math).
+// With `clamp` (aligned rows, K % 4 == 0) offsets past K read the row's last
+// four values instead: their products meet staged x values of zero.
+template <int MATH>
+__device__ __forceinline__ void load_wfrag(const GemmArgs& g, int n0, int k0, int lane, bool clamp, float (&w)[8]) {
+  const int rl = lane & 15, ks = lane >> 4;
+  const int ka = MATH == kMathBF16 ? k0 + 8 * ks : k0 + 4 * ks;
+  const int kb = MATH == kMathBF16 ? ka + 4 : ka + 16;
+  const int n = n0 + rl;
+  const float* p = g.w + static_cast<int64_t>(n < g.N ? n : g.N - 1) * g.K;
+  float lo[4], hi[4];
+  if (clamp) {
+    gload_fast<float, 4>(p, min(ka, g.K - 4), lo);
+    gload_fast<float, 4>(p, min(kb, g.K - 4), hi);
+  } else {
+    gload<float, 4>(p, true, ka, g.K, false, lo);
+    gload<float, 4>(p, true, kb, g.K, false, hi);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    w[q] = lo[q];
+    w[4 + q] = hi[q];
+  }
+}
+
+// The MFMAs of one K step for one 16-column tile (mma_step's products, W the
+// first operand); bf16 math rounds both operands to bf16 here.
+template <int MATH>
+__device__ __forceinline__ void mma_direct(const XStep& a, const float (&w)[8], f32x4 (&acc)[2][1]) {
+  if constexpr (MATH == kMathBF16) {
+    bf16x8 wb;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) wb[q] = static_cast<__bf16>(w[q]);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      bf16x8 xa;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) xa[q] = static_cast<__bf16>(a.v[r][q]);
+      acc[r][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb, xa, acc[r][0], 0, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          acc[r][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 * h + q], a.v[r][4 * h + q], acc[r][0], 0, 0, 0);
+  }
+}
+
+// Four x values of the staged tile as fp32 (zero past M or K).
+template <typename TX>
+__device__ __forceinline__ void xload4(const TX* p, bool vec, int64_t m, int64_t M, int k, int K, float (&v)[4]) {
+  if constexpr (std::is_same_v<TX, float>) {
+    if (vec && m < M && k + 4 <= K) {
+      const float4 t = *reinterpret_cast<const float4*>(p);
+      v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+      return;
+    }
+  } else {
+    if (vec && m < M && k + 4 <= K) {
+      const uint2 t = *reinterpret_cast<const uint2*>(p);
+      v[0] = __uint_as_float(t.x << 16); v[1] = __uint_as_float(t.x & 0xffff0000u);
+      v[2] = __uint_as_float(t.y << 16); v[3] = __uint_as_float(t.y & 0xffff0000u);
+      return;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = (m < M && k + q < K) ? to_f32(p[q]) : 0.0f;
+}
+
+template <typename TX, int MATH, int EPI>
+__global__ __launch_bounds__(kThreads) void gemm_nt_narrow_kernel(GemmArgs g) {
+  __shared__ __align__(16) float xs[2][kNarrowRows * kNarrowLS];  // 33.8 KB
+  const int lane = lane_id();
+  const int n0 = 16 * __builtin_amdgcn_readfirstlane(wave_id());  // wave-uniform
+  const int rl = lane & 15, ks = lane >> 4;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kNarrowRows;
+  const TX* x = static_cast<const TX*>(g.x);
+  // x rows start 16-byte (fp32) or 8-byte (bf16) aligned
+  const bool xvec = g.vec;
+  const bool clamp = g.vec && g.K % 4 == 0;
+  constexpr int CPT = kNarrowRows * kNarrowKC / 4 / kThreads;  // four-value chunks per thread and chunk (4)
+  float st[CPT][4];
+  auto load_chunk = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      const int r = id / (kNarrowKC / 4), k = c * kNarrowKC + 4 * (id % (kNarrowKC / 4));
+      const int64_t m = row0 + r;
+      xload4<TX>(x + (m < g.M ? m : 0) * g.K + k, xvec, m, g.M, k, g.K, st[i]);
+    }
+  };
+  auto store_chunk = [&](float* d) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      const int r = id / (kNarrowKC / 4), k = 4 * (id % (kNarrowKC / 4));
+      *reinterpret_cast<float4*>(d + r * kNarrowLS + k) = make_float4(st[i][0], st[i][1], st[i][2], st[i][3]);
+    }
+  };
+  f32x4 acc[2][1];
+  acc[0][0] = acc[1][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int nk = (g.K + kBK - 1) / kBK;
+  const int nchunks = (g.K + kNarrowKC - 1) / kNarrowKC;
+  load_chunk(0);
+  store_chunk(xs[0]);
+  float w0[8], w1[8];
+  load_wfrag<MATH>(g, n0, 0, lane, clamp, w0);
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const bool more = c + 1 < nchunks;
+    if (more) load_chunk(c + 1);
+    const float* X = xs[c & 1];
+#pragma unroll
+    for (int t = 0; t < kNarrowKC / kBK; ++t) {
+      const int s = c * (kNarrowKC / kBK) + t;
+      if (s >= nk) break;  // uniform
+      // the next step's W fragment in flight during this step's MFMAs
+      if (s + 1 < nk) load_wfrag<MATH>(g, n0, (s + 1) * kBK, lane, clamp, (t & 1) ? w0 : w1);
+      XStep a;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const float* xr = X + (16 * r + rl) * kNarrowLS + t * kBK;
+        const int ka = MATH == kMathBF16 ? 8 * ks : 4 * ks;
+        const int kb = MATH == kMathBF16 ? ka + 4 : ka + 16;
+        const float4 lo = *reinterpret_cast<const float4*>(xr + ka);
+        const float4 hi = *reinterpret_cast<const float4*>(xr + kb);
+        a.v[r][0] = lo.x; a.v[r][1] = lo.y; a.v[r][2] = lo.z; a.v[r][3] = lo.w;
+        a.v[r][4] = hi.x; a.v[r][5] = hi.y; a.v[r][6] = hi.z; a.v[r][7] = hi.w;
+      }
+      mma_direct<MATH>(a, (t & 1) ? w1 : w0, acc);
+    }
+    if (more) store_chunk(xs[(c + 1) & 1]);
+    __syncthreads();
+  }
+  if (n0 < g.N) epilogue_swapped<EPI, 1>(g, acc, row0, n0, lane);
+}
+
+// grad_W partials of a narrow projection: a workgroup owns a row chunk, all
+// (at most 64) outputs n and 64 inputs k0 .. k0 + 63; its four wavefronts
+// take a quarter of the chunk's rows each for the whole 64 x 64 tile. The
+// reduction dimension is m, and 16-byte loads feed the MFMAs directly: for
+// four rows m .. m+3, lane l loads x[m + l/16][k0 + 4*(l%16) .. +3] and
+// grad_y[m + l/16][4*(l%16) .. +3] (each load four rows x 256 contiguous
+// bytes), and value i of the lane's x quad is operand row l%16 of "k tile" i,
+// the sixteen inputs k0 + 4r + i, r < 16 (strided, which the products do not
+// mind), likewise for n; the 4 x 4 tile pairs take sixteen 16 x 16 x 4 MFMAs
+// per two loads. A lane then holds, per n tile j and row r of its result
+// fragment, the four consecutive inputs k0 + 16*(l/16) + 4r .. +3 of output
+// n = 4*(l%16) + j: one 16-byte store. Columns past N or K are clamped to the
+// last aligned quad (outputs never stored); rows past the chunk read its last
+// row and count zero. Under bf16 math both operands are rounded to bf16
+// (exact products, fp32 sums, as the bf16 MFMA gives). The four wavefronts'
+// tiles are added in LDS in wave order and written as the chunk's partial;
+// colsum_kernel adds the chunks in order. Needs N and K multiples of 4 and
+// 16-byte (fp32) / 8-byte (bf16 grad_y) aligned rows.
+constexpr int kWnK = 64;          // k per workgroup tile
+constexpr int kWnChunkRows = 64;  // row chunks: four wavefronts x whole batches
+constexpr int kWnUnroll = 2;      // four-row groups per batch (two batches in flight)
+
+template <typename TG>
+__device__ __forceinline__ void load_quad(const TG* p, float (&v)[4]) {
+  if constexpr (std::is_same_v<TG, float>) {
+    const float4 t = *reinterpret_cast<const float4*>(p);
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+  } else {
+    const uint2 t = *reinterpret_cast<const uint2*>(p);
+    v[0] = __uint_as_float(t.x << 16); v[1] = __uint_as_float(t.x & 0xffff0000u);
+    v[2] = __uint_as_float(t.y << 16); v[3] = __uint_as_float(t.y & 0xffff0000u);
+  }
+}
+
+template <int MATH, typename TG>
+struct WnBatch {
+  float x[kWnUnroll][4], g[kWnUnroll][4];
+  // four-row groups m .. m + 4U - 1; rows past m1 read row m1 - 1
+  __device__ __forceinline__ void load(const TG* gy, const float* xs, int N, int K, int64_t m, int64_t m1, int kc,
+                                       int nc, int lane) {
+    const int ks = lane >> 4;
+#pragma unroll
+    for (int u = 0; u < kWnUnroll; ++u) {
+      const int64_t mr = m + 4 * u + ks;
+      const int64_t mc = mr < m1 ? mr : m1 - 1;
+      load_quad<float>(xs + mc * K + kc, x[u]);
+      load_quad<TG>(gy + mc * N + nc, g[u]);
+    }
+  }
+  __device__ __forceinline__ void mma(f32x4 (&acc)[4][4], int64_t m, int64_t m1, int lane) const {
+    const int ks = lane >> 4;
+#pragma unroll
+    for (int u = 0; u < kWnUnroll; ++u) {
+      const bool ok = m + 4 * u + ks < m1;
+      float xv[4], gv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xv[i] = ok ? (MATH == kMathBF16 ? round_bf16(x[u][i]) : x[u][i]) : 0.0f;
+        gv[i] = MATH == kMathBF16 ? round_bf16(g[u][i]) : g[u][i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], gv[j], acc[i][j], 0, 0, 0);
+    }
+  }
+};
+
+template <int MATH, typename TG = float>
+__global__ __launch_bounds__(kThreads) void wgrad_narrow_kernel(const TG* gy, const float* x, int64_t M, int N, int K,
+                                                                int64_t chunk, int nchunks, int ntk, float* part) {
+  __shared__ f32x4 red[3][16][kWave];  // waves 1..3: 16 accumulator tiles x 64 lanes (48 KB)
+  const int lane = lane_id();
+  // wave-uniform (the compiler cannot tell from threadIdx.x), so the row loop
+  // below is a scalar loop and the accumulators stay in place
+  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
+  int tile, cy;
+  if (!wg_tile_chunk(ntk, nchunks, true, tile, cy)) return;  // whole workgroup
+  const int k0 = tile * kWnK;
+  const int64_t c0 = static_cast<int64_t>(cy) * chunk;
+  const int64_t c1 = c0 + chunk < M ? c0 + chunk : M;
+  const int64_t q = chunk / 4;  // the wave's quarter of the chunk (a multiple of the batch rows)
+  const int64_t m0 = c0 + wave * q;
+  const int64_t m1 = m0 + q < c1 ? m0 + q : c1;
+  const int rl = lane & 15, ks = lane >> 4;
+  const int kc = min(k0 + 4 * rl, K - 4), nc = min(4 * rl, N - 4);
+  f32x4 acc[4][4];  // [k tile][n tile]
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr int B = 4 * kWnUnroll;  // rows per batch
+  if (m0 < m1) {
+    // Two batches in flight. Each batch's loads are issued right after its
+    // MFMAs and held there by scheduling barriers (the scheduler otherwise
+    // sinks them to their use, one memory round trip per batch); a batch
+    // past m1 (the last pair of a short quarter) counts zero.
+    WnBatch<MATH, TG> b0, b1;
+    b0.load(gy, x, N, K, m0, m1, kc, nc, lane);
+    b1.load(gy, x, N, K, m0 + B, m1, kc, nc, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int64_t m = m0; m < m1; m += 2 * B) {
+      b0.mma(acc, m, m1, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      b0.load(gy, x, N, K, m + 2 * B, m1, kc, nc, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      b1.mma(acc, m + B, m1, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      b1.load(gy, x, N, K, m + 3 * B, m1, kc, nc, lane);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[wave - 1][4 * i + j][lane] = acc[i][j];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; ++w)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] += red[w][4 * i + j][lane];
+  float* out = part + static_cast<int64_t>(cy) * N * K;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = 4 * rl + j;
+    if (n >= N) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int k = k0 + 16 * ks + 4 * r;
+      if (k >= K) continue;  // K % 4 == 0: the quad is whole or past K
+      *reinterpret_cast<float4*>(out + static_cast<int64_t>(n) * K + k) =
+          make_float4(acc[0][j][r], acc[1][j][r], acc[2][j][r], acc[3][j][r]);
+    }
+  }
+}
+
 // ---- Backward of a projection with few outputs (N <= kSmallN, e.g. the
 // classifier): two streaming passes on the VALU, where the library GEMMs
 // pick poor kernels for the degenerate shapes. Under autocast (RB) every
@@ -1754,6 +2053,16 @@ void launch_nt_bn(hipStream_t st, const GemmArgs& g, int bn, int64_t blocks, int
 
 template <typename TX, int MATH, int EPI>
 int launch_nt(hipStream_t st, const GemmArgs& g, int bn) {
+  if (g.N <= kNarrowN && (EPI != kEpiLogits || g.C == 16)) {
+    // at most 64 outputs: 32-row tiles, a 16-column tile per wavefront (the
+    // logits epilogue needs each head inside one wavefront's columns)
+    const int64_t blocks = (g.M + kNarrowRows - 1) / kNarrowRows;
+    if (blocks == 0) return kOk;
+    if (blocks > 0x7fffffff) return set_error(kInvalid, "cign linear: too many tiles");
+    hipLaunchKernelGGL((gemm_nt_narrow_kernel<TX, MATH, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
+                       0, st, g);
+    return check_launch("cign linear (narrow)");
+  }
   const int nrt = static_cast<int>((g.M + kBM - 1) / kBM);
   const int nct = (g.N + bn - 1) / bn;
   const int64_t blocks = static_cast<int64_t>(nrt) * nct;
@@ -1814,6 +2123,21 @@ inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias, bool xcd = true) {
   // chunks; the MFMA kernel takes chunks of >= 256 rows, about 512
   // workgroups over its 128 x 128 tiles
   const bool small = N <= kSmallN;
+  if (!small && N <= kNarrowN) {
+    // wgrad_narrow_kernel: 64-wide k tiles, chunks of a multiple of 64 rows
+    // (16-row batches per wavefront), about 512 workgroups, every tile of a
+    // chunk on one XCD
+    const int64_t ntk = (K + kWnK - 1) / kWnK;
+    int64_t wgc = wg_chunk_count(M, std::max<int64_t>(1, 512 / ntk), true);
+    L.wg_chunk = std::max<int64_t>(kWnChunkRows,
+                                   ((M + wgc - 1) / wgc + kWnChunkRows - 1) / kWnChunkRows * kWnChunkRows);
+    wgc = M > 0 ? (M + L.wg_chunk - 1) / L.wg_chunk : 1;
+    L.wg_chunks = static_cast<int>(wgc);
+    L.part_w = off; off = al(off + 4LL * wgc * N * K);
+    L.wt = off; off = al(off + 4LL * N * K);
+    L.total = off;
+    return L;
+  }
   const int64_t tiles = static_cast<int64_t>((N + kWgT - 1) / kWgT) * ((K + kWgT - 1) / kWgT);
   int64_t wgc = wg_chunk_count(M, std::max<int64_t>(1, 512 / tiles), xcd);
   L.wg_chunk = std::max<int64_t>(kWgM, ((M + wgc - 1) / wgc + kWgM - 1) / kWgM * kWgM);
@@ -2013,7 +2337,16 @@ int cign_linear_bwd_bf16gy(void* stream, int64_t M, int32_t N, int32_t K, const 
   int rc;
   if (M == 0) return rowops::zero_outputs(st, grad_w, N * K, nullptr, 0, "cign_linear_bwd_bf16gy");
   const bf16h* gy = static_cast<const bf16h*>(grad_y);
-  {
+  if (N <= kNarrowN && N % 4 == 0 && K % 4 == 0 && aligned16(grad_y) && aligned16(x)) {
+    const int ntk = (K + kWnK - 1) / kWnK;
+    float* part = reinterpret_cast<float*>(ws + L.part_w);
+    hipLaunchKernelGGL((wgrad_narrow_kernel<kMathBF16, bf16h>), dim3(wg_grid(ntk, L.wg_chunks, true)), dim3(kThreads),
+                       0, st, gy, x, M, N, K, L.wg_chunk, L.wg_chunks, ntk, part);
+    if ((rc = check_launch("cign_linear_bwd_bf16gy (grad_W partials, narrow)"))) return rc;
+    if ((rc = rowops::launch_colsum(st, part, L.wg_chunks, N * K, 1, grad_w, nullptr,
+                                    "cign_linear_bwd_bf16gy (grad_W)", true)))
+      return rc;
+  } else {
     const int ntk = (K + kWgT - 1) / kWgT;
     const dim3 grid(wg_grid(((N + kWgT - 1) / kWgT) * ntk, L.wg_chunks, true));
     const bool vec = N % 4 == 0 && K % 4 == 0 && aligned16(grad_y) && aligned16(x);
@@ -2085,7 +2418,21 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
     return bias_grad();
   }
   // grad_W [N,K] = grad_y^T x: split-M MFMA partials, then chunk sums.
-  {
+  if (N <= kNarrowN && N % 4 == 0 && K % 4 == 0 && aligned16(grad_y) && aligned16(x)) {
+    const int ntk = (K + kWnK - 1) / kWnK;
+    float* part = reinterpret_cast<float*>(ws + L.part_w);
+    const dim3 grid(wg_grid(ntk, L.wg_chunks, true));
+    if (math == kMathBF16)
+      hipLaunchKernelGGL(wgrad_narrow_kernel<kMathBF16>, grid, dim3(kThreads), 0, st, grad_y, x, M, N, K, L.wg_chunk,
+                         L.wg_chunks, ntk, part);
+    else
+      hipLaunchKernelGGL(wgrad_narrow_kernel<kMathF32>, grid, dim3(kThreads), 0, st, grad_y, x, M, N, K, L.wg_chunk,
+                         L.wg_chunks, ntk, part);
+    if ((rc = check_launch("cign_linear_bwd (grad_W partials, narrow)"))) return rc;
+    if ((rc = rowops::launch_colsum(st, part, L.wg_chunks, N * K, 1, grad_w, nullptr, "cign_linear_bwd (grad_W)",
+                                    rb)))
+      return rc;
+  } else {
     const int ntk = (K + kWgT - 1) / kWgT;
     const dim3 grid(wg_grid(((N + kWgT - 1) / kWgT) * ntk, L.wg_chunks, math == kMathBF16));
     const bool vec = N % 4 == 0 && K % 4 == 0 && aligned16(grad_y) && aligned16(x);
