@@ -117,6 +117,34 @@ def assert_bf16_sum_close(actual, expected_rounded, abs_terms_sum, n_terms, name
                              f"got {a[i]!r} expected {e[i]!r} bound {bound[i]!r}")
 
 
+def bf16_store_bound(exact, abs_terms, n_terms, carried=0.0):
+    """Elementwise bound of |a - e| for a result a that the GPU sums in
+    float32 and stores once as bf16, against the float64 oracle e of the same
+    sum on the same (bf16-rounded) inputs: the float32 sum s32 differs from
+    e by at most d = n 2^-24 sum|terms| (the summation bound gamma_n), and
+    rounding to bf16 moves it by at most half a bf16 spacing, 2^-8 |s32|, so
+    |a - e| <= 2^-8 (|e| + d) + d. `carried`: an error the inputs already
+    hold (earlier bf16 roundings in a chain, propagated through the sum's
+    absolute weights), added to both |e| and d."""
+    e = np.abs(np.asarray(exact, np.float64))
+    d = np.asarray(n_terms, np.float64) * 2.0 ** -24 * np.asarray(abs_terms, np.float64) + carried
+    return 2.0 ** -8 * (e + d) + d
+
+
+def assert_within(actual, expected, bound, name=""):
+    """|a - e| <= bound elementwise (a NaN matches only a NaN)."""
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    b = np.broadcast_to(np.asarray(bound, np.float64), e.shape)
+    assert a.shape == e.shape, f"{name}: shape {a.shape} != {e.shape}"
+    err = np.abs(a - e)
+    bad = ~(err <= b) & ~(np.isnan(a) & np.isnan(e))
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - b), a.shape)
+        raise AssertionError(f"{name}: {int(bad.sum())} of {a.size} outside the derived bound; worst at {i}: "
+                             f"got {a[i]!r} expected {e[i]!r} bound {b[i]!r}")
+
+
 def bf16_flip_atol(expected):
     """Extra absolute tolerance of a selective-bf16 result compared with an
     oracle that rounds to bf16 at the same points: where fp32 (GPU) and fp64

@@ -1,8 +1,11 @@
 """GPU parity of the collapsed GAT (forward + backward) against the oracle,
 through the drop-in API (collapsed_gat.ensure_collapsed_gat_loaded().forward/
 backward and collapsed_gat_mean_bias_silu with autograd), which calls the
-C-ABI. Tolerances: fp32 1e-4 rel / 1e-5 abs; bf16 2e-2 rel. Dropout masks and
-CSR/CSC/perm are bit-exact."""
+C-ABI. Tolerances: fp32 1e-4 rel / 1e-5 abs; outputs stored in bf16 (from
+fp32 math on bf16 inputs, the oracle on the same rounded inputs) 2e-2
+relative with a 1e-5 absolute floor (one bf16 rounding is 2^-8 relative;
+the floor covers fp32 rounding near zero). Dropout masks and CSR/CSC/perm
+are bit-exact."""
 import numpy as np
 import pytest
 import torch
@@ -11,7 +14,7 @@ from oracle import cign_oracle as O
 from tests.conftest import assert_close, random_gat_graph
 
 pytestmark = pytest.mark.gpu
-TOL = {torch.float32: dict(rtol=1e-4, atol=1e-5), torch.bfloat16: dict(rtol=2e-2, atol=2e-2)}
+TOL = {torch.float32: dict(rtol=1e-4, atol=1e-5), torch.bfloat16: dict(rtol=2e-2, atol=1e-5)}
 
 
 def _graph(rng, n, hubs):
@@ -171,7 +174,7 @@ def test_autograd_full_c2(c2, dtype):
     f = O.collapsed_gat_forward(*args)
     g = O.collapsed_gat_backward(*args, gy.double().cpu().numpy())
     t = TOL[torch.float32]
-    tl = t if dtype == torch.float32 else dict(rtol=2e-2, atol=1e-5)
+    tl = TOL[dtype]
     assert_close(y.detach().double().cpu().numpy(), f["out"], name="out", **tl)
     assert x.grad.dtype == dtype
     assert_close(x.grad.double().cpu().numpy(), g["grad_feat"], name="grad_feat", **tl)

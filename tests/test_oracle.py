@@ -753,3 +753,34 @@ def test_assert_close_rejects_nan():
     with pytest.raises(AssertionError):
         assert_close_fp32_derived(a, e, e)
     assert_close(a, a, rtol=1e-4, atol=1e-5)
+
+
+def test_bf16_store_bound_covers_fp32_sums_stored_in_bf16(rng):
+    """conftest.bf16_store_bound: float32 sums of products (row sums of a
+    random sparse-like matrix, sequential and pairwise orders) rounded once to
+    bf16 lie within the bound around the float64 sum; a result two bf16
+    spacings away (a rounding too many, or a dropped term of that size)
+    does not; and an input error carried through |P| widens it exactly by
+    that propagated amount."""
+    import torch
+
+    from tests.conftest import assert_within, bf16_store_bound
+
+    n, k = 400, 37
+    P = rng.random((n, k)) * (rng.random((n, k)) < 0.5)
+    x = O.bf16_round(rng.standard_normal(k))
+    exact = P @ x
+    terms = np.abs(P) @ np.abs(x)
+    bound = bf16_store_bound(exact, terms, k)
+    P32, x32 = P.astype(np.float32), x.astype(np.float32)
+    for sums in (np.array([np.float32(sum(np.float32(p) * np.float32(v) for p, v in zip(row, x32))) for row in P32]),
+                 (P32 @ x32).astype(np.float32)):
+        stored = torch.from_numpy(sums).to(torch.bfloat16).double().numpy()
+        assert_within(stored, exact, bound, "fp32 sum stored in bf16")
+    off = exact + 2 * 2.0 ** -7 * np.abs(exact) + 1e-3
+    with pytest.raises(AssertionError, match="outside the derived bound"):
+        assert_within(off, exact, bound, "two spacings off")
+    carried = np.full(k, 1e-3)
+    wider = bf16_store_bound(exact, terms, k, np.abs(P) @ carried)
+    assert np.all(wider > bound)
+    assert np.allclose(wider - bound, (1 + 2.0 ** -8) * (np.abs(P) @ carried))
