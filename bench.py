@@ -57,11 +57,13 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="bounded sample of each CPU baseline, seconds (0 disables)")
-    ap.add_argument("--workload", choices=["layer", "scale", "block", "train", "c3", "c4pack"], default="layer",
+    ap.add_argument("--workload", choices=["layer", "scale", "block", "train", "c3", "c4pack", "c2proj"],
+                    default="layer",
                     help="layer: the headline c2+c3 layer (24,492 nodes); scale: the same layer at c5 size "
                          "(2.4M nodes, ~62M edges, GAT 4x32 + SpMM D=256, bf16 by default); c3: the 3-hop SpMM "
                          "pipeline alone at D = 64, 256, 512 in fp32 and bf16; c4pack: the Clifford pack and the "
-                         "side ops of BASELINE config c4 (N=24,492, D=256, p=0.5); block: the full "
+                         "side ops of BASELINE config c4 (N=24,492, D=256, p=0.5); c2proj: the c2 step with its "
+                         "300 -> 4x16 projection alone (fp32, or bf16 autocast with --dtype bf16); block: the full "
                          "Clifford block forward+backward at the production shape (D=256, 6 GAT heads, hops 1-3) "
                          "with every component kernel timed against its own roofline (bf16 = selective AMP GEMMs)")
     ap.add_argument("--dtype", choices=["f32", "bf16"], default=None)
@@ -776,12 +778,14 @@ def main():
             args.dtype = "bf16"
         run_train(args, torch)
         return
-    if args.workload in ("c3", "c4pack"):
+    if args.workload in ("c3", "c4pack", "c2proj"):
         from cign_amd import workloads
 
         if args.calibrate_copy:
             calibration_copy(torch, dev)
-        if args.workload == "c3":
+        if args.workload == "c2proj":
+            res = {"c2_with_projection": measure_c2proj(torch, args.dtype or "f32", args.steps, args.warmup)}
+        elif args.workload == "c3":
             w = workloads.build(workloads.C2, device=dev)
             dts = (args.dtype,) if args.dtype else ("f32", "bf16")
             res = {"c3_multihop": [measure_multihop(torch, w, int(D), dt) for D in args.dims.split(",") for dt in dts]}
@@ -1186,6 +1190,36 @@ def measure_c4_pack(torch):
             "nodes": N, "dim": D, "hops": K, "dtype": "f32", "ms_per_step": round(step, 5),
             "algorithmic_bytes_per_step": total_b, "GB_s": round(total_b / (step * 1e-3) / 1e9, 1),
             "roofline_frac": round(total_b / (step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "calls": out}
+
+
+def measure_c2proj(torch, dtype, steps, warmup):
+    """projected_layer on its own: the c2 graph, the 3-hop plan at D = 64 and
+    its gradient probes, HIP-graph replays as in the headline run."""
+    from cign_amd import workloads
+    from cign_amd.multihop_csr_pipeline import MultiHopCSR3GraphOperator
+
+    dev = torch.device("cuda:0")
+    dt = torch.float32 if dtype == "f32" else torch.bfloat16
+    w = workloads.build(workloads.C2, device=dev)
+    g = torch.Generator(device="cpu").manual_seed(0)
+    X = torch.randn(w.n, 64, generator=g).to(dev).to(dt)
+    grads = tuple(torch.randn(w.n, 64, generator=g).to(dev).to(dt) for _ in range(3))
+    plan = MultiHopCSR3GraphOperator(w.operator, dense_cols=64, dense_dtype=dt).plan
+
+    def capture(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            fn()
+        return gr
+
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    return projected_layer(torch, w, dtype, steps, warmup, plan, X, grads, capture, ev)
 
 
 def projected_layer(torch, w, dtype, steps, warmup, plan, X, grads, capture, ev):
