@@ -1207,7 +1207,7 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_narrow_kernel(GemmArgs g) {
 // 16-byte (fp32) / 8-byte (bf16 grad_y) aligned rows.
 constexpr int kWnK = 64;          // k per workgroup tile
 constexpr int kWnChunkRows = 64;  // row chunks: four wavefronts x whole batches
-constexpr int kWnUnroll = 2;      // four-row groups per batch (two batches in flight)
+constexpr int kWnUnroll = 2;       // four-row groups per batch (two batches in flight; 4 measured slower)
 
 template <typename TG>
 __device__ __forceinline__ void load_quad(const TG* p, float (&v)[4]) {
@@ -2128,6 +2128,8 @@ inline BwdWs bwd_ws(int64_t M, int N, int K, bool bias, bool xcd = true) {
     // (16-row batches per wavefront), about 512 workgroups, every tile of a
     // chunk on one XCD
     const int64_t ntk = (K + kWnK - 1) / kWnK;
+    // (about 512: fewer workgroups left the chip short, more spent longer
+    // on the chunk partials and their sums than they saved, at the c2 lin)
     int64_t wgc = wg_chunk_count(M, std::max<int64_t>(1, 512 / ntk), true);
     L.wg_chunk = std::max<int64_t>(kWnChunkRows,
                                    ((M + wgc - 1) / wgc + kWnChunkRows - 1) / kWnChunkRows * kWnChunkRows);
