@@ -381,7 +381,9 @@ int64_t cign_pack_proj_bwd_workspace_bytes(int64_t n, int32_t D, int32_t K);
  * grad_b (NULL to skip) = sum_n grad_g. With gate_weight (the node gate of
  * cign_hop_gate_fwd that produced alpha, stride K), the gate's backward is
  * added: its input terms into grad_H / grad_C, grad_gate_weight [K,2D],
- * grad_gate_bias [K]. Replaces the autograd of the same lines. */
+ * grad_gate_bias [K]. With math = 1, grad_G, grad_w and grad_b are rounded to
+ * bf16 (autocast's backward outputs) and the products read bf16 operands.
+ * Replaces the autograd of the same lines. */
 int cign_pack_proj_bwd(void* stream, int64_t n, int32_t D, int32_t K, int32_t interaction, int32_t math,
                        const float* grad_g, const float* H, const float* C, const float* const* props,
                        int64_t prop_stride, const float* alpha, int64_t alpha_stride, const float* w,
@@ -468,8 +470,11 @@ int64_t cign_linear_bwd_workspace_bytes(int64_t M, int32_t N, int32_t K, int32_t
  * W^T, which the workspace holds), grad_w [N,K] =
  * grad_y^T x (split-M MFMA partials summed in order) and grad_b [N] =
  * sum_m grad_y (NULL to skip), fp32 accumulation, grad_w and grad_b
- * deterministic; with math = 1 every product reads bf16-rounded operands (the
- * autocast backward). N <= 16 runs two VALU streaming kernels instead. grad_y,
+ * deterministic; with math = 1 every product reads bf16-rounded operands and
+ * grad_x, grad_w, grad_b are rounded to bf16 (grad_b the sum of the rounded
+ * grad_y): the outputs of the bf16 Linear's backward under autocast. N <= 16
+ * runs two VALU streaming kernels instead, N <= 64 narrow-output MFMA kernels.
+ * grad_y,
  * x float32. Replaces the autograd backward of the Linear layers above. */
 int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math, const float* grad_y, const float* x,
                     const float* w, float* grad_x, float* grad_w, float* grad_b, void* workspace,
