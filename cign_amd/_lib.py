@@ -76,6 +76,8 @@ _SIGNATURES = {
     "cign_linear_bwd_workspace_bytes": (_I64, [_I64, _I32, _I32, _I32]),
     "cign_linear_bwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _I64]),
     "cign_linear_bwd_bf16gy": (C.c_int, [_P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _I64]),
+    "cign_lin_logits_wgrad_workspace_bytes": (_I64, [_I64, _I32, _I32]),
+    "cign_lin_logits_wgrad": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _I32] + [_P] * 11 + [_I64]),
     "cign_pack_proj_fwd_workspace_bytes": (_I64, [_I32, _I32, _I32]),
     "cign_pack_proj_fwd": (C.c_int, [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _I64, _P, _I64, _P, _P, _P, _P,
                                      _F32, _U64, _P, _P, _P, _P, _I64]),

@@ -35,6 +35,7 @@
 // column l%16 and the same k-slice, D holds rows 4*(l/16)+i, i < 4, of
 // column l%16.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "clifford.h"
@@ -1042,7 +1043,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(const TG* gy, const flo
 constexpr int kNarrowN = 64;
 constexpr int kNarrowRows = 32;
 constexpr int kNarrowKC = 128;             // k per staged chunk (four K steps)
-constexpr int kNarrowLS = kNarrowKC + 4;   // LDS row stride: 132 = 4 mod 64 banks
+constexpr int kNarrowLS = kNarrowKC + 8;   // LDS row stride: 136 = 8 x odd (mod 64): the fastest fragment reads
 
 // W fragment of one K step for the wave's 16-column tile, laid out as the LDS
 // tile reads of mma_step give them: lane l holds W row n0 + l%16 (row N-1
@@ -1119,17 +1120,43 @@ __device__ __forceinline__ void xload4(const TX* p, bool vec, int64_t m, int64_t
   for (int q = 0; q < 4; ++q) v[q] = (m < M && k + q < K) ? to_f32(p[q]) : 0.0f;
 }
 
-template <typename TX, int MATH, int EPI>
+// Four x values at k of row m for the aligned path (`vec`: rows 16-byte
+// (fp32) or 8-byte (bf16) aligned, K % 4 == 0): the row is clamped to M - 1
+// (its products land in output rows that are never stored) and the offset to
+// K - 4; the LDS store writes zeros for k >= K (a select once the data is
+// there: zeroing the registers here would wait for the load).
+template <typename TX>
+__device__ __forceinline__ void xload4_vec(const TX* x, int64_t m, int64_t M, int k, int K, float (&v)[4]) {
+  const int64_t mc = m < M ? m : M - 1;
+  const int kc = k < K ? k : K - 4;
+  if constexpr (std::is_same_v<TX, float>) {
+    const float4 t = *reinterpret_cast<const float4*>(x + mc * K + kc);
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+  } else {
+    const uint2 t = *reinterpret_cast<const uint2*>(x + mc * K + kc);
+    v[0] = __uint_as_float(t.x << 16); v[1] = __uint_as_float(t.x & 0xffff0000u);
+    v[2] = __uint_as_float(t.y << 16); v[3] = __uint_as_float(t.y & 0xffff0000u);
+  }
+}
+
+// The loop issues the next chunk's loads (its W fragments, then its x) before
+// the current chunk's MFMAs, which read only LDS and W fragments that arrived
+// during the previous chunk: the loads wait once per chunk, at the LDS store,
+// so a chunk's memory latency overlaps the previous chunk's MFMAs. (Loads
+// return in issue order, so a W fragment issued after the x loads could not
+// be waited for without them.) VEC: the aligned path (g.vec), branch-free.
+template <typename TX, int MATH, int EPI, bool VEC>
 __global__ __launch_bounds__(kThreads) void gemm_nt_narrow_kernel(GemmArgs g) {
-  __shared__ __align__(16) float xs[2][kNarrowRows * kNarrowLS];  // 33.8 KB
+  __shared__ __align__(16) float xs[2][kNarrowRows * kNarrowLS];  // 34.8 KB
+  constexpr int SPC = kNarrowKC / kBK;                             // K steps per chunk (4)
   const int lane = lane_id();
   const int n0 = 16 * __builtin_amdgcn_readfirstlane(wave_id());  // wave-uniform
   const int rl = lane & 15, ks = lane >> 4;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kNarrowRows;
   const TX* x = static_cast<const TX*>(g.x);
-  // x rows start 16-byte (fp32) or 8-byte (bf16) aligned
-  const bool xvec = g.vec;
-  const bool clamp = g.vec && g.K % 4 == 0;
+  // g.vec: x and W rows start 16-byte (fp32) / 8-byte (bf16) aligned and
+  // K % 4 == 0, so W offsets clamp to the row's last aligned quad
+  const bool clamp = VEC || (g.vec && g.K % 4 == 0);
   constexpr int CPT = kNarrowRows * kNarrowKC / 4 / kThreads;  // four-value chunks per thread and chunk (4)
   float st[CPT][4];
   auto load_chunk = [&](int c) {
@@ -1138,53 +1165,309 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_narrow_kernel(GemmArgs g) {
       const int id = threadIdx.x + i * kThreads;
       const int r = id / (kNarrowKC / 4), k = c * kNarrowKC + 4 * (id % (kNarrowKC / 4));
       const int64_t m = row0 + r;
-      xload4<TX>(x + (m < g.M ? m : 0) * g.K + k, xvec, m, g.M, k, g.K, st[i]);
+      if constexpr (VEC)
+        xload4_vec<TX>(x, m, g.M, k, g.K, st[i]);
+      else
+        xload4<TX>(x + (m < g.M ? m : 0) * g.K + k, g.vec, m, g.M, k, g.K, st[i]);
     }
   };
-  auto store_chunk = [&](float* d) {
+  auto store_chunk = [&](int c, float* d) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int id = threadIdx.x + i * kThreads;
       const int r = id / (kNarrowKC / 4), k = 4 * (id % (kNarrowKC / 4));
-      *reinterpret_cast<float4*>(d + r * kNarrowLS + k) = make_float4(st[i][0], st[i][1], st[i][2], st[i][3]);
+      const bool in = !VEC || c * kNarrowKC + k < g.K;
+      *reinterpret_cast<float4*>(d + r * kNarrowLS + k) =
+          in ? make_float4(st[i][0], st[i][1], st[i][2], st[i][3]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
+  };
+  // the W fragments of chunk c's K steps (offsets past K clamped or zero)
+  auto load_w = [&](int c, float (&w)[SPC][8]) {
+#pragma unroll
+    for (int t = 0; t < SPC; ++t) load_wfrag<MATH>(g, n0, (c * SPC + t) * kBK, lane, clamp, w[t]);
   };
   f32x4 acc[2][1];
   acc[0][0] = acc[1][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const int nk = (g.K + kBK - 1) / kBK;
   const int nchunks = (g.K + kNarrowKC - 1) / kNarrowKC;
-  load_chunk(0);
-  store_chunk(xs[0]);
-  float w0[8], w1[8];
-  load_wfrag<MATH>(g, n0, 0, lane, clamp, w0);
-  __syncthreads();
-  for (int c = 0; c < nchunks; ++c) {
-    const bool more = c + 1 < nchunks;
-    if (more) load_chunk(c + 1);
+  // chunk c's MFMAs; `tail`: the last chunk, whose K steps past K are skipped
+  auto compute = [&](int c, const float (&w)[SPC][8], bool tail) {
     const float* X = xs[c & 1];
 #pragma unroll
-    for (int t = 0; t < kNarrowKC / kBK; ++t) {
-      const int s = c * (kNarrowKC / kBK) + t;
-      if (s >= nk) break;  // uniform
-      // the next step's W fragment in flight during this step's MFMAs
-      if (s + 1 < nk) load_wfrag<MATH>(g, n0, (s + 1) * kBK, lane, clamp, (t & 1) ? w0 : w1);
-      XStep a;
+    for (int t = 0; t < SPC; ++t) {
+      if (!tail || c * SPC + t < nk) {  // uniform
+        XStep a;
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const float* xr = X + (16 * r + rl) * kNarrowLS + t * kBK;
-        const int ka = MATH == kMathBF16 ? 8 * ks : 4 * ks;
-        const int kb = MATH == kMathBF16 ? ka + 4 : ka + 16;
-        const float4 lo = *reinterpret_cast<const float4*>(xr + ka);
-        const float4 hi = *reinterpret_cast<const float4*>(xr + kb);
-        a.v[r][0] = lo.x; a.v[r][1] = lo.y; a.v[r][2] = lo.z; a.v[r][3] = lo.w;
-        a.v[r][4] = hi.x; a.v[r][5] = hi.y; a.v[r][6] = hi.z; a.v[r][7] = hi.w;
+        for (int r = 0; r < 2; ++r) {
+          const float* xr = X + (16 * r + rl) * kNarrowLS + t * kBK;
+          const int ka = MATH == kMathBF16 ? 8 * ks : 4 * ks;
+          const int kb = MATH == kMathBF16 ? ka + 4 : ka + 16;
+          const float4 lo = *reinterpret_cast<const float4*>(xr + ka);
+          const float4 hi = *reinterpret_cast<const float4*>(xr + kb);
+          a.v[r][0] = lo.x; a.v[r][1] = lo.y; a.v[r][2] = lo.z; a.v[r][3] = lo.w;
+          a.v[r][4] = hi.x; a.v[r][5] = hi.y; a.v[r][6] = hi.z; a.v[r][7] = hi.w;
+        }
+        mma_direct<MATH>(a, w[t], acc);
       }
-      mma_direct<MATH>(a, (t & 1) ? w1 : w0, acc);
     }
-    if (more) store_chunk(xs[(c + 1) & 1]);
+  };
+  // a chunk that is not the last: the next chunk's loads in flight, this
+  // chunk's MFMAs, then the next chunk's x into the other buffer. No branch
+  // around the loads, so the only wait on them is at the LDS store.
+  auto step = [&](int c, const float (&wcur)[SPC][8], float (&wnext)[SPC][8]) {
+    load_w(c + 1, wnext);
+    load_chunk(c + 1);
+    __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs
+    compute(c, wcur, false);
+    __builtin_amdgcn_sched_barrier(0);  // the store's wait for x after the MFMAs
+    store_chunk(c + 1, xs[(c + 1) & 1]);
     __syncthreads();
+  };
+  float wa[SPC][8], wb[SPC][8];
+  load_w(0, wa);
+  load_chunk(0);
+  store_chunk(0, xs[0]);
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+  int c = 0;
+  for (; c + 2 < nchunks; c += 2) {
+    step(c, wa, wb);
+    step(c + 1, wb, wa);
+  }
+  if (c + 1 < nchunks) {
+    step(c, wa, wb);
+    compute(c + 1, wb, true);
+  } else {
+    compute(c, wa, true);
   }
   if (n0 < g.N) epilogue_swapped<EPI, 1>(g, acc, row0, n0, lane);
+}
+
+// ---- Narrow fp32 projections with W in registers (128 <= K <= 304)
+// The kernel above reads each workgroup's W fragments from L2 per K step and
+// syncs per chunk. Here each wavefront loads the W fragments of its
+// 16-column tile for all of K once (NB = K/16 rounded up float4 per lane:
+// lane l holds W[16 w + l%16][16 b + 4*(l/16) .. +3] for block b) and keeps
+// them in registers, and the workgroup walks 16-row x tiles t = blockIdx.x,
+// + gridDim.x, ..., double-buffered in LDS: the next tile's loads are issued
+// before the current tile's MFMAs, which read one float4 of LDS per four
+// 16 x 16 x 4 MFMAs (x value q of the lane's quad is k-slot l/16 of MFMA q,
+// as in the W fragment, so the products pair up; two accumulators). Three
+// workgroups per CU (three wavefronts per SIMD) cover one another's
+// stores, epilogues and barriers. K is zero-padded to whole 16-k blocks; W
+// rows past N are zero. Needs g.vec (rows 16-byte aligned, K % 4 == 0).
+// Measured at the c2 lin (24,492 x 300 -> 64, fp32): 17.3 us against 18.3
+// for the kernel above; variants with W staged once per CU in LDS (one
+// workgroup of eight wavefronts, or x fragments in registers with one
+// wavefront per SIMD) took 18.2-19.3 us. The floor is the fp32 MFMA work
+// (7.1 us at the 2.06 GHz this kernel runs at) behind a first x round that
+// no wavefront can compute without.
+constexpr int kNrRows = 16;
+constexpr int kNrMinK = 128;
+constexpr int kNrMaxK = 304;
+// LDS row stride: 8 x odd (mod 64 floats). Measured ds_read_b128 rates of
+// this fragment pattern (lane l: row l%16, column 4*(l/16)) on MI355X: 166-175
+// B/clk per CU for strides of 8 x odd mod 64, as fast as linear reads; about
+// 123 for 4 x odd, 63 for 32 mod 64, 31 for 0 mod 64.
+// Under bf16 math K is padded to 32-k blocks (up to 320 values a row).
+template <int MATH>
+constexpr int nr_stride() { return MATH == kMathBF16 ? 320 + 8 : kNrMaxK + 8; }
+constexpr int kNrXq = 5;      // x float4 per thread and tile: 16 lanes per row, quads slot + 16 j, j < 5
+constexpr int kNrPerCu = 3;  // workgroups per CU (VGPR-bound)
+
+// MATH: fp32 (NB 16-k blocks, 16 x 16 x 4 MFMAs) or bf16 (NB 32-k blocks:
+// lane l's fragments are k = 32 b + 8*(l/16) .. +7 of its row, both operands
+// rounded to bf16, one 16 x 16 x 32 MFMA per block).
+template <int EPI, int NB, int MATH>
+__global__ __launch_bounds__(kThreads) void gemm_nt_narrow_r_kernel(GemmArgs g, int ntiles) {
+  constexpr int kNrS = nr_stride<MATH>();
+  constexpr int KB = MATH == kMathBF16 ? 32 : 16;  // k per block
+  __shared__ __align__(16) float xs[2][kNrRows * kNrS];  // 39.9 KB (fp32), 42.0 KB (bf16)
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int ct = __builtin_amdgcn_readfirstlane(wave_id());  // the wave's 16-column tile
+  const int rl = lane & 15, ks = lane >> 4;
+  const int K = g.K;
+  const int Q = K / 4;  // data quads per row
+  constexpr int QP = KB / 4 * NB;
+  static_assert(QP <= 16 * kNrXq && 4 * QP <= kNrS, "x tile slots");
+  const float* x = static_cast<const float*>(g.x);
+  // x tile slots: row xrow, quads xslot + 16 j (16 lanes read 256 contiguous bytes)
+  const int xrow = tid >> 4, xslot = tid & 15;
+  float4 st[kNrXq];
+  auto load_x = [&](int t) {
+    const int64_t m = static_cast<int64_t>(t) * kNrRows + xrow;
+    const float* p = x + (m < g.M ? m : g.M - 1) * K;  // rows past M: outputs never stored
+#pragma unroll
+    for (int j = 0; j < kNrXq; ++j) {
+      const int q = xslot + 16 * j;
+      st[j] = *reinterpret_cast<const float4*>(p + 4 * (q < Q ? q : Q - 1));
+    }
+  };
+  auto store_x = [&](float* d) {
+#pragma unroll
+    for (int j = 0; j < kNrXq; ++j) {
+      const int q = xslot + 16 * j;
+      if (q < QP) *reinterpret_cast<float4*>(d + xrow * kNrS + 4 * q) = q < Q ? st[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  };
+  // W fragments (loads first, so waiting for them does not wait for x)
+  const int wn = 16 * ct + rl;
+  constexpr int WQ = KB / 16;  // float4 of W per lane and block
+  float4 w[NB][WQ];
+  {
+    const float* p = g.w + static_cast<int64_t>(wn < g.N ? wn : g.N - 1) * K;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int h = 0; h < WQ; ++h) {
+        const int k = KB * b + 4 * WQ * ks + 4 * h;
+        w[b][h] = *reinterpret_cast<const float4*>(p + (k < K ? k : K - 4));
+      }
+  }
+  int t = blockIdx.x;
+  load_x(t);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int h = 0; h < WQ; ++h)
+      if (wn >= g.N || KB * b + 4 * WQ * ks + 4 * h >= K) w[b][h] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  [[maybe_unused]] bf16x8 wb16[MATH == kMathBF16 ? NB : 1];
+  if constexpr (MATH == kMathBF16) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      wb16[b] = bf16x8{static_cast<__bf16>(w[b][0].x), static_cast<__bf16>(w[b][0].y), static_cast<__bf16>(w[b][0].z),
+                       static_cast<__bf16>(w[b][0].w), static_cast<__bf16>(w[b][1].x), static_cast<__bf16>(w[b][1].y),
+                       static_cast<__bf16>(w[b][1].z), static_cast<__bf16>(w[b][1].w)};
+  }
+  store_x(xs[0]);
+  // the lane's output columns nc0 .. nc0 + 3: bias and attention vectors
+  const int nc0 = 16 * ct + 4 * ks;
+  const bool cols = 16 * ct < g.N;
+  const bool full4 = g.vec4 && nc0 + 4 <= g.N;
+  const int H = EPI == kEpiLogits ? g.N / g.C : 0;
+  float bv[4], as[4], ad[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int n = nc0 + q;
+    // autocast casts the bias to bf16 with the other operands
+    const float bq = (g.bias && n < g.N) ? g.bias[n] : 0.0f;
+    bv[q] = g.round_bf16 ? round_bf16(bq) : bq;
+    as[q] = ad[q] = 0.0f;
+    if constexpr (EPI == kEpiLogits) {
+      if (n < g.N) {
+        as[q] = g.att_src[n];  // head ct (C == 16), channel n - 16 ct: offset ct * C + (n - ct * C) = n
+        ad[q] = g.att_dst[n];
+      }
+    }
+  }
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+  for (int i = 0; t < ntiles; ++i, t += gridDim.x) {
+    // the next tile's x (the last tile re-reads itself, from L2: no branch
+    // around the loads, whose only wait is at the LDS store)
+    const int tn = t + static_cast<int>(gridDim.x) < ntiles ? t + static_cast<int>(gridDim.x) : t;
+    load_x(tn);
+    __builtin_amdgcn_sched_barrier(0);  // the next tile's loads ahead of the MFMAs
+    const float* xp = xs[i & 1] + rl * kNrS + 4 * WQ * ks;
+    f32x4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (MATH == kMathBF16) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float4 lo = *reinterpret_cast<const float4*>(xp + KB * b);
+        const float4 hi = *reinterpret_cast<const float4*>(xp + KB * b + 4);
+        const bf16x8 xb{static_cast<__bf16>(lo.x), static_cast<__bf16>(lo.y), static_cast<__bf16>(lo.z),
+                        static_cast<__bf16>(lo.w), static_cast<__bf16>(hi.x), static_cast<__bf16>(hi.y),
+                        static_cast<__bf16>(hi.z), static_cast<__bf16>(hi.w)};
+        // one chain in block order: the sums of the narrow kernel above
+        // (cign_linear_bwd_bf16gy's grad_x takes that kernel on bf16 storage
+        // and must match cign_linear_bwd's bit for bit)
+        a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wb16[b], xb, a0, 0, 0, 0);
+      }
+    } else {
+      float4 xv = *reinterpret_cast<const float4*>(xp);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const float4 xn = *reinterpret_cast<const float4*>(xp + 16 * (b + 1 < NB ? b + 1 : b));
+        a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(w[b][0].x, xv.x, a0, 0, 0, 0);
+        a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(w[b][0].y, xv.y, a1, 0, 0, 0);
+        a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(w[b][0].z, xv.z, a0, 0, 0, 0);
+        a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(w[b][0].w, xv.w, a1, 0, 0, 0);
+        xv = xn;
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the store's wait for x after the MFMAs
+    store_x(xs[(i + 1) & 1]);
+    // epilogue (epilogue_swapped's for one 16 x 16 tile, with the bias and
+    // attention vectors loaded once per workgroup above)
+    const int64_t m = static_cast<int64_t>(t) * kNrRows + rl;
+    const f32x4 acc = a0 + a1;
+    float v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = g.round_bf16 ? round_bf16(acc[q] + bv[q]) : acc[q] + bv[q];
+    if (cols && m < g.M) {
+      const int64_t o = m * g.N + nc0;
+      if (g.y_bf16) {
+        __bf16* yb = reinterpret_cast<__bf16*>(g.y);
+        if (full4) {
+          *reinterpret_cast<bf16x4*>(yb + o) = bf16x4{static_cast<__bf16>(v[0]), static_cast<__bf16>(v[1]),
+                                                      static_cast<__bf16>(v[2]), static_cast<__bf16>(v[3])};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (nc0 + q < g.N) yb[o + q] = static_cast<__bf16>(v[q]);
+        }
+      } else if (full4) {
+        *reinterpret_cast<float4*>(g.y + o) = make_float4(v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (nc0 + q < g.N) g.y[o + q] = v[q];
+      }
+    }
+    if constexpr (EPI == kEpiLogits) {
+      float ss = 0.0f, sd = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        ss = fmaf(v[q], as[q], ss);
+        sd = fmaf(v[q], ad[q], sd);
+      }
+#pragma unroll
+      for (int o = 16; o < kWave; o <<= 1) {
+        ss += shfl_xor(ss, o);
+        sd += shfl_xor(sd, o);
+      }
+      if (cols && lane < 16 && ct < H && m < g.M) {
+        g.alpha_src[m * H + ct] = ss;
+        g.alpha_dst[m * H + ct] = sd;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int EPI, int MATH, int NB>
+int launch_narrow_r(hipStream_t st, const GemmArgs& g, int grid, int ntiles) {
+  constexpr int KB = MATH == kMathBF16 ? 32 : 16;
+  if (NB == (g.K + KB - 1) / KB) {
+    hipLaunchKernelGGL((gemm_nt_narrow_r_kernel<EPI, NB, MATH>), dim3(grid), dim3(kThreads), 0, st, g, ntiles);
+    return check_launch("cign linear (narrow, W in registers)");
+  }
+  if constexpr (NB > kNrMinK / KB) return launch_narrow_r<EPI, MATH, NB - 1>(st, g, grid, ntiles);
+  return set_error(kInvalid, "cign linear: K=%d outside the register-W kernel's range", g.K);
+}
+
+// CUs of the current device, cached per device.
+inline int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+  cache[dev].store(v, std::memory_order_relaxed);
+  return v;
 }
 
 // grad_W partials of a narrow projection: a workgroup owns a row chunk, all
@@ -1322,6 +1605,215 @@ __global__ __launch_bounds__(kThreads) void wgrad_narrow_kernel(const TG* gy, co
     for (int r = 0; r < 4; ++r) {
       const int k = k0 + 16 * ks + 4 * r;
       if (k >= K) continue;  // K % 4 == 0: the quad is whole or past K
+      *reinterpret_cast<float4*>(out + static_cast<int64_t>(n) * K + k) =
+          make_float4(acc[0][j][r], acc[1][j][r], acc[2][j][r], acc[3][j][r]);
+    }
+  }
+}
+
+// ---- Weight gradient of the GAT lin with its attention logits (narrow):
+// the logits' backward fused into wgrad_narrow_kernel. The projection's
+// output gradient is gy = g + g_src (x) att_src + g_dst (x) att_dst (per
+// head h: gy[m, h, c] = g[m, h, c] + g_src[m, h] att_src[h, c] + g_dst[m, h]
+// att_dst[h, c], the sum attn_bwd_kernel forms), built per 4-column quad as
+// the batches load, so it is never stored; and the attention gradients
+// sum_m g_src[m, h] x_proj[m, h, c] (likewise g_dst) are summed by every
+// workgroup of a row chunk over its share of the chunk's rows after its
+// GEMM loop, into partial rows of their own (N for att_src, N for att_dst);
+// one colsum launch reduces both partial arrays. Under bf16 math gy and x are rounded to bf16 before
+// their products (gy after the fp32 sum, as cign_linear_bwd_bf16gy reads the
+// stored sum). Needs N, K, C multiples of 4, N <= 64.
+struct WlArgs {
+  const float* gf;     // gradient of x_proj from the GAT [M, N]
+  const float* gs;     // gradient of alpha_src [M, H]
+  const float* gd;     // gradient of alpha_dst [M, H]
+  const void* xp;      // x_proj [M, N]: fp32, or bf16 (TXP)
+  const float* att_s;  // [N]
+  const float* att_d;  // [N]
+  const float* x;      // [M, K]
+  int64_t M;
+  int N, K, C, H;
+  int64_t chunk;
+  int nchunks, ntk;
+  float* part;   // grad_W partials [nchunks][N K]
+  float* part2;  // attention partials [nchunks ntk][2 N]
+};
+
+template <int MATH>
+struct WlBatch {
+  float x[kWnUnroll][4], g[kWnUnroll][4], s[kWnUnroll], d[kWnUnroll];
+  __device__ __forceinline__ void load(const WlArgs& a, int64_t m, int64_t m1, int kc, int nc, int h, int lane) {
+    const int ks = lane >> 4;
+#pragma unroll
+    for (int u = 0; u < kWnUnroll; ++u) {
+      const int64_t mr = m + 4 * u + ks;
+      const int64_t mc = mr < m1 ? mr : m1 - 1;
+      load_quad<float>(a.x + mc * a.K + kc, x[u]);
+      load_quad<float>(a.gf + mc * a.N + nc, g[u]);
+      s[u] = a.gs[mc * a.H + h];
+      d[u] = a.gd[mc * a.H + h];
+    }
+  }
+  __device__ __forceinline__ void mma(f32x4 (&acc)[4][4], const float (&as)[4], const float (&ad)[4], int64_t m,
+                                      int64_t m1, int lane) const {
+    const int ks = lane >> 4;
+#pragma unroll
+    for (int u = 0; u < kWnUnroll; ++u) {
+      const bool ok = m + 4 * u + ks < m1;
+      float xv[4], gv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float o = s[u] * as[i] + d[u] * ad[i];  // attn_bwd_kernel's sum
+        o = g[u][i] + o;
+        gv[i] = MATH == kMathBF16 ? round_bf16(o) : o;
+        xv[i] = ok ? (MATH == kMathBF16 ? round_bf16(x[u][i]) : x[u][i]) : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], gv[j], acc[i][j], 0, 0, 0);
+    }
+  }
+};
+
+// The attention gradients' sums over rows [m0, m1) for the lane's quad of
+// columns nc (rows m + l/16), in a pass of their own after the GEMM loop
+// (inside it, their registers cost the kernel its second wavefront per SIMD).
+template <typename TXP>
+__device__ __forceinline__ void wl_attn_rows(const WlArgs& a, int64_t m0, int64_t m1, int nc, int h, int lane,
+                                             float (&accs)[4], float (&accd)[4]) {
+  const int ks = lane >> 4;
+  const TXP* xp = static_cast<const TXP*>(a.xp);
+  constexpr int U = 4;  // row groups in flight
+  for (int64_t m = m0; m < m1; m += 4 * U) {
+    float p[U][4], sv[U], dv[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t mr = m + 4 * u + ks;
+      ok[u] = mr < m1;
+      const int64_t mc = ok[u] ? mr : m1 - 1;
+      load_quad<TXP>(xp + mc * a.N + nc, p[u]);
+      sv[u] = a.gs[mc * a.H + h];
+      dv[u] = a.gd[mc * a.H + h];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (ok[u]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          accs[i] = fmaf(sv[u], p[u][i], accs[i]);
+          accd[i] = fmaf(dv[u], p[u][i], accd[i]);
+        }
+      }
+  }
+}
+
+template <int MATH, typename TXP>
+__global__ __launch_bounds__(kThreads) void wgrad_logits_narrow_kernel(WlArgs a) {
+  __shared__ f32x4 red[3][16][kWave];  // waves 1..3: 16 accumulator tiles x 64 lanes (48 KB)
+  __shared__ float ared[4][2][kNarrowN];
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
+  int tile, cy;
+  if (!wg_tile_chunk(a.ntk, a.nchunks, true, tile, cy)) return;  // whole workgroup
+  const int N = a.N, K = a.K;
+  const int k0 = tile * kWnK;
+  const int64_t c0 = static_cast<int64_t>(cy) * a.chunk;
+  const int64_t c1 = c0 + a.chunk < a.M ? c0 + a.chunk : a.M;
+  const int64_t q = a.chunk / 4;
+  const int64_t m0 = c0 + wave * q;
+  const int64_t m1 = m0 + q < c1 ? m0 + q : c1;
+  const int rl = lane & 15, ks = lane >> 4;
+  const int kc = min(k0 + 4 * rl, K - 4), nc = min(4 * rl, N - 4);
+  const int h = nc / a.C;  // C % 4 == 0: the quad lies in one head
+  float as[4], ad[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    as[i] = a.att_s[nc + i];
+    ad[i] = a.att_d[nc + i];
+  }
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float accs[4] = {0.0f, 0.0f, 0.0f, 0.0f}, accd[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr int B = 4 * kWnUnroll;
+  if (m0 < m1) {
+    WlBatch<MATH> b0, b1;
+    b0.load(a, m0, m1, kc, nc, h, lane);
+    b1.load(a, m0 + B, m1, kc, nc, h, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int64_t m = m0; m < m1; m += 2 * B) {
+      b0.mma(acc, as, ad, m, m1, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      b0.load(a, m + 2 * B, m1, kc, nc, h, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      b1.mma(acc, as, ad, m + B, m1, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      b1.load(a, m + 3 * B, m1, kc, nc, h, lane);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  float* out = a.part + static_cast<int64_t>(cy) * N * K;
+  {
+    // the attention sums over this workgroup's share of the chunk: tile t
+    // of ntk takes rows c0 + t R .. (R a multiple of 16), the wave a quarter
+    const int64_t R = (a.chunk / a.ntk + 15) / 16 * 16;
+    const int64_t r0 = c0 + tile * R;
+    const int64_t r1 = r0 + R < c1 ? r0 + R : c1;
+    const int64_t wa0 = r0 + wave * (R / 4);
+    const int64_t wa1 = wa0 + R / 4 < r1 ? wa0 + R / 4 : r1;
+    if (wa0 < wa1) wl_attn_rows<TXP>(a, wa0, wa1, nc, h, lane, accs, accd);
+    // the wave's sums over its four row slots, then the waves in order
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int o = 16; o < kWave; o <<= 1) {
+        accs[i] += shfl_xor(accs[i], o);
+        accd[i] += shfl_xor(accd[i], o);
+      }
+    if (ks == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ared[wave][0][4 * rl + i] = accs[i];
+        ared[wave][1][4 * rl + i] = accd[i];
+      }
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[wave - 1][4 * i + j][lane] = acc[i][j];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  {
+    float* out2 = a.part2 + (static_cast<int64_t>(cy) * a.ntk + tile) * 2 * N;
+    for (int f = lane; f < 2 * N; f += kWave) {
+      const int which = f >= N, c = f - which * N;
+      float v = ared[0][which][c];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) v += ared[w][which][c];
+      out2[f] = v;
+    }
+  }
+#pragma unroll
+  for (int w = 0; w < 3; ++w)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] += red[w][4 * i + j][lane];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = 4 * rl + j;
+    if (n >= N) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int k = k0 + 16 * ks + 4 * r;
+      if (k >= K) continue;
       *reinterpret_cast<float4*>(out + static_cast<int64_t>(n) * K + k) =
           make_float4(acc[0][j][r], acc[1][j][r], acc[2][j][r], acc[3][j][r]);
     }
@@ -2020,6 +2512,7 @@ __global__ __launch_bounds__(kThreads) void pack_wgrad_kernel(const float* gy, P
 // Host side
 // ---------------------------------------------------------------------------
 inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+inline bool aligned8(const void* p) { return reinterpret_cast<uintptr_t>(p) % 8 == 0; }
 
 // Column tile: fp32 math 64 (two waves per SIMD with the register-resident x
 // fragments); bf16 math 64 up to N = 256 (more workgroups for the skinny
@@ -2059,8 +2552,22 @@ int launch_nt(hipStream_t st, const GemmArgs& g, int bn) {
     const int64_t blocks = (g.M + kNarrowRows - 1) / kNarrowRows;
     if (blocks == 0) return kOk;
     if (blocks > 0x7fffffff) return set_error(kInvalid, "cign linear: too many tiles");
-    hipLaunchKernelGGL((gemm_nt_narrow_kernel<TX, MATH, EPI>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
-                       0, st, g);
+    if constexpr (std::is_same_v<TX, float> && EPI != kEpiGamma) {
+      if (g.vec && g.K >= kNrMinK && g.K <= kNrMaxK) {
+        // W in registers over 16-row tiles, kNrPerCu workgroups per CU
+        const int64_t ntiles = (g.M + kNrRows - 1) / kNrRows;
+        if (ntiles > 0x7fffffff) return set_error(kInvalid, "cign linear: too many tiles");
+        const int grid = static_cast<int>(std::min<int64_t>(ntiles, static_cast<int64_t>(kNrPerCu) * device_cus()));
+        constexpr int KB = MATH == kMathBF16 ? 32 : 16;
+        return launch_narrow_r<EPI, MATH, (kNrMaxK + KB - 1) / KB>(st, g, grid, static_cast<int>(ntiles));
+      }
+    }
+    if (g.vec)
+      hipLaunchKernelGGL((gemm_nt_narrow_kernel<TX, MATH, EPI, true>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(kThreads), 0, st, g);
+    else
+      hipLaunchKernelGGL((gemm_nt_narrow_kernel<TX, MATH, EPI, false>), dim3(static_cast<unsigned>(blocks)),
+                         dim3(kThreads), 0, st, g);
     return check_launch("cign linear (narrow)");
   }
   const int nrt = static_cast<int>((g.M + kBM - 1) / kBM);
@@ -2319,6 +2826,86 @@ int cign_linear_gamma_fwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t
 
 int64_t cign_linear_bwd_workspace_bytes(int64_t M, int32_t N, int32_t K, int32_t with_bias) {
   return bwd_ws(M, N, K, with_bias != 0).total;
+}
+
+// Row chunks of cign_lin_logits_wgrad (wgrad_narrow_kernel's) and its
+// workspace: a grad_W partial row (N K floats) per chunk, then an attention
+// partial row (2 N) per workgroup.
+struct WlWs {
+  int64_t chunk, part2, total;
+  int chunks, ntk;
+};
+
+inline WlWs wl_ws(int64_t M, int N, int K) {
+  WlWs L;
+  L.ntk = (K + kWnK - 1) / kWnK;
+  int64_t wgc = wg_chunk_count(M, std::max<int64_t>(1, 512 / L.ntk), true);
+  L.chunk = std::max<int64_t>(kWnChunkRows, ((M + wgc - 1) / wgc + kWnChunkRows - 1) / kWnChunkRows * kWnChunkRows);
+  wgc = M > 0 ? (M + L.chunk - 1) / L.chunk : 1;
+  L.chunks = static_cast<int>(wgc);
+  auto al = [](int64_t v) { return (v + 255) & ~int64_t(255); };
+  L.part2 = al(4LL * wgc * N * K);
+  L.total = al(L.part2 + 4LL * wgc * L.ntk * 2 * N);
+  return L;
+}
+
+int64_t cign_lin_logits_wgrad_workspace_bytes(int64_t M, int32_t N, int32_t K) {
+  if (M < 0 || N <= 0 || K <= 0) return 0;
+  return wl_ws(M, N, K).total;
+}
+
+int cign_lin_logits_wgrad(void* stream, int64_t M, int32_t heads, int32_t channels, int32_t K, int32_t xp_dtype,
+                          int32_t math, const float* grad_xp, const float* grad_src, const float* grad_dst,
+                          const void* xp, const float* att_src, const float* att_dst, const float* x, float* grad_w,
+                          float* grad_att_src, float* grad_att_dst, void* workspace, int64_t workspace_bytes) {
+  const char* who = "cign_lin_logits_wgrad";
+  const int H = heads, C = channels;
+  if (M < 0 || H < 1 || C < 1 || K <= 0) return set_error(kInvalid, "%s: bad sizes", who);
+  const int N = H * C;
+  if (N > kNarrowN || N <= kSmallN || C % 4 != 0 || K % 4 != 0)
+    return set_error(kInvalid, "%s: needs %d < heads*channels <= %d, channels and K multiples of 4 (N=%d C=%d K=%d)",
+                     who, kSmallN, kNarrowN, N, C, K);
+  if (math != kMathF32 && math != kMathBF16) return set_error(kInvalid, "%s: math must be 0 or 1", who);
+  if (xp_dtype != kF32 && xp_dtype != kBF16) return set_error(kInvalid, "%s: xp_dtype must be 0 or 1", who);
+  if (!grad_w || !grad_att_src || !grad_att_dst || !att_src || !att_dst ||
+      (M > 0 && (!grad_xp || !grad_src || !grad_dst || !xp || !x)))
+    return set_error(kInvalid, "%s: null pointer", who);
+  if (M > 0x7fffffff) return set_error(kInvalid, "%s: M too large", who);
+  if (M > 0 && !(aligned16(grad_xp) && aligned16(x) && (xp_dtype == kF32 ? aligned16(xp) : aligned8(xp))))
+    return set_error(kInvalid, "%s: grad_xp, x and xp rows must start 16-byte (bf16 xp: 8-byte) aligned", who);
+  const WlWs L = wl_ws(M, N, K);
+  if (workspace_bytes < L.total || !workspace)
+    return set_error(kInvalid, "%s: workspace too small (%lld < %lld)", who, static_cast<long long>(workspace_bytes),
+                     static_cast<long long>(L.total));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (M == 0) {
+    int rc = rowops::zero_outputs(st, grad_w, N * K, grad_att_src, N, who);
+    return rc ? rc : rowops::zero_outputs(st, grad_att_dst, N, nullptr, 0, who);
+  }
+  WlArgs a{};
+  a.gf = grad_xp; a.gs = grad_src; a.gd = grad_dst; a.xp = xp; a.att_s = att_src; a.att_d = att_dst; a.x = x;
+  a.M = M; a.N = N; a.K = K; a.C = C; a.H = H;
+  a.chunk = L.chunk; a.nchunks = L.chunks; a.ntk = L.ntk;
+  a.part = static_cast<float*>(workspace);
+  a.part2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + L.part2);
+  const dim3 grid(wg_grid(L.ntk, L.chunks, true));
+  if (math == kMathBF16) {
+    if (xp_dtype == kBF16)
+      hipLaunchKernelGGL((wgrad_logits_narrow_kernel<kMathBF16, bf16h>), grid, dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((wgrad_logits_narrow_kernel<kMathBF16, float>), grid, dim3(kThreads), 0, st, a);
+  } else {
+    if (xp_dtype == kBF16)
+      hipLaunchKernelGGL((wgrad_logits_narrow_kernel<kMathF32, bf16h>), grid, dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((wgrad_logits_narrow_kernel<kMathF32, float>), grid, dim3(kThreads), 0, st, a);
+  }
+  int rc = check_launch(who);
+  if (rc) return rc;
+  // grad_W under bf16 math is the bf16 output of autocast's Linear backward;
+  // the attention vectors' gradients stay float32 (cign_attn_logits_bwd_acc's)
+  return rowops::launch_colsum_split(st, a.part, L.chunks, N * K, grad_w, a.part2, L.chunks * L.ntk, N, grad_att_src,
+                                     grad_att_dst, who, math == kMathBF16);
 }
 
 // cign_linear_bwd with bf16 math (no bias) whose grad_y is bf16 storage: the

@@ -27,28 +27,45 @@ __device__ __forceinline__ float bf16_rounded(float v) { return to_f32(from_f32<
 // kColsumThreads / kCols slices; thread (c, s) sums the partials b = s,
 // s + slices, ... with eight independent accumulators (combined in a fixed
 // order), then the slices are added through an LDS tree.
+//
+// Split outputs (a TailSum): workgroups past the first split / kCols (split
+// a multiple of kCols) reduce a second partial array instead, tail.part
+// [tail.nb][2 tn], whose columns j < tn go to tail.out0 and the rest to
+// tail.out1 (never rounded): two reductions in one launch.
+struct TailSum {
+  const float* part = nullptr;
+  int nb = 0, tn = 0;
+  float* out0 = nullptr;
+  float* out1 = nullptr;
+};
+
 template <int kCols>
 __global__ __launch_bounds__(kColsumThreads) void colsum_kernel(const float* part, int nb, int width, float* out0,
-                                                                float* out1, bool rb) {
+                                                                float* out1, bool rb, int split = 0x7fffffff,
+                                                                TailSum tail = TailSum()) {
   // kCols columns x kSlices partial slices per workgroup; a slice thread
   // keeps eight partial rows in flight, then the slices meet in an LDS tree
   // (a fixed order, so the sums are deterministic).
   constexpr int kSlices = kColsumThreads / kCols;
   __shared__ float red[kColsumThreads];
-  const float* src = part + static_cast<int64_t>(blockIdx.y) * nb * width;
+  const bool in_tail = static_cast<int64_t>(blockIdx.x) * kCols >= split;  // whole workgroup
+  const float* src = in_tail ? tail.part : part + static_cast<int64_t>(blockIdx.y) * nb * width;
+  const int rows = in_tail ? tail.nb : nb;
+  const int w = in_tail ? 2 * tail.tn : width;
   float* out = blockIdx.y == 0 ? out0 : out1;
   const int t = threadIdx.x;
-  const int c = blockIdx.x * kCols + t % kCols;
+  const int c = (in_tail ? static_cast<int>(blockIdx.x) * kCols - split : static_cast<int>(blockIdx.x) * kCols) +
+                t % kCols;
   const int s = t / kCols;
   float acc[8];
 #pragma unroll
   for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
-  if (c < width) {
+  if (c < w) {
     int b = s;
-    for (; b + 7 * kSlices < nb; b += 8 * kSlices)
+    for (; b + 7 * kSlices < rows; b += 8 * kSlices)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc[u] += src[static_cast<int64_t>(b + u * kSlices) * width + c];
-    for (; b < nb; b += kSlices) acc[0] += src[static_cast<int64_t>(b) * width + c];
+      for (int u = 0; u < 8; ++u) acc[u] += src[static_cast<int64_t>(b + u * kSlices) * w + c];
+    for (; b < rows; b += kSlices) acc[0] += src[static_cast<int64_t>(b) * w + c];
   }
   red[t] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
@@ -56,7 +73,14 @@ __global__ __launch_bounds__(kColsumThreads) void colsum_kernel(const float* par
     if (s < h) red[t] += red[t + h * kCols];
     __syncthreads();
   }
-  if (s == 0 && c < width) out[c] = rb ? bf16_rounded(red[t]) : red[t];
+  if (s == 0 && c < w) {
+    if (!in_tail)
+      out[c] = rb ? bf16_rounded(red[t]) : red[t];
+    else if (c < tail.tn)
+      tail.out0[c] = red[t];
+    else
+      tail.out1[c - tail.tn] = red[t];
+  }
 }
 
 // Wide outputs over few partial rows (weight gradients): one thread per four
@@ -102,6 +126,22 @@ int zero_outputs(hipStream_t st, float* a, int na, float* b, int nbv, const char
   const int m = na > nbv ? na : nbv;
   if (m <= 0) return kOk;
   hipLaunchKernelGGL(zero_kernel, dim3((m + kBlock - 1) / kBlock), dim3(kBlock), 0, st, a, na, b, nbv);
+  return check_launch(who);
+}
+
+int launch_colsum_split(hipStream_t st, const float* part, int nb, int split, float* out, const float* tail_part,
+                        int tail_nb, int tn, float* tail0, float* tail1, const char* who, bool round_bf16_out) {
+  if (split % 16 != 0) return set_error(kInvalid, "%s: split colsum needs a multiple of 16 columns", who);
+  TailSum tail;
+  tail.part = tail_part;
+  tail.nb = tail_nb;
+  tail.tn = tn;
+  tail.out0 = tail0;
+  tail.out1 = tail1;
+  const int blocks = split / 16 + (2 * tn + 15) / 16;
+  if (blocks == 0) return kOk;
+  hipLaunchKernelGGL(colsum_kernel<16>, dim3(blocks, 1), dim3(kColsumThreads), 0, st, part, nb, split, out, nullptr,
+                     round_bf16_out, split, tail);
   return check_launch(who);
 }
 

@@ -89,6 +89,14 @@ int zero_outputs(hipStream_t st, float* a, int na, float* b, int nbv, const char
 int launch_colsum(hipStream_t st, const float* part, int nb, int width, int quantities, float* out0, float* out1,
                   const char* who, bool round_bf16_out = false);
 
+// Two reductions in one launch: out[c] = sum_b part[b][c] over nb partial
+// rows of split columns (split % 16 == 0; rounded to bf16 when
+// round_bf16_out), and tail0[j] = sum_b tail_part[b][j], tail1[j] =
+// sum_b tail_part[b][tn + j] over tail_nb rows of 2 tn columns, each in
+// colsum_kernel's fixed order.
+int launch_colsum_split(hipStream_t st, const float* part, int nb, int split, float* out, const float* tail_part,
+                        int tail_nb, int tn, float* tail0, float* tail1, const char* who, bool round_bf16_out);
+
 // Calls f(IC<LPR>, IC<V>) for a row of qc chunks: LPR = next power of two
 // >= qc up to 64, then V = 2 or 4 chunks per lane (qc <= 256). Returns -1 when
 // qc > 256 (the caller tiles or rejects).

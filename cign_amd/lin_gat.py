@@ -37,6 +37,7 @@ _FUSED_LOGITS_C = (16, 32, 64, 128)
 _GATHER_MAX_DEGREE = 12
 # cign_linear_bwd runs outputs up to this many on VALU kernels
 _SMALL_N = 16
+_NARROW_N = 64  # cign_lin_logits_wgrad's widest projection
 
 
 def holds_bf16(heads: int, channels: int, math: int) -> bool:
@@ -126,6 +127,18 @@ class _LinGatFn(torch.autograd.Function):
         g_s = torch.empty_like(s)
         g_d = torch.empty_like(d)
         st = _lib.stream_ptr(dev)
+        K = x2.size(1)
+        if (not ctx.needs_input_grad[0] and _SMALL_N < H * C <= _NARROW_N and C % 4 == 0 and K % 4 == 0
+                and x2.dtype == torch.float32 and x2.is_contiguous() and x2.data_ptr() % 16 == 0):
+            # input features that are data (config c2): the logits' backward
+            # fused into the weight gradient, gy never stored
+            gw = torch.empty((H * C, K), dtype=torch.float32, device=dev)
+            ws_bytes = int(lib.cign_lin_logits_wgrad_workspace_bytes(M, H * C, K))
+            ws = _lib.workspace(ws_bytes, dev)
+            lib.call("cign_lin_logits_wgrad", st, M, H, C, K, 1 if ctx.hold else 0, ctx.math, grad_feat.data_ptr(),
+                     g_attn_col.data_ptr(), g_attn_row.data_ptr(), xp.data_ptr(), s.data_ptr(), d.data_ptr(),
+                     x2.data_ptr(), gw.data_ptr(), g_s.data_ptr(), g_d.data_ptr(), ws.data_ptr(), ws_bytes)
+            return (None, gw if ctx.needs_input_grad[1] else None, g_s, g_d, g_bias) + (None,) * 10
         # With x_proj held in bf16 the sum is written rounded to bf16, the
         # values the projection's bf16-math backward reads of it.
         gy16 = ctx.hold and C % 8 == 0 and H * C > _SMALL_N

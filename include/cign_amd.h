@@ -489,6 +489,27 @@ int cign_linear_bwd(void* stream, int64_t M, int32_t N, int32_t K, int32_t math,
 int cign_linear_bwd_bf16gy(void* stream, int64_t M, int32_t N, int32_t K, const void* grad_y, const float* x,
                            const float* w, float* grad_x, float* grad_w, void* workspace, int64_t workspace_bytes);
 
+/* The GAT lin's weight and attention-vector gradients when its input needs
+ * none (input features are data): with N = heads*channels,
+ * gy = grad_xp + grad_src (x) att_src + grad_dst (x) att_dst per head (the sum
+ * cign_attn_logits_bwd_acc forms, never stored), grad_w [N,K] = gy^T x
+ * (math 1: gy and x rounded to bf16 before their products and grad_w
+ * rounded to bf16, as cign_linear_bwd_bf16gy on the stored sum),
+ * grad_att_src [N] = sum_m grad_src[m,h] xp[m,h,c] and grad_att_dst likewise
+ * (float32), all deterministic: one fused kernel writes per-row-chunk
+ * partials of grad_w and of the two sums and one launch adds them in order.
+ * Needs 16 < N <= 64, channels and K multiples of 4, grad_xp and x rows
+ * 16-byte aligned, xp (xp_dtype 0 = float32, 1 = bf16 storage) 16-byte
+ * (bf16: 8-byte) aligned. Workspace: cign_lin_logits_wgrad_workspace_bytes.
+ * No counterpart in the reference: it fuses ext attention_backward
+ * (fused_gat_sideops.cpp:54-66) with the weight gradient of the lin's
+ * Linear (model_cign.py:546-553) for the narrow projection of config c2. */
+int64_t cign_lin_logits_wgrad_workspace_bytes(int64_t M, int32_t N, int32_t K);
+int cign_lin_logits_wgrad(void* stream, int64_t M, int32_t heads, int32_t channels, int32_t K, int32_t xp_dtype,
+                          int32_t math, const float* grad_xp, const float* grad_src, const float* grad_dst,
+                          const void* xp, const float* att_src, const float* att_dst, const float* x, float* grad_w,
+                          float* grad_att_src, float* grad_att_dst, void* workspace, int64_t workspace_bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -275,3 +275,58 @@ def test_bf16_gradient_entry_points_reject():
     with pytest.raises(RuntimeError, match="workspace too small"):
         lib.call("cign_linear_bwd_bf16gy", st, n, 24, 8, x16.data_ptr(), torch.zeros((n, 8), device="cuda").data_ptr(),
                  torch.zeros((24, 8), device="cuda").data_ptr(), None, gw.data_ptr(), lws.data_ptr(), 0)
+
+
+@pytest.mark.parametrize("amp", [False, True])
+@pytest.mark.parametrize("n,K", [(300, 48), (24492, 300)])
+def test_lin_gat_data_input_fused_wgrad(n, K, amp):
+    """Input features that need no gradient (config c2: x is data) take
+    cign_lin_logits_wgrad, the logits' backward fused into the weight
+    gradient; with x requiring a gradient the module runs the logits
+    backward and the Linear backward apart. Same forward (bit for bit), the
+    GAT bias gradient bit for bit, the weight and attention-vector gradients
+    to the fp32 tolerance of another summation order (under AMP the weight
+    gradient, a bf16 output, within one bf16 ulp)."""
+    from cign_amd.graph import prepare_fused_gat_graph
+    from cign_amd.model_cign import CompatibleCollapsedFusedGATConv
+    from tests.conftest import bf16_flip_atol
+
+    H, C = 4, 16
+    print(f"fused lin wgrad n={n} K={K} amp={amp}", flush=True)
+    from oracle import cign_oracle as O
+
+    rng = np.random.default_rng(n + K)
+    if n <= 1000:
+        ei = _graph(rng, n, {2: min(500, n - 1)})
+    else:  # about 8.6 edges a node, as the c2 graph, plus a hub column
+        src = np.concatenate([rng.integers(0, n, 8 * n), np.full(2000, 7)])
+        dst = np.concatenate([rng.integers(0, n, 8 * n), rng.integers(0, n, 2000)])
+        ei = O.gat_edge_index(np.stack([src, dst]).astype(np.int64), n)
+        r, c, _ = O.coalesce(ei[0], ei[1], n)
+        ei = np.stack([r, c])
+    (rowptr, col), (row, colptr), perm = prepare_fused_gat_graph(torch.from_numpy(ei), n)
+    csr, csc, perm = (rowptr.cuda(), col.cuda()), (row.cuda(), colptr.cuda()), perm.cuda()
+    torch.manual_seed(0)
+    mod = CompatibleCollapsedFusedGATConv(K, C, heads=H, dropout=0.0).cuda().train()
+    with torch.no_grad():
+        mod.bias.normal_()
+        mod.att_src.normal_()
+        mod.att_dst.normal_()
+    mod._selective_amp_enabled = amp
+    mod._selective_amp_dtype = torch.bfloat16
+    x0 = torch.from_numpy(rng.standard_normal((n, K)).astype(np.float32)).cuda()
+    gy = torch.from_numpy((rng.standard_normal((n, C)) / np.sqrt(n)).astype(np.float32)).cuda()
+    res = {}
+    for data in (True, False):
+        x = x0.clone().requires_grad_(not data)
+        mod.zero_grad(set_to_none=True)
+        y = mod(x, csr, csc, perm)
+        y.backward(gy)
+        res[data] = {"y": y.detach().clone()}
+        res[data].update({k: v.grad.clone() for k, v in mod.named_parameters()})
+    assert torch.equal(res[True]["y"], res[False]["y"])
+    assert torch.equal(res[True]["bias"], res[False]["bias"])
+    for k in ("lin.weight", "att_src", "att_dst"):
+        a, e = res[True][k], res[False][k]
+        extra = bf16_flip_atol(e.cpu().numpy()) if amp and k == "lin.weight" else 0.0
+        assert_close(a, e, rtol=1e-4, atol=1e-5 * max(1.0, float(e.abs().max())) + extra, name=k)
