@@ -83,6 +83,72 @@ __global__ __launch_bounds__(kColsumThreads) void colsum_kernel(const float* par
   }
 }
 
+// Wide outputs over many partial rows, four columns a thread: a workgroup
+// (256 threads) covers 64 columns in 16 slices; slice s sums the partial rows
+// b = s, s + 16, ... as float4 with eight independent accumulators (combined
+// in a fixed order), then the slices meet in an LDS tree. Split outputs as in
+// colsum_kernel (split a multiple of 64, the first split / 64 workgroups);
+// the tail's workgroups cover 16 columns in 64 slices (its partial rows are
+// many: one per workgroup of the producing kernel). Needs width % 4 == 0,
+// tn % 4 == 0 and 16-byte aligned rows and outputs.
+__global__ __launch_bounds__(kBlock) void colsum4_kernel(const float* part, int nb, int width, float* out, bool rb,
+                                                         int split, TailSum tail) {
+  __shared__ float4 red[kBlock];
+  const int head_blocks = split / 64;
+  const bool in_tail = static_cast<int>(blockIdx.x) >= head_blocks;  // whole workgroup
+  const int quads = in_tail ? 4 : 16;
+  const int slices = kBlock / quads;
+  const float* src = in_tail ? tail.part : part;
+  const int rows = in_tail ? tail.nb : nb;
+  const int w = in_tail ? 2 * tail.tn : width;
+  const int t = threadIdx.x;
+  const int c = (in_tail ? (static_cast<int>(blockIdx.x) - head_blocks) * 16 : static_cast<int>(blockIdx.x) * 64) +
+                4 * (t % quads);
+  const int s = t / quads;
+  float4 acc[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) acc[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (c < w) {
+    int b = s;
+    for (; b + 7 * slices < rows; b += 8 * slices)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float4 v = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(b + u * slices) * w + c);
+        acc[u].x += v.x; acc[u].y += v.y; acc[u].z += v.z; acc[u].w += v.w;
+      }
+    for (; b < rows; b += slices) {
+      const float4 v = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(b) * w + c);
+      acc[0].x += v.x; acc[0].y += v.y; acc[0].z += v.z; acc[0].w += v.w;
+    }
+  }
+#pragma unroll
+  for (int h = 4; h > 0; h >>= 1)
+#pragma unroll
+    for (int u = 0; u < h; ++u) {
+      acc[u].x += acc[u + h].x; acc[u].y += acc[u + h].y; acc[u].z += acc[u + h].z; acc[u].w += acc[u + h].w;
+    }
+  red[t] = acc[0];
+  __syncthreads();
+  for (int h = slices / 2; h > 0; h >>= 1) {
+    if (s < h) {
+      const float4 v = red[t + h * quads];
+      red[t].x += v.x; red[t].y += v.y; red[t].z += v.z; red[t].w += v.w;
+    }
+    __syncthreads();
+  }
+  if (s == 0 && c < w) {
+    float4 r = red[t];
+    if (!in_tail) {
+      if (rb) r = make_float4(bf16_rounded(r.x), bf16_rounded(r.y), bf16_rounded(r.z), bf16_rounded(r.w));
+      *reinterpret_cast<float4*>(out + c) = r;
+    } else {
+      // tn % 4 == 0: the quad lies in one tail output
+      float* o = c < tail.tn ? tail.out0 + c : tail.out1 + (c - tail.tn);
+      *reinterpret_cast<float4*>(o) = r;
+    }
+  }
+}
+
 // Wide outputs over few partial rows (weight gradients): one thread per four
 // columns walks every partial row in order, eight rows in flight.
 __global__ __launch_bounds__(kBlock) void colsum_wide_kernel(const float* part, int nb, int width, float* out0,
@@ -131,13 +197,23 @@ int zero_outputs(hipStream_t st, float* a, int na, float* b, int nbv, const char
 
 int launch_colsum_split(hipStream_t st, const float* part, int nb, int split, float* out, const float* tail_part,
                         int tail_nb, int tn, float* tail0, float* tail1, const char* who, bool round_bf16_out) {
-  if (split % 16 != 0) return set_error(kInvalid, "%s: split colsum needs a multiple of 16 columns", who);
   TailSum tail;
   tail.part = tail_part;
   tail.nb = tail_nb;
   tail.tn = tn;
   tail.out0 = tail0;
   tail.out1 = tail1;
+  if (split % 64 == 0 && tn % 4 == 0 && aligned16(part) && aligned16(out) && aligned16(tail_part) &&
+      aligned16(tail0) && aligned16(tail1)) {
+    // four columns a thread (the c2 lin: 19,200 + 128 columns over 96 and
+    // 480 partial rows: 7.9 us on colsum_kernel<16>)
+    const int blocks = split / 64 + (2 * tn + 15) / 16;
+    if (blocks == 0) return kOk;
+    hipLaunchKernelGGL(colsum4_kernel, dim3(blocks), dim3(kBlock), 0, st, part, nb, split, out, round_bf16_out, split,
+                       tail);
+    return check_launch(who);
+  }
+  if (split % 16 != 0) return set_error(kInvalid, "%s: split colsum needs a multiple of 16 columns", who);
   const int blocks = split / 16 + (2 * tn + 15) / 16;
   if (blocks == 0) return kOk;
   hipLaunchKernelGGL(colsum_kernel<16>, dim3(blocks, 1), dim3(kColsumThreads), 0, st, part, nb, split, out, nullptr,
@@ -157,6 +233,12 @@ int launch_colsum(hipStream_t st, const float* part, int nb, int width, int quan
   // kernel walking 128 rows took 26 us), take 16 columns x 64 slices, so more
   // workgroups share the rows; the rest 64 columns x 16 slices.
   const bool vec = width % 4 == 0 && aligned16(part) && aligned16(out0) && (!out1 || aligned16(out1));
+  if (width > 4096 && width < 65536 && nb >= 16 && quantities == 1 && vec) {
+    // four columns a thread: 64 columns x 16 slices a workgroup
+    hipLaunchKernelGGL(colsum4_kernel, dim3((width + 63) / 64), dim3(kBlock), 0, st, part, nb, width, out0,
+                       round_bf16_out, 0x7fffffff, TailSum());
+    return check_launch(who);
+  }
   if (width > 4096 && width < 65536 && nb >= 16)
     hipLaunchKernelGGL(colsum_kernel<16>, dim3((width + 15) / 16, quantities), dim3(kColsumThreads), 0, st, part, nb,
                        width, out0, out1, round_bf16_out);

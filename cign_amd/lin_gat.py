@@ -33,8 +33,12 @@ from .schedule import gat_schedule
 
 _FUSED_LOGITS_C = (16, 32, 64, 128)
 # Largest average degree at which bf16 x_proj is gathered again in the
-# backward instead of saving per-row aggregates.
+# backward instead of saving per-row aggregates, and the narrowest rows
+# (H*C values) for which it is: a gather of 64-value rows is a chain of
+# short dependent loads (the c2 lin, 4 x 16: the rows pass took 14.0 us
+# gathering against 5.2 us reading aggregates).
 _GATHER_MAX_DEGREE = 12
+_GATHER_MIN_WIDTH = 512
 # cign_linear_bwd runs outputs up to this many on VALU kernels
 _SMALL_N = 16
 _NARROW_N = 64  # cign_lin_logits_wgrad's widest projection
@@ -95,7 +99,7 @@ class _LinGatFn(torch.autograd.Function):
         # rows): with bf16 rows on a sparse graph the gather is cheaper, its
         # rows largely cache hits (production block, average degree 8.6:
         # forward + backward 336 -> 292 us; fp32 rows: 434 against 463 us).
-        want_agg = not (hold and col.numel() <= _GATHER_MAX_DEGREE * M)
+        want_agg = not (hold and H * C >= _GATHER_MIN_WIDTH and col.numel() <= _GATHER_MAX_DEGREE * M)
         (y, pre, edge_max, edge_sum, edge_mask), agg = ext.forward_agg(
             a_dst, a_src, rowptr, col, float(negative_slope), xp, bias_c, float(attn_drop), int(seed), want_agg,
             f32_out=hold)
