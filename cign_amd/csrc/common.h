@@ -357,24 +357,55 @@ __device__ __forceinline__ bool block_keep(uint64_t seed, uint64_t idx, float p)
 
 // ---------------------------------------------------------------------------
 // Cross-workgroup "last arrival" for segmented rows. Each participating block
-// publishes its partial result, then calls this with thread 0's view of the
-// per-row counter. Exactly one block (the last to arrive) sees `true`; it
-// resets the counter so the next launch starts from zero again. No block ever
-// waits on another, so this cannot hang.
+// publishes its partial result with st_agent (below), then calls this with
+// thread 0's view of the per-row counter. Exactly one block (the last to
+// arrive) sees `true`; it resets the counter so the next launch starts from
+// zero again, and reads the partials with ld_agent. No block ever waits on
+// another, so this cannot hang.
+//
+// The handoff needs no L2 write-back or invalidate: the partials are stored
+// with agent-scope atomic stores (written through to the level coherent
+// across the XCDs' L2 caches) and loaded with agent-scope atomic loads (read
+// from it), so the only order to keep is each store's completion before the
+// counter's increment (s_waitcnt vmcnt(0) in every wavefront, then the
+// barrier). An agent-scope release/acquire pair instead writes back and
+// invalidates the whole L2 of the XCD twice per call (buffer_wbl2 sc1,
+// buffer_inv sc1): at the c2 layer that was 4 us of the GAT backward's 23.
+// Every datum one block hands to another in the same launch must go through
+// st_agent / ld_agent.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int N>
+__device__ __forceinline__ void st_agent_n(float* p, const float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) st_agent(p + i, v[i]);
+}
+
+template <int N>
+__device__ __forceinline__ void ld_agent_n(const float* p, float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = ld_agent(p + i);
+}
+
 __device__ __forceinline__ bool arrive_last(int* counter, int expected, int* lds_flag) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);  // this wavefront's partial stores have completed
   __syncthreads();
   if (threadIdx.x == 0) {
-    __threadfence();
-    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = (prev == expected - 1);
-    if (last) {
-      __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __threadfence();
-    }
+    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *lds_flag = last ? 1 : 0;
   }
   __syncthreads();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   return *lds_flag != 0;
 }
 

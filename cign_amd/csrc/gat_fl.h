@@ -630,12 +630,12 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
 #pragma unroll
     for (int v = 0; v < V; ++v)
       if (ln.qv[v]) {
-        store_f32<W>(mine + ln.q[v] * W, st.acc[v]);
-        store_f32<W>(mine + F + ln.q[v] * W, st.accl[v]);
+        st_agent_n<W>(mine + ln.q[v] * W, st.acc[v]);
+        st_agent_n<W>(mine + F + ln.q[v] * W, st.accl[v]);
         if (ln.cw == 0) {
-          mine[2 * F + ln.hq[v]] = st.m[v];
-          mine[2 * F + a.H + ln.hq[v]] = st.s[v];
-          mine[2 * F + 2 * a.H + ln.hq[v]] = st.bl[v];
+          st_agent(mine + 2 * F + ln.hq[v], st.m[v]);
+          st_agent(mine + 2 * F + a.H + ln.hq[v], st.s[v]);
+          st_agent(mine + 2 * F + 2 * a.H + ln.hq[v], st.bl[v]);
         }
       }
   if (!arrive_last(a.counters + sg.w, hr.y, &flag)) return;
@@ -647,9 +647,10 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_fl_kernel(GatFwdArgs<T> a, Sch
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       float a2[W], l2[W];
-      load_f32<W>(pz + ln.q[v] * W, a2);
-      load_f32<W>(pz + F + ln.q[v] * W, l2);
-      st.merge(v, pz[2 * F + ln.hq[v]], pz[2 * F + a.H + ln.hq[v]], pz[2 * F + 2 * a.H + ln.hq[v]], a2, l2);
+      ld_agent_n<W>(pz + ln.q[v] * W, a2);
+      ld_agent_n<W>(pz + F + ln.q[v] * W, l2);
+      st.merge(v, ld_agent(pz + 2 * F + ln.hq[v]), ld_agent(pz + 2 * F + a.H + ln.hq[v]),
+               ld_agent(pz + 2 * F + 2 * a.H + ln.hq[v]), a2, l2);
     }
   }
   fwd_emit<T, L, V>(a, ln, cq, row, ln.g == 0, st);
@@ -971,16 +972,16 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_fl_kernel(GatBwdArgs<T> a
     return;
   }
   float* mine = a.part_row + static_cast<int64_t>(b) * 3 * a.H;
-  if (threadIdx.x < 3 * a.H) mine[threadIdx.x] = red[0][threadIdx.x / a.H][threadIdx.x % a.H];
+  if (threadIdx.x < 3 * a.H) st_agent(mine + threadIdx.x, red[0][threadIdx.x / a.H][threadIdx.x % a.H]);
   if (!arrive_last(a.row_counters + sg.w, hr.y, &flag)) return;
   if (threadIdx.x < a.H) {
     const int h = threadIdx.x;
     float w = 0.0f, AA = 0.0f, BB = 0.0f;
     for (int z = 0; z < hr.y; ++z) {
       const float* pz = a.part_row + static_cast<int64_t>(hr.x + z) * 3 * a.H;
-      w += pz[h];
-      AA += pz[a.H + h];
-      BB += pz[2 * a.H + h];
+      w += ld_agent(pz + h);
+      AA += ld_agent(pz + a.H + h);
+      BB += ld_agent(pz + 2 * a.H + h);
     }
     float ar, em, ies;
     row_head1(a, row, h, ar, em, ies);
@@ -1486,19 +1487,19 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
   for (int k = threadIdx.x; k < F; k += kBlock) {
     const float v = red[k];
     if (single) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<GatOut<T>>(v * a.inv_h);
-    else mine[k] = v;
+    else st_agent(mine + k, v);
   }
   if (threadIdx.x < a.H) {
     const int h = threadIdx.x;
     const float v = gred[0][h] + gred[1][h] + gred[2][h] + gred[3][h];
     if (single) a.grad_attn_col[static_cast<int64_t>(j) * a.H + h] = v;
-    else mine[F + h] = v;
+    else st_agent(mine + F + h, v);
   }
   if (single) return;
   if (!arrive_last(a.col_counters + sg.w, hr.y, &flag)) return;
   for (int k = threadIdx.x; k < stride; k += kBlock) {
     float v = 0.0f;
-    for (int z = 0; z < hr.y; ++z) v += a.part_col[static_cast<int64_t>(hr.x + z) * stride + k];
+    for (int z = 0; z < hr.y; ++z) v += ld_agent(a.part_col + static_cast<int64_t>(hr.x + z) * stride + k);
     if (k < F) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<GatOut<T>>(v * a.inv_h);
     else a.grad_attn_col[static_cast<int64_t>(j) * a.H + (k - F)] = v;
   }
@@ -1812,19 +1813,19 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_cm_kernel(GatBwdArgs<T> a
     const float v = red[0][cc][h * 4 + q] + red[1][cc][h * 4 + q] + red[2][cc][h * 4 + q] + red[3][cc][h * 4 + q];
     const int k = h * C + 4 * cc + q;
     if (single) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<GatOut<T>>(v * a.inv_h);
-    else mine[k] = v;
+    else st_agent(mine + k, v);
   }
   if (threadIdx.x < HH) {
     const int h = threadIdx.x;
     const float v = gred[0][h] + gred[1][h] + gred[2][h] + gred[3][h];
     if (single) a.grad_attn_col[static_cast<int64_t>(j) * HH + h] = v;
-    else mine[F + h] = v;
+    else st_agent(mine + F + h, v);
   }
   if (single) return;
   if (!arrive_last(a.col_counters + sg.w, hr.y, &flag)) return;
   for (int k = threadIdx.x; k < stride; k += kBlock) {
     float v = 0.0f;
-    for (int z = 0; z < hr.y; ++z) v += a.part_col[static_cast<int64_t>(hr.x + z) * stride + k];
+    for (int z = 0; z < hr.y; ++z) v += ld_agent(a.part_col + static_cast<int64_t>(hr.x + z) * stride + k);
     if (k < F) a.grad_feat[static_cast<int64_t>(j) * F + k] = from_f32<GatOut<T>>(v * a.inv_h);
     else a.grad_attn_col[static_cast<int64_t>(j) * HH + (k - F)] = v;
   }

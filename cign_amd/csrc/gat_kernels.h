@@ -408,7 +408,7 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_kernel(GatFwdArgs<T> a, Sched 
       __syncthreads();
       for (int q = threadIdx.x; q < HP * CP; q += kBlock) {
         const int hh = q / CP, c = q % CP, cc = cb * CP + c;
-        if (hh < a.H && cc < a.C) mine[hh * a.C + cc] = red[0][q] + red[1][q] + red[2][q] + red[3][q];
+        if (hh < a.H && cc < a.C) st_agent(mine + hh * a.C + cc, red[0][q] + red[1][q] + red[2][q] + red[3][q]);
       }
       __syncthreads();
     }
@@ -421,8 +421,8 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_kernel(GatFwdArgs<T> a, Sched 
     return;
   }
   if (wave == 0 && L.el == 0 && L.hv) {
-    mine[HC + L.h] = M;
-    mine[HC + a.H + L.h] = S;
+    st_agent(mine + HC + L.h, M);
+    st_agent(mine + HC + a.H + L.h, S);
   }
   if (!arrive_last(a.counters + sg.w, hr.y, &flag)) return;
   // Last segment of this row: merge the per-segment (m, s, acc) in order.
@@ -432,7 +432,7 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_kernel(GatFwdArgs<T> a, Sched 
     float MM = kNegBig, SS = 0.0f;
     for (int q = 0; q < hr.y; ++q) {
       const float* pq = a.partial + static_cast<int64_t>(hr.x + q) * stride;
-      ms_merge(MM, SS, pq[HC + hh], pq[HC + a.H + hh]);
+      ms_merge(MM, SS, ld_agent(pq + HC + hh), ld_agent(pq + HC + a.H + hh));
     }
     fin_m[hh] = MM;
     fin_s[hh] = SS;
@@ -446,7 +446,7 @@ __global__ __launch_bounds__(kBlock) void gat_fwd_kernel(GatFwdArgs<T> a, Sched 
       float acch = 0.0f;
       for (int q = 0; q < hr.y; ++q) {
         const float* pq = a.partial + static_cast<int64_t>(hr.x + q) * stride;
-        acch += pq[hh * a.C + c] * softmax_exp(pq[HC + hh] - fin_m[hh]);
+        acch += ld_agent(pq + hh * a.C + c) * softmax_exp(ld_agent(pq + HC + hh) - fin_m[hh]);
       }
       if (fin_s[hh] > 0.0f) total += acch / fin_s[hh];
     }
@@ -667,15 +667,15 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_rows_kernel(GatBwdArgs<T> a, S
     return;
   }
   float* mine = a.part_row + static_cast<int64_t>(b) * 3 * a.H;
-  if (threadIdx.x < 3 * a.H) mine[threadIdx.x] = red[0][threadIdx.x / a.H][threadIdx.x % a.H];
+  if (threadIdx.x < 3 * a.H) st_agent(mine + threadIdx.x, red[0][threadIdx.x / a.H][threadIdx.x % a.H]);
   if (!arrive_last(a.row_counters + sg.w, hr.y, &flag)) return;
   if (threadIdx.x < a.H) {
     float w = 0.0f, AA = 0.0f, BB = 0.0f;
     for (int q = 0; q < hr.y; ++q) {
       const float* pq = a.part_row + static_cast<int64_t>(hr.x + q) * 3 * a.H;
-      w += pq[threadIdx.x];
-      AA += pq[a.H + threadIdx.x];
-      BB += pq[2 * a.H + threadIdx.x];
+      w += ld_agent(pq + threadIdx.x);
+      AA += ld_agent(pq + a.H + threadIdx.x);
+      BB += ld_agent(pq + 2 * a.H + threadIdx.x);
     }
     a.wsum[static_cast<int64_t>(row) * a.H + threadIdx.x] = w;
     a.grad_attn_row[static_cast<int64_t>(row) * a.H + threadIdx.x] = AA - w * BB;
@@ -766,13 +766,13 @@ __device__ __forceinline__ void bias_reduce(const GatBwdArgs<T>& a, int q, int* 
   auto reduce = [&](const float* src, int lo, int hi, float* dst) {
     float t = 0.0f;
     if (r0 < rows_per)
-      for (int r = lo + r0; r < hi; r += rows_per) t += src[static_cast<int64_t>(r) * C + c];
+      for (int r = lo + r0; r < hi; r += rows_per) t += ld_agent(src + static_cast<int64_t>(r) * C + c);
     red[tid] = r0 < rows_per ? t : 0.0f;
     __syncthreads();
     if (tid < C) {
       float u = 0.0f;
       for (int k = 0; k < rows_per; ++k) u += red[k * C + tid];
-      dst[tid] = u;
+      st_agent(dst + tid, u);
     }
     __syncthreads();
   };
@@ -797,11 +797,15 @@ __device__ __forceinline__ void bias_from_grad_pre(const GatBwdArgs<T>& a, int q
   const int tid = threadIdx.x;
   const int c4 = tid % c4n;
   const int r0 = tid / c4n;
-  auto reduce = [&](const float* src, int stride, int lo, int hi, float* dst) {
+  // agent: src was written in this launch (the second level reads the
+  // first level's partials through ld_agent)
+  auto reduce = [&](const float* src, int stride, int lo, int hi, float* dst, bool agent) {
     float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll 4
     for (int r = lo + r0; r < hi; r += rpi) {
-      const float4 v = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(r) * stride + c4 * 4);
+      const float* p = src + static_cast<int64_t>(r) * stride + c4 * 4;
+      const float4 v = agent ? make_float4(ld_agent(p), ld_agent(p + 1), ld_agent(p + 2), ld_agent(p + 3))
+                             : *reinterpret_cast<const float4*>(p);
       t.x += v.x;
       t.y += v.y;
       t.z += v.z;
@@ -809,25 +813,36 @@ __device__ __forceinline__ void bias_from_grad_pre(const GatBwdArgs<T>& a, int q
     }
     red[tid] = t;
     __syncthreads();
-    if (tid < c4n) {
-      float4 u = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      for (int k = 0; k < rpi; ++k) {
-        const float4 v = red[k * c4n + tid];
+    // the rpi row slots in a pairwise tree (fixed order; a serial sum by the
+    // c4n chunk threads took 64 dependent LDS reads at C = 16, and the bias
+    // workgroups were the c2 columns kernel's last 7 us)
+    for (int h = 1; h < rpi; h <<= 1) {
+      if (r0 < rpi && (r0 & (2 * h - 1)) == 0 && r0 + h < rpi) {
+        const float4 v = red[tid + h * c4n];
+        float4 u = red[tid];
         u.x += v.x;
         u.y += v.y;
         u.z += v.z;
         u.w += v.w;
+        red[tid] = u;
       }
-      *reinterpret_cast<float4*>(dst + tid * 4) = u;
+      __syncthreads();
+    }
+    if (tid < c4n) {
+      const float4 u = red[tid];
+      st_agent(dst + tid * 4, u.x);
+      st_agent(dst + tid * 4 + 1, u.y);
+      st_agent(dst + tid * 4 + 2, u.z);
+      st_agent(dst + tid * 4 + 3, u.w);
     }
     __syncthreads();
   };
   const int R = (a.bias_n + a.n_l2 - 1) / a.n_l2;
   const int lo = min(a.bias_n, q * R), hi = min(a.bias_n, lo + R);
   reduce(a.grad_pre + static_cast<int64_t>(a.bias_lo) * a.gp_stride, a.gp_stride, lo, hi,
-         a.bias_l2 + static_cast<int64_t>(q) * C);
+         a.bias_l2 + static_cast<int64_t>(q) * C, false);
   if (!arrive_last(counter, a.n_l2, flag)) return;
-  reduce(a.bias_l2, C, 0, a.n_l2, a.grad_bias);
+  reduce(a.bias_l2, C, 0, a.n_l2, a.grad_bias, true);
 }
 
 template <typename T, int HP, int CP>
@@ -909,7 +924,7 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_kernel(GatBwdArgs<T> a, S
       if (hh < a.H && cc < a.C) {
         const float v = red[0][q] + red[1][q] + red[2][q] + red[3][q];
         if (single) store_gx(a, j, hh, cc, v);
-        else mine[hh * a.C + cc] = v;
+        else st_agent(mine + hh * a.C + cc, v);
       }
     }
     __syncthreads();
@@ -921,14 +936,14 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_kernel(GatBwdArgs<T> a, S
     const int hh = threadIdx.x;
     const float v = gred[0][hh] + gred[1][hh] + gred[2][hh] + gred[3][hh];
     if (single) a.grad_attn_col[static_cast<int64_t>(j) * a.H + hh] = v;
-    else mine[HC + hh] = v;
+    else st_agent(mine + HC + hh, v);
   }
   if (single) return;
   if (!arrive_last(a.col_counters + sg.w, hr.y, &flag)) return;
   const int stride = HC + a.H;
   for (int q = threadIdx.x; q < HC + a.H; q += kBlock) {
     float t = 0.0f;
-    for (int z = 0; z < hr.y; ++z) t += a.part_col[static_cast<int64_t>(hr.x + z) * stride + q];
+    for (int z = 0; z < hr.y; ++z) t += ld_agent(a.part_col + static_cast<int64_t>(hr.x + z) * stride + q);
     if (q < HC) store_gx(a, j, q / a.C, q % a.C, t);
     else a.grad_attn_col[static_cast<int64_t>(j) * a.H + (q - HC)] = t;
   }

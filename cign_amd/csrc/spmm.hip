@@ -254,12 +254,12 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a,
     float t = 0.0f;
 #pragma unroll
     for (int v = 0; v < kSpmmWaves; ++v) t += red[v][c];
-    part[c] = t;
+    st_agent(part + c, t);
   }
   if (!arrive_last(a.counters + sg.w, hr.y, &flag)) return;
   for (int c = threadIdx.x; c < width; c += kSpmmBlock) {
     float t = 0.0f;
-    for (int q = 0; q < hr.y; ++q) t += a.partial[static_cast<int64_t>(hr.x + q) * width + c];
+    for (int q = 0; q < hr.y; ++q) t += ld_agent(a.partial + static_cast<int64_t>(hr.x + q) * width + c);
     const int64_t off = static_cast<int64_t>(row) * a.ld + a.c0 + c;
     if (a.add) t += to_f32(a.add[off]);
     a.y[off] = from_f32<T>(t);
