@@ -1382,12 +1382,14 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_fl_kernel(GatBwdArgs<T> a
   __shared__ float red[V * kWave * W];
   __shared__ float gred[kWavesPerBlock][kFlHeads];
   __shared__ int flag;
+  // the grad_bias workgroups first: their sums of grad_pre rows overlap the
+  // columns (placed last they were the launch's tail)
   int b = blockIdx.x;
-  const int nsched = s.n_seg + mid_blocks + (s.n_light - n_mid + kWavesPerBlock * G - 1) / (kWavesPerBlock * G);
-  if (b >= nsched) {
-    bias_from_grad_pre(a, b - nsched, a.col_counters + s.n_hrow, &flag);
+  if (b < a.n_l2) {
+    bias_from_grad_pre(a, b, a.col_counters + s.n_hrow, &flag);
     return;
   }
+  b -= a.n_l2;
   ColAcc<W, V> st;
   st.clear();
   float ac[V], gac[V];
@@ -1704,11 +1706,13 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_cm_kernel(GatBwdArgs<T> a
   __shared__ float red[kWavesPerBlock][LC][HH * 4];
   __shared__ float gred[kWavesPerBlock][HH];
   __shared__ int flag;
+  // the grad_bias workgroups first, as in gat_bwd_cols_fl_kernel
   int b = blockIdx.x;
-  if (b >= s.n_seg + light_blocks) {
-    bias_from_grad_pre(a, b - s.n_seg - light_blocks, a.col_counters + s.n_hrow, &flag);
+  if (b < a.n_l2) {
+    bias_from_grad_pre(a, b, a.col_counters + s.n_hrow, &flag);
     return;
   }
+  b -= a.n_l2;
   CmAcc<HH> st;
   st.clear();
   typename Four<T>::Raw xr[HH];

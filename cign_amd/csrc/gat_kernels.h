@@ -853,16 +853,16 @@ __global__ __launch_bounds__(kBlock) void gat_bwd_cols_kernel(GatBwdArgs<T> a, S
   const Lanes<HP> L(a.H);
   const int wave = wave_id();
   const int ncb = (a.C + CP - 1) / CP;
-  const int b = blockIdx.x;
-  const int nsched = sched_blocks(s);
   __shared__ float red[kWavesPerBlock][HP * CP];
   __shared__ float gred[kWavesPerBlock][HP];
   __shared__ int flag;
 
-  if (b >= nsched) {
-    bias_reduce(a, b - nsched, a.col_counters + s.n_hrow, &flag);
+  // the grad_bias workgroups first (their sums overlap the columns)
+  if (static_cast<int>(blockIdx.x) < a.n_l2) {
+    bias_reduce(a, blockIdx.x, a.col_counters + s.n_hrow, &flag);
     return;
   }
+  const int b = blockIdx.x - a.n_l2;
 
   if (b >= s.n_seg) {
     const int li = (b - s.n_seg) * kWavesPerBlock + wave;
