@@ -36,6 +36,7 @@
 // column l%16.
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 #include <type_traits>
 
 #include "clifford.h"
@@ -777,6 +778,353 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_lds_kernel(GemmArgs g, int n
 }
 
 // ---------------------------------------------------------------------------
+// bf16 math, K <= 256: x fragments resident in registers
+// ---------------------------------------------------------------------------
+// For M >> N with a short K (the GAT lin of the production block, 24.5K x 256
+// -> 1536) the 128 x BN tiles above fetch each x row once per column tile (12
+// times at N = 1536, 300 MB of L2 reads for a 25 MB input). Here a workgroup
+// owns 128 rows and a run of column tiles: each wavefront converts its 32 x
+// rows to bf16 MFMA fragments once, for all of K, and keeps them in registers
+// (K/4 VGPRs) while the workgroup streams the W tiles of its columns through
+// LDS (64 columns x 64 k per stage, converted at the LDS store, double
+// buffered, one stage of loads in flight across tile boundaries). Every
+// output takes the same MFMA sequence as in gemm_nt_lds_kernel (K steps of
+// 32 in order from zero, W the first operand), so the results are identical.
+constexpr int kXrBN = 64;          // columns per tile (each wavefront: its 32 rows x all 64)
+constexpr int kXrKC = 64;          // k per W stage
+constexpr int kXrLS = kXrKC + 16;  // LDS row stride in bf16: 160 B, 8 x odd floats
+constexpr int kXrMaxK = 256;
+constexpr int kXrPerCu = 3;        // workgroups per CU the grid is sized for
+constexpr int kXrMaxTiles = 16;    // column tiles per workgroup (its bias slice in LDS)
+
+// Epilogue of gemm_nt_xres_kernel: the wavefront's 32 x 64 output tile passes
+// through LDS, 16 rows at a time, so that every global store writes whole
+// lines (bf16 y: 8 rows x 128 B an instruction; fp32 y: 4 rows x 256 B). The
+// swapped layout's own stores (16 rows x 32 or 64 B an instruction) took as
+// long as the kernel's loads and MFMAs together at N = 1536 (24 of 57 us).
+// E: this wavefront's 16 x kXrES floats; LDS operations of one wavefront run
+// in order, so its staged rows need no barrier.
+constexpr int kXrES = 72;  // staged row stride in floats: 288 B, 8 x odd
+
+__device__ __forceinline__ void xres_epilogue(const GemmArgs& g, f32x4 (&acc)[2][kXrBN / 16], int64_t row0, int n0,
+                                              int lane, const float* bias, float* E) {
+  constexpr int TN = kXrBN / 16;
+  const int cg = (lane >> 4) * 4;
+  float bv[TN][4];
+#pragma unroll
+  for (int f = 0; f < TN; ++f) {
+    const float4 t = *reinterpret_cast<const float4*>(bias + 16 * f + cg);
+    bv[f][0] = t.x; bv[f][1] = t.y; bv[f][2] = t.z; bv[f][3] = t.w;
+  }
+  const bool vec8 = g.vec4 && g.N % 8 == 0;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+#pragma unroll
+    for (int f = 0; f < TN; ++f) {
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v[q] = acc[r][f][q] + bv[f][q];
+        if (g.round_bf16) v[q] = round_bf16(v[q]);
+      }
+      *reinterpret_cast<float4*>(E + (lane & 15) * kXrES + 16 * f + cg) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    if (g.y_bf16) {
+      __bf16* yb = reinterpret_cast<__bf16*>(g.y);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int id = lane + kWave * i;
+        const int rr = id / 8, c = id % 8;
+        const float4 a = *reinterpret_cast<const float4*>(E + rr * kXrES + 8 * c);
+        const float4 b = *reinterpret_cast<const float4*>(E + rr * kXrES + 8 * c + 4);
+        const int64_t m = row0 + 16 * r + rr;
+        const int n = n0 + 8 * c;
+        if (m >= g.M) continue;
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        if (vec8 && n + 8 <= g.N) {
+          bf16x8 t;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) t[q] = static_cast<__bf16>(v[q]);
+          *reinterpret_cast<bf16x8*>(yb + m * g.N + n) = t;
+        } else {
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            if (n + q < g.N) yb[m * g.N + n + q] = static_cast<__bf16>(v[q]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int id = lane + kWave * i;
+        const int rr = id / 16, c = id % 16;
+        const float4 a = *reinterpret_cast<const float4*>(E + rr * kXrES + 4 * c);
+        const int64_t m = row0 + 16 * r + rr;
+        const int n = n0 + 4 * c;
+        if (m >= g.M) continue;
+        if (g.vec4 && n + 4 <= g.N) {
+          *reinterpret_cast<float4*>(g.y + m * g.N + n) = a;
+        } else {
+          const float v[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (n + q < g.N) g.y[m * g.N + n + q] = v[q];
+        }
+      }
+    }
+  }
+}
+
+// bf16 y: the wavefront's 32 x 64 tile is staged in LDS as bf16 (row stride
+// kXrEB) and stored as four instructions of 8 rows x 128 B, issued during the
+// next column tile's W stages, each right after that stage's W loads.
+// Stores and loads share one in-order counter (vmcnt), so a load issued after
+// a store cannot be waited for without waiting for the store: stores issued
+// in a block at the end of a tile made the next tile's first W wait take
+// their acknowledgements (24 of 57 us at N = 1536). Interleaved this way, the
+// wait at the end of each stage covers only the stores of the stage before.
+constexpr int kXrEB = 80;  // staged bf16 row stride: 160 B, 8 x odd floats
+
+__device__ __forceinline__ void xres_stage_bf16(f32x4 (&acc)[2][kXrBN / 16], const float* bias, int lane,
+                                                __bf16* E) {
+  constexpr int TN = kXrBN / 16;
+  const int cg = (lane >> 4) * 4;
+#pragma unroll
+  for (int f = 0; f < TN; ++f) {
+    const float4 bv = *reinterpret_cast<const float4*>(bias + 16 * f + cg);
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      *reinterpret_cast<bf16x4*>(E + (16 * r + (lane & 15)) * kXrEB + 16 * f + cg) =
+          bf16x4{static_cast<__bf16>(acc[r][f][0] + bv.x), static_cast<__bf16>(acc[r][f][1] + bv.y),
+                 static_cast<__bf16>(acc[r][f][2] + bv.z), static_cast<__bf16>(acc[r][f][3] + bv.w)};
+  }
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Store instruction i (< 4) of a staged tile: rows 8i .. 8i+7 of the
+// wavefront's 32, lane: row 8i + lane/8, columns n0 + 8 (lane%8) .. +7.
+// mlim: rows at or past it are not stored (0 before the first tile).
+// YB == 2 (N % 8 == 0, aligned, y under 2 GiB): one buffer store with no
+// branch, rows past mlim and columns past N sent past the buffer's end (the
+// hardware drops them), so the count of memory operations after each stage's loads is the
+// same on every path and the stage's wait can leave the store in flight.
+// YB == 1: guarded stores.
+template <int YB>
+__device__ __forceinline__ void xres_store_bf16(const GemmArgs& g, __amdgpu_buffer_rsrc_t yr, int64_t row0, int64_t mlim,
+                                                int n0, int lane, const __bf16* E, int i) {
+  const int rr = 8 * i + lane / 8, c = lane % 8;
+  const bf16x8 t = *reinterpret_cast<const bf16x8*>(E + rr * kXrEB + 8 * c);
+  const int64_t m = row0 + rr;
+  const int n = n0 + 8 * c;
+  if constexpr (YB == 2) {
+    // (N % 8 == 0: a chunk lies wholly inside or wholly past the row)
+    const uint32_t off = m < mlim && n < g.N ? static_cast<uint32_t>((m * g.N + n) * 2) : 0x80000000u;
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, t), yr, off, 0, 0);
+  } else {
+    if (m >= mlim) return;
+    __bf16* yb = reinterpret_cast<__bf16*>(g.y) + m * g.N + n;
+    if (g.vec4 && g.N % 8 == 0 && n + 8 <= g.N) {
+      *reinterpret_cast<bf16x8*>(yb) = t;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (n + q < g.N) yb[q] = t[q];
+    }
+  }
+}
+
+// W stage registers between the global load and the LDS store: 256 threads
+// x 4 chunks of 4 fp32 (16 threads a row). Stage j: column tile ct0 + j /
+// STAGES, k0 = 64 (j % STAGES); rows past N read row N-1 (never stored).
+struct XrWf32 {
+  float v[4][4];
+  __device__ __forceinline__ void load(const GemmArgs& g, int n0, int k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      const int n = n0 + id / 16;
+      gload_fast<float, 4>(g.w + static_cast<int64_t>(n < g.N ? n : g.N - 1) * g.K, k0 + 4 * (id % 16), v[i]);
+    }
+  }
+  __device__ __forceinline__ void store(__bf16* d) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int id = threadIdx.x + i * kThreads;
+      st_lds<__bf16, 4>(d + (id / 16) * kXrLS + 4 * (id % 16), v[i]);
+    }
+  }
+};
+
+// (K = 192 keeps two waves a SIMD: three would spill)
+template <typename TX, int KS, int YB>
+__global__ __launch_bounds__(kThreads, KS == 6 ? 2 : kXrPerCu) void gemm_nt_xres_kernel(GemmArgs g, int nrt, int ncg, int tpg) {
+  static_assert(KS % 2 == 0 && KS * kBK <= kXrMaxK, "K is a multiple of 64, at most 256");
+  constexpr int STAGES = KS * kBK / kXrKC;  // W stages per column tile
+  constexpr int TN = kXrBN / 16;
+  using WReg = XrWf32;
+  __shared__ __align__(16) __bf16 Ws[2][kXrBN * kXrLS];
+  // per wavefront: 16 x kXrES floats (fp32 y) or 32 x kXrEB bf16 (bf16 y)
+  constexpr int kEsFloats = 32 * kXrEB / 2 > 16 * kXrES ? 32 * kXrEB / 2 : 16 * kXrES;
+  __shared__ __align__(16) float Es[kThreads / kWave][kEsFloats];
+  // the bias of the group's columns (bf16-rounded under autocast, 0 without
+  // one), so that the epilogues issue no global loads
+  __shared__ __align__(16) float Bias[kXrMaxTiles * kXrBN];
+  const int lane = lane_id();
+  const int wave = wave_id();
+  int rt, cg;
+  tile_of(nrt, ncg, rt, cg);
+  const int nct = (g.N + kXrBN - 1) / kXrBN;
+  const int ct0 = cg * tpg;
+  const int ct1 = min(ct0 + tpg, nct);
+  const int nsteps = (ct1 - ct0) * STAGES;  // >= STAGES: the host gives every group a tile
+  const int64_t row0 = static_cast<int64_t>(rt) * kBM + wave * kRowsPerWave;
+  const TX* x = static_cast<const TX*>(g.x);
+  // stages past the last reload the last (in bounds, never stored)
+  auto wload = [&](WReg& w, int j) __attribute__((always_inline)) {
+    j = min(j, nsteps - 1);
+    w.load(g, (ct0 + j / STAGES) * kXrBN, (j % STAGES) * kXrKC);
+  };
+
+  for (int t = threadIdx.x; t < (ct1 - ct0) * kXrBN; t += kThreads) {
+    const int n = ct0 * kXrBN + t;
+    const float b = g.bias ? g.bias[n < g.N ? n : g.N - 1] : 0.0f;
+    Bias[t] = g.round_bf16 ? round_bf16(b) : b;
+  }
+  WReg w0;  // stage 0, stored to LDS after the x loads
+  wload(w0, 0);
+  // x fragments (rows past M read row M-1; their outputs are never stored),
+  // in two halves of K to bound the fp32 staging registers
+  bf16x8 xf[2][KS];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float v[2][KS / 2][8];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int s = 0; s < KS / 2; ++s)
+        load_x<TX, kMathBF16>(g, x, row0 + 16 * r + (lane & 15), (h * KS / 2 + s) * kBK, lane >> 4, true, v[r][s]);
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int s = 0; s < KS / 2; ++s)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) xf[r][h * KS / 2 + s][q] = static_cast<__bf16>(v[r][s][q]);
+  }
+  w0.store(Ws[0]);
+  __syncthreads();
+
+  f32x4 acc[2][TN];
+  const int rl = lane & 15, ks = lane >> 4;
+  __bf16* Eb = reinterpret_cast<__bf16*>(Es[wave]);
+  // y as a buffer of M N bf16 (used when YB == 2; the host checks it is under 2 GiB)
+  const __amdgpu_buffer_rsrc_t yr =
+      __builtin_amdgcn_make_buffer_rsrc(g.y, 0, YB == 2 ? static_cast<int>(g.M * g.N * 2) : 0, 0x00020000);
+  int64_t mlim = 0;  // row limit of the staged tile's stores (0: nothing staged)
+  int pend_n0 = 0;   // its first column
+
+  // Stage st of column tile ct: the loads of stage j + 1 go out, then a share
+  // of the previous tile's stores, the MFMAs on stage j, and stage j + 1 goes
+  // to LDS.
+  auto stage = [&](int ct, int st) __attribute__((always_inline)) {
+    const int j = (ct - ct0) * STAGES + st;
+    WReg nw;
+    wload(nw, j + 1);
+    if constexpr (YB != 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (i * STAGES / 4 == st) xres_store_bf16<YB>(g, yr, row0, mlim, pend_n0, lane, Eb, i);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the next stage's loads ahead of the MFMAs
+    const __bf16* B = Ws[j & 1];
+#pragma unroll
+    for (int sub = 0; sub < kXrKC / kBK; ++sub) {
+#pragma unroll
+      for (int f = 0; f < TN; ++f) {
+        const bf16x8 wb = *reinterpret_cast<const bf16x8*>(B + (16 * f + rl) * kXrLS + sub * kBK + ks * 8);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) mfma_bf16_acc(acc[r][f], wb, xf[r][st * (kXrKC / kBK) + sub]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // and the MFMAs ahead of the wait for them
+    nw.store(Ws[(j + 1) & 1]);
+    __syncthreads();
+  };
+
+  for (int ct = ct0; ct < ct1; ++ct) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int f = 0; f < TN; ++f) acc[r][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    mfma_settle(acc);
+#pragma unroll
+    for (int st = 0; st < STAGES; ++st) stage(ct, st);
+    mfma_settle(acc);
+    if constexpr (YB != 0) {
+      xres_stage_bf16(acc, Bias + (ct - ct0) * kXrBN, lane, Eb);
+      mlim = g.M;
+      pend_n0 = ct * kXrBN;
+    } else {
+      xres_epilogue(g, acc, row0, ct * kXrBN, lane, Bias + (ct - ct0) * kXrBN, Es[wave]);
+    }
+  }
+  if constexpr (YB != 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xres_store_bf16<YB>(g, yr, row0, mlim, pend_n0, lane, Eb, i);
+  }
+}
+
+// CUs of the current device, cached per device.
+inline int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+  cache[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
+// CIGN_GEMM_XRES=0 (read at each call) keeps these shapes on
+// gemm_nt_lds_kernel, for comparisons.
+inline bool xres_enabled() {
+  const char* e = std::getenv("CIGN_GEMM_XRES");
+  return !(e && e[0] == '0');
+}
+
+// bf16 y the x-resident kernel can store with branch-free buffer stores
+inline bool xres_buffer_y(const GemmArgs& g) { return g.vec4 && g.N % 8 == 0 && g.M * g.N * 2 < 0x80000000LL; }
+
+template <typename TX>
+int launch_xres(hipStream_t st, const GemmArgs& g) {
+  const int nrt = static_cast<int>((g.M + kBM - 1) / kBM);
+  const int nct = (g.N + kXrBN - 1) / kXrBN;
+  // column groups so that the grid fills kXrPerCu workgroups per CU (each
+  // group re-reads its rows of x once); every group gets at least one tile
+  const int64_t slots = static_cast<int64_t>(kXrPerCu) * device_cus();
+  int ncg = static_cast<int>(std::min<int64_t>(nct, std::max<int64_t>(1, (slots + nrt - 1) / nrt)));
+  ncg = std::max(ncg, (nct + kXrMaxTiles - 1) / kXrMaxTiles);
+  const int tpg = (nct + ncg - 1) / ncg;
+  ncg = (nct + tpg - 1) / tpg;
+  const int64_t blocks = static_cast<int64_t>(nrt) * ncg;
+  if (blocks > 0x7fffffff) return set_error(kInvalid, "cign linear: too many tiles");
+  const dim3 grid(static_cast<unsigned>(blocks));
+  auto go = [&](auto YBC) {
+    constexpr int YB = decltype(YBC)::value;
+    switch (g.K / kBK) {
+      case 2: hipLaunchKernelGGL((gemm_nt_xres_kernel<TX, 2, YB>), grid, dim3(kThreads), 0, st, g, nrt, ncg, tpg); break;
+      case 4: hipLaunchKernelGGL((gemm_nt_xres_kernel<TX, 4, YB>), grid, dim3(kThreads), 0, st, g, nrt, ncg, tpg); break;
+      case 6: hipLaunchKernelGGL((gemm_nt_xres_kernel<TX, 6, YB>), grid, dim3(kThreads), 0, st, g, nrt, ncg, tpg); break;
+      default: hipLaunchKernelGGL((gemm_nt_xres_kernel<TX, 8, YB>), grid, dim3(kThreads), 0, st, g, nrt, ncg, tpg);
+    }
+  };
+  if (!g.y_bf16) go(std::integral_constant<int, 0>());
+  else if (xres_buffer_y(g)) go(std::integral_constant<int, 2>());
+  else go(std::integral_constant<int, 1>());
+  return check_launch("cign linear (x-resident)");
+}
+
+// ---------------------------------------------------------------------------
 
 // ---------------------------------------------------------------------------
 // Backward helpers
@@ -1456,18 +1804,6 @@ int launch_narrow_r(hipStream_t st, const GemmArgs& g, int grid, int ntiles) {
   }
   if constexpr (NB > kNrMinK / KB) return launch_narrow_r<EPI, MATH, NB - 1>(st, g, grid, ntiles);
   return set_error(kInvalid, "cign linear: K=%d outside the register-W kernel's range", g.K);
-}
-
-// CUs of the current device, cached per device.
-inline int device_cus() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int v = cache[dev].load(std::memory_order_relaxed);
-  if (v > 0) return v;
-  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-  cache[dev].store(v, std::memory_order_relaxed);
-  return v;
 }
 
 // grad_W partials of a narrow projection: a workgroup owns a row chunk, all
@@ -2569,6 +2905,10 @@ int launch_nt(hipStream_t st, const GemmArgs& g, int bn) {
       hipLaunchKernelGGL((gemm_nt_narrow_kernel<TX, MATH, EPI, false>), dim3(static_cast<unsigned>(blocks)),
                          dim3(kThreads), 0, st, g);
     return check_launch("cign linear (narrow)");
+  }
+  if (g.M == 0) return kOk;
+  if constexpr (MATH == kMathBF16 && EPI == kEpiStore) {
+    if (g.vec && g.K % kXrKC == 0 && g.K <= kXrMaxK && xres_enabled()) return launch_xres<TX>(st, g);
   }
   const int nrt = static_cast<int>((g.M + kBM - 1) / kBM);
   const int nct = (g.N + bn - 1) / bn;

@@ -202,3 +202,46 @@ def test_linear_argument_errors():
         a = torch.empty(4, 2, device="cuda")
         lib.call("cign_linear_logits_fwd", _lib.stream_ptr(), 4, 2, 20, 8, 0, 0, x.data_ptr(), w.data_ptr(),
                  w.data_ptr(), w.data_ptr(), y.data_ptr(), a.data_ptr(), a.data_ptr())
+
+
+@pytest.mark.parametrize("M,N,K,xdt,ybf16,bias", [
+    (24492, 1536, 256, torch.float32, True, False),   # the production block's GAT lin
+    (1000, 1536, 256, torch.bfloat16, True, True),
+    (777, 200, 192, torch.float32, True, True),       # N % 64 != 0: a partial last column tile
+    (500, 96, 64, torch.bfloat16, True, False),
+    (333, 100, 128, torch.float32, True, True),       # N % 8 != 0: guarded bf16 stores
+    (130, 1536, 256, torch.float32, False, True),     # fp32 y
+    (257, 72, 128, torch.float32, False, False),
+])
+def test_linear_bf16_x_resident_matches_tiled(M, N, K, xdt, ybf16, bias, monkeypatch):
+    """The x-resident bf16 kernel (K <= 256, a multiple of 64) runs every
+    output through the same MFMA sequence as the 128 x BN tiled kernel:
+    its bytes equal the tiled kernel's (CIGN_GEMM_XRES=0), for bf16 and fp32
+    y, partial tiles and rows, with and without a bias. Both are pinned to
+    the oracle by test_linear_forward_backward."""
+    from cign_amd import _lib
+
+    print(f"x-resident M={M} N={N} K={K} x={xdt} ybf16={ybf16} bias={bias}", flush=True)
+    lib = _lib.load_library()
+    rng = np.random.default_rng(M + N + K)
+    x = _t(rng.standard_normal((M, K)), xdt)
+    w = _t(rng.standard_normal((N, K)) / np.sqrt(K))
+    b = _t(rng.standard_normal(N) * 0.1) if bias else None
+    outs = []
+    for mode in ("0", "1"):
+        monkeypatch.setenv("CIGN_GEMM_XRES", mode)
+        y = torch.full((M, N), float("nan"), dtype=torch.bfloat16 if ybf16 else torch.float32, device="cuda")
+        if ybf16:
+            lib.call("cign_linear_fwd_bf16y", _lib.stream_ptr(), M, N, K, _lib.dtype_code(x), x.data_ptr(),
+                     w.data_ptr(), _lib.ptr(b), y.data_ptr())
+        else:
+            lib.call("cign_linear_fwd", _lib.stream_ptr(), M, N, K, _lib.dtype_code(x), 1, x.data_ptr(), w.data_ptr(),
+                     _lib.ptr(b), y.data_ptr())
+        torch.cuda.synchronize()
+        outs.append(y)
+    it = torch.int16 if ybf16 else torch.int32
+    assert not torch.isnan(outs[1].float()).any(), "x-resident kernel left outputs unwritten"
+    assert torch.equal(outs[0].view(it), outs[1].view(it))
+    if M <= 1000:  # and the oracle, with autocast's rounding points
+        ref = O.linear_forward(_np(x), _np(w), None if b is None else _np(b), amp=True)
+        assert_close(_np(outs[1]), ref, name="y", rtol=2.0 ** -7, atol=1e-6)
