@@ -421,28 +421,68 @@ __device__ __forceinline__ void tile_of(int nrt, int nct, int& rt, int& ct) {
 
 // Epilogue of the swapped-operand layout: lane holds output row m = row0 +
 // 16r + lane%16 (r < RT) and columns n = n0 + 16f + 4*(lane/16) + q, q < 4.
+// Every load here is unconditional, at an index clamped into the tensor
+// (values for columns past N or rows past M are never stored): a load behind
+// a per-lane branch ends in its own block, and the compiler then waits for
+// every memory operation in flight (vmcnt(0)) once per value, 16 to 80 waits
+// per workgroup before. Stores stay guarded.
 template <int EPI, int TN, int RT = 2>
 __device__ __forceinline__ void epilogue_swapped(const GemmArgs& g, f32x4 (&acc)[RT][TN], int64_t row0, int n0,
                                                  int lane) {
   const int cg = (lane >> 4) * 4;
+  const int nmax = g.N - 1;
+  float bv[TN][4];
+  if (g.bias) {
 #pragma unroll
-  for (int f = 0; f < TN; ++f) {
-    const int nb = n0 + 16 * f + cg;
-    const bool full4 = g.vec4 && nb + 4 <= g.N;
-    float bv[4];
+    for (int f = 0; f < TN; ++f)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < 4; ++q) bv[f][q] = g.bias[min(n0 + 16 * f + cg + q, nmax)];
+  } else {
+#pragma unroll
+    for (int f = 0; f < TN; ++f)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bv[f][q] = 0.0f;
+  }
+  float gmv[EPI == kEpiGamma ? TN : 1][4];
+  if constexpr (EPI == kEpiGamma) {
+#pragma unroll
+    for (int f = 0; f < TN; ++f)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) gmv[f][q] = g.gamma[min(n0 + 16 * f + cg + q, nmax)];
+  }
+#pragma unroll
+  for (int f = 0; f < TN; ++f)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
       // Autocast casts the bias to bf16 with the other operands.
-      const float b = (g.bias && nb + q < g.N) ? g.bias[nb + q] : 0.0f;
-      bv[q] = g.round_bf16 ? round_bf16(b) : b;
+      if (g.round_bf16) bv[f][q] = round_bf16(bv[f][q]);
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    const int64_t m = row0 + 16 * r + (lane & 15);
+    // the residual rows of this r, loaded before any of its stores
+    float hv[EPI == kEpiGamma ? TN : 1][4];
+    if constexpr (EPI == kEpiGamma) {
+      const int64_t mc = m < g.M ? m : g.M - 1;
+#pragma unroll
+      for (int f = 0; f < TN; ++f) {
+        const int nb = n0 + 16 * f + cg;
+        if (g.vec4) {
+          const float4 t = *reinterpret_cast<const float4*>(g.h + mc * g.N + min(nb, g.N - 4));
+          hv[f][0] = t.x; hv[f][1] = t.y; hv[f][2] = t.z; hv[f][3] = t.w;
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) hv[f][q] = g.h[mc * g.N + min(nb + q, nmax)];
+        }
+      }
     }
 #pragma unroll
-    for (int r = 0; r < RT; ++r) {
-      const int64_t m = row0 + 16 * r + (lane & 15);
+    for (int f = 0; f < TN; ++f) {
+      const int nb = n0 + 16 * f + cg;
+      const bool full4 = g.vec4 && nb + 4 <= g.N;
       float v[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        v[q] = acc[r][f][q] + bv[q];
+        v[q] = acc[r][f][q] + bv[f][q];
         if (g.round_bf16) v[q] = round_bf16(v[q]);
         acc[r][f][q] = v[q];
       }
@@ -466,20 +506,13 @@ __device__ __forceinline__ void epilogue_swapped(const GemmArgs& g, f32x4 (&acc)
           if (nb + q < g.N) g.y[o + q] = v[q];
       }
       if constexpr (EPI == kEpiGamma) {
-        float hv[4], ov[4];
+        float ov[4];
         uint8_t mk[4];
-        if (full4) {
-          const float4 t = *reinterpret_cast<const float4*>(g.h + o);
-          hv[0] = t.x; hv[1] = t.y; hv[2] = t.z; hv[3] = t.w;
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) hv[q] = nb + q < g.N ? g.h[o + q] : 0.0f;
-        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const bool keep = block_keep(g.seed, static_cast<uint64_t>(o + q), g.p);
           const float dv = keep ? (g.p > 0.0f ? v[q] / (1.0f - g.p) : v[q]) : 0.0f;
-          ov[q] = hv[q] + (nb + q < g.N ? g.gamma[nb + q] : 0.0f) * dv;
+          ov[q] = hv[f][q] + gmv[f][q] * dv;
           mk[q] = keep ? 1 : 0;
         }
         if (full4) {
@@ -513,9 +546,11 @@ __device__ __forceinline__ void epilogue_swapped(const GemmArgs& g, f32x4 (&acc)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int n = n0 + 16 * f + cg + q;
-          const int c = n - head * g.C;
-          const float as = n < g.N ? g.att_src[static_cast<int64_t>(head) * g.C + c] : 0.0f;
-          const float ad = n < g.N ? g.att_dst[static_cast<int64_t>(head) * g.C + c] : 0.0f;
+          // att_* are [H, C] = N values: the clamped index stays inside
+          const int64_t ai = min(n, nmax);
+          const float asv = g.att_src[ai], adv = g.att_dst[ai];
+          const float as = n < g.N ? asv : 0.0f;
+          const float ad = n < g.N ? adv : 0.0f;
 #pragma unroll
           for (int r = 0; r < RT; ++r) {
             ss[r] = fmaf(acc[r][f][q], as, ss[r]);
