@@ -142,8 +142,27 @@ __device__ __forceinline__ void gather(const SpmmArgs<T, W, VPL>& a, int jj, flo
   for_batches<(kSpmmInflight / VPL > 0 ? kSpmmInflight / VPL : 1)>(need, sb);
 }
 
+// The add row's chunks of a light row, loaded once the row is known and
+// before its gathers (at the write they were one more memory round trip
+// after the gathers, on every hop with a fused add). Chunks past the tile
+// read the tile's last chunk (never used).
 template <typename T, int W, int VPL>
-__device__ __forceinline__ void write_row(const SpmmArgs<T, W, VPL>& a, int row, int gl, const float (&acc)[VPL][W]) {
+struct AddRow {
+  typename Chunk<T, W>::Raw raw[VPL];
+  __device__ __forceinline__ void load(const SpmmArgs<T, W, VPL>& a, int row, int gl) {
+    if (!a.add) return;  // uniform
+    const T* base = a.add + static_cast<int64_t>(row) * a.ld + a.c0;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const int c = min(gl + (v << a.lgL), a.nch - 1);
+      raw[v] = Chunk<T, W>::load_raw(base + c * W);
+    }
+  }
+};
+
+template <typename T, int W, int VPL>
+__device__ __forceinline__ void write_row(const SpmmArgs<T, W, VPL>& a, int row, int gl, const float (&acc)[VPL][W],
+                                          const AddRow<T, W, VPL>& ar) {
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int c = gl + (v << a.lgL);
@@ -154,7 +173,7 @@ __device__ __forceinline__ void write_row(const SpmmArgs<T, W, VPL>& a, int row,
       for (int w = 0; w < W; ++w) out[w] = acc[v][w];
       if (a.add) {
         float ad[W];
-        Chunk<T, W>::load(a.add + off, ad);
+        Chunk<T, W>::unpack(ar.raw[v], ad);
 #pragma unroll
         for (int w = 0; w < W; ++w) out[w] += ad[w];
       }
@@ -186,9 +205,11 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a,
       const bool mine = lane < deg;
       const int jj = mine ? a.col[r.y + lane] : 0;
       const float vv = mine ? a.val[r.y + lane] : 0.0f;
+      AddRow<T, W, VPL> ar;
+      ar.load(a, r.x, gl);
       gather(a, jj, vv, 0, g, G, deg, (deg + G - 1) / G, gl, acc);
       sum_across_n(acc, a.L);
-      if (lane < a.L) write_row(a, r.x, gl, acc);
+      if (lane < a.L) write_row(a, r.x, gl, acc, ar);
       return;
     }
     // Tiny rows (degree <= L): one per lane group.
@@ -199,8 +220,10 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_kernel(SpmmArgs<T, W, VPL> a,
     const bool mine = gl < deg;
     const int jj = mine ? a.col[r.y + gl] : 0;
     const float vv = mine ? a.val[r.y + gl] : 0.0f;
+    AddRow<T, W, VPL> ar;
+    ar.load(a, r.x, gl);  // (row 0 for a group with no row: read, unused)
     gather(a, jj, vv, g << a.lgL, 0, 1, deg, wave_max_over_groups(deg, a.L), gl, acc);
-    if (has) write_row(a, r.x, gl, acc);
+    if (has) write_row(a, r.x, gl, acc, ar);
     return;
   }
 
