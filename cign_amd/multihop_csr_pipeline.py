@@ -20,7 +20,7 @@ import torch
 
 from . import _lib
 from .graph import _hip_parts
-from .schedule import build_row_schedule, seg_floor_for
+from .schedule import build_row_schedule
 
 _EXT = None
 _EXT_ERROR = None
@@ -102,10 +102,8 @@ class MultiHopCsrPlan:
         self._algorithm = algorithm
         self._nnz = int(p_values.numel())
         self._device = dev
-        # segment floor from the row width in fp32 (bf16 rows are narrower)
-        floor = seg_floor_for(4 * int(dense_cols))
-        self._p_sched = build_row_schedule(p_crow, seg_floor=floor)
-        self._pt_sched = build_row_schedule(pt_crow, seg_floor=floor)
+        self._p_sched = build_row_schedule(p_crow)
+        self._pt_sched = build_row_schedule(pt_crow)
         self._part = None
         self._prepared = False
 

@@ -344,18 +344,17 @@ class ShardedMultiHop:
 
     def __init__(self, operator, ranges, dense_cols: int):
         from .multihop_csr_pipeline import _csr_parts_int32
-        from .schedule import LIGHT_MAX, seg_floor_for, segment_edges_for
+        from .schedule import LIGHT_MAX, segment_edges_for
 
         self.dense_cols = int(dense_cols)
         self.ranges = [(int(lo), int(hi)) for lo, hi in ranges]
         self.n = int(operator.shape[0])
-        floor = seg_floor_for(4 * self.dense_cols)
         self.p_shards, self.pt_shards = [], []
         n_seg = 0
         for csr, dst in ((operator.csr, self.p_shards), (operator.csr_t, self.pt_shards)):
             crow, col, val = _csr_parts_int32(csr)
             # the whole operator's schedule geometry, as MultiHopCsrPlan builds it
-            light, seg = LIGHT_MAX, segment_edges_for(int(col.numel()), floor)
+            light, seg = LIGHT_MAX, segment_edges_for(int(col.numel()))
             rp, cl = _host_i64(crow), _host_i64(col)
             for lo, hi in self.ranges:
                 sh = _row_shard(rp, cl, val.contiguous(), lo, hi, light, seg, crow.device)

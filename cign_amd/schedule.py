@@ -19,27 +19,21 @@ from ._lib import load_library
 
 # SpMM schedules: rows with at most LIGHT_MAX edges get one wavefront (or a
 # lane group), heavier rows are cut into segments of seg_edges edges, one
-# 256-thread workgroup each, processed in rounds of 256 edges. Rows longer
-# than one segment merge their partial sums across workgroups, which costs an
-# agent-scope release/acquire (an L2 write-back and invalidate on the XCDs
-# involved); long segments instead serialise rounds inside one workgroup.
-# segment_edges_for() balances the two by graph size.
+# 512-thread workgroup each, processed in rounds of 512 edges. Rows longer
+# than one segment merge their partial sums across workgroups (partials
+# stored and loaded write-through, the last workgroup to arrive adds them in
+# segment order); long segments instead serialise rounds inside one
+# workgroup. segment_edges_for() balances the two by graph size.
 LIGHT_MAX = 64
-SEG_EDGES = 512       # smallest segment (small graphs)
+# Smallest segment (small graphs), for every row width. Gathers of narrow rows
+# (at most 256 bytes: D = 64 fp32, the c2/c3 GAT's 4 x 16) once started at
+# 1024 edges, when a cross-workgroup merge cost an L2 write-back and
+# invalidate on the XCDs involved (c2 SpMM hop 9.9 -> 9.2 us against 512).
+# With write-through merges 512 is ahead for them too: c2 layer step 0.0912
+# -> 0.0864 ms, the SpMM hops 26.2 / 27.6 -> 24.9 / 25.8 us per three, the
+# GAT forward unchanged (256, 1024 and 2048 measured too).
+SEG_EDGES = 512
 SEG_EDGES_MAX = 16384
-# Gathers of narrow rows (at most 256 bytes: D = 64 fp32, the c2/c3 GAT's
-# 4 x 16) carry little per edge, so their segments start at 1024 edges. At c2
-# (24.5K nodes, 211K edges) that took the SpMM hop from 9.9 to 9.2 us and the
-# GAT forward from 15.0 to 14.3 us, while the GAT backward (more work per
-# edge: 23.7 -> 25.4 us), the D = 512 hop and the 6 x 256 GAT forward of the
-# production block (55 -> 63 us, 240 -> 261 us) were faster at 512.
-SEG_EDGES_NARROW = 1024
-SEG_NARROW_ROW_BYTES = 256
-
-
-def seg_floor_for(row_bytes: int) -> int:
-    """Smallest segment for gathers of rows of row_bytes bytes."""
-    return SEG_EDGES_NARROW if row_bytes <= SEG_NARROW_ROW_BYTES else SEG_EDGES
 
 
 def segment_edges_for(nnz: int, floor: int = SEG_EDGES) -> int:
@@ -129,13 +123,11 @@ def gat_schedule(rowptr: torch.Tensor, pass_: int, dtype_code: int, heads: int, 
     1 = backward), with the geometry the library asks for that shape. When
     the library accepts any multiple of 256 as the segment length (its
     feature-layout kernels, seg_edges reported as 0 = "any"), the length
-    follows the graph size like the SpMM's, from 1024 edges for the forward
-    over narrow rows and from 512 otherwise."""
+    follows the graph size like the SpMM's (from SEG_EDGES)."""
     lib = load_library(require_gpu=False)
     light, seg = C.c_int32(), C.c_int32()
     lib.call("cign_gat_schedule_params", int(pass_), int(dtype_code), int(heads), int(channels), C.byref(light),
              C.byref(seg))
     if seg.value > 0:
         return cached_row_schedule(rowptr, light.value, seg.value)
-    row_bytes = int(heads) * int(channels) * (2 if dtype_code in (1, 2) else 4)
-    return cached_row_schedule(rowptr, light.value, None, seg_floor_for(row_bytes) if pass_ == 0 else SEG_EDGES)
+    return cached_row_schedule(rowptr, light.value, None, SEG_EDGES)

@@ -191,15 +191,14 @@ def test_gat_edge_index_reads_stay_in_bounds(rng):
 
 
 def test_segment_edges_for_graph_size():
-    """Segment length: 512 on small graphs (c2/c3), from 1024 for gathers of
-    rows of at most 256 bytes, 16384 at c5 (62.4M edges), a power of two in
-    between that grows with nnz."""
-    from cign_amd.schedule import SEG_EDGES_MAX, SEG_EDGES_NARROW, seg_floor_for, segment_edges_for
+    """Segment length: 512 on small graphs (c2/c3), 16384 at c5 (62.4M
+    edges), a power of two in between that grows with nnz, never below the
+    floor asked for."""
+    from cign_amd.schedule import SEG_EDGES, SEG_EDGES_MAX, segment_edges_for
 
     assert segment_edges_for(0) == SEG_EDGES == 512
     assert segment_edges_for(210_592) == 512
-    assert segment_edges_for(210_592, seg_floor_for(256)) == SEG_EDGES_NARROW == 1024
-    assert seg_floor_for(257) == seg_floor_for(6144) == 512
+    assert segment_edges_for(210_592, 1024) == 1024
     assert segment_edges_for(62_400_000) == segment_edges_for(62_400_000, 1024) == SEG_EDGES_MAX == 16384
     prev = 0
     for nnz in np.logspace(3, 9, 40).astype(np.int64):
@@ -208,22 +207,22 @@ def test_segment_edges_for_graph_size():
         prev = s
 
 
-def test_gat_schedules_pick_the_segment_floor(rng):
-    """The GAT forward over rows of at most 256 bytes gets 1024-edge segments
-    on a small graph; the backward's passes and wider rows keep 512 (header
-    word 3 is the schedule's segment length). The SpMM plan takes its floor
-    from the fp32 row width of its dense operand the same way."""
+def test_gat_schedules_take_the_graph_size_segment(rng):
+    """The GAT feature-layout schedules (the library accepts any multiple of
+    256) get the SpMM's segment length for the graph size: 512 on a small
+    graph for every pass and row width (header word 3 is the schedule's
+    segment length); the SpMM plan's schedules likewise."""
     from cign_amd import schedule as S
 
     deg = rng.integers(0, 30, 400)
     deg[7] = 3000
     rowptr = torch.from_numpy(np.concatenate([[0], np.cumsum(deg)]).astype(np.int32))
     seg = lambda sch: int(sch.header[3])
-    assert seg(S.gat_schedule(rowptr, 0, 0, 4, 16)) == 1024  # 4 x 16 fp32: 256-byte rows
-    assert seg(S.gat_schedule(rowptr, 0, 1, 4, 32)) == 1024  # 4 x 32 bf16: 256-byte rows
+    assert seg(S.gat_schedule(rowptr, 0, 0, 4, 16)) == 512  # 4 x 16 fp32: 256-byte rows
+    assert seg(S.gat_schedule(rowptr, 0, 1, 4, 32)) == 512  # 4 x 32 bf16: 256-byte rows
     assert seg(S.gat_schedule(rowptr, 0, 0, 6, 256)) == 512  # wide rows
     assert seg(S.gat_schedule(rowptr, 1, 0, 4, 16)) == 512  # backward passes
-    assert S.seg_floor_for(4 * 64) == 1024 and S.seg_floor_for(4 * 512) == 512
+    assert seg(S.build_row_schedule(rowptr)) == 512
 
 
 def test_spmm_noalloc_rejects_schedules_beyond_its_scratch():
