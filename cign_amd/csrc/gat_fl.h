@@ -94,6 +94,12 @@ inline int64_t big_graph_edges() {
 #endif
 constexpr int kFwdU = CIGN_FL_FWD_U;
 constexpr int kFwdUBig = CIGN_FL_FWD_U_BIG;
+// fp32 rows of one chunk per lane (V = 1: the c2 GAT's 4 x 16) take 8 slots
+// on small graphs too since their hub rows split into 512-edge segments with
+// write-through merges: c2 forward 12.2 -> 11.6 us. bf16 rows (11.3 -> 11.9 us)
+// and wide rows (production block, bf16 96 -> 106 us, fp32 237 -> 301 us)
+// keep 16.
+constexpr int kFwdUNarrowF32 = 8;
 constexpr int kRowsU = CIGN_FL_ROWS_U;
 constexpr int kColsU = CIGN_FL_COLS_U;
 // Batch cap of the shared-weight columns batches (large graphs): 4 slots
@@ -673,6 +679,7 @@ int FwdFlLauncher<T, L, V>::run(hipStream_t st, const GatFwdArgs<T>& a, const Sc
   if (blocks <= 0) return kOk;
   // R lanes per head share the softmax work: min(cq, 4) (cq <= L).
   const bool big = a.graph_nnz >= big_graph_edges();
+  constexpr int kU = std::is_same_v<T, float> && V == 1 ? kFwdUNarrowF32 : kFwdU;
   auto launch = [&](auto RC) {
     constexpr int R = decltype(RC)::value;
     if (a.p > 0.0f) {
@@ -680,14 +687,14 @@ int FwdFlLauncher<T, L, V>::run(hipStream_t st, const GatFwdArgs<T>& a, const Sc
         hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, true, R, kFwdUBig>), dim3(blocks), dim3(kBlock), 0, st, a, s,
                            n_mid, mid_blocks, lgcq);
       else
-        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, true, R, kFwdU>), dim3(blocks), dim3(kBlock), 0, st, a, s,
+        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, true, R, kU>), dim3(blocks), dim3(kBlock), 0, st, a, s,
                            n_mid, mid_blocks, lgcq);
     } else {
       if (big)
         hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, false, R, kFwdUBig>), dim3(blocks), dim3(kBlock), 0, st, a, s,
                            n_mid, mid_blocks, lgcq);
       else
-        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, false, R, kFwdU>), dim3(blocks), dim3(kBlock), 0, st, a, s,
+        hipLaunchKernelGGL((gat_fwd_fl_kernel<T, L, V, false, R, kU>), dim3(blocks), dim3(kBlock), 0, st, a, s,
                            n_mid, mid_blocks, lgcq);
     }
   };
