@@ -832,13 +832,13 @@ constexpr int kXrMaxK = 256;
 constexpr int kXrPerCu = 3;        // workgroups per CU the grid is sized for
 constexpr int kXrMaxTiles = 16;    // column tiles per workgroup (its bias slice in LDS)
 
-// Epilogue of gemm_nt_xres_kernel: the wavefront's 32 x 64 output tile passes
-// through LDS, 16 rows at a time, so that every global store writes whole
-// lines (bf16 y: 8 rows x 128 B an instruction; fp32 y: 4 rows x 256 B). The
-// swapped layout's own stores (16 rows x 32 or 64 B an instruction) took as
-// long as the kernel's loads and MFMAs together at N = 1536 (24 of 57 us).
-// E: this wavefront's 16 x kXrES floats; LDS operations of one wavefront run
-// in order, so its staged rows need no barrier.
+// fp32-y epilogue of gemm_nt_xres_kernel: the wavefront's 32 x 64 output tile
+// passes through LDS, 16 rows at a time, so that every global store writes
+// whole lines (4 rows x 256 B an instruction, against 16 rows x 64 B for the
+// swapped layout's own stores). Its stores go out at the end of the tile, so
+// the next tile's first W wait also waits for them; bf16 y takes the deferred
+// path below instead. E: this wavefront's 16 x kXrES floats; LDS operations
+// of one wavefront run in order, so its staged rows need no barrier.
 constexpr int kXrES = 72;  // staged row stride in floats: 288 B, 8 x odd
 
 __device__ __forceinline__ void xres_epilogue(const GemmArgs& g, f32x4 (&acc)[2][kXrBN / 16], int64_t row0, int n0,
@@ -851,7 +851,6 @@ __device__ __forceinline__ void xres_epilogue(const GemmArgs& g, f32x4 (&acc)[2]
     const float4 t = *reinterpret_cast<const float4*>(bias + 16 * f + cg);
     bv[f][0] = t.x; bv[f][1] = t.y; bv[f][2] = t.z; bv[f][3] = t.w;
   }
-  const bool vec8 = g.vec4 && g.N % 8 == 0;
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
 #pragma unroll
@@ -864,46 +863,21 @@ __device__ __forceinline__ void xres_epilogue(const GemmArgs& g, f32x4 (&acc)[2]
       }
       *reinterpret_cast<float4*>(E + (lane & 15) * kXrES + 16 * f + cg) = make_float4(v[0], v[1], v[2], v[3]);
     }
-    if (g.y_bf16) {
-      __bf16* yb = reinterpret_cast<__bf16*>(g.y);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int id = lane + kWave * i;
-        const int rr = id / 8, c = id % 8;
-        const float4 a = *reinterpret_cast<const float4*>(E + rr * kXrES + 8 * c);
-        const float4 b = *reinterpret_cast<const float4*>(E + rr * kXrES + 8 * c + 4);
-        const int64_t m = row0 + 16 * r + rr;
-        const int n = n0 + 8 * c;
-        if (m >= g.M) continue;
-        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        if (vec8 && n + 8 <= g.N) {
-          bf16x8 t;
+    for (int i = 0; i < 4; ++i) {
+      const int id = lane + kWave * i;
+      const int rr = id / 16, c = id % 16;
+      const float4 a = *reinterpret_cast<const float4*>(E + rr * kXrES + 4 * c);
+      const int64_t m = row0 + 16 * r + rr;
+      const int n = n0 + 4 * c;
+      if (m >= g.M) continue;
+      if (g.vec4 && n + 4 <= g.N) {
+        *reinterpret_cast<float4*>(g.y + m * g.N + n) = a;
+      } else {
+        const float v[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-          for (int q = 0; q < 8; ++q) t[q] = static_cast<__bf16>(v[q]);
-          *reinterpret_cast<bf16x8*>(yb + m * g.N + n) = t;
-        } else {
-#pragma unroll
-          for (int q = 0; q < 8; ++q)
-            if (n + q < g.N) yb[m * g.N + n + q] = static_cast<__bf16>(v[q]);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int id = lane + kWave * i;
-        const int rr = id / 16, c = id % 16;
-        const float4 a = *reinterpret_cast<const float4*>(E + rr * kXrES + 4 * c);
-        const int64_t m = row0 + 16 * r + rr;
-        const int n = n0 + 4 * c;
-        if (m >= g.M) continue;
-        if (g.vec4 && n + 4 <= g.N) {
-          *reinterpret_cast<float4*>(g.y + m * g.N + n) = a;
-        } else {
-          const float v[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (n + q < g.N) g.y[m * g.N + n + q] = v[q];
-        }
+        for (int q = 0; q < 4; ++q)
+          if (n + q < g.N) g.y[m * g.N + n + q] = v[q];
       }
     }
   }
