@@ -59,7 +59,7 @@ def random_gat_graph(rng, n, avg_deg=6, hubs=None):
     return np.stack([r, c])
 
 
-def assert_close_fp32_derived(actual, expected64, expected32, name="", rtol=1e-4, atol=1e-5, k=4.0):
+def assert_close_fp32_derived(actual, expected64, expected32, name="", rtol=1e-4, atol=1e-5, k=4.0, per_row=False):
     """Tolerance for float32 results that sum over many nodes (parameter
     gradients): |a - e64| <= atol + rtol |e64| + k |e32 - e64| + max |e32 -
     e64| elementwise, where e32 is the same oracle computation carried out in
@@ -69,13 +69,31 @@ def assert_close_fp32_derived(actual, expected64, expected32, name="", rtol=1e-4
     where the oracle's own order happened to round well (the GPU's order
     rounds differently: at D = 128 a GAT attention gradient the fp32 oracle
     got within 7e-6 was 2.3e-4 off on the GPU, inside the 5.6e-4 the oracle
-    itself missed by elsewhere in that tensor)."""
+    itself missed by elsewhere in that tensor).
+
+    per_row: for tensors whose first axis is the node (outputs, gradients of
+    node features), the last term is 2 max |e32 - e64| over the element's own
+    row instead of over the tensor: a node's row comes from that node's sums
+    (its neighbours, its LayerNorm row), so the row's worst float32 error is
+    the scale of the rounding a different order gives there. Over the block,
+    pack-projection, net and c4 tests on the GPU the results reached at most
+    1.07 times that row maximum beyond atol + rtol |e64| + 4 |e32 - e64|
+    (grad H at D = 256), where the tensor-wide maximum was 13 times larger
+    than what was needed."""
     a = np.asarray(actual, dtype=np.float64)
     e = np.asarray(expected64, dtype=np.float64)
     e32 = np.asarray(expected32, dtype=np.float64)
     assert a.shape == e.shape == e32.shape, f"{name}: shapes {a.shape} {e.shape} {e32.shape}"
     err32 = np.abs(e32 - e)
-    bound = atol + rtol * np.abs(e) + k * err32 + (err32.max() if err32.size else 0.0)
+    if not err32.size:
+        spread = 0.0
+    elif per_row and err32.ndim >= 2:
+        spread = 2.0 * err32.reshape(err32.shape[0], -1).max(axis=1).reshape((-1,) + (1,) * (err32.ndim - 1))
+    elif per_row:
+        spread = 2.0 * err32
+    else:
+        spread = err32.max()
+    bound = atol + rtol * np.abs(e) + k * err32 + spread
     err = np.abs(a - e)
     bad = ~(err <= bound) & ~(np.isnan(a) & np.isnan(e))
     if bad.any():

@@ -131,7 +131,8 @@ def check_training_step(n, mh, gat_graph, rp, cl, p_np, *, D, heads, in_dim, cla
     if derived_logits:
         ref32, loss32 = refs[torch.float32][0], refs[torch.float32][1]
         assert_close_fp32_derived(logits.detach().double().cpu().numpy(), ref.numpy(),
-                                  ref32.double().numpy(), name="logits", rtol=rtol, atol=1e-5 + flip(ref))
+                                  ref32.double().numpy(), name="logits", rtol=rtol, atol=1e-5 + flip(ref),
+                                  per_row=True)
         assert_close_fp32_derived(loss.detach().double().cpu().numpy(), ref_loss.numpy(),
                                   loss32.double().numpy(), name="loss", rtol=rtol, atol=1e-5 + flip(ref_loss))
     else:

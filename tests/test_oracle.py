@@ -755,6 +755,26 @@ def test_assert_close_rejects_nan():
     assert_close(a, a, rtol=1e-4, atol=1e-5)
 
 
+def test_fp32_derived_per_row_spread():
+    """per_row takes the spread term over each row: an element off by 3e-4
+    in a row whose float32 error is 1e-7 fails, though another row's 1e-3
+    float32 error would have covered it tensor-wide."""
+    from tests.conftest import assert_close_fp32_derived
+
+    e = np.linspace(-1.0, 1.0, 40).reshape(4, 10)
+    e32 = e.copy()
+    e32[0, :] += 1e-3
+    e32[1:, :] += 1e-7
+    a = e.copy()
+    a[2, 3] += 3e-4
+    assert_close_fp32_derived(a, e, e32)
+    with pytest.raises(AssertionError):
+        assert_close_fp32_derived(a, e, e32, per_row=True)
+    a[2, 3] = e[2, 3]
+    a[0, 5] += 2.5e-3
+    assert_close_fp32_derived(a, e, e32, per_row=True)
+
+
 def test_bf16_store_bound_covers_fp32_sums_stored_in_bf16(rng):
     """conftest.bf16_store_bound: float32 sums of products (row sums of a
     random sparse-like matrix, sequential and pairwise orders) rounded once to
